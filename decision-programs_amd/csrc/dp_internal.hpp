@@ -1,0 +1,226 @@
+// Internal declarations shared by the HIP kernel files and the host library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/dpgbdt.h"
+
+namespace dp {
+
+struct Error : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+
+[[noreturn]] inline void fail(const std::string& message) { throw Error(message); }
+inline void need(bool ok, const std::string& message) {
+  if (!ok) fail(message);
+}
+inline void hip_check(hipError_t status, const char* what) {
+  if (status != hipSuccess) fail(std::string(what) + ": " + hipGetErrorString(status));
+}
+#define DP_HIP(call) ::dp::hip_check((call), #call)
+
+// Owning device allocation.
+template <class T>
+struct DeviceBuffer {
+  T* p = nullptr;
+  size_t n = 0;
+  DeviceBuffer() = default;
+  explicit DeviceBuffer(size_t count) { resize(count); }
+  DeviceBuffer(const DeviceBuffer&) = delete;
+  DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+  DeviceBuffer(DeviceBuffer&& o) noexcept : p(o.p), n(o.n) { o.p = nullptr; o.n = 0; }
+  DeviceBuffer& operator=(DeviceBuffer&& o) noexcept {
+    if (this != &o) { release(); p = o.p; n = o.n; o.p = nullptr; o.n = 0; }
+    return *this;
+  }
+  ~DeviceBuffer() { release(); }
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    n = 0;
+  }
+  void resize(size_t count) {
+    release();
+    if (count) DP_HIP(hipMalloc(reinterpret_cast<void**>(&p), count * sizeof(T)));
+    n = count;
+  }
+  // Grows (discarding contents) when smaller than `count`.
+  void reserve(size_t count) {
+    if (count > n) resize(count);
+  }
+  size_t bytes() const { return n * sizeof(T); }
+};
+
+// Pinned host allocation (hipHostMalloc; never hipHostRegister).
+struct PinnedBuffer {
+  uint8_t* p = nullptr;
+  size_t n = 0;
+  PinnedBuffer() = default;
+  PinnedBuffer(const PinnedBuffer&) = delete;
+  PinnedBuffer& operator=(const PinnedBuffer&) = delete;
+  ~PinnedBuffer() { if (p) (void)hipHostFree(p); }
+  void reserve(size_t count) {
+    if (count <= n) return;
+    if (p) (void)hipHostFree(p);
+    p = nullptr;
+    DP_HIP(hipHostMalloc(reinterpret_cast<void**>(&p), count, hipHostMallocDefault));
+    n = count;
+  }
+};
+
+// Fixed-point quantiser precision: |q| <= 2^kQuantBits.
+constexpr int kQuantBits = 30;
+constexpr double kRtEps = 1e-6;
+constexpr int kMaxBins = 256;
+
+// One histogram work item: rows [begin, end) of node `slot` for one tile.
+struct HistWork {
+  int32_t slot;
+  int32_t tile;
+  int64_t begin;
+  int64_t end;
+};
+
+// One partition work item: rows [begin, end) of ridx, belonging to `node`.
+struct PartWork {
+  int32_t node;
+  int32_t pad;
+  int64_t begin;
+  int64_t end;
+};
+
+// One margin-update work item.
+struct LeafWork {
+  float value;
+  int32_t pad;
+  int64_t begin;
+  int64_t end;
+};
+
+}  // namespace dp
+
+// Device scratch shared by the operator entry points.  Host-side data for a
+// call is staged into pinned memory and copied with one async copy; the
+// staging buffer is reused only after the previous copy has completed.
+struct dp_workspace_s {
+  int device = 0;
+  dp::DeviceBuffer<uint8_t> staged_dev;
+  dp::PinnedBuffer staged_host;
+  dp::DeviceBuffer<uint8_t> scratch;
+  hipEvent_t staged_done = nullptr;
+  size_t staged_used = 0;
+  size_t scratch_used = 0;
+
+  dp_workspace_s();
+  ~dp_workspace_s();
+  // Starts a call: waits for the previous staging copy, resets bump offsets
+  // and makes room for `staging_bytes` of staged data (each stage() call adds
+  // up to 255 bytes of alignment).
+  void begin(size_t staging_bytes = 0);
+  // Reserves room for `count` T in the staging area; returns the host pointer.
+  template <class T>
+  T* stage(size_t count, T** device_ptr) {
+    size_t offset = (staged_used + 255) & ~size_t(255);
+    size_t bytes = count * sizeof(T);
+    grow_staging(offset + bytes);
+    staged_used = offset + bytes;
+    *device_ptr = reinterpret_cast<T*>(staged_dev.p + offset);
+    return reinterpret_cast<T*>(staged_host.p + offset);
+  }
+  // Copies everything staged since begin() to the device on `stream`.
+  void commit(hipStream_t stream);
+  // Device-only scratch, valid until the next begin().
+  template <class T>
+  T* take(size_t count) {
+    size_t offset = (scratch_used + 255) & ~size_t(255);
+    size_t bytes = count * sizeof(T);
+    if (offset + bytes > scratch.n) {
+      need_scratch(offset + bytes);
+    }
+    scratch_used = offset + bytes;
+    return reinterpret_cast<T*>(scratch.p + offset);
+  }
+  void reserve_scratch(size_t bytes);
+
+ private:
+  void grow_staging(size_t bytes);
+  [[noreturn]] void need_scratch(size_t bytes);
+};
+
+namespace dp {
+
+// ---- kernel launchers (implemented in the .hip files) -------------------
+void launch_fill_i64(int64_t* p, int64_t n, int64_t value, hipStream_t s);
+void launch_fill_u8(uint8_t* p, int64_t n, uint8_t value, hipStream_t s);
+void launch_iota_u32(uint32_t* p, int64_t n, hipStream_t s);
+
+// Histograms: every work item accumulates into hist[slot]; hist must be zero.
+void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t* gpair,
+                 const uint32_t* ridx, const HistWork* work, int32_t n_work,
+                 int32_t bin_stride, int64_t* hist, hipStream_t s);
+// Splits work into items of at most `chunk` rows per tile.
+int64_t hist_chunk_rows(const dp_bin_layout& layout, int64_t total_rows, int32_t n_nodes);
+void launch_subtract(const int64_t* parent, const int64_t* built, int64_t* sibling, int64_t n,
+                     hipStream_t s);
+
+// Subtraction for many (parent, built, sibling) triples of `n` int64 each.
+struct SubtractJob {
+  int64_t parent;
+  int64_t built;
+  int64_t sibling;
+};
+void launch_subtract_many(const int64_t* base_parent, const int64_t* base_child,
+                          int64_t* base_out, const SubtractJob* jobs, int32_t n_jobs,
+                          int64_t n, hipStream_t s);
+
+void launch_evaluate(const int64_t* hist, int32_t n_nodes, int32_t n_features,
+                     int32_t bin_stride, const int32_t* n_bins, const int64_t* node_sums,
+                     const int32_t* exps, int32_t exp_g, int32_t exp_h,
+                     const dp_train_param& param, dp_split_record* out, hipStream_t s);
+
+// Partition: counts, per-node scan, scatter.
+void launch_partition(const uint8_t* bins, const dp_bin_layout& layout, const uint32_t* ridx_in,
+                      uint32_t* ridx_out, const PartWork* work, int32_t n_work,
+                      const int64_t* seg_begin, const dp_split_record* splits,
+                      const int32_t* node_first_work, int32_t n_nodes, int64_t* work_left,
+                      int64_t* work_offset, int64_t* node_left, hipStream_t s);
+constexpr int64_t kPartChunk = 4096;
+
+void launch_update_margin(const uint32_t* ridx, const LeafWork* work, int32_t n_work,
+                          float* margin, int64_t stride, hipStream_t s);
+
+void launch_gradients(int32_t objective, const float* margin, const float* label,
+                      int64_t n_rows, int32_t n_classes, float* grad, float* hess,
+                      hipStream_t s);
+// maxima: uint32 [n_classes][2] scratch; exps int32 [n_classes][2];
+// gpair int32 [n_classes][n_rows][2]; sums int64 [n_classes][2].
+void launch_quantise(const float* grad, const float* hess, int64_t n_rows, int32_t n_classes,
+                     uint32_t* maxima, int32_t* exps, int32_t* gpair, int64_t* sums,
+                     hipStream_t s);
+
+void launch_bin_values(const float* values, const dp_bin_layout& layout, const int32_t* cut_ptr,
+                       const float* cut_values, uint8_t* bins, hipStream_t s);
+
+// Quantile cuts on the device; host outputs as in dp_sketch_cuts.
+void sketch_cuts(dp_workspace_s& ws, const float* values, int64_t n_rows, int32_t n_features,
+                 int32_t max_bin, int32_t* cut_ptr, float* cut_values, float* min_values,
+                 int32_t* has_missing, hipStream_t s);
+
+void launch_synth(int32_t config, uint64_t seed, int64_t n_rows, int32_t n_features,
+                  float* values, float* labels, float* grad, float* hess, hipStream_t s);
+
+inline int grid_for(int64_t n, int threads, int64_t cap = 65536) {
+  int64_t g = (n + threads - 1) / threads;
+  if (g < 1) g = 1;
+  if (g > cap) g = cap;
+  return int(g);
+}
+
+}  // namespace dp

@@ -1,0 +1,201 @@
+// Stable row partition of split nodes and the leaf margin update.
+//
+// Upstream applies a level's splits by moving each node's row ids so the left
+// child's rows precede the right child's (inside XGBoosterUpdateOneIter,
+// class_native_training.cuh:67).  Here every expanding node's segment of
+// ridx_in is split in three launches:
+//   1. count: one workgroup per chunk of <= kPartChunk rows counts left rows
+//      with wavefront ballots;
+//   2. scan: one workgroup per node turns its chunk counts into exclusive
+//      offsets and the node's left total;
+//   3. scatter: each chunk ranks its rows in position order (ballot prefix
+//      counts, 256 rows per step) and writes lefts to [begin + left rank) and
+//      rights to [begin + n_left + right rank) of ridx_out.
+// The row goes left iff its bin of the split feature is <= the split bin, or it
+// is missing and the split's default is left.
+#include "dp_internal.hpp"
+
+namespace dp {
+namespace {
+
+constexpr int kPartThreads = 256;
+constexpr int kPartSteps = int(kPartChunk / kPartThreads);  // 16 rows per lane
+
+__device__ __forceinline__ bool goes_left(const uint8_t* __restrict__ bins, int64_t n_rows,
+                                          int tile_width, uint32_t row, int feature,
+                                          int split_bin, int default_left, int missing_bin) {
+  const int64_t tile = feature / tile_width;
+  const int within = feature - int(tile) * tile_width;
+  const int b = bins[tile * n_rows * tile_width + int64_t(row) * tile_width + within];
+  if (b == missing_bin) return default_left != 0;
+  return b <= split_bin;
+}
+
+__device__ __forceinline__ int popc64(unsigned long long m) { return __popcll(m); }
+
+__global__ __launch_bounds__(kPartThreads) void part_count_kernel(
+    const uint8_t* __restrict__ bins, int64_t n_rows, int tile_width, int missing_bin,
+    const uint32_t* __restrict__ ridx, const PartWork* __restrict__ work,
+    const dp_split_record* __restrict__ splits, int64_t* __restrict__ work_left) {
+  __shared__ int wave_count[kPartThreads / 64];
+  const PartWork w = work[blockIdx.x];
+  const dp_split_record s = splits[w.node];
+  if (!s.expand) {
+    if (threadIdx.x == 0) work_left[blockIdx.x] = 0;
+    return;
+  }
+  int count = 0;
+  for (int step = 0; step < kPartSteps; ++step) {
+    const int64_t i = w.begin + int64_t(step) * kPartThreads + threadIdx.x;
+    bool left = false;
+    if (i < w.end)
+      left = goes_left(bins, n_rows, tile_width, ridx[i], s.feature, s.bin, s.default_left,
+                       missing_bin);
+    count += popc64(__ballot(left));
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) wave_count[wave] = count;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int64_t t = 0;
+    for (int k = 0; k < kPartThreads / 64; ++k) t += wave_count[k];
+    work_left[blockIdx.x] = t;
+  }
+}
+
+// One workgroup per node: exclusive scan of its chunks' left counts.
+__global__ __launch_bounds__(kPartThreads) void part_scan_kernel(
+    const int32_t* __restrict__ node_first_work, const int64_t* __restrict__ work_left,
+    int64_t* __restrict__ work_offset, int64_t* __restrict__ node_left) {
+  __shared__ int64_t partial[kPartThreads];
+  __shared__ int64_t carry;
+  const int node = blockIdx.x;
+  const int first = node_first_work[node], last = node_first_work[node + 1];
+  if (threadIdx.x == 0) carry = 0;
+  __syncthreads();
+  for (int base = first; base < last; base += kPartThreads) {
+    const int i = base + threadIdx.x;
+    const int64_t v = i < last ? work_left[i] : 0;
+    partial[threadIdx.x] = v;
+    __syncthreads();
+    // Hillis-Steele inclusive scan over the block.
+    for (int d = 1; d < kPartThreads; d <<= 1) {
+      const int64_t add = threadIdx.x >= d ? partial[threadIdx.x - d] : 0;
+      __syncthreads();
+      partial[threadIdx.x] += add;
+      __syncthreads();
+    }
+    if (i < last) work_offset[i] = carry + partial[threadIdx.x] - v;
+    __syncthreads();
+    if (threadIdx.x == kPartThreads - 1) carry += partial[threadIdx.x];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) node_left[node] = carry;
+}
+
+__global__ __launch_bounds__(kPartThreads) void part_scatter_kernel(
+    const uint8_t* __restrict__ bins, int64_t n_rows, int tile_width, int missing_bin,
+    const uint32_t* __restrict__ ridx_in, uint32_t* __restrict__ ridx_out,
+    const PartWork* __restrict__ work, const dp_split_record* __restrict__ splits,
+    const int64_t* __restrict__ seg_begin, const int64_t* __restrict__ work_offset,
+    const int64_t* __restrict__ node_left) {
+  __shared__ int wave_count[kPartThreads / 64];
+  const PartWork w = work[blockIdx.x];
+  const dp_split_record s = splits[w.node];
+  if (!s.expand) return;
+  const int64_t begin = seg_begin[w.node];
+  const int64_t n_left = node_left[w.node];
+  int64_t lefts_before = work_offset[blockIdx.x];  // lefts before this step
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int step = 0; step < kPartSteps; ++step) {
+    const int64_t step_base = w.begin + int64_t(step) * kPartThreads;
+    if (step_base >= w.end) break;
+    const int64_t i = step_base + threadIdx.x;
+    bool valid = i < w.end;
+    uint32_t row = 0;
+    bool left = false;
+    if (valid) {
+      row = ridx_in[i];
+      left = goes_left(bins, n_rows, tile_width, row, s.feature, s.bin, s.default_left,
+                       missing_bin);
+    }
+    const unsigned long long mask = __ballot(left);
+    if (lane == 0) wave_count[wave] = popc64(mask);
+    __syncthreads();
+    int64_t prefix = lefts_before;
+    int step_total = 0;
+    for (int k = 0; k < kPartThreads / 64; ++k) {
+      if (k < wave) prefix += wave_count[k];
+      step_total += wave_count[k];
+    }
+    prefix += popc64(mask & below);
+    if (valid) {
+      if (left) {
+        ridx_out[begin + prefix] = row;
+      } else {
+        const int64_t rights_before = (i - begin) - prefix;
+        ridx_out[begin + n_left + rights_before] = row;
+      }
+    }
+    lefts_before += step_total;
+    __syncthreads();
+  }
+}
+
+__global__ void update_margin_kernel(const uint32_t* __restrict__ ridx,
+                                     const LeafWork* __restrict__ work, float* __restrict__ margin,
+                                     int64_t stride) {
+  const LeafWork w = work[blockIdx.x];
+  for (int64_t i = w.begin + threadIdx.x; i < w.end; i += blockDim.x)
+    margin[int64_t(ridx[i]) * stride] += w.value;
+}
+
+__global__ void leaf_positions_kernel(const uint32_t* __restrict__ ridx,
+                                      const LeafWork* __restrict__ work,
+                                      int32_t* __restrict__ positions) {
+  const LeafWork w = work[blockIdx.x];
+  for (int64_t i = w.begin + threadIdx.x; i < w.end; i += blockDim.x)
+    positions[ridx[i]] = w.pad;
+}
+
+}  // namespace
+
+void launch_leaf_positions(const uint32_t* ridx, const LeafWork* work, int32_t n_work,
+                           int32_t* positions, hipStream_t s) {
+  if (n_work <= 0) return;
+  hipLaunchKernelGGL(leaf_positions_kernel, dim3(n_work), dim3(256), 0, s, ridx, work, positions);
+  DP_HIP(hipGetLastError());
+}
+
+void launch_partition(const uint8_t* bins, const dp_bin_layout& layout, const uint32_t* ridx_in,
+                      uint32_t* ridx_out, const PartWork* work, int32_t n_work,
+                      const int64_t* seg_begin, const dp_split_record* splits,
+                      const int32_t* node_first_work, int32_t n_nodes, int64_t* work_left,
+                      int64_t* work_offset, int64_t* node_left, hipStream_t s) {
+  if (n_nodes <= 0) return;
+  const int missing = layout.missing_bin;
+  if (n_work > 0)
+    hipLaunchKernelGGL(part_count_kernel, dim3(n_work), dim3(kPartThreads), 0, s, bins,
+                       layout.n_rows, layout.tile_width, missing, ridx_in, work, splits,
+                       work_left);
+  DP_HIP(hipGetLastError());
+  hipLaunchKernelGGL(part_scan_kernel, dim3(n_nodes), dim3(kPartThreads), 0, s, node_first_work,
+                     work_left, work_offset, node_left);
+  DP_HIP(hipGetLastError());
+  if (n_work > 0)
+    hipLaunchKernelGGL(part_scatter_kernel, dim3(n_work), dim3(kPartThreads), 0, s, bins,
+                       layout.n_rows, layout.tile_width, missing, ridx_in, ridx_out, work, splits,
+                       seg_begin, work_offset, node_left);
+  DP_HIP(hipGetLastError());
+}
+
+void launch_update_margin(const uint32_t* ridx, const LeafWork* work, int32_t n_work,
+                          float* margin, int64_t stride, hipStream_t s) {
+  if (n_work <= 0) return;
+  hipLaunchKernelGGL(update_margin_kernel, dim3(n_work), dim3(256), 0, s, ridx, work, margin,
+                     stride);
+  DP_HIP(hipGetLastError());
+}
+
+}  // namespace dp

@@ -1,0 +1,329 @@
+// Quantile cuts and uint8 binning on the device.
+//
+// The reference obtains both inside XGDMatrixCreateFromCudaArrayInterface and
+// the first update (class_native_training.cuh:51).  This build fixes an exact
+// definition (upstream's sketch is approximate and cannot be run here):
+//   v = sorted non-missing values of a feature (-0.0 folded into +0.0),
+//   u = its distinct values, m = |u|;
+//   m <= max_bin: cuts = u[1..m-1] then `last`;
+//   m >  max_bin: cuts = the strictly increasing subsequence (above u[0]) of
+//                 v[floor(i*n/max_bin)], i = 1..max_bin-1, then `last`;
+//   last = max + (|max| + 1e-5f); an all-missing feature gets the one cut 1e-5f.
+//   bin(x) = index of the first cut > x, clamped to the last bin.
+// Sorting uses rocPRIM's radix sort on order-preserving 32-bit keys (NaN maps
+// to 0xffffffff and sorts last); one workgroup per feature then extracts cuts.
+#include "dp_internal.hpp"
+
+#include <rocprim/device/device_radix_sort.hpp>
+
+#include <cmath>
+
+namespace dp {
+namespace {
+
+__device__ __forceinline__ uint32_t order_key(float x) {
+  if (x != x) return 0xffffffffu;
+  if (x == 0.0f) return 0x80000000u;
+  const uint32_t b = __float_as_uint(x);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ float key_value(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+__device__ __forceinline__ float end_cut(float v) { return v + (fabsf(v) + 1e-5f); }
+
+__global__ void keys_kernel(const float* __restrict__ values, int64_t n_rows, int32_t n_features,
+                            int32_t f_begin, int32_t f_count, uint32_t* __restrict__ keys) {
+  const int64_t total = n_rows * f_count;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += int64_t(blockDim.x) * gridDim.x) {
+    const int64_t r = i / f_count;
+    const int32_t j = int32_t(i - r * f_count);
+    keys[int64_t(j) * n_rows + r] = order_key(values[r * n_features + f_begin + j]);
+  }
+}
+
+constexpr int kCutThreads = 256;
+
+// One workgroup per feature of the sorted key block.
+__global__ __launch_bounds__(kCutThreads) void cuts_kernel(const uint32_t* __restrict__ sorted,
+                                                           int64_t n_rows, int32_t f_begin,
+                                                           int32_t max_bin,
+                                                           int32_t* __restrict__ counts,
+                                                           float* __restrict__ cuts,
+                                                           float* __restrict__ mins,
+                                                           int32_t* __restrict__ any_missing) {
+  __shared__ int64_t s_valid;
+  __shared__ int64_t s_distinct;
+  __shared__ int s_wave[kCutThreads / 64];
+  __shared__ float s_cand[kMaxBins];
+  const int j = blockIdx.x;
+  const int f = f_begin + j;
+  const uint32_t* v = sorted + int64_t(j) * n_rows;
+  float* out = cuts + int64_t(f) * max_bin;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (threadIdx.x == 0) {
+    int64_t lo = 0, hi = n_rows;  // first NaN key
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) >> 1;
+      if (v[mid] == 0xffffffffu) hi = mid; else lo = mid + 1;
+    }
+    s_valid = lo;
+    if (lo < n_rows) atomicOr(any_missing, 1);
+    s_distinct = 0;
+  }
+  __syncthreads();
+  const int64_t n = s_valid;
+  if (n == 0) {
+    if (threadIdx.x == 0) {
+      out[0] = end_cut(0.0f);
+      counts[f] = 1;
+      mins[f] = 0.0f;
+    }
+    return;
+  }
+  // Distinct count, stopping once it exceeds max_bin.
+  for (int64_t base = 0; base < n; base += kCutThreads) {
+    const int64_t i = base + threadIdx.x;
+    const bool first = i < n && (i == 0 || v[i] != v[i - 1]);
+    const unsigned long long m = __ballot(first);
+    if (lane == 0) s_wave[wave] = __popcll(m);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      for (int w = 0; w < kCutThreads / 64; ++w) s_distinct += s_wave[w];
+    }
+    __syncthreads();
+    if (s_distinct > max_bin) break;
+  }
+  const int64_t distinct = s_distinct;
+  if (distinct <= max_bin) {
+    // Every distinct value after the first is a cut, in order.
+    int64_t written = 0;  // distinct values seen before this sweep
+    for (int64_t base = 0; base < n; base += kCutThreads) {
+      const int64_t i = base + threadIdx.x;
+      const bool first = i < n && (i == 0 || v[i] != v[i - 1]);
+      const unsigned long long m = __ballot(first);
+      if (lane == 0) s_wave[wave] = __popcll(m);
+      __syncthreads();
+      int64_t rank = written;
+      int64_t sweep = 0;
+      for (int w = 0; w < kCutThreads / 64; ++w) {
+        if (w < wave) rank += s_wave[w];
+        sweep += s_wave[w];
+      }
+      const unsigned long long below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+      rank += __popcll(m & below);
+      if (first && rank >= 1) out[rank - 1] = key_value(v[i]);
+      written += sweep;
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+      out[distinct - 1] = end_cut(key_value(v[n - 1]));
+      counts[f] = int32_t(distinct);
+      mins[f] = key_value(v[0]);
+    }
+    return;
+  }
+  for (int i = 1 + threadIdx.x; i < max_bin; i += kCutThreads)
+    s_cand[i] = key_value(v[(int64_t(i) * n) / max_bin]);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float prev = key_value(v[0]);
+    int32_t c = 0;
+    for (int i = 1; i < max_bin; ++i) {
+      const float x = s_cand[i];
+      if (x > prev) {
+        out[c++] = x;
+        prev = x;
+      }
+    }
+    out[c++] = end_cut(key_value(v[n - 1]));
+    counts[f] = c;
+    mins[f] = key_value(v[0]);
+  }
+}
+
+// Bins for one tile of FT features; cuts of the tile staged in LDS.
+template <int FT>
+__global__ __launch_bounds__(256) void bin_kernel(const float* __restrict__ values,
+                                                  int64_t n_rows, int32_t n_features,
+                                                  const int32_t* __restrict__ cut_ptr,
+                                                  const float* __restrict__ cut_values,
+                                                  int32_t stride, int32_t missing_bin,
+                                                  uint8_t* __restrict__ bins) {
+  extern __shared__ float s_cuts[];  // [FT][stride]
+  __shared__ int s_count[FT];
+  const int tile = blockIdx.y;
+  const int f0 = tile * FT;
+  for (int e = threadIdx.x; e < FT; e += blockDim.x) {
+    const int f = f0 + e;
+    s_count[e] = f < n_features ? cut_ptr[f + 1] - cut_ptr[f] : 0;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < FT * stride; e += blockDim.x) {
+    const int jf = e / stride, b = e % stride;
+    const int f = f0 + jf;
+    s_cuts[e] = (f < n_features && b < s_count[jf]) ? cut_values[cut_ptr[f] + b] : 0.0f;
+  }
+  __syncthreads();
+  constexpr int TPR = FT / 16;
+  const int sub = threadIdx.x % TPR;
+  const int64_t rows_per_block = blockDim.x / TPR;
+  uint8_t* tile_base = bins + int64_t(tile) * n_rows * FT;
+  for (int64_t r = int64_t(blockIdx.x) * rows_per_block + threadIdx.x / TPR; r < n_rows;
+       r += int64_t(gridDim.x) * rows_per_block) {
+    uint32_t word[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int jf = sub * 16 + k;
+      const int f = f0 + jf;
+      uint32_t b = 0;
+      if (f < n_features) {
+        const float x = values[r * n_features + f];
+        if (x != x) {
+          b = uint32_t(missing_bin);
+        } else {
+          const float* c = s_cuts + jf * stride;
+          int lo = 0, hi = s_count[jf];
+          while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (c[mid] > x) hi = mid; else lo = mid + 1;
+          }
+          b = uint32_t(lo < s_count[jf] ? lo : s_count[jf] - 1);
+        }
+      }
+      word[k >> 2] |= (b & 0xffu) << ((k & 3) * 8);
+    }
+    *reinterpret_cast<uint4*>(tile_base + r * FT + sub * 16) =
+        make_uint4(word[0], word[1], word[2], word[3]);
+  }
+}
+
+__global__ void any_nan_kernel(const float* __restrict__ values, int64_t n,
+                               int32_t* __restrict__ flag) {
+  bool found = false;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += int64_t(blockDim.x) * gridDim.x)
+    found = found || (values[i] != values[i]);
+  if (__ballot(found) && (threadIdx.x & 63) == 0) atomicOr(flag, 1);
+}
+
+// Dense row-major copy; values equal to `missing` become NaN, +-inf is flagged
+// (the reference's prepare_values kernel rejects inf the same way,
+// class_native_training.cuh:42-46).
+__global__ void copy_matrix_kernel(const float* __restrict__ src, int64_t row_stride,
+                                   int64_t n_rows, int32_t n_features, float missing,
+                                   float* __restrict__ dst, int32_t* __restrict__ bad) {
+  const int64_t total = n_rows * n_features;
+  bool inf = false;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += int64_t(blockDim.x) * gridDim.x) {
+    const int64_t r = i / n_features;
+    const int64_t f = i - r * n_features;
+    float x = src[r * row_stride + f];
+    if (x == missing) x = __builtin_nanf("");
+    inf = inf || isinf(x);
+    dst[i] = x;
+  }
+  if (__ballot(inf) && (threadIdx.x & 63) == 0) atomicOr(bad, 1);
+}
+
+}  // namespace
+
+void launch_any_nan(const float* values, int64_t n, int32_t* flag, hipStream_t s) {
+  launch_fill_u8(reinterpret_cast<uint8_t*>(flag), 4, 0, s);
+  if (n <= 0) return;
+  hipLaunchKernelGGL(any_nan_kernel, dim3(grid_for(n, 256, 8192)), dim3(256), 0, s, values, n,
+                     flag);
+  DP_HIP(hipGetLastError());
+}
+
+void launch_copy_matrix(const float* src, int64_t row_stride, int64_t n_rows, int32_t n_features,
+                        float missing, float* dst, int32_t* bad, hipStream_t s) {
+  launch_fill_u8(reinterpret_cast<uint8_t*>(bad), 4, 0, s);
+  const int64_t total = n_rows * n_features;
+  if (total <= 0) return;
+  hipLaunchKernelGGL(copy_matrix_kernel, dim3(grid_for(total, 256, 16384)), dim3(256), 0, s, src,
+                     row_stride, n_rows, n_features, missing, dst, bad);
+  DP_HIP(hipGetLastError());
+}
+
+void launch_bin_values(const float* values, const dp_bin_layout& layout, const int32_t* cut_ptr,
+                       const float* cut_values, uint8_t* bins, hipStream_t s) {
+  if (layout.n_rows <= 0) return;
+  const int stride = kMaxBins;
+  const int rows_per_block = 256 / (layout.tile_width / 16);
+  const int gx = grid_for(layout.n_rows, rows_per_block, 4096);
+  const size_t lds = size_t(layout.tile_width) * stride * sizeof(float);
+  if (layout.tile_width == 16) {
+    hipLaunchKernelGGL(bin_kernel<16>, dim3(gx, layout.n_tiles), dim3(256), lds, s, values,
+                       layout.n_rows, layout.n_features, cut_ptr, cut_values, stride,
+                       layout.missing_bin, bins);
+  } else if (layout.tile_width == 32) {
+    static bool configured = false;
+    if (!configured) {
+      DP_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(bin_kernel<32>),
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024));
+      configured = true;
+    }
+    hipLaunchKernelGGL(bin_kernel<32>, dim3(gx, layout.n_tiles), dim3(256), lds, s, values,
+                       layout.n_rows, layout.n_features, cut_ptr, cut_values, stride,
+                       layout.missing_bin, bins);
+  } else {
+    fail("unsupported tile width");
+  }
+  DP_HIP(hipGetLastError());
+}
+
+void sketch_cuts(dp_workspace_s& ws, const float* values, int64_t n_rows, int32_t n_features,
+                 int32_t max_bin, int32_t* cut_ptr, float* cut_values, float* min_values,
+                 int32_t* has_missing, hipStream_t s) {
+  need(max_bin >= 2 && max_bin <= kMaxBins, "max_bin must be in [2, 256]");
+  need(n_rows > 0 && n_features > 0, "empty matrix");
+  need(n_rows <= int64_t(UINT32_MAX), "row count exceeds uint32 row ids");
+  // Features are sorted in blocks bounded to ~2^31 keys of device scratch.
+  int64_t block = (int64_t(1) << 31) / n_rows;
+  if (block < 1) block = 1;
+  if (block > n_features) block = n_features;
+  DeviceBuffer<uint32_t> keys(static_cast<size_t>(block * n_rows)), sorted(static_cast<size_t>(block * n_rows));
+  DeviceBuffer<int32_t> counts(static_cast<size_t>(n_features)), flag(1);
+  DeviceBuffer<float> cuts(static_cast<size_t>(n_features) * max_bin), mins(static_cast<size_t>(n_features));
+  size_t temp_bytes = 0;
+  DP_HIP(rocprim::radix_sort_keys(nullptr, temp_bytes, keys.p, sorted.p, size_t(n_rows), 0, 32, s));
+  DeviceBuffer<uint8_t> temp(temp_bytes ? temp_bytes : 1);
+  launch_fill_u8(reinterpret_cast<uint8_t*>(flag.p), 4, 0, s);
+  (void)ws;
+  for (int64_t f0 = 0; f0 < n_features; f0 += block) {
+    const int32_t fc = int32_t(std::min<int64_t>(block, n_features - f0));
+    hipLaunchKernelGGL(keys_kernel, dim3(grid_for(n_rows * fc, 256, 16384)), dim3(256), 0, s,
+                       values, n_rows, n_features, int32_t(f0), fc, keys.p);
+    DP_HIP(hipGetLastError());
+    for (int32_t j = 0; j < fc; ++j) {
+      size_t tb = temp_bytes;
+      DP_HIP(rocprim::radix_sort_keys(temp.p, tb, keys.p + int64_t(j) * n_rows,
+                                      sorted.p + int64_t(j) * n_rows, size_t(n_rows), 0, 32, s));
+    }
+    hipLaunchKernelGGL(cuts_kernel, dim3(fc), dim3(kCutThreads), 0, s, sorted.p, n_rows,
+                       int32_t(f0), max_bin, counts.p, cuts.p, mins.p, flag.p);
+    DP_HIP(hipGetLastError());
+  }
+  std::vector<int32_t> h_counts(static_cast<size_t>(n_features));
+  std::vector<float> h_cuts(static_cast<size_t>(n_features) * max_bin);
+  DP_HIP(hipMemcpyAsync(h_counts.data(), counts.p, counts.bytes(), hipMemcpyDeviceToHost, s));
+  DP_HIP(hipMemcpyAsync(h_cuts.data(), cuts.p, cuts.bytes(), hipMemcpyDeviceToHost, s));
+  DP_HIP(hipMemcpyAsync(min_values, mins.p, mins.bytes(), hipMemcpyDeviceToHost, s));
+  DP_HIP(hipMemcpyAsync(has_missing, flag.p, sizeof(int32_t), hipMemcpyDeviceToHost, s));
+  DP_HIP(hipStreamSynchronize(s));
+  cut_ptr[0] = 0;
+  for (int32_t f = 0; f < n_features; ++f) {
+    const int32_t c = h_counts[size_t(f)];
+    need(c >= 1 && c <= max_bin, "cut count out of range");
+    std::memcpy(cut_values + cut_ptr[f], h_cuts.data() + int64_t(f) * max_bin,
+                sizeof(float) * size_t(c));
+    cut_ptr[f + 1] = cut_ptr[f] + c;
+  }
+}
+
+}  // namespace dp

@@ -1,0 +1,210 @@
+// Split evaluation: per node, per feature, a wavefront prefix scan over the
+// bins of the fixed-point histogram, the loss change of every candidate in
+// both missing directions, and an argmax with deterministic ties.
+//
+// Semantics (upstream CalcGain/CalcWeight with max_delta_step 0, reached in the
+// reference only through XGBoosterUpdateOneIter, class_native_training.cuh:67;
+// regularisation parameters whitelisted at class_native_training.cuh:18-27):
+//   T(G) = sign(G) max(|G| - alpha, 0);  gain(G,H) = T(G)^2 / (H + lambda),
+//   0 when H < min_child_weight or H <= 0.
+//   Candidate (f, b): bins <= b left; missing right, then missing left (kept
+//   only when strictly better).  Valid iff both children have positive
+//   quantised hessian and H >= min_child_weight.  loss = (gain(L) + gain(R)) -
+//   gain(P) in double.  Argmax: largest loss, ties to lowest feature, then
+//   lowest bin.  expand = valid && loss > 1e-6 && loss >= gamma.
+// All double arithmetic is compiled with -ffp-contract=off so each value
+// rounds exactly as the CPU restatement computes it.
+#include "dp_internal.hpp"
+
+#include <cmath>
+
+namespace dp {
+namespace {
+
+constexpr int kEvalThreads = 256;
+constexpr int kEvalWaves = kEvalThreads / 64;
+
+struct Param {
+  double lambda, alpha, mcw, gamma;
+};
+
+__device__ __forceinline__ double threshold_l1(double g, double alpha) {
+  if (g > alpha) return g - alpha;
+  if (g < -alpha) return g + alpha;
+  return 0.0;
+}
+
+__device__ __forceinline__ double calc_gain(const Param& p, double g, double h) {
+  if (h < p.mcw || h <= 0.0) return 0.0;
+  const double t = threshold_l1(g, p.alpha);
+  return (t * t) / (h + p.lambda);
+}
+
+__device__ __forceinline__ double split_loss(const Param& p, long long qgl, long long qhl,
+                                             long long qgr, long long qhr, double ug, double uh,
+                                             double parent_gain) {
+  if (qhl <= 0 || qhr <= 0) return -INFINITY;
+  const double gl = double(qgl) * ug, hl = double(qhl) * uh;
+  const double gr = double(qgr) * ug, hr = double(qhr) * uh;
+  if (hl < p.mcw || hr < p.mcw) return -INFINITY;
+  return (calc_gain(p, gl, hl) + calc_gain(p, gr, hr)) - parent_gain;
+}
+
+struct Cand {
+  double loss;
+  long long gl, hl;
+  int feature, bin, dl;
+};
+
+// a strictly better than b: larger loss; equal loss -> lower feature, then bin.
+__device__ __forceinline__ bool better(const Cand& a, const Cand& b) {
+  if (a.loss > b.loss) return true;
+  if (a.loss < b.loss) return false;
+  if (a.feature != b.feature) return unsigned(a.feature) < unsigned(b.feature);
+  return unsigned(a.bin) < unsigned(b.bin);
+}
+
+__device__ __forceinline__ Cand shfl_xor_cand(const Cand& c, int mask) {
+  Cand o;
+  o.loss = __shfl_xor(c.loss, mask, 64);
+  o.gl = __shfl_xor(c.gl, mask, 64);
+  o.hl = __shfl_xor(c.hl, mask, 64);
+  o.feature = __shfl_xor(c.feature, mask, 64);
+  o.bin = __shfl_xor(c.bin, mask, 64);
+  o.dl = __shfl_xor(c.dl, mask, 64);
+  return o;
+}
+
+// BPL: bins per lane (bin_stride <= 64 * BPL).
+template <int BPL>
+__global__ __launch_bounds__(kEvalThreads) void evaluate_kernel(
+    const long long* __restrict__ hist, int32_t n_features, int32_t bin_stride,
+    const int32_t* __restrict__ n_bins, const long long* __restrict__ node_sums,
+    const int32_t* __restrict__ exps, int32_t exp_g_host, int32_t exp_h_host, Param p,
+    dp_split_record* __restrict__ out) {
+  __shared__ Cand wave_best[kEvalWaves];
+  const int node = blockIdx.x;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int exp_g = exps ? exps[0] : exp_g_host;
+  const int exp_h = exps ? exps[1] : exp_h_host;
+  const double ug = ldexp(1.0, -exp_g), uh = ldexp(1.0, -exp_h);
+  const long long gp = node_sums[2 * node], hp = node_sums[2 * node + 1];
+  const double parent_gain = calc_gain(p, double(gp) * ug, double(hp) * uh);
+
+  Cand best;
+  best.loss = -INFINITY;
+  best.gl = best.hl = 0;
+  best.feature = -1;
+  best.bin = -1;
+  best.dl = 0;
+  const long long* node_hist = hist + int64_t(node) * n_features * bin_stride * 2;
+  for (int f = wave; f < n_features; f += kEvalWaves) {
+    const int nb = n_bins[f];
+    const long long* hf = node_hist + int64_t(f) * bin_stride * 2;
+    long long sg[BPL], sh[BPL];
+    long long rg = 0, rh = 0;
+#pragma unroll
+    for (int j = 0; j < BPL; ++j) {
+      const int b = lane * BPL + j;
+      long long g = 0, h = 0;
+      if (b < bin_stride) {
+        g = hf[2 * b];
+        h = hf[2 * b + 1];
+      }
+      rg += g;
+      rh += h;
+      sg[j] = rg;
+      sh[j] = rh;
+    }
+    // inclusive wavefront scan of the lane totals
+    long long ig = rg, ih = rh;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const long long tg = __shfl_up(ig, d, 64);
+      const long long th = __shfl_up(ih, d, 64);
+      if (lane >= d) {
+        ig += tg;
+        ih += th;
+      }
+    }
+    const long long total_g = __shfl(ig, 63, 64), total_h = __shfl(ih, 63, 64);
+    const long long og = ig - rg, oh = ih - rh;  // exclusive offset of this lane
+    const long long mg = gp - total_g, mh = hp - total_h;
+
+    Cand c;
+    c.loss = -INFINITY;
+    c.gl = c.hl = 0;
+    c.feature = f;
+    c.bin = -1;
+    c.dl = 0;
+#pragma unroll
+    for (int j = 0; j < BPL; ++j) {
+      const int b = lane * BPL + j;
+      if (b < nb) {
+        const long long lg = og + sg[j], lh = oh + sh[j];
+        const double right_missing = split_loss(p, lg, lh, gp - lg, hp - lh, ug, uh, parent_gain);
+        const double left_missing =
+            split_loss(p, lg + mg, lh + mh, gp - lg - mg, hp - lh - mh, ug, uh, parent_gain);
+        const int dl = left_missing > right_missing;
+        const double loss = dl ? left_missing : right_missing;
+        if (loss > c.loss) {
+          c.loss = loss;
+          c.bin = b;
+          c.dl = dl;
+          c.gl = dl ? lg + mg : lg;
+          c.hl = dl ? lh + mh : lh;
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+      const Cand o = shfl_xor_cand(c, m);
+      if (better(o, c)) c = o;
+    }
+    if (c.loss > best.loss) best = c;
+  }
+  if (lane == 0) wave_best[wave] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    Cand r = wave_best[0];
+    for (int k = 1; k < kEvalWaves; ++k)
+      if (better(wave_best[k], r)) r = wave_best[k];
+    dp_split_record rec;
+    rec.loss_chg = r.loss;
+    rec.gl = r.gl;
+    rec.hl = r.hl;
+    rec.feature = r.feature;
+    rec.bin = r.bin;
+    rec.default_left = r.dl;
+    rec.valid = r.loss > -INFINITY ? 1 : 0;
+    rec.expand = rec.valid && r.loss > kRtEps && r.loss >= p.gamma;
+    rec.pad = 0;
+    out[node] = rec;
+  }
+}
+
+}  // namespace
+
+void launch_evaluate(const int64_t* hist, int32_t n_nodes, int32_t n_features,
+                     int32_t bin_stride, const int32_t* n_bins, const int64_t* node_sums,
+                     const int32_t* exps, int32_t exp_g, int32_t exp_h,
+                     const dp_train_param& param, dp_split_record* out, hipStream_t s) {
+  if (n_nodes <= 0) return;
+  need(bin_stride >= 1 && bin_stride <= kMaxBins, "split bin stride out of range");
+  Param p{double(param.lambda), double(param.alpha), double(param.min_child_weight),
+          double(param.gamma)};
+  const auto* h = reinterpret_cast<const long long*>(hist);
+  const auto* sums = reinterpret_cast<const long long*>(node_sums);
+  if (bin_stride <= 64)
+    hipLaunchKernelGGL(evaluate_kernel<1>, dim3(n_nodes), dim3(kEvalThreads), 0, s, h,
+                       n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p, out);
+  else if (bin_stride <= 128)
+    hipLaunchKernelGGL(evaluate_kernel<2>, dim3(n_nodes), dim3(kEvalThreads), 0, s, h,
+                       n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p, out);
+  else
+    hipLaunchKernelGGL(evaluate_kernel<4>, dim3(n_nodes), dim3(kEvalThreads), 0, s, h,
+                       n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p, out);
+  DP_HIP(hipGetLastError());
+}
+
+}  // namespace dp

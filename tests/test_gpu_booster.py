@@ -1,0 +1,166 @@
+"""Whole-booster parity: libdpgbdt_hip.so trained through the XGBoost C-API
+subset versus the CPU oracle's booster on identical seeded inputs.
+
+Trees must be identical node for node (feature, bin, default direction,
+threshold, leaf value, quantised sums), the row partition (final leaf of every
+row) and the training margins bit-exact, and the saved model must predict the
+training margins when walked with the routing rule x < threshold -> left,
+NaN -> default (native/class_native_source_contract.hpp:24-31).
+"""
+import json
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TREE_KEYS_EXACT = ["left", "right", "parent", "feature", "split_bin", "default_left",
+                   "sum_qg", "sum_qh"]
+TREE_KEYS_BITS = ["split_condition", "base_weight", "sum_hess"]
+
+
+def _train_both(dp, oracle, device, config, n, f, objective, k, p, rounds, seed, injected=False,
+                max_bin=256, base_score=None):
+    import torch
+    from dpgbdt import ops
+
+    values, labels, g, h = ops.synth(config, n, seed, n_features=f, want_grad=injected)
+    obj_name = {0: "binary:logistic", 1: "multi:softmax", 2: "reg:squarederror"}[objective]
+    dtrain = dp.DMatrix(values, labels)
+    params = {"objective": obj_name, "tree_method": "hist", "device": "cuda:0", "max_bin": max_bin,
+              "max_depth": p["max_depth"], "eta": p["eta"], "lambda": p.get("lam", 1.0),
+              "alpha": p.get("alpha", 0.0), "gamma": p.get("gamma", 0.0),
+              "min_child_weight": p.get("min_child_weight", 1.0), "dp_record_positions": 1}
+    if objective == 1:
+        params["num_class"] = k
+    if base_score is not None:
+        params["base_score"] = base_score
+    bst = dp.Booster(params, [dtrain])
+    gpu_positions = []
+    for r in range(rounds):
+        if injected:
+            gr = torch.roll(g, shifts=r).contiguous()
+            hr = torch.roll(h, shifts=r).contiguous()
+            bst.boost(dtrain, r, gr, hr)
+        else:
+            bst.update(dtrain, r)
+        gpu_positions.append(bst.last_positions(n))
+    x = values.cpu().numpy()
+    has_missing = bool(np.isnan(x).any())
+    eff = oracle.effective_max_bin(max_bin, has_missing)
+    cut_ptr, cuts, _ = oracle.compute_cuts(x, eff)
+    mb = 255 if has_missing else -1
+    bins = oracle.bin_matrix(x, cut_ptr, cuts, mb)
+    op = oracle.params(eta=p["eta"], lam=p.get("lam", 1.0), alpha=p.get("alpha", 0.0),
+                       gamma=p.get("gamma", 0.0), min_child_weight=p.get("min_child_weight", 1.0),
+                       max_depth=p["max_depth"])
+    inj = None
+    if injected:
+        gn, hn = g.cpu().numpy(), h.cpu().numpy()
+        inj = lambda r: (np.roll(gn, r)[:, None], np.roll(hn, r)[:, None])  # noqa: E731
+    base_margin = 0.0
+    if base_score is not None and objective != 0:
+        base_margin = float(base_score)
+    o_trees, o_margin, _ = oracle.train(bins, cut_ptr, cuts, mb, objective, labels.cpu().numpy(),
+                                        k, op, rounds, base_margin=base_margin,
+                                        bin_stride=int(np.diff(cut_ptr).max()), injected=inj)
+    return bst, x, o_trees, o_margin, gpu_positions, n
+
+
+def _compare(bst, o_trees, o_margin, gpu_positions, n, k):
+    assert bst.num_trees() == len(o_trees)
+    for t, ot in enumerate(o_trees):
+        gt = bst.tree(t)
+        for key in TREE_KEYS_EXACT:
+            np.testing.assert_array_equal(gt[key], ot[key], err_msg=f"tree {t} {key}")
+        for key in TREE_KEYS_BITS:
+            np.testing.assert_array_equal(gt[key].view(np.uint32), ot[key].view(np.uint32),
+                                          err_msg=f"tree {t} {key}")
+        leaves = ot["left"] == -1
+        np.testing.assert_array_equal(gt["loss_chg"][~leaves].view(np.uint32),
+                                      ot["loss_chg"][~leaves].view(np.uint32))
+    for r, pos in enumerate(gpu_positions):
+        np.testing.assert_array_equal(pos, o_trees[(r + 1) * k - 1]["positions"],
+                                      err_msg=f"round {r} positions")
+    np.testing.assert_array_equal(bst.margins(n, k).view(np.uint32), o_margin.view(np.uint32))
+
+
+def _predict_model(model, x, k, base):
+    """Walk the saved model JSON: sum of leaves per output plus the base margin."""
+    trees = model["learner"]["gradient_booster"]["model"]["trees"]
+    info = model["learner"]["gradient_booster"]["model"]["tree_info"]
+    out = np.tile(np.asarray(base, dtype=np.float32), (x.shape[0], 1))
+    for t, tree in enumerate(trees):
+        left = np.array(tree["left_children"])
+        right = np.array(tree["right_children"])
+        feat = np.array(tree["split_indices"])
+        cond = np.array(tree["split_conditions"], dtype=np.float32)
+        dl = np.array(tree["default_left"]).astype(bool)
+        nid = np.zeros(x.shape[0], dtype=np.int64)
+        active = left[nid] != -1
+        while active.any():
+            v = x[np.arange(x.shape[0]), feat[nid]]
+            go_left = np.where(np.isnan(v), dl[nid], v < cond[nid])
+            nxt = np.where(go_left, left[nid], right[nid])
+            nid = np.where(active, nxt, nid)
+            active = left[nid] != -1
+        out[:, info[t]] += cond[nid]
+    return out
+
+
+def test_c1_binary_logistic(dp, oracle, device):
+    """C1: 10,000 x 8 U(0,1), 256 bins, depth 6, 10 trees, eta 0.3, lambda 1."""
+    p = {"max_depth": 6, "eta": 0.3}
+    bst, x, o_trees, o_margin, pos, n = _train_both(dp, oracle, device, 1, 10000, 8, 0, 1, p, 10,
+                                                    20261201)
+    _compare(bst, o_trees, o_margin, pos, n, 1)
+    model = json.loads(bst.save_raw())
+    assert model["version"] == [3, 4, 1]
+    m = _predict_model(model, x, 1, [0.0])
+    np.testing.assert_array_equal(m.view(np.uint32), o_margin.view(np.uint32))
+    cfg = json.loads(bst.save_config())
+    assert cfg["learner"]["generic_param"]["device"] == "cuda:0"
+    assert [u["name"] for u in cfg["learner"]["gradient_booster"]["updater"]] == ["grow_gpu_hist"]
+
+
+def test_c2_reduced_logistic_depth8(dp, oracle, device):
+    p = {"max_depth": 8, "eta": 0.1}
+    bst, x, o_trees, o_margin, pos, n = _train_both(dp, oracle, device, 2, 40000, 28, 0, 1, p, 3,
+                                                    20261202)
+    _compare(bst, o_trees, o_margin, pos, n, 1)
+
+
+def test_c4_reduced_softmax(dp, oracle, device):
+    p = {"max_depth": 4, "eta": 0.3}
+    bst, x, o_trees, o_margin, pos, n = _train_both(dp, oracle, device, 4, 2000, 784, 1, 10, p, 2,
+                                                    20261204)
+    _compare(bst, o_trees, o_margin, pos, n, 10)
+    model = json.loads(bst.save_raw())
+    assert model["learner"]["gradient_booster"]["model"]["tree_info"] == list(range(10)) * 2
+    assert model["learner"]["gradient_booster"]["model"]["iteration_indptr"] == [0, 10, 20]
+
+
+def test_c5_reduced_missing_squared(dp, oracle, device):
+    p = {"max_depth": 7, "eta": 0.3}
+    bst, x, o_trees, o_margin, pos, n = _train_both(dp, oracle, device, 5, 6000, 120, 2, 1, p, 3,
+                                                    20261205, max_bin=65)
+    _compare(bst, o_trees, o_margin, pos, n, 1)
+    assert any(t["default_left"].any() for t in o_trees), "learned default direction unused"
+    m = _predict_model(json.loads(bst.save_raw()), x, 1, [0.0])
+    np.testing.assert_array_equal(m.view(np.uint32), o_margin.view(np.uint32))
+
+
+def test_c3_reduced_injected_gradients(dp, oracle, device):
+    p = {"max_depth": 8, "eta": 0.3}
+    bst, x, o_trees, o_margin, pos, n = _train_both(dp, oracle, device, 3, 30000, 128, 2, 1, p, 2,
+                                                    20261203, injected=True)
+    _compare(bst, o_trees, o_margin, pos, n, 1)
+
+
+def test_regularisation_paths(dp, oracle, device):
+    """alpha, gamma and min_child_weight change the chosen splits identically."""
+    p = {"max_depth": 5, "eta": 0.5, "alpha": 0.7, "gamma": 2.0, "min_child_weight": 8.0,
+         "lam": 0.0}
+    bst, x, o_trees, o_margin, pos, n = _train_both(dp, oracle, device, 1, 8000, 8, 0, 1, p, 3,
+                                                    31)
+    _compare(bst, o_trees, o_margin, pos, n, 1)

@@ -1,0 +1,260 @@
+"""GPU parity of every kernel on the path against the CPU oracle.
+
+Each test drives one operator through the C ABI (libdpgbdt_hip.so) and the
+oracle on the same seeded inputs.  The bar: bit-exact for cuts, bins, counts,
+fixed-point histograms, subtraction, split records (feature, bin, default
+direction, loss change, left sums) and partitions; the float histogram
+equivalent is checked against float64 sums within 1e-5 relative.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def _synth(ops, config, n, seed, f=None, grad=False):
+    values, labels, g, h = ops.synth(config, n, seed, n_features=f, want_grad=grad)
+    return values, labels, g, h
+
+
+def _prepare(dp, oracle, ws, values, max_bin=256):
+    """GPU cuts + bins, checked bit-exactly against the oracle's; returns both."""
+    from dpgbdt import ops
+
+    x = values.cpu().numpy()
+    has_missing = bool(np.isnan(x).any())
+    eff = oracle.effective_max_bin(max_bin, has_missing)
+    cut_ptr, cuts, mins, gpu_missing = ops.sketch_cuts(ws, values, eff)
+    o_ptr, o_cuts, o_mins = oracle.compute_cuts(x, eff)
+    assert gpu_missing == has_missing
+    np.testing.assert_array_equal(cut_ptr, o_ptr)
+    np.testing.assert_array_equal(cuts.view(np.uint32), o_cuts.view(np.uint32))
+    np.testing.assert_array_equal(mins.view(np.uint32), o_mins.view(np.uint32))
+    missing_bin = 255 if has_missing else -1
+    lay = ops.layout(x.shape[0], x.shape[1], 0, missing_bin)
+    bins = ops.bin_values(values, lay, cut_ptr, cuts)
+    o_bins = oracle.bin_matrix(x, o_ptr, o_cuts, missing_bin)
+    np.testing.assert_array_equal(ops.from_tiles(bins.cpu().numpy(), lay), o_bins)
+    n_bins = np.diff(cut_ptr).astype(np.int32)
+    return lay, bins, o_bins, cut_ptr, cuts, n_bins, missing_bin
+
+
+@pytest.mark.parametrize("config,n,f", [(1, 10000, 8), (3, 20000, 128), (4, 3000, 784),
+                                        (5, 3000, 200), (2, 20000, 28)])
+def test_cuts_and_bins_bit_exact(dp, oracle, ws, device, config, n, f):
+    from dpgbdt import ops
+
+    values, *_ = _synth(ops, config, n, 20261201 + config, f)
+    _prepare(dp, oracle, ws, values)
+
+
+def test_cuts_small_max_bin_and_ties(dp, oracle, ws, device):
+    """Rank path with heavy ties and a tiny max_bin; distinct path for few values."""
+    import torch
+    from dpgbdt import ops
+
+    rng = np.random.default_rng(7)
+    x = np.stack([rng.integers(0, 40, 5000).astype(np.float32),
+                  rng.normal(size=5000).astype(np.float32),
+                  np.where(rng.random(5000) < 0.5, np.float32(0.0), np.float32(-0.0)),
+                  np.full(5000, np.nan, dtype=np.float32)], axis=1)
+    x[::7, 1] = np.nan
+    values = torch.as_tensor(x, device=device)
+    _prepare(dp, oracle, ws, values, max_bin=16)
+
+
+@pytest.mark.parametrize("objective,k", [(0, 1), (1, 10), (2, 1)])
+def test_gradients_bit_exact(dp, oracle, device, objective, k):
+    import torch
+    from dpgbdt import ops
+
+    rng = np.random.default_rng(11 + objective)
+    n = 50000
+    margin = (rng.normal(size=(n, k)) * 4).astype(np.float32)
+    margin[:7, 0] = [0.0, 90.0, -90.0, 88.0, -87.5, 1e-30, -1e-30]
+    if objective == 1:
+        label = rng.integers(0, k, n).astype(np.float32)
+    elif objective == 0:
+        label = rng.integers(0, 2, n).astype(np.float32)
+    else:
+        label = rng.normal(size=n).astype(np.float32)
+    g, h = ops.objective_gradients(objective, torch.as_tensor(margin, device=device),
+                                   torch.as_tensor(label, device=device), k)
+    og, oh = oracle.gradients(objective, margin if k > 1 else margin[:, 0], label, k)
+    np.testing.assert_array_equal(g.cpu().numpy().view(np.uint32), og.view(np.uint32))
+    np.testing.assert_array_equal(h.cpu().numpy().view(np.uint32), oh.view(np.uint32))
+
+
+def test_quantise_bit_exact(dp, oracle, ws, device):
+    import torch
+    from dpgbdt import ops
+
+    rng = np.random.default_rng(3)
+    n, k = 40000, 3
+    g = rng.normal(size=(n, k)).astype(np.float32)
+    h = rng.uniform(0.01, 0.25, size=(n, k)).astype(np.float32)
+    g[:, 2] *= 1e-20  # tiny scale still quantises to full precision
+    exps, gpair, sums = ops.quantise(ws, torch.as_tensor(g, device=device),
+                                     torch.as_tensor(h, device=device))
+    exps, gpair, sums = exps.cpu().numpy(), gpair.cpu().numpy(), sums.cpu().numpy()
+    for c, (eg, eh, qg, qh) in enumerate(oracle.quantise(g, h)):
+        assert (exps[c, 0], exps[c, 1]) == (eg, eh)
+        np.testing.assert_array_equal(gpair[c, :, 0], qg)
+        np.testing.assert_array_equal(gpair[c, :, 1], qh)
+        assert sums[c, 0] == qg.astype(np.int64).sum() and sums[c, 1] == qh.astype(np.int64).sum()
+        assert np.abs(qg).max() <= 2 ** 30 and np.abs(qh).max() <= 2 ** 30
+
+
+def _gpair(ws, device, g, h):
+    import torch
+    from dpgbdt import ops
+
+    exps, gpair, sums = ops.quantise(ws, torch.as_tensor(g, device=device),
+                                     torch.as_tensor(h, device=device))
+    return exps.cpu().numpy()[0], gpair[0].contiguous(), sums.cpu().numpy()[0]
+
+
+@pytest.mark.parametrize("config,n,f", [(1, 10000, 8), (3, 60000, 128), (5, 20000, 300),
+                                        (4, 4000, 784)])
+def test_root_histogram_bit_exact(dp, oracle, ws, device, config, n, f):
+    import torch
+    from dpgbdt import ops
+
+    values, _, g, h = _synth(ops, config, n, 99 + config, f, grad=True)
+    lay, bins, o_bins, cut_ptr, cuts, n_bins, mb = _prepare(dp, oracle, ws, values)
+    stride = int(n_bins.max())
+    gn, hn = g.cpu().numpy(), h.cpu().numpy()
+    (eg, eh), gpair, _ = _gpair(ws, device, gn, hn)
+    hist = ops.hist_build(ws, bins, lay, gpair, [(0, n)], stride).cpu().numpy()[0]
+    q = oracle.quantise(gn, hn)[0]
+    ref = oracle.hist(o_bins, q[2], q[3], bin_stride=stride, missing_bin=mb)
+    np.testing.assert_array_equal(hist, ref)
+    # counts: the same kernel with unit gradients equals np.bincount
+    ones = torch.ones((n, 2), dtype=torch.int32, device=device)
+    counts = ops.hist_build(ws, bins, lay, ones, [(0, n)], stride).cpu().numpy()[0]
+    for feat in range(0, f, max(1, f // 16)):
+        col = o_bins[:, feat]
+        col = col[col != 255] if mb == 255 else col
+        np.testing.assert_array_equal(counts[feat, :, 0], np.bincount(col, minlength=stride)[:stride])
+    # float sums within 1e-5 of the float64 sums of the raw gradients
+    gsum = hist[..., 0] * oracle.unscale(eg)
+    for feat in range(0, f, max(1, f // 8)):
+        col = o_bins[:, feat]
+        keep = col != 255 if mb == 255 else np.ones(n, bool)
+        exact = np.bincount(col[keep], weights=gn[keep].astype(np.float64), minlength=stride)[:stride]
+        mass = np.bincount(col[keep], weights=np.abs(gn[keep]).astype(np.float64), minlength=stride)[:stride]
+        assert np.all(np.abs(gsum[feat] - exact) <= 1e-5 * np.maximum(mass, 1e-30))
+
+
+def test_gathered_histograms_and_subtraction(dp, oracle, ws, device):
+    import torch
+    from dpgbdt import ops
+
+    n, f = 50000, 128
+    values, _, g, h = _synth(ops, 3, n, 5, f, grad=True)
+    lay, bins, o_bins, cut_ptr, cuts, n_bins, mb = _prepare(dp, oracle, ws, values)
+    stride = int(n_bins.max())
+    gn, hn = g.cpu().numpy(), h.cpu().numpy()
+    _, gpair, _ = _gpair(ws, device, gn, hn)
+    q = oracle.quantise(gn, hn)[0]
+    rng = np.random.default_rng(1)
+    ridx = rng.permutation(n).astype(np.uint32)
+    segs = [(0, 1), (1, 700), (700, 20000), (20000, 20000), (20000, n)]
+    d_ridx = torch.as_tensor(ridx.view(np.int32), device=device)
+    hist = ops.hist_build(ws, bins, lay, gpair, segs, stride, ridx=d_ridx)
+    hn_ = hist.cpu().numpy()
+    for i, (b, e) in enumerate(segs):
+        ref = oracle.hist(o_bins, q[2], q[3], rows=ridx[b:e], bin_stride=stride, missing_bin=mb)
+        np.testing.assert_array_equal(hn_[i], ref)
+    parent = ops.hist_build(ws, bins, lay, gpair, [(0, n)], stride)
+    sib = ops.hist_subtract(parent[0], hist[2] + hist[0] + hist[1] + hist[3])
+    np.testing.assert_array_equal(sib.cpu().numpy(), hn_[4])
+
+
+def test_split_evaluation_bit_exact(dp, oracle, ws, device):
+    import torch
+    from dpgbdt import ops
+
+    n, f = 30000, 128
+    values, _, g, h = _synth(ops, 3, n, 17, f, grad=True)
+    lay, bins, o_bins, cut_ptr, cuts, n_bins, mb = _prepare(dp, oracle, ws, values)
+    stride = int(n_bins.max())
+    gn, hn = g.cpu().numpy(), h.cpu().numpy()
+    (eg, eh), gpair, sums = _gpair(ws, device, gn, hn)
+    q = oracle.quantise(gn, hn)[0]
+    rng = np.random.default_rng(2)
+    ridx = rng.permutation(n).astype(np.uint32)
+    segs = [(0, n // 2), (n // 2, n // 2 + 40), (n // 2 + 40, n)]
+    hist = ops.hist_build(ws, bins, lay, gpair, segs, stride,
+                          ridx=torch.as_tensor(ridx.view(np.int32), device=device))
+    node_sums = []
+    for b, e in segs:
+        rows = ridx[b:e]
+        node_sums.append((q[2][rows].astype(np.int64).sum(), q[3][rows].astype(np.int64).sum()))
+    d_sums = torch.as_tensor(np.array(node_sums, dtype=np.int64), device=device)
+    d_nbins = torch.as_tensor(n_bins, device=device)
+    for prm in [dict(), dict(lam=0.0, alpha=0.5, gamma=1.0, min_child_weight=3.0)]:
+        rec = ops.splits_to_numpy(ops.evaluate_splits(hist, d_nbins, d_sums, eg, eh,
+                                                      ops.train_param(**prm)))
+        p = oracle.params(**prm)
+        for i in range(len(segs)):
+            o = oracle.evaluate_split(hist[i].cpu().numpy(), n_bins, node_sums[i][0],
+                                      node_sums[i][1], eg, eh, p)
+            assert rec[i]["valid"] == o["valid"]
+            assert (rec[i]["feature"], rec[i]["bin"], rec[i]["default_left"]) == \
+                (o["feature"], o["bin"], o["default_left"])
+            assert np.float64(rec[i]["loss_chg"]).tobytes() == np.float64(o["loss_chg"]).tobytes()
+            assert (rec[i]["gl"], rec[i]["hl"]) == (o["gl"], o["hl"])
+
+
+def test_partition_bit_exact(dp, oracle, ws, device):
+    import torch
+    from dpgbdt import ops
+
+    n, f = 30000, 200
+    values, *_ = _synth(ops, 5, n, 23, f)
+    lay, bins, o_bins, *_ , mb = _prepare(dp, oracle, ws, values)
+    rng = np.random.default_rng(4)
+    ridx = rng.permutation(n).astype(np.uint32)
+    segs = [(0, 10000), (10000, 10001), (10001, 25000), (25000, n)]
+    rec = np.zeros(len(segs), dtype=ops.SPLIT_DTYPE)
+    choices = [(3, 10, 1, 1), (5, 0, 0, 1), (17, 30, 0, 0), (199, 5, 1, 1)]
+    for i, (feat, b, dl, ex) in enumerate(choices):
+        rec[i]["feature"], rec[i]["bin"], rec[i]["default_left"], rec[i]["expand"] = feat, b, dl, ex
+        rec[i]["valid"] = 1
+    d_rec = torch.as_tensor(np.frombuffer(rec.tobytes(), dtype=np.uint8).copy(), device=device)
+    d_ridx = torch.as_tensor(ridx.view(np.int32), device=device)
+    out, left = ops.partition(ws, bins, lay, d_ridx, segs, d_rec)
+    out = out.cpu().numpy().view(np.uint32)
+    left = left.cpu().numpy()
+    expect = ridx.copy()
+    for i, ((b, e), (feat, sb, dl, ex)) in enumerate(zip(segs, choices)):
+        if not ex:
+            assert left[i] == 0
+            continue
+        part, nl = oracle.partition(ridx, b, e, o_bins, feat, sb, dl, mb)
+        expect[b:e] = part[b:e]
+        assert left[i] == nl
+    for (b, e), (*_, ex) in zip(segs, choices):
+        if ex:
+            np.testing.assert_array_equal(out[b:e], expect[b:e])
+
+
+def test_update_margin(dp, ws, device):
+    import torch
+    from dpgbdt import ops
+
+    n = 70000
+    rng = np.random.default_rng(6)
+    ridx = rng.permutation(n).astype(np.uint32)
+    segs = [(0, 30000), (30000, 30001), (30001, n)]
+    vals = [0.25, -1.5, 3.0]
+    margin = torch.zeros(n * 2, dtype=torch.float32, device=device)
+    ops.update_margin(ws, torch.as_tensor(ridx.view(np.int32), device=device), segs, vals,
+                      margin[1:], stride=2)
+    m = margin.cpu().numpy().reshape(n, 2)
+    expect = np.zeros(n, np.float32)
+    for (b, e), v in zip(segs, vals):
+        expect[ridx[b:e]] += np.float32(v)
+    np.testing.assert_array_equal(m[:, 1], expect)
+    assert not m[:, 0].any()
