@@ -1,0 +1,255 @@
+#!/usr/bin/env python3
+"""Benchmark of the gradient-boosting training hot path on one MI355X.
+
+Headline (`value`): histogram build throughput in rows*features/s on the C3
+workload -- 10,000,000 rows x 128 features, 256 quantile bins, uint8 bins,
+fixed-point (g, h) -- with everything resident in HBM.  One step is one
+histogram pass over all 10M rows (one launch of the histogram kernel).
+
+The same JSON line carries
+  roofline      the histogram kernel's algorithmic bytes per launch over its
+                average launch duration (HIP events on the launch stream),
+                against the 8 TB/s HBM3E peak;
+  trees_per_s   full boosting rounds on C2 (1M x 28, depth 8, 100 trees,
+                binary:logistic) and C3 (depth 8, injected gradients, 20 trees);
+  cpu_baseline  the CPU restatement (oracle, OpenMP) of the same histogram
+                pass on a bounded row sample, on this box's host cores.
+
+Data are synthetic (dp_synth, fixed seeds); nothing is read from disk.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for sub in ("decision-programs_amd", "oracle"):
+    p = os.path.join(ROOT, sub)
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+METRIC = "histogram build rows·features/s + % HBM peak; trees/s (1M×28, depth 8)"
+HBM_PEAK_GBS = 8000.0
+SEED = 20261201
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def algorithmic_hist_bytes(n_rows, n_features, n_bins, gathered=False):
+    """u8 bins + 8 B (g, h) per row (+4 B row id when gathered) + F*B*8 B output."""
+    return n_rows * n_features + 8 * n_rows + (4 * n_rows if gathered else 0) + \
+        n_features * n_bins * 8
+
+
+def read_traffic():
+    """HBM bytes per launch of the C3 root histogram from the committed PMC summary."""
+    path = os.path.join(ROOT, "profiles", "hist_c3_root_pmc.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def hist_leg(args, torch, dp, ops):
+    """C3 root-pass histogram: K timed launches, events around each launch."""
+    n, f = args.rows, 128
+    dev = torch.device("cuda:0")
+    log(f"C3 data: {n} x {f} synth + quantile cuts + bins")
+    values, _, g, h = ops.synth(3, n, SEED + 3, device=dev, want_grad=True)
+    ws = ops.Workspace()
+    cut_ptr, cuts, _, missing = ops.sketch_cuts(ws, values, 256)
+    import numpy as np
+
+    lay = ops.layout(n, f, 0, -1)
+    bins = ops.bin_values(values, lay, cut_ptr, cuts)
+    del values
+    n_bins = np.diff(cut_ptr)
+    stride = int(n_bins.max())
+    exps, gpair, sums = ops.quantise(ws, g, h)
+    gp = gpair[0].contiguous()
+    hist = torch.zeros((1, f, stride, 2), dtype=torch.int64, device=dev)
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        ops.hist_accumulate(ws, bins, lay, gp, [(0, n)], hist)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev[0].record(stream)
+    for k in range(args.steps):
+        ops.hist_accumulate(ws, bins, lay, gp, [(0, n)], hist)
+        ev[k + 1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    launch_ms = [ev[k].elapsed_time(ev[k + 1]) for k in range(args.steps)]
+    avg_ms = sum(launch_ms) / len(launch_ms)
+    # size-independent check: every feature's bins sum to the root totals
+    h0 = hist[0].sum(dim=1)  # [F, 2]
+    reps = args.warmup + args.steps
+    tot = sums[0].to(torch.int64) * reps
+    assert bool((h0 == tot).all()), "histogram totals differ from the gradient sums"
+    abytes = algorithmic_hist_bytes(n, f, 256)
+    achieved = abytes / (avg_ms * 1e-3) / 1e9
+    out = {
+        "n": n, "f": f, "stride": stride, "avg_ms": avg_ms, "wall_s": wall,
+        "ms_per_step": wall / args.steps * 1e3,
+        "rows_features_per_s": n * f / (avg_ms * 1e-3),
+        "achieved_gbs": achieved, "algorithmic_bytes": abytes,
+        "min_ms": min(launch_ms), "max_ms": max(launch_ms),
+    }
+    sample = None
+    if not args.skip_cpu:
+        rows = min(n, args.cpu_rows)
+        tiles = bins.view(lay.n_tiles, n, lay.tile_width)[:, :rows, :]
+        sample_bins = tiles.permute(1, 0, 2).reshape(rows, -1)[:, :f].contiguous().cpu().numpy()
+        gq = gp[:rows].cpu().numpy()
+        sample = (sample_bins, np.ascontiguousarray(gq[:, 0]), np.ascontiguousarray(gq[:, 1]),
+                  stride, hist, exps, sums)
+    return out, sample, ws, bins, lay, gp, stride
+
+
+def cpu_leg(sample, args):
+    import numpy as np
+    import pyoracle
+
+    bins, qg, qh, stride = sample[:4]
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    rows, f = bins.shape
+    pyoracle.hist_parallel(bins[: min(rows, 4096)], qg[:4096], qh[:4096], stride, -1, threads)
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        res = pyoracle.hist_parallel(bins, qg, qh, stride, -1, threads)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= args.cpu_seconds or reps >= 200:
+            break
+    per_pass = el / reps
+    # the sample histogram must equal the sum over its rows (exact integers)
+    assert int(res[0, :, 0].sum()) == int(qg.astype(np.int64).sum())
+    return {"value": rows * f / per_pass, "unit": "rows·features/s", "cores": threads,
+            "kind": "port",
+            "sample": f"oracle dpo_hist_parallel root pass over the first {rows} rows x {f} "
+                      f"features of the C3 matrix, {reps} passes, {el:.1f} s",
+            "gbs": algorithmic_hist_bytes(rows, f, 256) / per_pass / 1e9}
+
+
+def trees_leg(torch, dp, ops, n, config, rounds, depth, eta, injected, warm_rounds=2):
+    """Wall time of `rounds` boosting rounds on a fresh booster (matrix already quantised)."""
+    f = ops.SYNTH_FEATURES[config]
+    values, labels, g, h = ops.synth(config, n, SEED + config, want_grad=injected)
+    dtrain = dp.DMatrix(values, labels)
+    del values
+    params = {"objective": "binary:logistic" if not injected else "reg:squarederror",
+              "tree_method": "hist", "device": "cuda:0", "max_depth": depth, "eta": eta,
+              "lambda": 1.0, "min_child_weight": 1.0, "max_bin": 256}
+    g1 = g.reshape(-1, 1).contiguous() if injected else None
+    h1 = h.reshape(-1, 1).contiguous() if injected else None
+    warm = dp.Booster(params, [dtrain])  # quantises the matrix, warms kernels
+    for r in range(warm_rounds):
+        warm.boost(dtrain, r, g1, h1) if injected else warm.update(dtrain, r)
+    del warm
+    bst = dp.Booster(params, [dtrain])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for r in range(rounds):
+        bst.boost(dtrain, r, g1, h1) if injected else bst.update(dtrain, r)
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    nodes = sum(len(bst.tree(t)["left"]) for t in range(bst.num_trees()))
+    return {"trees": rounds, "seconds": el, "value": rounds / el, "unit": "trees/s",
+            "rows": n, "features": f, "depth": depth, "nodes": nodes}
+
+
+def copy_leg(torch, args):
+    """Plain device copy of a known size (counter calibration for PMC runs)."""
+    nbytes = 1 << 30
+    a = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda:0").fill_(1.0)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    for _ in range(args.steps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes,
+                      "launches": args.steps}))
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--rows", type=int, default=10_000_000)
+    ap.add_argument("--mode", choices=["full", "hist", "copy"], default="full")
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--cpu-rows", type=int, default=1_000_000)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
+              "row-sharded design is described in DESIGN.md and not run here.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import dpgbdt as dp
+    from dpgbdt import ops
+
+    dp.load()
+    if args.mode == "copy":
+        copy_leg(torch, args)
+        return
+    hist, sample, *_ = hist_leg(args, torch, dp, ops)
+    log(f"hist: {hist['avg_ms']:.3f} ms/launch, {hist['achieved_gbs']:.0f} GB/s algorithmic")
+    trees = {}
+    if args.mode == "full":
+        log("C2 trees: 1M x 28, depth 8, 100 rounds")
+        trees["C2"] = trees_leg(torch, dp, ops, 1_000_000, 2, 100, 8, 0.1, injected=False)
+        log(f"C2: {trees['C2']['value']:.1f} trees/s")
+        log("C3 trees: 10M x 128, depth 8, 20 rounds (injected gradients)")
+        trees["C3"] = trees_leg(torch, dp, ops, args.rows, 3, 20, 8, 0.3, injected=True)
+        log(f"C3: {trees['C3']['value']:.2f} trees/s")
+    cpu = None
+    if sample is not None:
+        log(f"CPU baseline: oracle histogram, {args.cpu_seconds:.0f} s budget")
+        cpu = cpu_leg(sample, args)
+    avg_s = hist["avg_ms"] * 1e-3
+    line = {
+        "metric": METRIC,
+        "value": hist["rows_features_per_s"],
+        "unit": "rows·features/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": hist["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int64",
+        "data": "synthetic (dp_synth C3: 64 N(0,1), 32 lognormal, 32 U{0..15} features; "
+                "g ~ N(0,1), h ~ U(0.01,0.25)); uint8 quantile bins",
+        "config": {"workload": f"C3 histogram root pass: {hist['n']} rows x {hist['f']} "
+                               f"features x 256 bins, one launch per step",
+                   "rows": hist["n"], "features": hist["f"], "max_bin": 256,
+                   "bin_stride": hist["stride"], "parallelism": "single GPU"},
+        "pct_hbm_peak": 100.0 * hist["achieved_gbs"] / HBM_PEAK_GBS,
+        "roofline": {"bound": "hbm", "achieved": hist["achieved_gbs"], "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": hist["achieved_gbs"] / HBM_PEAK_GBS,
+                     "traffic": read_traffic(),
+                     "kernel": "dp::hist_kernel<false>",
+                     "algorithmic_bytes_per_launch": hist["algorithmic_bytes"],
+                     "avg_launch_ms": hist["avg_ms"]},
+        "trees_per_s": trees,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

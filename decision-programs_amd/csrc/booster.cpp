@@ -185,14 +185,13 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, int32_t exp_g, int32
           jobs.push_back({int64_t(a.parent_slot) * S, int64_t(small) * S, int64_t(large) * S});
         }
       }
-      int64_t build_rows = 0;
-      for (int32_t k : build) build_rows += level[size_t(k)].end - level[size_t(k)].begin;
-      const int64_t chunk = hist_chunk_rows(L, build_rows, int32_t(build.size()));
-      std::vector<HistWork> hw;
-      for (int32_t t = 0; t < L.n_tiles; ++t)
-        for (int32_t k : build)
-          for (int64_t b = level[size_t(k)].begin; b < level[size_t(k)].end; b += chunk)
-            hw.push_back({k, t, b, std::min(b + chunk, level[size_t(k)].end)});
+      std::vector<int64_t> bb, be;
+      for (int32_t k : build) {
+        bb.push_back(level[size_t(k)].begin);
+        be.push_back(level[size_t(k)].end);
+      }
+      const std::vector<HistWork> hw =
+          make_hist_work(L, bb.data(), be.data(), build.data(), int32_t(build.size()));
 
       std::vector<PartWork> pw;
       std::vector<int32_t> first(static_cast<size_t>(n) + 1);

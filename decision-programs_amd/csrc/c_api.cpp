@@ -381,8 +381,8 @@ int dp_layout_init(int64_t n_rows, int32_t n_features, int32_t tile_width, int32
     dp::need(out != nullptr, "null layout");
     dp::need(n_rows > 0 && n_features > 0, "layout needs rows and features");
     dp::need(missing_bin == -1 || missing_bin == 255, "missing_bin must be -1 or 255");
-    if (tile_width == 0) tile_width = n_features <= 16 ? 16 : 32;
-    dp::need(tile_width == 16 || tile_width == 32, "tile_width must be 16 or 32");
+    if (tile_width == 0) tile_width = 16;
+    dp::need(tile_width == 16, "tile_width must be 16");
     out->n_rows = n_rows;
     out->n_features = n_features;
     out->tile_width = tile_width;
@@ -441,34 +441,48 @@ int dp_quantise_gradients(dp_workspace ws, const float* grad, const float* hess,
   });
 }
 
+namespace {
+void hist_call(dp_workspace ws, const uint8_t* bins, const dp_bin_layout* layout,
+               const int32_t* gpair, const uint32_t* ridx, const int64_t* begin,
+               const int64_t* end, int32_t n_nodes, int32_t bin_stride, int64_t* hist,
+               void* stream, bool accumulate) {
+  dp::need(ws && bins && layout && gpair && begin && end && hist, "null argument");
+  dp::need(n_nodes >= 0, "negative node count");
+  dp::need(bin_stride >= 1 && bin_stride <= dp::kMaxBins, "bin_stride must be in [1, 256]");
+  int64_t total = 0;
+  for (int32_t i = 0; i < n_nodes; ++i) {
+    dp::need(begin[i] >= 0 && begin[i] <= end[i], "node segment out of order");
+    dp::need(ridx != nullptr || end[i] <= layout->n_rows, "row range beyond the matrix");
+    total += end[i] - begin[i];
+  }
+  (void)total;
+  std::vector<dp::HistWork> work = dp::make_hist_work(*layout, begin, end, nullptr, n_nodes);
+  hipStream_t s = as_stream(stream);
+  ws->begin(sizeof(dp::HistWork) * work.size() + 256);
+  dp::HistWork* d_work;
+  std::copy(work.begin(), work.end(), ws->stage(work.size(), &d_work));
+  ws->commit(s);
+  const int64_t per_node = int64_t(layout->n_features) * bin_stride * 2;
+  if (!accumulate) dp::launch_fill_i64(hist, per_node * n_nodes, 0, s);
+  dp::launch_hist(bins, *layout, gpair, ridx, d_work, int32_t(work.size()), bin_stride, hist, s);
+}
+}  // namespace
+
 int dp_hist_build(dp_workspace ws, const uint8_t* bins, const dp_bin_layout* layout,
                   const int32_t* gpair, const uint32_t* ridx, const int64_t* begin,
                   const int64_t* end, int32_t n_nodes, int32_t bin_stride, int64_t* hist,
                   void* stream) {
   return guarded([&] {
-    dp::need(ws && bins && layout && gpair && begin && end && hist, "null argument");
-    dp::need(n_nodes >= 0, "negative node count");
-    dp::need(bin_stride >= 1 && bin_stride <= dp::kMaxBins, "bin_stride must be in [1, 256]");
-    int64_t total = 0;
-    for (int32_t i = 0; i < n_nodes; ++i) {
-      dp::need(begin[i] >= 0 && begin[i] <= end[i], "node segment out of order");
-      dp::need(ridx != nullptr || end[i] <= layout->n_rows, "row range beyond the matrix");
-      total += end[i] - begin[i];
-    }
-    const int64_t chunk = dp::hist_chunk_rows(*layout, total, n_nodes);
-    std::vector<dp::HistWork> work;
-    for (int32_t t = 0; t < layout->n_tiles; ++t)
-      for (int32_t i = 0; i < n_nodes; ++i)
-        for (int64_t b = begin[i]; b < end[i]; b += chunk)
-          work.push_back({i, t, b, std::min(b + chunk, end[i])});
-    hipStream_t s = as_stream(stream);
-    ws->begin(sizeof(dp::HistWork) * work.size() + 256);
-    dp::HistWork* d_work;
-    std::copy(work.begin(), work.end(), ws->stage(work.size(), &d_work));
-    ws->commit(s);
-    const int64_t per_node = int64_t(layout->n_features) * bin_stride * 2;
-    dp::launch_fill_i64(hist, per_node * n_nodes, 0, s);
-    dp::launch_hist(bins, *layout, gpair, ridx, d_work, int32_t(work.size()), bin_stride, hist, s);
+    hist_call(ws, bins, layout, gpair, ridx, begin, end, n_nodes, bin_stride, hist, stream, false);
+  });
+}
+
+int dp_hist_accumulate(dp_workspace ws, const uint8_t* bins, const dp_bin_layout* layout,
+                       const int32_t* gpair, const uint32_t* ridx, const int64_t* begin,
+                       const int64_t* end, int32_t n_nodes, int32_t bin_stride, int64_t* hist,
+                       void* stream) {
+  return guarded([&] {
+    hist_call(ws, bins, layout, gpair, ridx, begin, end, n_nodes, bin_stride, hist, stream, true);
   });
 }
 

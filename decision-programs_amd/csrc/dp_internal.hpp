@@ -165,8 +165,11 @@ void launch_iota_u32(uint32_t* p, int64_t n, hipStream_t s);
 void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t* gpair,
                  const uint32_t* ridx, const HistWork* work, int32_t n_work,
                  int32_t bin_stride, int64_t* hist, hipStream_t s);
-// Splits work into items of at most `chunk` rows per tile.
-int64_t hist_chunk_rows(const dp_bin_layout& layout, int64_t total_rows, int32_t n_nodes);
+// Work items for the histograms of n_nodes row sets (node i: [begin[i],
+// end[i]) of ridx, written to hist slot slots[i], or i when slots is null),
+// chunked and ordered for the XCD-aware dispatch; may contain empty items.
+std::vector<HistWork> make_hist_work(const dp_bin_layout& layout, const int64_t* begin,
+                                     const int64_t* end, const int32_t* slots, int32_t n_nodes);
 void launch_subtract(const int64_t* parent, const int64_t* built, int64_t* sibling, int64_t n,
                      hipStream_t s);
 

@@ -2,18 +2,17 @@
 //
 // The reference reaches this step only inside XGBoost's grow_gpu_hist updater
 // (native/class_native_training.cuh:67).  Design for CDNA4:
-//  * bins are uint8 in feature tiles of FT bytes per row (tile-major), so one
-//    lane reads 16 features of a row with one 128-bit load and a wavefront
-//    covers 64*16 contiguous bytes for contiguous rows;
-//  * each workgroup privatises the histogram of one tile in LDS as two int64
-//    planes (sum qg, sum qh) laid out [bin][feature], so the LDS word of
-//    (bin, f) sits in bank pair f mod 16 whatever the bin;
-//  * every lane walks its 16 features starting at a lane-dependent rotation,
-//    so at each step the 16 lanes of a group touch 16 different features and
-//    therefore 16 different bank pairs: the layout plus the rotation make the
-//    64-bit LDS atomics bank-conflict free for any bin values;
+//  * bins are uint8 in tiles of 16 features (tile-major: tile t holds 16 bytes
+//    per row), so one lane reads the 16 bins of a row with one 128-bit load and
+//    a wavefront of contiguous rows reads 1 KiB contiguous;
+//  * each workgroup privatises the histogram of one tile in 64 KiB of LDS (two
+//    workgroups per CU), as int64 fixed-point sums, see hist_kernel;
+//  * lane-dependent rotation of the 16 bytes keeps the 64-bit LDS atomics bank
+//    conflict free for any bin values (measured: zero SQ_LDS_BANK_CONFLICT);
 //  * sums are exact integers (fixed-point gradients), so the result does not
 //    depend on atomic order and equals the CPU restatement bit for bit;
+//  * work items are row chunks x tiles, ordered so the tiles of one chunk run on
+//    one XCD back to back (the chunk's gradients then come from that XCD's L2);
 //  * the workgroup merges its LDS histogram into the node histogram with
 //    64-bit global atomics, skipping empty bins.
 #include "dp_internal.hpp"
@@ -56,7 +55,10 @@ __device__ __forceinline__ void rotate16(uint32_t w[4], uint32_t rot) {
   w[3] = __builtin_amdgcn_alignbyte(b0, b3, s);
 }
 
-__device__ __forceinline__ void lds_add(unsigned long long* p, unsigned long long v) {
+typedef __attribute__((address_space(3))) unsigned long long lds_u64;
+typedef __attribute__((address_space(3))) unsigned char lds_u8;
+
+__device__ __forceinline__ void lds_add(lds_u64* p, unsigned long long v) {
   __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
@@ -64,98 +66,99 @@ __device__ __forceinline__ void global_add(unsigned long long* p, unsigned long 
   __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// FT: features per tile (16 or 32).  THREADS: workgroup size.  MISSING: the
-// matrix holds NaN, whose bin byte is skipped.
-template <int FT, int THREADS, bool MISSING>
-__global__ __launch_bounds__(THREADS) void hist_kernel(
+constexpr int kTile = 16;                // features per tile (bytes per row per tile)
+constexpr int kLdsWords = 256 * 2 * kTile;  // 64 KiB of int64
+constexpr int kHistThreads = 1024;
+constexpr int kHistUnroll = 2;           // rows per lane per pipeline stage
+
+// One work item = rows [begin, end) of node `slot` for one 16-feature tile.
+// LDS holds the tile's histogram as 256 rows of 256 bytes:
+//   row b = [ sum qg of features 0..15 | sum qh of features 0..15 ] (int64 each)
+// so the word of (b, f) is at byte b*256 + f*8 (g) and +128 (h).  A lane owns
+// one matrix row per pipeline step: one 128-bit load brings its 16 bin bytes.
+// The bytes are rotated by (lane & 15) so that at every one of the 16 steps the
+// 16 lanes of a group address 16 distinct features, i.e. 16 distinct bank pairs
+// (f*8 mod 128), whatever their bins: the 64-bit LDS atomics are conflict free.
+// The LDS address is assembled by one v_perm_b32: byte 1 = the bin byte, byte 0
+// = the lane's feature offset for that step.
+template <bool MISSING>
+__global__ __launch_bounds__(kHistThreads) void hist_kernel(
     const uint8_t* __restrict__ bins, int64_t n_rows, int32_t n_features,
     const int2* __restrict__ gpair, const uint32_t* __restrict__ ridx,
-    const HistWork* __restrict__ work, int32_t bin_stride, int32_t missing_bin,
+    const HistWork* __restrict__ work, int32_t bin_stride,
     unsigned long long* __restrict__ hist) {
-  extern __shared__ unsigned long long lds[];
-  constexpr int TPR = FT / 16;          // lanes per row
-  constexpr int ROWS = THREADS / TPR;   // rows per sweep of the workgroup
+  __shared__ unsigned long long lds[kLdsWords];
   const HistWork w = work[blockIdx.x];
-  const int plane = bin_stride * FT;
-  unsigned long long* gpl = lds;
-  unsigned long long* hpl = lds + plane;
-  for (int e = threadIdx.x; e < 2 * plane; e += THREADS) lds[e] = 0ull;
+  if (w.begin >= w.end) return;  // padding item (uniform per workgroup)
+  for (int e = threadIdx.x; e < kLdsWords; e += kHistThreads) lds[e] = 0ull;
   __syncthreads();
 
-  const int sub = threadIdx.x % TPR;
+  lds_u8* const lds_base = (lds_u8*)lds;
   const uint32_t rot = threadIdx.x & 15u;
-  const uint8_t* tile = bins + int64_t(w.tile) * n_rows * FT + sub * 16;
-  // byte offset of feature slot (sub*16 + ((k + rot) & 15)) in a plane row
-  uint32_t slot[16];
+  uint32_t slotw[4];  // byte i of slotw[m]: feature offset (bytes) of step 4m+i
 #pragma unroll
-  for (int k = 0; k < 16; ++k) slot[k] = uint32_t(sub * 16) + ((uint32_t(k) + rot) & 15u);
-
-  int64_t i = w.begin + threadIdx.x / TPR;
-  // Two rows in flight per lane.
-  for (; i + ROWS < w.end; i += 2 * ROWS) {
-    const uint32_t r0 = ridx ? ridx[i] : uint32_t(i);
-    const uint32_t r1 = ridx ? ridx[i + ROWS] : uint32_t(i + ROWS);
-    const uint4 v0 = *reinterpret_cast<const uint4*>(tile + int64_t(r0) * FT);
-    const uint4 v1 = *reinterpret_cast<const uint4*>(tile + int64_t(r1) * FT);
-    const int2 q0 = gpair[r0];
-    const int2 q1 = gpair[r1];
-    uint32_t a[4] = {v0.x, v0.y, v0.z, v0.w};
-    uint32_t b[4] = {v1.x, v1.y, v1.z, v1.w};
-    rotate16(a, rot);
-    rotate16(b, rot);
-    const unsigned long long g0 = (unsigned long long)(long long)q0.x;
-    const unsigned long long h0 = (unsigned long long)(long long)q0.y;
-    const unsigned long long g1 = (unsigned long long)(long long)q1.x;
-    const unsigned long long h1 = (unsigned long long)(long long)q1.y;
+  for (int m = 0; m < 4; ++m) {
+    uint32_t v = 0;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const uint32_t bin = (a[k >> 2] >> ((k & 3) * 8)) & 0xffu;
-      if (!MISSING || int(bin) != missing_bin) {
-        const uint32_t idx = bin * FT + slot[k];
-        lds_add(&gpl[idx], g0);
-        lds_add(&hpl[idx], h0);
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const uint32_t bin = (b[k >> 2] >> ((k & 3) * 8)) & 0xffu;
-      if (!MISSING || int(bin) != missing_bin) {
-        const uint32_t idx = bin * FT + slot[k];
-        lds_add(&gpl[idx], g1);
-        lds_add(&hpl[idx], h1);
-      }
-    }
+    for (int i = 0; i < 4; ++i) v |= (((uint32_t(4 * m + i) + rot) & 15u) * 8u) << (8 * i);
+    slotw[m] = v;
   }
-  if (i < w.end) {
-    const uint32_t r0 = ridx ? ridx[i] : uint32_t(i);
-    const uint4 v0 = *reinterpret_cast<const uint4*>(tile + int64_t(r0) * FT);
-    const int2 q0 = gpair[r0];
-    uint32_t a[4] = {v0.x, v0.y, v0.z, v0.w};
-    rotate16(a, rot);
-    const unsigned long long g0 = (unsigned long long)(long long)q0.x;
-    const unsigned long long h0 = (unsigned long long)(long long)q0.y;
+  const uint8_t* tile = bins + int64_t(w.tile) * n_rows * kTile;
+  constexpr int64_t kStep = int64_t(kHistThreads) * kHistUnroll;
+  uint4 v[2][kHistUnroll];
+  int2 q[2][kHistUnroll];
+  bool ok[2][kHistUnroll];
+  auto load = [&](int buf, int64_t at) {
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const uint32_t bin = (a[k >> 2] >> ((k & 3) * 8)) & 0xffu;
-      if (!MISSING || int(bin) != missing_bin) {
-        const uint32_t idx = bin * FT + slot[k];
-        lds_add(&gpl[idx], g0);
-        lds_add(&hpl[idx], h0);
+    for (int u = 0; u < kHistUnroll; ++u) {
+      const int64_t i = at + int64_t(u) * kHistThreads;
+      ok[buf][u] = i < w.end;
+      if (ok[buf][u]) {
+        const uint32_t r = ridx ? ridx[i] : uint32_t(i);
+        v[buf][u] = *reinterpret_cast<const uint4*>(tile + int64_t(r) * kTile);
+        q[buf][u] = gpair[r];
       }
     }
+  };
+  auto process = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < kHistUnroll; ++u) {
+      if (!ok[buf][u]) continue;
+      uint32_t a[4] = {v[buf][u].x, v[buf][u].y, v[buf][u].z, v[buf][u].w};
+      rotate16(a, rot);
+      const unsigned long long g = (unsigned long long)(long long)q[buf][u].x;
+      const unsigned long long h = (unsigned long long)(long long)q[buf][u].y;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const uint32_t sel = 0x0c0c0000u | ((4u + uint32_t(k & 3)) << 8) | uint32_t(k & 3);
+        const uint32_t off = __builtin_amdgcn_perm(a[k >> 2], slotw[k >> 2], sel);
+        if (MISSING && off >= 255u * 256u) continue;  // bin byte 255 = missing
+        lds_u64* p = (lds_u64*)(lds_base + off);
+        lds_add(p, g);
+        lds_add(p + 16, h);
+      }
+    }
+  };
+  // The loop bound is uniform per workgroup; rows past `end` are masked.
+  const int64_t lane = threadIdx.x;
+  load(0, w.begin + lane);
+  for (int64_t blk = w.begin; blk < w.end; blk += 2 * kStep) {
+    load(1, blk + kStep + lane);
+    process(0);
+    load(0, blk + 2 * kStep + lane);
+    process(1);
   }
   __syncthreads();
 
-  const int f0 = w.tile * FT;
   unsigned long long* out = hist + int64_t(w.slot) * n_features * bin_stride * 2;
-  for (int e = threadIdx.x; e < plane; e += THREADS) {
-    const int bin = e / FT, f = f0 + e % FT;
-    if (f >= n_features) continue;
-    const unsigned long long g = gpl[e], h = hpl[e];
-    if ((g | h) == 0ull) continue;
-    unsigned long long* cell = out + (int64_t(f) * bin_stride + bin) * 2;
-    global_add(cell, g);
-    global_add(cell + 1, h);
+  const int f0 = w.tile * kTile;
+  for (int e = threadIdx.x; e < kLdsWords; e += kHistThreads) {
+    const int bin = e >> 5, within = e & 31;
+    const int f = f0 + (within & 15);
+    if (f >= n_features || bin >= bin_stride) continue;
+    const unsigned long long x = lds[e];
+    if (x == 0ull) continue;
+    global_add(out + (int64_t(f) * bin_stride + bin) * 2 + (within >> 4), x);
   }
 }
 
@@ -181,25 +184,6 @@ __global__ void subtract_many_kernel(const int64_t* __restrict__ base_parent,
     s[i] = p[i] - c[i];
 }
 
-template <int FT, int THREADS, bool MISSING>
-void launch_hist_t(const uint8_t* bins, const dp_bin_layout& layout, const int32_t* gpair,
-                   const uint32_t* ridx, const HistWork* work, int32_t n_work, int32_t bin_stride,
-                   int64_t* hist, hipStream_t s) {
-  const size_t lds = size_t(2) * bin_stride * FT * sizeof(unsigned long long);
-  auto kernel = hist_kernel<FT, THREADS, MISSING>;
-  static bool configured = false;
-  if (!configured) {
-    DP_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-    configured = true;
-  }
-  hipLaunchKernelGGL(kernel, dim3(n_work), dim3(THREADS), lds, s, bins, layout.n_rows,
-                     layout.n_features, reinterpret_cast<const int2*>(gpair), ridx, work,
-                     bin_stride, layout.missing_bin,
-                     reinterpret_cast<unsigned long long*>(hist));
-  DP_HIP(hipGetLastError());
-}
-
 }  // namespace
 
 void launch_fill_i64(int64_t* p, int64_t n, int64_t value, hipStream_t s) {
@@ -220,14 +204,36 @@ void launch_iota_u32(uint32_t* p, int64_t n, hipStream_t s) {
   DP_HIP(hipGetLastError());
 }
 
-int64_t hist_chunk_rows(const dp_bin_layout& layout, int64_t total_rows, int32_t n_nodes) {
-  // Aim for about 1024 work items over the whole launch, with at least 2048
-  // rows per item so the LDS merge stays small next to the row work.
-  const int64_t items = 1024;
-  int64_t per = (total_rows * layout.n_tiles + items - 1) / items;
-  (void)n_nodes;
-  if (per < 2048) per = 2048;
-  return per;
+std::vector<HistWork> make_hist_work(const dp_bin_layout& layout, const int64_t* begin,
+                                     const int64_t* end, const int32_t* slots, int32_t n_nodes) {
+  // About 1024 items (two waves of 2 workgroups per CU on 256 CUs), at least
+  // 4096 rows each, so the per-item LDS merge stays small.
+  int64_t total = 0;
+  for (int32_t i = 0; i < n_nodes; ++i) total += end[i] - begin[i];
+  int64_t chunk = (total * layout.n_tiles + 1023) / 1024;
+  if (chunk < 4096) chunk = 4096;
+  struct Chunk {
+    int32_t slot;
+    int64_t b, e;
+  };
+  std::vector<Chunk> chunks;
+  for (int32_t i = 0; i < n_nodes; ++i)
+    for (int64_t b = begin[i]; b < end[i]; b += chunk)
+      chunks.push_back({slots ? slots[i] : i, b, std::min(b + chunk, end[i])});
+  // Blocks are dispatched round-robin over the 8 XCDs (block id mod 8).  Item
+  // order puts the tiles of one row chunk on the same XCD in consecutive
+  // dispatch slots, so that chunk's gradient pairs are read from HBM once and
+  // then hit that XCD's L2.
+  const int64_t T = layout.n_tiles;
+  const int64_t groups = (int64_t(chunks.size()) + 7) / 8;
+  std::vector<HistWork> work(size_t(groups * T * 8), HistWork{0, 0, 0, 0});
+  for (int64_t c = 0; c < int64_t(chunks.size()); ++c)
+    for (int64_t t = 0; t < T; ++t) {
+      const int64_t b = ((c / 8) * T + t) * 8 + (c % 8);
+      work[size_t(b)] = {chunks[size_t(c)].slot, int32_t(t), chunks[size_t(c)].b,
+                         chunks[size_t(c)].e};
+    }
+  return work;
 }
 
 void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t* gpair,
@@ -235,19 +241,18 @@ void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t
                  int64_t* hist, hipStream_t s) {
   if (n_work <= 0) return;
   need(bin_stride >= 1 && bin_stride <= kMaxBins, "histogram bin stride out of range");
-  const bool missing = layout.missing_bin >= 0;
-  switch (layout.tile_width) {
-    case 16:
-      if (missing) launch_hist_t<16, 512, true>(bins, layout, gpair, ridx, work, n_work, bin_stride, hist, s);
-      else launch_hist_t<16, 512, false>(bins, layout, gpair, ridx, work, n_work, bin_stride, hist, s);
-      break;
-    case 32:
-      if (missing) launch_hist_t<32, 1024, true>(bins, layout, gpair, ridx, work, n_work, bin_stride, hist, s);
-      else launch_hist_t<32, 1024, false>(bins, layout, gpair, ridx, work, n_work, bin_stride, hist, s);
-      break;
-    default:
-      fail("unsupported tile width " + std::to_string(layout.tile_width));
+  need(layout.tile_width == kTile, "histogram kernel needs 16-feature tiles");
+  auto* out = reinterpret_cast<unsigned long long*>(hist);
+  const auto* gp = reinterpret_cast<const int2*>(gpair);
+  if (layout.missing_bin >= 0) {
+    need(layout.missing_bin == 255, "missing bin must be 255");
+    hipLaunchKernelGGL(hist_kernel<true>, dim3(n_work), dim3(kHistThreads), 0, s, bins,
+                       layout.n_rows, layout.n_features, gp, ridx, work, bin_stride, out);
+  } else {
+    hipLaunchKernelGGL(hist_kernel<false>, dim3(n_work), dim3(kHistThreads), 0, s, bins,
+                       layout.n_rows, layout.n_features, gp, ridx, work, bin_stride, out);
   }
+  DP_HIP(hipGetLastError());
 }
 
 void launch_subtract(const int64_t* parent, const int64_t* built, int64_t* sibling, int64_t n,

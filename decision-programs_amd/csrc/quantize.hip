@@ -257,23 +257,10 @@ void launch_bin_values(const float* values, const dp_bin_layout& layout, const i
   const int rows_per_block = 256 / (layout.tile_width / 16);
   const int gx = grid_for(layout.n_rows, rows_per_block, 4096);
   const size_t lds = size_t(layout.tile_width) * stride * sizeof(float);
-  if (layout.tile_width == 16) {
-    hipLaunchKernelGGL(bin_kernel<16>, dim3(gx, layout.n_tiles), dim3(256), lds, s, values,
-                       layout.n_rows, layout.n_features, cut_ptr, cut_values, stride,
-                       layout.missing_bin, bins);
-  } else if (layout.tile_width == 32) {
-    static bool configured = false;
-    if (!configured) {
-      DP_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(bin_kernel<32>),
-                                 hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024));
-      configured = true;
-    }
-    hipLaunchKernelGGL(bin_kernel<32>, dim3(gx, layout.n_tiles), dim3(256), lds, s, values,
-                       layout.n_rows, layout.n_features, cut_ptr, cut_values, stride,
-                       layout.missing_bin, bins);
-  } else {
-    fail("unsupported tile width");
-  }
+  need(layout.tile_width == 16, "binning needs 16-feature tiles");
+  hipLaunchKernelGGL(bin_kernel<16>, dim3(gx, layout.n_tiles), dim3(256), lds, s, values,
+                     layout.n_rows, layout.n_features, cut_ptr, cut_values, stride,
+                     layout.missing_bin, bins);
   DP_HIP(hipGetLastError());
 }
 

@@ -138,6 +138,17 @@ def hist_build(ws, bins, lay, gpair, segments, bin_stride, ridx=None, out=None):
     return out
 
 
+def hist_accumulate(ws, bins, lay, gpair, segments, hist, ridx=None):
+    """Adds the histograms of row segments into `hist` [n_nodes, F, stride, 2]."""
+    seg = np.asarray(segments, dtype=np.int64).reshape(-1, 2)
+    begin = np.ascontiguousarray(seg[:, 0])
+    end = np.ascontiguousarray(seg[:, 1])
+    check(load().dp_hist_accumulate(ws.handle, _ptr(bins), ctypes.byref(lay), _ptr(gpair),
+                                    _ptr(ridx), begin.ctypes.data, end.ctypes.data, seg.shape[0],
+                                    hist.shape[2], _ptr(hist), _stream()))
+    return hist
+
+
 def hist_subtract(parent, built):
     import torch
 

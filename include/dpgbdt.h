@@ -159,12 +159,12 @@ int dp_workspace_free(dp_workspace ws);
 typedef struct {
   int64_t n_rows;
   int32_t n_features;
-  int32_t tile_width;   /* features per tile: 16, 32 or 64 */
+  int32_t tile_width;   /* features per tile: 16 */
   int32_t n_tiles;
   int32_t missing_bin;  /* -1 when the matrix holds no NaN, else 255 */
 } dp_bin_layout;
 
-/* Fills `out`; tile_width 0 picks the default for n_features. */
+/* Fills `out`; tile_width 0 selects the default (16). */
 int dp_layout_init(int64_t n_rows, int32_t n_features, int32_t tile_width, int32_t missing_bin,
                    dp_bin_layout* out);
 size_t dp_layout_bytes(const dp_bin_layout* layout);
@@ -205,6 +205,13 @@ int dp_hist_build(dp_workspace ws, const uint8_t* bins, const dp_bin_layout* lay
                   const int32_t* gpair, const uint32_t* ridx, const int64_t* begin,
                   const int64_t* end, int32_t n_nodes, int32_t bin_stride, int64_t* hist,
                   void* stream);
+
+/* As dp_hist_build but adds into hist instead of overwriting it (batches of
+ * rows, e.g. several device-resident row blocks, summed into one histogram). */
+int dp_hist_accumulate(dp_workspace ws, const uint8_t* bins, const dp_bin_layout* layout,
+                       const int32_t* gpair, const uint32_t* ridx, const int64_t* begin,
+                       const int64_t* end, int32_t n_nodes, int32_t bin_stride, int64_t* hist,
+                       void* stream);
 
 /* sibling = parent - built, element-wise over n int64 values. */
 int dp_hist_subtract(const int64_t* parent, const int64_t* built, int64_t* sibling, int64_t n,
