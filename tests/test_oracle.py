@@ -1,0 +1,333 @@
+"""Pins the CPU oracle (oracle/dp_oracle.c) to what the mathematics fixes.
+
+XGBoost 3.4.1 -- where the reference's implementation of this path lives --
+is absent, and the reference holds no numeric fixtures for it, so each oracle
+function is checked against something independent of its own formula:
+
+  expf            float64 numpy exp (ulp bound)
+  cuts / bins     the stated quantile definition via numpy sort/unique, the
+                  quantile property, np.searchsorted and the routing identity
+                  x < cut[b]  <=>  bin(x) <= b
+  gradients       float64 closed forms (sigmoid, softmax) and sum_k g_k = 0
+  quantiser       round-to-nearest of x * 2^e, |q| <= 2^30, frexp exponent
+  histogram       int64 np.add.at per feature; counts = np.bincount; the
+                  OpenMP version equals the serial one
+  subtraction     hist(P) = hist(L) + hist(R) for a random partition
+  gain / weight   numerical minimisation (scipy) of the regularised
+                  second-order objective G w + (H + lambda) w^2 / 2 + alpha |w|
+  split search    brute force over every (feature, threshold, missing side)
+                  computed from raw rows, not from histograms
+  partition       stable order of numpy masks
+  tree            an independent pure-Python depth-wise builder on raw rows
+"""
+import numpy as np
+import pytest
+from scipy.optimize import minimize_scalar
+
+
+def ulp_distance(a, b):
+    a = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    b = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    a = np.where(a < 0, np.int64(-2**31) - a, a)
+    b = np.where(b < 0, np.int64(-2**31) - b, b)
+    return np.abs(a - b)
+
+
+def test_expf_ulp(oracle):
+    xs = np.linspace(-86.9, 88.7, 200001, dtype=np.float32)
+    got = np.array([oracle.expf(x) for x in xs[::7]], dtype=np.float32)
+    ref = np.exp(xs[::7].astype(np.float64)).astype(np.float32)
+    assert ulp_distance(got, ref).max() <= 2
+    assert oracle.expf(0.0) == 1.0
+    assert oracle.expf(-100.0) == 0.0
+    assert np.isinf(oracle.expf(89.0))
+    assert np.isnan(oracle.expf(float("nan")))
+
+
+def _expected_cuts(col, max_bin):
+    """The stated exact quantile definition, via numpy."""
+    v = col[~np.isnan(col)].astype(np.float32)
+    v = np.where(v == 0, np.float32(0), v)
+    if v.size == 0:
+        return np.array([np.float32(1e-5)], np.float32)
+    v = np.sort(v)
+    u = np.unique(v)
+    last = np.float32(v[-1] + (np.float32(abs(v[-1])) + np.float32(1e-5)))
+    if u.size <= max_bin:
+        return np.concatenate([u[1:], [last]]).astype(np.float32)
+    out, prev = [], v[0]
+    for i in range(1, max_bin):
+        c = v[(i * v.size) // max_bin]
+        if c > prev:
+            out.append(c)
+            prev = c
+    return np.array(out + [last], np.float32)
+
+
+@pytest.mark.parametrize("max_bin", [2, 16, 64, 255, 256])
+def test_cuts_definition_and_quantiles(oracle, max_bin):
+    rng = np.random.default_rng(max_bin)
+    n = 5000
+    x = np.stack([rng.normal(size=n), rng.lognormal(size=n), rng.integers(0, 16, n),
+                  rng.integers(0, 400, n), np.full(n, 3.5), np.full(n, np.nan)],
+                 axis=1).astype(np.float32)
+    x[rng.random(n) < 0.3, 1] = np.nan
+    x[:5, 2] = -0.0
+    cut_ptr, cuts, mins = oracle.compute_cuts(x, max_bin)
+    for f in range(x.shape[1]):
+        c = cuts[cut_ptr[f]:cut_ptr[f + 1]]
+        np.testing.assert_array_equal(c.view(np.uint32), _expected_cuts(x[:, f], max_bin).view(np.uint32))
+        assert np.all(np.diff(c) > 0) and 1 <= c.size <= max_bin
+    # quantile property: continuous feature, bins hold ~n/max_bin rows each
+    bins = oracle.bin_matrix(x, cut_ptr, cuts, 255 if max_bin <= 255 else -1)
+    counts = np.bincount(bins[:, 0], minlength=max_bin)[: cut_ptr[1] - cut_ptr[0]]
+    assert counts.max() <= 2 * n / max_bin + 2
+
+
+def test_binning_routing_identity(oracle):
+    rng = np.random.default_rng(5)
+    x = rng.normal(size=(3000, 4)).astype(np.float32)
+    x[::11, 2] = np.nan
+    cut_ptr, cuts, _ = oracle.compute_cuts(x, 32)
+    bins = oracle.bin_matrix(x, cut_ptr, cuts, 255)
+    for f in range(4):
+        c = cuts[cut_ptr[f]:cut_ptr[f + 1]]
+        col = x[:, f]
+        ok = ~np.isnan(col)
+        expect = np.minimum(np.searchsorted(c, col[ok], side="right"), c.size - 1)
+        np.testing.assert_array_equal(bins[ok, f], expect)
+        assert np.all(bins[~ok, f] == 255)
+        for b in range(c.size):  # x < cut[b]  <=>  bin <= b
+            np.testing.assert_array_equal(col[ok] < c[b], bins[ok, f] <= b)
+
+
+def test_gradients_closed_forms(oracle):
+    rng = np.random.default_rng(9)
+    n, k = 4000, 5
+    m = (rng.normal(size=n) * 3).astype(np.float32)
+    y = rng.integers(0, 2, n).astype(np.float32)
+    g, h = oracle.gradients(oracle.OBJ_LOGISTIC, m, y, 1)
+    p = 1 / (1 + np.exp(-m.astype(np.float64)))
+    np.testing.assert_allclose(g[:, 0], p - y, rtol=0, atol=3e-7)
+    # float32 1 - p cancels near p = 1: bound the error by a few ulp of 1
+    np.testing.assert_allclose(h[:, 0], np.maximum(p * (1 - p), 1e-16), rtol=3e-6, atol=2e-7)
+    mm = (rng.normal(size=(n, k)) * 3).astype(np.float32)
+    yy = rng.integers(0, k, n).astype(np.float32)
+    g, h = oracle.gradients(oracle.OBJ_SOFTPROB, mm, yy, k)
+    e = np.exp(mm - mm.max(axis=1, keepdims=True))
+    sp = e / e.sum(axis=1, keepdims=True)
+    onehot = np.eye(k)[yy.astype(int)]
+    np.testing.assert_allclose(g, sp - onehot, atol=3e-7)
+    np.testing.assert_allclose(h, np.maximum(2 * sp * (1 - sp), 1e-16), rtol=3e-6, atol=4e-7)
+    assert np.abs(g.astype(np.float64).sum(axis=1)).max() < 1e-6
+    g, h = oracle.gradients(oracle.OBJ_SQUARED, m, y, 1)
+    np.testing.assert_array_equal(g[:, 0], m - y)
+    assert np.all(h == 1)
+
+
+def test_quantiser_round_to_nearest(oracle):
+    rng = np.random.default_rng(1)
+    g = (rng.normal(size=10000) * 7).astype(np.float32)
+    h = rng.uniform(0.01, 0.25, 10000).astype(np.float32)
+    eg, eh, qg, qh = oracle.quantise(g, h)[0]
+    assert eg == 30 - np.frexp(np.abs(g).max())[1]
+    assert eh == 30 - np.frexp(np.abs(h).max())[1]
+    np.testing.assert_array_equal(qg, np.rint(np.ldexp(g.astype(np.float64), eg)).astype(np.int32))
+    np.testing.assert_array_equal(qh, np.rint(np.ldexp(h.astype(np.float64), eh)).astype(np.int32))
+    assert np.abs(qg).max() <= 2**30 and np.abs(qg).max() > 2**29
+    assert oracle.unscale(eg) == 2.0 ** -eg
+
+
+def _quantised_case(oracle, n=2000, f=6, nb=24, seed=3, missing=True):
+    rng = np.random.default_rng(seed)
+    x = rng.normal(size=(n, f)).astype(np.float32)
+    x[:, 1] = rng.integers(0, 5, n)
+    if missing:
+        x[rng.random((n, f)) < 0.15] = np.nan
+    cut_ptr, cuts, _ = oracle.compute_cuts(x, nb)
+    mb = 255 if missing else -1
+    bins = oracle.bin_matrix(x, cut_ptr, cuts, mb)
+    g = rng.normal(size=n).astype(np.float32)
+    h = rng.uniform(0.05, 1.0, n).astype(np.float32)
+    eg, eh, qg, qh = oracle.quantise(g, h)[0]
+    return x, bins, cut_ptr, cuts, mb, qg, qh, eg, eh
+
+
+def test_histogram_counts_and_parallel(oracle):
+    x, bins, cut_ptr, cuts, mb, qg, qh, eg, eh = _quantised_case(oracle)
+    hist = oracle.hist(bins, qg, qh, bin_stride=32, missing_bin=mb)
+    for f in range(bins.shape[1]):
+        keep = bins[:, f] != mb
+        ref = np.zeros((32, 2), np.int64)
+        np.add.at(ref[:, 0], bins[keep, f], qg[keep].astype(np.int64))
+        np.add.at(ref[:, 1], bins[keep, f], qh[keep].astype(np.int64))
+        np.testing.assert_array_equal(hist[f], ref)
+    counts = oracle.hist(bins, np.ones_like(qg), np.zeros_like(qh), bin_stride=32, missing_bin=mb)
+    for f in range(bins.shape[1]):
+        keep = bins[:, f] != mb
+        np.testing.assert_array_equal(counts[f, :, 0], np.bincount(bins[keep, f], minlength=32))
+    par = oracle.hist_parallel(bins, qg, qh, bin_stride=32, missing_bin=mb, threads=4)
+    np.testing.assert_array_equal(par, hist)
+
+
+def test_subtraction_identity(oracle):
+    x, bins, cut_ptr, cuts, mb, qg, qh, eg, eh = _quantised_case(oracle, seed=8)
+    rng = np.random.default_rng(0)
+    perm = rng.permutation(bins.shape[0]).astype(np.uint32)
+    left, right = perm[:700], perm[700:]
+    hp = oracle.hist(bins, qg, qh, bin_stride=32, missing_bin=mb)
+    hl = oracle.hist(bins, qg, qh, rows=left, bin_stride=32, missing_bin=mb)
+    hr = oracle.hist(bins, qg, qh, rows=right, bin_stride=32, missing_bin=mb)
+    np.testing.assert_array_equal(hp, hl + hr)
+
+
+@pytest.mark.parametrize("lam,alpha,mcw", [(1.0, 0.0, 1.0), (0.5, 0.8, 0.0), (0.0, 2.0, 3.0)])
+def test_gain_and_weight_minimise_objective(oracle, lam, alpha, mcw):
+    """gain(G,H) = -2 min_w [G w + (H+lambda) w^2/2 + alpha|w|], weight = argmin."""
+    p = oracle.params(lam=lam, alpha=alpha, min_child_weight=mcw)
+    rng = np.random.default_rng(2)
+    for _ in range(40):
+        G = float(rng.normal() * 5)
+        H = float(rng.uniform(0.1, 10.0))
+        res = minimize_scalar(lambda w: G * w + 0.5 * (H + lam) * w * w + alpha * abs(w),
+                              bounds=(-1e3, 1e3), method="bounded", options={"xatol": 1e-12})
+        if H < mcw:
+            assert oracle.calc_gain(p, G, H) == 0.0 and oracle.calc_weight(p, G, H) == 0.0
+            continue
+        assert abs(oracle.calc_gain(p, G, H) + 2 * res.fun) < 1e-6 * max(1.0, abs(res.fun))
+        assert abs(oracle.calc_weight(p, G, H) - res.x) < 1e-5
+
+
+def _brute_force_split(bins, qg, qh, rows, nb_per_feature, mb, ug, uh, p):
+    """Every (feature, bin, missing side) from raw row selections; tie rule:
+    larger loss, then lower feature, then lower bin, then missing-right."""
+    lam, alpha, mcw = float(p.lambda_), float(p.alpha), float(p.min_child_weight)
+
+    def gain(G, H):
+        if H < mcw or H <= 0:
+            return 0.0
+        t = G - alpha if G > alpha else (G + alpha if G < -alpha else 0.0)
+        return (t * t) / (H + lam)
+
+    qg_r = qg[rows].astype(np.int64)
+    qh_r = qh[rows].astype(np.int64)
+    GP, HP = int(qg_r.sum()), int(qh_r.sum())
+    parent = gain(GP * ug, HP * uh)
+    best = (-np.inf, None)
+    for f in range(bins.shape[1]):
+        col = bins[rows, f].astype(np.int64)
+        miss = col == mb
+        for b in range(nb_per_feature[f]):
+            for dl in (0, 1):
+                left = (~miss & (col <= b)) | (miss & bool(dl))
+                gl, hl = int(qg_r[left].sum()), int(qh_r[left].sum())
+                gr, hr = GP - gl, HP - hl
+                if hl <= 0 or hr <= 0 or hl * uh < mcw or hr * uh < mcw:
+                    continue
+                loss = (gain(gl * ug, hl * uh) + gain(gr * ug, hr * uh)) - parent
+                key = (loss, -f, -b, -dl)
+                if best[1] is None or key > best[0]:
+                    best = (key, (f, b, dl, gl, hl))
+    return best
+
+
+@pytest.mark.parametrize("seed", [3, 4, 5])
+def test_split_search_matches_brute_force(oracle, seed):
+    x, bins, cut_ptr, cuts, mb, qg, qh, eg, eh = _quantised_case(oracle, n=300, f=4, nb=8,
+                                                                  seed=seed)
+    nbf = np.diff(cut_ptr).astype(np.int32)
+    rows = np.arange(0, 300, 2, dtype=np.uint32)
+    for p in (oracle.params(), oracle.params(lam=0.0, alpha=0.3, min_child_weight=2.0)):
+        hist = oracle.hist(bins, qg, qh, rows=rows, bin_stride=8, missing_bin=mb)
+        got = oracle.evaluate_split(hist, nbf, qg[rows].astype(np.int64).sum(),
+                                    qh[rows].astype(np.int64).sum(), eg, eh, p)
+        key, val = _brute_force_split(bins, qg, qh, rows, nbf, mb, oracle.unscale(eg),
+                                      oracle.unscale(eh), p)
+        assert got["valid"] == 1
+        assert (got["feature"], got["bin"], got["default_left"], got["gl"], got["hl"]) == val
+        assert got["loss_chg"] == key[0]
+
+
+def test_partition_is_stable(oracle):
+    x, bins, cut_ptr, cuts, mb, qg, qh, eg, eh = _quantised_case(oracle, seed=11)
+    rng = np.random.default_rng(3)
+    ridx = rng.permutation(bins.shape[0]).astype(np.uint32)
+    for feat, b, dl in [(0, 5, 0), (1, 2, 1), (3, 0, 1)]:
+        out, nl = oracle.partition(ridx, 100, 1500, bins, feat, b, dl, mb)
+        seg = ridx[100:1500]
+        col = bins[seg, feat].astype(np.int64)
+        left = np.where(col == mb, bool(dl), col <= b)
+        np.testing.assert_array_equal(out[100:1500], np.concatenate([seg[left], seg[~left]]))
+        assert nl == left.sum()
+        np.testing.assert_array_equal(out[:100], ridx[:100])
+        np.testing.assert_array_equal(out[1500:], ridx[1500:])
+
+
+def _reference_tree(bins, qg, qh, cut_ptr, mb, ug, uh, p):
+    """Independent depth-wise builder on raw rows (no histograms, no subtraction)."""
+    nbf = np.diff(cut_ptr).astype(np.int32)
+    nodes = [{"rows": np.arange(bins.shape[0], dtype=np.uint32), "depth": 0}]
+    out = []
+    level = [0]
+    while level:
+        nxt = []
+        for nid in level:
+            nd = nodes[nid]
+            rec = {"nid": nid, "left": -1}
+            if nd["depth"] < p.max_depth:
+                key, val = _brute_force_split(bins, qg, qh, nd["rows"], nbf, mb, ug, uh, p)
+                if val is not None and key[0] > 1e-6 and key[0] >= p.gamma:
+                    f, b, dl, gl, hl = val
+                    col = bins[nd["rows"], f].astype(np.int64)
+                    left = np.where(col == mb, bool(dl), col <= b)
+                    lid, rid = len(nodes), len(nodes) + 1
+                    nodes.append({"rows": nd["rows"][left], "depth": nd["depth"] + 1})
+                    nodes.append({"rows": nd["rows"][~left], "depth": nd["depth"] + 1})
+                    rec.update(left=lid, right=rid, feature=f, bin=b, dl=dl)
+                    nxt += [lid, rid]
+            out.append(rec)
+        level = nxt
+    out.sort(key=lambda r: r["nid"])
+    return out, nodes
+
+
+def test_tree_matches_independent_builder(oracle):
+    x, bins, cut_ptr, cuts, mb, qg, qh, eg, eh = _quantised_case(oracle, n=400, f=3, nb=6, seed=21)
+    p = oracle.params(max_depth=4, eta=0.5)
+    tree, ridx = oracle.grow_tree(bins, cut_ptr, cuts, mb, qg, qh, eg, eh, p, bin_stride=8)
+    ref, nodes = _reference_tree(bins, qg, qh, cut_ptr, mb, oracle.unscale(eg), oracle.unscale(eh), p)
+    assert len(ref) == len(tree["left"])
+    for r in ref:
+        nid = r["nid"]
+        assert tree["left"][nid] == r["left"]
+        if r["left"] != -1:
+            assert (tree["right"][nid], tree["feature"][nid], tree["split_bin"][nid],
+                    tree["default_left"][nid]) == (r["right"], r["feature"], r["bin"], r["dl"])
+        else:
+            rows = nodes[nid]["rows"]
+            G = qg[rows].astype(np.int64).sum() * oracle.unscale(eg)
+            H = qh[rows].astype(np.int64).sum() * oracle.unscale(eh)
+            assert tree["leaf_value"][nid] == np.float32(oracle.calc_weight(p, G, H) * 0.5)
+            np.testing.assert_array_equal(np.sort(ridx[tree["seg_begin"][nid]:tree["seg_end"][nid]]),
+                                          np.sort(rows))
+    # routing of the float matrix through split_conditions agrees with the partition
+    pos = oracle.positions(tree, ridx, bins.shape[0])
+    leaf_of = {nid: tree["leaf_value"][nid] for nid in range(len(tree["left"]))}
+    pred = oracle.predict_tree(tree, x)
+    np.testing.assert_array_equal(pred, np.array([leaf_of[i] for i in pos], np.float32))
+
+
+def test_booster_reduces_logloss(oracle):
+    rng = np.random.default_rng(0)
+    n = 3000
+    x = rng.uniform(size=(n, 4)).astype(np.float32)
+    y = (rng.uniform(size=n) < 1 / (1 + np.exp(-(4 * x[:, 0] - 2 + 3 * x[:, 1] * x[:, 2])))).astype(np.float32)
+    cut_ptr, cuts, _ = oracle.compute_cuts(x, 64)
+    bins = oracle.bin_matrix(x, cut_ptr, cuts, -1)
+    trees, margin, _ = oracle.train(bins, cut_ptr, cuts, -1, oracle.OBJ_LOGISTIC, y, 1,
+                                    oracle.params(eta=0.3, max_depth=3), 10, bin_stride=64)
+    p = 1 / (1 + np.exp(-margin[:, 0].astype(np.float64)))
+    ll = -np.mean(y * np.log(p) + (1 - y) * np.log(1 - p))
+    assert ll < 0.69 * 0.85
+    walked = sum(oracle.predict_tree(t, x) for t in trees)
+    np.testing.assert_allclose(walked, margin[:, 0], atol=1e-5)
