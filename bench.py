@@ -187,7 +187,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--rows", type=int, default=10_000_000)
-    ap.add_argument("--mode", choices=["full", "hist", "copy"], default="full")
+    ap.add_argument("--mode", choices=["full", "hist", "copy", "c2"], default="full")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=1_000_000)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -204,6 +204,9 @@ def main():
     dp.load()
     if args.mode == "copy":
         copy_leg(torch, args)
+        return
+    if args.mode == "c2":  # C2 boosting rounds only (for kernel-trace profiles)
+        print(json.dumps(trees_leg(torch, dp, ops, 1_000_000, 2, 100, 8, 0.1, injected=False)))
         return
     hist, sample, *_ = hist_leg(args, torch, dp, ops)
     log(f"hist: {hist['avg_ms']:.3f} ms/launch, {hist['achieved_gbs']:.0f} GB/s algorithmic")

@@ -1,4 +1,4 @@
-// Training objects: quantised matrix cache, level-wise tree grower, booster.
+// Training objects: quantised matrix cache, depth-wise tree grower, booster.
 //
 // The booster reproduces what the reference obtains from XGBoost 3.4.1 through
 // XGBoosterUpdateOneIter with tree_method=hist on the GPU
@@ -6,36 +6,29 @@
 // round, grown level by level.  Per level the device runs
 //   histogram build of the smaller child of every pair (gather by row ids)
 //   -> sibling = parent - built -> split evaluation -> stable partition
-// and the host reads back one small record per node (split and left count)
-// to number the children and compute leaf weights.
+//   -> planner (node records, child numbering, next level's work, leaf work)
+//   -> margin update of the level's leaves
+// with every count read from device memory, so a round's trees are enqueued
+// back to back and the host reads the node records once per round.
 #include "booster.hpp"
 
 #include <algorithm>
 #include <climits>
 #include <cmath>
+#include <charconv>
 #include <cstdlib>
+#include <limits>
 
 #include "json.hpp"
+#include "predict.hpp"
 
 namespace dp {
 
 void launch_any_nan(const float* values, int64_t n, int32_t* flag, hipStream_t s);
-void launch_leaf_positions(const uint32_t* ridx, const LeafWork* work, int32_t n_work,
-                           int32_t* positions, hipStream_t s);
+void launch_check_labels(const float* label, int64_t n, int32_t objective, int32_t n_classes,
+                         int32_t* bad, hipStream_t s);
 
 namespace {
-
-double threshold_l1(double g, double alpha) {
-  if (g > alpha) return g - alpha;
-  if (g < -alpha) return g + alpha;
-  return 0.0;
-}
-
-// Leaf weight -T(G)/(H + lambda); 0 when H < min_child_weight or H <= 0.
-double calc_weight(const TrainParam& p, double g, double h) {
-  if (h < double(p.min_child_weight) || h <= 0.0) return 0.0;
-  return -threshold_l1(g, double(p.alpha)) / (h + double(p.lambda));
-}
 
 float parse_float(const std::string& key, const std::string& v) {
   char* end = nullptr;
@@ -54,6 +47,78 @@ int32_t parse_int(const std::string& key, const std::string& v) {
 }
 
 }  // namespace
+
+// ---------------------------------------------------------------------------
+// Hyperparameter validation (the reference's rules, class_native_training.cuh:16-33)
+// ---------------------------------------------------------------------------
+std::string validate_hyperparameters(const std::string& text, uint32_t classes) {
+  const json::Value in = json::parse(text);
+  need(in.kind == json::Value::Object, "hyperparameters must be an object");
+  static const char* allowed[] = {"rounds", "max_depth", "eta", "lambda", "alpha", "gamma",
+                                  "min_child_weight", "max_bin", "seed", "subsample",
+                                  "colsample_bytree", "colsample_bylevel", "colsample_bynode"};
+  for (const auto& m : in.members) {
+    bool ok = false;
+    for (const char* a : allowed) ok = ok || m.first == a;
+    need(ok, "unsupported training hyperparameter: " + m.first);
+  }
+  auto integer = [&](const json::Value& v, const std::string& name, uint64_t maximum) {
+    need(v.kind == json::Value::Number && v.text.find_first_of(".eEn") == std::string::npos &&
+             v.text != "Infinity" && v.text != "+Infinity",
+         name + " must be an integer");
+    need(v.text[0] != '-', name + " must be nonnegative");
+    uint64_t x = 0;
+    auto r = std::from_chars(v.text.data() + (v.text[0] == '+'), v.text.data() + v.text.size(), x);
+    need(r.ec == std::errc() && r.ptr == v.text.data() + v.text.size() && x <= maximum,
+         name + " exceeds native metadata capacity");
+    return x;
+  };
+  auto numeric = [&](const json::Value& v, const std::string& name, double low, double high,
+                     bool strict_low) {
+    need(v.kind == json::Value::Number, name + " must be numeric");
+    const double x = v.number();
+    need(std::isfinite(x) && (strict_low ? x > low : x >= low) && x <= high,
+         name + " is outside the supported native parameter range");
+    return x;
+  };
+  auto get = [&](const char* k) { return in.find(k); };
+  need(get("rounds") != nullptr, "missing JSON key: rounds");
+  need(get("max_depth") != nullptr, "missing JSON key: max_depth");
+  const uint64_t rounds = integer(*get("rounds"), "rounds", uint64_t(INT_MAX) / classes);
+  const uint64_t depth = integer(*get("max_depth"), "max_depth", INT_MAX);
+  need(rounds > 0 && depth > 0, "positive rounds and max_depth required");
+  json::Value dflt;
+  dflt.kind = json::Value::Number;
+  auto or_default = [&](const char* k, const char* d) -> json::Value {
+    if (const auto* v = get(k)) return *v;
+    json::Value x = dflt;
+    x.text = d;
+    return x;
+  };
+  const uint64_t max_bin = integer(or_default("max_bin", "256"), "max_bin", INT_MAX);
+  need(max_bin >= 2, "max_bin must be at least 2");
+  const uint64_t seed = integer(or_default("seed", "0"), "seed", INT_MAX);
+  const double eta = numeric(or_default("eta", "0.3"), "eta", 0, 1, true);
+  std::string o = "{\"rounds\":" + std::to_string(rounds) + ",\"max_depth\":" +
+                  std::to_string(depth) + ",\"max_bin\":" + std::to_string(max_bin) +
+                  ",\"seed\":" + std::to_string(seed) + ",\"eta\":";
+  json::put_double(o, eta);
+  for (const char* k : {"lambda", "alpha", "gamma", "min_child_weight"}) {
+    const bool one = std::string(k) == "lambda" || std::string(k) == "min_child_weight";
+    const double x = numeric(or_default(k, one ? "1" : "0"), k, 0,
+                             std::numeric_limits<double>::max(), false);
+    o += ",\"" + std::string(k) + "\":";
+    json::put_double(o, x);
+  }
+  for (const char* k : {"subsample", "colsample_bytree", "colsample_bylevel", "colsample_bynode"}) {
+    if (const auto* v = get(k)) {
+      const double x = numeric(*v, k, 0, 1, true);
+      o += ",\"" + std::string(k) + "\":";
+      json::put_double(o, x);
+    }
+  }
+  return o + "}";
+}
 
 // ---------------------------------------------------------------------------
 // DMatrix quantisation
@@ -123,180 +188,246 @@ int32_t Tree::alloc(int32_t parent_id) {
 // ---------------------------------------------------------------------------
 // Grower
 // ---------------------------------------------------------------------------
+namespace {
+
+// Trees whose widest level can hold more nodes than this, or whose two
+// histogram levels would take more bytes, are grown level-synced.
+constexpr int64_t kEagerNodes = int64_t(1) << 16;
+constexpr int64_t kEagerHistBytes = int64_t(8) << 30;
+
+int64_t level_bound(int32_t depth, int64_t n_rows) {
+  return depth >= 62 ? n_rows : std::min<int64_t>(int64_t(1) << depth, n_rows);
+}
+
+int32_t* field(PlanCounts* c, int32_t PlanCounts::*m) { return &(c->*m); }
+
+}  // namespace
+
 Grower::Grower() = default;
 Grower::~Grower() = default;
 
-void Grower::grow(const Quantized& q, const int32_t* gpair, int32_t exp_g, int32_t exp_h,
-                  int64_t root_g, int64_t root_h, const TrainParam& p, float* margin,
-                  int64_t stride, Tree& tree, int32_t* positions, hipStream_t s) {
+void Grower::ensure_level(const Quantized& q, int64_t nb, int32_t d, int32_t D) {
+  const int64_t N = q.layout.n_rows;
+  const int32_t T = q.layout.n_tiles;
+  const int64_t S = int64_t(q.layout.n_features) * q.bin_stride * 2;
+  const int cur = d & 1, nxt = cur ^ 1;
+  const int64_t nn = d < D ? std::min(2 * nb, N) : 0;  // next level's bound
+  need(plan_hist_capacity(nn, T) < INT32_MAX && plan_part_capacity(nb, N) < INT32_MAX &&
+           plan_part_capacity(nn, N) < INT32_MAX && plan_leaf_capacity(nb, N) < INT32_MAX,
+       "tree level too wide for the planner's 32-bit work counts");
+  if (d < D) {
+    hist_[cur].reserve(size_t(nb * S));
+    splits_.reserve(size_t(nb));
+    node_left_.reserve(size_t(nb));
+    work_left_.reserve(size_t(plan_part_capacity(nb, N)));
+    work_offset_.reserve(size_t(plan_part_capacity(nb, N)));
+  }
+  level_[nxt].reserve(size_t(std::max<int64_t>(nn, 1)));
+  sums_[nxt].reserve(size_t(2 * std::max<int64_t>(nn, 1)));
+  seg_begin_[nxt].reserve(size_t(std::max<int64_t>(nn, 1)));
+  hist_work_[nxt].reserve(size_t(plan_hist_capacity(nn, T)));
+  sub_jobs_[nxt].reserve(size_t(nn / 2 + 1));
+  pair_chunk_.reserve(size_t(nn / 2 + 1));
+  part_work_[nxt].reserve(size_t(plan_part_capacity(nn, N)));
+  part_first_[nxt].reserve(size_t(nn + 1));
+  leaf_work_.reserve(size_t(plan_leaf_capacity(nb, N)));
+}
+
+void Grower::prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, hipStream_t s) {
   const dp_bin_layout& L = q.layout;
   const int64_t N = L.n_rows;
-  const int32_t F = L.n_features, B = q.bin_stride;
-  const int64_t S = int64_t(F) * B * 2;  // int64 values per node histogram
-  const double ug = std::ldexp(1.0, -exp_g), uh = std::ldexp(1.0, -exp_h);
-  need(p.max_depth >= 0 && p.max_depth <= 30, "max_depth out of supported range");
-  dp_train_param dtp{p.eta, p.lambda, p.alpha, p.gamma, p.min_child_weight, p.max_depth};
-
+  const int32_t D = p.max_depth;
+  const int64_t S = int64_t(L.n_features) * q.bin_stride * 2;
+  need(N >= 1, "training matrix has no rows");
+  need(N <= int64_t(UINT32_MAX), "row ids are 32-bit");
+  need(D >= 1 && D <= 30, "max_depth out of supported range");
   ridx_[0].reserve(size_t(N));
   ridx_[1].reserve(size_t(N));
+  counts_.reserve(1);
+  level_count_.reserve(sizeof(PlanCounts));
+  // level 0: the root
+  level_[0].reserve(1);
+  sums_[0].reserve(2);
+  seg_begin_[0].reserve(1);
+  part_work_[0].reserve(size_t(plan_part_capacity(1, N)));
+  part_first_[0].reserve(2);
+  if (root_rows_ != N) {
+    const int64_t b = 0, e = N;
+    const int32_t slot = 0;
+    const std::vector<HistWork> w = make_hist_work(L, &b, &e, &slot, 1);
+    root_work_.resize(w.size());
+    DP_HIP(hipMemcpy(root_work_.p, w.data(), sizeof(HistWork) * w.size(), hipMemcpyHostToDevice));
+    root_items_ = int32_t(w.size());
+    root_rows_ = N;
+  }
+  const int64_t widest = level_bound(D, N), widest_hist = level_bound(D - 1, N);
+  eager_ = widest <= kEagerNodes && 2 * widest_hist * S * int64_t(sizeof(int64_t)) <= kEagerHistBytes;
+  if (eager_) {
+    int64_t cap = 0;
+    for (int32_t d = 0; d <= D; ++d) {
+      ensure_level(q, level_bound(d, N), d, D);
+      cap += level_bound(d, N);
+    }
+    node_cap_ = std::min(cap, 2 * N - 1);
+    info_.reserve(size_t(node_cap_));
+    slot_bytes_ = (sizeof(PlanCounts) + sizeof(NodeInfo) * size_t(node_cap_) + 255) & ~size_t(255);
+    readback_.reserve(slot_bytes_ * size_t(n_slots));
+  } else {
+    ensure_level(q, 1, 0, D);
+    info_.reserve(3);
+    spill_.resize(size_t(n_slots));
+    spill_counts_.resize(size_t(n_slots));
+  }
+  (void)s;
+}
+
+void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
+                  const int64_t* root_sums, const TrainParam& p, float* margin, int64_t stride,
+                  int32_t* positions, int32_t slot, hipStream_t s) {
+  const dp_bin_layout& L = q.layout;
+  const int64_t N = L.n_rows;
+  const int32_t F = L.n_features, B = q.bin_stride, T = L.n_tiles, D = p.max_depth;
+  const int64_t S = int64_t(F) * B * 2;  // int64 values per node histogram
+  const dp_train_param dtp{p.eta, p.lambda, p.alpha, p.gamma, p.min_child_weight, p.max_depth};
+  PlanCounts* c = counts_.p;
+  auto* host_counts = reinterpret_cast<PlanCounts*>(level_count_.p);
+
   launch_iota_u32(ridx_[0].p, N, s);
-  tree = Tree{};
-  tree.alloc(-1);
-
-  struct LNode {
-    int32_t nid;
-    int32_t parent_slot;
-    int64_t begin, end, g, h;
-  };
-  struct Leaf {
-    float value;
-    int32_t parity;
-    int64_t begin, end;
-    int32_t nid;
-  };
-  std::vector<LNode> level{{0, -1, 0, N, root_g, root_h}};
-  std::vector<Leaf> leaves;
-
-  for (int32_t depth = 0; !level.empty(); ++depth) {
-    const int32_t n = int32_t(level.size());
-    const bool can_split = depth < p.max_depth;
-    const dp_split_record* rec = nullptr;
-    const int64_t* lefts = nullptr;
-    if (can_split) {
-      const int cur = depth & 1;
-      hist_[cur].reserve(size_t(n) * size_t(S));
-      sums_.reserve(size_t(2 * n));
-      splits_.reserve(size_t(n));
-      node_left_.reserve(size_t(n));
-
-      // Nodes whose histogram is built: the root, else the smaller child of
-      // every pair (ties: the left child).
-      std::vector<int32_t> build;
-      std::vector<SubtractJob> jobs;
-      if (depth == 0) {
-        build.push_back(0);
-      } else {
-        for (int32_t j = 0; j + 1 < n; j += 2) {
-          const LNode& a = level[size_t(j)];
-          const LNode& b = level[size_t(j) + 1];
-          const bool right_small = (b.end - b.begin) < (a.end - a.begin);
-          const int32_t small = right_small ? j + 1 : j, large = right_small ? j : j + 1;
-          build.push_back(small);
-          jobs.push_back({int64_t(a.parent_slot) * S, int64_t(small) * S, int64_t(large) * S});
-        }
-      }
-      std::vector<int64_t> bb, be;
-      for (int32_t k : build) {
-        bb.push_back(level[size_t(k)].begin);
-        be.push_back(level[size_t(k)].end);
-      }
-      const std::vector<HistWork> hw =
-          make_hist_work(L, bb.data(), be.data(), build.data(), int32_t(build.size()));
-
-      std::vector<PartWork> pw;
-      std::vector<int32_t> first(static_cast<size_t>(n) + 1);
-      for (int32_t i = 0; i < n; ++i) {
-        first[size_t(i)] = int32_t(pw.size());
-        for (int64_t b = level[size_t(i)].begin; b < level[size_t(i)].end; b += kPartChunk)
-          pw.push_back({i, 0, b, std::min(b + kPartChunk, level[size_t(i)].end)});
-      }
-      first[size_t(n)] = int32_t(pw.size());
-
-      ws_.begin(sizeof(HistWork) * hw.size() + sizeof(SubtractJob) * jobs.size() +
-                sizeof(int64_t) * size_t(3 * n) + sizeof(PartWork) * pw.size() +
-                sizeof(int32_t) * first.size() + 6 * 256);
-      ws_.reserve_scratch(2 * sizeof(int64_t) * pw.size() + 1024);
-      HistWork* d_hw;
-      SubtractJob* d_jobs;
-      int64_t* d_sums;
-      PartWork* d_pw;
-      int64_t* d_segb;
-      int32_t* d_first;
-      std::copy(hw.begin(), hw.end(), ws_.stage(hw.size(), &d_hw));
-      std::copy(jobs.begin(), jobs.end(), ws_.stage(jobs.size(), &d_jobs));
-      int64_t* h_sums = ws_.stage(size_t(2 * n), &d_sums);
-      int64_t* h_segb = ws_.stage(size_t(n), &d_segb);
-      for (int32_t i = 0; i < n; ++i) {
-        h_sums[2 * i] = level[size_t(i)].g;
-        h_sums[2 * i + 1] = level[size_t(i)].h;
-        h_segb[i] = level[size_t(i)].begin;
-      }
-      std::copy(pw.begin(), pw.end(), ws_.stage(pw.size(), &d_pw));
-      std::copy(first.begin(), first.end(), ws_.stage(first.size(), &d_first));
-      ws_.commit(s);
-      int64_t* work_left = ws_.take<int64_t>(pw.size());
-      int64_t* work_offset = ws_.take<int64_t>(pw.size());
-
-      launch_fill_i64(hist_[cur].p, int64_t(n) * S, 0, s);
-      launch_hist(q.bins.p, L, gpair, depth == 0 ? nullptr : ridx_[cur].p, d_hw,
-                  int32_t(hw.size()), B, hist_[cur].p, s);
-      if (!jobs.empty())
-        launch_subtract_many(hist_[cur ^ 1].p, hist_[cur].p, hist_[cur].p, d_jobs,
-                             int32_t(jobs.size()), S, s);
-      launch_evaluate(hist_[cur].p, n, F, B, q.d_nbins.p, d_sums, nullptr, exp_g, exp_h, dtp,
-                      splits_.p, s);
-      launch_partition(q.bins.p, L, ridx_[cur].p, ridx_[cur ^ 1].p, d_pw, int32_t(pw.size()),
-                       d_segb, splits_.p, d_first, n, work_left, work_offset, node_left_.p, s);
-      readback_.reserve(size_t(n) * (sizeof(dp_split_record) + sizeof(int64_t)));
-      auto* h_rec = reinterpret_cast<dp_split_record*>(readback_.p);
-      auto* h_left = reinterpret_cast<int64_t*>(readback_.p + size_t(n) * sizeof(dp_split_record));
-      DP_HIP(hipMemcpyAsync(h_rec, splits_.p, sizeof(dp_split_record) * size_t(n),
-                            hipMemcpyDeviceToHost, s));
-      DP_HIP(hipMemcpyAsync(h_left, node_left_.p, sizeof(int64_t) * size_t(n),
-                            hipMemcpyDeviceToHost, s));
+  launch_plan_root(level_[0].p, sums_[0].p, seg_begin_[0].p, part_work_[0].p, part_first_[0].p, c,
+                   N, root_sums, s);
+  int64_t nb = 1;  // bound of the current level's node count
+  for (int32_t d = 0; d <= D; ++d) {
+    const int cur = d & 1, nxt = cur ^ 1;
+    if (!eager_ && d > 0) {
+      DP_HIP(hipMemcpyAsync(host_counts, c, sizeof(PlanCounts), hipMemcpyDeviceToHost, s));
       DP_HIP(hipStreamSynchronize(s));
-      rec = h_rec;
-      lefts = h_left;
-    }
-
-    std::vector<LNode> next;
-    for (int32_t i = 0; i < n; ++i) {
-      const LNode nd = level[size_t(i)];
-      const double G = double(nd.g) * ug, H = double(nd.h) * uh;
-      const double w = calc_weight(p, G, H);
-      tree.base_weight[size_t(nd.nid)] = float(w);
-      tree.sum_hess[size_t(nd.nid)] = float(H);
-      tree.sum_qg[size_t(nd.nid)] = nd.g;
-      tree.sum_qh[size_t(nd.nid)] = nd.h;
-      if (can_split && rec[i].expand) {
-        const dp_split_record& r = rec[i];
-        const int64_t nl = lefts[i];
-        need(nl > 0 && nl < nd.end - nd.begin, "partition produced an empty child");
-        const int32_t l = tree.alloc(nd.nid), rr = tree.alloc(nd.nid);
-        const size_t id = size_t(nd.nid);
-        tree.left[id] = l;
-        tree.right[id] = rr;
-        tree.feature[id] = r.feature;
-        tree.split_bin[id] = r.bin;
-        tree.default_left[id] = uint8_t(r.default_left);
-        tree.cond[id] = q.cut_values[size_t(q.cut_ptr[size_t(r.feature)] + r.bin)];
-        tree.loss_chg[id] = float(r.loss_chg);
-        next.push_back({l, i, nd.begin, nd.begin + nl, r.gl, r.hl});
-        next.push_back({rr, i, nd.begin + nl, nd.end, nd.g - r.gl, nd.h - r.hl});
-      } else {
-        const float v = float(w * double(p.eta));
-        tree.cond[size_t(nd.nid)] = v;
-        leaves.push_back({v, depth & 1, nd.begin, nd.end, nd.nid});
+      nb = host_counts->n_level;
+      if (nb == 0) break;
+      ensure_level(q, nb, d, D);
+      const int64_t need_nodes = int64_t(host_counts->n_nodes) + 2 * nb;
+      if (int64_t(info_.n) < need_nodes) {
+        DeviceBuffer<NodeInfo> grown(size_t(std::max<int64_t>(need_nodes, 2 * int64_t(info_.n))));
+        DP_HIP(hipMemcpyAsync(grown.p, info_.p, info_.bytes(), hipMemcpyDeviceToDevice, s));
+        DP_HIP(hipStreamSynchronize(s));
+        info_ = std::move(grown);
       }
     }
-    level.swap(next);
+    const bool split = d < D;
+    int64_t* h = hist_[cur].p;
+    if (split) {
+      if (d == 0) {
+        launch_fill_i64(h, S, 0, s);
+        launch_hist(q.bins.p, L, gpair, nullptr, root_work_.p, root_items_, nullptr, B, h, s);
+      } else {
+        launch_zero_i64_dev(h, field(c, &PlanCounts::n_level), S, nb, s);
+        launch_hist(q.bins.p, L, gpair, ridx_[cur].p, hist_work_[cur].p,
+                    int32_t(plan_hist_capacity(nb, T)), field(c, &PlanCounts::n_hist), B, h, s);
+        launch_subtract_many(hist_[nxt].p, h, h, sub_jobs_[cur].p, int32_t(nb / 2 + 1),
+                             field(c, &PlanCounts::n_sub), S, s);
+      }
+      launch_evaluate(h, int32_t(nb), field(c, &PlanCounts::n_level), F, B, q.d_nbins.p,
+                      sums_[cur].p, exps, 0, 0, dtp, splits_.p, s);
+      launch_partition(q.bins.p, L, ridx_[cur].p, ridx_[nxt].p, part_work_[cur].p,
+                       int32_t(plan_part_capacity(nb, N)), field(c, &PlanCounts::n_part),
+                       seg_begin_[cur].p, splits_.p, part_first_[cur].p, int32_t(nb),
+                       field(c, &PlanCounts::n_level), work_left_.p, work_offset_.p,
+                       node_left_.p, s);
+    }
+    PlanArgs a{};
+    a.cur = level_[cur].p;
+    a.splits = split ? splits_.p : nullptr;
+    a.node_left = node_left_.p;
+    a.next = level_[nxt].p;
+    a.next_sums = sums_[nxt].p;
+    a.next_seg_begin = seg_begin_[nxt].p;
+    a.info = info_.p;
+    a.hist_work = hist_work_[nxt].p;
+    a.sub_jobs = sub_jobs_[nxt].p;
+    a.part_work = part_work_[nxt].p;
+    a.part_first = part_first_[nxt].p;
+    a.pair_chunk = pair_chunk_.p;
+    a.leaf_work = leaf_work_.p;
+    a.counts = c;
+    a.exps = exps;
+    a.depth = d;
+    a.max_depth = D;
+    a.n_tiles = T;
+    a.hist_elems = S;
+    a.eta = double(p.eta);
+    a.lambda = double(p.lambda);
+    a.alpha = double(p.alpha);
+    a.mcw = double(p.min_child_weight);
+    a.info_capacity = int32_t(info_.n);
+    a.level_capacity = int32_t(level_[nxt].n);
+    a.hist_capacity = int32_t(hist_work_[nxt].n);
+    a.part_capacity = int32_t(part_work_[nxt].n);
+    a.leaf_capacity = int32_t(leaf_work_.n);
+    launch_plan_level(a, s);
+    const int32_t leaf_bound = int32_t(plan_leaf_capacity(nb, N));
+    launch_update_margin(ridx_[cur].p, leaf_work_.p, leaf_bound, field(c, &PlanCounts::n_leaf),
+                         margin, stride, s);
+    if (positions)
+      launch_leaf_positions(ridx_[cur].p, leaf_work_.p, leaf_bound, field(c, &PlanCounts::n_leaf),
+                            positions, s);
+    nb = split ? std::min(2 * nb, N) : 0;
   }
 
-  // Leaf values into the margins (and leaf ids into positions).
-  constexpr int64_t kLeafChunk = 16384;
-  std::vector<LeafWork> lw[2];
-  for (const Leaf& lf : leaves)
-    for (int64_t b = lf.begin; b < lf.end; b += kLeafChunk)
-      lw[lf.parity].push_back({lf.value, lf.nid, b, std::min(b + kLeafChunk, lf.end)});
-  ws_.begin(sizeof(LeafWork) * (lw[0].size() + lw[1].size()) + 2 * 256);
-  LeafWork* d_lw[2];
-  for (int par = 0; par < 2; ++par)
-    std::copy(lw[par].begin(), lw[par].end(), ws_.stage(lw[par].size(), &d_lw[par]));
-  ws_.commit(s);
-  for (int par = 0; par < 2; ++par) {
-    launch_update_margin(ridx_[par].p, d_lw[par], int32_t(lw[par].size()), margin, stride, s);
-    if (positions)
-      launch_leaf_positions(ridx_[par].p, d_lw[par], int32_t(lw[par].size()), positions, s);
+  if (eager_) {
+    uint8_t* dst = readback_.p + slot_bytes_ * size_t(slot);
+    DP_HIP(hipMemcpyAsync(dst, c, sizeof(PlanCounts), hipMemcpyDeviceToHost, s));
+    DP_HIP(hipMemcpyAsync(dst + sizeof(PlanCounts), info_.p, sizeof(NodeInfo) * size_t(node_cap_),
+                          hipMemcpyDeviceToHost, s));
+  } else {
+    DP_HIP(hipMemcpyAsync(host_counts, c, sizeof(PlanCounts), hipMemcpyDeviceToHost, s));
+    DP_HIP(hipStreamSynchronize(s));
+    spill_counts_[size_t(slot)] = *host_counts;
+    auto& v = spill_[size_t(slot)];
+    v.resize(size_t(std::max(host_counts->n_nodes, 0)));
+    if (!v.empty())
+      DP_HIP(hipMemcpy(v.data(), info_.p, sizeof(NodeInfo) * v.size(), hipMemcpyDeviceToHost));
+  }
+}
+
+void Grower::collect(const Quantized& q, int32_t slot, Tree& tree) const {
+  const PlanCounts* c;
+  const NodeInfo* info;
+  if (eager_) {
+    const uint8_t* src = readback_.p + slot_bytes_ * size_t(slot);
+    c = reinterpret_cast<const PlanCounts*>(src);
+    info = reinterpret_cast<const NodeInfo*>(src + sizeof(PlanCounts));
+  } else {
+    c = &spill_counts_[size_t(slot)];
+    info = spill_[size_t(slot)].data();
+  }
+  need(c->error != 1, "partition produced an empty child");
+  need(c->error == 0, "tree planner capacity exceeded (code " + std::to_string(c->error) + ")");
+  const int32_t n = c->n_nodes;
+  need(n >= 1 && (!eager_ || n <= node_cap_), "tree planner reported an invalid node count");
+  tree = Tree{};
+  for (int32_t i = 0; i < n; ++i) tree.alloc(-1);
+  for (int32_t i = 0; i < n; ++i) {
+    const NodeInfo& r = info[i];
+    const size_t id = size_t(i);
+    tree.base_weight[id] = r.base_weight;
+    tree.sum_hess[id] = r.sum_hess;
+    tree.sum_qg[id] = r.g;
+    tree.sum_qh[id] = r.h;
+    if (r.left >= 0) {
+      need(r.left > i && r.left + 1 < n, "tree planner produced an invalid child id");
+      need(r.feature >= 0 && r.feature < q.layout.n_features && r.bin >= 0 &&
+               q.cut_ptr[size_t(r.feature)] + r.bin < q.cut_ptr[size_t(r.feature) + 1],
+           "tree planner produced an invalid split");
+      tree.left[id] = r.left;
+      tree.right[id] = r.left + 1;
+      tree.parent[size_t(r.left)] = tree.parent[size_t(r.left) + 1] = i;
+      tree.feature[id] = r.feature;
+      tree.split_bin[id] = r.bin;
+      tree.default_left[id] = uint8_t(r.default_left);
+      tree.cond[id] = q.cut_values[size_t(q.cut_ptr[size_t(r.feature)] + r.bin)];
+      tree.loss_chg[id] = float(r.loss_chg);
+    } else {
+      tree.cond[id] = r.leaf_value;
+    }
   }
 }
 
@@ -323,8 +454,18 @@ void Booster::set_param(const std::string& key, const std::string& value) {
   bool ok = false;
   for (const char* k : known) ok = ok || key == k;
   need(ok, "unsupported parameter: " + key);
-  if (rounds_ > 0 && (key == "objective" || key == "num_class" || key == "max_bin"))
-    need(params_[key] == value, "parameter " + key + " cannot change after training started");
+  if (model_only_ && key == "objective") {
+    const std::string cur = effective_objective();
+    const bool multi = [](const std::string& o) {
+      return o == "multi:softmax" || o == "multi:softprob";
+    }(cur);
+    need(value == cur || (multi && (value == "multi:softmax" || value == "multi:softprob")),
+         "a loaded model can only switch between multi:softmax and multi:softprob");
+  } else if (configured_ && (key == "objective" || key == "num_class" || key == "max_bin")) {
+    auto it = params_.find(key);
+    need(it != params_.end() && it->second == value,
+         "parameter " + key + " cannot change after training started");
+  }
   params_[key] = value;
   if (key == "dp_record_positions") record_positions_ = parse_int(key, value) != 0;
 }
@@ -425,9 +566,22 @@ void Booster::configure(DMatrix* d) {
 
 void Booster::update_one_iter(int iter, DMatrix* d) {
   need(d != nullptr, "null DMatrix");
+  need(!model_only_, "continuing training of a loaded or sliced model is not supported");
   need(iter == rounds_, "iteration index must equal the number of boosted rounds");
   configure(d);
   need(d->has_labels, "training DMatrix has no labels");
+  if (!labels_checked_) {
+    DeviceBuffer<int32_t> bad(1);
+    launch_check_labels(d->labels.p, d->n_rows, objective_id_, n_groups_, bad.p, stream_);
+    int32_t flag = 0;
+    DP_HIP(hipMemcpyAsync(&flag, bad.p, sizeof flag, hipMemcpyDeviceToHost, stream_));
+    DP_HIP(hipStreamSynchronize(stream_));
+    need(flag == 0, objective_id_ == DP_OBJ_SOFTPROB
+                        ? "labels must be exact class ids in [0, num_class)"
+                        : objective_id_ == DP_OBJ_LOGISTIC ? "logistic labels must be in [0, 1]"
+                                                           : "labels must be finite");
+    labels_checked_ = true;
+  }
   launch_gradients(objective_id_, margin_.p, d->labels.p, d->n_rows, n_groups_, grad_.p, hess_.p,
                    stream_);
   boost_from_gradients(d, grad_.p, hess_.p);
@@ -436,6 +590,7 @@ void Booster::update_one_iter(int iter, DMatrix* d) {
 void Booster::train_one_iter(DMatrix* d, int iter, const float* grad, const float* hess,
                              int64_t n, int32_t k) {
   need(d != nullptr, "null DMatrix");
+  need(!model_only_, "continuing training of a loaded or sliced model is not supported");
   need(iter == rounds_, "iteration index must equal the number of boosted rounds");
   configure(d);
   need(n == d->n_rows && k == n_groups_, "gradient shape differs from [rows, outputs]");
@@ -450,24 +605,25 @@ void Booster::boost_from_gradients(DMatrix* d, const float* grad, const float* h
   Quantized& q = d->quantize(tp_.max_bin, scratch, stream_);
   const int64_t N = d->n_rows;
   launch_quantise(grad, hess, N, n_groups_, maxima_.p, exps_.p, gpair_.p, sums_.p, stream_);
-  std::vector<int32_t> exps(static_cast<size_t>(2 * n_groups_));
-  std::vector<int64_t> sums(static_cast<size_t>(2 * n_groups_));
-  DP_HIP(hipMemcpyAsync(exps.data(), exps_.p, exps_.bytes(), hipMemcpyDeviceToHost, stream_));
-  DP_HIP(hipMemcpyAsync(sums.data(), sums_.p, sums_.bytes(), hipMemcpyDeviceToHost, stream_));
-  DP_HIP(hipStreamSynchronize(stream_));
-  last_exps_ = exps;
   if (record_positions_) positions_.reserve(size_t(N));
+  grower_->prepare(q, tp_, n_groups_, stream_);
+  for (int32_t k = 0; k < n_groups_; ++k)
+    grower_->grow(q, gpair_.p + int64_t(k) * N * 2, exps_.p + 2 * k, sums_.p + 2 * k, tp_,
+                  margin_.p + k, n_groups_, record_positions_ ? positions_.p : nullptr, k,
+                  stream_);
+  exps_host_.reserve(exps_.bytes());
+  DP_HIP(hipMemcpyAsync(exps_host_.p, exps_.p, exps_.bytes(), hipMemcpyDeviceToHost, stream_));
+  DP_HIP(hipStreamSynchronize(stream_));
+  const auto* e = reinterpret_cast<const int32_t*>(exps_host_.p);
+  last_exps_.assign(e, e + 2 * n_groups_);
   for (int32_t k = 0; k < n_groups_; ++k) {
     Tree tree;
-    grower_->grow(q, gpair_.p + int64_t(k) * N * 2, exps[size_t(2 * k)], exps[size_t(2 * k + 1)],
-                  sums[size_t(2 * k)], sums[size_t(2 * k + 1)], tp_, margin_.p + k, n_groups_,
-                  tree, record_positions_ ? positions_.p : nullptr, stream_);
+    grower_->collect(q, k, tree);
     trees_.push_back(std::move(tree));
     tree_info_.push_back(k);
   }
   iteration_indptr_.push_back(int32_t(trees_.size()));
   ++rounds_;
-  DP_HIP(hipStreamSynchronize(stream_));
 }
 
 void Booster::margins(float* out, size_t n) const {
@@ -570,8 +726,8 @@ std::string Booster::save_model() const {
   json::put_string(o, base_score_text(base_score_));
   o += ",\"boost_from_average\":\"0\",\"num_class\":\"" + std::to_string(num_class_) +
        "\",\"num_feature\":\"" + std::to_string(n_features_) +
-       "\",\"num_target\":\"1\"},\"objective\":" + objective_json(objective_, num_class_) +
-       "},\"version\":[3,4,1]}";
+       "\",\"num_target\":\"1\"},\"objective\":" +
+       objective_json(effective_objective(), num_class_) + "},\"version\":[3,4,1]}";
   return o;
 }
 
@@ -619,9 +775,221 @@ std::string Booster::save_config() const {
   o += ",\"boost_from_average\":\"0\",\"num_class\":\"" + std::to_string(num_class_) +
        "\",\"num_feature\":\"" + std::to_string(n_features_) +
        "\",\"num_target\":\"1\"},\"learner_train_param\":{\"booster\":\"gbtree\",\"objective\":";
-  json::put_string(o, objective_);
-  o += "},\"objective\":" + objective_json(objective_, num_class_) + "},\"version\":[3,4,1]}";
+  json::put_string(o, effective_objective());
+  o += "},\"objective\":" + objective_json(effective_objective(), num_class_) +
+       "},\"version\":[3,4,1]}";
   return o;
+}
+
+
+// ---------------------------------------------------------------------------
+// Prediction, loading and slicing
+// ---------------------------------------------------------------------------
+std::string Booster::effective_objective() const {
+  auto it = params_.find("objective");
+  if (model_only_ && it != params_.end()) return it->second;
+  return objective_;
+}
+
+void Booster::upload_forest(int32_t tree_begin, int32_t tree_end) {
+  if (forest_begin_ == tree_begin && forest_end_ == tree_end && forest_trees_ == trees_.size())
+    return;
+  std::vector<PredNode> nodes;
+  std::vector<int32_t> roots;
+  std::vector<std::vector<int32_t>> per_group(size_t(std::max(n_groups_, 1)));
+  for (int32_t t = tree_begin; t < tree_end; ++t) {
+    const Tree& tr = trees_[size_t(t)];
+    const int32_t base = int32_t(nodes.size());
+    for (int32_t i = 0; i < tr.size(); ++i) {
+      const bool leaf = tr.left[size_t(i)] == -1;
+      nodes.push_back({leaf ? -1 : base + tr.left[size_t(i)], leaf ? 0 : tr.feature[size_t(i)],
+                       tr.cond[size_t(i)], leaf ? 0 : int32_t(tr.default_left[size_t(i)])});
+    }
+    per_group[size_t(tree_info_[size_t(t)])].push_back(base);
+  }
+  std::vector<int32_t> group_ptr{0};
+  for (const auto& g : per_group) {
+    roots.insert(roots.end(), g.begin(), g.end());
+    group_ptr.push_back(int32_t(roots.size()));
+  }
+  std::vector<float> base(size_t(std::max(n_groups_, 1)));
+  for (size_t k = 0; k < base.size(); ++k) {
+    const float b = base_score_.empty() ? 0.0f : base_score_[k < base_score_.size() ? k : 0];
+    base[k] = objective_id_ == DP_OBJ_LOGISTIC ? float(std::log(double(b) / (1.0 - double(b)))) : b;
+  }
+  forest_nodes_.resize(std::max<size_t>(nodes.size(), 1) * sizeof(PredNode));
+  forest_roots_.resize(std::max<size_t>(roots.size(), 1));
+  forest_group_ptr_.resize(group_ptr.size());
+  forest_base_.resize(base.size());
+  if (!nodes.empty())
+    DP_HIP(hipMemcpy(forest_nodes_.p, nodes.data(), nodes.size() * sizeof(PredNode),
+                     hipMemcpyHostToDevice));
+  if (!roots.empty())
+    DP_HIP(hipMemcpy(forest_roots_.p, roots.data(), roots.size() * sizeof(int32_t),
+                     hipMemcpyHostToDevice));
+  DP_HIP(hipMemcpy(forest_group_ptr_.p, group_ptr.data(), group_ptr.size() * sizeof(int32_t),
+                   hipMemcpyHostToDevice));
+  DP_HIP(hipMemcpy(forest_base_.p, base.data(), base.size() * sizeof(float),
+                   hipMemcpyHostToDevice));
+  forest_begin_ = tree_begin;
+  forest_end_ = tree_end;
+  forest_trees_ = trees_.size();
+}
+
+const float* Booster::predict(const PredictRequest& req, std::vector<uint64_t>& shape) {
+  need(configured_ || model_only_, "booster holds no model");
+  need(req.features == n_features_, "prediction input has " + std::to_string(req.features) +
+                                        " features, the model " + std::to_string(n_features_));
+  need(req.rows >= 0 && req.row_stride >= req.features, "prediction input shape");
+  const int32_t begin = req.iteration_begin;
+  const int32_t end = req.iteration_end == 0 ? rounds_ : req.iteration_end;
+  need(begin >= 0 && begin <= end && end <= rounds_, "iteration range outside the model");
+  const std::string obj = effective_objective();
+  int32_t transform = kPredIdentity, outputs = n_groups_;
+  if (req.type == 0) {
+    if (obj == "binary:logistic") transform = kPredSigmoid;
+    else if (obj == "multi:softprob") transform = kPredSoftmax;
+    else if (obj == "multi:softmax") { transform = kPredArgmax; outputs = 1; }
+  } else {
+    need(req.type == 1, "prediction type must be 0 (value) or 1 (margin)");
+  }
+  upload_forest(iteration_indptr_[size_t(begin)], iteration_indptr_[size_t(end)]);
+  pred_out_.reserve(size_t(std::max<int64_t>(req.rows, 1)) * size_t(n_groups_));
+  hipStream_t s = stream_;
+  launch_predict(req.values, req.rows, req.features, req.row_stride, req.missing,
+                 reinterpret_cast<const PredNode*>(forest_nodes_.p), forest_roots_.p,
+                 forest_group_ptr_.p, n_groups_, forest_base_.p, transform, pred_out_.p, s);
+  DP_HIP(hipStreamSynchronize(s));
+  shape.clear();
+  shape.push_back(uint64_t(req.rows));
+  if (req.strict_shape || outputs > 1) shape.push_back(uint64_t(outputs));
+  return pred_out_.p;
+}
+
+void Booster::load_model(const std::string& text) {
+  need(!configured_, "cannot load into a booster that is training");
+  const json::Value doc = json::parse(text);
+  const auto& learner = doc.at("learner");
+  const auto& mp = learner.at("learner_model_param");
+  auto decimal = [](const json::Value& v, const char* what) {
+    need(v.kind == json::Value::String, std::string(what) + " must be a decimal string");
+    char* e = nullptr;
+    const long long x = std::strtoll(v.text.c_str(), &e, 10);
+    need(e && *e == '\0' && !v.text.empty() && x >= 0, std::string("invalid ") + what);
+    return int64_t(x);
+  };
+  n_features_ = int32_t(decimal(mp.at("num_feature"), "num_feature"));
+  num_class_ = int32_t(decimal(mp.at("num_class"), "num_class"));
+  objective_ = learner.at("objective").at("name").text;
+  if (objective_ == "binary:logistic") objective_id_ = DP_OBJ_LOGISTIC;
+  else if (objective_ == "multi:softmax" || objective_ == "multi:softprob") objective_id_ = DP_OBJ_SOFTPROB;
+  else if (objective_ == "reg:squarederror") objective_id_ = DP_OBJ_SQUARED;
+  else fail("unsupported objective in model: " + objective_);
+  n_groups_ = objective_id_ == DP_OBJ_SOFTPROB ? num_class_ : 1;
+  need(n_groups_ >= 1, "model output count");
+  json::Value bs = mp.at("base_score");
+  if (bs.kind == json::Value::String) bs = json::parse(bs.text);
+  base_score_.clear();
+  if (bs.kind == json::Value::Array)
+    for (const auto& x : bs.items) base_score_.push_back(float(x.number()));
+  else
+    base_score_.push_back(float(bs.number()));
+  need(base_score_.size() == 1 || base_score_.size() == size_t(n_groups_), "base_score size");
+  if (base_score_.size() == 1) base_score_.resize(size_t(n_groups_), base_score_[0]);
+  const auto& model = learner.at("gradient_booster").at("model");
+  const auto& trees = model.at("trees").items;
+  const auto& info = model.at("tree_info").items;
+  need(trees.size() == info.size(), "tree_info size differs from the tree count");
+  trees_.clear();
+  tree_info_.clear();
+  for (size_t t = 0; t < trees.size(); ++t) {
+    const json::Value& jt = trees[t];
+    auto ints = [&](const char* k) {
+      std::vector<int32_t> v;
+      for (const auto& x : jt.at(k).items) v.push_back(int32_t(x.i64()));
+      return v;
+    };
+    auto floats = [&](const char* k) {
+      std::vector<float> v;
+      if (const auto* a = jt.find(k))
+        for (const auto& x : a->items) v.push_back(float(x.number()));
+      return v;
+    };
+    Tree tr;
+    tr.left = ints("left_children");
+    tr.right = ints("right_children");
+    tr.feature = ints("split_indices");
+    tr.cond = floats("split_conditions");
+    const size_t n = tr.left.size();
+    need(n > 0 && tr.right.size() == n && tr.feature.size() == n && tr.cond.size() == n,
+         "tree node arrays differ in size");
+    for (const auto& x : jt.at("default_left").items)
+      tr.default_left.push_back(uint8_t(x.kind == json::Value::Bool ? x.boolean : x.i64() != 0));
+    need(tr.default_left.size() == n, "default_left size");
+    tr.base_weight = floats("base_weights");
+    tr.loss_chg = floats("loss_changes");
+    tr.sum_hess = floats("sum_hessian");
+    tr.base_weight.resize(n, 0.0f);
+    tr.loss_chg.resize(n, 0.0f);
+    tr.sum_hess.resize(n, 0.0f);
+    tr.parent.assign(n, -1);
+    tr.split_bin.assign(n, -1);
+    tr.sum_qg.assign(n, 0);
+    tr.sum_qh.assign(n, 0);
+    for (size_t i = 0; i < n; ++i) {
+      if (tr.left[i] == -1) continue;
+      need(tr.left[i] > int32_t(i) && tr.right[i] == tr.left[i] + 1 && tr.right[i] < int32_t(n),
+           "split successors must advance and be consecutive");
+      need(tr.feature[i] >= 0 && tr.feature[i] < n_features_, "split feature out of range");
+      tr.parent[size_t(tr.left[i])] = tr.parent[size_t(tr.right[i])] = int32_t(i);
+    }
+    const int32_t group = int32_t(info[t].i64());
+    need(group >= 0 && group < n_groups_, "tree_info class out of range");
+    trees_.push_back(std::move(tr));
+    tree_info_.push_back(group);
+  }
+  iteration_indptr_.clear();
+  if (const auto* ip = model.find("iteration_indptr")) {
+    for (const auto& x : ip->items) iteration_indptr_.push_back(int32_t(x.i64()));
+  } else {
+    for (size_t t = 0; t <= trees_.size(); t += size_t(n_groups_))
+      iteration_indptr_.push_back(int32_t(t));
+  }
+  need(iteration_indptr_.size() >= 1 && iteration_indptr_.front() == 0 &&
+           iteration_indptr_.back() == int32_t(trees_.size()),
+       "iteration_indptr does not cover the trees");
+  rounds_ = int(iteration_indptr_.size()) - 1;
+  model_only_ = true;
+  forest_begin_ = forest_end_ = -1;
+  if (!stream_) DP_HIP(hipStreamCreateWithFlags(&stream_, hipStreamDefault));
+}
+
+std::unique_ptr<Booster> Booster::slice(int begin, int end, int step) const {
+  need(configured_ || model_only_, "booster holds no model");
+  if (end == 0) end = rounds_;
+  need(step >= 1 && begin >= 0 && begin <= end && end <= rounds_, "slice range outside the model");
+  auto out = std::make_unique<Booster>(std::vector<DMatrix*>{});
+  out->params_ = params_;
+  out->params_.erase("dp_record_positions");
+  out->objective_ = effective_objective();
+  out->objective_id_ = objective_id_;
+  out->n_groups_ = n_groups_;
+  out->num_class_ = num_class_;
+  out->n_features_ = n_features_;
+  out->base_score_ = base_score_;
+  out->tp_ = tp_;
+  out->iteration_indptr_ = {0};
+  for (int r = begin; r < end; r += step) {
+    for (int32_t t = iteration_indptr_[size_t(r)]; t < iteration_indptr_[size_t(r) + 1]; ++t) {
+      out->trees_.push_back(trees_[size_t(t)]);
+      out->tree_info_.push_back(tree_info_[size_t(t)]);
+    }
+    out->iteration_indptr_.push_back(int32_t(out->trees_.size()));
+  }
+  out->rounds_ = int(out->iteration_indptr_.size()) - 1;
+  out->model_only_ = true;
+  DP_HIP(hipStreamCreateWithFlags(&out->stream_, hipStreamDefault));
+  return out;
 }
 
 }  // namespace dp

@@ -47,26 +47,69 @@ struct TrainParam {
   int32_t max_depth = 6, max_bin = 256;
 };
 
-// Level-wise tree growth on one quantised matrix (reusable device buffers).
+// Depth-wise tree growth on one quantised matrix (reusable device buffers).
+//
+// A tree is grown without a host round trip per level: every level's launches
+// take their item counts from device counters that a one-workgroup planner
+// kernel writes after the level's partition.  The host enqueues all levels,
+// then the tree's node records (and counters) are copied into a pinned slot;
+// collect() turns them into a Tree once the caller has synchronised the
+// stream.  Trees wider than the eager bound fall back to reading the level
+// size back before each level to size the buffers.
 class Grower {
  public:
   Grower();
   ~Grower();
-  // gpair: [n_rows][2] fixed-point gradients of one output; (root_g, root_h)
-  // their int64 sums; exps the quantiser exponents.  Adds the leaf values to
-  // margin[r * stride] and, when `positions` is set, writes each row's leaf id.
-  void grow(const Quantized& q, const int32_t* gpair, int32_t exp_g, int32_t exp_h,
-            int64_t root_g, int64_t root_h, const TrainParam& p, float* margin, int64_t stride,
-            Tree& tree, int32_t* positions, hipStream_t s);
+  // Sizes the buffers for trees over `q` with parameters `p`, with `n_slots`
+  // trees in flight before the caller synchronises.
+  void prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, hipStream_t s);
+  // Enqueues one tree.  gpair: [n_rows][2] fixed-point gradients of one output;
+  // exps (device): its two quantiser exponents; root_sums (device): the int64
+  // sums of gpair.  Adds the leaf values to margin[r * stride] and, when
+  // `positions` is set, writes each row's leaf id.
+  void grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
+            const int64_t* root_sums, const TrainParam& p, float* margin, int64_t stride,
+            int32_t* positions, int32_t slot, hipStream_t s);
+  // The tree grown into `slot`; the stream must have been synchronised.
+  void collect(const Quantized& q, int32_t slot, Tree& tree) const;
 
  private:
-  dp_workspace_s ws_;
+  void ensure_level(const Quantized& q, int64_t nodes, int32_t depth, int32_t max_depth);
   DeviceBuffer<uint32_t> ridx_[2];
   DeviceBuffer<int64_t> hist_[2];
-  DeviceBuffer<int64_t> sums_;
+  DeviceBuffer<LevelNode> level_[2];
+  DeviceBuffer<int64_t> sums_[2], seg_begin_[2];
+  DeviceBuffer<HistWork> hist_work_[2], root_work_;
+  DeviceBuffer<SubtractJob> sub_jobs_[2];
+  DeviceBuffer<PartWork> part_work_[2];
+  DeviceBuffer<int32_t> part_first_[2];
+  DeviceBuffer<int64_t> pair_chunk_, work_left_, work_offset_, node_left_;
   DeviceBuffer<dp_split_record> splits_;
-  DeviceBuffer<int64_t> node_left_;
-  PinnedBuffer readback_;
+  DeviceBuffer<LeafWork> leaf_work_;
+  DeviceBuffer<NodeInfo> info_;
+  DeviceBuffer<PlanCounts> counts_;
+  PinnedBuffer readback_;  // per slot: PlanCounts, then NodeInfo[node_cap_]
+  PinnedBuffer level_count_;
+  std::vector<std::vector<NodeInfo>> spill_;  // slots of trees grown level-synced
+  std::vector<PlanCounts> spill_counts_;
+  bool eager_ = true;
+  int64_t node_cap_ = 0;
+  size_t slot_bytes_ = 0;
+  int64_t root_rows_ = -1;
+  int32_t root_items_ = 0;
+};
+
+// Normalised hyperparameter JSON (see DPValidateHyperparameters).
+std::string validate_hyperparameters(const std::string& text, uint32_t classes);
+
+struct PredictRequest {
+  const float* values = nullptr;  // device, row-major
+  int64_t rows = 0, row_stride = 0;
+  int32_t features = 0;
+  float missing = 0.0f;  // NaN: only NaN is missing
+  int32_t type = 0;      // 0 = transformed value, 1 = margin
+  int32_t iteration_begin = 0, iteration_end = 0;  // rounds; end 0 = all
+  bool strict_shape = true;
 };
 
 class Booster {
@@ -86,8 +129,16 @@ class Booster {
   void margins(float* out, size_t n) const;
   void last_gradients(float* grad, float* hess, size_t n, int32_t* exps) const;
   void last_positions(int32_t* out, size_t n) const;
+  // Model from an XGBoost-schema JSON document (prediction / export only).
+  void load_model(const std::string& text);
+  // Rounds [begin, end) with the given step, as a new prediction-only booster.
+  std::unique_ptr<Booster> slice(int begin, int end, int step) const;
+  // Device output (library-owned, valid until the next predict) and its shape.
+  const float* predict(const PredictRequest& req, std::vector<uint64_t>& shape);
 
  private:
+  std::string effective_objective() const;
+  void upload_forest(int32_t tree_begin, int32_t tree_end);
   void configure(DMatrix* d);
   void boost_from_gradients(DMatrix* d, const float* grad, const float* hess);
   std::map<std::string, std::string> params_;
@@ -109,13 +160,22 @@ class Booster {
   DeviceBuffer<uint32_t> maxima_;
   DeviceBuffer<int32_t> positions_;
   std::vector<int32_t> last_exps_;
+  PinnedBuffer exps_host_;
   bool record_positions_ = false;
+  bool labels_checked_ = false;
   hipStream_t stream_ = nullptr;
   std::unique_ptr<Grower> grower_;
   std::vector<Tree> trees_;
   std::vector<int32_t> tree_info_;
   std::vector<int32_t> iteration_indptr_{0};
   int rounds_ = 0;
+  bool model_only_ = false;  // loaded or sliced: predicts, cannot train
+  // device forest for prediction
+  DeviceBuffer<uint8_t> forest_nodes_;
+  DeviceBuffer<int32_t> forest_roots_, forest_group_ptr_;
+  DeviceBuffer<float> forest_base_, pred_out_;
+  int32_t forest_begin_ = -1, forest_end_ = -1;
+  size_t forest_trees_ = 0;
 };
 
 }  // namespace dp

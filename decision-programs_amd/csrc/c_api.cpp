@@ -7,6 +7,7 @@
 #include <cstdio>
 #include <cstring>
 #include <fstream>
+#include <iterator>
 #include <memory>
 #include <string>
 
@@ -65,8 +66,7 @@ struct DMatrixObj {
 struct BoosterObj {
   std::unique_ptr<dp::Booster> b;
   std::string buffer;  // last returned string (model or config)
-  std::vector<std::string> scratch;
-  dp::Tree view_tree;
+  std::vector<bst_ulong> shape;  // last prediction shape
 };
 
 dp::DMatrix& dm(DMatrixHandle h) {
@@ -308,6 +308,70 @@ int XGBoosterSaveModelToBuffer(BoosterHandle handle, const char* config, bst_ulo
   });
 }
 
+int XGBoosterPredictFromCudaArray(BoosterHandle handle, const char* values, const char* config,
+                                  DMatrixHandle proxy, const bst_ulong** out_shape,
+                                  bst_ulong* out_dim, const float** out_result) {
+  return guarded([&] {
+    dp::need(out_shape && out_dim && out_result, "null output pointer");
+    dp::need(proxy == nullptr, "proxy DMatrix is not supported; pass NULL");
+    BoosterObj& b = bo(handle);
+    ArrayInterface a = parse_array(values);
+    dp::need(a.typestr == "<f4", "prediction input must be float32 (<f4)");
+    dp::need(a.shape.size() == 2, "prediction input must be [N, F]");
+    dp::PredictRequest req;
+    req.values = reinterpret_cast<const float*>(a.data);
+    req.rows = a.shape[0];
+    req.features = int32_t(a.shape[1]);
+    req.row_stride = a.shape[1];
+    if (!a.strides.empty()) {
+      dp::need(a.strides.size() == 2 && a.strides[1] == 4 && a.strides[0] % 4 == 0,
+               "unsupported input strides");
+      req.row_stride = a.strides[0] / 4;
+    }
+    req.missing = std::nanf("");
+    if (config) {
+      dp::json::Value c = dp::json::parse(config);
+      if (const auto* v = c.find("type")) req.type = int32_t(v->i64());
+      if (const auto* v = c.find("iteration_begin")) req.iteration_begin = int32_t(v->i64());
+      if (const auto* v = c.find("iteration_end")) req.iteration_end = int32_t(v->i64());
+      if (const auto* v = c.find("strict_shape")) req.strict_shape = v->boolean;
+      if (const auto* v = c.find("missing")) req.missing = float(v->number());
+    }
+    std::vector<uint64_t> shape;
+    *out_result = b.b->predict(req, shape);
+    b.shape.assign(shape.begin(), shape.end());
+    *out_shape = b.shape.data();
+    *out_dim = b.shape.size();
+  });
+}
+
+int XGBoosterLoadModelFromBuffer(BoosterHandle handle, const void* buf, bst_ulong len) {
+  return guarded([&] {
+    dp::need(buf != nullptr, "null model buffer");
+    bo(handle).b->load_model(std::string(static_cast<const char*>(buf), size_t(len)));
+  });
+}
+
+int XGBoosterLoadModel(BoosterHandle handle, const char* fname) {
+  return guarded([&] {
+    dp::need(fname != nullptr, "null file name");
+    std::ifstream f(fname, std::ios::binary);
+    dp::need(bool(f), std::string("cannot open ") + fname);
+    std::string text((std::istreambuf_iterator<char>(f)), std::istreambuf_iterator<char>());
+    bo(handle).b->load_model(text);
+  });
+}
+
+int XGBoosterSlice(BoosterHandle handle, int begin_layer, int end_layer, int step,
+                   BoosterHandle* out) {
+  return guarded([&] {
+    dp::need(out != nullptr, "null output handle");
+    auto obj = std::make_unique<BoosterObj>();
+    obj->b = bo(handle).b->slice(begin_layer, end_layer, step);
+    *out = obj.release();
+  });
+}
+
 // ---- parity hooks --------------------------------------------------------
 int DPBoosterNumTrees(BoosterHandle handle, int* out) {
   return guarded([&] { *out = int(bo(handle).b->trees().size()); });
@@ -345,6 +409,18 @@ int DPBoosterGetLastGradients(BoosterHandle handle, float* grad, float* hess, bs
 
 int DPBoosterGetLastPositions(BoosterHandle handle, int32_t* out, bst_ulong n) {
   return guarded([&] { bo(handle).b->last_positions(out, size_t(n)); });
+}
+
+int DPValidateHyperparameters(const char* hyperparameters, uint32_t classes, bst_ulong* out_len,
+                              const char** out) {
+  static thread_local std::string result;
+  return guarded([&] {
+    dp::need(hyperparameters && out_len && out, "null argument");
+    dp::need(classes >= 1, "classes must be positive");
+    result = dp::validate_hyperparameters(hyperparameters, classes);
+    *out_len = result.size();
+    *out = result.c_str();
+  });
 }
 
 int DPDMatrixGetCuts(DMatrixHandle handle, int32_t max_bin, int32_t* cut_ptr, float* cut_values,
@@ -464,7 +540,8 @@ void hist_call(dp_workspace ws, const uint8_t* bins, const dp_bin_layout* layout
   ws->commit(s);
   const int64_t per_node = int64_t(layout->n_features) * bin_stride * 2;
   if (!accumulate) dp::launch_fill_i64(hist, per_node * n_nodes, 0, s);
-  dp::launch_hist(bins, *layout, gpair, ridx, d_work, int32_t(work.size()), bin_stride, hist, s);
+  dp::launch_hist(bins, *layout, gpair, ridx, d_work, int32_t(work.size()), nullptr, bin_stride,
+                  hist, s);
 }
 }  // namespace
 
@@ -500,8 +577,8 @@ int dp_evaluate_splits(const int64_t* hist, int32_t n_nodes, int32_t n_features,
                        dp_split_record* out, void* stream) {
   return guarded([&] {
     dp::need(hist && n_bins && node_sums && param && out, "null argument");
-    dp::launch_evaluate(hist, n_nodes, n_features, bin_stride, n_bins, node_sums, nullptr, exp_g,
-                        exp_h, *param, out, as_stream(stream));
+    dp::launch_evaluate(hist, n_nodes, nullptr, n_features, bin_stride, n_bins, node_sums, nullptr,
+                        exp_g, exp_h, *param, out, as_stream(stream));
   });
 }
 
@@ -534,8 +611,9 @@ int dp_partition(dp_workspace ws, const uint8_t* bins, const dp_bin_layout* layo
     ws->commit(s);
     int64_t* work_left = ws->take<int64_t>(work.size());
     int64_t* work_offset = ws->take<int64_t>(work.size());
-    dp::launch_partition(bins, *layout, ridx_in, ridx_out, d_work, int32_t(work.size()), d_begin,
-                         splits, d_first, n_nodes, work_left, work_offset, left_count, s);
+    dp::launch_partition(bins, *layout, ridx_in, ridx_out, d_work, int32_t(work.size()), nullptr,
+                         d_begin, splits, d_first, n_nodes, nullptr, work_left, work_offset,
+                         left_count, s);
   });
 }
 
@@ -546,14 +624,14 @@ int dp_update_margin(dp_workspace ws, const uint32_t* ridx, const int64_t* begin
     dp::need(ws && ridx && begin && end && value && margin, "null argument");
     std::vector<dp::LeafWork> work;
     for (int32_t i = 0; i < n_leaves; ++i)
-      for (int64_t b = begin[i]; b < end[i]; b += 16384)
-        work.push_back({value[i], i, b, std::min<int64_t>(b + 16384, end[i])});
+      for (int64_t b = begin[i]; b < end[i]; b += dp::kLeafChunk)
+        work.push_back({value[i], i, b, std::min(b + dp::kLeafChunk, end[i])});
     hipStream_t s = as_stream(stream);
     ws->begin(sizeof(dp::LeafWork) * work.size() + 256);
     dp::LeafWork* d_work;
     std::copy(work.begin(), work.end(), ws->stage(work.size(), &d_work));
     ws->commit(s);
-    dp::launch_update_margin(ridx, d_work, int32_t(work.size()), margin, stride, s);
+    dp::launch_update_margin(ridx, d_work, int32_t(work.size()), nullptr, margin, stride, s);
   });
 }
 

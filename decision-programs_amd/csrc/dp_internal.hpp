@@ -104,6 +104,37 @@ struct LeafWork {
   int64_t end;
 };
 
+// A node of the level being grown (device-side planning).
+struct LevelNode {
+  int64_t begin, end;  // segment of ridx (buffer = depth & 1)
+  int64_t g, h;        // quantised sums
+  int32_t nid;         // tree node id
+  int32_t parent_slot; // index of the parent in the previous level
+};
+
+// Everything the host needs about one tree node, written by the planner.
+struct NodeInfo {
+  int64_t g, h;        // quantised sums
+  int64_t begin, end;  // final segment (leaves) / segment when split
+  double loss_chg;
+  int32_t left;        // left child id, -1 for a leaf
+  int32_t feature, bin, default_left;
+  float leaf_value, base_weight, sum_hess;
+  int32_t parity;      // ridx buffer holding the segment
+};
+
+// Device counters of the planner (one struct per tree).
+struct PlanCounts {
+  int32_t n_level;     // nodes of the current level
+  int32_t n_nodes;     // nodes allocated in the tree so far
+  int32_t n_hist;      // histogram work items for the current level
+  int32_t n_sub;       // subtraction jobs for the current level
+  int32_t n_part;      // partition work items for the current level
+  int32_t n_leaf;      // leaf work items produced by the last planner run
+  int32_t error;       // nonzero: inconsistent partition counts
+  int32_t pad;
+};
+
 }  // namespace dp
 
 // Device scratch shared by the operator entry points.  Host-side data for a
@@ -157,14 +188,19 @@ struct dp_workspace_s {
 namespace dp {
 
 // ---- kernel launchers (implemented in the .hip files) -------------------
+// Kernels that take (n_host, n_dev) process n_dev ? *n_dev : n_host items; the
+// host value is then an upper bound used to size a persistent grid.
 void launch_fill_i64(int64_t* p, int64_t n, int64_t value, hipStream_t s);
+// p[0 .. (*n_dev) * per) = 0, at most bound * per elements.
+void launch_zero_i64_dev(int64_t* p, const int32_t* n_dev, int64_t per, int64_t bound,
+                         hipStream_t s);
 void launch_fill_u8(uint8_t* p, int64_t n, uint8_t value, hipStream_t s);
 void launch_iota_u32(uint32_t* p, int64_t n, hipStream_t s);
 
 // Histograms: every work item accumulates into hist[slot]; hist must be zero.
 void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t* gpair,
                  const uint32_t* ridx, const HistWork* work, int32_t n_work,
-                 int32_t bin_stride, int64_t* hist, hipStream_t s);
+                 const int32_t* n_work_dev, int32_t bin_stride, int64_t* hist, hipStream_t s);
 // Work items for the histograms of n_nodes row sets (node i: [begin[i],
 // end[i]) of ridx, written to hist slot slots[i], or i when slots is null),
 // chunked and ordered for the XCD-aware dispatch; may contain empty items.
@@ -181,9 +217,10 @@ struct SubtractJob {
 };
 void launch_subtract_many(const int64_t* base_parent, const int64_t* base_child,
                           int64_t* base_out, const SubtractJob* jobs, int32_t n_jobs,
-                          int64_t n, hipStream_t s);
+                          const int32_t* n_jobs_dev, int64_t n, hipStream_t s);
 
-void launch_evaluate(const int64_t* hist, int32_t n_nodes, int32_t n_features,
+void launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_nodes_dev,
+                     int32_t n_features,
                      int32_t bin_stride, const int32_t* n_bins, const int64_t* node_sums,
                      const int32_t* exps, int32_t exp_g, int32_t exp_h,
                      const dp_train_param& param, dp_split_record* out, hipStream_t s);
@@ -191,13 +228,62 @@ void launch_evaluate(const int64_t* hist, int32_t n_nodes, int32_t n_features,
 // Partition: counts, per-node scan, scatter.
 void launch_partition(const uint8_t* bins, const dp_bin_layout& layout, const uint32_t* ridx_in,
                       uint32_t* ridx_out, const PartWork* work, int32_t n_work,
-                      const int64_t* seg_begin, const dp_split_record* splits,
-                      const int32_t* node_first_work, int32_t n_nodes, int64_t* work_left,
+                      const int32_t* n_work_dev, const int64_t* seg_begin,
+                      const dp_split_record* splits, const int32_t* node_first_work,
+                      int32_t n_nodes, const int32_t* n_nodes_dev, int64_t* work_left,
                       int64_t* work_offset, int64_t* node_left, hipStream_t s);
 constexpr int64_t kPartChunk = 4096;
 
 void launch_update_margin(const uint32_t* ridx, const LeafWork* work, int32_t n_work,
-                          float* margin, int64_t stride, hipStream_t s);
+                          const int32_t* n_work_dev, float* margin, int64_t stride, hipStream_t s);
+void launch_leaf_positions(const uint32_t* ridx, const LeafWork* work, int32_t n_work,
+                           const int32_t* n_work_dev, int32_t* positions, hipStream_t s);
+
+// Device-side level planner (grow.hip): one workgroup turns the evaluated
+// level (split records, left counts) into the tree's node records, the next
+// level's nodes, and the next level's histogram / subtraction / partition work
+// plus this level's leaf work.  Counts live in `counts`.
+struct PlanArgs {
+  const LevelNode* cur;
+  const dp_split_record* splits;  // null: every node of this level is a leaf
+  const int64_t* node_left;
+  LevelNode* next;
+  int64_t* next_sums;      // [slot][2]
+  int64_t* next_seg_begin; // [slot]
+  NodeInfo* info;          // indexed by node id
+  HistWork* hist_work;
+  SubtractJob* sub_jobs;
+  PartWork* part_work;
+  int32_t* part_first;     // [n_next + 1]
+  int64_t* pair_chunk;     // scratch: [n_pairs + 1] first chunk of each pair
+  LeafWork* leaf_work;
+  PlanCounts* counts;
+  const int32_t* exps;     // quantiser exponents (gradient, hessian)
+  int32_t depth, max_depth;
+  int32_t n_tiles;
+  int64_t hist_elems;      // int64 values per node histogram
+  double eta, lambda, alpha, mcw;
+  int32_t info_capacity, level_capacity;
+  int32_t hist_capacity, part_capacity, leaf_capacity;
+};
+void launch_plan_level(const PlanArgs& a, hipStream_t s);
+// counts->n_level = 1, n_nodes = 1, ...; cur[0] = root {0, n_rows, g, h, 0, -1}
+// with (g, h) = root_sums[0..1]; sums[0..1] = (g, h), seg_begin[0] = 0; root
+// partition work over [0, n_rows).
+void launch_plan_root(LevelNode* cur, int64_t* sums, int64_t* seg_begin, PartWork* part_work,
+                      int32_t* part_first, PlanCounts* counts, int64_t n_rows,
+                      const int64_t* root_sums, hipStream_t s);
+// Upper bounds of the planner's outputs for a level of at most `nodes` nodes.
+inline int64_t plan_hist_capacity(int64_t nodes, int32_t n_tiles) {
+  return 1024 + (nodes / 2 + 8) * int64_t(n_tiles);
+}
+inline int64_t plan_part_capacity(int64_t nodes, int64_t n_rows) {
+  return n_rows / kPartChunk + 1 + nodes;
+}
+constexpr int64_t kLeafChunk = 16384;
+inline int64_t plan_leaf_capacity(int64_t nodes, int64_t n_rows) {
+  return n_rows / kLeafChunk + 1 + nodes;
+}
 
 void launch_gradients(int32_t objective, const float* margin, const float* label,
                       int64_t n_rows, int32_t n_classes, float* grad, float* hess,

@@ -84,7 +84,19 @@ __global__ void absmax_kernel(const float* __restrict__ grad, const float* __res
     mg = max(mg, __shfl_xor(mg, d, 64));
     mh = max(mh, __shfl_xor(mh, d, 64));
   }
+  // one atomic per workgroup: per-wave atomics on two addresses serialise
+  __shared__ unsigned wave_max[2][4];
+  const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
+    wave_max[0][wave] = mg;
+    wave_max[1][wave] = mh;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < int(blockDim.x >> 6); ++w) {
+      mg = max(mg, wave_max[0][w]);
+      mh = max(mh, wave_max[1][w]);
+    }
     atomicMax(&maxima[2 * k], mg);
     atomicMax(&maxima[2 * k + 1], mh);
   }
@@ -140,7 +152,35 @@ __global__ void quantise_kernel(const float* __restrict__ grad, const float* __r
   }
 }
 
+// Label checks in the spirit of the reference's prepare_labels
+// (class_native_training.cuh:36-41): class ids must be exact integers in [0, K),
+// logistic labels in [0, 1], regression labels finite.
+__global__ void check_labels_kernel(const float* __restrict__ label, int64_t n, int objective,
+                                    int n_classes, int32_t* __restrict__ bad) {
+  bool wrong = false;
+  for (int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; r < n;
+       r += int64_t(blockDim.x) * gridDim.x) {
+    const float y = label[r];
+    if (objective == DP_OBJ_SOFTPROB)
+      wrong = wrong || !(y >= 0.0f) || !(y < float(n_classes)) || y != floorf(y);
+    else if (objective == DP_OBJ_LOGISTIC)
+      wrong = wrong || !(y >= 0.0f && y <= 1.0f);
+    else
+      wrong = wrong || !isfinite(y);
+  }
+  if (__ballot(wrong) && (threadIdx.x & 63) == 0) atomicOr(bad, 1);
+}
+
 }  // namespace
+
+void launch_check_labels(const float* label, int64_t n, int32_t objective, int32_t n_classes,
+                         int32_t* bad, hipStream_t s) {
+  launch_fill_u8(reinterpret_cast<uint8_t*>(bad), 4, 0, s);
+  if (n <= 0) return;
+  hipLaunchKernelGGL(check_labels_kernel, dim3(grid_for(n, 256, 4096)), dim3(256), 0, s, label, n,
+                     objective, n_classes, bad);
+  DP_HIP(hipGetLastError());
+}
 
 void launch_gradients(int32_t objective, const float* margin, const float* label,
                       int64_t n_rows, int32_t n_classes, float* grad, float* hess,
@@ -160,7 +200,8 @@ void launch_quantise(const float* grad, const float* hess, int64_t n_rows, int32
   need(n_classes >= 1 && n_classes <= 65535, "class count out of range");
   launch_fill_u8(reinterpret_cast<uint8_t*>(maxima), int64_t(sizeof(uint32_t)) * 2 * n_classes, 0, s);
   launch_fill_i64(sums, 2 * int64_t(n_classes), 0, s);
-  const int blocks = grid_for(n_rows, 256, 2048);
+  // A few hundred workgroups cover HBM; more only adds atomics on the totals.
+  const int blocks = grid_for(n_rows, 256, 512);
   hipLaunchKernelGGL(absmax_kernel, dim3(blocks, n_classes), dim3(256), 0, s, grad, hess, n_rows,
                      n_classes, reinterpret_cast<unsigned*>(maxima));
   DP_HIP(hipGetLastError());

@@ -81,15 +81,20 @@ constexpr int kHistUnroll = 2;           // rows per lane per pipeline stage
 // (f*8 mod 128), whatever their bins: the 64-bit LDS atomics are conflict free.
 // The LDS address is assembled by one v_perm_b32: byte 1 = the bin byte, byte 0
 // = the lane's feature offset for that step.
+// Workgroups loop over items (item = blockIdx.x + k * gridDim.x); with a grid
+// that is a multiple of 8, item i still runs on XCD i mod 8.
 template <bool MISSING>
 __global__ __launch_bounds__(kHistThreads) void hist_kernel(
     const uint8_t* __restrict__ bins, int64_t n_rows, int32_t n_features,
     const int2* __restrict__ gpair, const uint32_t* __restrict__ ridx,
-    const HistWork* __restrict__ work, int32_t bin_stride,
+    const HistWork* __restrict__ work, int32_t n_work_host,
+    const int32_t* __restrict__ n_work_dev, int32_t bin_stride,
     unsigned long long* __restrict__ hist) {
   __shared__ unsigned long long lds[kLdsWords];
-  const HistWork w = work[blockIdx.x];
-  if (w.begin >= w.end) return;  // padding item (uniform per workgroup)
+  const int32_t n_work = n_work_dev ? *n_work_dev : n_work_host;
+  for (int32_t item = blockIdx.x; item < n_work; item += gridDim.x) {
+  const HistWork w = work[item];
+  if (w.begin >= w.end) continue;  // padding item (uniform per workgroup)
   for (int e = threadIdx.x; e < kLdsWords; e += kHistThreads) lds[e] = 0ull;
   __syncthreads();
 
@@ -160,6 +165,16 @@ __global__ __launch_bounds__(kHistThreads) void hist_kernel(
     if (x == 0ull) continue;
     global_add(out + (int64_t(f) * bin_stride + bin) * 2 + (within >> 4), x);
   }
+  __syncthreads();  // the next item clears the LDS this item just read
+  }
+}
+
+__global__ void zero_i64_dev_kernel(int64_t* __restrict__ p, const int32_t* __restrict__ n_dev,
+                                    int64_t per) {
+  const int64_t n = int64_t(*n_dev) * per;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += int64_t(blockDim.x) * gridDim.x)
+    p[i] = 0;
 }
 
 __global__ void subtract_kernel(const int64_t* __restrict__ parent,
@@ -170,18 +185,22 @@ __global__ void subtract_kernel(const int64_t* __restrict__ parent,
     sibling[i] = parent[i] - built[i];
 }
 
-// blockIdx.y selects the job; the x dimension strides over its n elements.
+// The y dimension loops over jobs; the x dimension strides over their n elements.
 __global__ void subtract_many_kernel(const int64_t* __restrict__ base_parent,
                                      const int64_t* __restrict__ base_child,
                                      int64_t* __restrict__ base_out,
-                                     const SubtractJob* __restrict__ jobs, int64_t n) {
-  const SubtractJob j = jobs[blockIdx.y];
-  const int64_t* p = base_parent + j.parent;
-  const int64_t* c = base_child + j.built;
-  int64_t* s = base_out + j.sibling;
-  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
-       i += int64_t(blockDim.x) * gridDim.x)
-    s[i] = p[i] - c[i];
+                                     const SubtractJob* __restrict__ jobs, int32_t n_jobs_host,
+                                     const int32_t* __restrict__ n_jobs_dev, int64_t n) {
+  const int32_t n_jobs = n_jobs_dev ? *n_jobs_dev : n_jobs_host;
+  for (int32_t job = blockIdx.y; job < n_jobs; job += gridDim.y) {
+    const SubtractJob j = jobs[job];
+    const int64_t* p = base_parent + j.parent;
+    const int64_t* c = base_child + j.built;
+    int64_t* s = base_out + j.sibling;
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += int64_t(blockDim.x) * gridDim.x)
+      s[i] = p[i] - c[i];
+  }
 }
 
 }  // namespace
@@ -237,21 +256,34 @@ std::vector<HistWork> make_hist_work(const dp_bin_layout& layout, const int64_t*
 }
 
 void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t* gpair,
-                 const uint32_t* ridx, const HistWork* work, int32_t n_work, int32_t bin_stride,
-                 int64_t* hist, hipStream_t s) {
+                 const uint32_t* ridx, const HistWork* work, int32_t n_work,
+                 const int32_t* n_work_dev, int32_t bin_stride, int64_t* hist, hipStream_t s) {
   if (n_work <= 0) return;
   need(bin_stride >= 1 && bin_stride <= kMaxBins, "histogram bin stride out of range");
   need(layout.tile_width == kTile, "histogram kernel needs 16-feature tiles");
   auto* out = reinterpret_cast<unsigned long long*>(hist);
   const auto* gp = reinterpret_cast<const int2*>(gpair);
+  // At most 1024 resident workgroups (2 per CU, two rounds); a multiple of 8.
+  int grid = n_work < 1024 ? n_work : 1024;
+  grid = (grid + 7) / 8 * 8;
   if (layout.missing_bin >= 0) {
     need(layout.missing_bin == 255, "missing bin must be 255");
-    hipLaunchKernelGGL(hist_kernel<true>, dim3(n_work), dim3(kHistThreads), 0, s, bins,
-                       layout.n_rows, layout.n_features, gp, ridx, work, bin_stride, out);
+    hipLaunchKernelGGL(hist_kernel<true>, dim3(grid), dim3(kHistThreads), 0, s, bins,
+                       layout.n_rows, layout.n_features, gp, ridx, work, n_work, n_work_dev,
+                       bin_stride, out);
   } else {
-    hipLaunchKernelGGL(hist_kernel<false>, dim3(n_work), dim3(kHistThreads), 0, s, bins,
-                       layout.n_rows, layout.n_features, gp, ridx, work, bin_stride, out);
+    hipLaunchKernelGGL(hist_kernel<false>, dim3(grid), dim3(kHistThreads), 0, s, bins,
+                       layout.n_rows, layout.n_features, gp, ridx, work, n_work, n_work_dev,
+                       bin_stride, out);
   }
+  DP_HIP(hipGetLastError());
+}
+
+void launch_zero_i64_dev(int64_t* p, const int32_t* n_dev, int64_t per, int64_t bound,
+                         hipStream_t s) {
+  if (bound <= 0 || per <= 0) return;
+  hipLaunchKernelGGL(zero_i64_dev_kernel, dim3(grid_for(bound * per, 256, 8192)), dim3(256), 0, s,
+                     p, n_dev, per);
   DP_HIP(hipGetLastError());
 }
 
@@ -264,11 +296,12 @@ void launch_subtract(const int64_t* parent, const int64_t* built, int64_t* sibli
 }
 
 void launch_subtract_many(const int64_t* base_parent, const int64_t* base_child,
-                          int64_t* base_out, const SubtractJob* jobs, int32_t n_jobs, int64_t n,
-                          hipStream_t s) {
+                          int64_t* base_out, const SubtractJob* jobs, int32_t n_jobs,
+                          const int32_t* n_jobs_dev, int64_t n, hipStream_t s) {
   if (n_jobs <= 0 || n <= 0) return;
-  hipLaunchKernelGGL(subtract_many_kernel, dim3(grid_for(n, 256, 64), n_jobs), dim3(256), 0, s,
-                     base_parent, base_child, base_out, jobs, n);
+  const int gy = n_jobs < 256 ? n_jobs : 256;
+  hipLaunchKernelGGL(subtract_many_kernel, dim3(grid_for(n, 256, 32), gy), dim3(256), 0, s,
+                     base_parent, base_child, base_out, jobs, n_jobs, n_jobs_dev, n);
   DP_HIP(hipGetLastError());
 }
 

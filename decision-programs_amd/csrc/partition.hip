@@ -33,16 +33,20 @@ __device__ __forceinline__ bool goes_left(const uint8_t* __restrict__ bins, int6
 
 __device__ __forceinline__ int popc64(unsigned long long m) { return __popcll(m); }
 
+// The partition kernels loop over their items (item = blockIdx.x + k * gridDim.x).
 __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
     const uint8_t* __restrict__ bins, int64_t n_rows, int tile_width, int missing_bin,
-    const uint32_t* __restrict__ ridx, const PartWork* __restrict__ work,
-    const dp_split_record* __restrict__ splits, int64_t* __restrict__ work_left) {
+    const uint32_t* __restrict__ ridx, const PartWork* __restrict__ work, int32_t n_work_host,
+    const int32_t* __restrict__ n_work_dev, const dp_split_record* __restrict__ splits,
+    int64_t* __restrict__ work_left) {
   __shared__ int wave_count[kPartThreads / 64];
-  const PartWork w = work[blockIdx.x];
+  const int32_t n_work = n_work_dev ? *n_work_dev : n_work_host;
+  for (int32_t item = blockIdx.x; item < n_work; item += gridDim.x) {
+  const PartWork w = work[item];
   const dp_split_record s = splits[w.node];
   if (!s.expand) {
-    if (threadIdx.x == 0) work_left[blockIdx.x] = 0;
-    return;
+    if (threadIdx.x == 0) work_left[item] = 0;
+    continue;
   }
   int count = 0;
   for (int step = 0; step < kPartSteps; ++step) {
@@ -59,17 +63,21 @@ __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
   if (threadIdx.x == 0) {
     int64_t t = 0;
     for (int k = 0; k < kPartThreads / 64; ++k) t += wave_count[k];
-    work_left[blockIdx.x] = t;
+    work_left[item] = t;
+  }
+  __syncthreads();
   }
 }
 
 // One workgroup per node: exclusive scan of its chunks' left counts.
 __global__ __launch_bounds__(kPartThreads) void part_scan_kernel(
-    const int32_t* __restrict__ node_first_work, const int64_t* __restrict__ work_left,
+    const int32_t* __restrict__ node_first_work, int32_t n_nodes_host,
+    const int32_t* __restrict__ n_nodes_dev, const int64_t* __restrict__ work_left,
     int64_t* __restrict__ work_offset, int64_t* __restrict__ node_left) {
   __shared__ int64_t partial[kPartThreads];
   __shared__ int64_t carry;
-  const int node = blockIdx.x;
+  const int32_t n_nodes = n_nodes_dev ? *n_nodes_dev : n_nodes_host;
+  for (int node = blockIdx.x; node < n_nodes; node += gridDim.x) {
   const int first = node_first_work[node], last = node_first_work[node + 1];
   if (threadIdx.x == 0) carry = 0;
   __syncthreads();
@@ -91,21 +99,26 @@ __global__ __launch_bounds__(kPartThreads) void part_scan_kernel(
     __syncthreads();
   }
   if (threadIdx.x == 0) node_left[node] = carry;
+  __syncthreads();
+  }
 }
 
 __global__ __launch_bounds__(kPartThreads) void part_scatter_kernel(
     const uint8_t* __restrict__ bins, int64_t n_rows, int tile_width, int missing_bin,
     const uint32_t* __restrict__ ridx_in, uint32_t* __restrict__ ridx_out,
-    const PartWork* __restrict__ work, const dp_split_record* __restrict__ splits,
+    const PartWork* __restrict__ work, int32_t n_work_host,
+    const int32_t* __restrict__ n_work_dev, const dp_split_record* __restrict__ splits,
     const int64_t* __restrict__ seg_begin, const int64_t* __restrict__ work_offset,
     const int64_t* __restrict__ node_left) {
   __shared__ int wave_count[kPartThreads / 64];
-  const PartWork w = work[blockIdx.x];
+  const int32_t n_work = n_work_dev ? *n_work_dev : n_work_host;
+  for (int32_t item = blockIdx.x; item < n_work; item += gridDim.x) {
+  const PartWork w = work[item];
   const dp_split_record s = splits[w.node];
-  if (!s.expand) return;
+  if (!s.expand) continue;
   const int64_t begin = seg_begin[w.node];
   const int64_t n_left = node_left[w.node];
-  int64_t lefts_before = work_offset[blockIdx.x];  // lefts before this step
+  int64_t lefts_before = work_offset[item];  // lefts before this step
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   for (int step = 0; step < kPartSteps; ++step) {
@@ -141,60 +154,74 @@ __global__ __launch_bounds__(kPartThreads) void part_scatter_kernel(
     lefts_before += step_total;
     __syncthreads();
   }
+  }
 }
 
 __global__ void update_margin_kernel(const uint32_t* __restrict__ ridx,
-                                     const LeafWork* __restrict__ work, float* __restrict__ margin,
-                                     int64_t stride) {
-  const LeafWork w = work[blockIdx.x];
-  for (int64_t i = w.begin + threadIdx.x; i < w.end; i += blockDim.x)
-    margin[int64_t(ridx[i]) * stride] += w.value;
+                                     const LeafWork* __restrict__ work, int32_t n_work_host,
+                                     const int32_t* __restrict__ n_work_dev,
+                                     float* __restrict__ margin, int64_t stride) {
+  const int32_t n_work = n_work_dev ? *n_work_dev : n_work_host;
+  for (int32_t item = blockIdx.x; item < n_work; item += gridDim.x) {
+    const LeafWork w = work[item];
+    for (int64_t i = w.begin + threadIdx.x; i < w.end; i += blockDim.x)
+      margin[int64_t(ridx[i]) * stride] += w.value;
+  }
 }
 
 __global__ void leaf_positions_kernel(const uint32_t* __restrict__ ridx,
-                                      const LeafWork* __restrict__ work,
+                                      const LeafWork* __restrict__ work, int32_t n_work_host,
+                                      const int32_t* __restrict__ n_work_dev,
                                       int32_t* __restrict__ positions) {
-  const LeafWork w = work[blockIdx.x];
-  for (int64_t i = w.begin + threadIdx.x; i < w.end; i += blockDim.x)
-    positions[ridx[i]] = w.pad;
+  const int32_t n_work = n_work_dev ? *n_work_dev : n_work_host;
+  for (int32_t item = blockIdx.x; item < n_work; item += gridDim.x) {
+    const LeafWork w = work[item];
+    for (int64_t i = w.begin + threadIdx.x; i < w.end; i += blockDim.x)
+      positions[ridx[i]] = w.pad;
+  }
 }
 
 }  // namespace
 
 void launch_leaf_positions(const uint32_t* ridx, const LeafWork* work, int32_t n_work,
-                           int32_t* positions, hipStream_t s) {
+                           const int32_t* n_work_dev, int32_t* positions, hipStream_t s) {
   if (n_work <= 0) return;
-  hipLaunchKernelGGL(leaf_positions_kernel, dim3(n_work), dim3(256), 0, s, ridx, work, positions);
+  hipLaunchKernelGGL(leaf_positions_kernel, dim3(n_work < 2048 ? n_work : 2048), dim3(256), 0, s,
+                     ridx, work, n_work, n_work_dev, positions);
   DP_HIP(hipGetLastError());
 }
 
 void launch_partition(const uint8_t* bins, const dp_bin_layout& layout, const uint32_t* ridx_in,
                       uint32_t* ridx_out, const PartWork* work, int32_t n_work,
-                      const int64_t* seg_begin, const dp_split_record* splits,
-                      const int32_t* node_first_work, int32_t n_nodes, int64_t* work_left,
+                      const int32_t* n_work_dev, const int64_t* seg_begin,
+                      const dp_split_record* splits, const int32_t* node_first_work,
+                      int32_t n_nodes, const int32_t* n_nodes_dev, int64_t* work_left,
                       int64_t* work_offset, int64_t* node_left, hipStream_t s) {
   if (n_nodes <= 0) return;
   const int missing = layout.missing_bin;
+  const int gw = n_work < 2048 ? n_work : 2048;
+  const int gn = n_nodes < 512 ? n_nodes : 512;
   if (n_work > 0)
-    hipLaunchKernelGGL(part_count_kernel, dim3(n_work), dim3(kPartThreads), 0, s, bins,
-                       layout.n_rows, layout.tile_width, missing, ridx_in, work, splits,
+    hipLaunchKernelGGL(part_count_kernel, dim3(gw), dim3(kPartThreads), 0, s, bins, layout.n_rows,
+                       layout.tile_width, missing, ridx_in, work, n_work, n_work_dev, splits,
                        work_left);
   DP_HIP(hipGetLastError());
-  hipLaunchKernelGGL(part_scan_kernel, dim3(n_nodes), dim3(kPartThreads), 0, s, node_first_work,
-                     work_left, work_offset, node_left);
+  hipLaunchKernelGGL(part_scan_kernel, dim3(gn), dim3(kPartThreads), 0, s, node_first_work,
+                     n_nodes, n_nodes_dev, work_left, work_offset, node_left);
   DP_HIP(hipGetLastError());
   if (n_work > 0)
-    hipLaunchKernelGGL(part_scatter_kernel, dim3(n_work), dim3(kPartThreads), 0, s, bins,
-                       layout.n_rows, layout.tile_width, missing, ridx_in, ridx_out, work, splits,
-                       seg_begin, work_offset, node_left);
+    hipLaunchKernelGGL(part_scatter_kernel, dim3(gw), dim3(kPartThreads), 0, s, bins,
+                       layout.n_rows, layout.tile_width, missing, ridx_in, ridx_out, work, n_work,
+                       n_work_dev, splits, seg_begin, work_offset, node_left);
   DP_HIP(hipGetLastError());
 }
 
 void launch_update_margin(const uint32_t* ridx, const LeafWork* work, int32_t n_work,
-                          float* margin, int64_t stride, hipStream_t s) {
+                          const int32_t* n_work_dev, float* margin, int64_t stride,
+                          hipStream_t s) {
   if (n_work <= 0) return;
-  hipLaunchKernelGGL(update_margin_kernel, dim3(n_work), dim3(256), 0, s, ridx, work, margin,
-                     stride);
+  hipLaunchKernelGGL(update_margin_kernel, dim3(n_work < 2048 ? n_work : 2048), dim3(256), 0, s,
+                     ridx, work, n_work, n_work_dev, margin, stride);
   DP_HIP(hipGetLastError());
 }
 

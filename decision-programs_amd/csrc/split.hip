@@ -21,7 +21,7 @@
 namespace dp {
 namespace {
 
-constexpr int kEvalThreads = 256;
+constexpr int kEvalThreads = 1024;
 constexpr int kEvalWaves = kEvalThreads / 64;
 
 struct Param {
@@ -78,13 +78,15 @@ __device__ __forceinline__ Cand shfl_xor_cand(const Cand& c, int mask) {
 // BPL: bins per lane (bin_stride <= 64 * BPL).
 template <int BPL>
 __global__ __launch_bounds__(kEvalThreads) void evaluate_kernel(
-    const long long* __restrict__ hist, int32_t n_features, int32_t bin_stride,
+    const long long* __restrict__ hist, int32_t n_nodes_host,
+    const int32_t* __restrict__ n_nodes_dev, int32_t n_features, int32_t bin_stride,
     const int32_t* __restrict__ n_bins, const long long* __restrict__ node_sums,
     const int32_t* __restrict__ exps, int32_t exp_g_host, int32_t exp_h_host, Param p,
     dp_split_record* __restrict__ out) {
   __shared__ Cand wave_best[kEvalWaves];
-  const int node = blockIdx.x;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int32_t n_nodes = n_nodes_dev ? *n_nodes_dev : n_nodes_host;
+  for (int node = blockIdx.x; node < n_nodes; node += gridDim.x) {
   const int exp_g = exps ? exps[0] : exp_g_host;
   const int exp_h = exps ? exps[1] : exp_h_host;
   const double ug = ldexp(1.0, -exp_g), uh = ldexp(1.0, -exp_h);
@@ -181,11 +183,14 @@ __global__ __launch_bounds__(kEvalThreads) void evaluate_kernel(
     rec.pad = 0;
     out[node] = rec;
   }
+  __syncthreads();  // wave_best is reused by the next node
+  }
 }
 
 }  // namespace
 
-void launch_evaluate(const int64_t* hist, int32_t n_nodes, int32_t n_features,
+void launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_nodes_dev,
+                     int32_t n_features,
                      int32_t bin_stride, const int32_t* n_bins, const int64_t* node_sums,
                      const int32_t* exps, int32_t exp_g, int32_t exp_h,
                      const dp_train_param& param, dp_split_record* out, hipStream_t s) {
@@ -195,15 +200,16 @@ void launch_evaluate(const int64_t* hist, int32_t n_nodes, int32_t n_features,
           double(param.gamma)};
   const auto* h = reinterpret_cast<const long long*>(hist);
   const auto* sums = reinterpret_cast<const long long*>(node_sums);
+  const int grid = n_nodes < 512 ? n_nodes : 512;
   if (bin_stride <= 64)
-    hipLaunchKernelGGL(evaluate_kernel<1>, dim3(n_nodes), dim3(kEvalThreads), 0, s, h,
-                       n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p, out);
+    hipLaunchKernelGGL(evaluate_kernel<1>, dim3(grid), dim3(kEvalThreads), 0, s, h,
+                       n_nodes, n_nodes_dev, n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p, out);
   else if (bin_stride <= 128)
-    hipLaunchKernelGGL(evaluate_kernel<2>, dim3(n_nodes), dim3(kEvalThreads), 0, s, h,
-                       n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p, out);
+    hipLaunchKernelGGL(evaluate_kernel<2>, dim3(grid), dim3(kEvalThreads), 0, s, h,
+                       n_nodes, n_nodes_dev, n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p, out);
   else
-    hipLaunchKernelGGL(evaluate_kernel<4>, dim3(n_nodes), dim3(kEvalThreads), 0, s, h,
-                       n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p, out);
+    hipLaunchKernelGGL(evaluate_kernel<4>, dim3(grid), dim3(kEvalThreads), 0, s, h,
+                       n_nodes, n_nodes_dev, n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p, out);
   DP_HIP(hipGetLastError());
 }
 

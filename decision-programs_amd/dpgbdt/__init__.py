@@ -99,6 +99,14 @@ def load():
         "XGBoosterSaveJsonConfig": (c_int, [H, POINTER(c_uint64), POINTER(c_char_p)]),
         "XGBoosterSaveModel": (c_int, [H, c_char_p]),
         "XGBoosterSaveModelToBuffer": (c_int, [H, c_char_p, POINTER(c_uint64), POINTER(c_char_p)]),
+        "XGBoosterPredictFromCudaArray": (c_int, [H, c_char_p, c_char_p, H,
+                                                  POINTER(POINTER(c_uint64)), POINTER(c_uint64),
+                                                  POINTER(POINTER(ctypes.c_float))]),
+        "XGBoosterLoadModelFromBuffer": (c_int, [H, c_void_p, c_uint64]),
+        "XGBoosterLoadModel": (c_int, [H, c_char_p]),
+        "XGBoosterSlice": (c_int, [H, c_int, c_int, c_int, POINTER(H)]),
+        "DPValidateHyperparameters": (c_int, [c_char_p, ctypes.c_uint32, POINTER(c_uint64),
+                                              POINTER(c_char_p)]),
         "DPBoosterNumTrees": (c_int, [H, POINTER(c_int)]),
         "DPBoosterGetTree": (c_int, [H, c_int, POINTER(TreeView)]),
         "DPBoosterGetMargins": (c_int, [H, c_void_p, c_uint64]),
@@ -251,6 +259,48 @@ class Booster:
     def save_model(self, path):
         check(load().XGBoosterSaveModel(self.handle, str(path).encode()))
 
+    def predict(self, values, margin=False, iteration_begin=0, iteration_end=0, strict=True,
+                missing=float("nan")):
+        """Device prediction -> torch tensor (a copy of the library-owned output)."""
+        import torch
+
+        shape_p = POINTER(c_uint64)()
+        dim = c_uint64()
+        out = POINTER(ctypes.c_float)()
+        cfg = json.dumps({"type": 1 if margin else 0, "training": False,
+                          "iteration_begin": iteration_begin, "iteration_end": iteration_end,
+                          "strict_shape": bool(strict), "cache_id": 0, "missing": missing})
+        check(load().XGBoosterPredictFromCudaArray(self.handle, array_interface(values).encode(),
+                                                   cfg.encode(), None, ctypes.byref(shape_p),
+                                                   ctypes.byref(dim), ctypes.byref(out)))
+        shape = [shape_p[i] for i in range(dim.value)]
+        n = 1
+        for d in shape:
+            n *= d
+        # wrap the device pointer with torch through a raw copy
+        res = torch.empty(shape, dtype=torch.float32, device=values.device)
+        if n:
+            import ctypes as _c
+            hip = _hip_memcpy()
+            hip(_c.c_void_p(res.data_ptr()), _c.c_void_p(_c.addressof(out.contents)), n * 4)
+        return res
+
+    @classmethod
+    def from_buffer(cls, text):
+        b = cls()
+        raw = text.encode() if isinstance(text, str) else bytes(text)
+        buf = ctypes.create_string_buffer(raw, len(raw))
+        check(load().XGBoosterLoadModelFromBuffer(b.handle, buf, len(raw)))
+        return b
+
+    def slice(self, begin, end, step=1):
+        out = c_void_p()
+        check(load().XGBoosterSlice(self.handle, begin, end, step, ctypes.byref(out)))
+        b = Booster.__new__(Booster)
+        b._cache = []
+        b.handle = out
+        return b
+
     def num_trees(self):
         out = c_int()
         check(load().DPBoosterNumTrees(self.handle, ctypes.byref(out)))
@@ -306,6 +356,29 @@ class Booster:
         if getattr(self, "handle", None) and _lib is not None:
             _lib.XGBoosterFree(self.handle)
             self.handle = None
+
+
+_memcpy = None
+
+
+def _hip_memcpy():
+    """hipMemcpy (default kind) from the HIP runtime this process already uses."""
+    global _memcpy
+    if _memcpy is None:
+        import torch  # noqa: F401  (its HIP runtime is the one loaded)
+
+        rt = ctypes.CDLL("libamdhip64.so.7")
+        fn = rt.hipMemcpy
+        fn.argtypes = [c_void_p, c_void_p, c_size_t, c_int]
+        fn.restype = c_int
+
+        def copy(dst, src, nbytes):
+            status = fn(dst, src, nbytes, 4)  # hipMemcpyDefault
+            if status != 0:
+                raise DPError(f"hipMemcpy failed with status {status}")
+
+        _memcpy = copy
+    return _memcpy
 
 
 from . import ops  # noqa: E402  (kernel-level operators)

@@ -112,6 +112,28 @@ int XGBoosterSaveModel(BoosterHandle handle, const char* fname);
 int XGBoosterSaveModelToBuffer(BoosterHandle handle, const char* config, bst_ulong* out_len,
                                const char** out_dptr);
 
+/* Prediction from a dense float32 device array interface [N, F]
+ * (class_model_native_adapter.cuh:30, class_study_train.cu:151-163).  config:
+ * {"type": 0 value | 1 margin, "iteration_begin", "iteration_end" (rounds, 0 =
+ * all), "strict_shape", "missing", "training", "cache_id"}.  Value type applies
+ * the objective (logistic probability, softprob probabilities, softmax class
+ * id).  *out_result is library-owned device memory valid until the next
+ * prediction on this booster; proxy must be NULL. */
+int XGBoosterPredictFromCudaArray(BoosterHandle handle, const char* values, const char* config,
+                                  DMatrixHandle proxy, const bst_ulong** out_shape,
+                                  bst_ulong* out_dim, const float** out_result);
+
+/* XGBoost-3.4.1-schema JSON model from memory / a file (class_study_train.cu:
+ * 92-99, class_model_native_adapter.cuh:28).  The booster then predicts and
+ * exports; it cannot continue training. */
+int XGBoosterLoadModelFromBuffer(BoosterHandle handle, const void* buf, bst_ulong len);
+int XGBoosterLoadModel(BoosterHandle handle, const char* fname);
+
+/* Rounds [begin_layer, end_layer) with step as a new booster (end 0 = all),
+ * as the reference uses to clone a full-round view (class_study_train.cu:132). */
+int XGBoosterSlice(BoosterHandle handle, int begin_layer, int end_layer, int step,
+                   BoosterHandle* out);
+
 /* ---- parity hooks on a booster (extensions) ---------------------------- */
 typedef struct {
   int32_t n_nodes;
@@ -139,6 +161,19 @@ int DPBoosterGetLastGradients(BoosterHandle handle, float* grad, float* hess, bs
                               int32_t* exps);
 /* Final node id of every row in the last tree (the row partition). */
 int DPBoosterGetLastPositions(BoosterHandle handle, int32_t* out, bst_ulong n);
+
+/* Validates and defaults a training-hyperparameter object the way the reference
+ * does before training (class_native_training.cuh:16-33, via
+ * ResidentTrainer::validate_hyperparameters, class_study_train.cu:203-206):
+ * only rounds, max_depth, eta, lambda, alpha, gamma, min_child_weight, max_bin,
+ * seed, subsample, colsample_by{tree,level,node}; rounds and max_depth required
+ * positive integers (rounds <= INT_MAX / classes); max_bin >= 2 (default 256);
+ * seed >= 0 (default 0); eta in (0, 1] (0.3); lambda, alpha, gamma,
+ * min_child_weight finite >= 0 (1, 0, 0, 1); sampling keys in (0, 1] and kept
+ * only when given.  Writes the normalised JSON (library-owned string, valid
+ * until the next call on this thread). */
+int DPValidateHyperparameters(const char* hyperparameters, uint32_t classes, bst_ulong* out_len,
+                              const char** out);
 
 /* Quantile cuts and bins the booster trained on (built at first use). */
 int DPDMatrixGetCuts(DMatrixHandle handle, int32_t max_bin, int32_t* cut_ptr,

@@ -164,3 +164,91 @@ def test_regularisation_paths(dp, oracle, device):
     bst, x, o_trees, o_margin, pos, n = _train_both(dp, oracle, device, 1, 8000, 8, 0, 1, p, 3,
                                                     31)
     _compare(bst, o_trees, o_margin, pos, n, 1)
+
+
+def _small_booster(dp, config, n, f, objective, k, rounds, depth=5, seed=7, max_bin=256):
+    from dpgbdt import ops
+
+    values, labels, _, _ = ops.synth(config, n, seed, n_features=f)
+    obj = {0: "binary:logistic", 1: "multi:softmax", 2: "reg:squarederror"}[objective]
+    params = {"objective": obj, "max_depth": depth, "eta": 0.3, "max_bin": max_bin}
+    if objective == 1:
+        params["num_class"] = k
+    dtrain = dp.DMatrix(values, labels)
+    bst = dp.Booster(params, [dtrain])
+    for r in range(rounds):
+        bst.update(dtrain, r)
+    return bst, values, labels
+
+
+@pytest.mark.parametrize("config,n,f,objective,k", [(1, 5000, 8, 0, 1), (4, 1500, 784, 1, 10),
+                                                     (5, 4000, 60, 2, 1)])
+def test_prediction_equals_training_margins(dp, device, config, n, f, objective, k):
+    import model_reader
+
+    bst, values, labels = _small_booster(dp, config, n, f, objective, k, 4)
+    margins = bst.margins(n, k)
+    pm = bst.predict(values, margin=True).cpu().numpy()
+    np.testing.assert_array_equal(pm.view(np.uint32), margins.view(np.uint32))
+    doc = json.loads(bst.save_raw())
+    model_reader.read_model(doc)
+    walked = model_reader.predict_margin(doc, values.cpu().numpy())
+    base = 0.0
+    np.testing.assert_array_equal((walked + base).view(np.uint32), margins.view(np.uint32))
+    # iteration ranges and slices agree
+    p2 = bst.predict(values, margin=True, iteration_end=2).cpu().numpy()
+    s2 = bst.slice(0, 2).predict(values, margin=True).cpu().numpy()
+    np.testing.assert_array_equal(p2, s2)
+    assert not np.array_equal(p2, pm)
+    # a reloaded model predicts the same bits
+    again = dp.Booster.from_buffer(bst.save_raw())
+    np.testing.assert_array_equal(again.predict(values, margin=True).cpu().numpy(), pm)
+    assert again.num_boosted_rounds() == 4
+
+
+def test_prediction_transforms(dp, device):
+    bst, values, labels = _small_booster(dp, 1, 5000, 8, 0, 1, 3)
+    m = bst.predict(values, margin=True).cpu().numpy()[:, 0].astype(np.float64)
+    p = bst.predict(values).cpu().numpy()[:, 0]
+    np.testing.assert_allclose(p, 1 / (1 + np.exp(-m)), rtol=3e-6, atol=1e-7)
+    bst, values, labels = _small_booster(dp, 4, 1500, 784, 1, 10, 3)
+    m = bst.predict(values, margin=True).cpu().numpy()
+    cls = bst.predict(values).cpu().numpy()
+    assert cls.shape == (1500, 1)
+    np.testing.assert_array_equal(cls[:, 0], np.argmax(m, axis=1).astype(np.float32))
+    # the reference's probability view: slice a full clone, switch to softprob
+    view = bst.slice(0, 0)
+    view.set_param("objective", "multi:softprob")
+    prob = view.predict(values).cpu().numpy()
+    assert prob.shape == (1500, 10)
+    np.testing.assert_allclose(prob.sum(axis=1), 1.0, atol=2e-6)
+    e = np.exp(m - m.max(axis=1, keepdims=True))
+    np.testing.assert_allclose(prob, e / e.sum(axis=1, keepdims=True), atol=2e-6)
+    model = json.loads(view.save_raw())
+    assert model["learner"]["objective"]["name"] == "multi:softprob"
+
+
+def test_invalid_labels_are_refused(dp, device):
+    import torch
+    from dpgbdt import ops
+
+    values, _, _, _ = ops.synth(1, 1000, 3)
+    bad = torch.full((1000,), 3.0, device=device)
+    dtrain = dp.DMatrix(values, bad)
+    bst = dp.Booster({"objective": "multi:softmax", "num_class": 3}, [dtrain])
+    with pytest.raises(dp.DPError, match="class ids"):
+        bst.update(dtrain, 0)
+    half = torch.full((1000,), 0.5, device=device)
+    dtrain = dp.DMatrix(values, half)
+    bst = dp.Booster({"objective": "multi:softmax", "num_class": 3}, [dtrain])
+    with pytest.raises(dp.DPError, match="class ids"):
+        bst.update(dtrain, 0)
+    two = torch.full((1000,), 2.0, device=device)
+    dtrain = dp.DMatrix(values, two)
+    bst = dp.Booster({"objective": "binary:logistic"}, [dtrain])
+    with pytest.raises(dp.DPError, match=r"\[0, 1\]"):
+        bst.update(dtrain, 0)
+    inf = values.clone()
+    inf[3, 2] = float("inf")
+    with pytest.raises(dp.DPError, match="inf"):
+        dp.DMatrix(inf, half)

@@ -1,0 +1,63 @@
+"""Host-side contract of the trainer, without a GPU: hyperparameter validation
+as the reference performs it before training (native/class_native_training.cuh:16-33,
+reached through ResidentTrainer::validate_hyperparameters), including the three
+refusals of native/class_study_train_checks.cpp:14 and the accepted case of :13."""
+import ctypes
+import json
+
+import pytest
+
+
+def validate(dp, hp, classes=3):
+    lib = dp.load()
+    n, out = ctypes.c_uint64(), ctypes.c_char_p()
+    lib.DPValidateHyperparameters.argtypes = [ctypes.c_char_p, ctypes.c_uint32,
+                                              ctypes.POINTER(ctypes.c_uint64),
+                                              ctypes.POINTER(ctypes.c_char_p)]
+    rc = lib.DPValidateHyperparameters(json.dumps(hp).encode(), classes, ctypes.byref(n),
+                                       ctypes.byref(out))
+    if rc != 0:
+        raise dp.DPError(lib.XGBGetLastError().decode())
+    return json.loads(ctypes.string_at(out, n.value).decode())
+
+
+def test_reference_accepted_case(dp):
+    hp = validate(dp, {"rounds": 2, "max_depth": 3}, 3)
+    assert hp["rounds"] == 2 and hp["max_depth"] == 3
+    assert (hp["max_bin"], hp["seed"], hp["eta"], hp["lambda"], hp["alpha"], hp["gamma"],
+            hp["min_child_weight"]) == (256, 0, 0.3, 1.0, 0.0, 0.0, 1.0)
+    assert "subsample" not in hp
+
+
+@pytest.mark.parametrize("hp", [
+    {"rounds": 0, "max_depth": 2},
+    {"rounds": 2, "max_depth": 2, "unknown": 1},
+    {"rounds": 2, "max_depth": 2, "eta": 0.0},
+])
+def test_reference_refusals(dp, hp):
+    with pytest.raises(dp.DPError):
+        validate(dp, hp, 3)
+
+
+@pytest.mark.parametrize("hp,msg", [
+    ({"rounds": -1, "max_depth": 2}, "nonnegative"),
+    ({"rounds": 2.0, "max_depth": 2}, "integer"),
+    ({"rounds": 2, "max_depth": 0}, "positive"),
+    ({"max_depth": 2}, "rounds"),
+    ({"rounds": 2, "max_depth": 2, "eta": 1.5}, "range"),
+    ({"rounds": 2, "max_depth": 2, "lambda": -1}, "range"),
+    ({"rounds": 2, "max_depth": 2, "subsample": 0}, "range"),
+    ({"rounds": 2, "max_depth": 2, "max_bin": 1}, "max_bin"),
+    ({"rounds": 2**31 // 3 + 1, "max_depth": 2}, "capacity"),
+    ({"rounds": 2, "max_depth": 2, "gamma": "1"}, "numeric"),
+])
+def test_more_refusals(dp, hp, msg):
+    with pytest.raises(dp.DPError, match=msg):
+        validate(dp, hp, 3)
+
+
+def test_sampling_keys_kept_when_given(dp):
+    hp = validate(dp, {"rounds": 5, "max_depth": 4, "subsample": 1, "colsample_bynode": 0.5,
+                       "eta": 1, "max_bin": 64, "seed": 7}, 10)
+    assert hp["subsample"] == 1.0 and hp["colsample_bynode"] == 0.5
+    assert (hp["eta"], hp["max_bin"], hp["seed"]) == (1.0, 64, 7)
