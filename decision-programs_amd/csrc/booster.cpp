@@ -226,8 +226,8 @@ void Grower::ensure_level(const Quantized& q, int64_t nb, int32_t d, int32_t D) 
   sums_[nxt].reserve(size_t(2 * std::max<int64_t>(nn, 1)));
   seg_begin_[nxt].reserve(size_t(std::max<int64_t>(nn, 1)));
   hist_work_[nxt].reserve(size_t(plan_hist_capacity(nn, T)));
-  sub_jobs_[nxt].reserve(size_t(nn / 2 + 1));
-  pair_chunk_.reserve(size_t(nn / 2 + 1));
+  reduce_jobs_[nxt].reserve(size_t(nn / 2 + 1));
+  pair_chunk_.reserve(size_t(2 * (std::max(nb, nn) + 1)));
   part_work_[nxt].reserve(size_t(plan_part_capacity(nn, N)));
   part_first_[nxt].reserve(size_t(nn + 1));
   leaf_work_.reserve(size_t(plan_leaf_capacity(nb, N)));
@@ -251,14 +251,20 @@ void Grower::prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, h
   seg_begin_[0].reserve(1);
   part_work_[0].reserve(size_t(plan_part_capacity(1, N)));
   part_first_[0].reserve(2);
-  if (root_rows_ != N) {
+  partial_.reserve(size_t(hist_partial_capacity(L.n_tiles) * q.bin_stride * 32));
+  if (root_rows_ != N || root_tiles_ != L.n_tiles) {
     const int64_t b = 0, e = N;
     const int32_t slot = 0;
-    const std::vector<HistWork> w = make_hist_work(L, &b, &e, &slot, 1);
+    std::vector<HistWork> w;
+    std::vector<HistReduce> j;
+    make_hist_work(L, &b, &e, &slot, 1, true, w, j);
     root_work_.resize(w.size());
+    root_job_.resize(j.size());
     DP_HIP(hipMemcpy(root_work_.p, w.data(), sizeof(HistWork) * w.size(), hipMemcpyHostToDevice));
+    DP_HIP(hipMemcpy(root_job_.p, j.data(), sizeof(HistReduce) * j.size(), hipMemcpyHostToDevice));
     root_items_ = int32_t(w.size());
     root_rows_ = N;
+    root_tiles_ = L.n_tiles;
   }
   const int64_t widest = level_bound(D, N), widest_hist = level_bound(D - 1, N);
   eager_ = widest <= kEagerNodes && 2 * widest_hist * S * int64_t(sizeof(int64_t)) <= kEagerHistBytes;
@@ -316,14 +322,15 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     int64_t* h = hist_[cur].p;
     if (split) {
       if (d == 0) {
-        launch_fill_i64(h, S, 0, s);
-        launch_hist(q.bins.p, L, gpair, nullptr, root_work_.p, root_items_, nullptr, B, h, s);
+        launch_hist(q.bins.p, L, gpair, nullptr, root_work_.p, root_items_, nullptr, B, h,
+                    partial_.p, s);
+        launch_hist_reduce(partial_.p, root_job_.p, 1, nullptr, T, F, B, nullptr, h, false, s);
       } else {
-        launch_zero_i64_dev(h, field(c, &PlanCounts::n_level), S, nb, s);
         launch_hist(q.bins.p, L, gpair, ridx_[cur].p, hist_work_[cur].p,
-                    int32_t(plan_hist_capacity(nb, T)), field(c, &PlanCounts::n_hist), B, h, s);
-        launch_subtract_many(hist_[nxt].p, h, h, sub_jobs_[cur].p, int32_t(nb / 2 + 1),
-                             field(c, &PlanCounts::n_sub), S, s);
+                    int32_t(plan_hist_capacity(nb, T)), field(c, &PlanCounts::n_hist), B, h,
+                    partial_.p, s);
+        launch_hist_reduce(partial_.p, reduce_jobs_[cur].p, int32_t(nb / 2 + 1),
+                           field(c, &PlanCounts::n_reduce), T, F, B, hist_[nxt].p, h, false, s);
       }
       launch_evaluate(h, int32_t(nb), field(c, &PlanCounts::n_level), F, B, q.d_nbins.p,
                       sums_[cur].p, exps, 0, 0, dtp, splits_.p, s);
@@ -342,7 +349,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     a.next_seg_begin = seg_begin_[nxt].p;
     a.info = info_.p;
     a.hist_work = hist_work_[nxt].p;
-    a.sub_jobs = sub_jobs_[nxt].p;
+    a.reduce_jobs = reduce_jobs_[nxt].p;
     a.part_work = part_work_[nxt].p;
     a.part_first = part_first_[nxt].p;
     a.pair_chunk = pair_chunk_.p;
@@ -360,6 +367,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     a.info_capacity = int32_t(info_.n);
     a.level_capacity = int32_t(level_[nxt].n);
     a.hist_capacity = int32_t(hist_work_[nxt].n);
+    a.partial_capacity = int32_t(hist_partial_capacity(T));
     a.part_capacity = int32_t(part_work_[nxt].n);
     a.leaf_capacity = int32_t(leaf_work_.n);
     launch_plan_level(a, s);

@@ -80,7 +80,8 @@ class Grower {
   DeviceBuffer<LevelNode> level_[2];
   DeviceBuffer<int64_t> sums_[2], seg_begin_[2];
   DeviceBuffer<HistWork> hist_work_[2], root_work_;
-  DeviceBuffer<SubtractJob> sub_jobs_[2];
+  DeviceBuffer<HistReduce> reduce_jobs_[2], root_job_;
+  DeviceBuffer<int64_t> partial_;
   DeviceBuffer<PartWork> part_work_[2];
   DeviceBuffer<int32_t> part_first_[2];
   DeviceBuffer<int64_t> pair_chunk_, work_left_, work_offset_, node_left_;
@@ -96,7 +97,7 @@ class Grower {
   int64_t node_cap_ = 0;
   size_t slot_bytes_ = 0;
   int64_t root_rows_ = -1;
-  int32_t root_items_ = 0;
+  int32_t root_tiles_ = 0, root_items_ = 0;
 };
 
 // Normalised hyperparameter JSON (see DPValidateHyperparameters).

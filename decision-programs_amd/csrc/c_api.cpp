@@ -532,16 +532,26 @@ void hist_call(dp_workspace ws, const uint8_t* bins, const dp_bin_layout* layout
     total += end[i] - begin[i];
   }
   (void)total;
-  std::vector<dp::HistWork> work = dp::make_hist_work(*layout, begin, end, nullptr, n_nodes);
+  std::vector<dp::HistWork> work;
+  std::vector<dp::HistReduce> jobs;
+  // Overwriting builds let single-chunk nodes store their histogram directly;
+  // accumulating calls route every chunk through a partial slot.
+  const int32_t n_partial =
+      dp::make_hist_work(*layout, begin, end, nullptr, n_nodes, !accumulate, work, jobs);
   hipStream_t s = as_stream(stream);
-  ws->begin(sizeof(dp::HistWork) * work.size() + 256);
+  const size_t partial_words = size_t(n_partial) * size_t(bin_stride) * 32;
+  ws->begin(sizeof(dp::HistWork) * work.size() + sizeof(dp::HistReduce) * jobs.size() + 512);
+  ws->reserve_scratch(sizeof(int64_t) * partial_words + 256);
   dp::HistWork* d_work;
+  dp::HistReduce* d_jobs;
   std::copy(work.begin(), work.end(), ws->stage(work.size(), &d_work));
+  std::copy(jobs.begin(), jobs.end(), ws->stage(jobs.size(), &d_jobs));
   ws->commit(s);
-  const int64_t per_node = int64_t(layout->n_features) * bin_stride * 2;
-  if (!accumulate) dp::launch_fill_i64(hist, per_node * n_nodes, 0, s);
+  int64_t* partial = partial_words ? ws->take<int64_t>(partial_words) : nullptr;
   dp::launch_hist(bins, *layout, gpair, ridx, d_work, int32_t(work.size()), nullptr, bin_stride,
-                  hist, s);
+                  hist, partial, s);
+  dp::launch_hist_reduce(partial, d_jobs, n_nodes, nullptr, layout->n_tiles, layout->n_features,
+                         bin_stride, nullptr, hist, accumulate, s);
 }
 }  // namespace
 

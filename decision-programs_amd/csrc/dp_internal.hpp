@@ -81,11 +81,28 @@ constexpr double kRtEps = 1e-6;
 constexpr int kMaxBins = 256;
 
 // One histogram work item: rows [begin, end) of node `slot` for one tile.
+// partial >= 0: the workgroup stores its tile histogram in partial slot
+// `partial` (summed later by the reduce pass); partial < 0: the item is the
+// node's only chunk and writes the node histogram's tile directly.
 struct HistWork {
   int32_t slot;
   int32_t tile;
   int64_t begin;
   int64_t end;
+  int32_t partial;
+  int32_t pad;
+};
+
+// One reduce job (all tiles of one built node): node histogram `slot` = sum
+// of the partial tiles (p0 + k) * n_tiles + tile, k < nc (or, for nc == 1 with
+// a direct item, what that item wrote); then, when sibling >= 0, node
+// `sibling` = parent histogram at element offset `parent` - node `slot`.
+struct HistReduce {
+  int32_t slot;
+  int32_t sibling;
+  int64_t parent;
+  int32_t p0;
+  int32_t nc;
 };
 
 // One partition work item: rows [begin, end) of ridx, belonging to `node`.
@@ -128,7 +145,7 @@ struct PlanCounts {
   int32_t n_level;     // nodes of the current level
   int32_t n_nodes;     // nodes allocated in the tree so far
   int32_t n_hist;      // histogram work items for the current level
-  int32_t n_sub;       // subtraction jobs for the current level
+  int32_t n_reduce;    // histogram reduce jobs for the current level
   int32_t n_part;      // partition work items for the current level
   int32_t n_leaf;      // leaf work items produced by the last planner run
   int32_t error;       // nonzero: inconsistent partition counts
@@ -198,26 +215,39 @@ void launch_fill_u8(uint8_t* p, int64_t n, uint8_t value, hipStream_t s);
 void launch_iota_u32(uint32_t* p, int64_t n, hipStream_t s);
 
 // Histograms: every work item accumulates into hist[slot]; hist must be zero.
+// Direct items write hist; the others write partial (int64 [slot][bin_stride * 32]).
 void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t* gpair,
                  const uint32_t* ridx, const HistWork* work, int32_t n_work,
-                 const int32_t* n_work_dev, int32_t bin_stride, int64_t* hist, hipStream_t s);
-// Work items for the histograms of n_nodes row sets (node i: [begin[i],
-// end[i]) of ridx, written to hist slot slots[i], or i when slots is null),
-// chunked and ordered for the XCD-aware dispatch; may contain empty items.
-std::vector<HistWork> make_hist_work(const dp_bin_layout& layout, const int64_t* begin,
-                                     const int64_t* end, const int32_t* slots, int32_t n_nodes);
+                 const int32_t* n_work_dev, int32_t bin_stride, int64_t* hist,
+                 int64_t* partial, hipStream_t s);
+// Completes the histograms of launch_hist: sums partial tiles, writes built
+// and sibling node histograms.  accumulate: add the sums to hist instead of
+// storing them (then no job may rely on a direct item).
+void launch_hist_reduce(const int64_t* partial, const HistReduce* jobs, int32_t n_jobs,
+                        const int32_t* n_jobs_dev, int32_t n_tiles, int32_t n_features,
+                        int32_t bin_stride, const int64_t* parent_base, int64_t* hist,
+                        bool accumulate, hipStream_t s);
+// Minimum rows per histogram chunk and the chunk size for `rows` rows over
+// `n_tiles` tiles (about 1024 work items in all).
+constexpr int64_t kHistMinChunk = 4096;
+__host__ __device__ inline int64_t hist_chunk(int64_t rows, int32_t n_tiles) {
+  const int64_t c = (rows * n_tiles + 1023) / 1024;
+  return c < kHistMinChunk ? kHistMinChunk : c;
+}
+// Partial slots needed by one level (chunks of nodes with two or more chunks
+// number at most 2048 / n_tiles, each with n_tiles slots).
+inline int64_t hist_partial_capacity(int32_t n_tiles) { return 2048 + int64_t(n_tiles); }
+// Work items and reduce jobs for the histograms of n_nodes row sets (node i:
+// [begin[i], end[i]) of ridx, written to hist slot slots[i], or i when slots
+// is null), chunked and ordered for the XCD-aware dispatch; the work may hold
+// empty padding items.  allow_direct: single-chunk nodes write directly.
+// Returns the number of partial slots used.
+int32_t make_hist_work(const dp_bin_layout& layout, const int64_t* begin, const int64_t* end,
+                       const int32_t* slots, int32_t n_nodes, bool allow_direct,
+                       std::vector<HistWork>& work, std::vector<HistReduce>& jobs);
 void launch_subtract(const int64_t* parent, const int64_t* built, int64_t* sibling, int64_t n,
                      hipStream_t s);
 
-// Subtraction for many (parent, built, sibling) triples of `n` int64 each.
-struct SubtractJob {
-  int64_t parent;
-  int64_t built;
-  int64_t sibling;
-};
-void launch_subtract_many(const int64_t* base_parent, const int64_t* base_child,
-                          int64_t* base_out, const SubtractJob* jobs, int32_t n_jobs,
-                          const int32_t* n_jobs_dev, int64_t n, hipStream_t s);
 
 void launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_nodes_dev,
                      int32_t n_features,
@@ -252,10 +282,10 @@ struct PlanArgs {
   int64_t* next_seg_begin; // [slot]
   NodeInfo* info;          // indexed by node id
   HistWork* hist_work;
-  SubtractJob* sub_jobs;
+  HistReduce* reduce_jobs;
   PartWork* part_work;
   int32_t* part_first;     // [n_next + 1]
-  int64_t* pair_chunk;     // scratch: [n_pairs + 1] first chunk of each pair
+  int64_t* pair_chunk;     // scratch: 2 x [n_pairs + 1] first chunk / first partial chunk
   LeafWork* leaf_work;
   PlanCounts* counts;
   const int32_t* exps;     // quantiser exponents (gradient, hessian)
@@ -264,7 +294,7 @@ struct PlanArgs {
   int64_t hist_elems;      // int64 values per node histogram
   double eta, lambda, alpha, mcw;
   int32_t info_capacity, level_capacity;
-  int32_t hist_capacity, part_capacity, leaf_capacity;
+  int32_t hist_capacity, partial_capacity, part_capacity, leaf_capacity;
 };
 void launch_plan_level(const PlanArgs& a, hipStream_t s);
 // counts->n_level = 1, n_nodes = 1, ...; cur[0] = root {0, n_rows, g, h, 0, -1}

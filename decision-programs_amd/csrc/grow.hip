@@ -8,9 +8,13 @@
 //     native/class_native_source_contract.hpp:24-31);
 //   * the next level's nodes, their quantised sums and segment starts;
 //   * the next level's histogram work (the smaller child of every pair, rows
-//     chunked and ordered for the XCD-aware dispatch), the subtraction jobs
-//     deriving each sibling, and the partition work;
+//     chunked and ordered for the XCD-aware dispatch; a pair with one chunk
+//     per tile writes its histogram directly, larger ones use partial slots),
+//     the reduce jobs that finish the built histograms and derive each
+//     sibling, and the partition work;
 //   * the margin-update work of this level's leaves.
+// Counts are scanned over the workgroup and every work item is then written
+// by its own thread, which finds its node by binary search over the offsets.
 // Nothing goes back to the host until the tree is complete, so a whole tree
 // is enqueued without a host round trip per level.
 //
@@ -25,7 +29,6 @@ namespace dp {
 namespace {
 
 constexpr int kPlanThreads = 1024;
-constexpr int64_t kHistMinChunk = 4096;
 
 __device__ double plan_threshold_l1(double g, double alpha) {
   if (g > alpha) return g - alpha;
@@ -54,6 +57,18 @@ __device__ int64_t block_scan(int64_t v, int64_t* lds, int64_t* total) {
   *total = lds[kPlanThreads - 1];
   __syncthreads();
   return incl - v;
+}
+
+// Index of the segment holding item k: the last i in [0, n) with off[i] <= k
+// (off nondecreasing, off[0] <= k).
+template <class T>
+__device__ int32_t owner(const T* off, int32_t n, int64_t k) {
+  int32_t lo = 0, hi = n;
+  while (hi - lo > 1) {
+    const int32_t mid = (lo + hi) >> 1;
+    if (int64_t(off[mid]) <= k) lo = mid; else hi = mid;
+  }
+  return lo;
 }
 
 __device__ bool node_expands(const PlanArgs& a, int32_t i, int64_t rows) {
@@ -134,45 +149,51 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
   if (s_error) {  // inconsistent level or capacity exceeded: stop this tree
     if (tid == 0) {
       PlanCounts* c = a.counts;
-      c->n_level = c->n_hist = c->n_sub = c->n_part = c->n_leaf = 0;
+      c->n_level = c->n_hist = c->n_reduce = c->n_part = c->n_leaf = 0;
       if (!c->error) c->error = s_error;
     }
     return;
   }
 
   // ---- B: leaf work of this level -----------------------------------------
+  int64_t* off = a.pair_chunk;  // [n + 1]: first leaf chunk of each node
   carry = 0;
   for (int32_t base = 0; base < n; base += kPlanThreads) {
     const int32_t i = base + tid;
     int64_t chunks = 0;
-    LevelNode nd{};
     if (i < n) {
-      nd = a.cur[i];
+      const LevelNode nd = a.cur[i];
       if (!node_expands(a, i, nd.end - nd.begin))
         chunks = (nd.end - nd.begin + kLeafChunk - 1) / kLeafChunk;
     }
     int64_t total;
-    const int64_t off = carry + block_scan(chunks, scan, &total);
+    const int64_t o = carry + block_scan(chunks, scan, &total);
     carry += total;
-    if (chunks > 0) {
-      const float value = a.info[nd.nid].leaf_value;
-      for (int64_t j = 0; j < chunks; ++j) {
-        const int64_t at = off + j;
-        if (at >= a.leaf_capacity) { s_error = 3; break; }
-        const int64_t b = nd.begin + j * kLeafChunk;
-        a.leaf_work[at] = LeafWork{value, nd.nid, b, b + kLeafChunk < nd.end ? b + kLeafChunk : nd.end};
-      }
-    }
+    if (i < n) off[i] = o;
   }
-  const int64_t n_leaf = carry;
+  int64_t n_leaf = carry;
+  if (tid == 0) off[n] = n_leaf;
+  __syncthreads();
+  if (n_leaf > a.leaf_capacity) {
+    if (tid == 0) s_error = 3;
+    n_leaf = 0;
+  }
+  for (int64_t k = tid; k < n_leaf; k += kPlanThreads) {
+    const int32_t i = owner(off, n, k);
+    const LevelNode nd = a.cur[i];
+    const int64_t b = nd.begin + (k - off[i]) * kLeafChunk;
+    a.leaf_work[k] = LeafWork{a.info[nd.nid].leaf_value, nd.nid, b,
+                              b + kLeafChunk < nd.end ? b + kLeafChunk : nd.end};
+  }
+  __syncthreads();  // off is reused below
 
-  // ---- C: histogram work and subtraction jobs of the next level ----------
+  // ---- C: histogram work and reduce jobs of the next level ----------------
   const bool next_hist = n_next > 0 && a.depth + 1 < a.max_depth;
   int64_t n_hist = 0;
-  int32_t n_sub = 0;
+  int32_t n_reduce = 0;
   if (next_hist) {
-    // total rows of the smaller children
-    int64_t mine = 0;
+    const int32_t T = a.n_tiles;
+    int64_t mine = 0;  // rows of the smaller children
     for (int32_t j = tid; j < n_expand; j += kPlanThreads) {
       const LevelNode l = a.next[2 * j], r = a.next[2 * j + 1];
       const int64_t rl = l.end - l.begin, rr = r.end - r.begin;
@@ -180,9 +201,10 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
     }
     int64_t small_total;
     (void)block_scan(mine, scan, &small_total);
-    int64_t chunk = (small_total * a.n_tiles + 1023) / 1024;
-    if (chunk < kHistMinChunk) chunk = kHistMinChunk;
-    int64_t* cstart = a.pair_chunk;
+    const int64_t chunk = hist_chunk(small_total, T);
+    int64_t* cstart = a.pair_chunk;                 // [n_expand + 1]
+    int64_t* pstart = a.pair_chunk + n_expand + 1;  // [n_expand + 1]
+    int64_t pcarry = 0;
     carry = 0;
     for (int32_t base = 0; base < n_expand; base += kPlanThreads) {
       const int32_t j = base + tid;
@@ -190,52 +212,57 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
       if (j < n_expand) {
         const LevelNode l = a.next[2 * j], r = a.next[2 * j + 1];
         const int64_t rl = l.end - l.begin, rr = r.end - r.begin;
-        const int64_t rows = rr < rl ? rr : rl;
-        nc = (rows + chunk - 1) / chunk;
+        nc = ((rr < rl ? rr : rl) + chunk - 1) / chunk;
       }
-      int64_t total;
-      const int64_t off = carry + block_scan(nc, scan, &total);
+      int64_t total, ptotal;
+      const int64_t o = carry + block_scan(nc, scan, &total);
+      const int64_t po = pcarry + block_scan(nc >= 2 ? nc : 0, scan, &ptotal);
       carry += total;
-      if (j < n_expand) cstart[j] = off;
+      pcarry += ptotal;
+      if (j < n_expand) {
+        cstart[j] = o;
+        pstart[j] = po;
+      }
     }
     const int64_t C = carry;
     if (tid == 0) cstart[n_expand] = C;
     __syncthreads();
     const int64_t padded = (C + 7) / 8 * 8;
-    n_hist = padded * a.n_tiles;
-    if (n_hist > a.hist_capacity) {
+    n_hist = padded * T;
+    if (n_hist > a.hist_capacity || pcarry * T > a.partial_capacity) {
       if (tid == 0) s_error = 4;
       n_hist = 0;
     } else {
       for (int64_t c = tid; c < padded; c += kPlanThreads) {
-        HistWork item{0, 0, 0, 0};
+        HistWork item{0, 0, 0, 0, -1, 0};
+        int64_t p = -1;
         if (c < C) {
-          int32_t lo = 0, hi = n_expand;  // last pair with cstart <= c
-          while (hi - lo > 1) {
-            const int32_t mid = (lo + hi) >> 1;
-            if (cstart[mid] <= c) lo = mid; else hi = mid;
-          }
-          const int32_t j = lo;
+          const int32_t j = owner(cstart, n_expand, c);
           const LevelNode l = a.next[2 * j], r = a.next[2 * j + 1];
           const bool right_small = (r.end - r.begin) < (l.end - l.begin);
           const LevelNode sm = right_small ? r : l;
-          const int64_t b = sm.begin + (c - cstart[j]) * chunk;
-          item = HistWork{2 * j + (right_small ? 1 : 0), 0, b, b + chunk < sm.end ? b + chunk : sm.end};
+          const int64_t k = c - cstart[j];
+          const int64_t b = sm.begin + k * chunk;
+          item = HistWork{2 * j + (right_small ? 1 : 0), 0, b,
+                          b + chunk < sm.end ? b + chunk : sm.end, -1, 0};
+          if (cstart[j + 1] - cstart[j] >= 2) p = (pstart[j] + k) * T;
         }
-        for (int32_t t = 0; t < a.n_tiles; ++t) {
+        for (int32_t t = 0; t < T; ++t) {
           item.tile = t;
-          a.hist_work[((c / 8) * a.n_tiles + t) * 8 + (c % 8)] = item;
+          item.partial = p < 0 ? -1 : int32_t(p + t);
+          a.hist_work[((c / 8) * T + t) * 8 + (c % 8)] = item;
         }
       }
+      for (int32_t j = tid; j < n_expand; j += kPlanThreads) {
+        const LevelNode l = a.next[2 * j], r = a.next[2 * j + 1];
+        const bool right_small = (r.end - r.begin) < (l.end - l.begin);
+        const int32_t nc = int32_t(cstart[j + 1] - cstart[j]);
+        a.reduce_jobs[j] = HistReduce{2 * j + (right_small ? 1 : 0), 2 * j + (right_small ? 0 : 1),
+                                      int64_t(l.parent_slot) * a.hist_elems,
+                                      nc >= 2 ? int32_t(pstart[j]) : -1, nc};
+      }
+      n_reduce = n_expand;
     }
-    for (int32_t j = tid; j < n_expand; j += kPlanThreads) {
-      const LevelNode l = a.next[2 * j], r = a.next[2 * j + 1];
-      const bool right_small = (r.end - r.begin) < (l.end - l.begin);
-      const int32_t small = 2 * j + (right_small ? 1 : 0), large = 2 * j + (right_small ? 0 : 1);
-      a.sub_jobs[j] = SubtractJob{int64_t(l.parent_slot) * a.hist_elems,
-                                  int64_t(small) * a.hist_elems, int64_t(large) * a.hist_elems};
-    }
-    n_sub = n_expand;
   }
 
   // ---- D: partition work of the next level ----------------------------------
@@ -245,25 +272,28 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
     for (int32_t base = 0; base < n_next; base += kPlanThreads) {
       const int32_t i = base + tid;
       int64_t chunks = 0;
-      LevelNode nd{};
       if (i < n_next) {
-        nd = a.next[i];
+        const LevelNode nd = a.next[i];
         chunks = (nd.end - nd.begin + kPartChunk - 1) / kPartChunk;
       }
       int64_t total;
-      const int64_t off = carry + block_scan(chunks, scan, &total);
+      const int64_t o = carry + block_scan(chunks, scan, &total);
       carry += total;
-      if (i < n_next) {
-        a.part_first[i] = int32_t(off);
-        for (int64_t j = 0; j < chunks; ++j) {
-          if (off + j >= a.part_capacity) { s_error = 5; break; }
-          const int64_t b = nd.begin + j * kPartChunk;
-          a.part_work[off + j] = PartWork{i, 0, b, b + kPartChunk < nd.end ? b + kPartChunk : nd.end};
-        }
-      }
+      if (i < n_next) a.part_first[i] = int32_t(o);
     }
     n_part = carry;
     if (tid == 0) a.part_first[n_next] = int32_t(n_part);
+    __syncthreads();
+    if (n_part > a.part_capacity) {
+      if (tid == 0) s_error = 5;
+      n_part = 0;
+    }
+    for (int64_t k = tid; k < n_part; k += kPlanThreads) {
+      const int32_t i = owner(a.part_first, n_next, k);
+      const LevelNode nd = a.next[i];
+      const int64_t b = nd.begin + (k - a.part_first[i]) * kPartChunk;
+      a.part_work[k] = PartWork{i, 0, b, b + kPartChunk < nd.end ? b + kPartChunk : nd.end};
+    }
   }
 
   __syncthreads();
@@ -272,9 +302,9 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
     c->n_level = n_next;
     c->n_nodes = n_nodes0 + n_next;
     c->n_hist = int32_t(n_hist);
-    c->n_sub = n_sub;
-    c->n_part = int32_t(n_part > a.part_capacity ? 0 : n_part);
-    c->n_leaf = int32_t(n_leaf > a.leaf_capacity ? 0 : n_leaf);
+    c->n_reduce = n_reduce;
+    c->n_part = int32_t(n_part);
+    c->n_leaf = int32_t(n_leaf);
     if (s_error && !c->error) c->error = s_error;
   }
 }

@@ -10,11 +10,13 @@
 //  * lane-dependent rotation of the 16 bytes keeps the 64-bit LDS atomics bank
 //    conflict free for any bin values (measured: zero SQ_LDS_BANK_CONFLICT);
 //  * sums are exact integers (fixed-point gradients), so the result does not
-//    depend on atomic order and equals the CPU restatement bit for bit;
+//    depend on summation order and equals the CPU restatement bit for bit;
 //  * work items are row chunks x tiles, ordered so the tiles of one chunk run on
 //    one XCD back to back (the chunk's gradients then come from that XCD's L2);
-//  * the workgroup merges its LDS histogram into the node histogram with
-//    64-bit global atomics, skipping empty bins.
+//  * no global atomics: a node's only chunk stores its tile straight into the
+//    node histogram; chunks of larger nodes store their tile into a partial
+//    slot, and hist_reduce_kernel sums the partial slots of each node and
+//    derives the sibling (parent - built) in the same pass.
 #include "dp_internal.hpp"
 
 namespace dp {
@@ -62,10 +64,6 @@ __device__ __forceinline__ void lds_add(lds_u64* p, unsigned long long v) {
   __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-__device__ __forceinline__ void global_add(unsigned long long* p, unsigned long long v) {
-  __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 constexpr int kTile = 16;                // features per tile (bytes per row per tile)
 constexpr int kLdsWords = 256 * 2 * kTile;  // 64 KiB of int64
 constexpr int kHistThreads = 1024;
@@ -89,7 +87,7 @@ __global__ __launch_bounds__(kHistThreads) void hist_kernel(
     const int2* __restrict__ gpair, const uint32_t* __restrict__ ridx,
     const HistWork* __restrict__ work, int32_t n_work_host,
     const int32_t* __restrict__ n_work_dev, int32_t bin_stride,
-    unsigned long long* __restrict__ hist) {
+    unsigned long long* __restrict__ hist, unsigned long long* __restrict__ partial) {
   __shared__ unsigned long long lds[kLdsWords];
   const int32_t n_work = n_work_dev ? *n_work_dev : n_work_host;
   for (int32_t item = blockIdx.x; item < n_work; item += gridDim.x) {
@@ -155,15 +153,18 @@ __global__ __launch_bounds__(kHistThreads) void hist_kernel(
   }
   __syncthreads();
 
-  unsigned long long* out = hist + int64_t(w.slot) * n_features * bin_stride * 2;
-  const int f0 = w.tile * kTile;
-  for (int e = threadIdx.x; e < kLdsWords; e += kHistThreads) {
-    const int bin = e >> 5, within = e & 31;
-    const int f = f0 + (within & 15);
-    if (f >= n_features || bin >= bin_stride) continue;
-    const unsigned long long x = lds[e];
-    if (x == 0ull) continue;
-    global_add(out + (int64_t(f) * bin_stride + bin) * 2 + (within >> 4), x);
+  const int n_words = bin_stride * 32;  // bins < bin_stride, 32 words each
+  if (w.partial >= 0) {
+    unsigned long long* out = partial + int64_t(w.partial) * n_words;
+    for (int e = threadIdx.x; e < n_words; e += kHistThreads) out[e] = lds[e];
+  } else {
+    unsigned long long* out = hist + int64_t(w.slot) * n_features * bin_stride * 2;
+    const int f0 = w.tile * kTile;
+    for (int e = threadIdx.x; e < n_words; e += kHistThreads) {
+      const int bin = e >> 5, within = e & 31;
+      const int f = f0 + (within & 15);
+      if (f < n_features) out[(int64_t(f) * bin_stride + bin) * 2 + (within >> 4)] = lds[e];
+    }
   }
   __syncthreads();  // the next item clears the LDS this item just read
   }
@@ -185,21 +186,46 @@ __global__ void subtract_kernel(const int64_t* __restrict__ parent,
     sibling[i] = parent[i] - built[i];
 }
 
-// The y dimension loops over jobs; the x dimension strides over their n elements.
-__global__ void subtract_many_kernel(const int64_t* __restrict__ base_parent,
-                                     const int64_t* __restrict__ base_child,
-                                     int64_t* __restrict__ base_out,
-                                     const SubtractJob* __restrict__ jobs, int32_t n_jobs_host,
-                                     const int32_t* __restrict__ n_jobs_dev, int64_t n) {
+// Grid: x = blocks of 256 words of one tile (word e = bin * 32 + within, as
+// in the LDS image), y = tile, z strides over the jobs.  Each thread sums one
+// word over the job's partial slots and writes the built and sibling values in
+// the [feature][bin][g, h] layout.
+__global__ __launch_bounds__(256) void hist_reduce_kernel(
+    const long long* __restrict__ partial, const HistReduce* __restrict__ jobs,
+    int32_t n_jobs_host, const int32_t* __restrict__ n_jobs_dev, int32_t n_tiles,
+    int32_t n_features, int32_t bin_stride, const long long* __restrict__ parent_base,
+    long long* __restrict__ hist, int32_t accumulate) {
   const int32_t n_jobs = n_jobs_dev ? *n_jobs_dev : n_jobs_host;
-  for (int32_t job = blockIdx.y; job < n_jobs; job += gridDim.y) {
-    const SubtractJob j = jobs[job];
-    const int64_t* p = base_parent + j.parent;
-    const int64_t* c = base_child + j.built;
-    int64_t* s = base_out + j.sibling;
-    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
-         i += int64_t(blockDim.x) * gridDim.x)
-      s[i] = p[i] - c[i];
+  const int n_words = bin_stride * 32;
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  const int t = blockIdx.y;
+  const int within = e & 31, bin = e >> 5;
+  const int f = t * kTile + (within & 15);
+  if (e >= n_words || f >= n_features) return;  // no barriers below
+  const int64_t node_elems = int64_t(n_features) * bin_stride * 2;
+  const int64_t at = (int64_t(f) * bin_stride + bin) * 2 + (within >> 4);
+  for (int32_t jb = blockIdx.z; jb < n_jobs; jb += gridDim.z) {
+    const HistReduce j = jobs[jb];
+    long long* built = hist + int64_t(j.slot) * node_elems + at;
+    long long sum;
+    if (j.nc == 1 && j.p0 < 0) {
+      sum = *built;  // written directly by the node's only chunk
+    } else {
+      long long acc[4] = {0, 0, 0, 0};
+      const long long* src = partial + (int64_t(j.p0) * n_tiles + t) * n_words + e;
+      const int64_t step = int64_t(n_tiles) * n_words;
+      int k = 0;
+      for (; k + 4 <= j.nc; k += 4) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[u] += src[(k + u) * step];
+      }
+      for (; k < j.nc; ++k) acc[0] += src[k * step];
+      sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+      if (accumulate) sum += *built;
+      *built = sum;
+    }
+    if (j.sibling >= 0)
+      hist[int64_t(j.sibling) * node_elems + at] = parent_base[j.parent + at] - sum;
   }
 }
 
@@ -223,45 +249,58 @@ void launch_iota_u32(uint32_t* p, int64_t n, hipStream_t s) {
   DP_HIP(hipGetLastError());
 }
 
-std::vector<HistWork> make_hist_work(const dp_bin_layout& layout, const int64_t* begin,
-                                     const int64_t* end, const int32_t* slots, int32_t n_nodes) {
+int32_t make_hist_work(const dp_bin_layout& layout, const int64_t* begin, const int64_t* end,
+                       const int32_t* slots, int32_t n_nodes, bool allow_direct,
+                       std::vector<HistWork>& work, std::vector<HistReduce>& jobs) {
   // About 1024 items (two waves of 2 workgroups per CU on 256 CUs), at least
-  // 4096 rows each, so the per-item LDS merge stays small.
+  // kHistMinChunk rows each, so the per-item LDS clear and store stay small.
   int64_t total = 0;
   for (int32_t i = 0; i < n_nodes; ++i) total += end[i] - begin[i];
-  int64_t chunk = (total * layout.n_tiles + 1023) / 1024;
-  if (chunk < 4096) chunk = 4096;
+  const int64_t chunk = hist_chunk(total, layout.n_tiles);
   struct Chunk {
-    int32_t slot;
+    int32_t slot, partial;
     int64_t b, e;
   };
   std::vector<Chunk> chunks;
-  for (int32_t i = 0; i < n_nodes; ++i)
-    for (int64_t b = begin[i]; b < end[i]; b += chunk)
-      chunks.push_back({slots ? slots[i] : i, b, std::min(b + chunk, end[i])});
+  jobs.clear();
+  int32_t n_partial = 0;
+  for (int32_t i = 0; i < n_nodes; ++i) {
+    const int32_t slot = slots ? slots[i] : i;
+    const int32_t nc = int32_t((end[i] - begin[i] + chunk - 1) / chunk);
+    const bool direct = allow_direct && nc == 1;
+    jobs.push_back({slot, -1, 0, direct ? -1 : n_partial, nc});
+    for (int32_t k = 0; k < nc; ++k) {
+      const int64_t b = begin[i] + k * chunk;
+      chunks.push_back({slot, direct ? -1 : n_partial + k, b, std::min(b + chunk, end[i])});
+    }
+    if (!direct) n_partial += nc;
+  }
   // Blocks are dispatched round-robin over the 8 XCDs (block id mod 8).  Item
   // order puts the tiles of one row chunk on the same XCD in consecutive
   // dispatch slots, so that chunk's gradient pairs are read from HBM once and
   // then hit that XCD's L2.
   const int64_t T = layout.n_tiles;
   const int64_t groups = (int64_t(chunks.size()) + 7) / 8;
-  std::vector<HistWork> work(size_t(groups * T * 8), HistWork{0, 0, 0, 0});
+  work.assign(size_t(groups * T * 8), HistWork{0, 0, 0, 0, -1, 0});
   for (int64_t c = 0; c < int64_t(chunks.size()); ++c)
     for (int64_t t = 0; t < T; ++t) {
+      const Chunk& ch = chunks[size_t(c)];
       const int64_t b = ((c / 8) * T + t) * 8 + (c % 8);
-      work[size_t(b)] = {chunks[size_t(c)].slot, int32_t(t), chunks[size_t(c)].b,
-                         chunks[size_t(c)].e};
+      work[size_t(b)] = {ch.slot, int32_t(t), ch.b, ch.e,
+                         ch.partial < 0 ? -1 : int32_t(ch.partial * T + t), 0};
     }
-  return work;
+  return n_partial * int32_t(T);
 }
 
 void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t* gpair,
                  const uint32_t* ridx, const HistWork* work, int32_t n_work,
-                 const int32_t* n_work_dev, int32_t bin_stride, int64_t* hist, hipStream_t s) {
+                 const int32_t* n_work_dev, int32_t bin_stride, int64_t* hist,
+                 int64_t* partial, hipStream_t s) {
   if (n_work <= 0) return;
   need(bin_stride >= 1 && bin_stride <= kMaxBins, "histogram bin stride out of range");
   need(layout.tile_width == kTile, "histogram kernel needs 16-feature tiles");
   auto* out = reinterpret_cast<unsigned long long*>(hist);
+  auto* part = reinterpret_cast<unsigned long long*>(partial);
   const auto* gp = reinterpret_cast<const int2*>(gpair);
   // At most 1024 resident workgroups (2 per CU, two rounds); a multiple of 8.
   int grid = n_work < 1024 ? n_work : 1024;
@@ -270,11 +309,11 @@ void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t
     need(layout.missing_bin == 255, "missing bin must be 255");
     hipLaunchKernelGGL(hist_kernel<true>, dim3(grid), dim3(kHistThreads), 0, s, bins,
                        layout.n_rows, layout.n_features, gp, ridx, work, n_work, n_work_dev,
-                       bin_stride, out);
+                       bin_stride, out, part);
   } else {
     hipLaunchKernelGGL(hist_kernel<false>, dim3(grid), dim3(kHistThreads), 0, s, bins,
                        layout.n_rows, layout.n_features, gp, ridx, work, n_work, n_work_dev,
-                       bin_stride, out);
+                       bin_stride, out, part);
   }
   DP_HIP(hipGetLastError());
 }
@@ -295,13 +334,19 @@ void launch_subtract(const int64_t* parent, const int64_t* built, int64_t* sibli
   DP_HIP(hipGetLastError());
 }
 
-void launch_subtract_many(const int64_t* base_parent, const int64_t* base_child,
-                          int64_t* base_out, const SubtractJob* jobs, int32_t n_jobs,
-                          const int32_t* n_jobs_dev, int64_t n, hipStream_t s) {
-  if (n_jobs <= 0 || n <= 0) return;
-  const int gy = n_jobs < 256 ? n_jobs : 256;
-  hipLaunchKernelGGL(subtract_many_kernel, dim3(grid_for(n, 256, 32), gy), dim3(256), 0, s,
-                     base_parent, base_child, base_out, jobs, n_jobs, n_jobs_dev, n);
+void launch_hist_reduce(const int64_t* partial, const HistReduce* jobs, int32_t n_jobs,
+                        const int32_t* n_jobs_dev, int32_t n_tiles, int32_t n_features,
+                        int32_t bin_stride, const int64_t* parent_base, int64_t* hist,
+                        bool accumulate, hipStream_t s) {
+  if (n_jobs <= 0) return;
+  need(bin_stride >= 1 && bin_stride <= kMaxBins, "histogram bin stride out of range");
+  const dim3 grid(unsigned(bin_stride * 32 + 255) / 256, unsigned(n_tiles),
+                  unsigned(n_jobs < 64 ? n_jobs : 64));
+  hipLaunchKernelGGL(hist_reduce_kernel, grid, dim3(256), 0, s,
+                     reinterpret_cast<const long long*>(partial), jobs, n_jobs, n_jobs_dev,
+                     n_tiles, n_features, bin_stride,
+                     reinterpret_cast<const long long*>(parent_base),
+                     reinterpret_cast<long long*>(hist), accumulate ? 1 : 0);
   DP_HIP(hipGetLastError());
 }
 
