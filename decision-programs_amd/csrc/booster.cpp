@@ -218,6 +218,7 @@ void Grower::ensure_level(const Quantized& q, int64_t nb, int32_t d, int32_t D) 
   if (d < D) {
     hist_[cur].reserve(size_t(nb * S));
     splits_.reserve(size_t(nb));
+    eval_scratch_.reserve(evaluate_scratch_bytes(int32_t(nb), q.layout.n_features));
     node_left_.reserve(size_t(nb));
     work_left_.reserve(size_t(plan_part_capacity(nb, N)));
     work_offset_.reserve(size_t(plan_part_capacity(nb, N)));
@@ -333,7 +334,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
                            field(c, &PlanCounts::n_reduce), T, F, B, hist_[nxt].p, h, false, s);
       }
       launch_evaluate(h, int32_t(nb), field(c, &PlanCounts::n_level), F, B, q.d_nbins.p,
-                      sums_[cur].p, exps, 0, 0, dtp, splits_.p, s);
+                      sums_[cur].p, exps, 0, 0, dtp, eval_scratch_.p, splits_.p, s);
       launch_partition(q.bins.p, L, ridx_[cur].p, ridx_[nxt].p, part_work_[cur].p,
                        int32_t(plan_part_capacity(nb, N)), field(c, &PlanCounts::n_part),
                        seg_begin_[cur].p, splits_.p, part_first_[cur].p, int32_t(nb),

@@ -86,6 +86,7 @@ class Grower {
   DeviceBuffer<int32_t> part_first_[2];
   DeviceBuffer<int64_t> pair_chunk_, work_left_, work_offset_, node_left_;
   DeviceBuffer<dp_split_record> splits_;
+  DeviceBuffer<uint8_t> eval_scratch_;
   DeviceBuffer<LeafWork> leaf_work_;
   DeviceBuffer<NodeInfo> info_;
   DeviceBuffer<PlanCounts> counts_;

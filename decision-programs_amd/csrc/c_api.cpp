@@ -581,14 +581,20 @@ int dp_hist_subtract(const int64_t* parent, const int64_t* built, int64_t* sibli
   });
 }
 
-int dp_evaluate_splits(const int64_t* hist, int32_t n_nodes, int32_t n_features,
-                       int32_t bin_stride, const int32_t* n_bins, const int64_t* node_sums,
-                       int32_t exp_g, int32_t exp_h, const dp_train_param* param,
-                       dp_split_record* out, void* stream) {
+int dp_evaluate_splits(dp_workspace ws, const int64_t* hist, int32_t n_nodes,
+                       int32_t n_features, int32_t bin_stride, const int32_t* n_bins,
+                       const int64_t* node_sums, int32_t exp_g, int32_t exp_h,
+                       const dp_train_param* param, dp_split_record* out, void* stream) {
   return guarded([&] {
-    dp::need(hist && n_bins && node_sums && param && out, "null argument");
+    dp::need(ws && hist && n_bins && node_sums && param && out, "null argument");
+    dp::need(n_nodes >= 0 && n_features >= 1, "node and feature counts");
+    if (n_nodes == 0) return;
+    const size_t bytes = dp::evaluate_scratch_bytes(n_nodes, n_features);
+    ws->begin(0);
+    ws->reserve_scratch(bytes + 256);
+    void* scratch = ws->take<uint8_t>(bytes);
     dp::launch_evaluate(hist, n_nodes, nullptr, n_features, bin_stride, n_bins, node_sums, nullptr,
-                        exp_g, exp_h, *param, out, as_stream(stream));
+                        exp_g, exp_h, *param, scratch, out, as_stream(stream));
   });
 }
 

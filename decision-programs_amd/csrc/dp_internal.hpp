@@ -249,11 +249,13 @@ void launch_subtract(const int64_t* parent, const int64_t* built, int64_t* sibli
                      hipStream_t s);
 
 
+// Split evaluation; scratch holds evaluate_scratch_bytes(n_nodes, n_features).
+size_t evaluate_scratch_bytes(int32_t n_nodes, int32_t n_features);
 void launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_nodes_dev,
-                     int32_t n_features,
-                     int32_t bin_stride, const int32_t* n_bins, const int64_t* node_sums,
-                     const int32_t* exps, int32_t exp_g, int32_t exp_h,
-                     const dp_train_param& param, dp_split_record* out, hipStream_t s);
+                     int32_t n_features, int32_t bin_stride, const int32_t* n_bins,
+                     const int64_t* node_sums, const int32_t* exps, int32_t exp_g, int32_t exp_h,
+                     const dp_train_param& param, void* scratch, dp_split_record* out,
+                     hipStream_t s);
 
 // Partition: counts, per-node scan, scatter.
 void launch_partition(const uint8_t* bins, const dp_bin_layout& layout, const uint32_t* ridx_in,

@@ -79,24 +79,29 @@ constexpr int kHistUnroll = 2;           // rows per lane per pipeline stage
 // (f*8 mod 128), whatever their bins: the 64-bit LDS atomics are conflict free.
 // The LDS address is assembled by one v_perm_b32: byte 1 = the bin byte, byte 0
 // = the lane's feature offset for that step.
+//
+// The row loop has no branches, so the compiler's memory counters see a
+// straight pipeline: indices past `end` are clamped to the last row and their
+// (g, h) masked to zero, and a missing value (byte 255; matrices with missing
+// values have at most 255 bins) adds into LDS row 255, which is never read.
+// Contiguous rows (GATHER false) are loaded and accumulated block by block (the
+// 32 waves of a CU hide the load latency; measured: prefetching a block ahead
+// does not help, the loop is bound by the LDS atomics); gathered rows
+// (GATHER true) load their row ids two blocks ahead and the bins and gradients
+// one block ahead.  At most 64 VGPRs, so two workgroups fit on a CU.
 // Workgroups loop over items (item = blockIdx.x + k * gridDim.x); with a grid
 // that is a multiple of 8, item i still runs on XCD i mod 8.
-template <bool MISSING>
-__global__ __launch_bounds__(kHistThreads) void hist_kernel(
+template <bool GATHER>
+__global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8, 8))) void hist_kernel(
     const uint8_t* __restrict__ bins, int64_t n_rows, int32_t n_features,
     const int2* __restrict__ gpair, const uint32_t* __restrict__ ridx,
     const HistWork* __restrict__ work, int32_t n_work_host,
     const int32_t* __restrict__ n_work_dev, int32_t bin_stride,
     unsigned long long* __restrict__ hist, unsigned long long* __restrict__ partial) {
   __shared__ unsigned long long lds[kLdsWords];
+  constexpr int U = kHistUnroll;
+  constexpr int64_t kStep = int64_t(kHistThreads) * U;
   const int32_t n_work = n_work_dev ? *n_work_dev : n_work_host;
-  for (int32_t item = blockIdx.x; item < n_work; item += gridDim.x) {
-  const HistWork w = work[item];
-  if (w.begin >= w.end) continue;  // padding item (uniform per workgroup)
-  for (int e = threadIdx.x; e < kLdsWords; e += kHistThreads) lds[e] = 0ull;
-  __syncthreads();
-
-  lds_u8* const lds_base = (lds_u8*)lds;
   const uint32_t rot = threadIdx.x & 15u;
   uint32_t slotw[4];  // byte i of slotw[m]: feature offset (bytes) of step 4m+i
 #pragma unroll
@@ -106,50 +111,72 @@ __global__ __launch_bounds__(kHistThreads) void hist_kernel(
     for (int i = 0; i < 4; ++i) v |= (((uint32_t(4 * m + i) + rot) & 15u) * 8u) << (8 * i);
     slotw[m] = v;
   }
+  lds_u8* const lds_base = (lds_u8*)lds;
+  for (int32_t item = blockIdx.x; item < n_work; item += gridDim.x) {
+  const HistWork w = work[item];
+  if (w.begin >= w.end) continue;  // padding item (uniform per workgroup)
+  for (int e = threadIdx.x; e < kLdsWords; e += kHistThreads) lds[e] = 0ull;
+  __syncthreads();
+
   const uint8_t* tile = bins + int64_t(w.tile) * n_rows * kTile;
-  constexpr int64_t kStep = int64_t(kHistThreads) * kHistUnroll;
-  uint4 v[2][kHistUnroll];
-  int2 q[2][kHistUnroll];
-  bool ok[2][kHistUnroll];
-  auto load = [&](int buf, int64_t at) {
+  const int64_t last = w.end - 1;
+  const int64_t lane = threadIdx.x;
+  uint32_t rows[2][U];  // GATHER: row ids of the block after the next
+  uint4 v[2][U];
+  int2 q[2][U];
+  auto fetch_rows = [&](int b, int64_t base) {
 #pragma unroll
-    for (int u = 0; u < kHistUnroll; ++u) {
-      const int64_t i = at + int64_t(u) * kHistThreads;
-      ok[buf][u] = i < w.end;
-      if (ok[buf][u]) {
-        const uint32_t r = ridx ? ridx[i] : uint32_t(i);
-        v[buf][u] = *reinterpret_cast<const uint4*>(tile + int64_t(r) * kTile);
-        q[buf][u] = gpair[r];
-      }
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = base + int64_t(u) * kHistThreads + lane;
+      rows[b][u] = ridx[i < w.end ? i : last];
     }
   };
-  auto process = [&](int buf) {
+  auto fetch_data = [&](int b, int64_t base) {
 #pragma unroll
-    for (int u = 0; u < kHistUnroll; ++u) {
-      if (!ok[buf][u]) continue;
-      uint32_t a[4] = {v[buf][u].x, v[buf][u].y, v[buf][u].z, v[buf][u].w};
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = base + int64_t(u) * kHistThreads + lane;
+      const uint32_t r = GATHER ? rows[b][u] : uint32_t(i < w.end ? i : last);
+      v[b][u] = *reinterpret_cast<const uint4*>(tile + int64_t(r) * kTile);
+      q[b][u] = gpair[r];
+    }
+  };
+  auto process = [&](int b, int64_t base) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool ok = base + int64_t(u) * kHistThreads + lane < w.end;
+      uint32_t a[4] = {v[b][u].x, v[b][u].y, v[b][u].z, v[b][u].w};
       rotate16(a, rot);
-      const unsigned long long g = (unsigned long long)(long long)q[buf][u].x;
-      const unsigned long long h = (unsigned long long)(long long)q[buf][u].y;
+      const unsigned long long g = ok ? (unsigned long long)(long long)q[b][u].x : 0ull;
+      const unsigned long long h = ok ? (unsigned long long)(long long)q[b][u].y : 0ull;
 #pragma unroll
       for (int k = 0; k < 16; ++k) {
         const uint32_t sel = 0x0c0c0000u | ((4u + uint32_t(k & 3)) << 8) | uint32_t(k & 3);
         const uint32_t off = __builtin_amdgcn_perm(a[k >> 2], slotw[k >> 2], sel);
-        if (MISSING && off >= 255u * 256u) continue;  // bin byte 255 = missing
         lds_u64* p = (lds_u64*)(lds_base + off);
         lds_add(p, g);
         lds_add(p + 16, h);
       }
     }
   };
-  // The loop bound is uniform per workgroup; rows past `end` are masked.
-  const int64_t lane = threadIdx.x;
-  load(0, w.begin + lane);
-  for (int64_t blk = w.begin; blk < w.end; blk += 2 * kStep) {
-    load(1, blk + kStep + lane);
-    process(0);
-    load(0, blk + 2 * kStep + lane);
-    process(1);
+  // The loop bound is uniform per workgroup; buffer indices are static.
+  const int64_t b0 = w.begin;
+  if (GATHER) {
+    fetch_rows(0, b0);
+    fetch_rows(1, b0 + kStep);
+    fetch_data(0, b0);
+    for (int64_t blk = b0; blk < w.end; blk += 2 * kStep) {
+      fetch_rows(0, blk + 2 * kStep);
+      fetch_data(1, blk + kStep);
+      process(0, blk);
+      fetch_rows(1, blk + 3 * kStep);
+      fetch_data(0, blk + 2 * kStep);
+      process(1, blk + kStep);
+    }
+  } else {
+    for (int64_t blk = b0; blk < w.end; blk += kStep) {
+      fetch_data(0, blk);
+      process(0, blk);
+    }
   }
   __syncthreads();
 
@@ -305,16 +332,19 @@ void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t
   // At most 1024 resident workgroups (2 per CU, two rounds); a multiple of 8.
   int grid = n_work < 1024 ? n_work : 1024;
   grid = (grid + 7) / 8 * 8;
+  // A missing value's byte 255 must not alias a real bin (its LDS row is a sink).
   if (layout.missing_bin >= 0) {
     need(layout.missing_bin == 255, "missing bin must be 255");
+    need(bin_stride <= 255, "matrices with missing values have at most 255 bins");
+  }
+  if (ridx)
     hipLaunchKernelGGL(hist_kernel<true>, dim3(grid), dim3(kHistThreads), 0, s, bins,
                        layout.n_rows, layout.n_features, gp, ridx, work, n_work, n_work_dev,
                        bin_stride, out, part);
-  } else {
+  else
     hipLaunchKernelGGL(hist_kernel<false>, dim3(grid), dim3(kHistThreads), 0, s, bins,
                        layout.n_rows, layout.n_features, gp, ridx, work, n_work, n_work_dev,
                        bin_stride, out, part);
-  }
   DP_HIP(hipGetLastError());
 }
 

@@ -1,6 +1,9 @@
 // Split evaluation: per node, per feature, a wavefront prefix scan over the
 // bins of the fixed-point histogram, the loss change of every candidate in
-// both missing directions, and an argmax with deterministic ties.
+// both missing directions, and an argmax with deterministic ties.  One
+// wavefront per (node, feature) finds the feature's best candidate, so even a
+// single node spreads over the chip; a second kernel picks each node's best
+// feature.
 //
 // Semantics (upstream CalcGain/CalcWeight with max_delta_step 0, reached in the
 // reference only through XGBoosterUpdateOneIter, class_native_training.cuh:67;
@@ -20,9 +23,6 @@
 
 namespace dp {
 namespace {
-
-constexpr int kEvalThreads = 1024;
-constexpr int kEvalWaves = kEvalThreads / 64;
 
 struct Param {
   double lambda, alpha, mcw, gamma;
@@ -75,34 +75,41 @@ __device__ __forceinline__ Cand shfl_xor_cand(const Cand& c, int mask) {
   return o;
 }
 
-// BPL: bins per lane (bin_stride <= 64 * BPL).
+// Best candidate of one (node, feature), or loss -inf when it has none.
+struct FeatCand {
+  double loss;
+  long long gl, hl;
+  int32_t bin, dl;
+};
+
+constexpr int kFeatWaves = 4;  // features per workgroup in evaluate_features_kernel
+
+// One wavefront per (node, feature): BPL bins per lane (bin_stride <= 64 *
+// BPL), an inclusive prefix scan over the bins, both missing directions, and
+// the feature's best candidate.  Workgroups loop over (node, feature group)
+// items; the node count may come from device memory.
 template <int BPL>
-__global__ __launch_bounds__(kEvalThreads) void evaluate_kernel(
+__global__ __launch_bounds__(64 * kFeatWaves) void evaluate_features_kernel(
     const long long* __restrict__ hist, int32_t n_nodes_host,
     const int32_t* __restrict__ n_nodes_dev, int32_t n_features, int32_t bin_stride,
     const int32_t* __restrict__ n_bins, const long long* __restrict__ node_sums,
     const int32_t* __restrict__ exps, int32_t exp_g_host, int32_t exp_h_host, Param p,
-    dp_split_record* __restrict__ out) {
-  __shared__ Cand wave_best[kEvalWaves];
+    FeatCand* __restrict__ cand) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int32_t n_nodes = n_nodes_dev ? *n_nodes_dev : n_nodes_host;
-  for (int node = blockIdx.x; node < n_nodes; node += gridDim.x) {
+  const int32_t groups = (n_features + kFeatWaves - 1) / kFeatWaves;
+  const int64_t n_items = int64_t(n_nodes) * groups;
   const int exp_g = exps ? exps[0] : exp_g_host;
   const int exp_h = exps ? exps[1] : exp_h_host;
   const double ug = ldexp(1.0, -exp_g), uh = ldexp(1.0, -exp_h);
-  const long long gp = node_sums[2 * node], hp = node_sums[2 * node + 1];
-  const double parent_gain = calc_gain(p, double(gp) * ug, double(hp) * uh);
-
-  Cand best;
-  best.loss = -INFINITY;
-  best.gl = best.hl = 0;
-  best.feature = -1;
-  best.bin = -1;
-  best.dl = 0;
-  const long long* node_hist = hist + int64_t(node) * n_features * bin_stride * 2;
-  for (int f = wave; f < n_features; f += kEvalWaves) {
+  for (int64_t item = blockIdx.x; item < n_items; item += gridDim.x) {
+    const int32_t node = int32_t(item / groups);
+    const int32_t f = int32_t(item % groups) * kFeatWaves + wave;
+    if (f >= n_features) continue;  // wave-uniform; no barriers in this kernel
+    const long long gp = node_sums[2 * node], hp = node_sums[2 * node + 1];
+    const double parent_gain = calc_gain(p, double(gp) * ug, double(hp) * uh);
     const int nb = n_bins[f];
-    const long long* hf = node_hist + int64_t(f) * bin_stride * 2;
+    const long long* hf = hist + (int64_t(node) * n_features + f) * bin_stride * 2;
     long long sg[BPL], sh[BPL];
     long long rg = 0, rh = 0;
 #pragma unroll
@@ -163,53 +170,105 @@ __global__ __launch_bounds__(kEvalThreads) void evaluate_kernel(
       const Cand o = shfl_xor_cand(c, m);
       if (better(o, c)) c = o;
     }
-    if (c.loss > best.loss) best = c;
+    if (lane == 0) cand[int64_t(node) * n_features + f] = FeatCand{c.loss, c.gl, c.hl, c.bin, c.dl};
   }
-  if (lane == 0) wave_best[wave] = best;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    Cand r = wave_best[0];
-    for (int k = 1; k < kEvalWaves; ++k)
-      if (better(wave_best[k], r)) r = wave_best[k];
-    dp_split_record rec;
-    rec.loss_chg = r.loss;
-    rec.gl = r.gl;
-    rec.hl = r.hl;
-    rec.feature = r.feature;
-    rec.bin = r.bin;
-    rec.default_left = r.dl;
-    rec.valid = r.loss > -INFINITY ? 1 : 0;
-    rec.expand = rec.valid && r.loss > kRtEps && r.loss >= p.gamma;
-    rec.pad = 0;
-    out[node] = rec;
-  }
-  __syncthreads();  // wave_best is reused by the next node
+}
+
+constexpr int kSelectThreads = 256;
+
+// One workgroup per node (looping over nodes): argmax over the node's feature
+// candidates with ties to the lowest feature, then the split record.
+__global__ __launch_bounds__(kSelectThreads) void select_splits_kernel(
+    const FeatCand* __restrict__ cand, int32_t n_nodes_host,
+    const int32_t* __restrict__ n_nodes_dev, int32_t n_features, double gamma,
+    dp_split_record* __restrict__ out) {
+  __shared__ Cand wave_best[kSelectThreads / 64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int32_t n_nodes = n_nodes_dev ? *n_nodes_dev : n_nodes_host;
+  for (int32_t node = blockIdx.x; node < n_nodes; node += gridDim.x) {
+    Cand best;
+    best.loss = -INFINITY;
+    best.gl = best.hl = 0;
+    best.feature = -1;
+    best.bin = -1;
+    best.dl = 0;
+    for (int32_t f = threadIdx.x; f < n_features; f += kSelectThreads) {
+      const FeatCand fc = cand[int64_t(node) * n_features + f];
+      Cand c;
+      c.loss = fc.loss;
+      c.gl = fc.gl;
+      c.hl = fc.hl;
+      c.feature = f;
+      c.bin = fc.bin;
+      c.dl = fc.dl;
+      if (fc.loss > -INFINITY && better(c, best)) best = c;
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+      const Cand o = shfl_xor_cand(best, m);
+      if (better(o, best)) best = o;
+    }
+    if (lane == 0) wave_best[wave] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      Cand r = wave_best[0];
+      for (int k = 1; k < kSelectThreads / 64; ++k)
+        if (better(wave_best[k], r)) r = wave_best[k];
+      dp_split_record rec;
+      rec.loss_chg = r.loss;
+      rec.gl = r.gl;
+      rec.hl = r.hl;
+      rec.feature = r.feature;
+      rec.bin = r.bin;
+      rec.default_left = r.dl;
+      rec.valid = r.loss > -INFINITY ? 1 : 0;
+      rec.expand = rec.valid && r.loss > kRtEps && r.loss >= gamma;
+      rec.pad = 0;
+      out[node] = rec;
+    }
+    __syncthreads();  // wave_best is reused by the next node
   }
 }
 
 }  // namespace
 
+size_t evaluate_scratch_bytes(int32_t n_nodes, int32_t n_features) {
+  return sizeof(FeatCand) * size_t(n_nodes > 0 ? n_nodes : 0) * size_t(n_features);
+}
+
 void launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_nodes_dev,
-                     int32_t n_features,
-                     int32_t bin_stride, const int32_t* n_bins, const int64_t* node_sums,
-                     const int32_t* exps, int32_t exp_g, int32_t exp_h,
-                     const dp_train_param& param, dp_split_record* out, hipStream_t s) {
+                     int32_t n_features, int32_t bin_stride, const int32_t* n_bins,
+                     const int64_t* node_sums, const int32_t* exps, int32_t exp_g, int32_t exp_h,
+                     const dp_train_param& param, void* scratch, dp_split_record* out,
+                     hipStream_t s) {
   if (n_nodes <= 0) return;
   need(bin_stride >= 1 && bin_stride <= kMaxBins, "split bin stride out of range");
+  need(n_features >= 1, "split evaluation needs at least one feature");
   Param p{double(param.lambda), double(param.alpha), double(param.min_child_weight),
           double(param.gamma)};
   const auto* h = reinterpret_cast<const long long*>(hist);
   const auto* sums = reinterpret_cast<const long long*>(node_sums);
-  const int grid = n_nodes < 512 ? n_nodes : 512;
+  auto* cand = static_cast<FeatCand*>(scratch);
+  const int64_t groups = (n_features + kFeatWaves - 1) / kFeatWaves;
+  const int64_t items = int64_t(n_nodes) * groups;
+  const int grid = int(items < 2048 ? items : 2048);
+  const dim3 block(64 * kFeatWaves);
   if (bin_stride <= 64)
-    hipLaunchKernelGGL(evaluate_kernel<1>, dim3(grid), dim3(kEvalThreads), 0, s, h,
-                       n_nodes, n_nodes_dev, n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p, out);
+    hipLaunchKernelGGL(evaluate_features_kernel<1>, dim3(grid), block, 0, s, h, n_nodes,
+                       n_nodes_dev, n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p,
+                       cand);
   else if (bin_stride <= 128)
-    hipLaunchKernelGGL(evaluate_kernel<2>, dim3(grid), dim3(kEvalThreads), 0, s, h,
-                       n_nodes, n_nodes_dev, n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p, out);
+    hipLaunchKernelGGL(evaluate_features_kernel<2>, dim3(grid), block, 0, s, h, n_nodes,
+                       n_nodes_dev, n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p,
+                       cand);
   else
-    hipLaunchKernelGGL(evaluate_kernel<4>, dim3(grid), dim3(kEvalThreads), 0, s, h,
-                       n_nodes, n_nodes_dev, n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p, out);
+    hipLaunchKernelGGL(evaluate_features_kernel<4>, dim3(grid), block, 0, s, h, n_nodes,
+                       n_nodes_dev, n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p,
+                       cand);
+  DP_HIP(hipGetLastError());
+  hipLaunchKernelGGL(select_splits_kernel, dim3(n_nodes < 1024 ? n_nodes : 1024),
+                     dim3(kSelectThreads), 0, s, cand, n_nodes, n_nodes_dev, n_features,
+                     double(param.gamma), out);
   DP_HIP(hipGetLastError());
 }
 

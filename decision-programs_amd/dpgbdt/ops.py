@@ -161,13 +161,14 @@ def train_param(eta=0.3, lam=1.0, alpha=0.0, gamma=0.0, min_child_weight=1.0, ma
     return TrainParam(eta, lam, alpha, gamma, min_child_weight, max_depth)
 
 
-def evaluate_splits(hist, n_bins, node_sums, exp_g, exp_h, param):
-    """Best split per node -> numpy structured array (SPLIT_DTYPE)."""
+def evaluate_splits(ws, hist, n_bins, node_sums, exp_g, exp_h, param):
+    """Best split per node -> device tensor of split records (see splits_to_numpy)."""
     import torch
 
     n_nodes, f, stride, _ = hist.shape
     out = torch.empty((n_nodes, ctypes.sizeof(SplitRecord)), dtype=torch.uint8, device=hist.device)
-    check(load().dp_evaluate_splits(_ptr(hist), n_nodes, f, stride, _ptr(n_bins), _ptr(node_sums),
+    check(load().dp_evaluate_splits(ws.handle, _ptr(hist), n_nodes, f, stride, _ptr(n_bins),
+                                    _ptr(node_sums),
                                     int(exp_g), int(exp_h), ctypes.byref(param), _ptr(out),
                                     _stream()))
     return out

@@ -268,8 +268,9 @@ typedef struct {
 } dp_split_record;
 
 /* Best split of every node.  node_sums int64 [n_nodes][2], n_bins int32
- * [n_features] (device); exps = (exp_g, exp_h) of the quantiser. */
-int dp_evaluate_splits(const int64_t* hist, int32_t n_nodes, int32_t n_features,
+ * [n_features] (device); exps = (exp_g, exp_h) of the quantiser.  The
+ * workspace provides the per-(node, feature) candidate scratch. */
+int dp_evaluate_splits(dp_workspace ws, const int64_t* hist, int32_t n_nodes, int32_t n_features,
                        int32_t bin_stride, const int32_t* n_bins, const int64_t* node_sums,
                        int32_t exp_g, int32_t exp_h, const dp_train_param* param,
                        dp_split_record* out, void* stream);

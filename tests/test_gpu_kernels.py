@@ -194,8 +194,8 @@ def test_split_evaluation_bit_exact(dp, oracle, ws, device):
     d_sums = torch.as_tensor(np.array(node_sums, dtype=np.int64), device=device)
     d_nbins = torch.as_tensor(n_bins, device=device)
     for prm in [dict(), dict(lam=0.0, alpha=0.5, gamma=1.0, min_child_weight=3.0)]:
-        rec = ops.splits_to_numpy(ops.evaluate_splits(hist, d_nbins, d_sums, eg, eh,
-                                                      ops.train_param(**prm)))
+        rec = ops.splits_to_numpy(ops.evaluate_splits(ws, hist, d_nbins, d_sums, eg, eh,
+                                                          ops.train_param(**prm)))
         p = oracle.params(**prm)
         for i in range(len(segs)):
             o = oracle.evaluate_split(hist[i].cpu().numpy(), n_bins, node_sums[i][0],
