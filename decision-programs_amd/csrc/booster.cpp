@@ -162,6 +162,8 @@ Quantized& DMatrix::quantize(int32_t max_bin, dp_workspace_s& ws, hipStream_t s)
   DP_HIP(hipMemcpyAsync(q->d_nbins.p, nbins.data(), q->d_nbins.bytes(), hipMemcpyHostToDevice, s));
   q->bins.resize(dp_layout_bytes(&q->layout));
   launch_bin_values(values.p, q->layout, q->d_cut_ptr.p, q->d_cut_values.p, q->bins.p, s);
+  q->cols.resize(size_t(n_rows) * size_t(n_features));
+  launch_tiles_to_columns(q->bins.p, q->layout, q->cols.p, s);
   DP_HIP(hipStreamSynchronize(s));
   auto& ref = *q;
   quantized.emplace(max_bin, std::move(q));
@@ -335,7 +337,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
       }
       launch_evaluate(h, int32_t(nb), field(c, &PlanCounts::n_level), F, B, q.d_nbins.p,
                       sums_[cur].p, exps, 0, 0, dtp, eval_scratch_.p, splits_.p, s);
-      launch_partition(q.bins.p, L, ridx_[cur].p, ridx_[nxt].p, part_work_[cur].p,
+      launch_partition(q.bins.p, q.cols.p, L, ridx_[cur].p, ridx_[nxt].p, part_work_[cur].p,
                        int32_t(plan_part_capacity(nb, N)), field(c, &PlanCounts::n_part),
                        seg_begin_[cur].p, splits_.p, part_first_[cur].p, int32_t(nb),
                        field(c, &PlanCounts::n_level), work_left_.p, work_offset_.p,

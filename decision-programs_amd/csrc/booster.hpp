@@ -20,6 +20,7 @@ struct Quantized {
   DeviceBuffer<int32_t> d_cut_ptr, d_nbins;
   DeviceBuffer<float> d_cut_values;
   DeviceBuffer<uint8_t> bins;
+  DeviceBuffer<uint8_t> cols;  // column-major copy: cols[f * n_rows + r]
 };
 
 struct DMatrix {

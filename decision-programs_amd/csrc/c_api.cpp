@@ -627,7 +627,7 @@ int dp_partition(dp_workspace ws, const uint8_t* bins, const dp_bin_layout* layo
     ws->commit(s);
     int64_t* work_left = ws->take<int64_t>(work.size());
     int64_t* work_offset = ws->take<int64_t>(work.size());
-    dp::launch_partition(bins, *layout, ridx_in, ridx_out, d_work, int32_t(work.size()), nullptr,
+    dp::launch_partition(bins, nullptr, *layout, ridx_in, ridx_out, d_work, int32_t(work.size()), nullptr,
                          d_begin, splits, d_first, n_nodes, nullptr, work_left, work_offset,
                          left_count, s);
   });

@@ -257,10 +257,11 @@ void launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_node
                      const dp_train_param& param, void* scratch, dp_split_record* out,
                      hipStream_t s);
 
-// Partition: counts, per-node scan, scatter.
-void launch_partition(const uint8_t* bins, const dp_bin_layout& layout, const uint32_t* ridx_in,
-                      uint32_t* ridx_out, const PartWork* work, int32_t n_work,
-                      const int32_t* n_work_dev, const int64_t* seg_begin,
+// Partition: counts, per-node scan, scatter.  cols: column-major copy of the
+// bins (launch_tiles_to_columns) or null to read the tiles.
+void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_layout& layout,
+                      const uint32_t* ridx_in, uint32_t* ridx_out, const PartWork* work,
+                      int32_t n_work, const int32_t* n_work_dev, const int64_t* seg_begin,
                       const dp_split_record* splits, const int32_t* node_first_work,
                       int32_t n_nodes, const int32_t* n_nodes_dev, int64_t* work_left,
                       int64_t* work_offset, int64_t* node_left, hipStream_t s);
@@ -328,6 +329,9 @@ void launch_quantise(const float* grad, const float* hess, int64_t n_rows, int32
 
 void launch_bin_values(const float* values, const dp_bin_layout& layout, const int32_t* cut_ptr,
                        const float* cut_values, uint8_t* bins, hipStream_t s);
+// cols[f * n_rows + r] = bin of (r, f), from the tile-major bins.
+void launch_tiles_to_columns(const uint8_t* bins, const dp_bin_layout& layout, uint8_t* cols,
+                             hipStream_t s);
 
 // Quantile cuts on the device; host outputs as in dp_sketch_cuts.
 void sketch_cuts(dp_workspace_s& ws, const float* values, int64_t n_rows, int32_t n_features,

@@ -21,12 +21,20 @@ namespace {
 constexpr int kPartThreads = 256;
 constexpr int kPartSteps = int(kPartChunk / kPartThreads);  // 16 rows per lane
 
+// The split feature's bin of `row`: from the column-major copy when there is
+// one (one byte per row, contiguous within a feature), else from the tiles.
+template <bool COLS>
 __device__ __forceinline__ bool goes_left(const uint8_t* __restrict__ bins, int64_t n_rows,
                                           int tile_width, uint32_t row, int feature,
                                           int split_bin, int default_left, int missing_bin) {
-  const int64_t tile = feature / tile_width;
-  const int within = feature - int(tile) * tile_width;
-  const int b = bins[tile * n_rows * tile_width + int64_t(row) * tile_width + within];
+  int b;
+  if (COLS) {
+    b = bins[int64_t(feature) * n_rows + row];
+  } else {
+    const int64_t tile = feature / tile_width;
+    const int within = feature - int(tile) * tile_width;
+    b = bins[tile * n_rows * tile_width + int64_t(row) * tile_width + within];
+  }
   if (b == missing_bin) return default_left != 0;
   return b <= split_bin;
 }
@@ -34,6 +42,7 @@ __device__ __forceinline__ bool goes_left(const uint8_t* __restrict__ bins, int6
 __device__ __forceinline__ int popc64(unsigned long long m) { return __popcll(m); }
 
 // The partition kernels loop over their items (item = blockIdx.x + k * gridDim.x).
+template <bool COLS>
 __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
     const uint8_t* __restrict__ bins, int64_t n_rows, int tile_width, int missing_bin,
     const uint32_t* __restrict__ ridx, const PartWork* __restrict__ work, int32_t n_work_host,
@@ -53,8 +62,8 @@ __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
     const int64_t i = w.begin + int64_t(step) * kPartThreads + threadIdx.x;
     bool left = false;
     if (i < w.end)
-      left = goes_left(bins, n_rows, tile_width, ridx[i], s.feature, s.bin, s.default_left,
-                       missing_bin);
+      left = goes_left<COLS>(bins, n_rows, tile_width, ridx[i], s.feature, s.bin,
+                             s.default_left, missing_bin);
     count += popc64(__ballot(left));
   }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -103,6 +112,7 @@ __global__ __launch_bounds__(kPartThreads) void part_scan_kernel(
   }
 }
 
+template <bool COLS>
 __global__ __launch_bounds__(kPartThreads) void part_scatter_kernel(
     const uint8_t* __restrict__ bins, int64_t n_rows, int tile_width, int missing_bin,
     const uint32_t* __restrict__ ridx_in, uint32_t* __restrict__ ridx_out,
@@ -130,8 +140,8 @@ __global__ __launch_bounds__(kPartThreads) void part_scatter_kernel(
     bool left = false;
     if (valid) {
       row = ridx_in[i];
-      left = goes_left(bins, n_rows, tile_width, row, s.feature, s.bin, s.default_left,
-                       missing_bin);
+      left = goes_left<COLS>(bins, n_rows, tile_width, row, s.feature, s.bin, s.default_left,
+                             missing_bin);
     }
     const unsigned long long mask = __ballot(left);
     if (lane == 0) wave_count[wave] = popc64(mask);
@@ -191,9 +201,9 @@ void launch_leaf_positions(const uint32_t* ridx, const LeafWork* work, int32_t n
   DP_HIP(hipGetLastError());
 }
 
-void launch_partition(const uint8_t* bins, const dp_bin_layout& layout, const uint32_t* ridx_in,
-                      uint32_t* ridx_out, const PartWork* work, int32_t n_work,
-                      const int32_t* n_work_dev, const int64_t* seg_begin,
+void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_layout& layout,
+                      const uint32_t* ridx_in, uint32_t* ridx_out, const PartWork* work,
+                      int32_t n_work, const int32_t* n_work_dev, const int64_t* seg_begin,
                       const dp_split_record* splits, const int32_t* node_first_work,
                       int32_t n_nodes, const int32_t* n_nodes_dev, int64_t* work_left,
                       int64_t* work_offset, int64_t* node_left, hipStream_t s) {
@@ -201,18 +211,20 @@ void launch_partition(const uint8_t* bins, const dp_bin_layout& layout, const ui
   const int missing = layout.missing_bin;
   const int gw = n_work < 2048 ? n_work : 2048;
   const int gn = n_nodes < 512 ? n_nodes : 512;
+  const uint8_t* src = cols ? cols : bins;
   if (n_work > 0)
-    hipLaunchKernelGGL(part_count_kernel, dim3(gw), dim3(kPartThreads), 0, s, bins, layout.n_rows,
-                       layout.tile_width, missing, ridx_in, work, n_work, n_work_dev, splits,
-                       work_left);
+    hipLaunchKernelGGL(cols ? part_count_kernel<true> : part_count_kernel<false>, dim3(gw),
+                       dim3(kPartThreads), 0, s, src, layout.n_rows, layout.tile_width, missing,
+                       ridx_in, work, n_work, n_work_dev, splits, work_left);
   DP_HIP(hipGetLastError());
   hipLaunchKernelGGL(part_scan_kernel, dim3(gn), dim3(kPartThreads), 0, s, node_first_work,
                      n_nodes, n_nodes_dev, work_left, work_offset, node_left);
   DP_HIP(hipGetLastError());
   if (n_work > 0)
-    hipLaunchKernelGGL(part_scatter_kernel, dim3(gw), dim3(kPartThreads), 0, s, bins,
-                       layout.n_rows, layout.tile_width, missing, ridx_in, ridx_out, work, n_work,
-                       n_work_dev, splits, seg_begin, work_offset, node_left);
+    hipLaunchKernelGGL(cols ? part_scatter_kernel<true> : part_scatter_kernel<false>, dim3(gw),
+                       dim3(kPartThreads), 0, s, src, layout.n_rows, layout.tile_width, missing,
+                       ridx_in, ridx_out, work, n_work, n_work_dev, splits, seg_begin,
+                       work_offset, node_left);
   DP_HIP(hipGetLastError());
 }
 

@@ -230,7 +230,43 @@ __global__ void copy_matrix_kernel(const float* __restrict__ src, int64_t row_st
   if (__ballot(inf) && (threadIdx.x & 63) == 0) atomicOr(bad, 1);
 }
 
+// Column-major copy of tile-major bins: cols[f * n_rows + r].  A workgroup
+// stages 256 rows x 16 features in LDS and writes 16 runs of 256 bytes.
+__global__ __launch_bounds__(256) void tiles_to_columns_kernel(const uint8_t* __restrict__ bins,
+                                                               int64_t n_rows, int32_t n_features,
+                                                               uint8_t* __restrict__ cols) {
+  __shared__ uint8_t s[16][256 + 4];
+  const int tile = blockIdx.y;
+  const int f0 = tile * 16;
+  const uint8_t* tb = bins + int64_t(tile) * n_rows * 16;
+  for (int64_t r0 = int64_t(blockIdx.x) * 256; r0 < n_rows; r0 += int64_t(gridDim.x) * 256) {
+    const int64_t r = r0 + threadIdx.x;
+    if (r < n_rows) {
+      const uint4 v = *reinterpret_cast<const uint4*>(tb + r * 16);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int k = 0; k < 16; ++k) s[k][threadIdx.x] = uint8_t(w[k >> 2] >> (8 * (k & 3)));
+    }
+    __syncthreads();
+    if (r < n_rows)
+      for (int k = 0; k < 16 && f0 + k < n_features; ++k)
+        cols[int64_t(f0 + k) * n_rows + r] = s[k][threadIdx.x];
+    __syncthreads();
+  }
+}
+
 }  // namespace
+
+void launch_tiles_to_columns(const uint8_t* bins, const dp_bin_layout& layout, uint8_t* cols,
+                             hipStream_t s) {
+  if (layout.n_rows <= 0) return;
+  need(layout.tile_width == 16, "column copy needs 16-feature tiles");
+  hipLaunchKernelGGL(tiles_to_columns_kernel, dim3(grid_for(layout.n_rows, 256, 4096),
+                     layout.n_tiles), dim3(256), 0, s, bins, layout.n_rows, layout.n_features,
+                     cols);
+  DP_HIP(hipGetLastError());
+}
+
 
 void launch_any_nan(const float* values, int64_t n, int32_t* flag, hipStream_t s) {
   launch_fill_u8(reinterpret_cast<uint8_t*>(flag), 4, 0, s);
