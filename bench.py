@@ -7,11 +7,16 @@ fixed-point (g, h) -- with everything resident in HBM.  One step is one
 histogram pass over all 10M rows (one launch of the histogram kernel).
 
 The same JSON line carries
-  roofline      the histogram kernel's algorithmic bytes per launch over its
-                average launch duration (HIP events on the launch stream),
+  roofline      the histogram operation's algorithmic bytes per launch over
+                its average duration (HIP events on the launch stream around
+                dp_hist_accumulate, i.e. hist_kernel + hist_reduce_kernel),
                 against the 8 TB/s HBM3E peak;
-  trees_per_s   full boosting rounds on C2 (1M x 28, depth 8, 100 trees,
-                binary:logistic) and C3 (depth 8, injected gradients, 20 trees);
+  trees_per_s   full boosting rounds on every configuration: C1 (10k x 8,
+                depth 6, 10 trees, logistic), C2 (1M x 28, depth 8, 100 trees,
+                logistic), C3 (10M x 128, depth 8, 20 trees, injected
+                gradients), C4 (60k x 784, softprob K=10, depth 6, 50 rounds =
+                500 trees), C5 (2M x 1000, 95 % missing, 64 bins, squared
+                error, depth 10, 50 trees);
   cpu_baseline  the CPU restatement (oracle, OpenMP) of the same histogram
                 pass on a bounded row sample, on this box's host cores.
 
@@ -141,15 +146,30 @@ def cpu_leg(sample, args):
             "gbs": algorithmic_hist_bytes(rows, f, 256) / per_pass / 1e9}
 
 
-def trees_leg(torch, dp, ops, n, config, rounds, depth, eta, injected, warm_rounds=2):
-    """Wall time of `rounds` boosting rounds on a fresh booster (matrix already quantised)."""
+# name: (config, rows, rounds, depth, eta, objective, max_bin, injected gradients)
+TREE_CONFIGS = {
+    "C1": (1, 10_000, 10, 6, 0.3, "binary:logistic", 256, False),
+    "C2": (2, 1_000_000, 100, 8, 0.1, "binary:logistic", 256, False),
+    "C3": (3, 10_000_000, 20, 8, 0.3, "reg:squarederror", 256, True),
+    "C4": (4, 60_000, 50, 6, 0.3, "multi:softprob", 256, False),
+    "C5": (5, 2_000_000, 50, 10, 0.3, "reg:squarederror", 64, False),
+}
+
+
+def trees_leg(torch, dp, ops, name, rows=None, warm_rounds=2):
+    """Wall time of the configuration's boosting rounds on a fresh booster (the
+    matrix is quantised and the kernels warmed by a previous booster)."""
+    config, n, rounds, depth, eta, objective, max_bin, injected = TREE_CONFIGS[name]
+    n = rows or n
     f = ops.SYNTH_FEATURES[config]
     values, labels, g, h = ops.synth(config, n, SEED + config, want_grad=injected)
     dtrain = dp.DMatrix(values, labels)
     del values
-    params = {"objective": "binary:logistic" if not injected else "reg:squarederror",
-              "tree_method": "hist", "device": "cuda:0", "max_depth": depth, "eta": eta,
-              "lambda": 1.0, "min_child_weight": 1.0, "max_bin": 256}
+    params = {"objective": objective, "tree_method": "hist", "device": "cuda:0",
+              "max_depth": depth, "eta": eta, "lambda": 1.0, "min_child_weight": 1.0,
+              "max_bin": max_bin}
+    if objective == "multi:softprob":
+        params["num_class"] = 10
     g1 = g.reshape(-1, 1).contiguous() if injected else None
     h1 = h.reshape(-1, 1).contiguous() if injected else None
     warm = dp.Booster(params, [dtrain])  # quantises the matrix, warms kernels
@@ -163,9 +183,13 @@ def trees_leg(torch, dp, ops, n, config, rounds, depth, eta, injected, warm_roun
         bst.boost(dtrain, r, g1, h1) if injected else bst.update(dtrain, r)
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
-    nodes = sum(len(bst.tree(t)["left"]) for t in range(bst.num_trees()))
-    return {"trees": rounds, "seconds": el, "value": rounds / el, "unit": "trees/s",
-            "rows": n, "features": f, "depth": depth, "nodes": nodes}
+    trees = bst.num_trees()
+    nodes = sum(len(bst.tree(t)["left"]) for t in range(trees))
+    del bst, dtrain
+    torch.cuda.empty_cache()
+    return {"trees": trees, "rounds": rounds, "seconds": el, "value": trees / el,
+            "unit": "trees/s", "rows": n, "features": f, "depth": depth, "objective": objective,
+            "nodes": nodes}
 
 
 def copy_leg(torch, args):
@@ -187,7 +211,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--rows", type=int, default=10_000_000)
-    ap.add_argument("--mode", choices=["full", "hist", "copy", "c2"], default="full")
+    ap.add_argument("--mode", choices=["full", "hist", "copy", "c2", "trees"], default="full")
+    ap.add_argument("--configs", default="C1,C2,C3,C4,C5",
+                    help="tree configurations timed in full/trees mode")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=1_000_000)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -205,19 +231,20 @@ def main():
     if args.mode == "copy":
         copy_leg(torch, args)
         return
-    if args.mode == "c2":  # C2 boosting rounds only (for kernel-trace profiles)
-        print(json.dumps(trees_leg(torch, dp, ops, 1_000_000, 2, 100, 8, 0.1, injected=False)))
+    names = [c.strip() for c in args.configs.split(",") if c.strip()]
+    if args.mode in ("c2", "trees"):  # boosting rounds only (for kernel-trace profiles)
+        for name in (["C2"] if args.mode == "c2" else names):
+            print(json.dumps({name: trees_leg(torch, dp, ops, name)}), flush=True)
         return
     hist, sample, *_ = hist_leg(args, torch, dp, ops)
     log(f"hist: {hist['avg_ms']:.3f} ms/launch, {hist['achieved_gbs']:.0f} GB/s algorithmic")
     trees = {}
     if args.mode == "full":
-        log("C2 trees: 1M x 28, depth 8, 100 rounds")
-        trees["C2"] = trees_leg(torch, dp, ops, 1_000_000, 2, 100, 8, 0.1, injected=False)
-        log(f"C2: {trees['C2']['value']:.1f} trees/s")
-        log("C3 trees: 10M x 128, depth 8, 20 rounds (injected gradients)")
-        trees["C3"] = trees_leg(torch, dp, ops, args.rows, 3, 20, 8, 0.3, injected=True)
-        log(f"C3: {trees['C3']['value']:.2f} trees/s")
+        for name in names:
+            log(f"{name} trees: {TREE_CONFIGS[name]}")
+            trees[name] = trees_leg(torch, dp, ops, name,
+                                    rows=args.rows if name == "C3" else None)
+            log(f"{name}: {trees[name]['value']:.1f} trees/s")
     cpu = None
     if sample is not None:
         log(f"CPU baseline: oracle histogram, {args.cpu_seconds:.0f} s budget")
@@ -245,7 +272,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": hist["achieved_gbs"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": hist["achieved_gbs"] / HBM_PEAK_GBS,
                      "traffic": read_traffic(),
-                     "kernel": "dp::hist_kernel<false>",
+                     "kernel": "dp_hist_accumulate = dp::hist_kernel<false, false> + "
+                               "dp::hist_reduce_kernel",
                      "algorithmic_bytes_per_launch": hist["algorithmic_bytes"],
                      "avg_launch_ms": hist["avg_ms"]},
         "trees_per_s": trees,

@@ -80,10 +80,11 @@ constexpr int kHistUnroll = 2;           // rows per lane per pipeline stage
 // The LDS address is assembled by one v_perm_b32: byte 1 = the bin byte, byte 0
 // = the lane's feature offset for that step.
 //
-// The row loop has no branches, so the compiler's memory counters see a
+// The row loads have no branches, so the compiler's memory counters see a
 // straight pipeline: indices past `end` are clamped to the last row and their
-// (g, h) masked to zero, and a missing value (byte 255; matrices with missing
-// values have at most 255 bins) adds into LDS row 255, which is never read.
+// (g, h) masked to zero.  With MISSING, lanes whose byte is 255 (missing; such
+// matrices have at most 255 bins) skip the atomics by exec mask, which keeps
+// sparse data (C5: 95 % missing) from spending LDS cycles on absent values.
 // Contiguous rows (GATHER false) are loaded and accumulated block by block (the
 // 32 waves of a CU hide the load latency; measured: prefetching a block ahead
 // does not help, the loop is bound by the LDS atomics); gathered rows
@@ -91,7 +92,7 @@ constexpr int kHistUnroll = 2;           // rows per lane per pipeline stage
 // one block ahead.  At most 64 VGPRs, so two workgroups fit on a CU.
 // Workgroups loop over items (item = blockIdx.x + k * gridDim.x); with a grid
 // that is a multiple of 8, item i still runs on XCD i mod 8.
-template <bool GATHER>
+template <bool GATHER, bool MISSING>
 __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8, 8))) void hist_kernel(
     const uint8_t* __restrict__ bins, int64_t n_rows, int32_t n_features,
     const int2* __restrict__ gpair, const uint32_t* __restrict__ ridx,
@@ -152,6 +153,7 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8,
       for (int k = 0; k < 16; ++k) {
         const uint32_t sel = 0x0c0c0000u | ((4u + uint32_t(k & 3)) << 8) | uint32_t(k & 3);
         const uint32_t off = __builtin_amdgcn_perm(a[k >> 2], slotw[k >> 2], sel);
+        if (MISSING && off >= 255u * 256u) continue;  // byte 255: missing value
         lds_u64* p = (lds_u64*)(lds_base + off);
         lds_add(p, g);
         lds_add(p + 16, h);
@@ -332,19 +334,16 @@ void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t
   // At most 1024 resident workgroups (2 per CU, two rounds); a multiple of 8.
   int grid = n_work < 1024 ? n_work : 1024;
   grid = (grid + 7) / 8 * 8;
-  // A missing value's byte 255 must not alias a real bin (its LDS row is a sink).
+  // A missing value's byte 255 must not alias a real bin.
   if (layout.missing_bin >= 0) {
     need(layout.missing_bin == 255, "missing bin must be 255");
     need(bin_stride <= 255, "matrices with missing values have at most 255 bins");
   }
-  if (ridx)
-    hipLaunchKernelGGL(hist_kernel<true>, dim3(grid), dim3(kHistThreads), 0, s, bins,
-                       layout.n_rows, layout.n_features, gp, ridx, work, n_work, n_work_dev,
-                       bin_stride, out, part);
-  else
-    hipLaunchKernelGGL(hist_kernel<false>, dim3(grid), dim3(kHistThreads), 0, s, bins,
-                       layout.n_rows, layout.n_features, gp, ridx, work, n_work, n_work_dev,
-                       bin_stride, out, part);
+  const bool missing = layout.missing_bin >= 0;
+  auto kernel = ridx ? (missing ? hist_kernel<true, true> : hist_kernel<true, false>)
+                     : (missing ? hist_kernel<false, true> : hist_kernel<false, false>);
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(kHistThreads), 0, s, bins, layout.n_rows,
+                     layout.n_features, gp, ridx, work, n_work, n_work_dev, bin_stride, out, part);
   DP_HIP(hipGetLastError());
 }
 
