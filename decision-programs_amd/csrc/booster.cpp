@@ -214,16 +214,16 @@ void Grower::ensure_level(const Quantized& q, int64_t nb, int32_t d, int32_t D) 
   const int64_t S = int64_t(q.layout.n_features) * q.bin_stride * 2;
   const int cur = d & 1, nxt = cur ^ 1;
   const int64_t nn = d < D ? std::min(2 * nb, N) : 0;  // next level's bound
-  need(plan_hist_capacity(nn, T) < INT32_MAX && plan_part_capacity(nb, N) < INT32_MAX &&
-           plan_part_capacity(nn, N) < INT32_MAX && plan_leaf_capacity(nb, N) < INT32_MAX,
+  need(plan_hist_capacity(nn, T) < INT32_MAX && plan_part_capacity(nb, N, chunk_) < INT32_MAX &&
+           plan_part_capacity(nn, N, chunk_) < INT32_MAX && plan_leaf_capacity(nb, N, chunk_) < INT32_MAX,
        "tree level too wide for the planner's 32-bit work counts");
   if (d < D) {
     hist_[cur].reserve(size_t(nb * S));
     splits_.reserve(size_t(nb));
     eval_scratch_.reserve(evaluate_scratch_bytes(int32_t(nb), q.layout.n_features));
     node_left_.reserve(size_t(nb));
-    work_left_.reserve(size_t(plan_part_capacity(nb, N)));
-    work_offset_.reserve(size_t(plan_part_capacity(nb, N)));
+    work_left_.reserve(size_t(plan_part_capacity(nb, N, chunk_)));
+    work_offset_.reserve(size_t(plan_part_capacity(nb, N, chunk_)));
   }
   level_[nxt].reserve(size_t(std::max<int64_t>(nn, 1)));
   sums_[nxt].reserve(size_t(2 * std::max<int64_t>(nn, 1)));
@@ -231,9 +231,9 @@ void Grower::ensure_level(const Quantized& q, int64_t nb, int32_t d, int32_t D) 
   hist_work_[nxt].reserve(size_t(plan_hist_capacity(nn, T)));
   reduce_jobs_[nxt].reserve(size_t(nn / 2 + 1));
   pair_chunk_.reserve(size_t(2 * (std::max(nb, nn) + 1)));
-  part_work_[nxt].reserve(size_t(plan_part_capacity(nn, N)));
+  part_work_[nxt].reserve(size_t(plan_part_capacity(nn, N, chunk_)));
   part_first_[nxt].reserve(size_t(nn + 1));
-  leaf_work_.reserve(size_t(plan_leaf_capacity(nb, N)));
+  leaf_work_.reserve(size_t(plan_leaf_capacity(nb, N, chunk_)));
 }
 
 void Grower::prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, hipStream_t s) {
@@ -244,6 +244,7 @@ void Grower::prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, h
   need(N >= 1, "training matrix has no rows");
   need(N <= int64_t(UINT32_MAX), "row ids are 32-bit");
   need(D >= 1 && D <= 30, "max_depth out of supported range");
+  chunk_ = row_chunk(N);
   ridx_[0].reserve(size_t(N));
   ridx_[1].reserve(size_t(N));
   counts_.reserve(1);
@@ -252,7 +253,7 @@ void Grower::prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, h
   level_[0].reserve(1);
   sums_[0].reserve(2);
   seg_begin_[0].reserve(1);
-  part_work_[0].reserve(size_t(plan_part_capacity(1, N)));
+  part_work_[0].reserve(size_t(plan_part_capacity(1, N, chunk_)));
   part_first_[0].reserve(2);
   partial_.reserve(size_t(hist_partial_capacity(L.n_tiles) * q.bin_stride * 32));
   if (root_rows_ != N || root_tiles_ != L.n_tiles) {
@@ -303,7 +304,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
 
   launch_iota_u32(ridx_[0].p, N, s);
   launch_plan_root(level_[0].p, sums_[0].p, seg_begin_[0].p, part_work_[0].p, part_first_[0].p, c,
-                   N, root_sums, s);
+                   N, root_sums, chunk_, s);
   int64_t nb = 1;  // bound of the current level's node count
   for (int32_t d = 0; d <= D; ++d) {
     const int cur = d & 1, nxt = cur ^ 1;
@@ -330,7 +331,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
         launch_hist_reduce(partial_.p, root_job_.p, 1, nullptr, T, F, B, nullptr, h, false, s);
       } else {
         launch_hist(q.bins.p, L, gpair, ridx_[cur].p, hist_work_[cur].p,
-                    int32_t(plan_hist_capacity(nb, T)), field(c, &PlanCounts::n_hist), B, h,
+                    int32_t(plan_hist_items(nb, N, T)), field(c, &PlanCounts::n_hist), B, h,
                     partial_.p, s);
         launch_hist_reduce(partial_.p, reduce_jobs_[cur].p, int32_t(nb / 2 + 1),
                            field(c, &PlanCounts::n_reduce), T, F, B, hist_[nxt].p, h, false, s);
@@ -338,7 +339,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
       launch_evaluate(h, int32_t(nb), field(c, &PlanCounts::n_level), F, B, q.d_nbins.p,
                       sums_[cur].p, exps, 0, 0, dtp, eval_scratch_.p, splits_.p, s);
       launch_partition(q.bins.p, q.cols.p, L, ridx_[cur].p, ridx_[nxt].p, part_work_[cur].p,
-                       int32_t(plan_part_capacity(nb, N)), field(c, &PlanCounts::n_part),
+                       int32_t(plan_part_capacity(nb, N, chunk_)), field(c, &PlanCounts::n_part),
                        seg_begin_[cur].p, splits_.p, part_first_[cur].p, int32_t(nb),
                        field(c, &PlanCounts::n_level), work_left_.p, work_offset_.p,
                        node_left_.p, s);
@@ -363,6 +364,8 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     a.max_depth = D;
     a.n_tiles = T;
     a.hist_elems = S;
+    a.part_chunk = chunk_;
+    a.leaf_chunk = chunk_;
     a.eta = double(p.eta);
     a.lambda = double(p.lambda);
     a.alpha = double(p.alpha);
@@ -374,7 +377,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     a.part_capacity = int32_t(part_work_[nxt].n);
     a.leaf_capacity = int32_t(leaf_work_.n);
     launch_plan_level(a, s);
-    const int32_t leaf_bound = int32_t(plan_leaf_capacity(nb, N));
+    const int32_t leaf_bound = int32_t(plan_leaf_capacity(nb, N, chunk_));
     launch_update_margin(ridx_[cur].p, leaf_work_.p, leaf_bound, field(c, &PlanCounts::n_leaf),
                          margin, stride, s);
     if (positions)

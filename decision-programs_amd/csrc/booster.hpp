@@ -97,6 +97,7 @@ class Grower {
   std::vector<PlanCounts> spill_counts_;
   bool eager_ = true;
   int64_t node_cap_ = 0;
+  int64_t chunk_ = kPartChunk;  // rows per partition / margin-update item
   size_t slot_bytes_ = 0;
   int64_t root_rows_ = -1;
   int32_t root_tiles_ = 0, root_items_ = 0;

@@ -295,6 +295,7 @@ struct PlanArgs {
   int32_t depth, max_depth;
   int32_t n_tiles;
   int64_t hist_elems;      // int64 values per node histogram
+  int64_t part_chunk, leaf_chunk;  // rows per partition / margin-update item
   double eta, lambda, alpha, mcw;
   int32_t info_capacity, level_capacity;
   int32_t hist_capacity, partial_capacity, part_capacity, leaf_capacity;
@@ -305,18 +306,30 @@ void launch_plan_level(const PlanArgs& a, hipStream_t s);
 // partition work over [0, n_rows).
 void launch_plan_root(LevelNode* cur, int64_t* sums, int64_t* seg_begin, PartWork* part_work,
                       int32_t* part_first, PlanCounts* counts, int64_t n_rows,
-                      const int64_t* root_sums, hipStream_t s);
+                      const int64_t* root_sums, int64_t part_chunk, hipStream_t s);
 // Upper bounds of the planner's outputs for a level of at most `nodes` nodes.
 inline int64_t plan_hist_capacity(int64_t nodes, int32_t n_tiles) {
   return 1024 + (nodes / 2 + 8) * int64_t(n_tiles);
 }
-inline int64_t plan_part_capacity(int64_t nodes, int64_t n_rows) {
-  return n_rows / kPartChunk + 1 + nodes;
+// Rows per partition / margin-update work item of the planner: about 2048
+// items over the matrix, a multiple of 256 in [256, kPartChunk].
+inline int64_t row_chunk(int64_t n_rows) {
+  const int64_t c = (n_rows / 2048 + 255) / 256 * 256;
+  return c < 256 ? 256 : (c > kPartChunk ? kPartChunk : c);
 }
-constexpr int64_t kLeafChunk = 16384;
-inline int64_t plan_leaf_capacity(int64_t nodes, int64_t n_rows) {
-  return n_rows / kLeafChunk + 1 + nodes;
+inline int64_t plan_part_capacity(int64_t nodes, int64_t n_rows, int64_t chunk) {
+  return n_rows / chunk + 1 + nodes;
 }
+inline int64_t plan_leaf_capacity(int64_t nodes, int64_t n_rows, int64_t chunk) {
+  return n_rows / chunk + 1 + nodes;
+}
+// Histogram work items of a level of at most `nodes` nodes: C <= min(1024 /
+// n_tiles, n_rows / (2 kHistMinChunk)) + nodes / 2 row chunks, padded to 8.
+inline int64_t plan_hist_items(int64_t nodes, int64_t n_rows, int32_t n_tiles) {
+  const int64_t a = 1024 / n_tiles, b = n_rows / (2 * kHistMinChunk);
+  return ((a < b ? a : b) + nodes / 2 + 8) * int64_t(n_tiles);
+}
+constexpr int64_t kLeafChunk = 16384;  // margin-update items of the operator API
 
 void launch_gradients(int32_t objective, const float* margin, const float* label,
                       int64_t n_rows, int32_t n_classes, float* grad, float* hess,

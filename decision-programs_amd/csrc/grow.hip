@@ -42,21 +42,32 @@ __device__ double plan_weight(const PlanArgs& a, double g, double h) {
 }
 
 // Exclusive scan of one int64 per thread over the workgroup; returns this
-// thread's prefix and writes the total to *total.
+// thread's prefix and writes the total to *total.  Wavefront scans by
+// shuffles, then one wavefront scans the 16 wave totals (three barriers).
 __device__ int64_t block_scan(int64_t v, int64_t* lds, int64_t* total) {
-  const int t = threadIdx.x;
-  lds[t] = v;
-  __syncthreads();
-  for (int d = 1; d < kPlanThreads; d <<= 1) {
-    const int64_t add = t >= d ? lds[t - d] : 0;
-    __syncthreads();
-    lds[t] += add;
-    __syncthreads();
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  int64_t x = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int64_t y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
   }
-  const int64_t incl = lds[t];
-  *total = lds[kPlanThreads - 1];
+  if (lane == 63) lds[wave] = x;
   __syncthreads();
-  return incl - v;
+  if (wave == 0) {
+    int64_t w = lane < kPlanThreads / 64 ? lds[lane] : 0;
+#pragma unroll
+    for (int d = 1; d < kPlanThreads / 64; d <<= 1) {
+      const int64_t y = __shfl_up(w, d, 64);
+      if (lane >= d) w += y;
+    }
+    if (lane < kPlanThreads / 64) lds[kPlanThreads / 64 + lane] = w;  // inclusive
+  }
+  __syncthreads();
+  const int64_t before = wave ? lds[kPlanThreads / 64 + wave - 1] : 0;
+  *total = lds[2 * (kPlanThreads / 64) - 1];
+  __syncthreads();
+  return before + x - v;
 }
 
 // Index of the segment holding item k: the last i in [0, n) with off[i] <= k
@@ -164,7 +175,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
     if (i < n) {
       const LevelNode nd = a.cur[i];
       if (!node_expands(a, i, nd.end - nd.begin))
-        chunks = (nd.end - nd.begin + kLeafChunk - 1) / kLeafChunk;
+        chunks = (nd.end - nd.begin + a.leaf_chunk - 1) / a.leaf_chunk;
     }
     int64_t total;
     const int64_t o = carry + block_scan(chunks, scan, &total);
@@ -181,9 +192,9 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
   for (int64_t k = tid; k < n_leaf; k += kPlanThreads) {
     const int32_t i = owner(off, n, k);
     const LevelNode nd = a.cur[i];
-    const int64_t b = nd.begin + (k - off[i]) * kLeafChunk;
+    const int64_t b = nd.begin + (k - off[i]) * a.leaf_chunk;
     a.leaf_work[k] = LeafWork{a.info[nd.nid].leaf_value, nd.nid, b,
-                              b + kLeafChunk < nd.end ? b + kLeafChunk : nd.end};
+                              b + a.leaf_chunk < nd.end ? b + a.leaf_chunk : nd.end};
   }
   __syncthreads();  // off is reused below
 
@@ -274,7 +285,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
       int64_t chunks = 0;
       if (i < n_next) {
         const LevelNode nd = a.next[i];
-        chunks = (nd.end - nd.begin + kPartChunk - 1) / kPartChunk;
+        chunks = (nd.end - nd.begin + a.part_chunk - 1) / a.part_chunk;
       }
       int64_t total;
       const int64_t o = carry + block_scan(chunks, scan, &total);
@@ -291,8 +302,8 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
     for (int64_t k = tid; k < n_part; k += kPlanThreads) {
       const int32_t i = owner(a.part_first, n_next, k);
       const LevelNode nd = a.next[i];
-      const int64_t b = nd.begin + (k - a.part_first[i]) * kPartChunk;
-      a.part_work[k] = PartWork{i, 0, b, b + kPartChunk < nd.end ? b + kPartChunk : nd.end};
+      const int64_t b = nd.begin + (k - a.part_first[i]) * a.part_chunk;
+      a.part_work[k] = PartWork{i, 0, b, b + a.part_chunk < nd.end ? b + a.part_chunk : nd.end};
     }
   }
 
@@ -311,12 +322,12 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
 
 __global__ void plan_root_kernel(LevelNode* cur, int64_t* sums, int64_t* seg_begin,
                                  PartWork* part_work, int32_t* part_first, PlanCounts* counts,
-                                 int64_t n_rows, const int64_t* root_sums) {
-  const int64_t chunks = (n_rows + kPartChunk - 1) / kPartChunk;
+                                 int64_t n_rows, const int64_t* root_sums, int64_t part_chunk) {
+  const int64_t chunks = (n_rows + part_chunk - 1) / part_chunk;
   for (int64_t j = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; j < chunks;
        j += int64_t(blockDim.x) * gridDim.x) {
-    const int64_t b = j * kPartChunk;
-    part_work[j] = PartWork{0, 0, b, b + kPartChunk < n_rows ? b + kPartChunk : n_rows};
+    const int64_t b = j * part_chunk;
+    part_work[j] = PartWork{0, 0, b, b + part_chunk < n_rows ? b + part_chunk : n_rows};
   }
   if (blockIdx.x == 0 && threadIdx.x == 0) {
     const int64_t g = root_sums[0], h = root_sums[1];
@@ -343,10 +354,11 @@ void launch_plan_level(const PlanArgs& a, hipStream_t s) {
 
 void launch_plan_root(LevelNode* cur, int64_t* sums, int64_t* seg_begin, PartWork* part_work,
                       int32_t* part_first, PlanCounts* counts, int64_t n_rows,
-                      const int64_t* root_sums, hipStream_t s) {
-  const int64_t chunks = (n_rows + kPartChunk - 1) / kPartChunk;
+                      const int64_t* root_sums, int64_t part_chunk, hipStream_t s) {
+  need(part_chunk >= 1 && part_chunk <= kPartChunk, "partition chunk out of range");
+  const int64_t chunks = (n_rows + part_chunk - 1) / part_chunk;
   hipLaunchKernelGGL(plan_root_kernel, dim3(grid_for(chunks, 256, 1024)), dim3(256), 0, s, cur,
-                     sums, seg_begin, part_work, part_first, counts, n_rows, root_sums);
+                     sums, seg_begin, part_work, part_first, counts, n_rows, root_sums, part_chunk);
   DP_HIP(hipGetLastError());
 }
 

@@ -59,6 +59,7 @@ __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
   }
   int count = 0;
   for (int step = 0; step < kPartSteps; ++step) {
+    if (w.begin + int64_t(step) * kPartThreads >= w.end) break;  // uniform per workgroup
     const int64_t i = w.begin + int64_t(step) * kPartThreads + threadIdx.x;
     bool left = false;
     if (i < w.end)

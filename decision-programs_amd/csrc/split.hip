@@ -152,8 +152,11 @@ __global__ __launch_bounds__(64 * kFeatWaves) void evaluate_features_kernel(
       if (b < nb) {
         const long long lg = og + sg[j], lh = oh + sh[j];
         const double right_missing = split_loss(p, lg, lh, gp - lg, hp - lh, ug, uh, parent_gain);
+        // Without missing rows both directions are the same candidate.
         const double left_missing =
-            split_loss(p, lg + mg, lh + mh, gp - lg - mg, hp - lh - mh, ug, uh, parent_gain);
+            (mg == 0 && mh == 0)
+                ? right_missing
+                : split_loss(p, lg + mg, lh + mh, gp - lg - mg, hp - lh - mh, ug, uh, parent_gain);
         const int dl = left_missing > right_missing;
         const double loss = dl ? left_missing : right_missing;
         if (loss > c.loss) {
