@@ -164,6 +164,8 @@ Quantized& DMatrix::quantize(int32_t max_bin, dp_workspace_s& ws, hipStream_t s)
   launch_bin_values(values.p, q->layout, q->d_cut_ptr.p, q->d_cut_values.p, q->bins.p, s);
   q->cols.resize(size_t(n_rows) * size_t(n_features));
   launch_tiles_to_columns(q->bins.p, q->layout, q->cols.p, s);
+  q->rows.resize(dp_layout_bytes(&q->layout));
+  launch_tiles_to_rows(q->bins.p, q->layout, q->rows.p, s);
   DP_HIP(hipStreamSynchronize(s));
   auto& ref = *q;
   quantized.emplace(max_bin, std::move(q));
@@ -332,7 +334,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
       } else {
         launch_hist(q.bins.p, L, gpair, ridx_[cur].p, hist_work_[cur].p,
                     int32_t(plan_hist_items(nb, N, T)), field(c, &PlanCounts::n_hist), B, h,
-                    partial_.p, s);
+                    partial_.p, s, q.rows.p);
         launch_hist_reduce(partial_.p, reduce_jobs_[cur].p, int32_t(nb / 2 + 1),
                            field(c, &PlanCounts::n_reduce), T, F, B, hist_[nxt].p, h, false, s);
       }

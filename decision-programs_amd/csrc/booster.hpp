@@ -21,6 +21,7 @@ struct Quantized {
   DeviceBuffer<float> d_cut_values;
   DeviceBuffer<uint8_t> bins;
   DeviceBuffer<uint8_t> cols;  // column-major copy: cols[f * n_rows + r]
+  DeviceBuffer<uint8_t> rows;  // row-major copy: rows[(r * n_tiles + t) * 16 + j]
 };
 
 struct DMatrix {

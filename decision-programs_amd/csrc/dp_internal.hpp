@@ -216,10 +216,12 @@ void launch_iota_u32(uint32_t* p, int64_t n, hipStream_t s);
 
 // Histograms: every work item accumulates into hist[slot]; hist must be zero.
 // Direct items write hist; the others write partial (int64 [slot][bin_stride * 32]).
+// row_major: optional row-major copy of the bins (launch_tiles_to_rows), read
+// for gathered rows.
 void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t* gpair,
                  const uint32_t* ridx, const HistWork* work, int32_t n_work,
                  const int32_t* n_work_dev, int32_t bin_stride, int64_t* hist,
-                 int64_t* partial, hipStream_t s);
+                 int64_t* partial, hipStream_t s, const uint8_t* row_major = nullptr);
 // Completes the histograms of launch_hist: sums partial tiles, writes built
 // and sibling node histograms.  accumulate: add the sums to hist instead of
 // storing them (then no job may rely on a direct item).
@@ -345,6 +347,9 @@ void launch_bin_values(const float* values, const dp_bin_layout& layout, const i
 // cols[f * n_rows + r] = bin of (r, f), from the tile-major bins.
 void launch_tiles_to_columns(const uint8_t* bins, const dp_bin_layout& layout, uint8_t* cols,
                              hipStream_t s);
+// rows[r * n_tiles * 16 + t * 16 + j] = tile t's byte j of row r.
+void launch_tiles_to_rows(const uint8_t* bins, const dp_bin_layout& layout, uint8_t* rows,
+                          hipStream_t s);
 
 // Quantile cuts on the device; host outputs as in dp_sketch_cuts.
 void sketch_cuts(dp_workspace_s& ws, const float* values, int64_t n_rows, int32_t n_features,

@@ -5,6 +5,11 @@
 //  * bins are uint8 in tiles of 16 features (tile-major: tile t holds 16 bytes
 //    per row), so one lane reads the 16 bins of a row with one 128-bit load and
 //    a wavefront of contiguous rows reads 1 KiB contiguous;
+//  * gathered rows (levels below the root) read a row-major copy instead (all
+//    tiles of a row in one run of n_tiles * 16 bytes): the workgroups of one
+//    row chunk, one per tile, run together on one XCD and share every row's
+//    cache lines in L2, where the tile-major layout would fetch a 64-byte
+//    sector for each 16 bytes used;
 //  * each workgroup privatises the histogram of one tile in 64 KiB of LDS (two
 //    workgroups per CU), as int64 fixed-point sums, see hist_kernel;
 //  * lane-dependent rotation of the 16 bytes keeps the 64-bit LDS atomics bank
@@ -98,7 +103,8 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8,
     const int2* __restrict__ gpair, const uint32_t* __restrict__ ridx,
     const HistWork* __restrict__ work, int32_t n_work_host,
     const int32_t* __restrict__ n_work_dev, int32_t bin_stride,
-    unsigned long long* __restrict__ hist, unsigned long long* __restrict__ partial) {
+    unsigned long long* __restrict__ hist, unsigned long long* __restrict__ partial,
+    int64_t tile_step, int64_t row_step) {
   __shared__ unsigned long long lds[kLdsWords];
   constexpr int U = kHistUnroll;
   constexpr int64_t kStep = int64_t(kHistThreads) * U;
@@ -119,7 +125,7 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8,
   for (int e = threadIdx.x; e < kLdsWords; e += kHistThreads) lds[e] = 0ull;
   __syncthreads();
 
-  const uint8_t* tile = bins + int64_t(w.tile) * n_rows * kTile;
+  const uint8_t* tile = bins + int64_t(w.tile) * tile_step;  // row r at tile + r * row_step
   const int64_t last = w.end - 1;
   const int64_t lane = threadIdx.x;
   uint32_t rows[2][U];  // GATHER: row ids of the block after the next
@@ -137,7 +143,7 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8,
     for (int u = 0; u < U; ++u) {
       const int64_t i = base + int64_t(u) * kHistThreads + lane;
       const uint32_t r = GATHER ? rows[b][u] : uint32_t(i < w.end ? i : last);
-      v[b][u] = *reinterpret_cast<const uint4*>(tile + int64_t(r) * kTile);
+      v[b][u] = *reinterpret_cast<const uint4*>(tile + int64_t(r) * row_step);
       q[b][u] = gpair[r];
     }
   };
@@ -324,7 +330,7 @@ int32_t make_hist_work(const dp_bin_layout& layout, const int64_t* begin, const 
 void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t* gpair,
                  const uint32_t* ridx, const HistWork* work, int32_t n_work,
                  const int32_t* n_work_dev, int32_t bin_stride, int64_t* hist,
-                 int64_t* partial, hipStream_t s) {
+                 int64_t* partial, hipStream_t s, const uint8_t* row_major) {
   if (n_work <= 0) return;
   need(bin_stride >= 1 && bin_stride <= kMaxBins, "histogram bin stride out of range");
   need(layout.tile_width == kTile, "histogram kernel needs 16-feature tiles");
@@ -339,11 +345,16 @@ void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t
     need(layout.missing_bin == 255, "missing bin must be 255");
     need(bin_stride <= 255, "matrices with missing values have at most 255 bins");
   }
+  const bool rows = ridx && row_major;
+  const uint8_t* src = rows ? row_major : bins;
+  const int64_t tile_step = rows ? kTile : layout.n_rows * kTile;
+  const int64_t row_step = rows ? int64_t(layout.n_tiles) * kTile : kTile;
   const bool missing = layout.missing_bin >= 0;
   auto kernel = ridx ? (missing ? hist_kernel<true, true> : hist_kernel<true, false>)
                      : (missing ? hist_kernel<false, true> : hist_kernel<false, false>);
-  hipLaunchKernelGGL(kernel, dim3(grid), dim3(kHistThreads), 0, s, bins, layout.n_rows,
-                     layout.n_features, gp, ridx, work, n_work, n_work_dev, bin_stride, out, part);
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(kHistThreads), 0, s, src, layout.n_rows,
+                     layout.n_features, gp, ridx, work, n_work, n_work_dev, bin_stride, out, part,
+                     tile_step, row_step);
   DP_HIP(hipGetLastError());
 }
 

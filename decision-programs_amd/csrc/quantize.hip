@@ -255,7 +255,28 @@ __global__ __launch_bounds__(256) void tiles_to_columns_kernel(const uint8_t* __
   }
 }
 
+// Row-major copy of tile-major bins: one 16-byte piece per thread.
+__global__ void tiles_to_rows_kernel(const uint8_t* __restrict__ bins, int64_t n_rows,
+                                     int32_t n_tiles, uint8_t* __restrict__ rows) {
+  const int64_t n = n_rows * n_tiles;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += int64_t(blockDim.x) * gridDim.x) {
+    const int64_t t = i / n_rows, r = i - t * n_rows;
+    *reinterpret_cast<uint4*>(rows + (r * n_tiles + t) * 16) =
+        *reinterpret_cast<const uint4*>(bins + i * 16);
+  }
+}
+
 }  // namespace
+
+void launch_tiles_to_rows(const uint8_t* bins, const dp_bin_layout& layout, uint8_t* rows,
+                          hipStream_t s) {
+  if (layout.n_rows <= 0) return;
+  need(layout.tile_width == 16, "row copy needs 16-feature tiles");
+  hipLaunchKernelGGL(tiles_to_rows_kernel, dim3(grid_for(layout.n_rows * layout.n_tiles, 256, 8192)),
+                     dim3(256), 0, s, bins, layout.n_rows, layout.n_tiles, rows);
+  DP_HIP(hipGetLastError());
+}
 
 void launch_tiles_to_columns(const uint8_t* bins, const dp_bin_layout& layout, uint8_t* cols,
                              hipStream_t s) {
