@@ -239,4 +239,97 @@ inline void put_float_array(std::string& o, const std::vector<float>& v) {
   o += ']';
 }
 
+// Text of a parsed (or built) value: compact when indent < 0, else one
+// member / item per line indented by `indent` spaces per level.  Number
+// tokens are written as they were read.
+inline void dump_to(std::string& o, const Value& v, int indent, int level = 0) {
+  auto newline = [&](int lvl) {
+    if (indent < 0) return;
+    o += '\n';
+    o.append(size_t(indent) * size_t(lvl), ' ');
+  };
+  switch (v.kind) {
+    case Value::Null: o += "null"; break;
+    case Value::Bool: o += v.boolean ? "true" : "false"; break;
+    case Value::Number: o += v.text; break;
+    case Value::String: put_string(o, v.text); break;
+    case Value::Array:
+      if (v.items.empty()) { o += "[]"; break; }
+      o += '[';
+      for (size_t i = 0; i < v.items.size(); ++i) {
+        if (i) o += ',';
+        newline(level + 1);
+        dump_to(o, v.items[i], indent, level + 1);
+      }
+      newline(level);
+      o += ']';
+      break;
+    case Value::Object:
+      if (v.members.empty()) { o += "{}"; break; }
+      o += '{';
+      for (size_t i = 0; i < v.members.size(); ++i) {
+        if (i) o += ',';
+        newline(level + 1);
+        put_string(o, v.members[i].first);
+        o += indent < 0 ? ":" : ": ";
+        dump_to(o, v.members[i].second, indent, level + 1);
+      }
+      newline(level);
+      o += '}';
+      break;
+  }
+}
+
+inline std::string dump(const Value& v, int indent = -1) {
+  std::string o;
+  dump_to(o, v, indent);
+  return o;
+}
+
+// Builders for values written by the host tools.
+inline Value null_value() { return Value{}; }
+inline Value boolean(bool b) {
+  Value v;
+  v.kind = Value::Bool;
+  v.boolean = b;
+  return v;
+}
+inline Value string(std::string s) {
+  Value v;
+  v.kind = Value::String;
+  v.text = std::move(s);
+  return v;
+}
+inline Value number(double x) {
+  Value v;
+  v.kind = Value::Number;
+  put_double(v.text, x);
+  return v;
+}
+inline Value integer(int64_t x) {
+  Value v;
+  v.kind = Value::Number;
+  v.text = std::to_string(x);
+  return v;
+}
+inline Value object() {
+  Value v;
+  v.kind = Value::Object;
+  return v;
+}
+inline Value array() {
+  Value v;
+  v.kind = Value::Array;
+  return v;
+}
+// Sets (replacing) member `key` of object `o`.
+inline void set(Value& o, const std::string& key, Value value) {
+  for (auto& m : o.members)
+    if (m.first == key) {
+      m.second = std::move(value);
+      return;
+    }
+  o.members.emplace_back(key, std::move(value));
+}
+
 }  // namespace dp::json
