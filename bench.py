@@ -50,7 +50,8 @@ def algorithmic_hist_bytes(n_rows, n_features, n_bins, gathered=False):
 
 
 def read_traffic():
-    """HBM bytes per launch of the C3 root histogram from the committed PMC summary."""
+    """HBM bytes per C3 root histogram call (hist_kernel + hist_reduce_kernel) from the
+    committed PMC summary."""
     path = os.path.join(ROOT, "profiles", "hist_c3_root_pmc.md")
     try:
         for line in open(path):
