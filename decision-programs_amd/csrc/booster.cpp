@@ -223,10 +223,9 @@ void Grower::ensure_level(const Quantized& q, int64_t nb, int32_t d, int32_t D) 
     hist_[cur].reserve(size_t(nb * S));
     splits_.reserve(size_t(nb));
     eval_scratch_.reserve(evaluate_scratch_bytes(int32_t(nb), q.layout.n_features));
-    node_left_.reserve(size_t(nb));
     work_left_.reserve(size_t(plan_part_capacity(nb, N, chunk_)));
-    work_offset_.reserve(size_t(plan_part_capacity(nb, N, chunk_)));
   }
+  node_left_[nxt].reserve(size_t(std::max<int64_t>(nn, 1)));
   level_[nxt].reserve(size_t(std::max<int64_t>(nn, 1)));
   sums_[nxt].reserve(size_t(2 * std::max<int64_t>(nn, 1)));
   seg_begin_[nxt].reserve(size_t(std::max<int64_t>(nn, 1)));
@@ -257,6 +256,7 @@ void Grower::prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, h
   seg_begin_[0].reserve(1);
   part_work_[0].reserve(size_t(plan_part_capacity(1, N, chunk_)));
   part_first_[0].reserve(2);
+  node_left_[0].reserve(1);
   partial_.reserve(size_t(hist_partial_capacity(L.n_tiles) * q.bin_stride * 32));
   if (root_rows_ != N || root_tiles_ != L.n_tiles) {
     const int64_t b = 0, e = N;
@@ -305,8 +305,8 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
   auto* host_counts = reinterpret_cast<PlanCounts*>(level_count_.p);
 
   launch_iota_u32(ridx_[0].p, N, s);
-  launch_plan_root(level_[0].p, sums_[0].p, seg_begin_[0].p, part_work_[0].p, part_first_[0].p, c,
-                   N, root_sums, chunk_, s);
+  launch_plan_root(level_[0].p, sums_[0].p, seg_begin_[0].p, part_work_[0].p, part_first_[0].p,
+                   node_left_[0].p, c, N, root_sums, chunk_, s);
   int64_t nb = 1;  // bound of the current level's node count
   for (int32_t d = 0; d <= D; ++d) {
     const int cur = d & 1, nxt = cur ^ 1;
@@ -343,13 +343,13 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
       launch_partition(q.bins.p, q.cols.p, L, ridx_[cur].p, ridx_[nxt].p, part_work_[cur].p,
                        int32_t(plan_part_capacity(nb, N, chunk_)), field(c, &PlanCounts::n_part),
                        seg_begin_[cur].p, splits_.p, part_first_[cur].p, int32_t(nb),
-                       field(c, &PlanCounts::n_level), work_left_.p, work_offset_.p,
-                       node_left_.p, s);
+                       field(c, &PlanCounts::n_level), work_left_.p, node_left_[cur].p, true, s);
     }
     PlanArgs a{};
     a.cur = level_[cur].p;
     a.splits = split ? splits_.p : nullptr;
-    a.node_left = node_left_.p;
+    a.node_left = node_left_[cur].p;
+    a.next_node_left = node_left_[nxt].p;
     a.next = level_[nxt].p;
     a.next_sums = sums_[nxt].p;
     a.next_seg_begin = seg_begin_[nxt].p;

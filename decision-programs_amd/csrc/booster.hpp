@@ -86,7 +86,7 @@ class Grower {
   DeviceBuffer<int64_t> partial_;
   DeviceBuffer<PartWork> part_work_[2];
   DeviceBuffer<int32_t> part_first_[2];
-  DeviceBuffer<int64_t> pair_chunk_, work_left_, work_offset_, node_left_;
+  DeviceBuffer<int64_t> pair_chunk_, work_left_, node_left_[2];
   DeviceBuffer<dp_split_record> splits_;
   DeviceBuffer<uint8_t> eval_scratch_;
   DeviceBuffer<LeafWork> leaf_work_;

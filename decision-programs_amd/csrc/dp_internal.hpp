@@ -259,14 +259,17 @@ void launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_node
                      const dp_train_param& param, void* scratch, dp_split_record* out,
                      hipStream_t s);
 
-// Partition: counts, per-node scan, scatter.  cols: column-major copy of the
-// bins (launch_tiles_to_columns) or null to read the tiles.
+// Partition: counts, then scatter (which writes the left totals of the
+// expanding nodes into node_left).  cols: column-major copy of the bins
+// (launch_tiles_to_columns) or null to read the tiles.  node_left_zeroed: the
+// caller has zeroed node_left[0, nodes) (non-expanding nodes keep 0); else it
+// is cleared here for n_nodes nodes.
 void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_layout& layout,
                       const uint32_t* ridx_in, uint32_t* ridx_out, const PartWork* work,
                       int32_t n_work, const int32_t* n_work_dev, const int64_t* seg_begin,
                       const dp_split_record* splits, const int32_t* node_first_work,
                       int32_t n_nodes, const int32_t* n_nodes_dev, int64_t* work_left,
-                      int64_t* work_offset, int64_t* node_left, hipStream_t s);
+                      int64_t* node_left, bool node_left_zeroed, hipStream_t s);
 constexpr int64_t kPartChunk = 4096;
 
 void launch_update_margin(const uint32_t* ridx, const LeafWork* work, int32_t n_work,
@@ -282,6 +285,7 @@ struct PlanArgs {
   const LevelNode* cur;
   const dp_split_record* splits;  // null: every node of this level is a leaf
   const int64_t* node_left;
+  int64_t* next_node_left;  // zeroed for the next level's nodes
   LevelNode* next;
   int64_t* next_sums;      // [slot][2]
   int64_t* next_seg_begin; // [slot]
@@ -304,11 +308,12 @@ struct PlanArgs {
 };
 void launch_plan_level(const PlanArgs& a, hipStream_t s);
 // counts->n_level = 1, n_nodes = 1, ...; cur[0] = root {0, n_rows, g, h, 0, -1}
-// with (g, h) = root_sums[0..1]; sums[0..1] = (g, h), seg_begin[0] = 0; root
-// partition work over [0, n_rows).
+// with (g, h) = root_sums[0..1]; sums[0..1] = (g, h), seg_begin[0] = 0,
+// node_left[0] = 0; root partition work over [0, n_rows).
 void launch_plan_root(LevelNode* cur, int64_t* sums, int64_t* seg_begin, PartWork* part_work,
-                      int32_t* part_first, PlanCounts* counts, int64_t n_rows,
-                      const int64_t* root_sums, int64_t part_chunk, hipStream_t s);
+                      int32_t* part_first, int64_t* node_left, PlanCounts* counts,
+                      int64_t n_rows, const int64_t* root_sums, int64_t part_chunk,
+                      hipStream_t s);
 // Upper bounds of the planner's outputs for a level of at most `nodes` nodes.
 inline int64_t plan_hist_capacity(int64_t nodes, int32_t n_tiles) {
   return 1024 + (nodes / 2 + 8) * int64_t(n_tiles);

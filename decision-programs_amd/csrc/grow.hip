@@ -143,6 +143,8 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
           a.next_sums[2 * slot + 3] = nd.h - s.hl;
           a.next_seg_begin[slot] = nd.begin;
           a.next_seg_begin[slot + 1] = nd.begin + nl;
+          a.next_node_left[slot] = 0;
+          a.next_node_left[slot + 1] = 0;
         } else {
           s_error = 2;
         }
@@ -321,8 +323,9 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
 }
 
 __global__ void plan_root_kernel(LevelNode* cur, int64_t* sums, int64_t* seg_begin,
-                                 PartWork* part_work, int32_t* part_first, PlanCounts* counts,
-                                 int64_t n_rows, const int64_t* root_sums, int64_t part_chunk) {
+                                 PartWork* part_work, int32_t* part_first, int64_t* node_left,
+                                 PlanCounts* counts, int64_t n_rows, const int64_t* root_sums,
+                                 int64_t part_chunk) {
   const int64_t chunks = (n_rows + part_chunk - 1) / part_chunk;
   for (int64_t j = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; j < chunks;
        j += int64_t(blockDim.x) * gridDim.x) {
@@ -335,6 +338,7 @@ __global__ void plan_root_kernel(LevelNode* cur, int64_t* sums, int64_t* seg_beg
     sums[0] = g;
     sums[1] = h;
     seg_begin[0] = 0;
+    node_left[0] = 0;
     part_first[0] = 0;
     part_first[1] = int32_t(chunks);
     PlanCounts c{};
@@ -353,12 +357,14 @@ void launch_plan_level(const PlanArgs& a, hipStream_t s) {
 }
 
 void launch_plan_root(LevelNode* cur, int64_t* sums, int64_t* seg_begin, PartWork* part_work,
-                      int32_t* part_first, PlanCounts* counts, int64_t n_rows,
-                      const int64_t* root_sums, int64_t part_chunk, hipStream_t s) {
+                      int32_t* part_first, int64_t* node_left, PlanCounts* counts,
+                      int64_t n_rows, const int64_t* root_sums, int64_t part_chunk,
+                      hipStream_t s) {
   need(part_chunk >= 1 && part_chunk <= kPartChunk, "partition chunk out of range");
   const int64_t chunks = (n_rows + part_chunk - 1) / part_chunk;
   hipLaunchKernelGGL(plan_root_kernel, dim3(grid_for(chunks, 256, 1024)), dim3(256), 0, s, cur,
-                     sums, seg_begin, part_work, part_first, counts, n_rows, root_sums, part_chunk);
+                     sums, seg_begin, part_work, part_first, node_left, counts, n_rows, root_sums,
+                     part_chunk);
   DP_HIP(hipGetLastError());
 }
 

@@ -3,14 +3,15 @@
 // Upstream applies a level's splits by moving each node's row ids so the left
 // child's rows precede the right child's (inside XGBoosterUpdateOneIter,
 // class_native_training.cuh:67).  Here every expanding node's segment of
-// ridx_in is split in three launches:
-//   1. count: one workgroup per chunk of <= kPartChunk rows counts left rows
-//      with wavefront ballots;
-//   2. scan: one workgroup per node turns its chunk counts into exclusive
-//      offsets and the node's left total;
-//   3. scatter: each chunk ranks its rows in position order (ballot prefix
-//      counts, 256 rows per step) and writes lefts to [begin + left rank) and
-//      rights to [begin + n_left + right rank) of ridx_out.
+// ridx_in is split in two launches:
+//   1. count: one workgroup per chunk of <= kPartChunk rows counts its left
+//      rows with wavefront ballots;
+//   2. scatter: each chunk sums the counts of its node's chunks (the node's
+//      left total, and its own exclusive offset from the earlier ones; the
+//      node's first chunk publishes the total in node_left), ranks its rows in
+//      position order (ballot prefix counts, 256 rows per step) and writes
+//      lefts to [begin + left rank) and rights to [begin + n_left + right rank)
+//      of ridx_out.  No atomics: a node can have thousands of chunks.
 // The row goes left iff its bin of the split feature is <= the split bin, or it
 // is missing and the split's default is left.
 #include "dp_internal.hpp"
@@ -79,58 +80,47 @@ __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
   }
 }
 
-// One workgroup per node: exclusive scan of its chunks' left counts.
-__global__ __launch_bounds__(kPartThreads) void part_scan_kernel(
-    const int32_t* __restrict__ node_first_work, int32_t n_nodes_host,
-    const int32_t* __restrict__ n_nodes_dev, const int64_t* __restrict__ work_left,
-    int64_t* __restrict__ work_offset, int64_t* __restrict__ node_left) {
-  __shared__ int64_t partial[kPartThreads];
-  __shared__ int64_t carry;
-  const int32_t n_nodes = n_nodes_dev ? *n_nodes_dev : n_nodes_host;
-  for (int node = blockIdx.x; node < n_nodes; node += gridDim.x) {
-  const int first = node_first_work[node], last = node_first_work[node + 1];
-  if (threadIdx.x == 0) carry = 0;
-  __syncthreads();
-  for (int base = first; base < last; base += kPartThreads) {
-    const int i = base + threadIdx.x;
-    const int64_t v = i < last ? work_left[i] : 0;
-    partial[threadIdx.x] = v;
-    __syncthreads();
-    // Hillis-Steele inclusive scan over the block.
-    for (int d = 1; d < kPartThreads; d <<= 1) {
-      const int64_t add = threadIdx.x >= d ? partial[threadIdx.x - d] : 0;
-      __syncthreads();
-      partial[threadIdx.x] += add;
-      __syncthreads();
-    }
-    if (i < last) work_offset[i] = carry + partial[threadIdx.x] - v;
-    __syncthreads();
-    if (threadIdx.x == kPartThreads - 1) carry += partial[threadIdx.x];
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) node_left[node] = carry;
-  __syncthreads();
-  }
-}
-
 template <bool COLS>
 __global__ __launch_bounds__(kPartThreads) void part_scatter_kernel(
     const uint8_t* __restrict__ bins, int64_t n_rows, int tile_width, int missing_bin,
     const uint32_t* __restrict__ ridx_in, uint32_t* __restrict__ ridx_out,
     const PartWork* __restrict__ work, int32_t n_work_host,
     const int32_t* __restrict__ n_work_dev, const dp_split_record* __restrict__ splits,
-    const int64_t* __restrict__ seg_begin, const int64_t* __restrict__ work_offset,
-    const int64_t* __restrict__ node_left) {
+    const int64_t* __restrict__ seg_begin, const int32_t* __restrict__ node_first_work,
+    const int64_t* __restrict__ work_left, int64_t* __restrict__ node_left) {
   __shared__ int wave_count[kPartThreads / 64];
+  __shared__ int64_t wave_sum[2][kPartThreads / 64];
   const int32_t n_work = n_work_dev ? *n_work_dev : n_work_host;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   for (int32_t item = blockIdx.x; item < n_work; item += gridDim.x) {
   const PartWork w = work[item];
   const dp_split_record s = splits[w.node];
   if (!s.expand) continue;
   const int64_t begin = seg_begin[w.node];
-  const int64_t n_left = node_left[w.node];
-  int64_t lefts_before = work_offset[item];  // lefts before this step
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // the node's left total and the lefts in its chunks before this one
+  const int32_t first = node_first_work[w.node], last = node_first_work[w.node + 1];
+  int64_t before = 0, total = 0;
+  for (int32_t k = first + threadIdx.x; k < last; k += kPartThreads) {
+    const int64_t v = work_left[k];
+    total += v;
+    if (k < item) before += v;
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    before += __shfl_xor(before, m, 64);
+    total += __shfl_xor(total, m, 64);
+  }
+  if (lane == 0) {
+    wave_sum[0][wave] = before;
+    wave_sum[1][wave] = total;
+  }
+  __syncthreads();
+  int64_t lefts_before = 0, n_left = 0;  // lefts before this step; node total
+  for (int k = 0; k < kPartThreads / 64; ++k) {
+    lefts_before += wave_sum[0][k];
+    n_left += wave_sum[1][k];
+  }
+  if (item == first && threadIdx.x == 0) node_left[w.node] = n_left;
   const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   for (int step = 0; step < kPartSteps; ++step) {
     const int64_t step_base = w.begin + int64_t(step) * kPartThreads;
@@ -207,25 +197,22 @@ void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_lay
                       int32_t n_work, const int32_t* n_work_dev, const int64_t* seg_begin,
                       const dp_split_record* splits, const int32_t* node_first_work,
                       int32_t n_nodes, const int32_t* n_nodes_dev, int64_t* work_left,
-                      int64_t* work_offset, int64_t* node_left, hipStream_t s) {
+                      int64_t* node_left, bool node_left_zeroed, hipStream_t s) {
   if (n_nodes <= 0) return;
+  (void)n_nodes_dev;
   const int missing = layout.missing_bin;
   const int gw = n_work < 2048 ? n_work : 2048;
-  const int gn = n_nodes < 512 ? n_nodes : 512;
   const uint8_t* src = cols ? cols : bins;
-  if (n_work > 0)
-    hipLaunchKernelGGL(cols ? part_count_kernel<true> : part_count_kernel<false>, dim3(gw),
-                       dim3(kPartThreads), 0, s, src, layout.n_rows, layout.tile_width, missing,
-                       ridx_in, work, n_work, n_work_dev, splits, work_left);
+  if (!node_left_zeroed) launch_fill_i64(node_left, n_nodes, 0, s);
+  if (n_work <= 0) return;
+  hipLaunchKernelGGL(cols ? part_count_kernel<true> : part_count_kernel<false>, dim3(gw),
+                     dim3(kPartThreads), 0, s, src, layout.n_rows, layout.tile_width, missing,
+                     ridx_in, work, n_work, n_work_dev, splits, work_left);
   DP_HIP(hipGetLastError());
-  hipLaunchKernelGGL(part_scan_kernel, dim3(gn), dim3(kPartThreads), 0, s, node_first_work,
-                     n_nodes, n_nodes_dev, work_left, work_offset, node_left);
-  DP_HIP(hipGetLastError());
-  if (n_work > 0)
-    hipLaunchKernelGGL(cols ? part_scatter_kernel<true> : part_scatter_kernel<false>, dim3(gw),
-                       dim3(kPartThreads), 0, s, src, layout.n_rows, layout.tile_width, missing,
-                       ridx_in, ridx_out, work, n_work, n_work_dev, splits, seg_begin,
-                       work_offset, node_left);
+  hipLaunchKernelGGL(cols ? part_scatter_kernel<true> : part_scatter_kernel<false>, dim3(gw),
+                     dim3(kPartThreads), 0, s, src, layout.n_rows, layout.tile_width, missing,
+                     ridx_in, ridx_out, work, n_work, n_work_dev, splits, seg_begin,
+                     node_first_work, work_left, node_left);
   DP_HIP(hipGetLastError());
 }
 
