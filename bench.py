@@ -18,7 +18,9 @@ The same JSON line carries
                 500 trees), C5 (2M x 1000, 95 % missing, 64 bins, squared
                 error, depth 10, 50 trees);
   cpu_baseline  the CPU restatement (oracle, OpenMP) of the same histogram
-                pass on a bounded row sample, on this box's host cores.
+                pass on a bounded row sample, on this box's host cores; in
+                full mode also the oracle's single-threaded booster on C1 (10
+                trees) and C2 (2 trees) as trees/s.
 
 Data are synthetic (dp_synth, fixed seeds); nothing is read from disk.
 """
@@ -135,7 +137,7 @@ def cpu_leg(sample, args):
         res = pyoracle.hist_parallel(bins, qg, qh, stride, -1, threads)
         reps += 1
         el = time.perf_counter() - t0
-        if el >= args.cpu_seconds or reps >= 200:
+        if el >= args.cpu_seconds or reps >= 5000:
             break
     per_pass = el / reps
     # the sample histogram must equal the sum over its rows (exact integers)
@@ -145,6 +147,34 @@ def cpu_leg(sample, args):
             "sample": f"oracle dpo_hist_parallel root pass over the first {rows} rows x {f} "
                       f"features of the C3 matrix, {reps} passes, {el:.1f} s",
             "gbs": algorithmic_hist_bytes(rows, f, 256) / per_pass / 1e9}
+
+
+def cpu_trees_leg(ops, name, max_rounds):
+    """The oracle's single-threaded booster (same cuts, bins and tree rules) on the
+    configuration's data: trees/s over at most `max_rounds` rounds."""
+    import numpy as np
+    import pyoracle
+
+    config, n, rounds, depth, eta, objective, max_bin, injected = TREE_CONFIGS[name]
+    rounds = min(rounds, max_rounds)
+    values, labels, _, _ = ops.synth(config, n, SEED + config)
+    x = values.cpu().numpy()
+    y = labels.cpu().numpy()
+    del values, labels
+    has_missing = bool(np.isnan(x).any())
+    cut_ptr, cuts, _ = pyoracle.compute_cuts(x, pyoracle.effective_max_bin(max_bin, has_missing))
+    mb = 255 if has_missing else -1
+    bins = pyoracle.bin_matrix(x, cut_ptr, cuts, mb)
+    obj = {"binary:logistic": 0, "multi:softprob": 1, "reg:squarederror": 2}[objective]
+    k = 10 if obj == 1 else 1
+    p = pyoracle.params(eta=eta, max_depth=depth)
+    t0 = time.perf_counter()
+    trees, _, _ = pyoracle.train(bins, cut_ptr, cuts, mb, obj, y, k, p, rounds,
+                                 bin_stride=int(np.diff(cut_ptr).max()))
+    el = time.perf_counter() - t0
+    return {"value": len(trees) / el, "unit": "trees/s", "cores": 1, "kind": "port",
+            "sample": f"oracle booster, {len(trees)} trees of {name} ({n} x {x.shape[1]}, "
+                      f"depth {depth}), {el:.1f} s, one thread"}
 
 
 # name: (config, rows, rounds, depth, eta, objective, max_bin, injected gradients)
@@ -250,6 +280,11 @@ def main():
     if sample is not None:
         log(f"CPU baseline: oracle histogram, {args.cpu_seconds:.0f} s budget")
         cpu = cpu_leg(sample, args)
+        if args.mode == "full":
+            cpu["trees_per_s"] = {}
+            for name, cap in (("C1", 10), ("C2", 2)):
+                log(f"CPU baseline: oracle booster on {name}")
+                cpu["trees_per_s"][name] = cpu_trees_leg(ops, name, cap)
     avg_s = hist["avg_ms"] * 1e-3
     line = {
         "metric": METRIC,

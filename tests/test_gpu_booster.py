@@ -157,6 +157,28 @@ def test_c3_reduced_injected_gradients(dp, oracle, device):
     _compare(bst, o_trees, o_margin, pos, n, 1)
 
 
+def test_wide_tree_level_synced(dp, oracle, device):
+    """Depth 17 over 150,000 rows: a level may hold more than 65,536 nodes, so the
+    grower reads each level's size back and sizes its buffers per level instead
+    of enqueueing the whole tree (the path large trees take)."""
+    p = {"max_depth": 17, "eta": 0.3}
+    print("[booster] C1 150000 x 8, depth 17 (level-synced growth)", flush=True)
+    bst, x, o_trees, o_margin, pos, n = _train_both(dp, oracle, device, 1, 150000, 8, 0, 1, p, 2,
+                                                    20261211)
+    _compare(bst, o_trees, o_margin, pos, n, 1)
+    assert max(len(t["left"]) for t in o_trees) > 2 ** 12, "tree too small to exercise the path"
+
+
+def test_depth_one_and_single_chunk(dp, oracle, device):
+    """Smallest shapes: stumps (max_depth 1) and a matrix of one histogram chunk."""
+    for n, depth in [(50, 1), (4000, 3), (5000, 1)]:
+        p = {"max_depth": depth, "eta": 0.5}
+        print(f"[booster] C1 {n} x 8, depth {depth}", flush=True)
+        bst, x, o_trees, o_margin, pos, n = _train_both(dp, oracle, device, 1, n, 8, 0, 1, p, 3,
+                                                        20261212 + n)
+        _compare(bst, o_trees, o_margin, pos, n, 1)
+
+
 def test_regularisation_paths(dp, oracle, device):
     """alpha, gamma and min_child_weight change the chosen splits identically."""
     p = {"max_depth": 5, "eta": 0.5, "alpha": 0.7, "gamma": 2.0, "min_child_weight": 8.0,
