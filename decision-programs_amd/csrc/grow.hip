@@ -29,6 +29,9 @@ namespace dp {
 namespace {
 
 constexpr int kPlanThreads = 1024;
+// Offsets of levels up to this many segments are also kept in LDS, so the
+// per-item binary searches do not chase dependent global loads.
+constexpr int kLdsOffsets = 4096;
 
 __device__ double plan_threshold_l1(double g, double alpha) {
   if (g > alpha) return g - alpha;
@@ -90,6 +93,7 @@ __device__ bool node_expands(const PlanArgs& a, int32_t i, int64_t rows) {
 
 __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
   __shared__ int64_t scan[kPlanThreads];
+  __shared__ int64_t s_off[kLdsOffsets + 1];
   __shared__ int32_t s_error;
   const int tid = threadIdx.x;
   const int32_t n = a.counts->n_level;
@@ -182,19 +186,26 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
     int64_t total;
     const int64_t o = carry + block_scan(chunks, scan, &total);
     carry += total;
-    if (i < n) off[i] = o;
+    if (i < n) {
+      off[i] = o;
+      if (n <= kLdsOffsets) s_off[i] = o;
+    }
   }
   int64_t n_leaf = carry;
-  if (tid == 0) off[n] = n_leaf;
+  if (tid == 0) {
+    off[n] = n_leaf;
+    if (n <= kLdsOffsets) s_off[n] = n_leaf;
+  }
   __syncthreads();
+  const int64_t* leaf_off = n <= kLdsOffsets ? s_off : off;
   if (n_leaf > a.leaf_capacity) {
     if (tid == 0) s_error = 3;
     n_leaf = 0;
   }
   for (int64_t k = tid; k < n_leaf; k += kPlanThreads) {
-    const int32_t i = owner(off, n, k);
+    const int32_t i = owner(leaf_off, n, k);
     const LevelNode nd = a.cur[i];
-    const int64_t b = nd.begin + (k - off[i]) * a.leaf_chunk;
+    const int64_t b = nd.begin + (k - leaf_off[i]) * a.leaf_chunk;
     a.leaf_work[k] = LeafWork{a.info[nd.nid].leaf_value, nd.nid, b,
                               b + a.leaf_chunk < nd.end ? b + a.leaf_chunk : nd.end};
   }
@@ -235,11 +246,16 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
       if (j < n_expand) {
         cstart[j] = o;
         pstart[j] = po;
+        if (n_expand <= kLdsOffsets) s_off[j] = o;
       }
     }
     const int64_t C = carry;
-    if (tid == 0) cstart[n_expand] = C;
+    if (tid == 0) {
+      cstart[n_expand] = C;
+      if (n_expand <= kLdsOffsets) s_off[n_expand] = C;
+    }
     __syncthreads();
+    const int64_t* pair_off = n_expand <= kLdsOffsets ? s_off : cstart;
     const int64_t padded = (C + 7) / 8 * 8;
     n_hist = padded * T;
     if (n_hist > a.hist_capacity || pcarry * T > a.partial_capacity) {
@@ -250,15 +266,15 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
         HistWork item{0, 0, 0, 0, -1, 0};
         int64_t p = -1;
         if (c < C) {
-          const int32_t j = owner(cstart, n_expand, c);
+          const int32_t j = owner(pair_off, n_expand, c);
           const LevelNode l = a.next[2 * j], r = a.next[2 * j + 1];
           const bool right_small = (r.end - r.begin) < (l.end - l.begin);
           const LevelNode sm = right_small ? r : l;
-          const int64_t k = c - cstart[j];
+          const int64_t k = c - pair_off[j];
           const int64_t b = sm.begin + k * chunk;
           item = HistWork{2 * j + (right_small ? 1 : 0), 0, b,
                           b + chunk < sm.end ? b + chunk : sm.end, -1, 0};
-          if (cstart[j + 1] - cstart[j] >= 2) p = (pstart[j] + k) * T;
+          if (pair_off[j + 1] - pair_off[j] >= 2) p = (pstart[j] + k) * T;
         }
         for (int32_t t = 0; t < T; ++t) {
           item.tile = t;
@@ -269,7 +285,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
       for (int32_t j = tid; j < n_expand; j += kPlanThreads) {
         const LevelNode l = a.next[2 * j], r = a.next[2 * j + 1];
         const bool right_small = (r.end - r.begin) < (l.end - l.begin);
-        const int32_t nc = int32_t(cstart[j + 1] - cstart[j]);
+        const int32_t nc = int32_t(pair_off[j + 1] - pair_off[j]);
         a.reduce_jobs[j] = HistReduce{2 * j + (right_small ? 1 : 0), 2 * j + (right_small ? 0 : 1),
                                       int64_t(l.parent_slot) * a.hist_elems,
                                       nc >= 2 ? int32_t(pstart[j]) : -1, nc};
@@ -292,19 +308,26 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
       int64_t total;
       const int64_t o = carry + block_scan(chunks, scan, &total);
       carry += total;
-      if (i < n_next) a.part_first[i] = int32_t(o);
+      if (i < n_next) {
+        a.part_first[i] = int32_t(o);
+        if (n_next <= kLdsOffsets) s_off[i] = o;
+      }
     }
     n_part = carry;
-    if (tid == 0) a.part_first[n_next] = int32_t(n_part);
+    if (tid == 0) {
+      a.part_first[n_next] = int32_t(n_part);
+      if (n_next <= kLdsOffsets) s_off[n_next] = n_part;
+    }
     __syncthreads();
     if (n_part > a.part_capacity) {
       if (tid == 0) s_error = 5;
       n_part = 0;
     }
     for (int64_t k = tid; k < n_part; k += kPlanThreads) {
-      const int32_t i = owner(a.part_first, n_next, k);
+      const int32_t i = n_next <= kLdsOffsets ? owner(s_off, n_next, k) : owner(a.part_first, n_next, k);
       const LevelNode nd = a.next[i];
-      const int64_t b = nd.begin + (k - a.part_first[i]) * a.part_chunk;
+      const int64_t first = n_next <= kLdsOffsets ? s_off[i] : int64_t(a.part_first[i]);
+      const int64_t b = nd.begin + (k - first) * a.part_chunk;
       a.part_work[k] = PartWork{i, 0, b, b + a.part_chunk < nd.end ? b + a.part_chunk : nd.end};
     }
   }
