@@ -146,6 +146,42 @@ def test_root_histogram_bit_exact(dp, oracle, ws, device, config, n, f):
         assert np.all(np.abs(gsum[feat] - exact) <= 1e-5 * np.maximum(mass, 1e-30))
 
 
+@pytest.mark.parametrize("max_bin", [64, 128])
+def test_sparse_histograms_bit_exact(dp, oracle, ws, device, max_bin):
+    """Missing values with at most 128 bins take the compacting kernel (present
+    entries queued per wavefront, then full-wave atomics): contiguous and
+    gathered rows, against the oracle and against np.bincount counts."""
+    import torch
+    from dpgbdt import ops
+
+    n, f = 30000, 200
+    values, _, g, h = _synth(ops, 5, n, 41 + max_bin, f, grad=True)
+    lay, bins, o_bins, cut_ptr, cuts, n_bins, mb = _prepare(dp, oracle, ws, values, max_bin)
+    assert mb == 255
+    stride = int(n_bins.max())
+    assert stride <= 128
+    gn, hn = g.cpu().numpy(), h.cpu().numpy()
+    _, gpair, _ = _gpair(ws, device, gn, hn)
+    q = oracle.quantise(gn, hn)[0]
+    root = ops.hist_build(ws, bins, lay, gpair, [(0, n)], stride).cpu().numpy()[0]
+    np.testing.assert_array_equal(root, oracle.hist(o_bins, q[2], q[3], bin_stride=stride,
+                                                    missing_bin=mb))
+    rng = np.random.default_rng(3)
+    ridx = rng.permutation(n).astype(np.uint32)
+    segs = [(0, 1), (1, 333), (333, 9000), (9000, n)]
+    hist = ops.hist_build(ws, bins, lay, gpair, segs, stride,
+                          ridx=torch.as_tensor(ridx.view(np.int32), device=device)).cpu().numpy()
+    for i, (b, e) in enumerate(segs):
+        ref = oracle.hist(o_bins, q[2], q[3], rows=ridx[b:e], bin_stride=stride, missing_bin=mb)
+        np.testing.assert_array_equal(hist[i], ref, err_msg=f"segment {i}")
+    ones = torch.ones((n, 2), dtype=torch.int32, device=device)
+    counts = ops.hist_build(ws, bins, lay, ones, [(0, n)], stride).cpu().numpy()[0]
+    for feat in range(0, f, 13):
+        col = o_bins[:, feat]
+        np.testing.assert_array_equal(counts[feat, :, 0],
+                                      np.bincount(col[col != 255], minlength=stride)[:stride])
+
+
 def test_gathered_histograms_and_subtraction(dp, oracle, ws, device):
     import torch
     from dpgbdt import ops
