@@ -234,7 +234,7 @@ void Grower::ensure_level(const Quantized& q, int64_t nb, int32_t d, int32_t D) 
   pair_chunk_.reserve(size_t(2 * (std::max(nb, nn) + 1)));
   part_work_[nxt].reserve(size_t(plan_part_capacity(nn, N, chunk_)));
   part_first_[nxt].reserve(size_t(nn + 1));
-  leaf_work_.reserve(size_t(plan_leaf_capacity(nb, N, chunk_)));
+  leaf_work_[cur].reserve(size_t(plan_leaf_capacity(nb, N, chunk_)));
 }
 
 void Grower::prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, hipStream_t s) {
@@ -308,13 +308,22 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
   launch_plan_root(level_[0].p, sums_[0].p, seg_begin_[0].p, part_work_[0].p, part_first_[0].p,
                    node_left_[0].p, c, N, root_sums, chunk_, s);
   int64_t nb = 1;  // bound of the current level's node count
+  int64_t nb_prev = 0;
   for (int32_t d = 0; d <= D; ++d) {
     const int cur = d & 1, nxt = cur ^ 1;
     if (!eager_ && d > 0) {
       DP_HIP(hipMemcpyAsync(host_counts, c, sizeof(PlanCounts), hipMemcpyDeviceToHost, s));
       DP_HIP(hipStreamSynchronize(s));
       nb = host_counts->n_level;
-      if (nb == 0) break;
+      if (nb == 0) {  // the tree ended: apply the previous level's deferred leaves
+        const int32_t bound = int32_t(plan_leaf_capacity(nb_prev, N, chunk_));
+        launch_update_margin(ridx_[nxt].p, leaf_work_[nxt].p, bound,
+                             field(c, &PlanCounts::n_leaf), margin, stride, s);
+        if (positions)
+          launch_leaf_positions(ridx_[nxt].p, leaf_work_[nxt].p, bound,
+                                field(c, &PlanCounts::n_leaf), positions, s);
+        break;
+      }
       ensure_level(q, nb, d, D);
       const int64_t need_nodes = int64_t(host_counts->n_nodes) + 2 * nb;
       if (int64_t(info_.n) < need_nodes) {
@@ -340,10 +349,24 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
       }
       launch_evaluate(h, int32_t(nb), field(c, &PlanCounts::n_level), F, B, q.d_nbins.p,
                       sums_[cur].p, exps, 0, 0, dtp, eval_scratch_.p, splits_.p, s);
+      // The previous level's leaves (its planner wrote their chunks; their rows
+      // sit in that level's ridx buffer, untouched by this level's scatter)
+      // are applied by this level's count launch.
+      LeafPass prev;
+      if (d > 0) {
+        prev.ridx = ridx_[nxt].p;
+        prev.work = leaf_work_[nxt].p;
+        prev.n_dev = field(c, &PlanCounts::n_leaf);
+        prev.n_host = int32_t(plan_leaf_capacity(nb_prev, N, chunk_));
+        prev.margin = margin;
+        prev.stride = stride;
+        prev.positions = positions;
+      }
       launch_partition(q.bins.p, q.cols.p, L, ridx_[cur].p, ridx_[nxt].p, part_work_[cur].p,
                        int32_t(plan_part_capacity(nb, N, chunk_)), field(c, &PlanCounts::n_part),
                        seg_begin_[cur].p, splits_.p, part_first_[cur].p, int32_t(nb),
-                       field(c, &PlanCounts::n_level), work_left_.p, node_left_[cur].p, true, s);
+                       field(c, &PlanCounts::n_level), work_left_.p, node_left_[cur].p, true, s,
+                       d > 0 ? &prev : nullptr);
     }
     PlanArgs a{};
     a.cur = level_[cur].p;
@@ -359,7 +382,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     a.part_work = part_work_[nxt].p;
     a.part_first = part_first_[nxt].p;
     a.pair_chunk = pair_chunk_.p;
-    a.leaf_work = leaf_work_.p;
+    a.leaf_work = leaf_work_[cur].p;
     a.counts = c;
     a.exps = exps;
     a.depth = d;
@@ -377,14 +400,17 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     a.hist_capacity = int32_t(hist_work_[nxt].n);
     a.partial_capacity = int32_t(hist_partial_capacity(T));
     a.part_capacity = int32_t(part_work_[nxt].n);
-    a.leaf_capacity = int32_t(leaf_work_.n);
+    a.leaf_capacity = int32_t(leaf_work_[cur].n);
     launch_plan_level(a, s);
-    const int32_t leaf_bound = int32_t(plan_leaf_capacity(nb, N, chunk_));
-    launch_update_margin(ridx_[cur].p, leaf_work_.p, leaf_bound, field(c, &PlanCounts::n_leaf),
-                         margin, stride, s);
-    if (positions)
-      launch_leaf_positions(ridx_[cur].p, leaf_work_.p, leaf_bound, field(c, &PlanCounts::n_leaf),
-                            positions, s);
+    if (d + 1 >= D) {  // no later count launch carries these leaves
+      const int32_t leaf_bound = int32_t(plan_leaf_capacity(nb, N, chunk_));
+      launch_update_margin(ridx_[cur].p, leaf_work_[cur].p, leaf_bound,
+                           field(c, &PlanCounts::n_leaf), margin, stride, s);
+      if (positions)
+        launch_leaf_positions(ridx_[cur].p, leaf_work_[cur].p, leaf_bound,
+                              field(c, &PlanCounts::n_leaf), positions, s);
+    }
+    nb_prev = nb;
     nb = split ? std::min(2 * nb, N) : 0;
   }
 

@@ -89,7 +89,7 @@ class Grower {
   DeviceBuffer<int64_t> pair_chunk_, work_left_, node_left_[2];
   DeviceBuffer<dp_split_record> splits_;
   DeviceBuffer<uint8_t> eval_scratch_;
-  DeviceBuffer<LeafWork> leaf_work_;
+  DeviceBuffer<LeafWork> leaf_work_[2];  // by level parity: applied one level later
   DeviceBuffer<NodeInfo> info_;
   DeviceBuffer<PlanCounts> counts_;
   PinnedBuffer readback_;  // per slot: PlanCounts, then NodeInfo[node_cap_]

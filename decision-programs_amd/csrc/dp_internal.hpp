@@ -259,6 +259,19 @@ void launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_node
                      const dp_train_param& param, void* scratch, dp_split_record* out,
                      hipStream_t s);
 
+// Margin (and optional leaf id) update of leaf chunks: margin[ridx[i] *
+// stride] += value, positions[ridx[i]] = leaf id; work count from n_dev when
+// set, else n_host (an upper bound for grid sizing either way).
+struct LeafPass {
+  const uint32_t* ridx = nullptr;
+  const LeafWork* work = nullptr;
+  const int32_t* n_dev = nullptr;
+  int32_t n_host = 0;
+  float* margin = nullptr;
+  int64_t stride = 1;
+  int32_t* positions = nullptr;
+};
+
 // Partition: counts, then scatter (which writes the left totals of the
 // expanding nodes into node_left).  cols: column-major copy of the bins
 // (launch_tiles_to_columns) or null to read the tiles.  node_left_zeroed: the
@@ -269,7 +282,8 @@ void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_lay
                       int32_t n_work, const int32_t* n_work_dev, const int64_t* seg_begin,
                       const dp_split_record* splits, const int32_t* node_first_work,
                       int32_t n_nodes, const int32_t* n_nodes_dev, int64_t* work_left,
-                      int64_t* node_left, bool node_left_zeroed, hipStream_t s);
+                      int64_t* node_left, bool node_left_zeroed, hipStream_t s,
+                      const LeafPass* leaves = nullptr);
 constexpr int64_t kPartChunk = 4096;
 
 void launch_update_margin(const uint32_t* ridx, const LeafWork* work, int32_t n_work,

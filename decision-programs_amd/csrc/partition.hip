@@ -42,16 +42,32 @@ __device__ __forceinline__ bool goes_left(const uint8_t* __restrict__ bins, int6
 
 __device__ __forceinline__ int popc64(unsigned long long m) { return __popcll(m); }
 
+// The margin (and leaf id) update of one leaf chunk.
+__device__ __forceinline__ void apply_leaf(const LeafPass& lp, const LeafWork& w) {
+  for (int64_t i = w.begin + threadIdx.x; i < w.end; i += blockDim.x) {
+    const uint32_t row = lp.ridx[i];
+    lp.margin[int64_t(row) * lp.stride] += w.value;
+    if (lp.positions) lp.positions[row] = w.pad;
+  }
+}
+
 // The partition kernels loop over their items (item = blockIdx.x + k * gridDim.x).
+// The count kernel also takes the previous level's leaf chunks as items
+// [n_work, n_work + n_leaves): their margin update rides in the same launch.
 template <bool COLS>
 __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
     const uint8_t* __restrict__ bins, int64_t n_rows, int tile_width, int missing_bin,
     const uint32_t* __restrict__ ridx, const PartWork* __restrict__ work, int32_t n_work_host,
     const int32_t* __restrict__ n_work_dev, const dp_split_record* __restrict__ splits,
-    int64_t* __restrict__ work_left) {
+    int64_t* __restrict__ work_left, LeafPass lp) {
   __shared__ int wave_count[kPartThreads / 64];
   const int32_t n_work = n_work_dev ? *n_work_dev : n_work_host;
-  for (int32_t item = blockIdx.x; item < n_work; item += gridDim.x) {
+  const int32_t n_leaves = lp.work ? (lp.n_dev ? *lp.n_dev : lp.n_host) : 0;
+  for (int32_t item = blockIdx.x; item < n_work + n_leaves; item += gridDim.x) {
+  if (item >= n_work) {  // uniform per workgroup; no barriers on this path
+    apply_leaf(lp, lp.work[item - n_work]);
+    continue;
+  }
   const PartWork w = work[item];
   const dp_split_record s = splits[w.node];
   if (!s.expand) {
@@ -197,17 +213,23 @@ void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_lay
                       int32_t n_work, const int32_t* n_work_dev, const int64_t* seg_begin,
                       const dp_split_record* splits, const int32_t* node_first_work,
                       int32_t n_nodes, const int32_t* n_nodes_dev, int64_t* work_left,
-                      int64_t* node_left, bool node_left_zeroed, hipStream_t s) {
+                      int64_t* node_left, bool node_left_zeroed, hipStream_t s,
+                      const LeafPass* leaves) {
   if (n_nodes <= 0) return;
   (void)n_nodes_dev;
   const int missing = layout.missing_bin;
+  const LeafPass lp = leaves ? *leaves : LeafPass{};
+  const int64_t items = int64_t(n_work) + (lp.work ? lp.n_host : 0);
+  const int gc = int(items < 2048 ? items : 2048);
   const int gw = n_work < 2048 ? n_work : 2048;
   const uint8_t* src = cols ? cols : bins;
   if (!node_left_zeroed) launch_fill_i64(node_left, n_nodes, 0, s);
-  if (n_work <= 0) return;
-  hipLaunchKernelGGL(cols ? part_count_kernel<true> : part_count_kernel<false>, dim3(gw),
+  if (items <= 0) return;
+  hipLaunchKernelGGL(cols ? part_count_kernel<true> : part_count_kernel<false>, dim3(gc),
                      dim3(kPartThreads), 0, s, src, layout.n_rows, layout.tile_width, missing,
-                     ridx_in, work, n_work, n_work_dev, splits, work_left);
+                     ridx_in, work, n_work, n_work_dev, splits, work_left, lp);
+  DP_HIP(hipGetLastError());
+  if (n_work <= 0) return;
   DP_HIP(hipGetLastError());
   hipLaunchKernelGGL(cols ? part_scatter_kernel<true> : part_scatter_kernel<false>, dim3(gw),
                      dim3(kPartThreads), 0, s, src, layout.n_rows, layout.tile_width, missing,
