@@ -593,7 +593,7 @@ void Booster::configure(DMatrix* d) {
   gpair_.resize(size_t(N) * n_groups_ * 2);
   exps_.resize(size_t(2 * n_groups_));
   sums_.resize(size_t(2 * n_groups_));
-  maxima_.resize(size_t(2 * n_groups_));
+  quant_scratch_.resize(quantise_scratch_bytes(N, n_groups_));
   std::vector<float> init(static_cast<size_t>(N) * n_groups_);
   for (int64_t r = 0; r < N; ++r)
     for (int32_t k = 0; k < n_groups_; ++k) {
@@ -624,9 +624,9 @@ void Booster::update_one_iter(int iter, DMatrix* d) {
                                                            : "labels must be finite");
     labels_checked_ = true;
   }
-  launch_gradients(objective_id_, margin_.p, d->labels.p, d->n_rows, n_groups_, grad_.p, hess_.p,
-                   stream_);
-  boost_from_gradients(d, grad_.p, hess_.p);
+  const bool maxima = launch_gradients(objective_id_, margin_.p, d->labels.p, d->n_rows,
+                                       n_groups_, grad_.p, hess_.p, quant_scratch_.p, stream_);
+  boost_from_gradients(d, grad_.p, hess_.p, maxima);
 }
 
 void Booster::train_one_iter(DMatrix* d, int iter, const float* grad, const float* hess,
@@ -639,14 +639,16 @@ void Booster::train_one_iter(DMatrix* d, int iter, const float* grad, const floa
   // Keep a copy so the parity hook can report the gradients of this round.
   DP_HIP(hipMemcpyAsync(grad_.p, grad, grad_.bytes(), hipMemcpyDeviceToDevice, stream_));
   DP_HIP(hipMemcpyAsync(hess_.p, hess, hess_.bytes(), hipMemcpyDeviceToDevice, stream_));
-  boost_from_gradients(d, grad_.p, hess_.p);
+  boost_from_gradients(d, grad_.p, hess_.p, false);
 }
 
-void Booster::boost_from_gradients(DMatrix* d, const float* grad, const float* hess) {
+void Booster::boost_from_gradients(DMatrix* d, const float* grad, const float* hess,
+                                   bool maxima_ready) {
   dp_workspace_s scratch;
   Quantized& q = d->quantize(tp_.max_bin, scratch, stream_);
   const int64_t N = d->n_rows;
-  launch_quantise(grad, hess, N, n_groups_, maxima_.p, exps_.p, gpair_.p, sums_.p, stream_);
+  launch_quantise(grad, hess, N, n_groups_, quant_scratch_.p, maxima_ready, exps_.p, gpair_.p,
+                  sums_.p, stream_);
   if (record_positions_) positions_.reserve(size_t(N));
   grower_->prepare(q, tp_, n_groups_, stream_);
   for (int32_t k = 0; k < n_groups_; ++k)

@@ -145,7 +145,8 @@ class Booster {
   std::string effective_objective() const;
   void upload_forest(int32_t tree_begin, int32_t tree_end);
   void configure(DMatrix* d);
-  void boost_from_gradients(DMatrix* d, const float* grad, const float* hess);
+  // maxima_ready: the gradient kernel already wrote the quantiser's maxima slots.
+  void boost_from_gradients(DMatrix* d, const float* grad, const float* hess, bool maxima_ready);
   std::map<std::string, std::string> params_;
   std::vector<DMatrix*> cache_;
   // configured state
@@ -162,7 +163,7 @@ class Booster {
   DeviceBuffer<float> margin_, grad_, hess_;
   DeviceBuffer<int32_t> gpair_, exps_;
   DeviceBuffer<int64_t> sums_;
-  DeviceBuffer<uint32_t> maxima_;
+  DeviceBuffer<uint8_t> quant_scratch_;  // quantiser reduction slots
   DeviceBuffer<int32_t> positions_;
   std::vector<int32_t> last_exps_;
   PinnedBuffer exps_host_;

@@ -498,7 +498,7 @@ int dp_objective_gradients(int32_t objective, const float* margin, const float* 
     dp::need(n_classes >= 1, "n_classes must be positive");
     dp::need(objective != DP_OBJ_SOFTPROB || n_classes >= 2, "softprob needs 2+ classes");
     dp::need(objective == DP_OBJ_SOFTPROB || n_classes == 1, "single-output objective");
-    dp::launch_gradients(objective, margin, label, n_rows, n_classes, grad, hess,
+    dp::launch_gradients(objective, margin, label, n_rows, n_classes, grad, hess, nullptr,
                          as_stream(stream));
   });
 }
@@ -508,10 +508,12 @@ int dp_quantise_gradients(dp_workspace ws, const float* grad, const float* hess,
                           void* stream) {
   return guarded([&] {
     dp::need(ws && grad && hess && exps && gpair && sums, "null argument");
+    dp::need(n_rows >= 1 && n_classes >= 1, "empty gradients");
     ws->begin();
-    ws->reserve_scratch(sizeof(uint32_t) * 2 * size_t(n_classes) + 256);
-    uint32_t* maxima = ws->take<uint32_t>(2 * size_t(n_classes));
-    dp::launch_quantise(grad, hess, n_rows, n_classes, maxima, exps, gpair, sums,
+    const size_t bytes = dp::quantise_scratch_bytes(n_rows, n_classes);
+    ws->reserve_scratch(bytes + 256);
+    void* scratch = ws->take<uint8_t>(bytes);
+    dp::launch_quantise(grad, hess, n_rows, n_classes, scratch, false, exps, gpair, sums,
                         as_stream(stream));
     ws->commit(as_stream(stream));
   });

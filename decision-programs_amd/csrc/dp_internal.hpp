@@ -352,14 +352,20 @@ inline int64_t plan_hist_items(int64_t nodes, int64_t n_rows, int32_t n_tiles) {
 }
 constexpr int64_t kLeafChunk = 16384;  // margin-update items of the operator API
 
-void launch_gradients(int32_t objective, const float* margin, const float* label,
+// Objective gradients.  With quant_scratch (quantise_scratch_bytes) and one
+// output, the per-workgroup maxima the quantiser needs are written too and
+// true is returned (pass maxima_ready to launch_quantise).
+bool launch_gradients(int32_t objective, const float* margin, const float* label,
                       int64_t n_rows, int32_t n_classes, float* grad, float* hess,
-                      hipStream_t s);
-// maxima: uint32 [n_classes][2] scratch; exps int32 [n_classes][2];
-// gpair int32 [n_classes][n_rows][2]; sums int64 [n_classes][2].
+                      void* quant_scratch, hipStream_t s);
+// Quantiser: exps int32 [n_classes][2]; gpair int32 [n_classes][n_rows][2];
+// sums int64 [n_classes][2]; scratch holds quantise_scratch_bytes.
+constexpr int kQuantBlocks = 512;  // workgroups (and reduction slots) per class
+int quantise_blocks(int64_t n_rows);
+size_t quantise_scratch_bytes(int64_t n_rows, int32_t n_classes);
 void launch_quantise(const float* grad, const float* hess, int64_t n_rows, int32_t n_classes,
-                     uint32_t* maxima, int32_t* exps, int32_t* gpair, int64_t* sums,
-                     hipStream_t s);
+                     void* scratch, bool maxima_ready, int32_t* exps, int32_t* gpair,
+                     int64_t* sums, hipStream_t s);
 
 void launch_bin_values(const float* values, const dp_bin_layout& layout, const int32_t* cut_ptr,
                        const float* cut_values, uint8_t* bins, hipStream_t s);

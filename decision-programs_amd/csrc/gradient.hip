@@ -12,8 +12,11 @@
 //
 // Quantiser: per class, e = frexp exponent of max|x| (max|x| < 2^e), exp =
 // 30 - e, q = rint(x * 2^exp), so |q| <= 2^30 and the sum of any row set is an
-// exact int64.  The maxima are reduced with integer atomicMax on the bit
-// patterns of |x| (order-independent, hence deterministic).
+// exact int64.  Maxima (integer max of the bit patterns of |x|) and sums are
+// reduced through per-workgroup slots, never by same-address atomics (512
+// workgroups on one word serialise): each quantiser workgroup reduces the
+// maxima slots itself, and a finishing kernel reduces the sum slots.  Single-
+// output objectives produce the maxima slots in the gradient kernel.
 #include "dp_internal.hpp"
 
 #include <cmath>
@@ -42,18 +45,52 @@ __device__ __forceinline__ float dp_expf(float x) {
   return ldexpf(p, int(k));
 }
 
-__global__ void gradients_kernel(int objective, const float* __restrict__ margin,
-                                 const float* __restrict__ label, int64_t n_rows, int n_classes,
-                                 float* __restrict__ grad, float* __restrict__ hess) {
+constexpr int kQuantThreads = 256;
+
+// Max of two values over a 256-thread workgroup; thread 0 gets the result.
+__device__ __forceinline__ void block_max2(unsigned& a, unsigned& b) {
+  __shared__ unsigned part[2][kQuantThreads / 64];
+  for (int d = 32; d >= 1; d >>= 1) {
+    a = max(a, __shfl_xor(a, d, 64));
+    b = max(b, __shfl_xor(b, d, 64));
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    part[0][wave] = a;
+    part[1][wave] = b;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0)
+    for (int w = 1; w < kQuantThreads / 64; ++w) {
+      a = max(a, part[0][w]);
+      b = max(b, part[1][w]);
+    }
+  __syncthreads();
+}
+
+// MAXIMA: single-output objectives also write this workgroup's max|g|, max|h|
+// bit patterns to max_slots[2 * blockIdx.x ..].
+template <bool MAXIMA>
+__global__ __launch_bounds__(kQuantThreads) void gradients_kernel(
+    int objective, const float* __restrict__ margin, const float* __restrict__ label,
+    int64_t n_rows, int n_classes, float* __restrict__ grad, float* __restrict__ hess,
+    unsigned* __restrict__ max_slots) {
+  unsigned mg = 0, mh = 0;
   for (int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; r < n_rows;
        r += int64_t(blockDim.x) * gridDim.x) {
     if (objective == DP_OBJ_LOGISTIC) {
       const float p = 1.0f / (1.0f + dp_expf(-margin[r]));
-      grad[r] = p - label[r];
-      hess[r] = fmaxf(p * (1.0f - p), 1e-16f);
+      const float g = p - label[r], h = fmaxf(p * (1.0f - p), 1e-16f);
+      grad[r] = g;
+      hess[r] = h;
+      mg = max(mg, __float_as_uint(fabsf(g)));
+      mh = max(mh, __float_as_uint(fabsf(h)));
     } else if (objective == DP_OBJ_SQUARED) {
-      grad[r] = margin[r] - label[r];
+      const float g = margin[r] - label[r];
+      grad[r] = g;
       hess[r] = 1.0f;
+      mg = max(mg, __float_as_uint(fabsf(g)));
+      mh = max(mh, __float_as_uint(1.0f));
     } else {
       const float* m = margin + r * n_classes;
       float mx = m[0];
@@ -68,11 +105,19 @@ __global__ void gradients_kernel(int objective, const float* __restrict__ margin
       }
     }
   }
+  if constexpr (MAXIMA) {
+    block_max2(mg, mh);
+    if (threadIdx.x == 0) {
+      max_slots[2 * blockIdx.x] = mg;
+      max_slots[2 * blockIdx.x + 1] = mh;
+    }
+  }
 }
 
-__global__ void absmax_kernel(const float* __restrict__ grad, const float* __restrict__ hess,
-                              int64_t n_rows, int n_classes, unsigned* __restrict__ maxima) {
-  // blockIdx.y = class
+// Per-workgroup max|g|, max|h| of class blockIdx.y into its slots.
+__global__ __launch_bounds__(kQuantThreads) void absmax_kernel(
+    const float* __restrict__ grad, const float* __restrict__ hess, int64_t n_rows,
+    int n_classes, unsigned* __restrict__ max_slots) {
   const int k = blockIdx.y;
   unsigned mg = 0, mh = 0;
   for (int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; r < n_rows;
@@ -80,25 +125,11 @@ __global__ void absmax_kernel(const float* __restrict__ grad, const float* __res
     mg = max(mg, __float_as_uint(fabsf(grad[r * n_classes + k])));
     mh = max(mh, __float_as_uint(fabsf(hess[r * n_classes + k])));
   }
-  for (int d = 32; d >= 1; d >>= 1) {
-    mg = max(mg, __shfl_xor(mg, d, 64));
-    mh = max(mh, __shfl_xor(mh, d, 64));
-  }
-  // one atomic per workgroup: per-wave atomics on two addresses serialise
-  __shared__ unsigned wave_max[2][4];
-  const int wave = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) {
-    wave_max[0][wave] = mg;
-    wave_max[1][wave] = mh;
-  }
-  __syncthreads();
+  block_max2(mg, mh);
   if (threadIdx.x == 0) {
-    for (int w = 1; w < int(blockDim.x >> 6); ++w) {
-      mg = max(mg, wave_max[0][w]);
-      mh = max(mh, wave_max[1][w]);
-    }
-    atomicMax(&maxima[2 * k], mg);
-    atomicMax(&maxima[2 * k + 1], mh);
+    unsigned* slot = max_slots + (int64_t(k) * gridDim.x + blockIdx.x) * 2;
+    slot[0] = mg;
+    slot[1] = mh;
   }
 }
 
@@ -110,17 +141,32 @@ __device__ __forceinline__ int quant_exp(unsigned bits) {
   return kQuantBits - e;
 }
 
-__global__ void quantise_kernel(const float* __restrict__ grad, const float* __restrict__ hess,
-                                int64_t n_rows, int n_classes, const unsigned* __restrict__ maxima,
-                                int32_t* __restrict__ exps, int2* __restrict__ gpair,
-                                long long* __restrict__ sums) {
-  __shared__ long long wave_sum[2][4];
+// Reduces class blockIdx.y's maxima slots, quantises its rows and writes this
+// workgroup's sums to the sum slots.
+__global__ __launch_bounds__(kQuantThreads) void quantise_kernel(
+    const float* __restrict__ grad, const float* __restrict__ hess, int64_t n_rows,
+    int n_classes, const unsigned* __restrict__ max_slots, int32_t* __restrict__ exps,
+    int2* __restrict__ gpair, long long* __restrict__ sum_slots) {
+  __shared__ long long wave_sum[2][kQuantThreads / 64];
+  __shared__ int s_exp[2];
   const int k = blockIdx.y;
-  const int eg = quant_exp(maxima[2 * k]), eh = quant_exp(maxima[2 * k + 1]);
-  if (blockIdx.x == 0 && threadIdx.x == 0) {
-    exps[2 * k] = eg;
-    exps[2 * k + 1] = eh;
+  unsigned mg = 0, mh = 0;
+  const unsigned* slots = max_slots + int64_t(k) * gridDim.x * 2;
+  for (int b = threadIdx.x; b < int(gridDim.x); b += kQuantThreads) {
+    mg = max(mg, slots[2 * b]);
+    mh = max(mh, slots[2 * b + 1]);
   }
+  block_max2(mg, mh);
+  if (threadIdx.x == 0) {
+    s_exp[0] = quant_exp(mg);
+    s_exp[1] = quant_exp(mh);
+    if (blockIdx.x == 0) {
+      exps[2 * k] = s_exp[0];
+      exps[2 * k + 1] = s_exp[1];
+    }
+  }
+  __syncthreads();
+  const int eg = s_exp[0], eh = s_exp[1];
   long long sg = 0, sh = 0;
   int2* out = gpair + int64_t(k) * n_rows;
   for (int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; r < n_rows;
@@ -143,12 +189,44 @@ __global__ void quantise_kernel(const float* __restrict__ grad, const float* __r
   __syncthreads();
   if (threadIdx.x == 0) {
     long long tg = 0, th = 0;
-    for (int w = 0; w < int(blockDim.x >> 6); ++w) {
+    for (int w = 0; w < kQuantThreads / 64; ++w) {
       tg += wave_sum[0][w];
       th += wave_sum[1][w];
     }
-    atomicAdd(reinterpret_cast<unsigned long long*>(&sums[2 * k]), (unsigned long long)tg);
-    atomicAdd(reinterpret_cast<unsigned long long*>(&sums[2 * k + 1]), (unsigned long long)th);
+    long long* slot = sum_slots + (int64_t(k) * gridDim.x + blockIdx.x) * 2;
+    slot[0] = tg;
+    slot[1] = th;
+  }
+}
+
+// One workgroup per class: sums[k] = the class's sum slots added up.
+__global__ __launch_bounds__(kQuantThreads) void finish_sums_kernel(
+    const long long* __restrict__ sum_slots, int blocks, long long* __restrict__ sums) {
+  __shared__ long long part[2][kQuantThreads / 64];
+  const int k = blockIdx.x;
+  long long sg = 0, sh = 0;
+  for (int b = threadIdx.x; b < blocks; b += kQuantThreads) {
+    sg += sum_slots[(int64_t(k) * blocks + b) * 2];
+    sh += sum_slots[(int64_t(k) * blocks + b) * 2 + 1];
+  }
+  for (int d = 32; d >= 1; d >>= 1) {
+    sg += __shfl_xor(sg, d, 64);
+    sh += __shfl_xor(sh, d, 64);
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    part[0][wave] = sg;
+    part[1][wave] = sh;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    long long tg = 0, th = 0;
+    for (int w = 0; w < kQuantThreads / 64; ++w) {
+      tg += part[0][w];
+      th += part[1][w];
+    }
+    sums[2 * k] = tg;
+    sums[2 * k + 1] = th;
   }
 }
 
@@ -182,32 +260,55 @@ void launch_check_labels(const float* label, int64_t n, int32_t objective, int32
   DP_HIP(hipGetLastError());
 }
 
-void launch_gradients(int32_t objective, const float* margin, const float* label,
+int quantise_blocks(int64_t n_rows) { return grid_for(n_rows, kQuantThreads, kQuantBlocks); }
+
+size_t quantise_scratch_bytes(int64_t n_rows, int32_t n_classes) {
+  const size_t slots = size_t(n_classes) * size_t(quantise_blocks(n_rows));
+  return slots * 2 * sizeof(uint32_t) + 256 + slots * 2 * sizeof(int64_t);
+}
+
+bool launch_gradients(int32_t objective, const float* margin, const float* label,
                       int64_t n_rows, int32_t n_classes, float* grad, float* hess,
-                      hipStream_t s) {
-  if (n_rows <= 0) return;
+                      void* quant_scratch, hipStream_t s) {
+  if (n_rows <= 0) return false;
   need(objective == DP_OBJ_LOGISTIC || objective == DP_OBJ_SOFTPROB ||
            objective == DP_OBJ_SQUARED,
        "unknown objective id");
-  hipLaunchKernelGGL(gradients_kernel, dim3(grid_for(n_rows, 256, 8192)), dim3(256), 0, s,
-                     objective, margin, label, n_rows, n_classes, grad, hess);
+  if (quant_scratch && n_classes == 1) {
+    hipLaunchKernelGGL(gradients_kernel<true>, dim3(quantise_blocks(n_rows)), dim3(kQuantThreads),
+                       0, s, objective, margin, label, n_rows, n_classes, grad, hess,
+                       static_cast<unsigned*>(quant_scratch));
+    DP_HIP(hipGetLastError());
+    return true;
+  }
+  hipLaunchKernelGGL(gradients_kernel<false>, dim3(grid_for(n_rows, kQuantThreads, 8192)),
+                     dim3(kQuantThreads), 0, s, objective, margin, label, n_rows, n_classes, grad,
+                     hess, nullptr);
   DP_HIP(hipGetLastError());
+  return false;
 }
 
 void launch_quantise(const float* grad, const float* hess, int64_t n_rows, int32_t n_classes,
-                     uint32_t* maxima, int32_t* exps, int32_t* gpair, int64_t* sums,
-                     hipStream_t s) {
+                     void* scratch, bool maxima_ready, int32_t* exps, int32_t* gpair,
+                     int64_t* sums, hipStream_t s) {
   need(n_classes >= 1 && n_classes <= 65535, "class count out of range");
-  launch_fill_u8(reinterpret_cast<uint8_t*>(maxima), int64_t(sizeof(uint32_t)) * 2 * n_classes, 0, s);
-  launch_fill_i64(sums, 2 * int64_t(n_classes), 0, s);
-  // A few hundred workgroups cover HBM; more only adds atomics on the totals.
-  const int blocks = grid_for(n_rows, 256, 512);
-  hipLaunchKernelGGL(absmax_kernel, dim3(blocks, n_classes), dim3(256), 0, s, grad, hess, n_rows,
-                     n_classes, reinterpret_cast<unsigned*>(maxima));
+  need(n_rows >= 1, "quantiser needs at least one row");
+  const int blocks = quantise_blocks(n_rows);
+  const size_t slots = size_t(n_classes) * size_t(blocks);
+  auto* max_slots = static_cast<unsigned*>(scratch);
+  auto* sum_slots = reinterpret_cast<long long*>(static_cast<uint8_t*>(scratch) +
+                                                 ((slots * 2 * sizeof(uint32_t) + 255) & ~size_t(255)));
+  if (!maxima_ready) {
+    hipLaunchKernelGGL(absmax_kernel, dim3(blocks, n_classes), dim3(kQuantThreads), 0, s, grad,
+                       hess, n_rows, n_classes, max_slots);
+    DP_HIP(hipGetLastError());
+  }
+  hipLaunchKernelGGL(quantise_kernel, dim3(blocks, n_classes), dim3(kQuantThreads), 0, s, grad,
+                     hess, n_rows, n_classes, max_slots, exps, reinterpret_cast<int2*>(gpair),
+                     sum_slots);
   DP_HIP(hipGetLastError());
-  hipLaunchKernelGGL(quantise_kernel, dim3(blocks, n_classes), dim3(256), 0, s, grad, hess,
-                     n_rows, n_classes, reinterpret_cast<const unsigned*>(maxima), exps,
-                     reinterpret_cast<int2*>(gpair), reinterpret_cast<long long*>(sums));
+  hipLaunchKernelGGL(finish_sums_kernel, dim3(n_classes), dim3(kQuantThreads), 0, s, sum_slots,
+                     blocks, reinterpret_cast<long long*>(sums));
   DP_HIP(hipGetLastError());
 }
 
