@@ -401,7 +401,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     a.partial_capacity = int32_t(hist_partial_capacity(T));
     a.part_capacity = int32_t(part_work_[nxt].n);
     a.leaf_capacity = int32_t(leaf_work_[cur].n);
-    launch_plan_level(a, s);
+    launch_plan_level(a, nb, s);
     if (d + 1 >= D) {  // no later count launch carries these leaves
       const int32_t leaf_bound = int32_t(plan_leaf_capacity(nb, N, chunk_));
       launch_update_margin(ridx_[cur].p, leaf_work_[cur].p, leaf_bound,

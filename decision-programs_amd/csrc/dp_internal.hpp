@@ -320,7 +320,8 @@ struct PlanArgs {
   int32_t info_capacity, level_capacity;
   int32_t hist_capacity, partial_capacity, part_capacity, leaf_capacity;
 };
-void launch_plan_level(const PlanArgs& a, hipStream_t s);
+// level_bound: an upper bound of the level's node count (selects the planner).
+void launch_plan_level(const PlanArgs& a, int64_t level_bound, hipStream_t s);
 // counts->n_level = 1, n_nodes = 1, ...; cur[0] = root {0, n_rows, g, h, 0, -1}
 // with (g, h) = root_sums[0..1]; sums[0..1] = (g, h), seg_begin[0] = 0,
 // node_left[0] = 0; root partition work over [0, n_rows).

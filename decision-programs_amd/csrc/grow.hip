@@ -345,6 +345,256 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
   }
 }
 
+// The planner for levels of at most kPlanThreads nodes: thread i owns node i
+// for the whole level, keeps the node and its children in registers, and
+// leaves in LDS what the per-item loops look up, so after the first loads no
+// section reads back what another section wrote to global memory.  Its work
+// lists are identical to plan_level_kernel's.
+__global__ __launch_bounds__(kPlanThreads) void plan_small_kernel(PlanArgs a) {
+  __shared__ int64_t scan[kPlanThreads];
+  __shared__ int64_t s_off[kPlanThreads + 1];  // per-node offsets of the section's items
+  __shared__ int64_t s_aux[kPlanThreads];      // C: partial chunk starts; D: left chunk counts
+  __shared__ int64_t s_begin[kPlanThreads];
+  __shared__ int64_t s_end[kPlanThreads];
+  __shared__ int64_t s_end2[kPlanThreads];
+  __shared__ int32_t s_id[kPlanThreads];
+  __shared__ float s_val[kPlanThreads];
+  __shared__ int32_t s_error;
+  const int tid = threadIdx.x;
+  const int32_t n = a.counts->n_level;  // <= kPlanThreads (the host bound)
+  const int32_t n_nodes0 = a.counts->n_nodes;
+  const double ug = ldexp(1.0, -a.exps[0]), uh = ldexp(1.0, -a.exps[1]);
+  __syncthreads();  // every thread has read the counts before any is rewritten
+  if (n > kPlanThreads) {  // the host chose this kernel on a wrong bound
+    if (tid == 0) {
+      PlanCounts* c = a.counts;
+      c->n_level = c->n_hist = c->n_reduce = c->n_part = c->n_leaf = 0;
+      if (!c->error) c->error = 6;
+    }
+    return;
+  }
+  if (tid == 0) s_error = 0;
+  __syncthreads();
+
+  // ---- A: numbering, node records, next-level nodes ----------------------
+  const bool live = tid < n;
+  LevelNode nd{};
+  dp_split_record sp{};
+  int64_t nl = 0;
+  bool e = false;
+  if (live) {
+    nd = a.cur[tid];
+    if (a.splits) {
+      sp = a.splits[tid];
+      if (sp.expand) {
+        nl = a.node_left[tid];
+        e = nl > 0 && nl < nd.end - nd.begin;
+        if (!e) s_error = 1;
+      }
+    }
+  }
+  int64_t total;
+  const int64_t rank = block_scan(e ? 1 : 0, scan, &total);
+  const int32_t n_expand = int32_t(total);
+  const int32_t n_next = 2 * n_expand;
+  LevelNode L{}, R{};
+  float leaf_value = 0.0f;
+  if (live) {
+    NodeInfo info{};
+    info.g = nd.g;
+    info.h = nd.h;
+    info.begin = nd.begin;
+    info.end = nd.end;
+    info.parity = a.depth & 1;
+    const double G = double(nd.g) * ug, H = double(nd.h) * uh;
+    const double w = plan_weight(a, G, H);
+    info.base_weight = float(w);
+    info.sum_hess = float(H);
+    info.bin = -1;
+    if (e) {
+      const int32_t left = n_nodes0 + int32_t(2 * rank);
+      info.left = left;
+      info.feature = sp.feature;
+      info.bin = sp.bin;
+      info.default_left = sp.default_left;
+      info.loss_chg = sp.loss_chg;
+      L = LevelNode{nd.begin, nd.begin + nl, sp.gl, sp.hl, left, tid};
+      R = LevelNode{nd.begin + nl, nd.end, nd.g - sp.gl, nd.h - sp.hl, left + 1, tid};
+      const int64_t slot = 2 * rank;
+      if (left + 1 < a.info_capacity && slot + 1 < a.level_capacity) {
+        a.next[slot] = L;
+        a.next[slot + 1] = R;
+        a.next_sums[2 * slot] = L.g;
+        a.next_sums[2 * slot + 1] = L.h;
+        a.next_sums[2 * slot + 2] = R.g;
+        a.next_sums[2 * slot + 3] = R.h;
+        a.next_seg_begin[slot] = L.begin;
+        a.next_seg_begin[slot + 1] = R.begin;
+        a.next_node_left[slot] = 0;
+        a.next_node_left[slot + 1] = 0;
+      } else {
+        s_error = 2;
+      }
+    } else {
+      info.left = -1;
+      leaf_value = float(w * a.eta);
+      info.leaf_value = leaf_value;
+    }
+    if (nd.nid >= 0 && nd.nid < a.info_capacity) a.info[nd.nid] = info;
+    else s_error = 2;
+  }
+  __syncthreads();
+  if (s_error) {  // inconsistent level or capacity exceeded: stop this tree
+    if (tid == 0) {
+      PlanCounts* c = a.counts;
+      c->n_level = c->n_hist = c->n_reduce = c->n_part = c->n_leaf = 0;
+      if (!c->error) c->error = s_error;
+    }
+    return;
+  }
+
+  // ---- B: leaf work of this level -----------------------------------------
+  const int64_t rows = nd.end - nd.begin;
+  const int64_t lc = (live && !e) ? (rows + a.leaf_chunk - 1) / a.leaf_chunk : 0;
+  const int64_t loff = block_scan(lc, scan, &total);
+  int64_t n_leaf = total;
+  if (live) {
+    s_off[tid] = loff;
+    s_begin[tid] = nd.begin;
+    s_end[tid] = nd.end;
+    s_id[tid] = nd.nid;
+    s_val[tid] = leaf_value;
+  }
+  if (tid == 0) s_off[n] = n_leaf;
+  __syncthreads();
+  if (n_leaf > a.leaf_capacity) {
+    if (tid == 0) s_error = 3;
+    n_leaf = 0;
+  }
+  for (int64_t k = tid; k < n_leaf; k += kPlanThreads) {
+    const int32_t j = owner(s_off, n, k);
+    const int64_t b = s_begin[j] + (k - s_off[j]) * a.leaf_chunk;
+    a.leaf_work[k] = LeafWork{s_val[j], s_id[j], b,
+                              b + a.leaf_chunk < s_end[j] ? b + a.leaf_chunk : s_end[j]};
+  }
+  __syncthreads();  // the LDS arrays are reused below
+
+  // ---- C: histogram work and reduce jobs of the next level ----------------
+  const bool next_hist = n_next > 0 && a.depth + 1 < a.max_depth;
+  int64_t n_hist = 0;
+  int32_t n_reduce = 0;
+  const int64_t lrows = L.end - L.begin, rrows = R.end - R.begin;
+  if (next_hist) {
+    const int32_t T = a.n_tiles;
+    const bool right_small = rrows < lrows;
+    const int64_t srows = e ? (right_small ? rrows : lrows) : 0;
+    (void)block_scan(srows, scan, &total);
+    const int64_t chunk = hist_chunk(total, T);
+    const int64_t nc = (srows + chunk - 1) / chunk;
+    const int64_t cs = block_scan(nc, scan, &total);
+    const int64_t C = total;
+    const int64_t ps = block_scan(nc >= 2 ? nc : 0, scan, &total);
+    const int64_t P = total;
+    if (live) {
+      s_off[tid] = cs;
+      s_aux[tid] = ps;
+      s_begin[tid] = right_small ? R.begin : L.begin;
+      s_end[tid] = right_small ? R.end : L.end;
+      s_id[tid] = int32_t(2 * rank) + (right_small ? 1 : 0);
+    }
+    if (tid == 0) s_off[n] = C;
+    __syncthreads();
+    const int64_t padded = (C + 7) / 8 * 8;
+    n_hist = padded * T;
+    if (n_hist > a.hist_capacity || P * T > a.partial_capacity) {
+      if (tid == 0) s_error = 4;
+      n_hist = 0;
+    } else {
+      for (int64_t c = tid; c < padded; c += kPlanThreads) {
+        HistWork item{0, 0, 0, 0, -1, 0};
+        int64_t p = -1;
+        if (c < C) {
+          const int32_t j = owner(s_off, n, c);
+          const int64_t k = c - s_off[j];
+          const int64_t b = s_begin[j] + k * chunk;
+          item = HistWork{s_id[j], 0, b, b + chunk < s_end[j] ? b + chunk : s_end[j], -1, 0};
+          if (s_off[j + 1] - s_off[j] >= 2) p = (s_aux[j] + k) * T;
+        }
+        for (int32_t t = 0; t < T; ++t) {
+          item.tile = t;
+          item.partial = p < 0 ? -1 : int32_t(p + t);
+          a.hist_work[((c / 8) * T + t) * 8 + (c % 8)] = item;
+        }
+      }
+      if (e)
+        a.reduce_jobs[rank] = HistReduce{int32_t(2 * rank) + (right_small ? 1 : 0),
+                                         int32_t(2 * rank) + (right_small ? 0 : 1),
+                                         int64_t(tid) * a.hist_elems,
+                                         nc >= 2 ? int32_t(ps) : -1, int32_t(nc)};
+      n_reduce = n_expand;
+    }
+    __syncthreads();  // the LDS arrays are reused below
+  }
+
+  // ---- D: partition work of the next level ----------------------------------
+  int64_t n_part = 0;
+  if (next_hist) {
+    const int64_t cl = e ? (lrows + a.part_chunk - 1) / a.part_chunk : 0;
+    const int64_t cr = e ? (rrows + a.part_chunk - 1) / a.part_chunk : 0;
+    const int64_t po = block_scan(cl + cr, scan, &total);
+    n_part = total;
+    if (e) {
+      a.part_first[2 * rank] = int32_t(po);
+      a.part_first[2 * rank + 1] = int32_t(po + cl);
+    }
+    if (live) {
+      s_off[tid] = po;
+      s_aux[tid] = cl;
+      s_begin[tid] = L.begin;
+      s_end[tid] = L.end;
+      s_end2[tid] = R.end;
+      s_id[tid] = int32_t(2 * rank);
+    }
+    if (tid == 0) {
+      s_off[n] = n_part;
+      a.part_first[n_next] = int32_t(n_part);
+    }
+    __syncthreads();
+    if (n_part > a.part_capacity) {
+      if (tid == 0) s_error = 5;
+      n_part = 0;
+    }
+    for (int64_t k = tid; k < n_part; k += kPlanThreads) {
+      const int32_t j = owner(s_off, n, k);
+      int64_t kk = k - s_off[j];
+      int32_t node = s_id[j];
+      int64_t b, end;
+      if (kk < s_aux[j]) {
+        b = s_begin[j] + kk * a.part_chunk;
+        end = s_end[j];
+      } else {
+        kk -= s_aux[j];
+        node += 1;
+        b = s_end[j] + kk * a.part_chunk;
+        end = s_end2[j];
+      }
+      a.part_work[k] = PartWork{node, 0, b, b + a.part_chunk < end ? b + a.part_chunk : end};
+    }
+  }
+
+  __syncthreads();
+  if (tid == 0) {
+    PlanCounts* c = a.counts;
+    c->n_level = n_next;
+    c->n_nodes = n_nodes0 + n_next;
+    c->n_hist = int32_t(n_hist);
+    c->n_reduce = n_reduce;
+    c->n_part = int32_t(n_part);
+    c->n_leaf = int32_t(n_leaf);
+    if (s_error && !c->error) c->error = s_error;
+  }
+}
+
 __global__ void plan_root_kernel(LevelNode* cur, int64_t* sums, int64_t* seg_begin,
                                  PartWork* part_work, int32_t* part_first, int64_t* node_left,
                                  PlanCounts* counts, int64_t n_rows, const int64_t* root_sums,
@@ -374,8 +624,11 @@ __global__ void plan_root_kernel(LevelNode* cur, int64_t* sums, int64_t* seg_beg
 
 }  // namespace
 
-void launch_plan_level(const PlanArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(plan_level_kernel, dim3(1), dim3(kPlanThreads), 0, s, a);
+void launch_plan_level(const PlanArgs& a, int64_t level_bound, hipStream_t s) {
+  if (level_bound <= kPlanThreads)
+    hipLaunchKernelGGL(plan_small_kernel, dim3(1), dim3(kPlanThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL(plan_level_kernel, dim3(1), dim3(kPlanThreads), 0, s, a);
   DP_HIP(hipGetLastError());
 }
 
