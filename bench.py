@@ -212,6 +212,7 @@ def trees_leg(torch, dp, ops, name, rows=None, warm_rounds=2):
     t0 = time.perf_counter()
     for r in range(rounds):
         bst.boost(dtrain, r, g1, h1) if injected else bst.update(dtrain, r)
+    assert bst.num_boosted_rounds() == rounds  # collects the last round's trees
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
     trees = bst.num_trees()

@@ -17,6 +17,7 @@
 #include <cmath>
 #include <charconv>
 #include <cstdlib>
+#include <cstring>
 #include <limits>
 
 #include "json.hpp"
@@ -281,9 +282,10 @@ void Grower::prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, h
       cap += level_bound(d, N);
     }
     node_cap_ = std::min(cap, 2 * N - 1);
-    info_.reserve(size_t(node_cap_));
     slot_bytes_ = (sizeof(PlanCounts) + sizeof(NodeInfo) * size_t(node_cap_) + 255) & ~size_t(255);
-    readback_.reserve(slot_bytes_ * size_t(n_slots));
+    slots_.reserve(slot_bytes_ * size_t(n_slots));
+    readback_.reserve(2 * slot_bytes_ * size_t(n_slots));
+    readback_slots_ = n_slots;
   } else {
     ensure_level(q, 1, 0, D);
     info_.reserve(3);
@@ -301,7 +303,11 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
   const int32_t F = L.n_features, B = q.bin_stride, T = L.n_tiles, D = p.max_depth;
   const int64_t S = int64_t(F) * B * 2;  // int64 values per node histogram
   const dp_train_param dtp{p.eta, p.lambda, p.alpha, p.gamma, p.min_child_weight, p.max_depth};
-  PlanCounts* c = counts_.p;
+  // Eager trees keep their counters and node records in their own slot, so
+  // the slots of a round come back to the host in one copy.
+  uint8_t* slot_dev = eager_ ? slots_.p + slot_bytes_ * size_t(slot) : nullptr;
+  PlanCounts* c = eager_ ? reinterpret_cast<PlanCounts*>(slot_dev) : counts_.p;
+  NodeInfo* info = eager_ ? reinterpret_cast<NodeInfo*>(slot_dev + sizeof(PlanCounts)) : info_.p;
   auto* host_counts = reinterpret_cast<PlanCounts*>(level_count_.p);
 
   launch_iota_u32(ridx_[0].p, N, s);
@@ -376,7 +382,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     a.next = level_[nxt].p;
     a.next_sums = sums_[nxt].p;
     a.next_seg_begin = seg_begin_[nxt].p;
-    a.info = info_.p;
+    a.info = eager_ ? info : info_.p;
     a.hist_work = hist_work_[nxt].p;
     a.reduce_jobs = reduce_jobs_[nxt].p;
     a.part_work = part_work_[nxt].p;
@@ -395,7 +401,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     a.lambda = double(p.lambda);
     a.alpha = double(p.alpha);
     a.mcw = double(p.min_child_weight);
-    a.info_capacity = int32_t(info_.n);
+    a.info_capacity = int32_t(eager_ ? node_cap_ : int64_t(info_.n));
     a.level_capacity = int32_t(level_[nxt].n);
     a.hist_capacity = int32_t(hist_work_[nxt].n);
     a.partial_capacity = int32_t(hist_partial_capacity(T));
@@ -414,12 +420,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     nb = split ? std::min(2 * nb, N) : 0;
   }
 
-  if (eager_) {
-    uint8_t* dst = readback_.p + slot_bytes_ * size_t(slot);
-    DP_HIP(hipMemcpyAsync(dst, c, sizeof(PlanCounts), hipMemcpyDeviceToHost, s));
-    DP_HIP(hipMemcpyAsync(dst + sizeof(PlanCounts), info_.p, sizeof(NodeInfo) * size_t(node_cap_),
-                          hipMemcpyDeviceToHost, s));
-  } else {
+  if (!eager_) {
     DP_HIP(hipMemcpyAsync(host_counts, c, sizeof(PlanCounts), hipMemcpyDeviceToHost, s));
     DP_HIP(hipStreamSynchronize(s));
     spill_counts_[size_t(slot)] = *host_counts;
@@ -430,11 +431,45 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
   }
 }
 
-void Grower::collect(const Quantized& q, int32_t slot, Tree& tree) const {
+void Grower::readback(int32_t n_slots, int32_t buffer, hipStream_t s) {
+  if (!eager_ || n_slots <= 0) return;
+  need(n_slots <= readback_slots_ && (buffer == 0 || buffer == 1),
+       "readback beyond the prepared slots");
+  DP_HIP(hipMemcpyAsync(readback_.p + size_t(buffer) * slot_bytes_ * size_t(readback_slots_),
+                        slots_.p, slot_bytes_ * size_t(n_slots), hipMemcpyDeviceToHost, s));
+}
+
+uint64_t Grower::signature() const {
+  uint64_t h = 1469598103934665603ull;  // FNV-1a over the buffers' addresses and sizes
+  auto mix = [&h](uint64_t v) {
+    for (int i = 0; i < 8; ++i) {
+      h ^= (v >> (8 * i)) & 0xffu;
+      h *= 1099511628211ull;
+    }
+  };
+  auto buf = [&mix](const auto& b) {
+    mix(reinterpret_cast<uint64_t>(b.p));
+    mix(uint64_t(b.n));
+  };
+  for (int i = 0; i < 2; ++i) {
+    buf(ridx_[i]); buf(hist_[i]); buf(level_[i]); buf(sums_[i]); buf(seg_begin_[i]);
+    buf(hist_work_[i]); buf(reduce_jobs_[i]); buf(part_work_[i]); buf(part_first_[i]);
+    buf(node_left_[i]); buf(leaf_work_[i]);
+  }
+  buf(root_work_); buf(root_job_); buf(partial_); buf(pair_chunk_); buf(work_left_);
+  buf(splits_); buf(eval_scratch_); buf(info_); buf(counts_); buf(slots_);
+  mix(uint64_t(eager_)); mix(uint64_t(node_cap_)); mix(uint64_t(chunk_));
+  mix(uint64_t(slot_bytes_)); mix(uint64_t(root_rows_)); mix(uint64_t(root_tiles_));
+  mix(uint64_t(root_items_));
+  return h;
+}
+
+void Grower::collect(const Quantized& q, int32_t slot, int32_t buffer, Tree& tree) const {
   const PlanCounts* c;
   const NodeInfo* info;
   if (eager_) {
-    const uint8_t* src = readback_.p + slot_bytes_ * size_t(slot);
+    const uint8_t* src =
+        readback_.p + slot_bytes_ * (size_t(buffer) * size_t(readback_slots_) + size_t(slot));
     c = reinterpret_cast<const PlanCounts*>(src);
     info = reinterpret_cast<const NodeInfo*>(src + sizeof(PlanCounts));
   } else {
@@ -479,11 +514,17 @@ void Grower::collect(const Quantized& q, int32_t slot, Tree& tree) const {
 Booster::Booster(std::vector<DMatrix*> cache) : cache_(std::move(cache)) {}
 
 Booster::~Booster() {
+  if (stream_) (void)hipStreamSynchronize(stream_);
+  for (hipEvent_t& e : round_done_)
+    if (e) (void)hipEventDestroy(e);
+  clear_graphs();
   grower_.reset();
-  if (stream_) {
-    (void)hipStreamSynchronize(stream_);
-    (void)hipStreamDestroy(stream_);
-  }
+  if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+void Booster::clear_graphs() {
+  for (auto& g : graphs_) (void)hipGraphExecDestroy(g.second);
+  graphs_.clear();
 }
 
 void Booster::set_param(const std::string& key, const std::string& value) {
@@ -492,7 +533,8 @@ void Booster::set_param(const std::string& key, const std::string& value) {
       "eta", "learning_rate", "lambda", "reg_lambda", "alpha", "reg_alpha", "gamma",
       "min_split_loss", "min_child_weight", "subsample", "colsample_bytree", "colsample_bylevel",
       "colsample_bynode", "base_score", "boost_from_average", "seed", "seed_per_iteration",
-      "nthread", "verbosity", "validate_parameters", "grow_policy", "dp_record_positions"};
+      "nthread", "verbosity", "validate_parameters", "grow_policy", "dp_record_positions",
+      "dp_graphs"};
   bool ok = false;
   for (const char* k : known) ok = ok || key == k;
   need(ok, "unsupported parameter: " + key);
@@ -510,6 +552,7 @@ void Booster::set_param(const std::string& key, const std::string& value) {
   }
   params_[key] = value;
   if (key == "dp_record_positions") record_positions_ = parse_int(key, value) != 0;
+  if (key == "dp_graphs") use_graphs_ = parse_int(key, value) != 0;
 }
 
 void Booster::configure(DMatrix* d) {
@@ -624,9 +667,7 @@ void Booster::update_one_iter(int iter, DMatrix* d) {
                                                            : "labels must be finite");
     labels_checked_ = true;
   }
-  const bool maxima = launch_gradients(objective_id_, margin_.p, d->labels.p, d->n_rows,
-                                       n_groups_, grad_.p, hess_.p, quant_scratch_.p, stream_);
-  boost_from_gradients(d, grad_.p, hess_.p, maxima);
+  run_round(d, true);
 }
 
 void Booster::train_one_iter(DMatrix* d, int iter, const float* grad, const float* hess,
@@ -639,44 +680,145 @@ void Booster::train_one_iter(DMatrix* d, int iter, const float* grad, const floa
   // Keep a copy so the parity hook can report the gradients of this round.
   DP_HIP(hipMemcpyAsync(grad_.p, grad, grad_.bytes(), hipMemcpyDeviceToDevice, stream_));
   DP_HIP(hipMemcpyAsync(hess_.p, hess, hess_.bytes(), hipMemcpyDeviceToDevice, stream_));
-  boost_from_gradients(d, grad_.p, hess_.p, false);
+  run_round(d, false);
 }
 
-void Booster::boost_from_gradients(DMatrix* d, const float* grad, const float* hess,
-                                   bool maxima_ready) {
-  dp_workspace_s scratch;
-  Quantized& q = d->quantize(tp_.max_bin, scratch, stream_);
+void Booster::enqueue(const std::vector<uint64_t>& key, bool capturable,
+                      const std::function<void()>& body) {
+  if (!use_graphs_ || !capturable) {
+    body();
+    return;
+  }
+  for (auto& g : graphs_)
+    if (g.first == key) {
+      DP_HIP(hipGraphLaunch(g.second, stream_));
+      return;
+    }
+  // Capture: nothing in body() allocates, synchronises or reads device
+  // memory on the host, so the captured launches are exactly the direct ones.
+  hipGraph_t graph = nullptr;
+  DP_HIP(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+  try {
+    body();
+  } catch (...) {
+    if (hipStreamEndCapture(stream_, &graph) == hipSuccess && graph) (void)hipGraphDestroy(graph);
+    throw;
+  }
+  DP_HIP(hipStreamEndCapture(stream_, &graph));
+  hipGraphExec_t exec = nullptr;
+  const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  DP_HIP(e);
+  constexpr size_t kMaxGraphs = 4;
+  if (graphs_.size() >= kMaxGraphs) {
+    DP_HIP(hipStreamSynchronize(stream_));  // the oldest may still be running
+    (void)hipGraphExecDestroy(graphs_.front().second);
+    graphs_.erase(graphs_.begin());
+  }
+  graphs_.emplace_back(key, exec);
+  DP_HIP(hipGraphLaunch(exec, stream_));
+}
+
+void Booster::run_round(DMatrix* d, bool with_gradients) {
   const int64_t N = d->n_rows;
-  launch_quantise(grad, hess, N, n_groups_, quant_scratch_.p, maxima_ready, exps_.p, gpair_.p,
-                  sums_.p, stream_);
+  // Host inputs that size buffers: when they change, the round in flight is
+  // collected first, so no buffer it uses moves under it.
+  std::vector<uint64_t> inputs = {reinterpret_cast<uint64_t>(d), uint64_t(record_positions_),
+                                  uint64_t(n_groups_)};
+  auto words = [](std::vector<uint64_t>& v, const void* p, size_t n) {
+    for (size_t i = 0; i < n; i += 8) {
+      uint64_t w = 0;
+      std::memcpy(&w, static_cast<const uint8_t*>(p) + i, std::min<size_t>(8, n - i));
+      v.push_back(w);
+    }
+  };
+  words(inputs, &tp_, sizeof tp_);
+  if (inputs != last_round_inputs_) flush();
+  Quantized* qp;
+  {
+    dp_workspace_s scratch;
+    qp = &d->quantize(tp_.max_bin, scratch, stream_);
+  }
+  Quantized& q = *qp;
   if (record_positions_) positions_.reserve(size_t(N));
   grower_->prepare(q, tp_, n_groups_, stream_);
-  for (int32_t k = 0; k < n_groups_; ++k)
-    grower_->grow(q, gpair_.p + int64_t(k) * N * 2, exps_.p + 2 * k, sums_.p + 2 * k, tp_,
-                  margin_.p + k, n_groups_, record_positions_ ? positions_.p : nullptr, k,
-                  stream_);
-  exps_host_.reserve(exps_.bytes());
-  DP_HIP(hipMemcpyAsync(exps_host_.p, exps_.p, exps_.bytes(), hipMemcpyDeviceToHost, stream_));
-  DP_HIP(hipStreamSynchronize(stream_));
-  const auto* e = reinterpret_cast<const int32_t*>(exps_host_.p);
+  // Level-synced trees copy their records during grow(): collect the round in
+  // flight before they are overwritten.
+  if (!grower_->eager()) flush();
+  last_round_inputs_ = inputs;
+  int32_t* positions = record_positions_ ? positions_.p : nullptr;
+  // Everything the enqueued launches depend on: a change of any of it gives
+  // a new graph.
+  std::vector<uint64_t> key = {
+      uint64_t(with_gradients), reinterpret_cast<uint64_t>(d), reinterpret_cast<uint64_t>(&q),
+      reinterpret_cast<uint64_t>(q.bins.p), reinterpret_cast<uint64_t>(q.cols.p),
+      reinterpret_cast<uint64_t>(q.rows.p), reinterpret_cast<uint64_t>(q.d_nbins.p),
+      uint64_t(q.bin_stride), uint64_t(N), reinterpret_cast<uint64_t>(d->labels.p),
+      uint64_t(objective_id_), uint64_t(n_groups_), reinterpret_cast<uint64_t>(margin_.p),
+      reinterpret_cast<uint64_t>(grad_.p), reinterpret_cast<uint64_t>(hess_.p),
+      reinterpret_cast<uint64_t>(gpair_.p), reinterpret_cast<uint64_t>(exps_.p),
+      reinterpret_cast<uint64_t>(sums_.p), reinterpret_cast<uint64_t>(quant_scratch_.p),
+      reinterpret_cast<uint64_t>(positions), grower_->signature()};
+  words(key, &q.layout, sizeof q.layout);
+  words(key, &tp_, sizeof tp_);
+  enqueue(key, grower_->eager(), [&] {
+    bool maxima = false;
+    if (with_gradients)
+      maxima = launch_gradients(objective_id_, margin_.p, d->labels.p, N, n_groups_, grad_.p,
+                                hess_.p, quant_scratch_.p, stream_);
+    launch_quantise(grad_.p, hess_.p, N, n_groups_, quant_scratch_.p, maxima, exps_.p, gpair_.p,
+                    sums_.p, stream_);
+    for (int32_t k = 0; k < n_groups_; ++k)
+      grower_->grow(q, gpair_.p + int64_t(k) * N * 2, exps_.p + 2 * k, sums_.p + 2 * k, tp_,
+                    margin_.p + k, n_groups_, positions, k, stream_);
+  });
+  // This round's records go to the buffer the round in flight does not use.
+  const int32_t buffer = pending_ ? 1 - pending_buffer_ : 0;
+  grower_->readback(n_groups_, buffer, stream_);
+  exps_host_.reserve(2 * exps_.bytes());
+  DP_HIP(hipMemcpyAsync(exps_host_.p + size_t(buffer) * exps_.bytes(), exps_.p, exps_.bytes(),
+                        hipMemcpyDeviceToHost, stream_));
+  if (!round_done_[buffer])
+    DP_HIP(hipEventCreateWithFlags(&round_done_[buffer], hipEventDisableTiming));
+  DP_HIP(hipEventRecord(round_done_[buffer], stream_));
+  flush();  // the previous round, which completed before this one started
+  pending_ = true;
+  pending_buffer_ = buffer;
+  pending_q_ = &q;
+  ++rounds_;
+  if (!grower_->eager()) flush();
+}
+
+void Booster::flush() const {
+  if (!pending_) return;
+  pending_ = false;
+  const int32_t b = pending_buffer_;
+  DP_HIP(hipEventSynchronize(round_done_[b]));
+  const auto* e = reinterpret_cast<const int32_t*>(exps_host_.p + size_t(b) * exps_.bytes());
   last_exps_.assign(e, e + 2 * n_groups_);
+  std::vector<Tree> round(static_cast<size_t>(n_groups_));
+  try {
+    for (int32_t k = 0; k < n_groups_; ++k) grower_->collect(*pending_q_, k, b, round[size_t(k)]);
+  } catch (...) {
+    rounds_ = int(iteration_indptr_.size()) - 1;  // the failed round is not part of the model
+    throw;
+  }
   for (int32_t k = 0; k < n_groups_; ++k) {
-    Tree tree;
-    grower_->collect(q, k, tree);
-    trees_.push_back(std::move(tree));
+    trees_.push_back(std::move(round[size_t(k)]));
     tree_info_.push_back(k);
   }
   iteration_indptr_.push_back(int32_t(trees_.size()));
-  ++rounds_;
 }
 
 void Booster::margins(float* out, size_t n) const {
+  flush();
   need(configured_, "booster has not been trained");
   need(n == margin_.n, "margin buffer size differs");
   DP_HIP(hipMemcpy(out, margin_.p, margin_.bytes(), hipMemcpyDeviceToHost));
 }
 
 void Booster::last_gradients(float* grad, float* hess, size_t n, int32_t* exps) const {
+  flush();
   need(configured_, "booster has not been trained");
   need(n == grad_.n, "gradient buffer size differs");
   if (grad) DP_HIP(hipMemcpy(grad, grad_.p, grad_.bytes(), hipMemcpyDeviceToHost));
@@ -685,6 +827,7 @@ void Booster::last_gradients(float* grad, float* hess, size_t n, int32_t* exps) 
 }
 
 void Booster::last_positions(int32_t* out, size_t n) const {
+  flush();
   need(record_positions_ && positions_.p, "set dp_record_positions=1 before training");
   need(n == size_t(train_->n_rows), "positions buffer size differs");
   DP_HIP(hipMemcpy(out, positions_.p, sizeof(int32_t) * n, hipMemcpyDeviceToHost));
@@ -719,6 +862,7 @@ std::string base_score_text(const std::vector<float>& b) {
 }  // namespace
 
 std::string Booster::save_model() const {
+  flush();
   std::string o;
   o.reserve(1 << 16);
   o += "{\"learner\":{\"attributes\":{},\"feature_names\":[],\"feature_types\":[],";
@@ -776,6 +920,7 @@ std::string Booster::save_model() const {
 }
 
 std::string Booster::save_config() const {
+  flush();
   auto get = [&](const char* k, const char* dflt) {
     auto it = params_.find(k);
     return it == params_.end() ? std::string(dflt) : it->second;
@@ -836,6 +981,7 @@ std::string Booster::effective_objective() const {
 }
 
 void Booster::upload_forest(int32_t tree_begin, int32_t tree_end) {
+  flush();
   if (forest_begin_ == tree_begin && forest_end_ == tree_end && forest_trees_ == trees_.size())
     return;
   std::vector<PredNode> nodes;
@@ -881,6 +1027,7 @@ void Booster::upload_forest(int32_t tree_begin, int32_t tree_end) {
 }
 
 const float* Booster::predict(const PredictRequest& req, std::vector<uint64_t>& shape) {
+  flush();
   need(configured_ || model_only_, "booster holds no model");
   need(req.features == n_features_, "prediction input has " + std::to_string(req.features) +
                                         " features, the model " + std::to_string(n_features_));
@@ -911,6 +1058,7 @@ const float* Booster::predict(const PredictRequest& req, std::vector<uint64_t>& 
 }
 
 void Booster::load_model(const std::string& text) {
+  flush();
   need(!configured_, "cannot load into a booster that is training");
   const json::Value doc = json::parse(text);
   const auto& learner = doc.at("learner");
@@ -1009,12 +1157,14 @@ void Booster::load_model(const std::string& text) {
 }
 
 std::unique_ptr<Booster> Booster::slice(int begin, int end, int step) const {
+  flush();
   need(configured_ || model_only_, "booster holds no model");
   if (end == 0) end = rounds_;
   need(step >= 1 && begin >= 0 && begin <= end && end <= rounds_, "slice range outside the model");
   auto out = std::make_unique<Booster>(std::vector<DMatrix*>{});
   out->params_ = params_;
   out->params_.erase("dp_record_positions");
+  out->params_.erase("dp_graphs");
   out->objective_ = effective_objective();
   out->objective_id_ = objective_id_;
   out->n_groups_ = n_groups_;

@@ -1,6 +1,7 @@
 // Host-side training objects behind the XGBoost-compatible C API.
 #pragma once
 
+#include <functional>
 #include <map>
 #include <memory>
 #include <string>
@@ -72,8 +73,16 @@ class Grower {
   void grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
             const int64_t* root_sums, const TrainParam& p, float* margin, int64_t stride,
             int32_t* positions, int32_t slot, hipStream_t s);
-  // The tree grown into `slot`; the stream must have been synchronised.
-  void collect(const Quantized& q, int32_t slot, Tree& tree) const;
+  // Copies the node records of slots [0, n_slots) to host buffer `buffer`
+  // (0 or 1; one copy; eager trees only, level-synced trees were copied by
+  // grow).
+  void readback(int32_t n_slots, int32_t buffer, hipStream_t s);
+  // The tree grown into `slot`; readback() into `buffer` has completed.
+  void collect(const Quantized& q, int32_t slot, int32_t buffer, Tree& tree) const;
+  // False when trees are grown level-synced (grow() then synchronises).
+  bool eager() const { return eager_; }
+  // Changes whenever a buffer that grow() passes to a kernel moves or resizes.
+  uint64_t signature() const;
 
  private:
   void ensure_level(const Quantized& q, int64_t nodes, int32_t depth, int32_t max_depth);
@@ -92,7 +101,9 @@ class Grower {
   DeviceBuffer<LeafWork> leaf_work_[2];  // by level parity: applied one level later
   DeviceBuffer<NodeInfo> info_;
   DeviceBuffer<PlanCounts> counts_;
-  PinnedBuffer readback_;  // per slot: PlanCounts, then NodeInfo[node_cap_]
+  DeviceBuffer<uint8_t> slots_;  // eager: per slot, PlanCounts then NodeInfo[node_cap_]
+  PinnedBuffer readback_;        // host copies of slots_: two buffers of readback_slots_ slots
+  int32_t readback_slots_ = 0;
   PinnedBuffer level_count_;
   std::vector<std::vector<NodeInfo>> spill_;  // slots of trees grown level-synced
   std::vector<PlanCounts> spill_counts_;
@@ -127,10 +138,19 @@ class Booster {
   void update_one_iter(int iter, DMatrix* d);
   void train_one_iter(DMatrix* d, int iter, const float* grad, const float* hess, int64_t n,
                       int32_t k);
-  int boosted_rounds() const { return rounds_; }
+  int boosted_rounds() const {
+    flush();
+    return rounds_;
+  }
   std::string save_config() const;
   std::string save_model() const;
-  const std::vector<Tree>& trees() const { return trees_; }
+  const std::vector<Tree>& trees() const {
+    flush();
+    return trees_;
+  }
+  // Collects the trees of a round still in flight (rounds are pipelined: a
+  // round's trees come back while the next round runs on the GPU).
+  void flush() const;
   void margins(float* out, size_t n) const;
   void last_gradients(float* grad, float* hess, size_t n, int32_t* exps) const;
   void last_positions(int32_t* out, size_t n) const;
@@ -145,8 +165,15 @@ class Booster {
   std::string effective_objective() const;
   void upload_forest(int32_t tree_begin, int32_t tree_end);
   void configure(DMatrix* d);
-  // maxima_ready: the gradient kernel already wrote the quantiser's maxima slots.
-  void boost_from_gradients(DMatrix* d, const float* grad, const float* hess, bool maxima_ready);
+  // One boosting round: quantise + sizes the buffers (host), then enqueues
+  // the round's device work (gradients when `with_gradients`, the quantiser
+  // and the K trees) through a cached HIP graph, then collects the trees.
+  void run_round(DMatrix* d, bool with_gradients);
+  // Enqueues body() on stream_: replays the graph cached for `key`, or
+  // captures body() into a new graph and launches it (direct launches when
+  // graphs are off or the trees are grown level-synced).
+  void enqueue(const std::vector<uint64_t>& key, bool capturable, const std::function<void()>& body);
+  void clear_graphs();
   std::map<std::string, std::string> params_;
   std::vector<DMatrix*> cache_;
   // configured state
@@ -165,16 +192,24 @@ class Booster {
   DeviceBuffer<int64_t> sums_;
   DeviceBuffer<uint8_t> quant_scratch_;  // quantiser reduction slots
   DeviceBuffer<int32_t> positions_;
-  std::vector<int32_t> last_exps_;
-  PinnedBuffer exps_host_;
+  mutable std::vector<int32_t> last_exps_;
+  PinnedBuffer exps_host_;  // two buffers, by round parity
   bool record_positions_ = false;
+  bool use_graphs_ = true;
   bool labels_checked_ = false;
+  std::vector<std::pair<std::vector<uint64_t>, hipGraphExec_t>> graphs_;  // newest last
   hipStream_t stream_ = nullptr;
   std::unique_ptr<Grower> grower_;
-  std::vector<Tree> trees_;
-  std::vector<int32_t> tree_info_;
-  std::vector<int32_t> iteration_indptr_{0};
-  int rounds_ = 0;
+  mutable std::vector<Tree> trees_;
+  mutable std::vector<int32_t> tree_info_;
+  mutable std::vector<int32_t> iteration_indptr_{0};
+  // The round in flight: its readback buffer, matrix and completion event.
+  mutable bool pending_ = false;
+  int32_t pending_buffer_ = 0;
+  const Quantized* pending_q_ = nullptr;
+  hipEvent_t round_done_[2] = {nullptr, nullptr};
+  std::vector<uint64_t> last_round_inputs_;  // host inputs of the last round enqueued
+  mutable int rounds_ = 0;
   bool model_only_ = false;  // loaded or sliced: predicts, cannot train
   // device forest for prediction
   DeviceBuffer<uint8_t> forest_nodes_;

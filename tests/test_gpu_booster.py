@@ -274,3 +274,56 @@ def test_invalid_labels_are_refused(dp, device):
     inf[3, 2] = float("inf")
     with pytest.raises(dp.DPError, match="inf"):
         dp.DMatrix(inf, half)
+
+
+@pytest.mark.parametrize("objective,k", [(0, 1), (1, 3)])
+def test_graph_replays_equal_direct_launches(dp, device, objective, k):
+    """Rounds replayed from cached HIP graphs give the same model, margins and row positions
+    as rounds launched directly; a parameter change between rounds captures a new graph, and
+    caller gradients (a graph without the objective kernel) replay the same way.  Rounds left
+    in flight back to back (trees collected one call later) give the same model too."""
+    import torch
+    from dpgbdt import ops
+
+    n, f = 20_000, 12
+    values, labels, g, h = ops.synth(1, n, 7, n_features=f, want_grad=True)
+    if objective == 1:
+        labels = (torch.arange(n, device=values.device) % k).to(torch.float32)
+    values[::97, 3] = float("nan")
+    obj_name = {0: "binary:logistic", 1: "multi:softmax"}[objective]
+
+    def train(graphs, inspect=True):
+        dtrain = dp.DMatrix(values, labels)
+        params = {"objective": obj_name, "max_depth": 5, "eta": 0.3, "dp_record_positions": 1,
+                  "dp_graphs": graphs}
+        if objective == 1:
+            params["num_class"] = k
+        bst = dp.Booster(params, [dtrain])
+        positions, margins = [], []
+        for r in range(6):
+            if r == 3:
+                bst.set_param("eta", 0.1)
+            bst.update(dtrain, r)
+            if inspect:  # collects the round; otherwise rounds stay in flight back to back
+                positions.append(bst.last_positions(n))
+                margins.append(bst.margins(n, k))
+        gk = g.repeat_interleave(k).reshape(n, k).contiguous() if k > 1 else g
+        hk = h.repeat_interleave(k).reshape(n, k).contiguous() if k > 1 else h
+        for r in range(6, 9):
+            bst.boost(dtrain, r, gk, hk)
+            if inspect:
+                positions.append(bst.last_positions(n))
+                margins.append(bst.margins(n, k))
+        assert bst.num_boosted_rounds() == 9
+        return bst.save_raw(), positions, margins
+
+    raw_direct, pos_direct, m_direct = train(0)
+    raw_graph, pos_graph, m_graph = train(1)
+    assert raw_graph == raw_direct
+    assert train(1, inspect=False)[0] == raw_direct
+    assert train(0, inspect=False)[0] == raw_direct
+    for r, (a, b) in enumerate(zip(pos_graph, pos_direct)):
+        np.testing.assert_array_equal(a, b, err_msg=f"round {r} positions")
+    for r, (a, b) in enumerate(zip(m_graph, m_direct)):
+        np.testing.assert_array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32),
+                                      err_msg=f"round {r} margins")
