@@ -637,14 +637,16 @@ void Booster::configure(DMatrix* d) {
   exps_.resize(size_t(2 * n_groups_));
   sums_.resize(size_t(2 * n_groups_));
   quant_scratch_.resize(quantise_scratch_bytes(N, n_groups_));
-  std::vector<float> init(static_cast<size_t>(N) * n_groups_);
-  for (int64_t r = 0; r < N; ++r)
-    for (int32_t k = 0; k < n_groups_; ++k) {
-      const float b = base_score_[size_t(k)];
-      init[size_t(r * n_groups_ + k)] =
-          objective_id_ == DP_OBJ_LOGISTIC ? float(std::log(double(b) / (1.0 - double(b)))) : b;
-    }
-  DP_HIP(hipMemcpy(margin_.p, init.data(), margin_.bytes(), hipMemcpyHostToDevice));
+  std::vector<float> init(static_cast<size_t>(n_groups_));
+  for (int32_t k = 0; k < n_groups_; ++k) {
+    const float b = base_score_[size_t(k)];
+    init[size_t(k)] =
+        objective_id_ == DP_OBJ_LOGISTIC ? float(std::log(double(b) / (1.0 - double(b)))) : b;
+  }
+  DeviceBuffer<float> base(init.size());
+  DP_HIP(hipMemcpy(base.p, init.data(), base.bytes(), hipMemcpyHostToDevice));
+  launch_init_margin(margin_.p, N, n_groups_, base.p, stream_);
+  DP_HIP(hipStreamSynchronize(stream_));  // before `base` is freed
   grower_ = std::make_unique<Grower>();
   configured_ = true;
 }

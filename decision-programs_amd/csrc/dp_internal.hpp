@@ -353,6 +353,10 @@ inline int64_t plan_hist_items(int64_t nodes, int64_t n_rows, int32_t n_tiles) {
 }
 constexpr int64_t kLeafChunk = 16384;  // margin-update items of the operator API
 
+// margin[r * n_outputs + k] = base[k] (base: n_outputs device floats).
+void launch_init_margin(float* margin, int64_t n_rows, int32_t n_outputs, const float* base,
+                        hipStream_t s);
+
 // Objective gradients.  With quant_scratch (quantise_scratch_bytes) and one
 // output, the per-workgroup maxima the quantiser needs are written too and
 // true is returned (pass maxima_ready to launch_quantise).

@@ -249,6 +249,14 @@ __global__ void check_labels_kernel(const float* __restrict__ label, int64_t n, 
   if (__ballot(wrong) && (threadIdx.x & 63) == 0) atomicOr(bad, 1);
 }
 
+// margin[r * K + k] = base[k]: the starting margins of every row.
+__global__ void init_margin_kernel(float* __restrict__ margin, int64_t n, int32_t k,
+                                   const float* __restrict__ base) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += int64_t(blockDim.x) * gridDim.x)
+    margin[i] = base[i % k];
+}
+
 }  // namespace
 
 void launch_check_labels(const float* label, int64_t n, int32_t objective, int32_t n_classes,
@@ -265,6 +273,14 @@ int quantise_blocks(int64_t n_rows) { return grid_for(n_rows, kQuantThreads, kQu
 size_t quantise_scratch_bytes(int64_t n_rows, int32_t n_classes) {
   const size_t slots = size_t(n_classes) * size_t(quantise_blocks(n_rows));
   return slots * 2 * sizeof(uint32_t) + 256 + slots * 2 * sizeof(int64_t);
+}
+
+void launch_init_margin(float* margin, int64_t n_rows, int32_t n_outputs, const float* base,
+                        hipStream_t s) {
+  if (n_rows <= 0 || n_outputs <= 0) return;
+  hipLaunchKernelGGL(init_margin_kernel, dim3(grid_for(n_rows * n_outputs, 256, 8192)), dim3(256),
+                     0, s, margin, n_rows * n_outputs, n_outputs, base);
+  DP_HIP(hipGetLastError());
 }
 
 bool launch_gradients(int32_t objective, const float* margin, const float* label,

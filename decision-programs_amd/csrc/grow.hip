@@ -345,19 +345,66 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
   }
 }
 
+// Exclusive scan of V int64 values per thread over the workgroup (the
+// values of one thread scanned side by side); writes the totals.  lds holds at
+// least 2 * 16 * V values.  Three barriers, whatever V.
+template <int V>
+__device__ void block_scan_n(const int64_t (&v)[V], int64_t (&out)[V], int64_t (&total)[V],
+                             int64_t* lds) {
+  constexpr int W = kPlanThreads / 64;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  int64_t x[V];
+#pragma unroll
+  for (int k = 0; k < V; ++k) x[k] = v[k];
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      const int64_t y = __shfl_up(x[k], d, 64);
+      if (lane >= d) x[k] += y;
+    }
+  }
+  if (lane == 63)
+#pragma unroll
+    for (int k = 0; k < V; ++k) lds[k * W + wave] = x[k];
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      int64_t w = lane < W ? lds[k * W + lane] : 0;
+#pragma unroll
+      for (int d = 1; d < W; d <<= 1) {
+        const int64_t y = __shfl_up(w, d, 64);
+        if (lane >= d) w += y;
+      }
+      if (lane < W) lds[(V + k) * W + lane] = w;  // inclusive
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    out[k] = (wave ? lds[(V + k) * W + wave - 1] : 0) + x[k] - v[k];
+    total[k] = lds[(V + k) * W + W - 1];
+  }
+  __syncthreads();
+}
+
 // The planner for levels of at most kPlanThreads nodes: thread i owns node i
-// for the whole level, keeps the node and its children in registers, and
-// leaves in LDS what the per-item loops look up, so after the first loads no
-// section reads back what another section wrote to global memory.  Its work
-// lists are identical to plan_level_kernel's.
+// for the whole level and keeps the node and its split in registers.  Every
+// per-node count the level's work lists need is known once the split is
+// read, so two multi-value scans give all offsets (the second depends on the
+// histogram chunk, which depends on the first's totals); the offsets and
+// segments then sit in LDS, read-only, for the item loops.  Its work lists
+// are identical to plan_level_kernel's.
 __global__ __launch_bounds__(kPlanThreads) void plan_small_kernel(PlanArgs a) {
-  __shared__ int64_t scan[kPlanThreads];
-  __shared__ int64_t s_off[kPlanThreads + 1];  // per-node offsets of the section's items
-  __shared__ int64_t s_aux[kPlanThreads];      // C: partial chunk starts; D: left chunk counts
-  __shared__ int64_t s_begin[kPlanThreads];
-  __shared__ int64_t s_end[kPlanThreads];
-  __shared__ int64_t s_end2[kPlanThreads];
-  __shared__ int32_t s_id[kPlanThreads];
+  __shared__ int64_t scan[2 * (kPlanThreads / 64) * 4];
+  __shared__ int64_t s_leaf[kPlanThreads + 1];  // first leaf chunk per node
+  __shared__ int64_t s_cs[kPlanThreads + 1];    // first histogram chunk per node
+  __shared__ int64_t s_ps[kPlanThreads];        // first partial chunk per node
+  __shared__ int64_t s_po[kPlanThreads + 1];    // first partition item per node
+  __shared__ int64_t s_begin[kPlanThreads], s_mid[kPlanThreads], s_end[kPlanThreads];
+  __shared__ int32_t s_nid[kPlanThreads];
+  __shared__ int32_t s_slot[kPlanThreads];  // 2 * rank + (right child is the smaller)
   __shared__ float s_val[kPlanThreads];
   __shared__ int32_t s_error;
   const int tid = threadIdx.x;
@@ -374,9 +421,8 @@ __global__ __launch_bounds__(kPlanThreads) void plan_small_kernel(PlanArgs a) {
     return;
   }
   if (tid == 0) s_error = 0;
-  __syncthreads();
 
-  // ---- A: numbering, node records, next-level nodes ----------------------
+  // ---- per-node state and counts ----------------------------------------------
   const bool live = tid < n;
   LevelNode nd{};
   dp_split_record sp{};
@@ -389,15 +435,26 @@ __global__ __launch_bounds__(kPlanThreads) void plan_small_kernel(PlanArgs a) {
       if (sp.expand) {
         nl = a.node_left[tid];
         e = nl > 0 && nl < nd.end - nd.begin;
-        if (!e) s_error = 1;
       }
     }
   }
-  int64_t total;
-  const int64_t rank = block_scan(e ? 1 : 0, scan, &total);
-  const int32_t n_expand = int32_t(total);
+  const bool next_hist = a.depth + 1 < a.max_depth;  // children get histograms
+  const int64_t rows = nd.end - nd.begin, lrows = nl, rrows = rows - nl;
+  const bool right_small = rrows < lrows;
+  int64_t cnt[4] = {e ? 1 : 0,                                                       // expanded
+                    (live && !e) ? (rows + a.leaf_chunk - 1) / a.leaf_chunk : 0,     // leaf chunks
+                    (e && next_hist) ? (right_small ? rrows : lrows) : 0,            // smaller child
+                    (e && next_hist) ? (lrows + a.part_chunk - 1) / a.part_chunk +   // partition
+                                           (rrows + a.part_chunk - 1) / a.part_chunk
+                                     : 0};
+  int64_t off[4], tot[4];
+  block_scan_n<4>(cnt, off, tot, scan);  // its barriers also publish s_error = 0
+  if (live && a.splits && sp.expand && !e) s_error = 1;
+  const int64_t rank = off[0];
+  const int32_t n_expand = int32_t(tot[0]);
   const int32_t n_next = 2 * n_expand;
-  LevelNode L{}, R{};
+
+  // ---- A: node records and next-level nodes ----------------------------------
   float leaf_value = 0.0f;
   if (live) {
     NodeInfo info{};
@@ -418,18 +475,16 @@ __global__ __launch_bounds__(kPlanThreads) void plan_small_kernel(PlanArgs a) {
       info.bin = sp.bin;
       info.default_left = sp.default_left;
       info.loss_chg = sp.loss_chg;
-      L = LevelNode{nd.begin, nd.begin + nl, sp.gl, sp.hl, left, tid};
-      R = LevelNode{nd.begin + nl, nd.end, nd.g - sp.gl, nd.h - sp.hl, left + 1, tid};
       const int64_t slot = 2 * rank;
       if (left + 1 < a.info_capacity && slot + 1 < a.level_capacity) {
-        a.next[slot] = L;
-        a.next[slot + 1] = R;
-        a.next_sums[2 * slot] = L.g;
-        a.next_sums[2 * slot + 1] = L.h;
-        a.next_sums[2 * slot + 2] = R.g;
-        a.next_sums[2 * slot + 3] = R.h;
-        a.next_seg_begin[slot] = L.begin;
-        a.next_seg_begin[slot + 1] = R.begin;
+        a.next[slot] = LevelNode{nd.begin, nd.begin + nl, sp.gl, sp.hl, left, tid};
+        a.next[slot + 1] = LevelNode{nd.begin + nl, nd.end, nd.g - sp.gl, nd.h - sp.hl, left + 1, tid};
+        a.next_sums[2 * slot] = sp.gl;
+        a.next_sums[2 * slot + 1] = sp.hl;
+        a.next_sums[2 * slot + 2] = nd.g - sp.gl;
+        a.next_sums[2 * slot + 3] = nd.h - sp.hl;
+        a.next_seg_begin[slot] = nd.begin;
+        a.next_seg_begin[slot + 1] = nd.begin + nl;
         a.next_node_left[slot] = 0;
         a.next_node_left[slot + 1] = 0;
       } else {
@@ -443,6 +498,32 @@ __global__ __launch_bounds__(kPlanThreads) void plan_small_kernel(PlanArgs a) {
     if (nd.nid >= 0 && nd.nid < a.info_capacity) a.info[nd.nid] = info;
     else s_error = 2;
   }
+
+  // ---- second scan: histogram chunks of the smaller children -----------------
+  const int32_t T = a.n_tiles;
+  const int64_t chunk = hist_chunk(tot[2], T);
+  const int64_t nc = (cnt[2] + chunk - 1) / chunk;
+  int64_t cnt2[2] = {nc, nc >= 2 ? nc : 0}, off2[2], tot2[2];
+  if (live) {
+    s_leaf[tid] = off[1];
+    s_po[tid] = off[3];
+    s_begin[tid] = nd.begin;
+    s_mid[tid] = nd.begin + nl;
+    s_end[tid] = nd.end;
+    s_nid[tid] = nd.nid;
+    s_slot[tid] = int32_t(2 * rank) + (right_small ? 1 : 0);
+    s_val[tid] = leaf_value;
+  }
+  if (tid == 0) {
+    s_leaf[n] = tot[1];
+    s_po[n] = tot[3];
+  }
+  block_scan_n<2>(cnt2, off2, tot2, scan);  // its barriers also publish the arrays above
+  if (live) {
+    s_cs[tid] = off2[0];
+    s_ps[tid] = off2[1];
+  }
+  if (tid == 0) s_cs[n] = tot2[0];
   __syncthreads();
   if (s_error) {  // inconsistent level or capacity exceeded: stop this tree
     if (tid == 0) {
@@ -452,73 +533,43 @@ __global__ __launch_bounds__(kPlanThreads) void plan_small_kernel(PlanArgs a) {
     }
     return;
   }
+  int32_t error = 0;
 
   // ---- B: leaf work of this level -----------------------------------------
-  const int64_t rows = nd.end - nd.begin;
-  const int64_t lc = (live && !e) ? (rows + a.leaf_chunk - 1) / a.leaf_chunk : 0;
-  const int64_t loff = block_scan(lc, scan, &total);
-  int64_t n_leaf = total;
-  if (live) {
-    s_off[tid] = loff;
-    s_begin[tid] = nd.begin;
-    s_end[tid] = nd.end;
-    s_id[tid] = nd.nid;
-    s_val[tid] = leaf_value;
-  }
-  if (tid == 0) s_off[n] = n_leaf;
-  __syncthreads();
+  int64_t n_leaf = tot[1];
   if (n_leaf > a.leaf_capacity) {
-    if (tid == 0) s_error = 3;
+    error = 3;
     n_leaf = 0;
   }
   for (int64_t k = tid; k < n_leaf; k += kPlanThreads) {
-    const int32_t j = owner(s_off, n, k);
-    const int64_t b = s_begin[j] + (k - s_off[j]) * a.leaf_chunk;
-    a.leaf_work[k] = LeafWork{s_val[j], s_id[j], b,
+    const int32_t j = owner(s_leaf, n, k);
+    const int64_t b = s_begin[j] + (k - s_leaf[j]) * a.leaf_chunk;
+    a.leaf_work[k] = LeafWork{s_val[j], s_nid[j], b,
                               b + a.leaf_chunk < s_end[j] ? b + a.leaf_chunk : s_end[j]};
   }
-  __syncthreads();  // the LDS arrays are reused below
 
   // ---- C: histogram work and reduce jobs of the next level ----------------
-  const bool next_hist = n_next > 0 && a.depth + 1 < a.max_depth;
   int64_t n_hist = 0;
   int32_t n_reduce = 0;
-  const int64_t lrows = L.end - L.begin, rrows = R.end - R.begin;
-  if (next_hist) {
-    const int32_t T = a.n_tiles;
-    const bool right_small = rrows < lrows;
-    const int64_t srows = e ? (right_small ? rrows : lrows) : 0;
-    (void)block_scan(srows, scan, &total);
-    const int64_t chunk = hist_chunk(total, T);
-    const int64_t nc = (srows + chunk - 1) / chunk;
-    const int64_t cs = block_scan(nc, scan, &total);
-    const int64_t C = total;
-    const int64_t ps = block_scan(nc >= 2 ? nc : 0, scan, &total);
-    const int64_t P = total;
-    if (live) {
-      s_off[tid] = cs;
-      s_aux[tid] = ps;
-      s_begin[tid] = right_small ? R.begin : L.begin;
-      s_end[tid] = right_small ? R.end : L.end;
-      s_id[tid] = int32_t(2 * rank) + (right_small ? 1 : 0);
-    }
-    if (tid == 0) s_off[n] = C;
-    __syncthreads();
+  if (next_hist && n_next > 0) {
+    const int64_t C = tot2[0];
     const int64_t padded = (C + 7) / 8 * 8;
     n_hist = padded * T;
-    if (n_hist > a.hist_capacity || P * T > a.partial_capacity) {
-      if (tid == 0) s_error = 4;
+    if (n_hist > a.hist_capacity || tot2[1] * T > a.partial_capacity) {
+      error = 4;
       n_hist = 0;
     } else {
       for (int64_t c = tid; c < padded; c += kPlanThreads) {
         HistWork item{0, 0, 0, 0, -1, 0};
         int64_t p = -1;
         if (c < C) {
-          const int32_t j = owner(s_off, n, c);
-          const int64_t k = c - s_off[j];
-          const int64_t b = s_begin[j] + k * chunk;
-          item = HistWork{s_id[j], 0, b, b + chunk < s_end[j] ? b + chunk : s_end[j], -1, 0};
-          if (s_off[j + 1] - s_off[j] >= 2) p = (s_aux[j] + k) * T;
+          const int32_t j = owner(s_cs, n, c);
+          const int64_t k = c - s_cs[j];
+          const bool rs = s_slot[j] & 1;
+          const int64_t sb = rs ? s_mid[j] : s_begin[j], se = rs ? s_end[j] : s_mid[j];
+          const int64_t b = sb + k * chunk;
+          item = HistWork{s_slot[j], 0, b, b + chunk < se ? b + chunk : se, -1, 0};
+          if (s_cs[j + 1] - s_cs[j] >= 2) p = (s_ps[j] + k) * T;
         }
         for (int32_t t = 0; t < T; ++t) {
           item.tile = t;
@@ -530,59 +581,44 @@ __global__ __launch_bounds__(kPlanThreads) void plan_small_kernel(PlanArgs a) {
         a.reduce_jobs[rank] = HistReduce{int32_t(2 * rank) + (right_small ? 1 : 0),
                                          int32_t(2 * rank) + (right_small ? 0 : 1),
                                          int64_t(tid) * a.hist_elems,
-                                         nc >= 2 ? int32_t(ps) : -1, int32_t(nc)};
+                                         nc >= 2 ? int32_t(off2[1]) : -1, int32_t(nc)};
       n_reduce = n_expand;
     }
-    __syncthreads();  // the LDS arrays are reused below
   }
 
   // ---- D: partition work of the next level ----------------------------------
   int64_t n_part = 0;
-  if (next_hist) {
-    const int64_t cl = e ? (lrows + a.part_chunk - 1) / a.part_chunk : 0;
-    const int64_t cr = e ? (rrows + a.part_chunk - 1) / a.part_chunk : 0;
-    const int64_t po = block_scan(cl + cr, scan, &total);
-    n_part = total;
+  if (next_hist && n_next > 0) {
+    n_part = tot[3];
     if (e) {
-      a.part_first[2 * rank] = int32_t(po);
-      a.part_first[2 * rank + 1] = int32_t(po + cl);
+      const int64_t cl = (lrows + a.part_chunk - 1) / a.part_chunk;
+      a.part_first[2 * rank] = int32_t(off[3]);
+      a.part_first[2 * rank + 1] = int32_t(off[3] + cl);
     }
-    if (live) {
-      s_off[tid] = po;
-      s_aux[tid] = cl;
-      s_begin[tid] = L.begin;
-      s_end[tid] = L.end;
-      s_end2[tid] = R.end;
-      s_id[tid] = int32_t(2 * rank);
-    }
-    if (tid == 0) {
-      s_off[n] = n_part;
-      a.part_first[n_next] = int32_t(n_part);
-    }
-    __syncthreads();
+    if (tid == 0) a.part_first[n_next] = int32_t(n_part);
     if (n_part > a.part_capacity) {
-      if (tid == 0) s_error = 5;
+      error = 5;
       n_part = 0;
     }
     for (int64_t k = tid; k < n_part; k += kPlanThreads) {
-      const int32_t j = owner(s_off, n, k);
-      int64_t kk = k - s_off[j];
-      int32_t node = s_id[j];
+      const int32_t j = owner(s_po, n, k);
+      const int64_t cl = (s_mid[j] - s_begin[j] + a.part_chunk - 1) / a.part_chunk;
+      int64_t kk = k - s_po[j];
+      int32_t node = s_slot[j] & ~1;
       int64_t b, end;
-      if (kk < s_aux[j]) {
+      if (kk < cl) {
         b = s_begin[j] + kk * a.part_chunk;
-        end = s_end[j];
+        end = s_mid[j];
       } else {
-        kk -= s_aux[j];
+        kk -= cl;
         node += 1;
-        b = s_end[j] + kk * a.part_chunk;
-        end = s_end2[j];
+        b = s_mid[j] + kk * a.part_chunk;
+        end = s_end[j];
       }
       a.part_work[k] = PartWork{node, 0, b, b + a.part_chunk < end ? b + a.part_chunk : end};
     }
   }
 
-  __syncthreads();
   if (tid == 0) {
     PlanCounts* c = a.counts;
     c->n_level = n_next;
@@ -591,7 +627,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_small_kernel(PlanArgs a) {
     c->n_reduce = n_reduce;
     c->n_part = int32_t(n_part);
     c->n_leaf = int32_t(n_leaf);
-    if (s_error && !c->error) c->error = s_error;
+    if (error && !c->error) c->error = error;
   }
 }
 

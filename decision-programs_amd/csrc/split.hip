@@ -1,8 +1,10 @@
 // Split evaluation: per node, per feature, a wavefront prefix scan over the
 // bins of the fixed-point histogram, the loss change of every candidate in
 // both missing directions, and an argmax with deterministic ties.  One
-// wavefront per (node, feature) finds the feature's best candidate, so even a
-// single node spreads over the chip; a second kernel picks each node's best
+// wavefront per (node, feature) finds the feature's best candidate.  With up
+// to 64 features one workgroup of 16 wavefronts takes a whole node and writes
+// its split record (one launch per level); with more, the (node, feature)
+// items spread over the chip and a second kernel picks each node's best
 // feature.
 //
 // Semantics (upstream CalcGain/CalcWeight with max_delta_step 0, reached in the
@@ -84,10 +86,114 @@ struct FeatCand {
 
 constexpr int kFeatWaves = 4;  // features per workgroup in evaluate_features_kernel
 
-// One wavefront per (node, feature): BPL bins per lane (bin_stride <= 64 *
-// BPL), an inclusive prefix scan over the bins, both missing directions, and
-// the feature's best candidate.  Workgroups loop over (node, feature group)
-// items; the node count may come from device memory.
+// One feature's histogram of one node as one wavefront holds it: bins
+// lane * BPL + j (bins past bin_stride read as zero).
+template <int BPL>
+struct FeatBins {
+  long long g[BPL], h[BPL];
+};
+
+template <int BPL>
+__device__ __forceinline__ void load_feature(const long long* __restrict__ hist, int32_t node,
+                                             int32_t f, int32_t n_features, int32_t bin_stride,
+                                             FeatBins<BPL>& d) {
+  const int lane = threadIdx.x & 63;
+  const long long* hf = hist + (int64_t(node) * n_features + f) * bin_stride * 2;
+#pragma unroll
+  for (int j = 0; j < BPL; ++j) {
+    const int b = lane * BPL + j;
+    d.g[j] = b < bin_stride ? hf[2 * b] : 0;
+    d.h[j] = b < bin_stride ? hf[2 * b + 1] : 0;
+  }
+}
+
+// The best candidate of feature f of one node, computed by one wavefront
+// (BPL bins per lane, bin_stride <= 64 * BPL): an inclusive prefix scan over
+// the bins, both missing directions, and the argmax.  Every lane returns the
+// same result; loss is -inf when the feature has no valid candidate.
+template <int BPL>
+__device__ __forceinline__ Cand feature_best(const FeatBins<BPL>& d, int32_t f, int nb,
+                                             long long gp, long long hp, double parent_gain,
+                                             double ug, double uh, const Param& p) {
+  const int lane = threadIdx.x & 63;
+  long long sg[BPL], sh[BPL];
+  long long rg = 0, rh = 0;
+#pragma unroll
+  for (int j = 0; j < BPL; ++j) {
+    rg += d.g[j];
+    rh += d.h[j];
+    sg[j] = rg;
+    sh[j] = rh;
+  }
+  // inclusive wavefront scan of the lane totals
+  long long ig = rg, ih = rh;
+#pragma unroll
+  for (int s = 1; s < 64; s <<= 1) {
+    const long long tg = __shfl_up(ig, s, 64);
+    const long long th = __shfl_up(ih, s, 64);
+    if (lane >= s) {
+      ig += tg;
+      ih += th;
+    }
+  }
+  const long long total_g = __shfl(ig, 63, 64), total_h = __shfl(ih, 63, 64);
+  const long long og = ig - rg, oh = ih - rh;  // exclusive offset of this lane
+  const long long mg = gp - total_g, mh = hp - total_h;
+
+  Cand c;
+  c.loss = -INFINITY;
+  c.gl = c.hl = 0;
+  c.feature = f;
+  c.bin = -1;
+  c.dl = 0;
+#pragma unroll
+  for (int j = 0; j < BPL; ++j) {
+    const int b = lane * BPL + j;
+    if (b < nb) {
+      const long long lg = og + sg[j], lh = oh + sh[j];
+      const double right_missing = split_loss(p, lg, lh, gp - lg, hp - lh, ug, uh, parent_gain);
+      // Without missing rows both directions are the same candidate.
+      const double left_missing =
+          (mg == 0 && mh == 0)
+              ? right_missing
+              : split_loss(p, lg + mg, lh + mh, gp - lg - mg, hp - lh - mh, ug, uh, parent_gain);
+      const int dl = left_missing > right_missing;
+      const double loss = dl ? left_missing : right_missing;
+      if (loss > c.loss) {
+        c.loss = loss;
+        c.bin = b;
+        c.dl = dl;
+        c.gl = dl ? lg + mg : lg;
+        c.hl = dl ? lh + mh : lh;
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const Cand o = shfl_xor_cand(c, m);
+    if (better(o, c)) c = o;
+  }
+  return c;
+}
+
+// The split record of a node's best candidate.
+__device__ __forceinline__ dp_split_record make_record(const Cand& r, double gamma) {
+  dp_split_record rec;
+  rec.loss_chg = r.loss;
+  rec.gl = r.gl;
+  rec.hl = r.hl;
+  rec.feature = r.feature;
+  rec.bin = r.bin;
+  rec.default_left = r.dl;
+  rec.valid = r.loss > -INFINITY ? 1 : 0;
+  rec.expand = rec.valid && r.loss > kRtEps && r.loss >= gamma;
+  rec.pad = 0;
+  return rec;
+}
+
+// One wavefront per (node, feature): the feature's best candidate.
+// Workgroups loop over (node, feature group) items; the node count may come
+// from device memory.
 template <int BPL>
 __global__ __launch_bounds__(64 * kFeatWaves) void evaluate_features_kernel(
     const long long* __restrict__ hist, int32_t n_nodes_host,
@@ -106,74 +212,62 @@ __global__ __launch_bounds__(64 * kFeatWaves) void evaluate_features_kernel(
     const int32_t node = int32_t(item / groups);
     const int32_t f = int32_t(item % groups) * kFeatWaves + wave;
     if (f >= n_features) continue;  // wave-uniform; no barriers in this kernel
+    FeatBins<BPL> bins;
+    load_feature<BPL>(hist, node, f, n_features, bin_stride, bins);
     const long long gp = node_sums[2 * node], hp = node_sums[2 * node + 1];
     const double parent_gain = calc_gain(p, double(gp) * ug, double(hp) * uh);
-    const int nb = n_bins[f];
-    const long long* hf = hist + (int64_t(node) * n_features + f) * bin_stride * 2;
-    long long sg[BPL], sh[BPL];
-    long long rg = 0, rh = 0;
-#pragma unroll
-    for (int j = 0; j < BPL; ++j) {
-      const int b = lane * BPL + j;
-      long long g = 0, h = 0;
-      if (b < bin_stride) {
-        g = hf[2 * b];
-        h = hf[2 * b + 1];
-      }
-      rg += g;
-      rh += h;
-      sg[j] = rg;
-      sh[j] = rh;
-    }
-    // inclusive wavefront scan of the lane totals
-    long long ig = rg, ih = rh;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const long long tg = __shfl_up(ig, d, 64);
-      const long long th = __shfl_up(ih, d, 64);
-      if (lane >= d) {
-        ig += tg;
-        ih += th;
-      }
-    }
-    const long long total_g = __shfl(ig, 63, 64), total_h = __shfl(ih, 63, 64);
-    const long long og = ig - rg, oh = ih - rh;  // exclusive offset of this lane
-    const long long mg = gp - total_g, mh = hp - total_h;
-
-    Cand c;
-    c.loss = -INFINITY;
-    c.gl = c.hl = 0;
-    c.feature = f;
-    c.bin = -1;
-    c.dl = 0;
-#pragma unroll
-    for (int j = 0; j < BPL; ++j) {
-      const int b = lane * BPL + j;
-      if (b < nb) {
-        const long long lg = og + sg[j], lh = oh + sh[j];
-        const double right_missing = split_loss(p, lg, lh, gp - lg, hp - lh, ug, uh, parent_gain);
-        // Without missing rows both directions are the same candidate.
-        const double left_missing =
-            (mg == 0 && mh == 0)
-                ? right_missing
-                : split_loss(p, lg + mg, lh + mh, gp - lg - mg, hp - lh - mh, ug, uh, parent_gain);
-        const int dl = left_missing > right_missing;
-        const double loss = dl ? left_missing : right_missing;
-        if (loss > c.loss) {
-          c.loss = loss;
-          c.bin = b;
-          c.dl = dl;
-          c.gl = dl ? lg + mg : lg;
-          c.hl = dl ? lh + mh : lh;
-        }
-      }
-    }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-      const Cand o = shfl_xor_cand(c, m);
-      if (better(o, c)) c = o;
-    }
+    const Cand c = feature_best<BPL>(bins, f, n_bins[f], gp, hp, parent_gain, ug, uh, p);
     if (lane == 0) cand[int64_t(node) * n_features + f] = FeatCand{c.loss, c.gl, c.hl, c.bin, c.dl};
+  }
+}
+
+constexpr int kNodeWaves = 16;     // wavefronts per node in evaluate_nodes_kernel
+constexpr int kNodeFeatures = 16;  // feature counts up to this use evaluate_nodes_kernel
+
+// Few features: one workgroup per node (looping over nodes); wavefront w
+// scans features w, w + 16, ..., keeps its best, and the workgroup's best is
+// the node's split record -- the whole evaluation in one launch.
+template <int BPL>
+__global__ __launch_bounds__(64 * kNodeWaves) void evaluate_nodes_kernel(
+    const long long* __restrict__ hist, int32_t n_nodes_host,
+    const int32_t* __restrict__ n_nodes_dev, int32_t n_features, int32_t bin_stride,
+    const int32_t* __restrict__ n_bins, const long long* __restrict__ node_sums,
+    const int32_t* __restrict__ exps, int32_t exp_g_host, int32_t exp_h_host, Param p,
+    dp_split_record* __restrict__ out) {
+  __shared__ Cand wave_best[kNodeWaves];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int32_t n_nodes = n_nodes_dev ? *n_nodes_dev : n_nodes_host;
+  const int exp_g = exps ? exps[0] : exp_g_host;
+  const int exp_h = exps ? exps[1] : exp_h_host;
+  const double ug = ldexp(1.0, -exp_g), uh = ldexp(1.0, -exp_h);
+  for (int32_t node = blockIdx.x; node < n_nodes; node += gridDim.x) {
+    // The wave's next feature is loaded while the current one is evaluated.
+    FeatBins<BPL> cur, nxt;
+    if (wave < n_features) load_feature<BPL>(hist, node, wave, n_features, bin_stride, cur);
+    const long long gp = node_sums[2 * node], hp = node_sums[2 * node + 1];
+    const double parent_gain = calc_gain(p, double(gp) * ug, double(hp) * uh);
+    Cand best;
+    best.loss = -INFINITY;
+    best.gl = best.hl = 0;
+    best.feature = -1;
+    best.bin = -1;
+    best.dl = 0;
+    for (int32_t f = wave; f < n_features; f += kNodeWaves) {  // wave-uniform
+      if (f + kNodeWaves < n_features)
+        load_feature<BPL>(hist, node, f + kNodeWaves, n_features, bin_stride, nxt);
+      const Cand c = feature_best<BPL>(cur, f, n_bins[f], gp, hp, parent_gain, ug, uh, p);
+      if (c.loss > -INFINITY && better(c, best)) best = c;
+      cur = nxt;
+    }
+    if (lane == 0) wave_best[wave] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      Cand r = wave_best[0];
+      for (int k = 1; k < kNodeWaves; ++k)
+        if (better(wave_best[k], r)) r = wave_best[k];
+      out[node] = make_record(r, p.gamma);
+    }
+    __syncthreads();  // wave_best is reused by the next node
   }
 }
 
@@ -217,17 +311,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_splits_kernel(
       Cand r = wave_best[0];
       for (int k = 1; k < kSelectThreads / 64; ++k)
         if (better(wave_best[k], r)) r = wave_best[k];
-      dp_split_record rec;
-      rec.loss_chg = r.loss;
-      rec.gl = r.gl;
-      rec.hl = r.hl;
-      rec.feature = r.feature;
-      rec.bin = r.bin;
-      rec.default_left = r.dl;
-      rec.valid = r.loss > -INFINITY ? 1 : 0;
-      rec.expand = rec.valid && r.loss > kRtEps && r.loss >= gamma;
-      rec.pad = 0;
-      out[node] = rec;
+      out[node] = make_record(r, gamma);
     }
     __syncthreads();  // wave_best is reused by the next node
   }
@@ -251,6 +335,20 @@ void launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_node
           double(param.gamma)};
   const auto* h = reinterpret_cast<const long long*>(hist);
   const auto* sums = reinterpret_cast<const long long*>(node_sums);
+  if (n_features <= kNodeFeatures) {
+    const dim3 grid(n_nodes < 2048 ? n_nodes : 2048), block(64 * kNodeWaves);
+    if (bin_stride <= 64)
+      hipLaunchKernelGGL(evaluate_nodes_kernel<1>, grid, block, 0, s, h, n_nodes, n_nodes_dev,
+                         n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p, out);
+    else if (bin_stride <= 128)
+      hipLaunchKernelGGL(evaluate_nodes_kernel<2>, grid, block, 0, s, h, n_nodes, n_nodes_dev,
+                         n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p, out);
+    else
+      hipLaunchKernelGGL(evaluate_nodes_kernel<4>, grid, block, 0, s, h, n_nodes, n_nodes_dev,
+                         n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p, out);
+    DP_HIP(hipGetLastError());
+    return;
+  }
   auto* cand = static_cast<FeatCand*>(scratch);
   const int64_t groups = (n_features + kFeatWaves - 1) / kFeatWaves;
   const int64_t items = int64_t(n_nodes) * groups;

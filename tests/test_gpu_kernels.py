@@ -207,12 +207,14 @@ def test_gathered_histograms_and_subtraction(dp, oracle, ws, device):
     np.testing.assert_array_equal(sib.cpu().numpy(), hn_[4])
 
 
-def test_split_evaluation_bit_exact(dp, oracle, ws, device):
+# 128 features: feature-parallel items, then a select kernel; 8: one workgroup per node
+@pytest.mark.parametrize("config,f", [(3, 128), (1, 8)])
+def test_split_evaluation_bit_exact(dp, oracle, ws, device, config, f):
     import torch
     from dpgbdt import ops
 
-    n, f = 30000, 128
-    values, _, g, h = _synth(ops, 3, n, 17, f, grad=True)
+    n = 30000
+    values, _, g, h = _synth(ops, config, n, 17, f, grad=True)
     lay, bins, o_bins, cut_ptr, cuts, n_bins, mb = _prepare(dp, oracle, ws, values)
     stride = int(n_bins.max())
     gn, hn = g.cpu().numpy(), h.cpu().numpy()
