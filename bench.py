@@ -10,7 +10,8 @@ The same JSON line carries
   roofline      the histogram operation's algorithmic bytes per launch over
                 its average duration (HIP events on the launch stream around
                 dp_hist_accumulate, i.e. hist_kernel + hist_reduce_kernel),
-                against the 8 TB/s HBM3E peak;
+                against the 8 TB/s HBM3E peak, and beside it the LDS atomic roof
+                (libdp_roof.so: the same LDS addressing with no global loads);
   trees_per_s   full boosting rounds on every configuration: C1 (10k x 8,
                 depth 6, 10 trees, logistic), C2 (1M x 28, depth 8, 100 trees,
                 logistic), C3 (10M x 128, depth 8, 20 trees, injected
@@ -121,6 +122,37 @@ def hist_leg(args, torch, dp, ops):
         sample = (sample_bins, np.ascontiguousarray(gq[:, 0]), np.ascontiguousarray(gq[:, 1]),
                   stride, hist, exps, sums)
     return out, sample, ws, bins, lay, gp, stride
+
+
+def lds_roof_leg(torch, elements):
+    """LDS atomic roof (libdp_roof.so): the histogram kernel's LDS addressing with no
+    global loads, timed per mode and scaled to `elements` row-features.  Mode 0 (two
+    64-bit atomics per element) is the exact accumulation the histogram kernel does."""
+    import ctypes
+
+    path = os.path.join(ROOT, "decision-programs_amd", "lib", "libdp_roof.so")
+    if not os.path.exists(path):
+        log("libdp_roof.so not built; LDS roof not measured")
+        return None
+    lib = ctypes.CDLL(path)
+    lib.dp_roof_lds_atomics.argtypes = [ctypes.c_int] * 4 + [ctypes.c_void_p,
+                                                            ctypes.POINTER(ctypes.c_float),
+                                                            ctypes.c_void_p]
+    grid, rows = 4096, 20
+    probe_elements = grid * 1024 * rows * 16
+    out = torch.empty(grid * 1024, dtype=torch.int64, device="cuda:0")
+    stream = torch.cuda.current_stream().cuda_stream
+    names = ["two_u64", "one_u64", "two_u32", "one_u32", "no_lds"]
+    res = {}
+    for mode, name in enumerate(names):
+        ms = ctypes.c_float()
+        rc = lib.dp_roof_lds_atomics(mode, grid, rows, 4, out.data_ptr(), ctypes.byref(ms),
+                                     stream)
+        if rc != 0:
+            raise RuntimeError(f"dp_roof_lds_atomics failed ({rc})")
+        res[name + "_ms"] = ms.value * elements / probe_elements
+    torch.cuda.synchronize()
+    return res
 
 
 def cpu_leg(sample, args):
@@ -270,6 +302,14 @@ def main():
         return
     hist, sample, *_ = hist_leg(args, torch, dp, ops)
     log(f"hist: {hist['avg_ms']:.3f} ms/launch, {hist['achieved_gbs']:.0f} GB/s algorithmic")
+    roof = lds_roof_leg(torch, hist["n"] * hist["f"])
+    if roof:
+        roof["frac"] = roof["two_u64_ms"] / hist["avg_ms"]
+        roof["note"] = ("LDS atomic roof at this pass's row-features: the histogram's exact "
+                        "accumulation (two 64-bit LDS atomics per element) with no global "
+                        "loads; frac = roof time / measured launch time")
+        log(f"LDS roof (two 64-bit atomics): {roof['two_u64_ms']:.3f} ms, "
+            f"{100 * roof['frac']:.0f}% reached")
     trees = {}
     if args.mode == "full":
         for name in names:
@@ -312,6 +352,7 @@ def main():
                      "kernel": "dp_hist_accumulate = dp::hist_kernel<false, false> + "
                                "dp::hist_reduce_kernel",
                      "algorithmic_bytes_per_launch": hist["algorithmic_bytes"],
+                     "lds_atomic_roof": roof,
                      "avg_launch_ms": hist["avg_ms"]},
         "trees_per_s": trees,
         "cpu_baseline": cpu,
