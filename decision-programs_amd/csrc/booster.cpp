@@ -165,8 +165,6 @@ Quantized& DMatrix::quantize(int32_t max_bin, dp_workspace_s& ws, hipStream_t s)
   launch_bin_values(values.p, q->layout, q->d_cut_ptr.p, q->d_cut_values.p, q->bins.p, s);
   q->cols.resize(size_t(n_rows) * size_t(n_features));
   launch_tiles_to_columns(q->bins.p, q->layout, q->cols.p, s);
-  q->rows.resize(dp_layout_bytes(&q->layout));
-  launch_tiles_to_rows(q->bins.p, q->layout, q->rows.p, s);
   DP_HIP(hipStreamSynchronize(s));
   auto& ref = *q;
   quantized.emplace(max_bin, std::move(q));
@@ -213,7 +211,7 @@ Grower::~Grower() = default;
 
 void Grower::ensure_level(const Quantized& q, int64_t nb, int32_t d, int32_t D) {
   const int64_t N = q.layout.n_rows;
-  const int32_t T = q.layout.n_tiles;
+  const int32_t T = tiles_;
   const int64_t S = int64_t(q.layout.n_features) * q.bin_stride * 2;
   const int cur = d & 1, nxt = cur ^ 1;
   const int64_t nn = d < D ? std::min(2 * nb, N) : 0;  // next level's bound
@@ -238,8 +236,12 @@ void Grower::ensure_level(const Quantized& q, int64_t nb, int32_t d, int32_t D) 
   leaf_work_[cur].reserve(size_t(plan_leaf_capacity(nb, N, chunk_)));
 }
 
-void Grower::prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, hipStream_t s) {
+void Grower::prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, bool sparse,
+                     hipStream_t s) {
   const dp_bin_layout& L = q.layout;
+  need(sparse ? q.sparse.n_tiles > 0 : q.rows.n > 0, "histogram layout not built");
+  sparse_ = sparse;
+  tiles_ = sparse ? q.sparse.n_tiles : L.n_tiles;
   const int64_t N = L.n_rows;
   const int32_t D = p.max_depth;
   const int64_t S = int64_t(L.n_features) * q.bin_stride * 2;
@@ -258,20 +260,22 @@ void Grower::prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, h
   part_work_[0].reserve(size_t(plan_part_capacity(1, N, chunk_)));
   part_first_[0].reserve(2);
   node_left_[0].reserve(1);
-  partial_.reserve(size_t(hist_partial_capacity(L.n_tiles) * q.bin_stride * 32));
-  if (root_rows_ != N || root_tiles_ != L.n_tiles) {
+  const int64_t slot_words = sparse ? int64_t(q.sparse.tile_features) * q.bin_stride * 2
+                                    : int64_t(q.bin_stride) * 32;
+  partial_.reserve(size_t(hist_partial_capacity(tiles_) * slot_words));
+  if (root_rows_ != N || root_tiles_ != tiles_) {
     const int64_t b = 0, e = N;
     const int32_t slot = 0;
     std::vector<HistWork> w;
     std::vector<HistReduce> j;
-    make_hist_work(L, &b, &e, &slot, 1, true, w, j);
+    make_hist_work(L, &b, &e, &slot, 1, true, w, j, tiles_);
     root_work_.resize(w.size());
     root_job_.resize(j.size());
     DP_HIP(hipMemcpy(root_work_.p, w.data(), sizeof(HistWork) * w.size(), hipMemcpyHostToDevice));
     DP_HIP(hipMemcpy(root_job_.p, j.data(), sizeof(HistReduce) * j.size(), hipMemcpyHostToDevice));
     root_items_ = int32_t(w.size());
     root_rows_ = N;
-    root_tiles_ = L.n_tiles;
+    root_tiles_ = tiles_;
   }
   const int64_t widest = level_bound(D, N), widest_hist = level_bound(D - 1, N);
   eager_ = widest <= kEagerNodes && 2 * widest_hist * S * int64_t(sizeof(int64_t)) <= kEagerHistBytes;
@@ -300,7 +304,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
                   int32_t* positions, int32_t slot, hipStream_t s) {
   const dp_bin_layout& L = q.layout;
   const int64_t N = L.n_rows;
-  const int32_t F = L.n_features, B = q.bin_stride, T = L.n_tiles, D = p.max_depth;
+  const int32_t F = L.n_features, B = q.bin_stride, T = tiles_, D = p.max_depth;
   const int64_t S = int64_t(F) * B * 2;  // int64 values per node histogram
   const dp_train_param dtp{p.eta, p.lambda, p.alpha, p.gamma, p.min_child_weight, p.max_depth};
   // Eager trees keep their counters and node records in their own slot, so
@@ -342,10 +346,21 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     const bool split = d < D;
     int64_t* h = hist_[cur].p;
     if (split) {
-      if (d == 0) {
+      const int32_t tf = q.sparse.tile_features;
+      if (d == 0 && sparse_) {
+        launch_hist_sparse(q.sparse, N, F, gpair, nullptr, root_work_.p, root_items_, nullptr, B,
+                           h, partial_.p, s);
+        launch_hist_reduce_flat(partial_.p, root_job_.p, 1, nullptr, T, tf, F, B, nullptr, h, s);
+      } else if (d == 0) {
         launch_hist(q.bins.p, L, gpair, nullptr, root_work_.p, root_items_, nullptr, B, h,
                     partial_.p, s);
         launch_hist_reduce(partial_.p, root_job_.p, 1, nullptr, T, F, B, nullptr, h, false, s);
+      } else if (sparse_) {
+        launch_hist_sparse(q.sparse, N, F, gpair, ridx_[cur].p, hist_work_[cur].p,
+                           int32_t(plan_hist_items(nb, N, T)), field(c, &PlanCounts::n_hist), B,
+                           h, partial_.p, s);
+        launch_hist_reduce_flat(partial_.p, reduce_jobs_[cur].p, int32_t(nb / 2 + 1),
+                                field(c, &PlanCounts::n_reduce), T, tf, F, B, hist_[nxt].p, h, s);
       } else {
         launch_hist(q.bins.p, L, gpair, ridx_[cur].p, hist_work_[cur].p,
                     int32_t(plan_hist_items(nb, N, T)), field(c, &PlanCounts::n_hist), B, h,
@@ -458,7 +473,8 @@ uint64_t Grower::signature() const {
   }
   buf(root_work_); buf(root_job_); buf(partial_); buf(pair_chunk_); buf(work_left_);
   buf(splits_); buf(eval_scratch_); buf(info_); buf(counts_); buf(slots_);
-  mix(uint64_t(eager_)); mix(uint64_t(node_cap_)); mix(uint64_t(chunk_));
+  mix(uint64_t(eager_)); mix(uint64_t(sparse_)); mix(uint64_t(tiles_));
+  mix(uint64_t(node_cap_)); mix(uint64_t(chunk_));
   mix(uint64_t(slot_bytes_)); mix(uint64_t(root_rows_)); mix(uint64_t(root_tiles_));
   mix(uint64_t(root_items_));
   return h;
@@ -534,7 +550,7 @@ void Booster::set_param(const std::string& key, const std::string& value) {
       "min_split_loss", "min_child_weight", "subsample", "colsample_bytree", "colsample_bylevel",
       "colsample_bynode", "base_score", "boost_from_average", "seed", "seed_per_iteration",
       "nthread", "verbosity", "validate_parameters", "grow_policy", "dp_record_positions",
-      "dp_graphs"};
+      "dp_graphs", "dp_sparse_hist"};
   bool ok = false;
   for (const char* k : known) ok = ok || key == k;
   need(ok, "unsupported parameter: " + key);
@@ -553,6 +569,11 @@ void Booster::set_param(const std::string& key, const std::string& value) {
   params_[key] = value;
   if (key == "dp_record_positions") record_positions_ = parse_int(key, value) != 0;
   if (key == "dp_graphs") use_graphs_ = parse_int(key, value) != 0;
+  if (key == "dp_sparse_hist") {
+    const int32_t m = parse_int(key, value);
+    need(m >= 0 && m <= 2, "dp_sparse_hist must be 0, 1 or 2");
+    sparse_mode_ = m;
+  }
 }
 
 void Booster::configure(DMatrix* d) {
@@ -726,7 +747,7 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
   // Host inputs that size buffers: when they change, the round in flight is
   // collected first, so no buffer it uses moves under it.
   std::vector<uint64_t> inputs = {reinterpret_cast<uint64_t>(d), uint64_t(record_positions_),
-                                  uint64_t(n_groups_)};
+                                  uint64_t(n_groups_), uint64_t(sparse_mode_)};
   auto words = [](std::vector<uint64_t>& v, const void* p, size_t n) {
     for (size_t i = 0; i < n; i += 8) {
       uint64_t w = 0;
@@ -742,8 +763,23 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
     qp = &d->quantize(tp_.max_bin, scratch, stream_);
   }
   Quantized& q = *qp;
+  // Histogram layout: the present-value layout for mostly-missing matrices,
+  // else the row-major copy of the tiles for gathered rows.
+  bool sparse = false;
+  if (sparse_mode_ != 0 && q.layout.missing_bin >= 0) {
+    const double limit = sparse_mode_ == 2 ? 1.0 : kSparseDensity;
+    if (q.sparse.n_tiles == 0 && q.sparse_limit < limit) {
+      q.density = build_sparse_bins(q.bins.p, q.layout, q.bin_stride, limit, q.sparse, stream_);
+      q.sparse_limit = limit;
+    }
+    sparse = q.sparse.n_tiles > 0;
+  }
+  if (!sparse && q.rows.n == 0) {
+    q.rows.resize(dp_layout_bytes(&q.layout));
+    launch_tiles_to_rows(q.bins.p, q.layout, q.rows.p, stream_);
+  }
   if (record_positions_) positions_.reserve(size_t(N));
-  grower_->prepare(q, tp_, n_groups_, stream_);
+  grower_->prepare(q, tp_, n_groups_, sparse, stream_);
   // Level-synced trees copy their records during grow(): collect the round in
   // flight before they are overwritten.
   if (!grower_->eager()) flush();
@@ -760,7 +796,8 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
       reinterpret_cast<uint64_t>(grad_.p), reinterpret_cast<uint64_t>(hess_.p),
       reinterpret_cast<uint64_t>(gpair_.p), reinterpret_cast<uint64_t>(exps_.p),
       reinterpret_cast<uint64_t>(sums_.p), reinterpret_cast<uint64_t>(quant_scratch_.p),
-      reinterpret_cast<uint64_t>(positions), grower_->signature()};
+      reinterpret_cast<uint64_t>(positions), reinterpret_cast<uint64_t>(q.sparse.ptr.p),
+      reinterpret_cast<uint64_t>(q.sparse.entries.p), uint64_t(sparse), grower_->signature()};
   words(key, &q.layout, sizeof q.layout);
   words(key, &tp_, sizeof tp_);
   enqueue(key, grower_->eager(), [&] {
@@ -1167,6 +1204,7 @@ std::unique_ptr<Booster> Booster::slice(int begin, int end, int step) const {
   out->params_ = params_;
   out->params_.erase("dp_record_positions");
   out->params_.erase("dp_graphs");
+  out->params_.erase("dp_sparse_hist");
   out->objective_ = effective_objective();
   out->objective_id_ = objective_id_;
   out->n_groups_ = n_groups_;

@@ -22,7 +22,10 @@ struct Quantized {
   DeviceBuffer<float> d_cut_values;
   DeviceBuffer<uint8_t> bins;
   DeviceBuffer<uint8_t> cols;  // column-major copy: cols[f * n_rows + r]
-  DeviceBuffer<uint8_t> rows;  // row-major copy: rows[(r * n_tiles + t) * 16 + j]
+  DeviceBuffer<uint8_t> rows;  // row-major copy: rows[(r * n_tiles + t) * 16 + j] (on demand)
+  SparseBins sparse;           // present-value layout (on demand, mostly-missing matrices)
+  double sparse_limit = -1.0;  // largest density limit the layout was tried with
+  double density = -1.0;       // share of present values, once counted
 };
 
 struct DMatrix {
@@ -65,7 +68,10 @@ class Grower {
   ~Grower();
   // Sizes the buffers for trees over `q` with parameters `p`, with `n_slots`
   // trees in flight before the caller synchronises.
-  void prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, hipStream_t s);
+  // sparse: build histograms from q.sparse (which must be built) instead of
+  // the 16-feature tiles and the row-major copy (which must then be built).
+  void prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, bool sparse,
+               hipStream_t s);
   // Enqueues one tree.  gpair: [n_rows][2] fixed-point gradients of one output;
   // exps (device): its two quantiser exponents; root_sums (device): the int64
   // sums of gpair.  Adds the leaf values to margin[r * stride] and, when
@@ -108,6 +114,8 @@ class Grower {
   std::vector<std::vector<NodeInfo>> spill_;  // slots of trees grown level-synced
   std::vector<PlanCounts> spill_counts_;
   bool eager_ = true;
+  bool sparse_ = false;  // histograms from the present-value layout
+  int32_t tiles_ = 0;    // histogram tiles per row chunk (16-feature or sparse tiles)
   int64_t node_cap_ = 0;
   int64_t chunk_ = kPartChunk;  // rows per partition / margin-update item
   size_t slot_bytes_ = 0;
@@ -196,6 +204,7 @@ class Booster {
   PinnedBuffer exps_host_;  // two buffers, by round parity
   bool record_positions_ = false;
   bool use_graphs_ = true;
+  int32_t sparse_mode_ = 1;  // dp_sparse_hist: 0 never, 1 when <= 1/4 present, 2 with any NaN
   bool labels_checked_ = false;
   std::vector<std::pair<std::vector<uint64_t>, hipGraphExec_t>> graphs_;  // newest last
   hipStream_t stream_ = nullptr;

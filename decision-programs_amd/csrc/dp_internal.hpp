@@ -243,10 +243,12 @@ inline int64_t hist_partial_capacity(int32_t n_tiles) { return 2048 + int64_t(n_
 // [begin[i], end[i]) of ridx, written to hist slot slots[i], or i when slots
 // is null), chunked and ordered for the XCD-aware dispatch; the work may hold
 // empty padding items.  allow_direct: single-chunk nodes write directly.
+// n_tiles > 0 overrides the layout's tile count (present-value tiles).
 // Returns the number of partial slots used.
 int32_t make_hist_work(const dp_bin_layout& layout, const int64_t* begin, const int64_t* end,
                        const int32_t* slots, int32_t n_nodes, bool allow_direct,
-                       std::vector<HistWork>& work, std::vector<HistReduce>& jobs);
+                       std::vector<HistWork>& work, std::vector<HistReduce>& jobs,
+                       int32_t n_tiles = 0);
 void launch_subtract(const int64_t* parent, const int64_t* built, int64_t* sibling, int64_t n,
                      hipStream_t s);
 
@@ -375,6 +377,38 @@ void launch_quantise(const float* grad, const float* hess, int64_t n_rows, int32
 void launch_bin_values(const float* values, const dp_bin_layout& layout, const int32_t* cut_ptr,
                        const float* cut_values, uint8_t* bins, hipStream_t s);
 // cols[f * n_rows + r] = bin of (r, f), from the tile-major bins.
+// Present-value layout of a mostly-missing matrix.  Features are grouped in
+// tiles of tile_features (a multiple of 16, at most 256, sized so that one
+// tile's histogram fills kSparseLdsBytes of LDS).  For tile t and row r the
+// row's present values in the tile are
+//   entries[ptr[t * n_rows + r] .. ptr[t * n_rows + r + 1])
+// in feature order, each (feature - t * tile_features) << 8 | bin.
+struct SparseBins {
+  int32_t tile_features = 0, n_tiles = 0;  // n_tiles 0: not built
+  int64_t nnz = 0;
+  DeviceBuffer<uint32_t> ptr;      // [n_tiles * n_rows + 1]
+  DeviceBuffer<uint16_t> entries;  // [nnz]
+};
+constexpr int64_t kSparseLdsBytes = 128 * 1024;
+constexpr double kSparseDensity = 0.25;  // automatic use: at most this share present
+int32_t sparse_tile_features(int32_t bin_stride);
+// Counts the present values of `bins` (16-feature tiles, missing byte 255) and
+// builds `out` when their share is at most max_density (and the count fits
+// 32-bit offsets); returns the share.  Synchronises the stream.
+double build_sparse_bins(const uint8_t* bins, const dp_bin_layout& layout, int32_t bin_stride,
+                         double max_density, SparseBins& out, hipStream_t s);
+// Histograms from the present-value layout: work items as for launch_hist,
+// with `tile` a sparse tile; partial slots of tile_features * bin_stride * 2
+// words in the node histogram's layout.  Finished by launch_hist_reduce_flat.
+void launch_hist_sparse(const SparseBins& sp, int64_t n_rows, int32_t n_features,
+                        const int32_t* gpair, const uint32_t* ridx, const HistWork* work,
+                        int32_t n_work, const int32_t* n_work_dev, int32_t bin_stride,
+                        int64_t* hist, int64_t* partial, hipStream_t s);
+void launch_hist_reduce_flat(const int64_t* partial, const HistReduce* jobs, int32_t n_jobs,
+                             const int32_t* n_jobs_dev, int32_t n_tiles, int32_t tile_features,
+                             int32_t n_features, int32_t bin_stride, const int64_t* parent_base,
+                             int64_t* hist, hipStream_t s);
+
 void launch_tiles_to_columns(const uint8_t* bins, const dp_bin_layout& layout, uint8_t* cols,
                              hipStream_t s);
 // rows[r * n_tiles * 16 + t * 16 + j] = tile t's byte j of row r.

@@ -205,6 +205,96 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8,
   }
 }
 
+// Histograms from the present-value layout (SparseBins): one work item = rows
+// [begin, end) of node `slot` for one sparse tile of tile_features features.
+// The tile's histogram lives in LDS as the node histogram's own layout,
+// [feature][bin][g, h] int64 (tile_features * bin_stride * 16 bytes, dynamic
+// LDS), so the store is one contiguous copy.  A lane takes one row at a time
+// and walks the row's present values in the tile (two 64-bit LDS atomics
+// each); rows without values in the tile cost two loads.  The per-lane trip
+// counts differ, but no barrier sits inside the row loop.
+template <bool GATHER>
+__global__ __launch_bounds__(kHistThreads) void hist_sparse_kernel(
+    const uint32_t* __restrict__ ptr, const uint16_t* __restrict__ entries, int64_t n_rows,
+    int32_t n_features, int32_t tile_features, const int2* __restrict__ gpair,
+    const uint32_t* __restrict__ ridx, const HistWork* __restrict__ work, int32_t n_work_host,
+    const int32_t* __restrict__ n_work_dev, int32_t bin_stride,
+    unsigned long long* __restrict__ hist, unsigned long long* __restrict__ partial) {
+  extern __shared__ unsigned long long lds_tile[];
+  const int32_t n_work = n_work_dev ? *n_work_dev : n_work_host;
+  const int64_t slot_words = int64_t(tile_features) * bin_stride * 2;
+  for (int32_t item = blockIdx.x; item < n_work; item += gridDim.x) {
+    const HistWork w = work[item];
+    if (w.begin >= w.end) continue;  // padding item (uniform per workgroup)
+    const int32_t f0 = w.tile * tile_features;
+    const int32_t nf = f0 + tile_features < n_features ? tile_features : n_features - f0;
+    const int32_t words = nf * bin_stride * 2;
+    for (int e = threadIdx.x; e < words; e += kHistThreads) lds_tile[e] = 0ull;
+    __syncthreads();
+    const uint32_t* tp = ptr + int64_t(w.tile) * n_rows;
+    for (int64_t i = w.begin + threadIdx.x; i < w.end; i += kHistThreads) {
+      const uint32_t r = GATHER ? ridx[i] : uint32_t(i);
+      const uint32_t b = tp[r], e = tp[r + 1];
+      const int2 q = gpair[r];
+      const unsigned long long g = (unsigned long long)(long long)q.x;
+      const unsigned long long h = (unsigned long long)(long long)q.y;
+      for (uint32_t j = b; j < e; ++j) {
+        const uint32_t v = entries[j];
+        lds_u64* p = (lds_u64*)lds_tile + ((v >> 8) * uint32_t(bin_stride) + (v & 0xffu)) * 2u;
+        lds_add(p, g);
+        lds_add(p + 1, h);
+      }
+    }
+    __syncthreads();
+    unsigned long long* out =
+        w.partial >= 0 ? partial + int64_t(w.partial) * slot_words
+                       : hist + (int64_t(w.slot) * n_features + f0) * bin_stride * 2;
+    for (int e = threadIdx.x; e < words; e += kHistThreads) out[e] = lds_tile[e];
+    __syncthreads();  // the next item clears the LDS this item just read
+  }
+}
+
+// Reduce for the present-value path: partial slots hold a sparse tile in the
+// node histogram's layout, so word e of tile t is word t * tile_features *
+// bin_stride * 2 + e of the node histogram.  Otherwise as hist_reduce_kernel.
+__global__ __launch_bounds__(256) void hist_reduce_flat_kernel(
+    const long long* __restrict__ partial, const HistReduce* __restrict__ jobs,
+    int32_t n_jobs_host, const int32_t* __restrict__ n_jobs_dev, int32_t n_tiles,
+    int32_t tile_features, int32_t n_features, int32_t bin_stride,
+    const long long* __restrict__ parent_base, long long* __restrict__ hist) {
+  const int32_t n_jobs = n_jobs_dev ? *n_jobs_dev : n_jobs_host;
+  const int t = blockIdx.y;
+  const int32_t f0 = t * tile_features;
+  const int32_t nf = f0 + tile_features < n_features ? tile_features : n_features - f0;
+  const int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (e >= int64_t(nf) * bin_stride * 2) return;  // no barriers below
+  const int64_t slot_words = int64_t(tile_features) * bin_stride * 2;
+  const int64_t node_elems = int64_t(n_features) * bin_stride * 2;
+  const int64_t at = int64_t(f0) * bin_stride * 2 + e;
+  for (int32_t jb = blockIdx.z; jb < n_jobs; jb += gridDim.z) {
+    const HistReduce j = jobs[jb];
+    long long* built = hist + int64_t(j.slot) * node_elems + at;
+    long long sum;
+    if (j.nc == 1 && j.p0 < 0) {
+      sum = *built;  // written directly by the node's only chunk
+    } else {
+      long long acc[4] = {0, 0, 0, 0};
+      const long long* src = partial + (int64_t(j.p0) * n_tiles + t) * slot_words + e;
+      const int64_t step = int64_t(n_tiles) * slot_words;
+      int k = 0;
+      for (; k + 4 <= j.nc; k += 4) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[u] += src[(k + u) * step];
+      }
+      for (; k < j.nc; ++k) acc[0] += src[k * step];
+      sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+      *built = sum;
+    }
+    if (j.sibling >= 0)
+      hist[int64_t(j.sibling) * node_elems + at] = parent_base[j.parent + at] - sum;
+  }
+}
+
 __global__ void zero_i64_dev_kernel(int64_t* __restrict__ p, const int32_t* __restrict__ n_dev,
                                     int64_t per) {
   const int64_t n = int64_t(*n_dev) * per;
@@ -286,12 +376,14 @@ void launch_iota_u32(uint32_t* p, int64_t n, hipStream_t s) {
 
 int32_t make_hist_work(const dp_bin_layout& layout, const int64_t* begin, const int64_t* end,
                        const int32_t* slots, int32_t n_nodes, bool allow_direct,
-                       std::vector<HistWork>& work, std::vector<HistReduce>& jobs) {
+                       std::vector<HistWork>& work, std::vector<HistReduce>& jobs,
+                       int32_t n_tiles) {
+  const int64_t T = n_tiles > 0 ? n_tiles : layout.n_tiles;
   // About 1024 items (two waves of 2 workgroups per CU on 256 CUs), at least
   // kHistMinChunk rows each, so the per-item LDS clear and store stay small.
   int64_t total = 0;
   for (int32_t i = 0; i < n_nodes; ++i) total += end[i] - begin[i];
-  const int64_t chunk = hist_chunk(total, layout.n_tiles);
+  const int64_t chunk = hist_chunk(total, int32_t(T));
   struct Chunk {
     int32_t slot, partial;
     int64_t b, e;
@@ -314,7 +406,6 @@ int32_t make_hist_work(const dp_bin_layout& layout, const int64_t* begin, const 
   // order puts the tiles of one row chunk on the same XCD in consecutive
   // dispatch slots, so that chunk's gradient pairs are read from HBM once and
   // then hit that XCD's L2.
-  const int64_t T = layout.n_tiles;
   const int64_t groups = (int64_t(chunks.size()) + 7) / 8;
   work.assign(size_t(groups * T * 8), HistWork{0, 0, 0, 0, -1, 0});
   for (int64_t c = 0; c < int64_t(chunks.size()); ++c)
@@ -387,6 +478,49 @@ void launch_hist_reduce(const int64_t* partial, const HistReduce* jobs, int32_t 
                      n_tiles, n_features, bin_stride,
                      reinterpret_cast<const long long*>(parent_base),
                      reinterpret_cast<long long*>(hist), accumulate ? 1 : 0);
+  DP_HIP(hipGetLastError());
+}
+
+void launch_hist_sparse(const SparseBins& sp, int64_t n_rows, int32_t n_features,
+                        const int32_t* gpair, const uint32_t* ridx, const HistWork* work,
+                        int32_t n_work, const int32_t* n_work_dev, int32_t bin_stride,
+                        int64_t* hist, int64_t* partial, hipStream_t s) {
+  if (n_work <= 0) return;
+  need(sp.n_tiles > 0, "present-value layout not built");
+  need(bin_stride >= 1 && bin_stride <= kMaxBins, "histogram bin stride out of range");
+  const size_t lds = size_t(sp.tile_features) * size_t(bin_stride) * 16;
+  need(lds <= size_t(kSparseLdsBytes), "sparse tile exceeds its LDS budget");
+  auto kernel = ridx ? hist_sparse_kernel<true> : hist_sparse_kernel<false>;
+  static bool attr_set[2] = {false, false};
+  if (!attr_set[ridx ? 1 : 0]) {
+    DP_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, int(kSparseLdsBytes)));
+    attr_set[ridx ? 1 : 0] = true;
+  }
+  // One workgroup per CU (the tile's LDS), a multiple of 8 for the XCD order.
+  int grid = n_work < 512 ? n_work : 512;
+  grid = (grid + 7) / 8 * 8;
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(kHistThreads), lds, s, sp.ptr.p, sp.entries.p,
+                     n_rows, n_features, sp.tile_features, reinterpret_cast<const int2*>(gpair),
+                     ridx, work, n_work, n_work_dev, bin_stride,
+                     reinterpret_cast<unsigned long long*>(hist),
+                     reinterpret_cast<unsigned long long*>(partial));
+  DP_HIP(hipGetLastError());
+}
+
+void launch_hist_reduce_flat(const int64_t* partial, const HistReduce* jobs, int32_t n_jobs,
+                             const int32_t* n_jobs_dev, int32_t n_tiles, int32_t tile_features,
+                             int32_t n_features, int32_t bin_stride, const int64_t* parent_base,
+                             int64_t* hist, hipStream_t s) {
+  if (n_jobs <= 0) return;
+  const int64_t words = int64_t(tile_features) * bin_stride * 2;
+  const dim3 grid(unsigned((words + 255) / 256), unsigned(n_tiles),
+                  unsigned(n_jobs < 64 ? n_jobs : 64));
+  hipLaunchKernelGGL(hist_reduce_flat_kernel, grid, dim3(256), 0, s,
+                     reinterpret_cast<const long long*>(partial), jobs, n_jobs, n_jobs_dev,
+                     n_tiles, tile_features, n_features, bin_stride,
+                     reinterpret_cast<const long long*>(parent_base),
+                     reinterpret_cast<long long*>(hist));
   DP_HIP(hipGetLastError());
 }
 

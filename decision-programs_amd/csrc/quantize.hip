@@ -15,6 +15,8 @@
 #include "dp_internal.hpp"
 
 #include <rocprim/device/device_radix_sort.hpp>
+#include <rocprim/device/device_scan.hpp>
+#include <rocprim/device/device_reduce.hpp>
 
 #include <cmath>
 
@@ -267,6 +269,65 @@ __global__ void tiles_to_rows_kernel(const uint8_t* __restrict__ bins, int64_t n
   }
 }
 
+// Present-value layout (see SparseBins): one thread per (sparse tile, row),
+// i = tile * n_rows + row.  The row's bytes of the tile's features are read
+// from the 16-feature tiles (16 bytes per dense tile); bytes of features past
+// n_features are padding, not values.
+__device__ __forceinline__ void sparse_tile_row(int64_t i, int64_t n_rows, int32_t n_features,
+                                                int32_t tile_features, int64_t& row,
+                                                int32_t& f_begin, int32_t& f_end) {
+  const int64_t t = i / n_rows;
+  row = i - t * n_rows;
+  f_begin = int32_t(t) * tile_features;
+  f_end = f_begin + tile_features < n_features ? f_begin + tile_features : n_features;
+}
+
+__global__ void sparse_count_kernel(const uint8_t* __restrict__ bins, int64_t n_rows,
+                                    int32_t n_features, int32_t tile_features, int64_t n,
+                                    int32_t missing_bin, uint32_t* __restrict__ counts) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += int64_t(blockDim.x) * gridDim.x) {
+    int64_t r;
+    int32_t fb, fe;
+    sparse_tile_row(i, n_rows, n_features, tile_features, r, fb, fe);
+    uint32_t c = 0;
+    for (int32_t d = fb / 16; d * 16 < fe; ++d) {
+      const uint4 v = *reinterpret_cast<const uint4*>(bins + (int64_t(d) * n_rows + r) * 16);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const int32_t f = d * 16 + k;
+        const uint32_t b = (w[k >> 2] >> (8 * (k & 3))) & 0xffu;
+        c += (f < fe && int32_t(b) != missing_bin) ? 1u : 0u;
+      }
+    }
+    counts[i] = c;
+  }
+}
+
+__global__ void sparse_fill_kernel(const uint8_t* __restrict__ bins, int64_t n_rows,
+                                   int32_t n_features, int32_t tile_features, int64_t n,
+                                   int32_t missing_bin, const uint32_t* __restrict__ ptr,
+                                   uint16_t* __restrict__ entries) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += int64_t(blockDim.x) * gridDim.x) {
+    int64_t r;
+    int32_t fb, fe;
+    sparse_tile_row(i, n_rows, n_features, tile_features, r, fb, fe);
+    uint32_t o = ptr[i];
+    for (int32_t d = fb / 16; d * 16 < fe; ++d) {
+      const uint4 v = *reinterpret_cast<const uint4*>(bins + (int64_t(d) * n_rows + r) * 16);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const int32_t f = d * 16 + k;
+        const uint32_t b = (w[k >> 2] >> (8 * (k & 3))) & 0xffu;
+        if (f < fe && int32_t(b) != missing_bin) entries[o++] = uint16_t(uint32_t(f - fb) << 8 | b);
+      }
+    }
+  }
+}
+
 }  // namespace
 
 void launch_tiles_to_rows(const uint8_t* bins, const dp_bin_layout& layout, uint8_t* rows,
@@ -288,6 +349,60 @@ void launch_tiles_to_columns(const uint8_t* bins, const dp_bin_layout& layout, u
   DP_HIP(hipGetLastError());
 }
 
+
+int32_t sparse_tile_features(int32_t bin_stride) {
+  int32_t t = int32_t(kSparseLdsBytes / (int64_t(bin_stride) * 16)) / 16 * 16;
+  if (t > 256) t = 256;
+  return t < 16 ? 16 : t;
+}
+
+double build_sparse_bins(const uint8_t* bins, const dp_bin_layout& layout, int32_t bin_stride,
+                         double max_density, SparseBins& out, hipStream_t s) {
+  need(layout.tile_width == 16, "present-value layout needs 16-feature tiles");
+  need(layout.missing_bin == 255, "present-value layout needs missing values");
+  const int64_t N = layout.n_rows;
+  const int32_t tf = sparse_tile_features(bin_stride);
+  const int32_t T = (layout.n_features + tf - 1) / tf;
+  const int64_t n = N * T;
+  DeviceBuffer<uint32_t> counts(size_t(n + 1)), ptr(size_t(n + 1));
+  launch_fill_u8(reinterpret_cast<uint8_t*>(counts.p + n), sizeof(uint32_t), 0, s);
+  const dim3 grid(grid_for(n, 256, 16384));
+  hipLaunchKernelGGL(sparse_count_kernel, grid, dim3(256), 0, s, bins, N, layout.n_features, tf,
+                     n, layout.missing_bin, counts.p);
+  DP_HIP(hipGetLastError());
+  // Exclusive scan over n + 1 counts (the last is 0): ptr[n] is the total.  A
+  // 64-bit accumulator catches totals that do not fit 32-bit offsets.
+  size_t temp_bytes = 0;
+  DP_HIP(rocprim::exclusive_scan(nullptr, temp_bytes, counts.p, ptr.p, 0u, size_t(n + 1),
+                                 rocprim::plus<uint32_t>(), s));
+  DeviceBuffer<uint8_t> temp(temp_bytes ? temp_bytes : 1);
+  DP_HIP(rocprim::exclusive_scan(temp.p, temp_bytes, counts.p, ptr.p, 0u, size_t(n + 1),
+                                 rocprim::plus<uint32_t>(), s));
+  DeviceBuffer<unsigned long long> total(1);
+  launch_fill_u8(reinterpret_cast<uint8_t*>(total.p), sizeof(unsigned long long), 0, s);
+  size_t sum_bytes = 0;
+  DP_HIP(rocprim::reduce(nullptr, sum_bytes, counts.p, total.p, 0ull, size_t(n),
+                         rocprim::plus<unsigned long long>(), s));
+  DeviceBuffer<uint8_t> sum_temp(sum_bytes ? sum_bytes : 1);
+  DP_HIP(rocprim::reduce(sum_temp.p, sum_bytes, counts.p, total.p, 0ull, size_t(n),
+                         rocprim::plus<unsigned long long>(), s));
+  unsigned long long nnz = 0;
+  DP_HIP(hipMemcpyAsync(&nnz, total.p, sizeof nnz, hipMemcpyDeviceToHost, s));
+  DP_HIP(hipStreamSynchronize(s));
+  const double density = double(nnz) / (double(N) * double(layout.n_features));
+  if (density > max_density || nnz >= (1ull << 32)) return density;
+  DeviceBuffer<uint16_t> entries(size_t(nnz ? nnz : 1));
+  hipLaunchKernelGGL(sparse_fill_kernel, grid, dim3(256), 0, s, bins, N, layout.n_features, tf, n,
+                     layout.missing_bin, ptr.p, entries.p);
+  DP_HIP(hipGetLastError());
+  DP_HIP(hipStreamSynchronize(s));
+  out.tile_features = tf;
+  out.n_tiles = T;
+  out.nnz = int64_t(nnz);
+  out.ptr = std::move(ptr);
+  out.entries = std::move(entries);
+  return density;
+}
 
 void launch_any_nan(const float* values, int64_t n, int32_t* flag, hipStream_t s) {
   launch_fill_u8(reinterpret_cast<uint8_t*>(flag), 4, 0, s);

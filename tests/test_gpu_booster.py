@@ -20,11 +20,13 @@ TREE_KEYS_BITS = ["split_condition", "base_weight", "sum_hess"]
 
 
 def _train_both(dp, oracle, device, config, n, f, objective, k, p, rounds, seed, injected=False,
-                max_bin=256, base_score=None):
+                max_bin=256, base_score=None, extra=None, mutate=None):
     import torch
     from dpgbdt import ops
 
     values, labels, g, h = ops.synth(config, n, seed, n_features=f, want_grad=injected)
+    if mutate is not None:
+        values = mutate(values)
     obj_name = {0: "binary:logistic", 1: "multi:softmax", 2: "reg:squarederror"}[objective]
     dtrain = dp.DMatrix(values, labels)
     params = {"objective": obj_name, "tree_method": "hist", "device": "cuda:0", "max_bin": max_bin,
@@ -35,6 +37,7 @@ def _train_both(dp, oracle, device, config, n, f, objective, k, p, rounds, seed,
         params["num_class"] = k
     if base_score is not None:
         params["base_score"] = base_score
+    params.update(extra or {})
     bst = dp.Booster(params, [dtrain])
     gpu_positions = []
     for r in range(rounds):
@@ -140,14 +143,38 @@ def test_c4_reduced_softmax(dp, oracle, device):
     assert model["learner"]["gradient_booster"]["model"]["iteration_indptr"] == [0, 10, 20]
 
 
-def test_c5_reduced_missing_squared(dp, oracle, device):
+# dp_sparse_hist 1: histograms from the present-value layout (5 % present); 0: dense tiles
+@pytest.mark.parametrize("sparse", [1, 0])
+def test_c5_reduced_missing_squared(dp, oracle, device, sparse):
     p = {"max_depth": 7, "eta": 0.3}
     bst, x, o_trees, o_margin, pos, n = _train_both(dp, oracle, device, 5, 6000, 120, 2, 1, p, 3,
-                                                    20261205, max_bin=65)
+                                                    20261205, max_bin=65,
+                                                    extra={"dp_sparse_hist": sparse})
     _compare(bst, o_trees, o_margin, pos, n, 1)
     assert any(t["default_left"].any() for t in o_trees), "learned default direction unused"
     m = _predict_model(json.loads(bst.save_raw()), x, 1, [0.0])
     np.testing.assert_array_equal(m.view(np.uint32), o_margin.view(np.uint32))
+
+
+@pytest.mark.parametrize("max_bin,f", [(256, 50), (64, 300)])
+def test_present_value_histograms_forced(dp, oracle, device, max_bin, f):
+    """The present-value layout forced on a matrix with 40 % missing values: 32- and 128-feature
+    sparse tiles with a partial last tile, multi-chunk nodes (partial slots) and single-chunk
+    nodes (direct stores), against the oracle."""
+    import torch
+
+    def holes(v):
+        g = torch.Generator(device="cpu").manual_seed(11)
+        m = torch.rand(v.shape, generator=g) < 0.4
+        v = v.clone()
+        v[m.to(v.device)] = float("nan")
+        return v
+
+    p = {"max_depth": 6, "eta": 0.3}
+    bst, x, o_trees, o_margin, pos, n = _train_both(dp, oracle, device, 1, 40000, f, 0, 1, p, 2,
+                                                    20261207, max_bin=max_bin,
+                                                    extra={"dp_sparse_hist": 2}, mutate=holes)
+    _compare(bst, o_trees, o_margin, pos, n, 1)
 
 
 def test_c3_reduced_injected_gradients(dp, oracle, device):
