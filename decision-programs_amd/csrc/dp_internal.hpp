@@ -389,7 +389,7 @@ struct SparseBins {
   DeviceBuffer<uint32_t> ptr;      // [n_tiles * n_rows + 1]
   DeviceBuffer<uint16_t> entries;  // [nnz]
 };
-constexpr int64_t kSparseLdsBytes = 128 * 1024;
+constexpr int64_t kSparseLdsBytes = 64 * 1024;
 constexpr double kSparseDensity = 0.25;  // automatic use: at most this share present
 int32_t sparse_tile_features(int32_t bin_stride);
 // Counts the present values of `bins` (16-feature tiles, missing byte 255) and

@@ -211,8 +211,12 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8,
 // [feature][bin][g, h] int64 (tile_features * bin_stride * 16 bytes, dynamic
 // LDS), so the store is one contiguous copy.  A lane takes one row at a time
 // and walks the row's present values in the tile (two 64-bit LDS atomics
-// each); rows without values in the tile cost two loads.  The per-lane trip
-// counts differ, but no barrier sits inside the row loop.
+// each), loading kSparseBatch entries at once.  The lane's rows are
+// software-pipelined: while row i's entries are accumulated, the row id of
+// row i + 2 * 1024 and the entry range and (g, h) of row i + 1024 are in
+// flight.  Per-lane trip counts differ; no barrier sits inside the row loop.
+constexpr int kSparseBatch = 4;
+
 template <bool GATHER>
 __global__ __launch_bounds__(kHistThreads) void hist_sparse_kernel(
     const uint32_t* __restrict__ ptr, const uint16_t* __restrict__ entries, int64_t n_rows,
@@ -223,6 +227,7 @@ __global__ __launch_bounds__(kHistThreads) void hist_sparse_kernel(
   extern __shared__ unsigned long long lds_tile[];
   const int32_t n_work = n_work_dev ? *n_work_dev : n_work_host;
   const int64_t slot_words = int64_t(tile_features) * bin_stride * 2;
+  const uint32_t stride = uint32_t(bin_stride);
   for (int32_t item = blockIdx.x; item < n_work; item += gridDim.x) {
     const HistWork w = work[item];
     if (w.begin >= w.end) continue;  // padding item (uniform per workgroup)
@@ -232,24 +237,55 @@ __global__ __launch_bounds__(kHistThreads) void hist_sparse_kernel(
     for (int e = threadIdx.x; e < words; e += kHistThreads) lds_tile[e] = 0ull;
     __syncthreads();
     const uint32_t* tp = ptr + int64_t(w.tile) * n_rows;
-    for (int64_t i = w.begin + threadIdx.x; i < w.end; i += kHistThreads) {
-      const uint32_t r = GATHER ? ridx[i] : uint32_t(i);
-      const uint32_t b = tp[r], e = tp[r + 1];
-      const int2 q = gpair[r];
+    auto row_of = [&](int64_t i) -> uint32_t {
+      return GATHER ? ridx[i] : uint32_t(i);
+    };
+    // stage 0: row id of row i2 = i + 2 * 1024; stage 1: range and (g, h) of i1 = i + 1024
+    int64_t i = w.begin + threadIdx.x;
+    uint32_t b = 0, e = 0;
+    int2 q = make_int2(0, 0);
+    if (i < w.end) {
+      const uint32_t r = row_of(i);
+      b = tp[r];
+      e = tp[r + 1];
+      q = gpair[r];
+    }
+    uint32_t r1 = i + kHistThreads < w.end ? row_of(i + kHistThreads) : 0;
+    for (; i < w.end; i += kHistThreads) {
+      const int64_t i1 = i + kHistThreads, i2 = i + 2 * kHistThreads;
+      const uint32_t r2 = i2 < w.end ? row_of(i2) : 0;
+      uint32_t b1 = 0, e1 = 0;
+      int2 q1 = make_int2(0, 0);
+      if (i1 < w.end) {
+        b1 = tp[r1];
+        e1 = tp[r1 + 1];
+        q1 = gpair[r1];
+      }
       const unsigned long long g = (unsigned long long)(long long)q.x;
       const unsigned long long h = (unsigned long long)(long long)q.y;
-      for (uint32_t j = b; j < e; ++j) {
-        const uint32_t v = entries[j];
-        lds_u64* p = (lds_u64*)lds_tile + ((v >> 8) * uint32_t(bin_stride) + (v & 0xffu)) * 2u;
-        lds_add(p, g);
-        lds_add(p + 1, h);
+      for (uint32_t j = b; j < e; j += kSparseBatch) {
+        uint32_t v[kSparseBatch];
+#pragma unroll
+        for (int k = 0; k < kSparseBatch; ++k) v[k] = j + k < e ? entries[j + k] : 0u;
+#pragma unroll
+        for (int k = 0; k < kSparseBatch; ++k) {
+          if (j + k < e) {
+            lds_u64* p = (lds_u64*)lds_tile + ((v[k] >> 8) * stride + (v[k] & 0xffu)) * 2u;
+            lds_add(p, g);
+            lds_add(p + 1, h);
+          }
+        }
       }
+      b = b1;
+      e = e1;
+      q = q1;
+      r1 = r2;
     }
     __syncthreads();
     unsigned long long* out =
         w.partial >= 0 ? partial + int64_t(w.partial) * slot_words
                        : hist + (int64_t(w.slot) * n_features + f0) * bin_stride * 2;
-    for (int e = threadIdx.x; e < words; e += kHistThreads) out[e] = lds_tile[e];
+    for (int k = threadIdx.x; k < words; k += kHistThreads) out[k] = lds_tile[k];
     __syncthreads();  // the next item clears the LDS this item just read
   }
 }
@@ -498,7 +534,7 @@ void launch_hist_sparse(const SparseBins& sp, int64_t n_rows, int32_t n_features
     attr_set[ridx ? 1 : 0] = true;
   }
   // One workgroup per CU (the tile's LDS), a multiple of 8 for the XCD order.
-  int grid = n_work < 512 ? n_work : 512;
+  int grid = n_work < 1024 ? n_work : 1024;
   grid = (grid + 7) / 8 * 8;
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(kHistThreads), lds, s, sp.ptr.p, sp.entries.p,
                      n_rows, n_features, sp.tile_features, reinterpret_cast<const int2*>(gpair),
