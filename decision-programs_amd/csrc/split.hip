@@ -168,12 +168,27 @@ __device__ __forceinline__ Cand feature_best(const FeatBins<BPL>& d, int32_t f, 
       }
     }
   }
+  // Wave argmax: the largest loss, then the lowest lane holding it (lanes hold
+  // increasing bins, and each lane kept its lowest bin on ties), so the
+  // winner is the lowest bin with the largest loss -- better()'s order within
+  // one feature.  Only the loss crosses lanes in the reduction; the winner's
+  // fields are then read from its lane.
+  double best = c.loss;
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) {
-    const Cand o = shfl_xor_cand(c, m);
-    if (better(o, c)) c = o;
+    const double o = __shfl_xor(best, m, 64);
+    best = o > best ? o : best;
   }
-  return c;
+  const unsigned long long hit = __ballot(c.loss == best);
+  const int winner = __builtin_ctzll(hit);
+  Cand r;
+  r.loss = __shfl(c.loss, winner, 64);
+  r.gl = __shfl(c.gl, winner, 64);
+  r.hl = __shfl(c.hl, winner, 64);
+  r.feature = f;
+  r.bin = __shfl(c.bin, winner, 64);
+  r.dl = __shfl(c.dl, winner, 64);
+  return r;
 }
 
 // The split record of a node's best candidate.
