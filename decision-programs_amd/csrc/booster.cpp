@@ -223,6 +223,7 @@ void Grower::ensure_level(const Quantized& q, int64_t nb, int32_t d, int32_t D) 
     splits_.reserve(size_t(nb));
     eval_scratch_.reserve(evaluate_scratch_bytes(int32_t(nb), q.layout.n_features));
     work_left_.reserve(size_t(plan_part_capacity(nb, N, chunk_)));
+    part_masks_.reserve(size_t(plan_part_capacity(nb, N, chunk_)) * kPartMasks);
   }
   node_left_[nxt].reserve(size_t(std::max<int64_t>(nn, 1)));
   level_[nxt].reserve(size_t(std::max<int64_t>(nn, 1)));
@@ -386,7 +387,8 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
       launch_partition(q.bins.p, q.cols.p, L, ridx_[cur].p, ridx_[nxt].p, part_work_[cur].p,
                        int32_t(plan_part_capacity(nb, N, chunk_)), field(c, &PlanCounts::n_part),
                        seg_begin_[cur].p, splits_.p, part_first_[cur].p, int32_t(nb),
-                       field(c, &PlanCounts::n_level), work_left_.p, node_left_[cur].p, true, s,
+                       field(c, &PlanCounts::n_level), work_left_.p, part_masks_.p,
+                       node_left_[cur].p, true, s,
                        d > 0 ? &prev : nullptr);
     }
     PlanArgs a{};
@@ -472,6 +474,7 @@ uint64_t Grower::signature() const {
     buf(node_left_[i]); buf(leaf_work_[i]);
   }
   buf(root_work_); buf(root_job_); buf(partial_); buf(pair_chunk_); buf(work_left_);
+  buf(part_masks_);
   buf(splits_); buf(eval_scratch_); buf(info_); buf(counts_); buf(slots_);
   mix(uint64_t(eager_)); mix(uint64_t(sparse_)); mix(uint64_t(tiles_));
   mix(uint64_t(node_cap_)); mix(uint64_t(chunk_));

@@ -102,6 +102,7 @@ class Grower {
   DeviceBuffer<PartWork> part_work_[2];
   DeviceBuffer<int32_t> part_first_[2];
   DeviceBuffer<int64_t> pair_chunk_, work_left_, node_left_[2];
+  DeviceBuffer<unsigned long long> part_masks_;  // count ballots, kPartMasks per item
   DeviceBuffer<dp_split_record> splits_;
   DeviceBuffer<uint8_t> eval_scratch_;
   DeviceBuffer<LeafWork> leaf_work_[2];  // by level parity: applied one level later

@@ -619,7 +619,8 @@ int dp_partition(dp_workspace ws, const uint8_t* bins, const dp_bin_layout* layo
     hipStream_t s = as_stream(stream);
     ws->begin(sizeof(dp::PartWork) * work.size() + sizeof(int64_t) * size_t(n_nodes) +
               sizeof(int32_t) * first.size() + 3 * 256);
-    ws->reserve_scratch(sizeof(int64_t) * work.size() + 1024);
+    ws->reserve_scratch((sizeof(int64_t) + sizeof(uint64_t) * dp::kPartMasks) * work.size() +
+                        2048);
     dp::PartWork* d_work;
     int64_t* d_begin;
     int32_t* d_first;
@@ -628,8 +629,9 @@ int dp_partition(dp_workspace ws, const uint8_t* bins, const dp_bin_layout* layo
     std::copy(first.begin(), first.end(), ws->stage(first.size(), &d_first));
     ws->commit(s);
     int64_t* work_left = ws->take<int64_t>(work.size());
+    auto* masks = ws->take<unsigned long long>(work.size() * dp::kPartMasks);
     dp::launch_partition(bins, nullptr, *layout, ridx_in, ridx_out, d_work, int32_t(work.size()),
-                         nullptr, d_begin, splits, d_first, n_nodes, nullptr, work_left,
+                         nullptr, d_begin, splits, d_first, n_nodes, nullptr, work_left, masks,
                          left_count, false, s);
   });
 }

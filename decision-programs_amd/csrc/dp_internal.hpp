@@ -276,17 +276,20 @@ struct LeafPass {
 
 // Partition: counts, then scatter (which writes the left totals of the
 // expanding nodes into node_left).  cols: column-major copy of the bins
-// (launch_tiles_to_columns) or null to read the tiles.  node_left_zeroed: the
-// caller has zeroed node_left[0, nodes) (non-expanding nodes keep 0); else it
-// is cleared here for n_nodes nodes.
+// (launch_tiles_to_columns) or null to read the tiles.  work_left: one word
+// per work item; masks: kPartMasks words per work item (the count kernel's
+// ballots, read back by the scatter).  node_left_zeroed: the caller has zeroed
+// node_left[0, nodes) (non-expanding nodes keep 0); else it is cleared here
+// for n_nodes nodes.
 void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_layout& layout,
                       const uint32_t* ridx_in, uint32_t* ridx_out, const PartWork* work,
                       int32_t n_work, const int32_t* n_work_dev, const int64_t* seg_begin,
                       const dp_split_record* splits, const int32_t* node_first_work,
                       int32_t n_nodes, const int32_t* n_nodes_dev, int64_t* work_left,
-                      int64_t* node_left, bool node_left_zeroed, hipStream_t s,
-                      const LeafPass* leaves = nullptr);
+                      unsigned long long* masks, int64_t* node_left, bool node_left_zeroed,
+                      hipStream_t s, const LeafPass* leaves = nullptr);
 constexpr int64_t kPartChunk = 4096;
+constexpr int kPartMasks = 64;  // ballot words per partition work item (kPartChunk / 64)
 
 void launch_update_margin(const uint32_t* ridx, const LeafWork* work, int32_t n_work,
                           const int32_t* n_work_dev, float* margin, int64_t stride, hipStream_t s);

@@ -5,7 +5,9 @@
 // class_native_training.cuh:67).  Here every expanding node's segment of
 // ridx_in is split in two launches:
 //   1. count: one workgroup per chunk of <= kPartChunk rows counts its left
-//      rows with wavefront ballots;
+//      rows with wavefront ballots and keeps the ballots (one 64-bit mask per
+//      wavefront and 256-row step, 64 per chunk), so the split feature's bins
+//      are gathered once per level;
 //   2. scatter: each chunk sums the counts of its node's chunks (the node's
 //      left total, and its own exclusive offset from the earlier ones; the
 //      node's first chunk publishes the total in node_left), ranks its rows in
@@ -21,6 +23,7 @@ namespace {
 
 constexpr int kPartThreads = 256;
 constexpr int kPartSteps = int(kPartChunk / kPartThreads);  // 16 rows per lane
+static_assert(kPartSteps * (kPartThreads / 64) == kPartMasks, "one mask per wave and step");
 
 // The split feature's bin of `row`: from the column-major copy when there is
 // one (one byte per row, contiguous within a feature), else from the tiles.
@@ -59,7 +62,7 @@ __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
     const uint8_t* __restrict__ bins, int64_t n_rows, int tile_width, int missing_bin,
     const uint32_t* __restrict__ ridx, const PartWork* __restrict__ work, int32_t n_work_host,
     const int32_t* __restrict__ n_work_dev, const dp_split_record* __restrict__ splits,
-    int64_t* __restrict__ work_left, LeafPass lp) {
+    int64_t* __restrict__ work_left, unsigned long long* __restrict__ masks, LeafPass lp) {
   __shared__ int wave_count[kPartThreads / 64];
   const int32_t n_work = n_work_dev ? *n_work_dev : n_work_host;
   const int32_t n_leaves = lp.work ? (lp.n_dev ? *lp.n_dev : lp.n_host) : 0;
@@ -82,7 +85,10 @@ __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
     if (i < w.end)
       left = goes_left<COLS>(bins, n_rows, tile_width, ridx[i], s.feature, s.bin,
                              s.default_left, missing_bin);
-    count += popc64(__ballot(left));
+    const unsigned long long m = __ballot(left);
+    if ((threadIdx.x & 63) == 0)
+      masks[int64_t(item) * kPartMasks + step * (kPartThreads / 64) + (threadIdx.x >> 6)] = m;
+    count += popc64(m);
   }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (lane == 0) wave_count[wave] = count;
@@ -103,7 +109,8 @@ __global__ __launch_bounds__(kPartThreads) void part_scatter_kernel(
     const PartWork* __restrict__ work, int32_t n_work_host,
     const int32_t* __restrict__ n_work_dev, const dp_split_record* __restrict__ splits,
     const int64_t* __restrict__ seg_begin, const int32_t* __restrict__ node_first_work,
-    const int64_t* __restrict__ work_left, int64_t* __restrict__ node_left) {
+    const int64_t* __restrict__ work_left, const unsigned long long* __restrict__ masks,
+    int64_t* __restrict__ node_left) {
   __shared__ int wave_count[kPartThreads / 64];
   __shared__ int64_t wave_sum[2][kPartThreads / 64];
   const int32_t n_work = n_work_dev ? *n_work_dev : n_work_host;
@@ -144,13 +151,11 @@ __global__ __launch_bounds__(kPartThreads) void part_scatter_kernel(
     const int64_t i = step_base + threadIdx.x;
     bool valid = i < w.end;
     uint32_t row = 0;
-    bool left = false;
-    if (valid) {
-      row = ridx_in[i];
-      left = goes_left<COLS>(bins, n_rows, tile_width, row, s.feature, s.bin, s.default_left,
-                             missing_bin);
-    }
-    const unsigned long long mask = __ballot(left);
+    // the count kernel's ballot for this wavefront and step
+    const unsigned long long mask =
+        masks[int64_t(item) * kPartMasks + step * (kPartThreads / 64) + wave];
+    const bool left = (mask >> lane) & 1ull;
+    if (valid) row = ridx_in[i];
     if (lane == 0) wave_count[wave] = popc64(mask);
     __syncthreads();
     int64_t prefix = lefts_before;
@@ -213,8 +218,8 @@ void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_lay
                       int32_t n_work, const int32_t* n_work_dev, const int64_t* seg_begin,
                       const dp_split_record* splits, const int32_t* node_first_work,
                       int32_t n_nodes, const int32_t* n_nodes_dev, int64_t* work_left,
-                      int64_t* node_left, bool node_left_zeroed, hipStream_t s,
-                      const LeafPass* leaves) {
+                      unsigned long long* masks, int64_t* node_left, bool node_left_zeroed,
+                      hipStream_t s, const LeafPass* leaves) {
   if (n_nodes <= 0) return;
   (void)n_nodes_dev;
   const int missing = layout.missing_bin;
@@ -227,14 +232,14 @@ void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_lay
   if (items <= 0) return;
   hipLaunchKernelGGL(cols ? part_count_kernel<true> : part_count_kernel<false>, dim3(gc),
                      dim3(kPartThreads), 0, s, src, layout.n_rows, layout.tile_width, missing,
-                     ridx_in, work, n_work, n_work_dev, splits, work_left, lp);
+                     ridx_in, work, n_work, n_work_dev, splits, work_left, masks, lp);
   DP_HIP(hipGetLastError());
   if (n_work <= 0) return;
   DP_HIP(hipGetLastError());
   hipLaunchKernelGGL(cols ? part_scatter_kernel<true> : part_scatter_kernel<false>, dim3(gw),
                      dim3(kPartThreads), 0, s, src, layout.n_rows, layout.tile_width, missing,
                      ridx_in, ridx_out, work, n_work, n_work_dev, splits, seg_begin,
-                     node_first_work, work_left, node_left);
+                     node_first_work, work_left, masks, node_left);
   DP_HIP(hipGetLastError());
 }
 
