@@ -532,7 +532,24 @@ void Grower::collect(const Quantized& q, int32_t slot, int32_t buffer, Tree& tre
 // ---------------------------------------------------------------------------
 Booster::Booster(std::vector<DMatrix*> cache) : cache_(std::move(cache)) {}
 
+void DMatrix::release_pending() {
+  const std::vector<const Booster*> users = pending;
+  for (const Booster* b : users) {
+    try {
+      b->flush();
+    } catch (...) {
+      // the booster keeps its last good rounds; the matrix is freed regardless
+    }
+  }
+  pending.clear();
+  (void)hipDeviceSynchronize();
+}
+
 Booster::~Booster() {
+  if (pending_ && pending_d_) {  // the round in flight is dropped, not collected
+    auto& v = pending_d_->pending;
+    v.erase(std::remove(v.begin(), v.end(), this), v.end());
+  }
   if (stream_) (void)hipStreamSynchronize(stream_);
   for (hipEvent_t& e : round_done_)
     if (e) (void)hipEventDestroy(e);
@@ -827,6 +844,8 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
   pending_ = true;
   pending_buffer_ = buffer;
   pending_q_ = &q;
+  pending_d_ = d;
+  d->pending.push_back(this);
   ++rounds_;
   if (!grower_->eager()) flush();
 }
@@ -834,6 +853,10 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
 void Booster::flush() const {
   if (!pending_) return;
   pending_ = false;
+  if (pending_d_) {
+    auto& v = pending_d_->pending;
+    v.erase(std::remove(v.begin(), v.end(), this), v.end());
+  }
   const int32_t b = pending_buffer_;
   DP_HIP(hipEventSynchronize(round_done_[b]));
   const auto* e = reinterpret_cast<const int32_t*>(exps_host_.p + size_t(b) * exps_.bytes());

@@ -28,6 +28,8 @@ struct Quantized {
   double density = -1.0;       // share of present values, once counted
 };
 
+class Booster;
+
 struct DMatrix {
   int64_t n_rows = 0;
   int32_t n_features = 0;
@@ -36,6 +38,10 @@ struct DMatrix {
   bool has_labels = false;
   std::map<int32_t, std::unique_ptr<Quantized>> quantized;  // by requested max_bin
   Quantized& quantize(int32_t max_bin, dp_workspace_s& ws, hipStream_t s);
+  // Boosters with a round in flight on this matrix.  Freeing the matrix
+  // collects those rounds first (release_pending) and waits for the device.
+  std::vector<const Booster*> pending;
+  void release_pending();
 };
 
 // One regression tree in XGBoost's RegTree JSON field order plus parity data.
@@ -217,6 +223,7 @@ class Booster {
   mutable bool pending_ = false;
   int32_t pending_buffer_ = 0;
   const Quantized* pending_q_ = nullptr;
+  DMatrix* pending_d_ = nullptr;
   hipEvent_t round_done_[2] = {nullptr, nullptr};
   std::vector<uint64_t> last_round_inputs_;  // host inputs of the last round enqueued
   mutable int rounds_ = 0;

@@ -226,7 +226,11 @@ int XGDMatrixNumCol(DMatrixHandle handle, bst_ulong* out) {
 }
 
 int XGDMatrixFree(DMatrixHandle handle) {
-  return guarded([&] { delete static_cast<DMatrixObj*>(handle); });
+  return guarded([&] {
+    auto* obj = static_cast<DMatrixObj*>(handle);
+    if (obj) obj->m.release_pending();  // rounds in flight still read the matrix
+    delete obj;
+  });
 }
 
 int XGBoosterCreate(const DMatrixHandle dmats[], bst_ulong len, BoosterHandle* out) {

@@ -354,3 +354,30 @@ def test_graph_replays_equal_direct_launches(dp, device, objective, k):
     for r, (a, b) in enumerate(zip(m_graph, m_direct)):
         np.testing.assert_array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32),
                                       err_msg=f"round {r} margins")
+
+
+def test_matrix_freed_with_round_in_flight(dp, device):
+    """Freeing the training matrix right after a round (whose trees are still being collected
+    asynchronously) collects that round first: the model equals one whose rounds were collected
+    call by call."""
+    import gc
+
+    from dpgbdt import ops
+
+    values, labels, _, _ = ops.synth(2, 50_000, 3, n_features=28)
+    params = {"objective": "binary:logistic", "max_depth": 6, "eta": 0.3}
+
+    def train(inspect):
+        dtrain = dp.DMatrix(values, labels)
+        bst = dp.Booster(params, [dtrain])
+        for r in range(4):
+            bst.update(dtrain, r)
+            if inspect:
+                assert bst.num_boosted_rounds() == r + 1
+        # the booster's Python cache keeps the wrapper alive: free the matrix through the C API
+        assert dp.load().XGDMatrixFree(dtrain.handle) == 0
+        dtrain.handle = None
+        gc.collect()
+        return bst.save_raw()
+
+    assert train(False) == train(True)
