@@ -86,6 +86,54 @@ struct FeatCand {
 
 constexpr int kFeatWaves = 4;  // features per workgroup in evaluate_features_kernel
 
+// Cross-lane moves on the DPP path (VALU lane swizzles, no LDS round trip).
+// dpp64 moves a 64-bit value as two 32-bit halves; lanes whose source is out
+// of range or whose row is masked off receive `old`.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ long long dpp64(long long v, long long old) {
+  const int lo = __builtin_amdgcn_update_dpp(int(old), int(v), CTRL, ROW_MASK, 0xf, false);
+  const int hi = __builtin_amdgcn_update_dpp(int(old >> 32), int(v >> 32), CTRL, ROW_MASK, 0xf,
+                                             false);
+  return (long long)((uint64_t(uint32_t(hi)) << 32) | uint32_t(lo));
+}
+
+__device__ __forceinline__ double dpp_f64_bits(long long bits) { return __longlong_as_double(bits); }
+
+// Inclusive wavefront scan: row_shr 1, 2, 4, 8 within each 16-lane row, then
+// row_bcast15 (lane 15 of rows 0 and 2 into rows 1 and 3) and row_bcast31
+// (lane 31 into rows 2 and 3).
+__device__ __forceinline__ long long wave_inclusive_sum(long long x) {
+  x += dpp64<0x111>(x, 0);
+  x += dpp64<0x112>(x, 0);
+  x += dpp64<0x114>(x, 0);
+  x += dpp64<0x118>(x, 0);
+  x += dpp64<0x142, 0xa>(x, 0);
+  x += dpp64<0x143, 0xc>(x, 0);
+  return x;
+}
+
+// The largest value of the wavefront, in lane 63 (the same steps as the scan).
+__device__ __forceinline__ double wave_max_to_last(double v) {
+  long long b = __double_as_longlong(v);
+  auto step = [&](long long o) {
+    const double ov = dpp_f64_bits(o), cv = dpp_f64_bits(b);
+    if (ov > cv) b = o;
+  };
+  step(dpp64<0x111>(b, b));
+  step(dpp64<0x112>(b, b));
+  step(dpp64<0x114>(b, b));
+  step(dpp64<0x118>(b, b));
+  step(dpp64<0x142, 0xa>(b, b));
+  step(dpp64<0x143, 0xc>(b, b));
+  return dpp_f64_bits(b);
+}
+
+__device__ __forceinline__ long long readlane64(long long v, int lane) {
+  const int lo = __builtin_amdgcn_readlane(int(v), lane);
+  const int hi = __builtin_amdgcn_readlane(int(v >> 32), lane);
+  return (long long)((uint64_t(uint32_t(hi)) << 32) | uint32_t(lo));
+}
+
 // One feature's histogram of one node as one wavefront holds it: bins
 // lane * BPL + j (bins past bin_stride read as zero).
 template <int BPL>
@@ -126,17 +174,8 @@ __device__ __forceinline__ Cand feature_best(const FeatBins<BPL>& d, int32_t f, 
     sh[j] = rh;
   }
   // inclusive wavefront scan of the lane totals
-  long long ig = rg, ih = rh;
-#pragma unroll
-  for (int s = 1; s < 64; s <<= 1) {
-    const long long tg = __shfl_up(ig, s, 64);
-    const long long th = __shfl_up(ih, s, 64);
-    if (lane >= s) {
-      ig += tg;
-      ih += th;
-    }
-  }
-  const long long total_g = __shfl(ig, 63, 64), total_h = __shfl(ih, 63, 64);
+  const long long ig = wave_inclusive_sum(rg), ih = wave_inclusive_sum(rh);
+  const long long total_g = readlane64(ig, 63), total_h = readlane64(ih, 63);
   const long long og = ig - rg, oh = ih - rh;  // exclusive offset of this lane
   const long long mg = gp - total_g, mh = hp - total_h;
 
@@ -173,21 +212,16 @@ __device__ __forceinline__ Cand feature_best(const FeatBins<BPL>& d, int32_t f, 
   // winner is the lowest bin with the largest loss -- better()'s order within
   // one feature.  Only the loss crosses lanes in the reduction; the winner's
   // fields are then read from its lane.
-  double best = c.loss;
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    const double o = __shfl_xor(best, m, 64);
-    best = o > best ? o : best;
-  }
+  const double best = dpp_f64_bits(readlane64(__double_as_longlong(wave_max_to_last(c.loss)), 63));
   const unsigned long long hit = __ballot(c.loss == best);
   const int winner = __builtin_ctzll(hit);
   Cand r;
-  r.loss = __shfl(c.loss, winner, 64);
-  r.gl = __shfl(c.gl, winner, 64);
-  r.hl = __shfl(c.hl, winner, 64);
+  r.loss = dpp_f64_bits(readlane64(__double_as_longlong(c.loss), winner));
+  r.gl = readlane64(c.gl, winner);
+  r.hl = readlane64(c.hl, winner);
   r.feature = f;
-  r.bin = __shfl(c.bin, winner, 64);
-  r.dl = __shfl(c.dl, winner, 64);
+  r.bin = __builtin_amdgcn_readlane(c.bin, winner);
+  r.dl = __builtin_amdgcn_readlane(c.dl, winner);
   return r;
 }
 
