@@ -554,7 +554,10 @@ Booster::~Booster() {
   for (hipEvent_t& e : round_done_)
     if (e) (void)hipEventDestroy(e);
   clear_graphs();
-  grower_.reset();
+  growers_.clear();
+  for (hipStream_t t : tree_streams_) (void)hipStreamDestroy(t);
+  for (hipEvent_t e : tree_done_) (void)hipEventDestroy(e);
+  if (fork_) (void)hipEventDestroy(fork_);
   if (stream_) (void)hipStreamDestroy(stream_);
 }
 
@@ -570,7 +573,7 @@ void Booster::set_param(const std::string& key, const std::string& value) {
       "min_split_loss", "min_child_weight", "subsample", "colsample_bytree", "colsample_bylevel",
       "colsample_bynode", "base_score", "boost_from_average", "seed", "seed_per_iteration",
       "nthread", "verbosity", "validate_parameters", "grow_policy", "dp_record_positions",
-      "dp_graphs", "dp_sparse_hist"};
+      "dp_graphs", "dp_sparse_hist", "dp_concurrent_trees"};
   bool ok = false;
   for (const char* k : known) ok = ok || key == k;
   need(ok, "unsupported parameter: " + key);
@@ -589,6 +592,11 @@ void Booster::set_param(const std::string& key, const std::string& value) {
   params_[key] = value;
   if (key == "dp_record_positions") record_positions_ = parse_int(key, value) != 0;
   if (key == "dp_graphs") use_graphs_ = parse_int(key, value) != 0;
+  if (key == "dp_concurrent_trees") {
+    const int32_t m = parse_int(key, value);
+    need(m >= 1 && m <= 8, "dp_concurrent_trees must be in [1, 8]");
+    concurrent_trees_ = m;
+  }
   if (key == "dp_sparse_hist") {
     const int32_t m = parse_int(key, value);
     need(m >= 0 && m <= 2, "dp_sparse_hist must be 0, 1 or 2");
@@ -688,7 +696,6 @@ void Booster::configure(DMatrix* d) {
   DP_HIP(hipMemcpy(base.p, init.data(), base.bytes(), hipMemcpyHostToDevice));
   launch_init_margin(margin_.p, N, n_groups_, base.p, stream_);
   DP_HIP(hipStreamSynchronize(stream_));  // before `base` is freed
-  grower_ = std::make_unique<Grower>();
   configured_ = true;
 }
 
@@ -767,7 +774,8 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
   // Host inputs that size buffers: when they change, the round in flight is
   // collected first, so no buffer it uses moves under it.
   std::vector<uint64_t> inputs = {reinterpret_cast<uint64_t>(d), uint64_t(record_positions_),
-                                  uint64_t(n_groups_), uint64_t(sparse_mode_)};
+                                  uint64_t(n_groups_), uint64_t(sparse_mode_),
+                                  uint64_t(concurrent_trees_)};
   auto words = [](std::vector<uint64_t>& v, const void* p, size_t n) {
     for (size_t i = 0; i < n; i += 8) {
       uint64_t w = 0;
@@ -799,10 +807,30 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
     launch_tiles_to_rows(q.bins.p, q.layout, q.rows.p, stream_);
   }
   if (record_positions_) positions_.reserve(size_t(N));
-  grower_->prepare(q, tp_, n_groups_, sparse, stream_);
+  const int32_t K = n_groups_;
+  int32_t S = std::min(K, concurrent_trees_);
+  while (int32_t(growers_.size()) < S) growers_.push_back(std::make_unique<Grower>());
+  if (growers_.empty()) growers_.push_back(std::make_unique<Grower>());
+  growers_[0]->prepare(q, tp_, (K + S - 1) / S, sparse, stream_);
+  const bool eager = growers_[0]->eager();
+  if (!eager && S > 1) {  // level-synced trees synchronise per level: one at a time
+    S = 1;
+    growers_[0]->prepare(q, tp_, K, sparse, stream_);
+  }
+  for (int32_t l = 1; l < S; ++l) growers_[size_t(l)]->prepare(q, tp_, (K - l + S - 1) / S, sparse,
+                                                              stream_);
+  while (S > 1 && int32_t(tree_streams_.size()) < S) {
+    hipStream_t t;
+    DP_HIP(hipStreamCreateWithFlags(&t, hipStreamNonBlocking));
+    tree_streams_.push_back(t);
+    hipEvent_t e;
+    DP_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    tree_done_.push_back(e);
+  }
+  if (S > 1 && !fork_) DP_HIP(hipEventCreateWithFlags(&fork_, hipEventDisableTiming));
   // Level-synced trees copy their records during grow(): collect the round in
   // flight before they are overwritten.
-  if (!grower_->eager()) flush();
+  if (!eager) flush();
   last_round_inputs_ = inputs;
   int32_t* positions = record_positions_ ? positions_.p : nullptr;
   // Everything the enqueued launches depend on: a change of any of it gives
@@ -817,23 +845,41 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
       reinterpret_cast<uint64_t>(gpair_.p), reinterpret_cast<uint64_t>(exps_.p),
       reinterpret_cast<uint64_t>(sums_.p), reinterpret_cast<uint64_t>(quant_scratch_.p),
       reinterpret_cast<uint64_t>(positions), reinterpret_cast<uint64_t>(q.sparse.ptr.p),
-      reinterpret_cast<uint64_t>(q.sparse.entries.p), uint64_t(sparse), grower_->signature()};
+      reinterpret_cast<uint64_t>(q.sparse.entries.p), uint64_t(sparse), uint64_t(S)};
+  for (int32_t l = 0; l < S; ++l) key.push_back(growers_[size_t(l)]->signature());
   words(key, &q.layout, sizeof q.layout);
   words(key, &tp_, sizeof tp_);
-  enqueue(key, grower_->eager(), [&] {
+  enqueue(key, eager, [&] {
     bool maxima = false;
     if (with_gradients)
-      maxima = launch_gradients(objective_id_, margin_.p, d->labels.p, N, n_groups_, grad_.p,
-                                hess_.p, quant_scratch_.p, stream_);
-    launch_quantise(grad_.p, hess_.p, N, n_groups_, quant_scratch_.p, maxima, exps_.p, gpair_.p,
-                    sums_.p, stream_);
-    for (int32_t k = 0; k < n_groups_; ++k)
-      grower_->grow(q, gpair_.p + int64_t(k) * N * 2, exps_.p + 2 * k, sums_.p + 2 * k, tp_,
-                    margin_.p + k, n_groups_, positions, k, stream_);
+      maxima = launch_gradients(objective_id_, margin_.p, d->labels.p, N, K, grad_.p, hess_.p,
+                                quant_scratch_.p, stream_);
+    launch_quantise(grad_.p, hess_.p, N, K, quant_scratch_.p, maxima, exps_.p, gpair_.p, sums_.p,
+                    stream_);
+    if (S == 1) {
+      for (int32_t k = 0; k < K; ++k)
+        growers_[0]->grow(q, gpair_.p + int64_t(k) * N * 2, exps_.p + 2 * k, sums_.p + 2 * k, tp_,
+                          margin_.p + k, K, positions, k, stream_);
+      return;
+    }
+    // Each tree writes its own margin column; only the last writes the row
+    // positions (the round's positions are its last tree's).
+    DP_HIP(hipEventRecord(fork_, stream_));
+    for (int32_t l = 0; l < S; ++l) DP_HIP(hipStreamWaitEvent(tree_streams_[size_t(l)], fork_, 0));
+    for (int32_t k = 0; k < K; ++k)
+      growers_[size_t(k % S)]->grow(q, gpair_.p + int64_t(k) * N * 2, exps_.p + 2 * k,
+                                    sums_.p + 2 * k, tp_, margin_.p + k, K,
+                                    k == K - 1 ? positions : nullptr, k / S,
+                                    tree_streams_[size_t(k % S)]);
+    for (int32_t l = 0; l < S; ++l) {
+      DP_HIP(hipEventRecord(tree_done_[size_t(l)], tree_streams_[size_t(l)]));
+      DP_HIP(hipStreamWaitEvent(stream_, tree_done_[size_t(l)], 0));
+    }
   });
   // This round's records go to the buffer the round in flight does not use.
   const int32_t buffer = pending_ ? 1 - pending_buffer_ : 0;
-  grower_->readback(n_groups_, buffer, stream_);
+  for (int32_t l = 0; l < S; ++l)
+    growers_[size_t(l)]->readback(S == 1 ? K : (K - l + S - 1) / S, buffer, stream_);
   exps_host_.reserve(2 * exps_.bytes());
   DP_HIP(hipMemcpyAsync(exps_host_.p + size_t(buffer) * exps_.bytes(), exps_.p, exps_.bytes(),
                         hipMemcpyDeviceToHost, stream_));
@@ -845,9 +891,10 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
   pending_buffer_ = buffer;
   pending_q_ = &q;
   pending_d_ = d;
+  pending_lanes_ = S;
   d->pending.push_back(this);
   ++rounds_;
-  if (!grower_->eager()) flush();
+  if (!eager) flush();
 }
 
 void Booster::flush() const {
@@ -863,7 +910,9 @@ void Booster::flush() const {
   last_exps_.assign(e, e + 2 * n_groups_);
   std::vector<Tree> round(static_cast<size_t>(n_groups_));
   try {
-    for (int32_t k = 0; k < n_groups_; ++k) grower_->collect(*pending_q_, k, b, round[size_t(k)]);
+    const int32_t S = pending_lanes_;
+    for (int32_t k = 0; k < n_groups_; ++k)
+      growers_[size_t(k % S)]->collect(*pending_q_, k / S, b, round[size_t(k)]);
   } catch (...) {
     rounds_ = int(iteration_indptr_.size()) - 1;  // the failed round is not part of the model
     throw;
@@ -1231,6 +1280,7 @@ std::unique_ptr<Booster> Booster::slice(int begin, int end, int step) const {
   out->params_.erase("dp_record_positions");
   out->params_.erase("dp_graphs");
   out->params_.erase("dp_sparse_hist");
+  out->params_.erase("dp_concurrent_trees");
   out->objective_ = effective_objective();
   out->objective_id_ = objective_id_;
   out->n_groups_ = n_groups_;

@@ -215,7 +215,15 @@ class Booster {
   bool labels_checked_ = false;
   std::vector<std::pair<std::vector<uint64_t>, hipGraphExec_t>> graphs_;  // newest last
   hipStream_t stream_ = nullptr;
-  std::unique_ptr<Grower> grower_;
+  // Trees of a round run concurrently: tree k on growers_[k % S] and, when S
+  // > 1, on tree_streams_[k % S] (forked from and joined back to stream_ by
+  // events).  S = min(outputs, dp_concurrent_trees).
+  std::vector<std::unique_ptr<Grower>> growers_;
+  std::vector<hipStream_t> tree_streams_;
+  std::vector<hipEvent_t> tree_done_;
+  hipEvent_t fork_ = nullptr;
+  int32_t concurrent_trees_ = 4;
+  int32_t pending_lanes_ = 1;  // S of the round in flight
   mutable std::vector<Tree> trees_;
   mutable std::vector<int32_t> tree_info_;
   mutable std::vector<int32_t> iteration_indptr_{0};
