@@ -206,6 +206,27 @@ def test_depth_one_and_single_chunk(dp, oracle, device):
         _compare(bst, o_trees, o_margin, pos, n, 1)
 
 
+@pytest.mark.parametrize("sparse", [0, 2])
+def test_degenerate_features_and_tiny_matrices(dp, oracle, device, sparse):
+    """A feature that is all missing, a constant feature and a feature missing in every other
+    row, on 1, 2, 63 and 5000 rows, dense and present-value histograms, against the oracle."""
+    def degenerate(v):
+        v = v.clone()
+        v[:, 0] = float("nan")
+        v[:, 1] = 0.25
+        v[::2, 2] = float("nan")
+        return v
+
+    for n in [1, 2, 63, 5000]:
+        p = {"max_depth": 4, "eta": 0.5}
+        print(f"[booster] degenerate {n} x 12, sparse {sparse}", flush=True)
+        bst, x, o_trees, o_margin, pos, n = _train_both(dp, oracle, device, 1, n, 12, 0, 1, p, 2,
+                                                        20261220 + n,
+                                                        extra={"dp_sparse_hist": sparse},
+                                                        mutate=degenerate)
+        _compare(bst, o_trees, o_margin, pos, n, 1)
+
+
 def test_regularisation_paths(dp, oracle, device):
     """alpha, gamma and min_child_weight change the chosen splits identically."""
     p = {"max_depth": 5, "eta": 0.5, "alpha": 0.7, "gamma": 2.0, "min_child_weight": 8.0,
