@@ -402,3 +402,22 @@ def test_matrix_freed_with_round_in_flight(dp, device):
         return bst.save_raw()
 
     assert train(False) == train(True)
+
+
+def test_concurrent_class_trees_equal_sequential(dp, device):
+    """The class trees of a round grown on 1, 2, 3 or 4 streams give the same model."""
+    import torch
+    from dpgbdt import ops
+
+    n, k = 30_000, 5
+    values, _, _, _ = ops.synth(1, n, 9, n_features=64)
+    labels = (torch.arange(n, device=values.device) % k).to(torch.float32)
+    dtrain = dp.DMatrix(values, labels)
+    models = []
+    for lanes in (1, 2, 3, 4):
+        bst = dp.Booster({"objective": "multi:softprob", "num_class": k, "max_depth": 5,
+                          "eta": 0.3, "dp_concurrent_trees": lanes}, [dtrain])
+        for r in range(3):
+            bst.update(dtrain, r)
+        models.append(bst.save_raw())
+    assert all(m == models[0] for m in models[1:])
