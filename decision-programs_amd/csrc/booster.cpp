@@ -185,6 +185,7 @@ int32_t Tree::alloc(int32_t parent_id) {
   default_left.push_back(0);
   sum_qg.push_back(0);
   sum_qh.push_back(0);
+  rows.push_back(-1);
   return id;
 }
 
@@ -508,6 +509,7 @@ void Grower::collect(const Quantized& q, int32_t slot, int32_t buffer, Tree& tre
     tree.sum_hess[id] = r.sum_hess;
     tree.sum_qg[id] = r.g;
     tree.sum_qh[id] = r.h;
+    tree.rows[id] = r.end - r.begin;
     if (r.left >= 0) {
       need(r.left > i && r.left + 1 < n, "tree planner produced an invalid child id");
       need(r.feature >= 0 && r.feature < q.layout.n_features && r.bin >= 0 &&

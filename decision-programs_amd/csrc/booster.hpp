@@ -50,6 +50,7 @@ struct Tree {
   std::vector<float> cond, base_weight, loss_chg, sum_hess;
   std::vector<uint8_t> default_left;
   std::vector<int64_t> sum_qg, sum_qh;
+  std::vector<int64_t> rows;  // training rows reaching the node; -1 when unknown (loaded)
   int32_t size() const { return int32_t(left.size()); }
   int32_t alloc(int32_t parent_id);
 };

@@ -399,6 +399,7 @@ int DPBoosterGetTree(BoosterHandle handle, int tree, DPTreeView* out) {
     out->sum_hessian = t.sum_hess.data();
     out->sum_qg = t.sum_qg.data();
     out->sum_qh = t.sum_qh.data();
+    out->row_counts = t.rows.data();
   });
 }
 

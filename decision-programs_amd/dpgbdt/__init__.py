@@ -56,7 +56,7 @@ class TreeView(Structure):
                 ("split_conditions", POINTER(c_float)), ("default_left", POINTER(c_uint8)),
                 ("base_weights", POINTER(c_float)), ("loss_changes", POINTER(c_float)),
                 ("sum_hessian", POINTER(c_float)), ("sum_qg", POINTER(c_int64)),
-                ("sum_qh", POINTER(c_int64))]
+                ("sum_qh", POINTER(c_int64)), ("row_counts", POINTER(c_int64))]
 
 
 _lib = None
@@ -326,6 +326,7 @@ class Booster:
             "base_weight": arr(v.base_weights, np.float32),
             "loss_chg": arr(v.loss_changes, np.float32), "sum_hess": arr(v.sum_hessian, np.float32),
             "sum_qg": arr(v.sum_qg, np.int64), "sum_qh": arr(v.sum_qh, np.int64),
+            "rows": arr(v.row_counts, np.int64),
         }
 
     def margins(self, n_rows, n_groups):

@@ -149,6 +149,7 @@ typedef struct {
   const float* sum_hessian;
   const int64_t* sum_qg;
   const int64_t* sum_qh;
+  const int64_t* row_counts; /* training rows reaching each node; -1 for loaded models */
 } DPTreeView;
 
 int DPBoosterNumTrees(BoosterHandle handle, int* out);

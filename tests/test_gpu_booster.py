@@ -82,6 +82,13 @@ def _compare(bst, o_trees, o_margin, gpu_positions, n, k):
         leaves = ot["left"] == -1
         np.testing.assert_array_equal(gt["loss_chg"][~leaves].view(np.uint32),
                                       ot["loss_chg"][~leaves].view(np.uint32))
+        # row counts: leaves from the oracle's partition, internal nodes as their children's sum
+        counts = np.bincount(ot["positions"], minlength=len(ot["left"]))
+        np.testing.assert_array_equal(gt["rows"][leaves], counts[leaves], err_msg=f"tree {t} rows")
+        inner = np.nonzero(~leaves)[0]
+        np.testing.assert_array_equal(gt["rows"][inner],
+                                      gt["rows"][ot["left"][inner]] + gt["rows"][ot["right"][inner]])
+        assert gt["rows"][0] == n
     for r, pos in enumerate(gpu_positions):
         np.testing.assert_array_equal(pos, o_trees[(r + 1) * k - 1]["positions"],
                                       err_msg=f"round {r} positions")
