@@ -17,7 +17,9 @@ The same JSON line carries
                 logistic), C3 (10M x 128, depth 8, 20 trees, injected
                 gradients), C4 (60k x 784, softprob K=10, depth 6, 50 rounds =
                 500 trees), C5 (2M x 1000, 95 % missing, 64 bins, squared
-                error, depth 10, 50 trees);
+                error, depth 10, 50 trees), each with its histogram layout,
+                algorithmic bytes per tree (from the trees' node row counts)
+                and the resulting share of the HBM peak;
   cpu_baseline  the CPU restatement (oracle, OpenMP) of the same histogram
                 pass on a bounded row sample, on this box's host cores; in
                 full mode also the oracle's single-threaded booster on C1 (10
@@ -219,6 +221,36 @@ TREE_CONFIGS = {
 }
 
 
+def tree_algorithmic_bytes(t, n_rows, n_features, n_bins, depth, density=None):
+    """Minimal HBM bytes of one tree from its node row counts, with the unit figures of
+    the build's measurement plan: histogram of a node with n rows n*F (u8 bins) + 8n (g, h)
+    + 4n if its rows are gathered + F*B*8 out (present-value layout: 3 B per present value
+    + 4 B row pointer + 8 B (g, h) per row instead of the bins and (g, h)); subtraction
+    3*F*B*8 per built pair; split scan F*B*8 per node evaluated; partition 9 B per row of
+    a split node; gradients 16 B per row."""
+    left, right, rows = t["left"], t["right"], t["rows"]
+    fb8 = n_features * n_bins * 8
+
+    def hist(n, gathered):
+        if density is None:
+            return n * n_features + 8 * n + (4 * n if gathered else 0) + fb8
+        return int(n * n_features * density) * 3 + 12 * n + (4 * n if gathered else 0) + fb8
+
+    dep = [0] * len(left)
+    total = hist(int(rows[0]), False) + 16 * n_rows
+    for v in range(len(left)):
+        if dep[v] < depth:
+            total += fb8  # split scan
+        if left[v] < 0:
+            continue
+        a, b = int(left[v]), int(right[v])
+        dep[a] = dep[b] = dep[v] + 1
+        total += 9 * int(rows[v])  # partition
+        if dep[v] + 1 < depth:  # the children get histograms: build the smaller, subtract
+            total += hist(min(int(rows[a]), int(rows[b])), True) + 3 * fb8
+    return total
+
+
 def trees_leg(torch, dp, ops, name, rows=None, warm_rounds=2):
     """Wall time of the configuration's boosting rounds on a fresh booster (the
     matrix is quantised and the kernels warmed by a previous booster)."""
@@ -227,6 +259,11 @@ def trees_leg(torch, dp, ops, name, rows=None, warm_rounds=2):
     f = ops.SYNTH_FEATURES[config]
     values, labels, g, h = ops.synth(config, n, SEED + config, want_grad=injected)
     dtrain = dp.DMatrix(values, labels)
+    present = float((~torch.isnan(values)).sum().item()) / (n * f)
+    # the booster's rule for the present-value layout (dp_sparse_hist=1)
+    density = present if present <= 0.25 else None
+    layout = ("present-value (sparse) histograms, {:.1%} present".format(present) if density
+              else "dense 16-feature tiles")
     del values
     params = {"objective": objective, "tree_method": "hist", "device": "cuda:0",
               "max_depth": depth, "eta": eta, "lambda": 1.0, "min_child_weight": 1.0,
@@ -248,12 +285,18 @@ def trees_leg(torch, dp, ops, name, rows=None, warm_rounds=2):
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
     trees = bst.num_trees()
-    nodes = sum(len(bst.tree(t)["left"]) for t in range(trees))
+    nodes, abytes = 0, 0
+    for t in range(trees):
+        tr = bst.tree(t)
+        nodes += len(tr["left"])
+        abytes += tree_algorithmic_bytes(tr, n, f, max_bin, depth, density)
     del bst, dtrain
     torch.cuda.empty_cache()
+    gbs = abytes / el / 1e9
     return {"trees": trees, "rounds": rounds, "seconds": el, "value": trees / el,
             "unit": "trees/s", "rows": n, "features": f, "depth": depth, "objective": objective,
-            "nodes": nodes}
+            "nodes": nodes, "layout": layout, "algorithmic_bytes_per_tree": abytes / trees,
+            "gbs": gbs, "pct_hbm_peak": 100.0 * gbs / HBM_PEAK_GBS}
 
 
 def copy_leg(torch, args):
