@@ -102,9 +102,7 @@ __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
   }
 }
 
-template <bool COLS>
 __global__ __launch_bounds__(kPartThreads) void part_scatter_kernel(
-    const uint8_t* __restrict__ bins, int64_t n_rows, int tile_width, int missing_bin,
     const uint32_t* __restrict__ ridx_in, uint32_t* __restrict__ ridx_out,
     const PartWork* __restrict__ work, int32_t n_work_host,
     const int32_t* __restrict__ n_work_dev, const dp_split_record* __restrict__ splits,
@@ -235,11 +233,9 @@ void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_lay
                      ridx_in, work, n_work, n_work_dev, splits, work_left, masks, lp);
   DP_HIP(hipGetLastError());
   if (n_work <= 0) return;
-  DP_HIP(hipGetLastError());
-  hipLaunchKernelGGL(cols ? part_scatter_kernel<true> : part_scatter_kernel<false>, dim3(gw),
-                     dim3(kPartThreads), 0, s, src, layout.n_rows, layout.tile_width, missing,
-                     ridx_in, ridx_out, work, n_work, n_work_dev, splits, seg_begin,
-                     node_first_work, work_left, masks, node_left);
+  hipLaunchKernelGGL(part_scatter_kernel, dim3(gw), dim3(kPartThreads), 0, s, ridx_in, ridx_out,
+                     work, n_work, n_work_dev, splits, seg_begin, node_first_work, work_left,
+                     masks, node_left);
   DP_HIP(hipGetLastError());
 }
 
