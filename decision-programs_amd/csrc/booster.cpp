@@ -748,19 +748,30 @@ void Booster::enqueue(const std::vector<uint64_t>& key, bool capturable,
     }
   // Capture: nothing in body() allocates, synchronises or reads device
   // memory on the host, so the captured launches are exactly the direct ones.
+  // A capture does not run its launches, so when the runtime refuses any step
+  // of it the body is simply launched directly (and graphs stay off).
+  auto direct = [&] {
+    (void)hipGetLastError();
+    use_graphs_ = false;
+    body();
+  };
   hipGraph_t graph = nullptr;
-  DP_HIP(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+  if (hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal) != hipSuccess)
+    return direct();
   try {
     body();
   } catch (...) {
     if (hipStreamEndCapture(stream_, &graph) == hipSuccess && graph) (void)hipGraphDestroy(graph);
     throw;
   }
-  DP_HIP(hipStreamEndCapture(stream_, &graph));
+  if (hipStreamEndCapture(stream_, &graph) != hipSuccess || !graph) {
+    if (graph) (void)hipGraphDestroy(graph);
+    return direct();
+  }
   hipGraphExec_t exec = nullptr;
   const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
   (void)hipGraphDestroy(graph);
-  DP_HIP(e);
+  if (e != hipSuccess) return direct();
   constexpr size_t kMaxGraphs = 4;
   if (graphs_.size() >= kMaxGraphs) {
     DP_HIP(hipStreamSynchronize(stream_));  // the oldest may still be running
