@@ -370,8 +370,14 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
         launch_hist_reduce(partial_.p, reduce_jobs_[cur].p, int32_t(nb / 2 + 1),
                            field(c, &PlanCounts::n_reduce), T, F, B, hist_[nxt].p, h, false, s);
       }
-      launch_evaluate(h, int32_t(nb), field(c, &PlanCounts::n_level), F, B, q.d_nbins.p,
-                      sums_[cur].p, exps, 0, 0, dtp, eval_scratch_.p, splits_.p, s);
+      // Without records from the evaluation, the count launch selects them.
+      const bool records = launch_evaluate(h, int32_t(nb), field(c, &PlanCounts::n_level), F, B,
+                                           q.d_nbins.p, sums_[cur].p, exps, 0, 0, dtp,
+                                           eval_scratch_.p, splits_.p, s, false);
+      SplitSelect sel;
+      sel.cand = reinterpret_cast<const FeatCand*>(eval_scratch_.p);
+      sel.n_features = F;
+      sel.gamma = double(p.gamma);
       // The previous level's leaves (its planner wrote their chunks; their rows
       // sit in that level's ridx buffer, untouched by this level's scatter)
       // are applied by this level's count launch.
@@ -389,8 +395,8 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
                        int32_t(plan_part_capacity(nb, N, chunk_)), field(c, &PlanCounts::n_part),
                        seg_begin_[cur].p, splits_.p, part_first_[cur].p, int32_t(nb),
                        field(c, &PlanCounts::n_level), work_left_.p, part_masks_.p,
-                       node_left_[cur].p, true, s,
-                       d > 0 ? &prev : nullptr);
+                       node_left_[cur].p, true, s, d > 0 ? &prev : nullptr,
+                       records ? nullptr : &sel);
     }
     PlanArgs a{};
     a.cur = level_[cur].p;

@@ -635,9 +635,10 @@ int dp_partition(dp_workspace ws, const uint8_t* bins, const dp_bin_layout* layo
     ws->commit(s);
     int64_t* work_left = ws->take<int64_t>(work.size());
     auto* masks = ws->take<unsigned long long>(work.size() * dp::kPartMasks);
+    // the records are only read: no SplitSelect is passed
     dp::launch_partition(bins, nullptr, *layout, ridx_in, ridx_out, d_work, int32_t(work.size()),
-                         nullptr, d_begin, splits, d_first, n_nodes, nullptr, work_left, masks,
-                         left_count, false, s);
+                         nullptr, d_begin, const_cast<dp_split_record*>(splits), d_first, n_nodes,
+                         nullptr, work_left, masks, left_count, false, s);
   });
 }
 

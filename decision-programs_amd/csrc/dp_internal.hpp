@@ -78,6 +78,14 @@ struct PinnedBuffer {
 // Fixed-point quantiser precision: |q| <= 2^kQuantBits.
 constexpr int kQuantBits = 30;
 constexpr double kRtEps = 1e-6;
+
+// Best candidate of one (node, feature) from the split evaluation, or loss
+// -inf when the feature has none.
+struct FeatCand {
+  double loss;
+  long long gl, hl;
+  int32_t bin, dl;
+};
 constexpr int kMaxBins = 256;
 
 // One histogram work item: rows [begin, end) of node `slot` for one tile.
@@ -253,13 +261,17 @@ void launch_subtract(const int64_t* parent, const int64_t* built, int64_t* sibli
                      hipStream_t s);
 
 
-// Split evaluation; scratch holds evaluate_scratch_bytes(n_nodes, n_features).
+// Split evaluation; scratch holds evaluate_scratch_bytes(n_nodes, n_features)
+// (the per-feature candidates, as FeatCand [node][feature]).  Returns whether
+// the split records were written: always with select; without it, only for
+// matrices few enough features for one workgroup per node -- otherwise the
+// caller selects from the candidates (SplitSelect in launch_partition).
 size_t evaluate_scratch_bytes(int32_t n_nodes, int32_t n_features);
-void launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_nodes_dev,
+bool launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_nodes_dev,
                      int32_t n_features, int32_t bin_stride, const int32_t* n_bins,
                      const int64_t* node_sums, const int32_t* exps, int32_t exp_g, int32_t exp_h,
                      const dp_train_param& param, void* scratch, dp_split_record* out,
-                     hipStream_t s);
+                     hipStream_t s, bool select = true);
 
 // Margin (and optional leaf id) update of leaf chunks: margin[ridx[i] *
 // stride] += value, positions[ridx[i]] = leaf id; work count from n_dev when
@@ -281,13 +293,21 @@ struct LeafPass {
 // ballots, read back by the scatter).  node_left_zeroed: the caller has zeroed
 // node_left[0, nodes) (non-expanding nodes keep 0); else it is cleared here
 // for n_nodes nodes.
+// Per-feature candidates left by launch_evaluate(..., select = false): the
+// partition count selects each node's split from them and writes the records.
+struct SplitSelect {
+  const FeatCand* cand = nullptr;
+  int32_t n_features = 0;
+  double gamma = 0.0;
+};
 void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_layout& layout,
                       const uint32_t* ridx_in, uint32_t* ridx_out, const PartWork* work,
                       int32_t n_work, const int32_t* n_work_dev, const int64_t* seg_begin,
-                      const dp_split_record* splits, const int32_t* node_first_work,
+                      dp_split_record* splits, const int32_t* node_first_work,
                       int32_t n_nodes, const int32_t* n_nodes_dev, int64_t* work_left,
                       unsigned long long* masks, int64_t* node_left, bool node_left_zeroed,
-                      hipStream_t s, const LeafPass* leaves = nullptr);
+                      hipStream_t s, const LeafPass* leaves = nullptr,
+                      const SplitSelect* select = nullptr);
 constexpr int64_t kPartChunk = 4096;
 constexpr int kPartMasks = 64;  // ballot words per partition work item (kPartChunk / 64)
 

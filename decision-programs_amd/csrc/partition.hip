@@ -17,6 +17,7 @@
 // The row goes left iff its bin of the split feature is <= the split bin, or it
 // is missing and the split's default is left.
 #include "dp_internal.hpp"
+#include "select.hpp"
 
 namespace dp {
 namespace {
@@ -57,13 +58,19 @@ __device__ __forceinline__ void apply_leaf(const LeafPass& lp, const LeafWork& w
 // The partition kernels loop over their items (item = blockIdx.x + k * gridDim.x).
 // The count kernel also takes the previous level's leaf chunks as items
 // [n_work, n_work + n_leaves): their margin update rides in the same launch.
+// With sel.cand set, the split records are not written yet: each item selects
+// its node's split from the per-feature candidates (every chunk of a node gets
+// the same record) and the node's first item writes it to splits.
 template <bool COLS>
 __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
     const uint8_t* __restrict__ bins, int64_t n_rows, int tile_width, int missing_bin,
     const uint32_t* __restrict__ ridx, const PartWork* __restrict__ work, int32_t n_work_host,
-    const int32_t* __restrict__ n_work_dev, const dp_split_record* __restrict__ splits,
+    const int32_t* __restrict__ n_work_dev, dp_split_record* __restrict__ splits,
+    SplitSelect sel, const int32_t* __restrict__ node_first_work,
     int64_t* __restrict__ work_left, unsigned long long* __restrict__ masks, LeafPass lp) {
   __shared__ int wave_count[kPartThreads / 64];
+  __shared__ Cand wave_best[kPartThreads / 64];
+  __shared__ dp_split_record sel_rec;
   const int32_t n_work = n_work_dev ? *n_work_dev : n_work_host;
   const int32_t n_leaves = lp.work ? (lp.n_dev ? *lp.n_dev : lp.n_host) : 0;
   for (int32_t item = blockIdx.x; item < n_work + n_leaves; item += gridDim.x) {
@@ -72,7 +79,14 @@ __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
     continue;
   }
   const PartWork w = work[item];
-  const dp_split_record s = splits[w.node];
+  dp_split_record s;
+  if (sel.cand) {  // uniform per launch
+    s = select_node<kPartThreads>(sel.cand, w.node, sel.n_features, sel.gamma, wave_best,
+                                  &sel_rec);
+    if (threadIdx.x == 0 && item == node_first_work[w.node]) splits[w.node] = s;
+  } else {
+    s = splits[w.node];
+  }
   if (!s.expand) {
     if (threadIdx.x == 0) work_left[item] = 0;
     continue;
@@ -214,10 +228,10 @@ void launch_leaf_positions(const uint32_t* ridx, const LeafWork* work, int32_t n
 void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_layout& layout,
                       const uint32_t* ridx_in, uint32_t* ridx_out, const PartWork* work,
                       int32_t n_work, const int32_t* n_work_dev, const int64_t* seg_begin,
-                      const dp_split_record* splits, const int32_t* node_first_work,
+                      dp_split_record* splits, const int32_t* node_first_work,
                       int32_t n_nodes, const int32_t* n_nodes_dev, int64_t* work_left,
                       unsigned long long* masks, int64_t* node_left, bool node_left_zeroed,
-                      hipStream_t s, const LeafPass* leaves) {
+                      hipStream_t s, const LeafPass* leaves, const SplitSelect* select) {
   if (n_nodes <= 0) return;
   (void)n_nodes_dev;
   const int missing = layout.missing_bin;
@@ -228,9 +242,11 @@ void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_lay
   const uint8_t* src = cols ? cols : bins;
   if (!node_left_zeroed) launch_fill_i64(node_left, n_nodes, 0, s);
   if (items <= 0) return;
+  const SplitSelect sel = select ? *select : SplitSelect{};
   hipLaunchKernelGGL(cols ? part_count_kernel<true> : part_count_kernel<false>, dim3(gc),
                      dim3(kPartThreads), 0, s, src, layout.n_rows, layout.tile_width, missing,
-                     ridx_in, work, n_work, n_work_dev, splits, work_left, masks, lp);
+                     ridx_in, work, n_work, n_work_dev, splits, sel, node_first_work, work_left,
+                     masks, lp);
   DP_HIP(hipGetLastError());
   if (n_work <= 0) return;
   hipLaunchKernelGGL(part_scatter_kernel, dim3(gw), dim3(kPartThreads), 0, s, ridx_in, ridx_out,

@@ -20,6 +20,7 @@
 // All double arithmetic is compiled with -ffp-contract=off so each value
 // rounds exactly as the CPU restatement computes it.
 #include "dp_internal.hpp"
+#include "select.hpp"
 
 #include <cmath>
 
@@ -52,50 +53,7 @@ __device__ __forceinline__ double split_loss(const Param& p, long long qgl, long
   return (calc_gain(p, gl, hl) + calc_gain(p, gr, hr)) - parent_gain;
 }
 
-struct Cand {
-  double loss;
-  long long gl, hl;
-  int feature, bin, dl;
-};
-
-// a strictly better than b: larger loss; equal loss -> lower feature, then bin.
-__device__ __forceinline__ bool better(const Cand& a, const Cand& b) {
-  if (a.loss > b.loss) return true;
-  if (a.loss < b.loss) return false;
-  if (a.feature != b.feature) return unsigned(a.feature) < unsigned(b.feature);
-  return unsigned(a.bin) < unsigned(b.bin);
-}
-
-__device__ __forceinline__ Cand shfl_xor_cand(const Cand& c, int mask) {
-  Cand o;
-  o.loss = __shfl_xor(c.loss, mask, 64);
-  o.gl = __shfl_xor(c.gl, mask, 64);
-  o.hl = __shfl_xor(c.hl, mask, 64);
-  o.feature = __shfl_xor(c.feature, mask, 64);
-  o.bin = __shfl_xor(c.bin, mask, 64);
-  o.dl = __shfl_xor(c.dl, mask, 64);
-  return o;
-}
-
-// Best candidate of one (node, feature), or loss -inf when it has none.
-struct FeatCand {
-  double loss;
-  long long gl, hl;
-  int32_t bin, dl;
-};
-
 constexpr int kFeatWaves = 4;  // features per workgroup in evaluate_features_kernel
-
-// Cross-lane moves on the DPP path (VALU lane swizzles, no LDS round trip).
-// dpp64 moves a 64-bit value as two 32-bit halves; lanes whose source is out
-// of range or whose row is masked off receive `old`.
-template <int CTRL, int ROW_MASK = 0xf>
-__device__ __forceinline__ long long dpp64(long long v, long long old) {
-  const int lo = __builtin_amdgcn_update_dpp(int(old), int(v), CTRL, ROW_MASK, 0xf, false);
-  const int hi = __builtin_amdgcn_update_dpp(int(old >> 32), int(v >> 32), CTRL, ROW_MASK, 0xf,
-                                             false);
-  return (long long)((uint64_t(uint32_t(hi)) << 32) | uint32_t(lo));
-}
 
 __device__ __forceinline__ double dpp_f64_bits(long long bits) { return __longlong_as_double(bits); }
 
@@ -128,11 +86,6 @@ __device__ __forceinline__ double wave_max_to_last(double v) {
   return dpp_f64_bits(b);
 }
 
-__device__ __forceinline__ long long readlane64(long long v, int lane) {
-  const int lo = __builtin_amdgcn_readlane(int(v), lane);
-  const int hi = __builtin_amdgcn_readlane(int(v >> 32), lane);
-  return (long long)((uint64_t(uint32_t(hi)) << 32) | uint32_t(lo));
-}
 
 // One feature's histogram of one node as one wavefront holds it: bins
 // lane * BPL + j (bins past bin_stride read as zero).
@@ -225,21 +178,6 @@ __device__ __forceinline__ Cand feature_best(const FeatBins<BPL>& d, int32_t f, 
   return r;
 }
 
-// The split record of a node's best candidate.
-__device__ __forceinline__ dp_split_record make_record(const Cand& r, double gamma) {
-  dp_split_record rec;
-  rec.loss_chg = r.loss;
-  rec.gl = r.gl;
-  rec.hl = r.hl;
-  rec.feature = r.feature;
-  rec.bin = r.bin;
-  rec.default_left = r.dl;
-  rec.valid = r.loss > -INFINITY ? 1 : 0;
-  rec.expand = rec.valid && r.loss > kRtEps && r.loss >= gamma;
-  rec.pad = 0;
-  return rec;
-}
-
 // One wavefront per (node, feature): the feature's best candidate.
 // Workgroups loop over (node, feature group) items; the node count may come
 // from device memory.
@@ -329,40 +267,12 @@ __global__ __launch_bounds__(kSelectThreads) void select_splits_kernel(
     const int32_t* __restrict__ n_nodes_dev, int32_t n_features, double gamma,
     dp_split_record* __restrict__ out) {
   __shared__ Cand wave_best[kSelectThreads / 64];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __shared__ dp_split_record rec;
   const int32_t n_nodes = n_nodes_dev ? *n_nodes_dev : n_nodes_host;
   for (int32_t node = blockIdx.x; node < n_nodes; node += gridDim.x) {
-    Cand best;
-    best.loss = -INFINITY;
-    best.gl = best.hl = 0;
-    best.feature = -1;
-    best.bin = -1;
-    best.dl = 0;
-    for (int32_t f = threadIdx.x; f < n_features; f += kSelectThreads) {
-      const FeatCand fc = cand[int64_t(node) * n_features + f];
-      Cand c;
-      c.loss = fc.loss;
-      c.gl = fc.gl;
-      c.hl = fc.hl;
-      c.feature = f;
-      c.bin = fc.bin;
-      c.dl = fc.dl;
-      if (fc.loss > -INFINITY && better(c, best)) best = c;
-    }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-      const Cand o = shfl_xor_cand(best, m);
-      if (better(o, best)) best = o;
-    }
-    if (lane == 0) wave_best[wave] = best;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      Cand r = wave_best[0];
-      for (int k = 1; k < kSelectThreads / 64; ++k)
-        if (better(wave_best[k], r)) r = wave_best[k];
-      out[node] = make_record(r, gamma);
-    }
-    __syncthreads();  // wave_best is reused by the next node
+    const dp_split_record r =
+        select_node<kSelectThreads>(cand, node, n_features, gamma, wave_best, &rec);
+    if (threadIdx.x == 0) out[node] = r;
   }
 }
 
@@ -372,12 +282,12 @@ size_t evaluate_scratch_bytes(int32_t n_nodes, int32_t n_features) {
   return sizeof(FeatCand) * size_t(n_nodes > 0 ? n_nodes : 0) * size_t(n_features);
 }
 
-void launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_nodes_dev,
+bool launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_nodes_dev,
                      int32_t n_features, int32_t bin_stride, const int32_t* n_bins,
                      const int64_t* node_sums, const int32_t* exps, int32_t exp_g, int32_t exp_h,
                      const dp_train_param& param, void* scratch, dp_split_record* out,
-                     hipStream_t s) {
-  if (n_nodes <= 0) return;
+                     hipStream_t s, bool select) {
+  if (n_nodes <= 0) return true;
   need(bin_stride >= 1 && bin_stride <= kMaxBins, "split bin stride out of range");
   need(n_features >= 1, "split evaluation needs at least one feature");
   Param p{double(param.lambda), double(param.alpha), double(param.min_child_weight),
@@ -396,7 +306,7 @@ void launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_node
       hipLaunchKernelGGL(evaluate_nodes_kernel<4>, grid, block, 0, s, h, n_nodes, n_nodes_dev,
                          n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p, out);
     DP_HIP(hipGetLastError());
-    return;
+    return true;
   }
   auto* cand = static_cast<FeatCand*>(scratch);
   const int64_t groups = (n_features + kFeatWaves - 1) / kFeatWaves;
@@ -416,10 +326,12 @@ void launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_node
                        n_nodes_dev, n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p,
                        cand);
   DP_HIP(hipGetLastError());
+  if (!select) return false;
   hipLaunchKernelGGL(select_splits_kernel, dim3(n_nodes < 1024 ? n_nodes : 1024),
                      dim3(kSelectThreads), 0, s, cand, n_nodes, n_nodes_dev, n_features,
                      double(param.gamma), out);
   DP_HIP(hipGetLastError());
+  return true;
 }
 
 }  // namespace dp
