@@ -108,6 +108,10 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8,
   __shared__ unsigned long long lds[kLdsWords];
   constexpr int U = kHistUnroll;
   constexpr int64_t kStep = int64_t(kHistThreads) * U;
+  // The first item is loaded alongside the device count (the host bound keeps
+  // it in range), so the two loads overlap instead of chaining.
+  const HistWork w_first =
+      int32_t(blockIdx.x) < n_work_host ? work[blockIdx.x] : HistWork{0, 0, 0, 0, -1, 0};
   const int32_t n_work = n_work_dev ? *n_work_dev : n_work_host;
   const uint32_t rot = threadIdx.x & 15u;
   uint32_t slotw[4];  // byte i of slotw[m]: feature offset (bytes) of step 4m+i
@@ -120,7 +124,7 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8,
   }
   lds_u8* const lds_base = (lds_u8*)lds;
   for (int32_t item = blockIdx.x; item < n_work; item += gridDim.x) {
-  const HistWork w = work[item];
+  const HistWork w = item == int32_t(blockIdx.x) ? w_first : work[item];
   if (w.begin >= w.end) continue;  // padding item (uniform per workgroup)
   for (int e = threadIdx.x; e < kLdsWords; e += kHistThreads) lds[e] = 0ull;
   __syncthreads();
@@ -356,6 +360,7 @@ __global__ __launch_bounds__(256) void hist_reduce_kernel(
     int32_t n_jobs_host, const int32_t* __restrict__ n_jobs_dev, int32_t n_tiles,
     int32_t n_features, int32_t bin_stride, const long long* __restrict__ parent_base,
     long long* __restrict__ hist, int32_t accumulate) {
+  const HistReduce j_first = int32_t(blockIdx.z) < n_jobs_host ? jobs[blockIdx.z] : HistReduce{};
   const int32_t n_jobs = n_jobs_dev ? *n_jobs_dev : n_jobs_host;
   const int n_words = bin_stride * 32;
   const int e = blockIdx.x * 256 + threadIdx.x;
@@ -366,7 +371,7 @@ __global__ __launch_bounds__(256) void hist_reduce_kernel(
   const int64_t node_elems = int64_t(n_features) * bin_stride * 2;
   const int64_t at = (int64_t(f) * bin_stride + bin) * 2 + (within >> 4);
   for (int32_t jb = blockIdx.z; jb < n_jobs; jb += gridDim.z) {
-    const HistReduce j = jobs[jb];
+    const HistReduce j = jb == int32_t(blockIdx.z) ? j_first : jobs[jb];
     long long* built = hist + int64_t(j.slot) * node_elems + at;
     long long sum;
     if (j.nc == 1 && j.p0 < 0) {

@@ -71,6 +71,10 @@ __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
   __shared__ int wave_count[kPartThreads / 64];
   __shared__ Cand wave_best[kPartThreads / 64];
   __shared__ dp_split_record sel_rec;
+  // The first item is loaded alongside the device counts (the host bound keeps
+  // it in range), so the loads overlap instead of chaining.
+  const PartWork w_first =
+      int32_t(blockIdx.x) < n_work_host ? work[blockIdx.x] : PartWork{0, 0, 0, 0};
   const int32_t n_work = n_work_dev ? *n_work_dev : n_work_host;
   const int32_t n_leaves = lp.work ? (lp.n_dev ? *lp.n_dev : lp.n_host) : 0;
   for (int32_t item = blockIdx.x; item < n_work + n_leaves; item += gridDim.x) {
@@ -78,7 +82,7 @@ __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
     apply_leaf(lp, lp.work[item - n_work]);
     continue;
   }
-  const PartWork w = work[item];
+  const PartWork w = item == int32_t(blockIdx.x) ? w_first : work[item];
   dp_split_record s;
   if (sel.cand) {  // uniform per launch
     s = select_node<kPartThreads>(sel.cand, w.node, sel.n_features, sel.gamma, wave_best,
@@ -125,10 +129,12 @@ __global__ __launch_bounds__(kPartThreads) void part_scatter_kernel(
     int64_t* __restrict__ node_left) {
   __shared__ int wave_count[kPartThreads / 64];
   __shared__ int64_t wave_sum[2][kPartThreads / 64];
+  const PartWork w_first =
+      int32_t(blockIdx.x) < n_work_host ? work[blockIdx.x] : PartWork{0, 0, 0, 0};
   const int32_t n_work = n_work_dev ? *n_work_dev : n_work_host;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   for (int32_t item = blockIdx.x; item < n_work; item += gridDim.x) {
-  const PartWork w = work[item];
+  const PartWork w = item == int32_t(blockIdx.x) ? w_first : work[item];
   const dp_split_record s = splits[w.node];
   if (!s.expand) continue;
   const int64_t begin = seg_begin[w.node];
