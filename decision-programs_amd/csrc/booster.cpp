@@ -339,7 +339,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
       ensure_level(q, nb, d, D);
       const int64_t need_nodes = int64_t(host_counts->n_nodes) + 2 * nb;
       if (int64_t(info_.n) < need_nodes) {
-        DeviceBuffer<NodeInfo> grown(size_t(std::max<int64_t>(need_nodes, 2 * int64_t(info_.n))));
+        PooledBuffer<NodeInfo> grown(size_t(std::max<int64_t>(need_nodes, 2 * int64_t(info_.n))));
         DP_HIP(hipMemcpyAsync(grown.p, info_.p, info_.bytes(), hipMemcpyDeviceToDevice, s));
         DP_HIP(hipStreamSynchronize(s));
         info_ = std::move(grown);

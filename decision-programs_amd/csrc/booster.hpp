@@ -99,26 +99,26 @@ class Grower {
 
  private:
   void ensure_level(const Quantized& q, int64_t nodes, int32_t depth, int32_t max_depth);
-  DeviceBuffer<uint32_t> ridx_[2];
-  DeviceBuffer<int64_t> hist_[2];
-  DeviceBuffer<LevelNode> level_[2];
-  DeviceBuffer<int64_t> sums_[2], seg_begin_[2];
-  DeviceBuffer<HistWork> hist_work_[2], root_work_;
-  DeviceBuffer<HistReduce> reduce_jobs_[2], root_job_;
-  DeviceBuffer<int64_t> partial_;
-  DeviceBuffer<PartWork> part_work_[2];
-  DeviceBuffer<int32_t> part_first_[2];
-  DeviceBuffer<int64_t> pair_chunk_, work_left_, node_left_[2];
-  DeviceBuffer<unsigned long long> part_masks_;  // count ballots, kPartMasks per item
-  DeviceBuffer<dp_split_record> splits_;
-  DeviceBuffer<uint8_t> eval_scratch_;
-  DeviceBuffer<LeafWork> leaf_work_[2];  // by level parity: applied one level later
-  DeviceBuffer<NodeInfo> info_;
-  DeviceBuffer<PlanCounts> counts_;
-  DeviceBuffer<uint8_t> slots_;  // eager: per slot, PlanCounts then NodeInfo[node_cap_]
-  PinnedBuffer readback_;        // host copies of slots_: two buffers of readback_slots_ slots
+  PooledBuffer<uint32_t> ridx_[2];
+  PooledBuffer<int64_t> hist_[2];
+  PooledBuffer<LevelNode> level_[2];
+  PooledBuffer<int64_t> sums_[2], seg_begin_[2];
+  PooledBuffer<HistWork> hist_work_[2], root_work_;
+  PooledBuffer<HistReduce> reduce_jobs_[2], root_job_;
+  PooledBuffer<int64_t> partial_;
+  PooledBuffer<PartWork> part_work_[2];
+  PooledBuffer<int32_t> part_first_[2];
+  PooledBuffer<int64_t> pair_chunk_, work_left_, node_left_[2];
+  PooledBuffer<unsigned long long> part_masks_;  // count ballots, kPartMasks per item
+  PooledBuffer<dp_split_record> splits_;
+  PooledBuffer<uint8_t> eval_scratch_;
+  PooledBuffer<LeafWork> leaf_work_[2];  // by level parity: applied one level later
+  PooledBuffer<NodeInfo> info_;
+  PooledBuffer<PlanCounts> counts_;
+  PooledBuffer<uint8_t> slots_;  // eager: per slot, PlanCounts then NodeInfo[node_cap_]
+  PooledPinnedBuffer readback_;        // host copies of slots_: two buffers of readback_slots_ slots
   int32_t readback_slots_ = 0;
-  PinnedBuffer level_count_;
+  PooledPinnedBuffer level_count_;
   std::vector<std::vector<NodeInfo>> spill_;  // slots of trees grown level-synced
   std::vector<PlanCounts> spill_counts_;
   bool eager_ = true;
@@ -203,13 +203,13 @@ class Booster {
   TrainParam tp_;
   DMatrix* train_ = nullptr;
   // training state
-  DeviceBuffer<float> margin_, grad_, hess_;
-  DeviceBuffer<int32_t> gpair_, exps_;
-  DeviceBuffer<int64_t> sums_;
-  DeviceBuffer<uint8_t> quant_scratch_;  // quantiser reduction slots
-  DeviceBuffer<int32_t> positions_;
+  PooledBuffer<float> margin_, grad_, hess_;
+  PooledBuffer<int32_t> gpair_, exps_;
+  PooledBuffer<int64_t> sums_;
+  PooledBuffer<uint8_t> quant_scratch_;  // quantiser reduction slots
+  PooledBuffer<int32_t> positions_;
   mutable std::vector<int32_t> last_exps_;
-  PinnedBuffer exps_host_;  // two buffers, by round parity
+  PooledPinnedBuffer exps_host_;  // two buffers, by round parity
   bool record_positions_ = false;
   bool use_graphs_ = true;
   int32_t sparse_mode_ = 1;  // dp_sparse_hist: 0 never, 1 when <= 1/4 present, 2 with any NaN

@@ -26,8 +26,20 @@ inline void hip_check(hipError_t status, const char* what) {
 }
 #define DP_HIP(call) ::dp::hip_check((call), #call)
 
-// Owning device allocation.
-template <class T>
+// Cached allocations for the booster's training buffers (pool.cpp).  A block
+// handed back is kept, by device and exact size, for the next allocation of
+// that size (a new booster on the same configuration, a study's next trial)
+// instead of going through hipMalloc / hipHostMalloc again.  Only buffers
+// whose last use has completed may be handed back: their owners synchronise
+// their streams first.  A miss that the device cannot serve empties the cache
+// and retries.
+void* device_pool_get(size_t bytes);
+void device_pool_put(void* p, size_t bytes);
+void* pinned_pool_get(size_t bytes);
+void pinned_pool_put(void* p, size_t bytes);
+
+// Owning device allocation (POOLED: through the cache above).
+template <class T, bool POOLED = false>
 struct DeviceBuffer {
   T* p = nullptr;
   size_t n = 0;
@@ -42,13 +54,19 @@ struct DeviceBuffer {
   }
   ~DeviceBuffer() { release(); }
   void release() {
-    if (p) (void)hipFree(p);
+    if (p) {
+      if (POOLED) device_pool_put(p, n * sizeof(T));
+      else (void)hipFree(p);
+    }
     p = nullptr;
     n = 0;
   }
   void resize(size_t count) {
     release();
-    if (count) DP_HIP(hipMalloc(reinterpret_cast<void**>(&p), count * sizeof(T)));
+    if (count) {
+      if (POOLED) p = static_cast<T*>(device_pool_get(count * sizeof(T)));
+      else DP_HIP(hipMalloc(reinterpret_cast<void**>(&p), count * sizeof(T)));
+    }
     n = count;
   }
   // Grows (discarding contents) when smaller than `count`.
@@ -57,23 +75,36 @@ struct DeviceBuffer {
   }
   size_t bytes() const { return n * sizeof(T); }
 };
+template <class T>
+using PooledBuffer = DeviceBuffer<T, true>;
 
 // Pinned host allocation (hipHostMalloc; never hipHostRegister).
-struct PinnedBuffer {
+template <bool POOLED = false>
+struct PinnedBufferT {
   uint8_t* p = nullptr;
   size_t n = 0;
-  PinnedBuffer() = default;
-  PinnedBuffer(const PinnedBuffer&) = delete;
-  PinnedBuffer& operator=(const PinnedBuffer&) = delete;
-  ~PinnedBuffer() { if (p) (void)hipHostFree(p); }
+  PinnedBufferT() = default;
+  PinnedBufferT(const PinnedBufferT&) = delete;
+  PinnedBufferT& operator=(const PinnedBufferT&) = delete;
+  ~PinnedBufferT() { release(); }
+  void release() {
+    if (p) {
+      if (POOLED) pinned_pool_put(p, n);
+      else (void)hipHostFree(p);
+    }
+    p = nullptr;
+    n = 0;
+  }
   void reserve(size_t count) {
     if (count <= n) return;
-    if (p) (void)hipHostFree(p);
-    p = nullptr;
-    DP_HIP(hipHostMalloc(reinterpret_cast<void**>(&p), count, hipHostMallocDefault));
+    release();
+    if (POOLED) p = static_cast<uint8_t*>(pinned_pool_get(count));
+    else DP_HIP(hipHostMalloc(reinterpret_cast<void**>(&p), count, hipHostMallocDefault));
     n = count;
   }
 };
+using PinnedBuffer = PinnedBufferT<false>;
+using PooledPinnedBuffer = PinnedBufferT<true>;
 
 // Fixed-point quantiser precision: |q| <= 2^kQuantBits.
 constexpr int kQuantBits = 30;
