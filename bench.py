@@ -251,9 +251,11 @@ def tree_algorithmic_bytes(t, n_rows, n_features, n_bins, depth, density=None):
     return total
 
 
-def trees_leg(torch, dp, ops, name, rows=None, warm_rounds=2):
+def trees_leg(torch, dp, ops, name, rows=None, warm_rounds=4):
     """Wall time of the configuration's boosting rounds on a fresh booster (the
-    matrix is quantised and the kernels warmed by a previous booster)."""
+    matrix is quantised and the kernels warmed by a previous booster).  The warm
+    booster runs four rounds: the first replay of a captured round in a process
+    takes a one-off 6-8 ms, paid by the third round's wait."""
     config, n, rounds, depth, eta, objective, max_bin, injected = TREE_CONFIGS[name]
     n = rows or n
     f = ops.SYNTH_FEATURES[config]
