@@ -11,7 +11,8 @@
 //   2. scatter: each chunk sums the counts of its node's chunks (the node's
 //      left total, and its own exclusive offset from the earlier ones; the
 //      node's first chunk publishes the total in node_left), ranks its rows in
-//      position order (ballot prefix counts, 256 rows per step) and writes
+//      position order (an exclusive scan of the chunk's 64 ballot counts, one
+//      per lane, plus the lane's prefix in its ballot) and writes
 //      lefts to [begin + left rank) and rights to [begin + n_left + right rank)
 //      of ridx_out.  No atomics: a node can have thousands of chunks.
 // The row goes left iff its bin of the split feature is <= the split bin, or it
@@ -29,29 +30,39 @@ static_assert(kPartSteps * (kPartThreads / 64) == kPartMasks, "one mask per wave
 // The split feature's bin of `row`: from the column-major copy when there is
 // one (one byte per row, contiguous within a feature), else from the tiles.
 template <bool COLS>
-__device__ __forceinline__ bool goes_left(const uint8_t* __restrict__ bins, int64_t n_rows,
-                                          int tile_width, uint32_t row, int feature,
-                                          int split_bin, int default_left, int missing_bin) {
-  int b;
-  if (COLS) {
-    b = bins[int64_t(feature) * n_rows + row];
-  } else {
-    const int64_t tile = feature / tile_width;
-    const int within = feature - int(tile) * tile_width;
-    b = bins[tile * n_rows * tile_width + int64_t(row) * tile_width + within];
-  }
-  if (b == missing_bin) return default_left != 0;
-  return b <= split_bin;
+__device__ __forceinline__ int split_bin_of(const uint8_t* __restrict__ bins, int64_t n_rows,
+                                            int tile_width, uint32_t row, int feature) {
+  if (COLS) return bins[int64_t(feature) * n_rows + row];
+  const int64_t tile = feature / tile_width;
+  const int within = feature - int(tile) * tile_width;
+  return bins[tile * n_rows * tile_width + int64_t(row) * tile_width + within];
 }
 
 __device__ __forceinline__ int popc64(unsigned long long m) { return __popcll(m); }
 
-// The margin (and leaf id) update of one leaf chunk.
-__device__ __forceinline__ void apply_leaf(const LeafPass& lp, const LeafWork& w) {
-  for (int64_t i = w.begin + threadIdx.x; i < w.end; i += blockDim.x) {
-    const uint32_t row = lp.ridx[i];
-    lp.margin[int64_t(row) * lp.stride] += w.value;
-    if (lp.positions) lp.positions[row] = w.pad;
+// The margin (and leaf id) update of one leaf chunk (taken by value: the
+// margin stores cannot alias it).  Row ids are loaded a batch ahead of their
+// margins, at indexes clamped into the chunk (i0 < end), so the loads need no
+// branch and overlap; a chunk's rows are distinct, so all margins of a batch
+// are read before any is written.
+__device__ __forceinline__ void apply_leaf(const LeafPass& lp, const LeafWork w) {
+  constexpr int kBatch = 8;
+  for (int64_t i0 = w.begin + threadIdx.x; i0 < w.end; i0 += int64_t(kBatch) * blockDim.x) {
+    uint32_t row[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int64_t i = i0 + int64_t(k) * blockDim.x;
+      row[k] = lp.ridx[i < w.end ? i : w.end - 1];
+    }
+    float m[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) m[k] = lp.margin[int64_t(row[k]) * lp.stride];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      if (i0 + int64_t(k) * blockDim.x >= w.end) break;
+      lp.margin[int64_t(row[k]) * lp.stride] = m[k] + w.value;
+      if (lp.positions) lp.positions[row[k]] = w.pad;
+    }
   }
 }
 
@@ -61,7 +72,11 @@ __device__ __forceinline__ void apply_leaf(const LeafPass& lp, const LeafWork& w
 // With sel.cand set, the split records are not written yet: each item selects
 // its node's split from the per-feature candidates (every chunk of a node gets
 // the same record) and the node's first item writes it to splits.
-template <bool COLS>
+// A lane handles rows begin + step * 256 + threadIdx.x, step = 0..15, in
+// groups of G steps whose row ids, then bins, are loaded together.  G = 4
+// keeps more loads in flight and pays on large levels; on levels of about a
+// million rows or fewer (data in cache) G = 1 measured faster.
+template <bool COLS, int G>
 __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
     const uint8_t* __restrict__ bins, int64_t n_rows, int tile_width, int missing_bin,
     const uint32_t* __restrict__ ridx, const PartWork* __restrict__ work, int32_t n_work_host,
@@ -77,6 +92,7 @@ __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
       int32_t(blockIdx.x) < n_work_host ? work[blockIdx.x] : PartWork{0, 0, 0, 0};
   const int32_t n_work = n_work_dev ? *n_work_dev : n_work_host;
   const int32_t n_leaves = lp.work ? (lp.n_dev ? *lp.n_dev : lp.n_host) : 0;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   for (int32_t item = blockIdx.x; item < n_work + n_leaves; item += gridDim.x) {
   if (item >= n_work) {  // uniform per workgroup; no barriers on this path
     apply_leaf(lp, lp.work[item - n_work]);
@@ -96,19 +112,31 @@ __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
     continue;
   }
   int count = 0;
-  for (int step = 0; step < kPartSteps; ++step) {
-    if (w.begin + int64_t(step) * kPartThreads >= w.end) break;  // uniform per workgroup
-    const int64_t i = w.begin + int64_t(step) * kPartThreads + threadIdx.x;
-    bool left = false;
-    if (i < w.end)
-      left = goes_left<COLS>(bins, n_rows, tile_width, ridx[i], s.feature, s.bin,
-                             s.default_left, missing_bin);
-    const unsigned long long m = __ballot(left);
-    if ((threadIdx.x & 63) == 0)
-      masks[int64_t(item) * kPartMasks + step * (kPartThreads / 64) + (threadIdx.x >> 6)] = m;
-    count += popc64(m);
+  unsigned long long* item_masks = masks + int64_t(item) * kPartMasks + wave;
+#pragma unroll 1
+  for (int g0 = 0; g0 < kPartSteps; g0 += G) {
+    if (w.begin + int64_t(g0) * kPartThreads >= w.end) break;  // uniform per workgroup
+    uint32_t row[G];
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+      const int64_t i = w.begin + int64_t(g0 + k) * kPartThreads + threadIdx.x;
+      row[k] = i < w.end ? ridx[i] : 0u;
+    }
+    int bin[G];
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+      const int64_t i = w.begin + int64_t(g0 + k) * kPartThreads + threadIdx.x;
+      bin[k] = i < w.end ? split_bin_of<COLS>(bins, n_rows, tile_width, row[k], s.feature) : -1;
+    }
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+      const int b = bin[k];
+      const bool left = b >= 0 && (b == missing_bin ? s.default_left != 0 : b <= s.bin);
+      const unsigned long long m = __ballot(left);
+      if (lane == 0) item_masks[(g0 + k) * (kPartThreads / 64)] = m;
+      count += popc64(m);
+    }
   }
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (lane == 0) wave_count[wave] = count;
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -120,6 +148,11 @@ __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
   }
 }
 
+// Lane l of every wavefront holds ballot l of the item (step l / 4, wavefront
+// l % 4), which is also position order; an exclusive scan of their counts
+// gives each (step, wavefront) its lefts before it in the item, so the steps
+// need no barrier.  The item's barriers share the node-level sums.
+template <int G>
 __global__ __launch_bounds__(kPartThreads) void part_scatter_kernel(
     const uint32_t* __restrict__ ridx_in, uint32_t* __restrict__ ridx_out,
     const PartWork* __restrict__ work, int32_t n_work_host,
@@ -127,72 +160,64 @@ __global__ __launch_bounds__(kPartThreads) void part_scatter_kernel(
     const int64_t* __restrict__ seg_begin, const int32_t* __restrict__ node_first_work,
     const int64_t* __restrict__ work_left, const unsigned long long* __restrict__ masks,
     int64_t* __restrict__ node_left) {
-  __shared__ int wave_count[kPartThreads / 64];
   __shared__ int64_t wave_sum[2][kPartThreads / 64];
   const PartWork w_first =
       int32_t(blockIdx.x) < n_work_host ? work[blockIdx.x] : PartWork{0, 0, 0, 0};
   const int32_t n_work = n_work_dev ? *n_work_dev : n_work_host;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   for (int32_t item = blockIdx.x; item < n_work; item += gridDim.x) {
   const PartWork w = item == int32_t(blockIdx.x) ? w_first : work[item];
   const dp_split_record s = splits[w.node];
   if (!s.expand) continue;
+  const unsigned long long my_mask = masks[int64_t(item) * kPartMasks + lane];
   const int64_t begin = seg_begin[w.node];
   // the node's left total and the lefts in its chunks before this one
   const int32_t first = node_first_work[w.node], last = node_first_work[w.node + 1];
-  int64_t before = 0, total = 0;
+  long long before = 0, total = 0;
   for (int32_t k = first + threadIdx.x; k < last; k += kPartThreads) {
     const int64_t v = work_left[k];
     total += v;
     if (k < item) before += v;
   }
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    before += __shfl_xor(before, m, 64);
-    total += __shfl_xor(total, m, 64);
-  }
-  if (lane == 0) {
+  before = wave_inclusive_sum(before);
+  total = wave_inclusive_sum(total);
+  if (lane == 63) {
     wave_sum[0][wave] = before;
     wave_sum[1][wave] = total;
   }
+  // lefts before each ballot of the item, in position order
+  const long long c = popc64(my_mask);
+  const int excl = int(wave_inclusive_sum(c) - c);
   __syncthreads();
-  int64_t lefts_before = 0, n_left = 0;  // lefts before this step; node total
+  int64_t lefts_before = 0, n_left = 0;  // lefts before this item; node total
   for (int k = 0; k < kPartThreads / 64; ++k) {
     lefts_before += wave_sum[0][k];
     n_left += wave_sum[1][k];
   }
+  __syncthreads();  // wave_sum is rewritten by the next item
   if (item == first && threadIdx.x == 0) node_left[w.node] = n_left;
-  const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int step = 0; step < kPartSteps; ++step) {
-    const int64_t step_base = w.begin + int64_t(step) * kPartThreads;
-    if (step_base >= w.end) break;
-    const int64_t i = step_base + threadIdx.x;
-    bool valid = i < w.end;
-    uint32_t row = 0;
-    // the count kernel's ballot for this wavefront and step
-    const unsigned long long mask =
-        masks[int64_t(item) * kPartMasks + step * (kPartThreads / 64) + wave];
-    const bool left = (mask >> lane) & 1ull;
-    if (valid) row = ridx_in[i];
-    if (lane == 0) wave_count[wave] = popc64(mask);
-    __syncthreads();
-    int64_t prefix = lefts_before;
-    int step_total = 0;
-    for (int k = 0; k < kPartThreads / 64; ++k) {
-      if (k < wave) prefix += wave_count[k];
-      step_total += wave_count[k];
+#pragma unroll 1
+  for (int g0 = 0; g0 < kPartSteps; g0 += G) {
+    if (w.begin + int64_t(g0) * kPartThreads >= w.end) break;  // uniform per workgroup
+    uint32_t row[G];
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+      const int64_t i = w.begin + int64_t(g0 + k) * kPartThreads + threadIdx.x;
+      row[k] = i < w.end ? ridx_in[i] : 0u;
     }
-    prefix += popc64(mask & below);
-    if (valid) {
-      if (left) {
-        ridx_out[begin + prefix] = row;
-      } else {
-        const int64_t rights_before = (i - begin) - prefix;
-        ridx_out[begin + n_left + rights_before] = row;
-      }
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+      const int64_t i = w.begin + int64_t(g0 + k) * kPartThreads + threadIdx.x;
+      const int idx = (g0 + k) * (kPartThreads / 64) + wave;
+      const unsigned long long mask = (unsigned long long)readlane64((long long)my_mask, idx);
+      const int64_t prefix =
+          lefts_before + __builtin_amdgcn_readlane(excl, idx) + popc64(mask & below);
+      const int64_t dst = ((mask >> lane) & 1ull) ? begin + prefix
+                                                  : begin + n_left + ((i - begin) - prefix);
+      if (i < w.end) ridx_out[dst] = row[k];
     }
-    lefts_before += step_total;
-    __syncthreads();
   }
   }
 }
@@ -202,10 +227,23 @@ __global__ void update_margin_kernel(const uint32_t* __restrict__ ridx,
                                      const int32_t* __restrict__ n_work_dev,
                                      float* __restrict__ margin, int64_t stride) {
   const int32_t n_work = n_work_dev ? *n_work_dev : n_work_host;
+  constexpr int kBatch = 8;  // as apply_leaf: row ids, then margins, then stores
   for (int32_t item = blockIdx.x; item < n_work; item += gridDim.x) {
     const LeafWork w = work[item];
-    for (int64_t i = w.begin + threadIdx.x; i < w.end; i += blockDim.x)
-      margin[int64_t(ridx[i]) * stride] += w.value;
+    for (int64_t i0 = w.begin + threadIdx.x; i0 < w.end; i0 += int64_t(kBatch) * blockDim.x) {
+      uint32_t row[kBatch];
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        const int64_t i = i0 + int64_t(k) * blockDim.x;
+        row[k] = ridx[i < w.end ? i : w.end - 1];
+      }
+      float m[kBatch];
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) m[k] = margin[int64_t(row[k]) * stride];
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k)
+        if (i0 + int64_t(k) * blockDim.x < w.end) margin[int64_t(row[k]) * stride] = m[k] + w.value;
+    }
   }
 }
 
@@ -249,15 +287,18 @@ void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_lay
   if (!node_left_zeroed) launch_fill_i64(node_left, n_nodes, 0, s);
   if (items <= 0) return;
   const SplitSelect sel = select ? *select : SplitSelect{};
-  hipLaunchKernelGGL(cols ? part_count_kernel<true> : part_count_kernel<false>, dim3(gc),
-                     dim3(kPartThreads), 0, s, src, layout.n_rows, layout.tile_width, missing,
-                     ridx_in, work, n_work, n_work_dev, splits, sel, node_first_work, work_left,
-                     masks, lp);
+  // Four steps per load group on matrices of 4M rows or more, else one.
+  const bool wide = layout.n_rows >= (int64_t(1) << 22);
+  auto count = cols ? (wide ? part_count_kernel<true, 4> : part_count_kernel<true, 1>)
+                    : (wide ? part_count_kernel<false, 4> : part_count_kernel<false, 1>);
+  hipLaunchKernelGGL(count, dim3(gc), dim3(kPartThreads), 0, s, src, layout.n_rows,
+                     layout.tile_width, missing, ridx_in, work, n_work, n_work_dev, splits, sel,
+                     node_first_work, work_left, masks, lp);
   DP_HIP(hipGetLastError());
   if (n_work <= 0) return;
-  hipLaunchKernelGGL(part_scatter_kernel, dim3(gw), dim3(kPartThreads), 0, s, ridx_in, ridx_out,
-                     work, n_work, n_work_dev, splits, seg_begin, node_first_work, work_left,
-                     masks, node_left);
+  hipLaunchKernelGGL(wide ? part_scatter_kernel<4> : part_scatter_kernel<1>, dim3(gw),
+                     dim3(kPartThreads), 0, s, ridx_in, ridx_out, work, n_work, n_work_dev,
+                     splits, seg_begin, node_first_work, work_left, masks, node_left);
   DP_HIP(hipGetLastError());
 }
 

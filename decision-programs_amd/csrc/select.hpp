@@ -72,6 +72,19 @@ __device__ __forceinline__ long long readlane64(long long v, int lane) {
   return (long long)((uint64_t(uint32_t(hi)) << 32) | uint32_t(lo));
 }
 
+// Inclusive wavefront scan: row_shr 1, 2, 4, 8 within each 16-lane row, then
+// row_bcast15 (lane 15 of rows 0 and 2 into rows 1 and 3) and row_bcast31
+// (lane 31 into rows 2 and 3).
+__device__ __forceinline__ long long wave_inclusive_sum(long long x) {
+  x += dpp64<0x111>(x, 0);
+  x += dpp64<0x112>(x, 0);
+  x += dpp64<0x114>(x, 0);
+  x += dpp64<0x118>(x, 0);
+  x += dpp64<0x142, 0xa>(x, 0);
+  x += dpp64<0x143, 0xc>(x, 0);
+  return x;
+}
+
 // The largest double of the wavefront, returned to every lane.
 __device__ __forceinline__ double wave_max_f64(double v) {
   long long b = __double_as_longlong(v);

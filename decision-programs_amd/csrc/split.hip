@@ -57,19 +57,6 @@ constexpr int kFeatWaves = 4;  // features per workgroup in evaluate_features_ke
 
 __device__ __forceinline__ double dpp_f64_bits(long long bits) { return __longlong_as_double(bits); }
 
-// Inclusive wavefront scan: row_shr 1, 2, 4, 8 within each 16-lane row, then
-// row_bcast15 (lane 15 of rows 0 and 2 into rows 1 and 3) and row_bcast31
-// (lane 31 into rows 2 and 3).
-__device__ __forceinline__ long long wave_inclusive_sum(long long x) {
-  x += dpp64<0x111>(x, 0);
-  x += dpp64<0x112>(x, 0);
-  x += dpp64<0x114>(x, 0);
-  x += dpp64<0x118>(x, 0);
-  x += dpp64<0x142, 0xa>(x, 0);
-  x += dpp64<0x143, 0xc>(x, 0);
-  return x;
-}
-
 // The largest value of the wavefront, in lane 63 (the same steps as the scan).
 __device__ __forceinline__ double wave_max_to_last(double v) {
   long long b = __double_as_longlong(v);

@@ -203,6 +203,16 @@ def test_wide_tree_level_synced(dp, oracle, device):
     assert max(len(t["left"]) for t in o_trees) > 2 ** 12, "tree too small to exercise the path"
 
 
+def test_large_matrix_grouped_partition(dp, oracle, device):
+    """4,300,000 rows: matrices of 4M rows or more take the partition kernels that
+    load four 256-row steps per group (from the column copy of the bins)."""
+    p = {"max_depth": 6, "eta": 0.3}
+    print("[booster] C1 4300000 x 8, depth 6 (grouped partition loads)", flush=True)
+    bst, x, o_trees, o_margin, pos, n = _train_both(dp, oracle, device, 1, 4_300_000, 8, 0, 1, p, 2,
+                                                    20261212)
+    _compare(bst, o_trees, o_margin, pos, n, 1)
+
+
 def test_depth_one_and_single_chunk(dp, oracle, device):
     """Smallest shapes: stumps (max_depth 1) and a matrix of one histogram chunk."""
     for n, depth in [(50, 1), (4000, 3), (5000, 1)]:

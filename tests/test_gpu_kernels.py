@@ -245,18 +245,22 @@ def test_split_evaluation_bit_exact(dp, oracle, ws, device, config, f):
             assert (rec[i]["gl"], rec[i]["hl"]) == (o["gl"], o["hl"])
 
 
-def test_partition_bit_exact(dp, oracle, ws, device):
+# 4,300,000 rows: matrices of 4M rows or more take the partition kernels that
+# load four 256-row steps per group (one step per group below).
+@pytest.mark.parametrize("n,f", [(30000, 200), (4_300_000, 24)])
+def test_partition_bit_exact(dp, oracle, ws, device, n, f):
     import torch
     from dpgbdt import ops
 
-    n, f = 30000, 200
+    print(f"[kernels] partition {n} x {f}", flush=True)
     values, *_ = _synth(ops, 5, n, 23, f)
     lay, bins, o_bins, *_ , mb = _prepare(dp, oracle, ws, values)
     rng = np.random.default_rng(4)
     ridx = rng.permutation(n).astype(np.uint32)
-    segs = [(0, 10000), (10000, 10001), (10001, 25000), (25000, n)]
+    cut = n // 3
+    segs = [(0, cut), (cut, cut + 1), (cut + 1, n - 5000), (n - 5000, n)]
     rec = np.zeros(len(segs), dtype=ops.SPLIT_DTYPE)
-    choices = [(3, 10, 1, 1), (5, 0, 0, 1), (17, 30, 0, 0), (199, 5, 1, 1)]
+    choices = [(3, 10, 1, 1), (5, 0, 0, 1), (17, 30, 0, 0), (f - 1, 5, 1, 1)]
     for i, (feat, b, dl, ex) in enumerate(choices):
         rec[i]["feature"], rec[i]["bin"], rec[i]["default_left"], rec[i]["expand"] = feat, b, dl, ex
         rec[i]["valid"] = 1
