@@ -431,6 +431,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     a.partial_capacity = int32_t(hist_partial_capacity(T));
     a.part_capacity = int32_t(part_work_[nxt].n);
     a.leaf_capacity = int32_t(leaf_work_[cur].n);
+    a.cur_bound = int32_t(std::min<int64_t>(nb, INT32_MAX));
     launch_plan_level(a, nb, s);
     if (d + 1 >= D) {  // no later count launch carries these leaves
       const int32_t leaf_bound = int32_t(plan_leaf_capacity(nb, N, chunk_));

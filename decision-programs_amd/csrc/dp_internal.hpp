@@ -375,6 +375,9 @@ struct PlanArgs {
   double eta, lambda, alpha, mcw;
   int32_t info_capacity, level_capacity;
   int32_t hist_capacity, partial_capacity, part_capacity, leaf_capacity;
+  // Entries of cur, splits and node_left that may be read before the level's
+  // node count is known (the host's bound of this level's size).
+  int32_t cur_bound;
 };
 // level_bound: an upper bound of the level's node count (selects the planner).
 void launch_plan_level(const PlanArgs& a, int64_t level_bound, hipStream_t s);

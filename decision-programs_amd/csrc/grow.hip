@@ -22,6 +22,7 @@
 // (-T(G)/(H + lambda), times eta, rounded to float), compiled with
 // -ffp-contract=off.
 #include "dp_internal.hpp"
+#include "select.hpp"
 
 #include <cmath>
 
@@ -44,33 +45,51 @@ __device__ double plan_weight(const PlanArgs& a, double g, double h) {
   return -plan_threshold_l1(g, a.alpha) / (h + a.lambda);
 }
 
+// ceil(rows / chunk) for 0 <= rows < 2^32 (row ids are 32-bit) and chunk >= 1:
+// a 32-bit division, far shorter than the 64-bit one.
+__device__ __forceinline__ int64_t ceil_rows(int64_t rows, int64_t chunk) {
+  if (chunk >> 32) return rows > 0 ? 1 : 0;
+  const uint32_t r = uint32_t(rows), c = uint32_t(chunk);
+  const uint32_t q = r / c;
+  return int64_t(q) + (r - q * c != 0u ? 1 : 0);
+}
+
+// Exclusive scans of V int64 values per thread over the workgroup (out) and
+// their totals.  Each wavefront scans with DPP lane moves; lane 63 leaves the
+// wavefront's totals in lds; after a barrier every wavefront scans the
+// (kPlanThreads / 64) totals the same way and reads its own prefix and the
+// grand total by readlane.  lds holds at least 16 * V values; two barriers.
+template <int V>
+__device__ void block_scan_n(const int64_t (&v)[V], int64_t (&out)[V], int64_t (&total)[V],
+                             int64_t* lds) {
+  constexpr int W = kPlanThreads / 64;
+  static_assert(W <= 64, "one wavefront scans the wavefront totals");
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  int64_t x[V];
+#pragma unroll
+  for (int k = 0; k < V; ++k) x[k] = wave_inclusive_sum(v[k]);
+  if (lane == 63)
+#pragma unroll
+    for (int k = 0; k < V; ++k) lds[k * W + wave] = x[k];
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    const int64_t w = wave_inclusive_sum(lane < W ? lds[k * W + lane] : 0);
+    out[k] = (wave ? readlane64(w, wave - 1) : 0) + x[k] - v[k];
+    total[k] = readlane64(w, W - 1);
+  }
+  __syncthreads();  // lds is reused by the next scan
+}
+
 // Exclusive scan of one int64 per thread over the workgroup; returns this
-// thread's prefix and writes the total to *total.  Wavefront scans by
-// shuffles, then one wavefront scans the 16 wave totals (three barriers).
+// thread's prefix and writes the total to *total (two barriers).
 __device__ int64_t block_scan(int64_t v, int64_t* lds, int64_t* total) {
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  int64_t x = v;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int64_t y = __shfl_up(x, d, 64);
-    if (lane >= d) x += y;
-  }
-  if (lane == 63) lds[wave] = x;
-  __syncthreads();
-  if (wave == 0) {
-    int64_t w = lane < kPlanThreads / 64 ? lds[lane] : 0;
-#pragma unroll
-    for (int d = 1; d < kPlanThreads / 64; d <<= 1) {
-      const int64_t y = __shfl_up(w, d, 64);
-      if (lane >= d) w += y;
-    }
-    if (lane < kPlanThreads / 64) lds[kPlanThreads / 64 + lane] = w;  // inclusive
-  }
-  __syncthreads();
-  const int64_t before = wave ? lds[kPlanThreads / 64 + wave - 1] : 0;
-  *total = lds[2 * (kPlanThreads / 64) - 1];
-  __syncthreads();
-  return before + x - v;
+  int64_t out[1], tot[1];
+  const int64_t in[1] = {v};
+  block_scan_n<1>(in, out, tot, lds);
+  *total = tot[0];
+  return out[0];
 }
 
 // Index of the segment holding item k: the last i in [0, n) with off[i] <= k
@@ -181,7 +200,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
     if (i < n) {
       const LevelNode nd = a.cur[i];
       if (!node_expands(a, i, nd.end - nd.begin))
-        chunks = (nd.end - nd.begin + a.leaf_chunk - 1) / a.leaf_chunk;
+        chunks = ceil_rows(nd.end - nd.begin, a.leaf_chunk);
     }
     int64_t total;
     const int64_t o = carry + block_scan(chunks, scan, &total);
@@ -236,7 +255,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
       if (j < n_expand) {
         const LevelNode l = a.next[2 * j], r = a.next[2 * j + 1];
         const int64_t rl = l.end - l.begin, rr = r.end - r.begin;
-        nc = ((rr < rl ? rr : rl) + chunk - 1) / chunk;
+        nc = ceil_rows(rr < rl ? rr : rl, chunk);
       }
       int64_t total, ptotal;
       const int64_t o = carry + block_scan(nc, scan, &total);
@@ -303,7 +322,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
       int64_t chunks = 0;
       if (i < n_next) {
         const LevelNode nd = a.next[i];
-        chunks = (nd.end - nd.begin + a.part_chunk - 1) / a.part_chunk;
+        chunks = ceil_rows(nd.end - nd.begin, a.part_chunk);
       }
       int64_t total;
       const int64_t o = carry + block_scan(chunks, scan, &total);
@@ -345,50 +364,6 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
   }
 }
 
-// Exclusive scan of V int64 values per thread over the workgroup (the
-// values of one thread scanned side by side); writes the totals.  lds holds at
-// least 2 * 16 * V values.  Three barriers, whatever V.
-template <int V>
-__device__ void block_scan_n(const int64_t (&v)[V], int64_t (&out)[V], int64_t (&total)[V],
-                             int64_t* lds) {
-  constexpr int W = kPlanThreads / 64;
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  int64_t x[V];
-#pragma unroll
-  for (int k = 0; k < V; ++k) x[k] = v[k];
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-#pragma unroll
-    for (int k = 0; k < V; ++k) {
-      const int64_t y = __shfl_up(x[k], d, 64);
-      if (lane >= d) x[k] += y;
-    }
-  }
-  if (lane == 63)
-#pragma unroll
-    for (int k = 0; k < V; ++k) lds[k * W + wave] = x[k];
-  __syncthreads();
-  if (wave == 0) {
-#pragma unroll
-    for (int k = 0; k < V; ++k) {
-      int64_t w = lane < W ? lds[k * W + lane] : 0;
-#pragma unroll
-      for (int d = 1; d < W; d <<= 1) {
-        const int64_t y = __shfl_up(w, d, 64);
-        if (lane >= d) w += y;
-      }
-      if (lane < W) lds[(V + k) * W + lane] = w;  // inclusive
-    }
-  }
-  __syncthreads();
-#pragma unroll
-  for (int k = 0; k < V; ++k) {
-    out[k] = (wave ? lds[(V + k) * W + wave - 1] : 0) + x[k] - v[k];
-    total[k] = lds[(V + k) * W + W - 1];
-  }
-  __syncthreads();
-}
-
 // The planner for levels of at most kPlanThreads nodes: thread i owns node i
 // for the whole level and keeps the node and its split in registers.  Every
 // per-node count the level's work lists need is known once the split is
@@ -408,6 +383,18 @@ __global__ __launch_bounds__(kPlanThreads) void plan_small_kernel(PlanArgs a) {
   __shared__ float s_val[kPlanThreads];
   __shared__ int32_t s_error;
   const int tid = threadIdx.x;
+  // This thread's node is loaded alongside the counts (the host bound keeps the
+  // index inside the level's buffers; the count decides whether it is used).
+  LevelNode nd_s{};
+  dp_split_record sp_s{};
+  int64_t nl_s = 0;
+  if (tid < a.cur_bound) {
+    nd_s = a.cur[tid];
+    if (a.splits) {
+      sp_s = a.splits[tid];
+      nl_s = a.node_left[tid];
+    }
+  }
   const int32_t n = a.counts->n_level;  // <= kPlanThreads (the host bound)
   const int32_t n_nodes0 = a.counts->n_nodes;
   const double ug = ldexp(1.0, -a.exps[0]), uh = ldexp(1.0, -a.exps[1]);
@@ -429,11 +416,11 @@ __global__ __launch_bounds__(kPlanThreads) void plan_small_kernel(PlanArgs a) {
   int64_t nl = 0;
   bool e = false;
   if (live) {
-    nd = a.cur[tid];
+    nd = nd_s;
     if (a.splits) {
-      sp = a.splits[tid];
+      sp = sp_s;
       if (sp.expand) {
-        nl = a.node_left[tid];
+        nl = nl_s;
         e = nl > 0 && nl < nd.end - nd.begin;
       }
     }
@@ -442,10 +429,10 @@ __global__ __launch_bounds__(kPlanThreads) void plan_small_kernel(PlanArgs a) {
   const int64_t rows = nd.end - nd.begin, lrows = nl, rrows = rows - nl;
   const bool right_small = rrows < lrows;
   int64_t cnt[4] = {e ? 1 : 0,                                                       // expanded
-                    (live && !e) ? (rows + a.leaf_chunk - 1) / a.leaf_chunk : 0,     // leaf chunks
+                    (live && !e) ? ceil_rows(rows, a.leaf_chunk) : 0,                 // leaf chunks
                     (e && next_hist) ? (right_small ? rrows : lrows) : 0,            // smaller child
-                    (e && next_hist) ? (lrows + a.part_chunk - 1) / a.part_chunk +   // partition
-                                           (rrows + a.part_chunk - 1) / a.part_chunk
+                    (e && next_hist) ? ceil_rows(lrows, a.part_chunk) +               // partition
+                                           ceil_rows(rrows, a.part_chunk)
                                      : 0};
   int64_t off[4], tot[4];
   block_scan_n<4>(cnt, off, tot, scan);  // its barriers also publish s_error = 0
@@ -502,7 +489,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_small_kernel(PlanArgs a) {
   // ---- second scan: histogram chunks of the smaller children -----------------
   const int32_t T = a.n_tiles;
   const int64_t chunk = hist_chunk(tot[2], T);
-  const int64_t nc = (cnt[2] + chunk - 1) / chunk;
+  const int64_t nc = ceil_rows(cnt[2], chunk);
   int64_t cnt2[2] = {nc, nc >= 2 ? nc : 0}, off2[2], tot2[2];
   if (live) {
     s_leaf[tid] = off[1];
@@ -591,7 +578,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_small_kernel(PlanArgs a) {
   if (next_hist && n_next > 0) {
     n_part = tot[3];
     if (e) {
-      const int64_t cl = (lrows + a.part_chunk - 1) / a.part_chunk;
+      const int64_t cl = ceil_rows(lrows, a.part_chunk);
       a.part_first[2 * rank] = int32_t(off[3]);
       a.part_first[2 * rank + 1] = int32_t(off[3] + cl);
     }
@@ -602,7 +589,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_small_kernel(PlanArgs a) {
     }
     for (int64_t k = tid; k < n_part; k += kPlanThreads) {
       const int32_t j = owner(s_po, n, k);
-      const int64_t cl = (s_mid[j] - s_begin[j] + a.part_chunk - 1) / a.part_chunk;
+      const int64_t cl = ceil_rows(s_mid[j] - s_begin[j], a.part_chunk);
       int64_t kk = k - s_po[j];
       int32_t node = s_slot[j] & ~1;
       int64_t b, end;
