@@ -269,10 +269,22 @@ void launch_hist_reduce(const int64_t* partial, const HistReduce* jobs, int32_t 
                         int32_t bin_stride, const int64_t* parent_base, int64_t* hist,
                         bool accumulate, hipStream_t s);
 // Minimum rows per histogram chunk and the chunk size for `rows` rows over
-// `n_tiles` tiles (about 1024 work items in all).
+// `n_tiles` tiles: about 1024 work items in all on large levels.  On smaller
+// levels of matrices with at most four tiles, about k * 256 items (k whole
+// items per CU, k = 1..3), so that no CU is left with one more item after the
+// others finish (with more tiles the item count moves in steps of n_tiles, and
+// the rule measured no better).
 constexpr int64_t kHistMinChunk = 4096;
 __host__ __device__ inline int64_t hist_chunk(int64_t rows, int32_t n_tiles) {
-  const int64_t c = (rows * n_tiles + 1023) / 1024;
+  const int64_t units = rows * n_tiles;
+  int64_t c;
+  if (n_tiles <= 4 && units < 1024 * kHistMinChunk) {  // units < 2^22: 32-bit division
+    const uint32_t u = uint32_t(units);
+    const uint32_t k = u < 256u * kHistMinChunk ? 1u : u / uint32_t(256 * kHistMinChunk);
+    c = int64_t((u + 256u * k - 1u) / (256u * k));
+  } else {
+    c = (units + 1023) / 1024;
+  }
   return c < kHistMinChunk ? kHistMinChunk : c;
 }
 // Partial slots needed by one level (chunks of nodes with two or more chunks
