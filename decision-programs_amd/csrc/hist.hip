@@ -377,16 +377,21 @@ __global__ __launch_bounds__(256) void hist_reduce_kernel(
     if (j.nc == 1 && j.p0 < 0) {
       sum = *built;  // written directly by the node's only chunk
     } else {
-      long long acc[4] = {0, 0, 0, 0};
+      long long acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
       const long long* src = partial + (int64_t(j.p0) * n_tiles + t) * n_words + e;
       const int64_t step = int64_t(n_tiles) * n_words;
       int k = 0;
-      for (; k + 4 <= j.nc; k += 4) {
+      for (; k + 8 <= j.nc; k += 8) {  // eight partial slots in flight per thread
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc[u] += src[(k + u) * step];
+      }
+      if (k + 4 <= j.nc) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) acc[u] += src[(k + u) * step];
+        k += 4;
       }
-      for (; k < j.nc; ++k) acc[0] += src[k * step];
-      sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+      for (; k < j.nc; ++k) acc[4] += src[k * step];
+      sum = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
       if (accumulate) sum += *built;
       *built = sum;
     }
