@@ -294,6 +294,26 @@ __global__ __launch_bounds__(kHistThreads) void hist_sparse_kernel(
   }
 }
 
+// Sum of nc partial-slot words src[k * step], k < nc, exact in int64: eight
+// loads in flight per thread (unguarded blocks of eight, then four, then one;
+// measured: per-load guards inside one unrolled loop serialise the loads).
+__device__ __forceinline__ long long sum_slots(const long long* __restrict__ src, int64_t step,
+                                               int32_t nc) {
+  long long acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  int32_t k = 0;
+  for (; k + 8 <= nc; k += 8) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc[u] += src[(k + u) * step];
+  }
+  if (k + 4 <= nc) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[u] += src[(k + u) * step];
+    k += 4;
+  }
+  for (; k < nc; ++k) acc[4] += src[k * step];
+  return ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+}
+
 // Reduce for the present-value path: partial slots hold a sparse tile in the
 // node histogram's layout, so word e of tile t is word t * tile_features *
 // bin_stride * 2 + e of the node histogram.  Otherwise as hist_reduce_kernel.
@@ -318,16 +338,8 @@ __global__ __launch_bounds__(256) void hist_reduce_flat_kernel(
     if (j.nc == 1 && j.p0 < 0) {
       sum = *built;  // written directly by the node's only chunk
     } else {
-      long long acc[4] = {0, 0, 0, 0};
-      const long long* src = partial + (int64_t(j.p0) * n_tiles + t) * slot_words + e;
-      const int64_t step = int64_t(n_tiles) * slot_words;
-      int k = 0;
-      for (; k + 4 <= j.nc; k += 4) {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) acc[u] += src[(k + u) * step];
-      }
-      for (; k < j.nc; ++k) acc[0] += src[k * step];
-      sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+      sum = sum_slots(partial + (int64_t(j.p0) * n_tiles + t) * slot_words + e,
+                      int64_t(n_tiles) * slot_words, j.nc);
       *built = sum;
     }
     if (j.sibling >= 0)
@@ -377,21 +389,8 @@ __global__ __launch_bounds__(256) void hist_reduce_kernel(
     if (j.nc == 1 && j.p0 < 0) {
       sum = *built;  // written directly by the node's only chunk
     } else {
-      long long acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      const long long* src = partial + (int64_t(j.p0) * n_tiles + t) * n_words + e;
-      const int64_t step = int64_t(n_tiles) * n_words;
-      int k = 0;
-      for (; k + 8 <= j.nc; k += 8) {  // eight partial slots in flight per thread
-#pragma unroll
-        for (int u = 0; u < 8; ++u) acc[u] += src[(k + u) * step];
-      }
-      if (k + 4 <= j.nc) {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) acc[u] += src[(k + u) * step];
-        k += 4;
-      }
-      for (; k < j.nc; ++k) acc[4] += src[k * step];
-      sum = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+      sum = sum_slots(partial + (int64_t(j.p0) * n_tiles + t) * n_words + e,
+                      int64_t(n_tiles) * n_words, j.nc);
       if (accumulate) sum += *built;
       *built = sum;
     }

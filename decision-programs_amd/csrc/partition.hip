@@ -176,10 +176,21 @@ __global__ __launch_bounds__(kPartThreads) void part_scatter_kernel(
   // the node's left total and the lefts in its chunks before this one
   const int32_t first = node_first_work[w.node], last = node_first_work[w.node + 1];
   long long before = 0, total = 0;
-  for (int32_t k = first + threadIdx.x; k < last; k += kPartThreads) {
-    const int64_t v = work_left[k];
-    total += v;
-    if (k < item) before += v;
+  for (int32_t k0 = first + threadIdx.x; k0 < last; k0 += 4 * kPartThreads) {
+    int64_t v[4];  // four counts in flight, at indexes clamped below last
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int32_t k = k0 + u * kPartThreads;
+      v[u] = work_left[k < last ? k : last - 1];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int32_t k = k0 + u * kPartThreads;
+      if (k < last) {
+        total += v[u];
+        if (k < item) before += v[u];
+      }
+    }
   }
   before = wave_inclusive_sum(before);
   total = wave_inclusive_sum(total);
