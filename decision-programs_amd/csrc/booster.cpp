@@ -302,7 +302,8 @@ void Grower::prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, b
 }
 
 void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
-                  const int64_t* root_sums, const TrainParam& p, float* margin, int64_t stride,
+                  const int64_t* root_slots, int32_t root_blocks, const TrainParam& p,
+                  float* margin, int64_t stride,
                   int32_t* positions, int32_t slot, hipStream_t s) {
   const dp_bin_layout& L = q.layout;
   const int64_t N = L.n_rows;
@@ -316,9 +317,8 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
   NodeInfo* info = eager_ ? reinterpret_cast<NodeInfo*>(slot_dev + sizeof(PlanCounts)) : info_.p;
   auto* host_counts = reinterpret_cast<PlanCounts*>(level_count_.p);
 
-  launch_iota_u32(ridx_[0].p, N, s);
   launch_plan_root(level_[0].p, sums_[0].p, seg_begin_[0].p, part_work_[0].p, part_first_[0].p,
-                   node_left_[0].p, c, N, root_sums, chunk_, s);
+                   node_left_[0].p, c, N, root_slots, root_blocks, chunk_, ridx_[0].p, s);
   int64_t nb = 1;  // bound of the current level's node count
   int64_t nb_prev = 0;
   for (int32_t d = 0; d <= D; ++d) {
@@ -433,13 +433,29 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     a.leaf_capacity = int32_t(leaf_work_[cur].n);
     a.cur_bound = int32_t(std::min<int64_t>(nb, INT32_MAX));
     launch_plan_level(a, nb, s);
-    if (d + 1 >= D) {  // no later count launch carries these leaves
+    // No later count launch carries the leaves of the last two levels: level
+    // D - 1's are applied with level D's, in one launch after the last planner
+    // (which keeps their count in n_leaf_prev).  A level-synced tree that ends
+    // before level D applies them when it stops, above.
+    if (d == D) {
       const int32_t leaf_bound = int32_t(plan_leaf_capacity(nb, N, chunk_));
+      LeafList prev_leaves;
+      if (D >= 1) {
+        prev_leaves.ridx = ridx_[nxt].p;
+        prev_leaves.work = leaf_work_[nxt].p;
+        prev_leaves.n_host = int32_t(plan_leaf_capacity(nb_prev, N, chunk_));
+        prev_leaves.n_dev = field(c, &PlanCounts::n_leaf_prev);
+      }
       launch_update_margin(ridx_[cur].p, leaf_work_[cur].p, leaf_bound,
-                           field(c, &PlanCounts::n_leaf), margin, stride, s);
-      if (positions)
+                           field(c, &PlanCounts::n_leaf), margin, stride, s,
+                           D >= 1 ? &prev_leaves : nullptr);
+      if (positions) {
+        if (D >= 1)
+          launch_leaf_positions(prev_leaves.ridx, prev_leaves.work, prev_leaves.n_host,
+                                prev_leaves.n_dev, positions, s);
         launch_leaf_positions(ridx_[cur].p, leaf_work_[cur].p, leaf_bound,
                               field(c, &PlanCounts::n_leaf), positions, s);
+      }
     }
     nb_prev = nb;
     nb = split ? std::min(2 * nb, N) : 0;
@@ -693,7 +709,6 @@ void Booster::configure(DMatrix* d) {
   hess_.resize(size_t(N) * n_groups_);
   gpair_.resize(size_t(N) * n_groups_ * 2);
   exps_.resize(size_t(2 * n_groups_));
-  sums_.resize(size_t(2 * n_groups_));
   quant_scratch_.resize(quantise_scratch_bytes(N, n_groups_));
   std::vector<float> init(static_cast<size_t>(n_groups_));
   for (int32_t k = 0; k < n_groups_; ++k) {
@@ -863,7 +878,7 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
       uint64_t(objective_id_), uint64_t(n_groups_), reinterpret_cast<uint64_t>(margin_.p),
       reinterpret_cast<uint64_t>(grad_.p), reinterpret_cast<uint64_t>(hess_.p),
       reinterpret_cast<uint64_t>(gpair_.p), reinterpret_cast<uint64_t>(exps_.p),
-      reinterpret_cast<uint64_t>(sums_.p), reinterpret_cast<uint64_t>(quant_scratch_.p),
+      reinterpret_cast<uint64_t>(quant_scratch_.p),
       reinterpret_cast<uint64_t>(positions), reinterpret_cast<uint64_t>(q.sparse.ptr.p),
       reinterpret_cast<uint64_t>(q.sparse.entries.p), uint64_t(sparse), uint64_t(S)};
   for (int32_t l = 0; l < S; ++l) key.push_back(growers_[size_t(l)]->signature());
@@ -874,12 +889,17 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
     if (with_gradients)
       maxima = launch_gradients(objective_id_, margin_.p, d->labels.p, N, K, grad_.p, hess_.p,
                                 quant_scratch_.p, stream_);
-    launch_quantise(grad_.p, hess_.p, N, K, quant_scratch_.p, maxima, exps_.p, gpair_.p, sums_.p,
+    // The per-workgroup sums stay in the quantiser's slots: each tree's first
+    // launch adds up its output's.
+    launch_quantise(grad_.p, hess_.p, N, K, quant_scratch_.p, maxima, exps_.p, gpair_.p, nullptr,
                     stream_);
+    const int32_t blocks = quantise_blocks(N);
+    const int64_t* slots = quantise_sum_slots(quant_scratch_.p, N, K);
     if (S == 1) {
       for (int32_t k = 0; k < K; ++k)
-        growers_[0]->grow(q, gpair_.p + int64_t(k) * N * 2, exps_.p + 2 * k, sums_.p + 2 * k, tp_,
-                          margin_.p + k, K, positions, k, stream_);
+        growers_[0]->grow(q, gpair_.p + int64_t(k) * N * 2, exps_.p + 2 * k,
+                          slots + int64_t(k) * blocks * 2, blocks, tp_, margin_.p + k, K,
+                          positions, k, stream_);
       return;
     }
     // Each tree writes its own margin column; only the last writes the row
@@ -888,8 +908,8 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
     for (int32_t l = 0; l < S; ++l) DP_HIP(hipStreamWaitEvent(tree_streams_[size_t(l)], fork_, 0));
     for (int32_t k = 0; k < K; ++k)
       growers_[size_t(k % S)]->grow(q, gpair_.p + int64_t(k) * N * 2, exps_.p + 2 * k,
-                                    sums_.p + 2 * k, tp_, margin_.p + k, K,
-                                    k == K - 1 ? positions : nullptr, k / S,
+                                    slots + int64_t(k) * blocks * 2, blocks, tp_, margin_.p + k,
+                                    K, k == K - 1 ? positions : nullptr, k / S,
                                     tree_streams_[size_t(k % S)]);
     for (int32_t l = 0; l < S; ++l) {
       DP_HIP(hipEventRecord(tree_done_[size_t(l)], tree_streams_[size_t(l)]));

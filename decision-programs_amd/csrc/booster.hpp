@@ -80,12 +80,13 @@ class Grower {
   void prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, bool sparse,
                hipStream_t s);
   // Enqueues one tree.  gpair: [n_rows][2] fixed-point gradients of one output;
-  // exps (device): its two quantiser exponents; root_sums (device): the int64
-  // sums of gpair.  Adds the leaf values to margin[r * stride] and, when
+  // exps (device): its two quantiser exponents; root_slots (device): the
+  // quantiser's root_blocks per-workgroup (g, h) sums of gpair, added up by the
+  // tree's first launch.  Adds the leaf values to margin[r * stride] and, when
   // `positions` is set, writes each row's leaf id.
   void grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
-            const int64_t* root_sums, const TrainParam& p, float* margin, int64_t stride,
-            int32_t* positions, int32_t slot, hipStream_t s);
+            const int64_t* root_slots, int32_t root_blocks, const TrainParam& p, float* margin,
+            int64_t stride, int32_t* positions, int32_t slot, hipStream_t s);
   // Copies the node records of slots [0, n_slots) to host buffer `buffer`
   // (0 or 1; one copy; eager trees only, level-synced trees were copied by
   // grow).
@@ -205,7 +206,6 @@ class Booster {
   // training state
   PooledBuffer<float> margin_, grad_, hess_;
   PooledBuffer<int32_t> gpair_, exps_;
-  PooledBuffer<int64_t> sums_;
   PooledBuffer<uint8_t> quant_scratch_;  // quantiser reduction slots
   PooledBuffer<int32_t> positions_;
   mutable std::vector<int32_t> last_exps_;

@@ -188,7 +188,7 @@ struct PlanCounts {
   int32_t n_part;      // partition work items for the current level
   int32_t n_leaf;      // leaf work items produced by the last planner run
   int32_t error;       // nonzero: inconsistent partition counts
-  int32_t pad;
+  int32_t n_leaf_prev; // leaf work items of the planner run before the last
 };
 
 }  // namespace dp
@@ -354,8 +354,19 @@ void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_lay
 constexpr int64_t kPartChunk = 4096;
 constexpr int kPartMasks = 64;  // ballot words per partition work item (kPartChunk / 64)
 
+// A list of leaf chunks over the rows of one row-id buffer; count from n_dev
+// when set, else n_host (an upper bound for grid sizing either way).
+struct LeafList {
+  const uint32_t* ridx = nullptr;
+  const LeafWork* work = nullptr;
+  int32_t n_host = 0;
+  const int32_t* n_dev = nullptr;
+};
+// margin[ridx[i] * stride] += value for the chunks of the list (ridx, work,
+// n_work, n_work_dev) and, in the same launch, of `second` when given.
 void launch_update_margin(const uint32_t* ridx, const LeafWork* work, int32_t n_work,
-                          const int32_t* n_work_dev, float* margin, int64_t stride, hipStream_t s);
+                          const int32_t* n_work_dev, float* margin, int64_t stride, hipStream_t s,
+                          const LeafList* second = nullptr);
 void launch_leaf_positions(const uint32_t* ridx, const LeafWork* work, int32_t n_work,
                            const int32_t* n_work_dev, int32_t* positions, hipStream_t s);
 
@@ -393,13 +404,15 @@ struct PlanArgs {
 };
 // level_bound: an upper bound of the level's node count (selects the planner).
 void launch_plan_level(const PlanArgs& a, int64_t level_bound, hipStream_t s);
-// counts->n_level = 1, n_nodes = 1, ...; cur[0] = root {0, n_rows, g, h, 0, -1}
-// with (g, h) = root_sums[0..1]; sums[0..1] = (g, h), seg_begin[0] = 0,
-// node_left[0] = 0; root partition work over [0, n_rows).
+// ridx[i] = i for i < n_rows; counts->n_level = 1, n_nodes = 1, ...; cur[0] =
+// root {0, n_rows, g, h, 0, -1} with (g, h) the sum of the root_blocks (g, h)
+// pairs of root_slots (the quantiser's per-workgroup sums of this output);
+// sums[0..1] = (g, h), seg_begin[0] = 0, node_left[0] = 0; root partition work
+// over [0, n_rows).
 void launch_plan_root(LevelNode* cur, int64_t* sums, int64_t* seg_begin, PartWork* part_work,
                       int32_t* part_first, int64_t* node_left, PlanCounts* counts,
-                      int64_t n_rows, const int64_t* root_sums, int64_t part_chunk,
-                      hipStream_t s);
+                      int64_t n_rows, const int64_t* root_slots, int32_t root_blocks,
+                      int64_t part_chunk, uint32_t* ridx, hipStream_t s);
 // Upper bounds of the planner's outputs for a level of at most `nodes` nodes.
 inline int64_t plan_hist_capacity(int64_t nodes, int32_t n_tiles) {
   return 1024 + (nodes / 2 + 8) * int64_t(n_tiles);
@@ -438,6 +451,9 @@ bool launch_gradients(int32_t objective, const float* margin, const float* label
 // sums int64 [n_classes][2]; scratch holds quantise_scratch_bytes.
 constexpr int kQuantBlocks = 512;  // workgroups (and reduction slots) per class
 int quantise_blocks(int64_t n_rows);
+// The quantiser's int64 sum slots in its scratch: class k's quantise_blocks
+// (g, h) pairs start at pair k * quantise_blocks(n_rows).
+const int64_t* quantise_sum_slots(const void* scratch, int64_t n_rows, int32_t n_classes);
 size_t quantise_scratch_bytes(int64_t n_rows, int32_t n_classes);
 void launch_quantise(const float* grad, const float* hess, int64_t n_rows, int32_t n_classes,
                      void* scratch, bool maxima_ready, int32_t* exps, int32_t* gpair,

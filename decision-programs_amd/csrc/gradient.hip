@@ -323,9 +323,16 @@ void launch_quantise(const float* grad, const float* hess, int64_t n_rows, int32
                      hess, n_rows, n_classes, max_slots, exps, reinterpret_cast<int2*>(gpair),
                      sum_slots);
   DP_HIP(hipGetLastError());
+  if (!sums) return;  // the caller reduces the sum slots itself
   hipLaunchKernelGGL(finish_sums_kernel, dim3(n_classes), dim3(kQuantThreads), 0, s, sum_slots,
                      blocks, reinterpret_cast<long long*>(sums));
   DP_HIP(hipGetLastError());
+}
+
+const int64_t* quantise_sum_slots(const void* scratch, int64_t n_rows, int32_t n_classes) {
+  const size_t slots = size_t(n_classes) * size_t(quantise_blocks(n_rows));
+  return reinterpret_cast<const int64_t*>(static_cast<const uint8_t*>(scratch) +
+                                          ((slots * 2 * sizeof(uint32_t) + 255) & ~size_t(255)));
 }
 
 }  // namespace dp

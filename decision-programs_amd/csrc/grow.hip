@@ -116,6 +116,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
   __shared__ int32_t s_error;
   const int tid = threadIdx.x;
   const int32_t n = a.counts->n_level;
+  const int32_t n_leaf_old = a.counts->n_leaf;
   const int32_t n_nodes0 = a.counts->n_nodes;
   const double ug = ldexp(1.0, -a.exps[0]), uh = ldexp(1.0, -a.exps[1]);
   if (tid == 0) s_error = 0;
@@ -185,7 +186,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
   if (s_error) {  // inconsistent level or capacity exceeded: stop this tree
     if (tid == 0) {
       PlanCounts* c = a.counts;
-      c->n_level = c->n_hist = c->n_reduce = c->n_part = c->n_leaf = 0;
+      c->n_level = c->n_hist = c->n_reduce = c->n_part = c->n_leaf = c->n_leaf_prev = 0;
       if (!c->error) c->error = s_error;
     }
     return;
@@ -359,6 +360,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
     c->n_hist = int32_t(n_hist);
     c->n_reduce = n_reduce;
     c->n_part = int32_t(n_part);
+    c->n_leaf_prev = n_leaf_old;  // the previous planner's leaves
     c->n_leaf = int32_t(n_leaf);
     if (s_error && !c->error) c->error = s_error;
   }
@@ -396,13 +398,14 @@ __global__ __launch_bounds__(kPlanThreads) void plan_small_kernel(PlanArgs a) {
     }
   }
   const int32_t n = a.counts->n_level;  // <= kPlanThreads (the host bound)
+  const int32_t n_leaf_old = a.counts->n_leaf;
   const int32_t n_nodes0 = a.counts->n_nodes;
   const double ug = ldexp(1.0, -a.exps[0]), uh = ldexp(1.0, -a.exps[1]);
   __syncthreads();  // every thread has read the counts before any is rewritten
   if (n > kPlanThreads) {  // the host chose this kernel on a wrong bound
     if (tid == 0) {
       PlanCounts* c = a.counts;
-      c->n_level = c->n_hist = c->n_reduce = c->n_part = c->n_leaf = 0;
+      c->n_level = c->n_hist = c->n_reduce = c->n_part = c->n_leaf = c->n_leaf_prev = 0;
       if (!c->error) c->error = 6;
     }
     return;
@@ -515,7 +518,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_small_kernel(PlanArgs a) {
   if (s_error) {  // inconsistent level or capacity exceeded: stop this tree
     if (tid == 0) {
       PlanCounts* c = a.counts;
-      c->n_level = c->n_hist = c->n_reduce = c->n_part = c->n_leaf = 0;
+      c->n_level = c->n_hist = c->n_reduce = c->n_part = c->n_leaf = c->n_leaf_prev = 0;
       if (!c->error) c->error = s_error;
     }
     return;
@@ -613,23 +616,42 @@ __global__ __launch_bounds__(kPlanThreads) void plan_small_kernel(PlanArgs a) {
     c->n_hist = int32_t(n_hist);
     c->n_reduce = n_reduce;
     c->n_part = int32_t(n_part);
+    c->n_leaf_prev = n_leaf_old;  // the previous planner's leaves
     c->n_leaf = int32_t(n_leaf);
     if (error && !c->error) c->error = error;
   }
 }
 
-__global__ void plan_root_kernel(LevelNode* cur, int64_t* sums, int64_t* seg_begin,
-                                 PartWork* part_work, int32_t* part_first, int64_t* node_left,
-                                 PlanCounts* counts, int64_t n_rows, const int64_t* root_sums,
-                                 int64_t part_chunk) {
+__global__ __launch_bounds__(256) void plan_root_kernel(
+    LevelNode* cur, int64_t* sums, int64_t* seg_begin, PartWork* part_work, int32_t* part_first,
+    int64_t* node_left, PlanCounts* counts, int64_t n_rows, const int64_t* __restrict__ root_slots,
+    int32_t root_blocks, int64_t part_chunk, uint32_t* __restrict__ ridx) {
+  __shared__ int64_t part[2][4];
   const int64_t chunks = (n_rows + part_chunk - 1) / part_chunk;
-  for (int64_t j = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; j < chunks;
-       j += int64_t(blockDim.x) * gridDim.x) {
+  const int64_t stride = int64_t(blockDim.x) * gridDim.x;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n_rows; i += stride)
+    ridx[i] = uint32_t(i);
+  for (int64_t j = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; j < chunks; j += stride) {
     const int64_t b = j * part_chunk;
     part_work[j] = PartWork{0, 0, b, b + part_chunk < n_rows ? b + part_chunk : n_rows};
   }
-  if (blockIdx.x == 0 && threadIdx.x == 0) {
-    const int64_t g = root_sums[0], h = root_sums[1];
+  if (blockIdx.x != 0) return;  // uniform per workgroup: the barrier below is block 0's alone
+  int64_t g = 0, h = 0;
+  for (int32_t k = threadIdx.x; k < root_blocks; k += blockDim.x) {
+    g += root_slots[2 * k];
+    h += root_slots[2 * k + 1];
+  }
+  g = wave_inclusive_sum(g);
+  h = wave_inclusive_sum(h);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 63) {
+    part[0][wave] = g;
+    part[1][wave] = h;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    g = (part[0][0] + part[0][1]) + (part[0][2] + part[0][3]);
+    h = (part[1][0] + part[1][1]) + (part[1][2] + part[1][3]);
     cur[0] = LevelNode{0, n_rows, g, h, 0, -1};
     sums[0] = g;
     sums[1] = h;
@@ -657,13 +679,13 @@ void launch_plan_level(const PlanArgs& a, int64_t level_bound, hipStream_t s) {
 
 void launch_plan_root(LevelNode* cur, int64_t* sums, int64_t* seg_begin, PartWork* part_work,
                       int32_t* part_first, int64_t* node_left, PlanCounts* counts,
-                      int64_t n_rows, const int64_t* root_sums, int64_t part_chunk,
-                      hipStream_t s) {
+                      int64_t n_rows, const int64_t* root_slots, int32_t root_blocks,
+                      int64_t part_chunk, uint32_t* ridx, hipStream_t s) {
   need(part_chunk >= 1 && part_chunk <= kPartChunk, "partition chunk out of range");
-  const int64_t chunks = (n_rows + part_chunk - 1) / part_chunk;
-  hipLaunchKernelGGL(plan_root_kernel, dim3(grid_for(chunks, 256, 1024)), dim3(256), 0, s, cur,
-                     sums, seg_begin, part_work, part_first, node_left, counts, n_rows, root_sums,
-                     part_chunk);
+  need(root_blocks >= 1, "root sums need at least one slot");
+  hipLaunchKernelGGL(plan_root_kernel, dim3(grid_for(n_rows, 256, 1024)), dim3(256), 0, s, cur,
+                     sums, seg_begin, part_work, part_first, node_left, counts, n_rows, root_slots,
+                     root_blocks, part_chunk, ridx);
   DP_HIP(hipGetLastError());
 }
 

@@ -233,21 +233,25 @@ __global__ __launch_bounds__(kPartThreads) void part_scatter_kernel(
   }
 }
 
-__global__ void update_margin_kernel(const uint32_t* __restrict__ ridx,
-                                     const LeafWork* __restrict__ work, int32_t n_work_host,
-                                     const int32_t* __restrict__ n_work_dev,
-                                     float* __restrict__ margin, int64_t stride) {
-  const int32_t n_work = n_work_dev ? *n_work_dev : n_work_host;
+// Two leaf lists (the second may be empty): items [0, n0) are list 0's,
+// [n0, n0 + n1) list 1's, each list with its own row-id buffer.
+__global__ void update_margin_kernel(LeafList l0, LeafList l1, float* __restrict__ margin,
+                                     int64_t stride) {
+  const int32_t n0 = l0.n_dev ? *l0.n_dev : l0.n_host;
+  const int32_t n1 = l1.work ? (l1.n_dev ? *l1.n_dev : l1.n_host) : 0;
   constexpr int kBatch = 8;  // as apply_leaf: row ids, then margins, then stores
-  for (int32_t item = blockIdx.x; item < n_work; item += gridDim.x) {
-    const LeafWork w = work[item];
+  for (int32_t item = blockIdx.x; item < n0 + n1; item += gridDim.x) {
+    const bool first = item < n0;  // uniform per workgroup
+    const uint32_t* __restrict__ ridx = first ? l0.ridx : l1.ridx;
+    const LeafWork w = first ? l0.work[item] : l1.work[item - n0];
     for (int64_t i0 = w.begin + threadIdx.x; i0 < w.end; i0 += int64_t(kBatch) * blockDim.x) {
       uint32_t row[kBatch];
 #pragma unroll
-      for (int k = 0; k < kBatch; ++k) {
+      for (int k = 0; k < kBatch; ++k) {  // clamped into the chunk: no branch
         const int64_t i = i0 + int64_t(k) * blockDim.x;
         row[k] = ridx[i < w.end ? i : w.end - 1];
       }
+      // A leaf's rows are distinct: all margins are read before any is written.
       float m[kBatch];
 #pragma unroll
       for (int k = 0; k < kBatch; ++k) m[k] = margin[int64_t(row[k]) * stride];
@@ -315,10 +319,13 @@ void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_lay
 
 void launch_update_margin(const uint32_t* ridx, const LeafWork* work, int32_t n_work,
                           const int32_t* n_work_dev, float* margin, int64_t stride,
-                          hipStream_t s) {
-  if (n_work <= 0) return;
-  hipLaunchKernelGGL(update_margin_kernel, dim3(n_work < 2048 ? n_work : 2048), dim3(256), 0, s,
-                     ridx, work, n_work, n_work_dev, margin, stride);
+                          hipStream_t s, const LeafList* second) {
+  const LeafList l1 = second ? *second : LeafList{};
+  const int64_t items = int64_t(n_work) + (l1.work ? l1.n_host : 0);
+  if (items <= 0) return;
+  const LeafList l0{ridx, work, n_work, n_work_dev};
+  hipLaunchKernelGGL(update_margin_kernel, dim3(items < 2048 ? items : 2048), dim3(256), 0, s, l0,
+                     l1, margin, stride);
   DP_HIP(hipGetLastError());
 }
 
