@@ -42,6 +42,10 @@ for sub in ("decision-programs_amd", "oracle"):
 METRIC = "histogram build rows·features/s + % HBM peak; trees/s (1M×28, depth 8)"
 HBM_PEAK_GBS = 8000.0
 SEED = 20261201
+# Idle seconds before each tree leg.  Right after a heavy leg (the C3 passes)
+# the GPU runs C2 about 6 % slower; measured: back to its fresh rate within 4 s.
+# The gap makes every leg start from the same state, whatever ran before it.
+LEG_GAP_S = 5.0
 
 
 def log(msg):
@@ -343,6 +347,7 @@ def main():
     names = [c.strip() for c in args.configs.split(",") if c.strip()]
     if args.mode in ("c2", "trees"):  # boosting rounds only (for kernel-trace profiles)
         for name in (["C2"] if args.mode == "c2" else names):
+            time.sleep(LEG_GAP_S)
             print(json.dumps({name: trees_leg(torch, dp, ops, name)}), flush=True)
         return
     hist, sample, *_ = hist_leg(args, torch, dp, ops)
@@ -358,7 +363,8 @@ def main():
     trees = {}
     if args.mode == "full":
         for name in names:
-            log(f"{name} trees: {TREE_CONFIGS[name]}")
+            log(f"{name} trees: {TREE_CONFIGS[name]} (after {LEG_GAP_S:.0f} s idle)")
+            time.sleep(LEG_GAP_S)
             trees[name] = trees_leg(torch, dp, ops, name,
                                     rows=args.rows if name == "C3" else None)
             log(f"{name}: {trees[name]['value']:.1f} trees/s")
