@@ -181,6 +181,8 @@ def cpu_leg(sample, args):
     # the sample histogram must equal the sum over its rows (exact integers)
     assert int(res[0, :, 0].sum()) == int(qg.astype(np.int64).sum())
     return {"value": rows * f / per_pass, "unit": "rows·features/s", "cores": threads,
+            "affinity_cores": len(os.sched_getaffinity(0)),
+            "hardware_concurrency": os.cpu_count(),
             "kind": "port",
             "sample": f"oracle dpo_hist_parallel root pass over the first {rows} rows x {f} "
                       f"features of the C3 matrix, {reps} passes, {el:.1f} s",
