@@ -87,7 +87,10 @@ def load():
 
 
 def _p(a):
-    return c_void_p(a.ctypes.data) if a is not None else c_void_p(0)
+    # data_as keeps a reference to the array, so a temporary made in the call's
+    # argument list (np.ascontiguousarray of a strided view) lives until the
+    # call returns instead of being freed before the C code reads it.
+    return a.ctypes.data_as(c_void_p) if a is not None else c_void_p(0)
 
 
 def params(eta=0.3, lam=1.0, alpha=0.0, gamma=0.0, min_child_weight=1.0, max_depth=6):

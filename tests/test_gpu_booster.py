@@ -213,6 +213,27 @@ def test_large_matrix_grouped_partition(dp, oracle, device):
     _compare(bst, o_trees, o_margin, pos, n, 1)
 
 
+def test_c2_full_size(dp, oracle, device):
+    """C2 at its benchmark size and parameters (1,000,000 x 28, depth 8, eta 0.1,
+    logistic): two rounds, every tree, the row partition and the margins
+    bit-exact against the oracle."""
+    p = {"max_depth": 8, "eta": 0.1}
+    print("[booster] C2 1000000 x 28, depth 8 (benchmark size)", flush=True)
+    bst, x, o_trees, o_margin, pos, n = _train_both(dp, oracle, device, 2, 1_000_000, 28, 0, 1, p, 2,
+                                                    20261201 + 2)
+    _compare(bst, o_trees, o_margin, pos, n, 1)
+
+
+def test_c4_full_size(dp, oracle, device):
+    """C4 at its benchmark size (60,000 x 784, 10 classes, depth 6, eta 0.3): one
+    round of ten trees, grown concurrently on four streams, against the oracle."""
+    p = {"max_depth": 6, "eta": 0.3}
+    print("[booster] C4 60000 x 784, 10 classes, depth 6 (benchmark size)", flush=True)
+    bst, x, o_trees, o_margin, pos, n = _train_both(dp, oracle, device, 4, 60_000, 784, 1, 10, p, 1,
+                                                    20261201 + 4)
+    _compare(bst, o_trees, o_margin, pos, n, 10)
+
+
 def test_depth_one_and_single_chunk(dp, oracle, device):
     """Smallest shapes: stumps (max_depth 1) and a matrix of one histogram chunk."""
     for n, depth in [(50, 1), (4000, 3), (5000, 1)]:

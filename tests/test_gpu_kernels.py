@@ -146,6 +146,35 @@ def test_root_histogram_bit_exact(dp, oracle, ws, device, config, n, f):
         assert np.all(np.abs(gsum[feat] - exact) <= 1e-5 * np.maximum(mass, 1e-30))
 
 
+def test_c3_root_histogram_full_size(dp, oracle, ws, device):
+    """The benchmark's C3 root pass at its size (10,000,000 x 128, 256 bins): the
+    device bins (whose cuts and binning the tests above pin against the oracle
+    at smaller sizes) are read back and histogrammed by the oracle's parallel
+    histogram; the GPU histogram must equal it bit for bit, and every feature's
+    sums must equal the sums of the quantised gradients (no row lost or counted
+    twice)."""
+    from dpgbdt import ops
+
+    n, f = 10_000_000, 128
+    print(f"[kernels] C3 root histogram {n} x {f}", flush=True)
+    values, _, g, h = _synth(ops, 3, n, 20261201 + 3, f, grad=True)
+    cut_ptr, cuts, _, missing = ops.sketch_cuts(ws, values, 256)
+    assert not missing
+    lay = ops.layout(n, f, 0, -1)
+    bins = ops.bin_values(values, lay, cut_ptr, cuts)
+    del values
+    stride = int(np.diff(cut_ptr).max())
+    (eg, eh), gpair, sums = _gpair(ws, device, g.cpu().numpy(), h.cpu().numpy())
+    hist = ops.hist_build(ws, bins, lay, gpair, [(0, n)], stride).cpu().numpy()[0]
+    qgqh = gpair.cpu().numpy()
+    np.testing.assert_array_equal(hist[:, :, 0].sum(axis=1), np.full(f, sums[0]))
+    np.testing.assert_array_equal(hist[:, :, 1].sum(axis=1), np.full(f, sums[1]))
+    host_bins = ops.from_tiles(bins.cpu().numpy(), lay)
+    del bins
+    ref = oracle.hist_parallel(host_bins, qgqh[:, 0], qgqh[:, 1], bin_stride=stride)
+    np.testing.assert_array_equal(hist, ref)
+
+
 @pytest.mark.parametrize("max_bin", [64, 128])
 def test_sparse_histograms_bit_exact(dp, oracle, ws, device, max_bin):
     """Missing values with at most 128 bins take the compacting kernel (present

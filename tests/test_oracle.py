@@ -331,3 +331,18 @@ def test_booster_reduces_logloss(oracle):
     assert ll < 0.69 * 0.85
     walked = sum(oracle.predict_tree(t, x) for t in trees)
     np.testing.assert_allclose(walked, margin[:, 0], atol=1e-5)
+
+
+def test_strided_arguments_stay_alive(oracle):
+    """Arguments the binding copies to contiguous arrays (strided views) must live
+    through the C call: 2M rows make the copies large enough to be returned to
+    the system as soon as they are freed."""
+    rng = np.random.default_rng(3)
+    n, f = 2_000_000, 4
+    bins = rng.integers(0, 256, (n, f), dtype=np.uint8)
+    q = rng.integers(-2 ** 20, 2 ** 20, (n, 2), dtype=np.int32)
+    strided = oracle.hist_parallel(bins, q[:, 0], q[:, 1], threads=2)
+    ref = oracle.hist(bins, np.ascontiguousarray(q[:, 0]), np.ascontiguousarray(q[:, 1]))
+    np.testing.assert_array_equal(strided, ref)
+    np.testing.assert_array_equal(strided[:, :, 0].sum(axis=1),
+                                  np.full(f, q[:, 0].astype(np.int64).sum()))
