@@ -195,6 +195,121 @@ __global__ __launch_bounds__(64 * kFeatWaves) void evaluate_features_kernel(
   }
 }
 
+// Up to 64 bins: four features per wavefront, one per 16-lane row, four bins
+// per lane (bin 4 * (lane % 16) + j).  The row's prefix scan and argmax take
+// the row_shr steps of the full-wave ones; the row total and the winner's
+// fields come by lane permutes.  Same per-bin arithmetic and tie rule as
+// feature_best, with a quarter of the wavefronts and of their fixed costs.
+// Workgroups loop over (node, group of 16 features) items.
+constexpr int kSegFeatures = 16;  // features per workgroup (four per wavefront)
+
+__device__ __forceinline__ long long row_shuffle64(long long v, int src) {
+  const int lo = __shfl(int(v), src, 64);
+  const int hi = __shfl(int(v >> 32), src, 64);
+  return (long long)((uint64_t(uint32_t(hi)) << 32) | uint32_t(lo));
+}
+
+__global__ __launch_bounds__(256) void evaluate_features_seg_kernel(
+    const long long* __restrict__ hist, int32_t n_nodes_host,
+    const int32_t* __restrict__ n_nodes_dev, int32_t n_features, int32_t bin_stride,
+    const int32_t* __restrict__ n_bins, const long long* __restrict__ node_sums,
+    const int32_t* __restrict__ exps, int32_t exp_g_host, int32_t exp_h_host, Param p,
+    FeatCand* __restrict__ cand) {
+  constexpr int BPL = 4;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int seg = lane >> 4, sub = lane & 15;
+  const int32_t n_nodes = n_nodes_dev ? *n_nodes_dev : n_nodes_host;
+  const int32_t groups = (n_features + kSegFeatures - 1) / kSegFeatures;
+  const int64_t n_items = int64_t(n_nodes) * groups;
+  const int exp_g = exps ? exps[0] : exp_g_host;
+  const int exp_h = exps ? exps[1] : exp_h_host;
+  const double ug = ldexp(1.0, -exp_g), uh = ldexp(1.0, -exp_h);
+  const int row_last = lane | 15;
+  for (int64_t item = blockIdx.x; item < n_items; item += gridDim.x) {
+    const int32_t node = int32_t(item / groups);
+    const int32_t f = int32_t(item % groups) * kSegFeatures + wave * 4 + seg;
+    const bool live = f < n_features;  // every lane takes part in the row steps
+    long long dg[BPL], dh[BPL];
+    const long long* hf = hist + (int64_t(node) * n_features + (live ? f : 0)) * bin_stride * 2;
+#pragma unroll
+    for (int j = 0; j < BPL; ++j) {
+      const int b = sub * BPL + j;
+      dg[j] = live && b < bin_stride ? hf[2 * b] : 0;
+      dh[j] = live && b < bin_stride ? hf[2 * b + 1] : 0;
+    }
+    const int nb = live ? n_bins[f] : 0;
+    const long long gp = node_sums[2 * node], hp = node_sums[2 * node + 1];
+    const double parent_gain = calc_gain(p, double(gp) * ug, double(hp) * uh);
+    long long sg[BPL], sh[BPL];
+    long long rg = 0, rh = 0;
+#pragma unroll
+    for (int j = 0; j < BPL; ++j) {
+      rg += dg[j];
+      rh += dh[j];
+      sg[j] = rg;
+      sh[j] = rh;
+    }
+    // inclusive scan of the lane totals within the 16-lane row
+    long long ig = rg, ih = rh;
+    ig += dpp64<0x111>(ig, 0);
+    ih += dpp64<0x111>(ih, 0);
+    ig += dpp64<0x112>(ig, 0);
+    ih += dpp64<0x112>(ih, 0);
+    ig += dpp64<0x114>(ig, 0);
+    ih += dpp64<0x114>(ih, 0);
+    ig += dpp64<0x118>(ig, 0);
+    ih += dpp64<0x118>(ih, 0);
+    const long long total_g = row_shuffle64(ig, row_last), total_h = row_shuffle64(ih, row_last);
+    const long long og = ig - rg, oh = ih - rh;
+    const long long mg = gp - total_g, mh = hp - total_h;
+
+    Cand c;
+    c.loss = -INFINITY;
+    c.gl = c.hl = 0;
+    c.feature = f;
+    c.bin = -1;
+    c.dl = 0;
+#pragma unroll
+    for (int j = 0; j < BPL; ++j) {
+      const int b = sub * BPL + j;
+      if (b < nb) {
+        const long long lg = og + sg[j], lh = oh + sh[j];
+        const double right_missing = split_loss(p, lg, lh, gp - lg, hp - lh, ug, uh, parent_gain);
+        const double left_missing =
+            (mg == 0 && mh == 0)
+                ? right_missing
+                : split_loss(p, lg + mg, lh + mh, gp - lg - mg, hp - lh - mh, ug, uh, parent_gain);
+        const int dl = left_missing > right_missing;
+        const double loss = dl ? left_missing : right_missing;
+        if (loss > c.loss) {
+          c.loss = loss;
+          c.bin = b;
+          c.dl = dl;
+          c.gl = dl ? lg + mg : lg;
+          c.hl = dl ? lh + mh : lh;
+        }
+      }
+    }
+    // Row argmax: the largest loss, then the lowest lane holding it (lanes hold
+    // increasing bins and each kept its lowest bin on ties).
+    long long bb = __double_as_longlong(c.loss);
+    auto step = [&](long long o) {
+      if (dpp_f64_bits(o) > dpp_f64_bits(bb)) bb = o;
+    };
+    step(dpp64<0x111>(bb, bb));
+    step(dpp64<0x112>(bb, bb));
+    step(dpp64<0x114>(bb, bb));
+    step(dpp64<0x118>(bb, bb));
+    const double best = dpp_f64_bits(row_shuffle64(bb, row_last));
+    const unsigned long long hit = __ballot(c.loss == best);
+    const int winner = seg * 16 + __builtin_ctzll((hit >> (seg * 16)) & 0xffffull);
+    const long long w_gl = row_shuffle64(c.gl, winner), w_hl = row_shuffle64(c.hl, winner);
+    const int w_bin = __shfl(c.bin, winner, 64), w_dl = __shfl(c.dl, winner, 64);
+    if (live && sub == 0)
+      cand[int64_t(node) * n_features + f] = FeatCand{best, w_gl, w_hl, w_bin, w_dl};
+  }
+}
+
 constexpr int kNodeWaves = 16;     // wavefronts per node in evaluate_nodes_kernel
 constexpr int kNodeFeatures = 16;  // feature counts up to this use evaluate_nodes_kernel
 
@@ -296,15 +411,24 @@ bool launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_node
     return true;
   }
   auto* cand = static_cast<FeatCand*>(scratch);
+  if (bin_stride <= 64) {
+    const int64_t items = int64_t(n_nodes) * ((n_features + kSegFeatures - 1) / kSegFeatures);
+    hipLaunchKernelGGL(evaluate_features_seg_kernel, dim3(items < 2048 ? items : 2048), dim3(256),
+                       0, s, h, n_nodes, n_nodes_dev, n_features, bin_stride, n_bins, sums, exps,
+                       exp_g, exp_h, p, cand);
+    DP_HIP(hipGetLastError());
+    if (!select) return false;
+    hipLaunchKernelGGL(select_splits_kernel, dim3(n_nodes < 1024 ? n_nodes : 1024),
+                       dim3(kSelectThreads), 0, s, cand, n_nodes, n_nodes_dev, n_features,
+                       double(param.gamma), out);
+    DP_HIP(hipGetLastError());
+    return true;
+  }
   const int64_t groups = (n_features + kFeatWaves - 1) / kFeatWaves;
   const int64_t items = int64_t(n_nodes) * groups;
   const int grid = int(items < 2048 ? items : 2048);
   const dim3 block(64 * kFeatWaves);
-  if (bin_stride <= 64)
-    hipLaunchKernelGGL(evaluate_features_kernel<1>, dim3(grid), block, 0, s, h, n_nodes,
-                       n_nodes_dev, n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p,
-                       cand);
-  else if (bin_stride <= 128)
+  if (bin_stride <= 128)
     hipLaunchKernelGGL(evaluate_features_kernel<2>, dim3(grid), block, 0, s, h, n_nodes,
                        n_nodes_dev, n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p,
                        cand);

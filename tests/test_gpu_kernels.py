@@ -236,15 +236,18 @@ def test_gathered_histograms_and_subtraction(dp, oracle, ws, device):
     np.testing.assert_array_equal(sib.cpu().numpy(), hn_[4])
 
 
-# 128 features: feature-parallel items, then a select kernel; 8: one workgroup per node
-@pytest.mark.parametrize("config,f", [(3, 128), (1, 8)])
-def test_split_evaluation_bit_exact(dp, oracle, ws, device, config, f):
+# 128 features: feature-parallel items (256 bins: one feature per wavefront),
+# then a select kernel; up to 64 bins: four features per wavefront (40 features:
+# the last group holds unused rows); 8 features: one workgroup per node.
+@pytest.mark.parametrize("config,f,max_bin", [(3, 128, 256), (1, 8, 256), (5, 300, 64),
+                                              (5, 40, 64)])
+def test_split_evaluation_bit_exact(dp, oracle, ws, device, config, f, max_bin):
     import torch
     from dpgbdt import ops
 
     n = 30000
     values, _, g, h = _synth(ops, config, n, 17, f, grad=True)
-    lay, bins, o_bins, cut_ptr, cuts, n_bins, mb = _prepare(dp, oracle, ws, values)
+    lay, bins, o_bins, cut_ptr, cuts, n_bins, mb = _prepare(dp, oracle, ws, values, max_bin)
     stride = int(n_bins.max())
     gn, hn = g.cpu().numpy(), h.cpu().numpy()
     (eg, eh), gpair, sums = _gpair(ws, device, gn, hn)
