@@ -33,8 +33,10 @@ inline void hip_check(hipError_t status, const char* what) {
 // whose last use has completed may be handed back: their owners synchronise
 // their streams first.  A miss that the device cannot serve empties the cache
 // and retries.
-void* device_pool_get(size_t bytes);
-void device_pool_put(void* p, size_t bytes);
+// device_pool_get reports the device the block belongs to (the current one);
+// device_pool_put files the block under that device, whichever is current.
+void* device_pool_get(size_t bytes, int* device);
+void device_pool_put(void* p, size_t bytes, int device);
 void* pinned_pool_get(size_t bytes);
 void pinned_pool_put(void* p, size_t bytes);
 
@@ -43,19 +45,27 @@ template <class T, bool POOLED = false>
 struct DeviceBuffer {
   T* p = nullptr;
   size_t n = 0;
+  int dev = 0;  // POOLED: the device the block belongs to
   DeviceBuffer() = default;
   explicit DeviceBuffer(size_t count) { resize(count); }
   DeviceBuffer(const DeviceBuffer&) = delete;
   DeviceBuffer& operator=(const DeviceBuffer&) = delete;
-  DeviceBuffer(DeviceBuffer&& o) noexcept : p(o.p), n(o.n) { o.p = nullptr; o.n = 0; }
+  DeviceBuffer(DeviceBuffer&& o) noexcept : p(o.p), n(o.n), dev(o.dev) { o.p = nullptr; o.n = 0; }
   DeviceBuffer& operator=(DeviceBuffer&& o) noexcept {
-    if (this != &o) { release(); p = o.p; n = o.n; o.p = nullptr; o.n = 0; }
+    if (this != &o) {
+      release();
+      p = o.p;
+      n = o.n;
+      dev = o.dev;
+      o.p = nullptr;
+      o.n = 0;
+    }
     return *this;
   }
   ~DeviceBuffer() { release(); }
   void release() {
     if (p) {
-      if (POOLED) device_pool_put(p, n * sizeof(T));
+      if (POOLED) device_pool_put(p, n * sizeof(T), dev);
       else (void)hipFree(p);
     }
     p = nullptr;
@@ -64,7 +74,7 @@ struct DeviceBuffer {
   void resize(size_t count) {
     release();
     if (count) {
-      if (POOLED) p = static_cast<T*>(device_pool_get(count * sizeof(T)));
+      if (POOLED) p = static_cast<T*>(device_pool_get(count * sizeof(T), &dev));
       else DP_HIP(hipMalloc(reinterpret_cast<void**>(&p), count * sizeof(T)));
     }
     n = count;

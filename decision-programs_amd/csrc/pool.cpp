@@ -37,13 +37,9 @@ Cache& pinned_cache() {
 
 size_t rounded(size_t bytes) { return (bytes + 255) & ~size_t(255); }
 
-int current_device(bool pinned) {
-  if (pinned) return -1;  // pinned host memory is not tied to a device
+int current_device() {
   int d = 0;
-  if (hipGetDevice(&d) != hipSuccess) {  // never throws: also called from destructors
-    (void)hipGetLastError();
-    d = 0;
-  }
+  DP_HIP(hipGetDevice(&d));
   return d;
 }
 
@@ -89,9 +85,10 @@ void give(Cache& c, int dev, void* p, size_t bytes, bool pinned) {
 
 }  // namespace
 
-void* device_pool_get(size_t bytes) {
+void* device_pool_get(size_t bytes, int* device) {
   bytes = rounded(bytes);
-  const int dev = current_device(false);
+  const int dev = current_device();
+  *device = dev;
   if (void* p = take(device_cache(), dev, bytes)) return p;
   void* p = nullptr;
   if (hipMalloc(&p, bytes) != hipSuccess) {
@@ -102,9 +99,9 @@ void* device_pool_get(size_t bytes) {
   return p;
 }
 
-void device_pool_put(void* p, size_t bytes) {
+void device_pool_put(void* p, size_t bytes, int device) {
   if (!p) return;
-  give(device_cache(), current_device(false), p, rounded(bytes), false);
+  give(device_cache(), device, p, rounded(bytes), false);
 }
 
 void* pinned_pool_get(size_t bytes) {
