@@ -335,7 +335,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
-              "row-sharded design is described in DESIGN.md and not run here.", file=sys.stderr)
+              "row-sharded path is a design that this build does not run.", file=sys.stderr)
         sys.exit(2)
     import torch
 
