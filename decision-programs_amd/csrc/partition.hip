@@ -99,6 +99,17 @@ __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
     continue;
   }
   const PartWork w = item == int32_t(blockIdx.x) ? w_first : work[item];
+  // Row ids of a group; the first group's are loaded before the split is
+  // known, each later group's while the group before it is gathered.
+  uint32_t row[G];
+  auto load_rows = [&](int g0) {
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+      const int64_t i = w.begin + int64_t(g0 + k) * kPartThreads + threadIdx.x;
+      row[k] = i < w.end ? ridx[i] : 0u;
+    }
+  };
+  load_rows(0);
   dp_split_record s;
   if (sel.cand) {  // uniform per launch
     s = select_node<kPartThreads>(sel.cand, w.node, sel.n_features, sel.gamma, wave_best,
@@ -116,18 +127,13 @@ __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
 #pragma unroll 1
   for (int g0 = 0; g0 < kPartSteps; g0 += G) {
     if (w.begin + int64_t(g0) * kPartThreads >= w.end) break;  // uniform per workgroup
-    uint32_t row[G];
-#pragma unroll
-    for (int k = 0; k < G; ++k) {
-      const int64_t i = w.begin + int64_t(g0 + k) * kPartThreads + threadIdx.x;
-      row[k] = i < w.end ? ridx[i] : 0u;
-    }
     int bin[G];
 #pragma unroll
     for (int k = 0; k < G; ++k) {
       const int64_t i = w.begin + int64_t(g0 + k) * kPartThreads + threadIdx.x;
       bin[k] = i < w.end ? split_bin_of<COLS>(bins, n_rows, tile_width, row[k], s.feature) : -1;
     }
+    if (g0 + G < kPartSteps) load_rows(g0 + G);
 #pragma unroll
     for (int k = 0; k < G; ++k) {
       const int b = bin[k];
