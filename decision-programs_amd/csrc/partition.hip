@@ -175,6 +175,18 @@ __global__ __launch_bounds__(kPartThreads) void part_scatter_kernel(
   const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   for (int32_t item = blockIdx.x; item < n_work; item += gridDim.x) {
   const PartWork w = item == int32_t(blockIdx.x) ? w_first : work[item];
+  // Row ids of a group: the first group's are loaded with the item's other
+  // inputs; with G > 1 (large matrices) each later group's while the group
+  // before it is written (measured: no gain with one step per group).
+  uint32_t row[G], nxt[G];
+  auto load_rows = [&](uint32_t (&r)[G], int g0) {
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+      const int64_t i = w.begin + int64_t(g0 + k) * kPartThreads + threadIdx.x;
+      r[k] = i < w.end ? ridx_in[i] : 0u;
+    }
+  };
+  load_rows(row, 0);
   const dp_split_record s = splits[w.node];
   if (!s.expand) continue;
   const unsigned long long my_mask = masks[int64_t(item) * kPartMasks + lane];
@@ -218,12 +230,8 @@ __global__ __launch_bounds__(kPartThreads) void part_scatter_kernel(
 #pragma unroll 1
   for (int g0 = 0; g0 < kPartSteps; g0 += G) {
     if (w.begin + int64_t(g0) * kPartThreads >= w.end) break;  // uniform per workgroup
-    uint32_t row[G];
-#pragma unroll
-    for (int k = 0; k < G; ++k) {
-      const int64_t i = w.begin + int64_t(g0 + k) * kPartThreads + threadIdx.x;
-      row[k] = i < w.end ? ridx_in[i] : 0u;
-    }
+    if (g0 > 0 && G == 1) load_rows(row, g0);
+    if (G > 1 && g0 + G < kPartSteps) load_rows(nxt, g0 + G);
 #pragma unroll
     for (int k = 0; k < G; ++k) {
       const int64_t i = w.begin + int64_t(g0 + k) * kPartThreads + threadIdx.x;
@@ -235,6 +243,9 @@ __global__ __launch_bounds__(kPartThreads) void part_scatter_kernel(
                                                   : begin + n_left + ((i - begin) - prefix);
       if (i < w.end) ridx_out[dst] = row[k];
     }
+    if (G > 1)
+#pragma unroll
+      for (int k = 0; k < G; ++k) row[k] = nxt[k];
   }
   }
 }
