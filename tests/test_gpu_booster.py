@@ -459,3 +459,28 @@ def test_concurrent_class_trees_equal_sequential(dp, device):
             bst.update(dtrain, r)
         models.append(bst.save_raw())
     assert all(m == models[0] for m in models[1:])
+
+
+def test_reused_buffers_give_the_same_model(dp, device):
+    """Training buffers come back from the allocation cache with the contents a
+    previous booster left in them: a booster trained after boosters of other
+    shapes (whose blocks it may reuse) and after one of its own shape must save
+    the same model as the first one trained in a fresh state."""
+    from dpgbdt import ops
+
+    def train(config, n, f, params, rounds):
+        values, labels, _, _ = ops.synth(config, n, 31, n_features=f)
+        dtrain = dp.DMatrix(values, labels)
+        bst = dp.Booster(dict(params, dp_record_positions=1), [dtrain])
+        for r in range(rounds):
+            bst.update(dtrain, r)
+        return bst.save_raw(), bst.last_positions(n)
+
+    logistic = {"objective": "binary:logistic", "max_depth": 6, "eta": 0.3}
+    first, first_pos = train(1, 20_000, 8, logistic, 3)
+    train(5, 30_000, 120, {"objective": "reg:squarederror", "max_depth": 7, "eta": 0.3,
+                           "max_bin": 64}, 2)
+    train(1, 20_000, 8, dict(logistic, max_depth=8), 2)
+    again, again_pos = train(1, 20_000, 8, logistic, 3)
+    assert again == first
+    assert (again_pos == first_pos).all()
