@@ -484,3 +484,37 @@ def test_reused_buffers_give_the_same_model(dp, device):
     again, again_pos = train(1, 20_000, 8, logistic, 3)
     assert again == first
     assert (again_pos == first_pos).all()
+
+
+def test_c5_full_size_layouts_agree(dp, device):
+    """C5 at its benchmark size and parameters (2,000,000 x 1,000, 95 % missing,
+    64 bins, depth 10, squared error), where the CPU oracle would take minutes:
+    two independent histogram paths -- the present-value layout and the dense
+    16-feature tiles -- must give the same model, the same final row partition
+    and the same margins, round after round."""
+    import torch
+    from dpgbdt import ops
+
+    n, f = 2_000_000, 1000
+    print(f"[booster] C5 {n} x {f}, depth 10: present-value vs dense histograms", flush=True)
+    values, labels, _, _ = ops.synth(5, n, 20261201 + 5, n_features=f)
+    dtrain = dp.DMatrix(values, labels)
+    del values
+    out = []
+    for sparse in (1, 0):
+        bst = dp.Booster({"objective": "reg:squarederror", "max_depth": 10, "eta": 0.3,
+                          "max_bin": 64, "dp_sparse_hist": sparse, "dp_record_positions": 1},
+                         [dtrain])
+        positions = []
+        for r in range(2):
+            bst.update(dtrain, r)
+            positions.append(bst.last_positions(n))
+        out.append((bst.save_raw(), positions, bst.margins(n, 1)))
+        del bst
+        torch.cuda.empty_cache()
+    (m1, p1, g1), (m0, p0, g0) = out
+    assert m1 == m0
+    for a, b in zip(p1, p0):
+        np.testing.assert_array_equal(a, b)
+    np.testing.assert_array_equal(np.asarray(g1).view(np.uint32), np.asarray(g0).view(np.uint32))
+    assert len(json.loads(m1)["learner"]["gradient_booster"]["model"]["trees"]) == 2
