@@ -307,6 +307,36 @@ def trees_leg(torch, dp, ops, name, rows=None, warm_rounds=4):
             "gbs": gbs, "pct_hbm_peak": 100.0 * gbs / HBM_PEAK_GBS}
 
 
+def paper_shape_leg(torch, dp, ops):
+    """A synthetic run shaped like the only training timing the reference
+    publishes (docs/paper/decision-programs-paper.tex:1198: a firewall 4-class
+    model, depth 16, 64 rounds, about 52k rows x 2 features, "about 2 seconds").
+    Not comparable (other data and GPU); reported for scale only."""
+    n = 52_000
+    values, _, _, _ = ops.synth(1, n, SEED + 11, n_features=2)
+    labels = ((values[:, 0] * 2).floor() * 2 + (values[:, 1] * 2).floor()).clamp(0, 3)
+    dtrain = dp.DMatrix(values, labels.to(torch.float32).contiguous())
+    params = {"objective": "multi:softmax", "num_class": 4, "max_depth": 16, "eta": 0.3}
+    warm = dp.Booster(params, [dtrain])
+    for r in range(4):
+        warm.update(dtrain, r)
+    del warm
+    time.sleep(LEG_GAP_S)
+    bst = dp.Booster(params, [dtrain])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for r in range(64):
+        bst.update(dtrain, r)
+    assert bst.num_boosted_rounds() == 64
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    nodes = sum(len(bst.tree(t)["left"]) for t in range(bst.num_trees()))
+    return {"workload": "52,000 x 2 synthetic, multi:softmax K=4, depth 16, 64 rounds",
+            "trees": bst.num_trees(), "nodes": nodes, "seconds": el,
+            "trees_per_s": bst.num_trees() / el,
+            "reference_paper": "about 2 s on an RTX A5000 laptop GPU (not comparable)"}
+
+
 def copy_leg(torch, args):
     """Plain device copy of a known size (counter calibration for PMC runs)."""
     nbytes = 1 << 30
@@ -326,7 +356,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--rows", type=int, default=10_000_000)
-    ap.add_argument("--mode", choices=["full", "hist", "copy", "c2", "trees"], default="full")
+    ap.add_argument("--mode", choices=["full", "hist", "copy", "c2", "trees", "paper"],
+                    default="full")
     ap.add_argument("--configs", default="C1,C2,C3,C4,C5",
                     help="tree configurations timed in full/trees mode")
     ap.add_argument("--skip-cpu", action="store_true")
@@ -345,6 +376,9 @@ def main():
     dp.load()
     if args.mode == "copy":
         copy_leg(torch, args)
+        return
+    if args.mode == "paper":
+        print(json.dumps(paper_shape_leg(torch, dp, ops)), flush=True)
         return
     names = [c.strip() for c in args.configs.split(",") if c.strip()]
     if args.mode in ("c2", "trees"):  # boosting rounds only (for kernel-trace profiles)
