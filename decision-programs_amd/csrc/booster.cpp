@@ -346,6 +346,10 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
       }
     }
     const bool split = d < D;
+    // A split level of at most 1024 nodes runs its planner and its partition
+    // scatter in one launch.
+    const bool merged = split && nb <= 1024;
+    ScatterArgs scatter{};
     int64_t* h = hist_[cur].p;
     if (split) {
       const int32_t tf = q.sparse.tile_features;
@@ -392,11 +396,11 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
         prev.positions = positions;
       }
       launch_partition(q.bins.p, q.cols.p, L, ridx_[cur].p, ridx_[nxt].p, part_work_[cur].p,
-                       int32_t(plan_part_capacity(nb, N, chunk_)), field(c, &PlanCounts::n_part),
+                       int32_t(plan_part_capacity(nb, N, chunk_)), &c->n_part[d & 1],
                        seg_begin_[cur].p, splits_.p, part_first_[cur].p, int32_t(nb),
                        field(c, &PlanCounts::n_level), work_left_.p, part_masks_.p,
                        node_left_[cur].p, true, s, d > 0 ? &prev : nullptr,
-                       records ? nullptr : &sel);
+                       records ? nullptr : &sel, merged ? &scatter : nullptr);
     }
     PlanArgs a{};
     a.cur = level_[cur].p;
@@ -432,7 +436,13 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     a.part_capacity = int32_t(part_work_[nxt].n);
     a.leaf_capacity = int32_t(leaf_work_[cur].n);
     a.cur_bound = int32_t(std::min<int64_t>(nb, INT32_MAX));
-    launch_plan_level(a, nb, s);
+    if (merged) {
+      a.work_left = work_left_.p;
+      a.cur_part_work = part_work_[cur].p;
+      launch_plan_scatter(a, scatter, N, s);
+    } else {
+      launch_plan_level(a, nb, s);
+    }
     // No later count launch carries the leaves of the last two levels: level
     // D - 1's are applied with level D's, in one launch after the last planner
     // (which keeps their count in n_leaf_prev).  A level-synced tree that ends

@@ -195,10 +195,14 @@ struct PlanCounts {
   int32_t n_nodes;     // nodes allocated in the tree so far
   int32_t n_hist;      // histogram work items for the current level
   int32_t n_reduce;    // histogram reduce jobs for the current level
-  int32_t n_part;      // partition work items for the current level
   int32_t n_leaf;      // leaf work items produced by the last planner run
   int32_t error;       // nonzero: inconsistent partition counts
   int32_t n_leaf_prev; // leaf work items of the planner run before the last
+  int32_t pad;
+  // Partition work items of the level of depth d in n_part[d & 1]: the planner
+  // of level d writes level d + 1's while that level's scatter, in the same
+  // launch, still reads level d's.
+  int32_t n_part[2];
 };
 
 }  // namespace dp
@@ -339,13 +343,30 @@ struct LeafPass {
   int32_t* positions = nullptr;
 };
 
+// The partition scatter's arguments (scatter.hpp).
+struct ScatterArgs {
+  const uint32_t* ridx_in;
+  uint32_t* ridx_out;
+  const PartWork* work;
+  int32_t n_work_host;       // bound of the item count (grid sizing, first-item prefetch)
+  const int32_t* n_work_dev; // the item count; n_work_host when null
+  const dp_split_record* splits;
+  const int64_t* seg_begin;
+  const int32_t* node_first_work;
+  const int64_t* work_left;
+  const unsigned long long* masks;
+  int64_t* node_left;        // the node's first item writes the node's left total; may be null
+};
+
 // Partition: counts, then scatter (which writes the left totals of the
 // expanding nodes into node_left).  cols: column-major copy of the bins
 // (launch_tiles_to_columns) or null to read the tiles.  work_left: one word
 // per work item; masks: kPartMasks words per work item (the count kernel's
 // ballots, read back by the scatter).  node_left_zeroed: the caller has zeroed
 // node_left[0, nodes) (non-expanding nodes keep 0); else it is cleared here
-// for n_nodes nodes.
+// for n_nodes nodes.  deferred: when given, the scatter is not launched; its
+// arguments are written there (n_work_host = 0: nothing to scatter) for
+// launch_plan_scatter.
 // Per-feature candidates left by launch_evaluate(..., select = false): the
 // partition count selects each node's split from them and writes the records.
 struct SplitSelect {
@@ -360,7 +381,7 @@ void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_lay
                       int32_t n_nodes, const int32_t* n_nodes_dev, int64_t* work_left,
                       unsigned long long* masks, int64_t* node_left, bool node_left_zeroed,
                       hipStream_t s, const LeafPass* leaves = nullptr,
-                      const SplitSelect* select = nullptr);
+                      const SplitSelect* select = nullptr, ScatterArgs* deferred = nullptr);
 constexpr int64_t kPartChunk = 4096;
 constexpr int kPartMasks = 64;  // ballot words per partition work item (kPartChunk / 64)
 
@@ -411,9 +432,18 @@ struct PlanArgs {
   // Entries of cur, splits and node_left that may be read before the level's
   // node count is known (the host's bound of this level's size).
   int32_t cur_bound;
+  // Set (with cur_part_work, this level's partition items): left rows are
+  // summed from the partition count's per-item counts instead of node_left.
+  const int64_t* work_left;
+  const PartWork* cur_part_work;
 };
 // level_bound: an upper bound of the level's node count (selects the planner).
 void launch_plan_level(const PlanArgs& a, int64_t level_bound, hipStream_t s);
+// The planner of a level of at most 1024 nodes (a.work_left set) and the
+// level's partition scatter (the arguments launch_partition deferred) in one
+// launch.
+void launch_plan_scatter(const PlanArgs& a, const ScatterArgs& sa, int64_t n_rows,
+                         hipStream_t s);
 // ridx[i] = i for i < n_rows; counts->n_level = 1, n_nodes = 1, ...; cur[0] =
 // root {0, n_rows, g, h, 0, -1} with (g, h) the sum of the root_blocks (g, h)
 // pairs of root_slots (the quantiser's per-workgroup sums of this output);

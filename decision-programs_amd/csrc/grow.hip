@@ -22,6 +22,7 @@
 // (-T(G)/(H + lambda), times eta, rounded to float), compiled with
 // -ffp-contract=off.
 #include "dp_internal.hpp"
+#include "scatter.hpp"
 #include "select.hpp"
 
 #include <cmath>
@@ -186,7 +187,8 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
   if (s_error) {  // inconsistent level or capacity exceeded: stop this tree
     if (tid == 0) {
       PlanCounts* c = a.counts;
-      c->n_level = c->n_hist = c->n_reduce = c->n_part = c->n_leaf = c->n_leaf_prev = 0;
+      c->n_level = c->n_hist = c->n_reduce = c->n_leaf = c->n_leaf_prev = 0;
+      c->n_part[(a.depth + 1) & 1] = 0;
       if (!c->error) c->error = s_error;
     }
     return;
@@ -359,7 +361,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
     c->n_nodes = n_nodes0 + n_next;
     c->n_hist = int32_t(n_hist);
     c->n_reduce = n_reduce;
-    c->n_part = int32_t(n_part);
+    c->n_part[(a.depth + 1) & 1] = int32_t(n_part);
     c->n_leaf_prev = n_leaf_old;  // the previous planner's leaves
     c->n_leaf = int32_t(n_leaf);
     if (s_error && !c->error) c->error = s_error;
@@ -372,9 +374,12 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
 // read, so two multi-value scans give all offsets (the second depends on the
 // histogram chunk, which depends on the first's totals); the offsets and
 // segments then sit in LDS, read-only, for the item loops.  Its work lists
-// are identical to plan_level_kernel's.
-__global__ __launch_bounds__(kPlanThreads) void plan_small_kernel(PlanArgs a) {
+// are identical to plan_level_kernel's.  With a.work_left set it sums each
+// node's left rows from the partition count's per-item counts itself, so it
+// can run beside the level's scatter (which publishes them in node_left).
+__device__ void plan_small_level(const PlanArgs& a) {
   __shared__ int64_t scan[2 * (kPlanThreads / 64) * 4];
+  __shared__ int64_t s_left[kPlanThreads];      // left rows per node (a.work_left set)
   __shared__ int64_t s_leaf[kPlanThreads + 1];  // first leaf chunk per node
   __shared__ int64_t s_cs[kPlanThreads + 1];    // first histogram chunk per node
   __shared__ int64_t s_ps[kPlanThreads];        // first partial chunk per node
@@ -390,22 +395,45 @@ __global__ __launch_bounds__(kPlanThreads) void plan_small_kernel(PlanArgs a) {
   LevelNode nd_s{};
   dp_split_record sp_s{};
   int64_t nl_s = 0;
+  const bool sum_left = a.splits && a.work_left;
   if (tid < a.cur_bound) {
     nd_s = a.cur[tid];
     if (a.splits) {
       sp_s = a.splits[tid];
-      nl_s = a.node_left[tid];
+      if (!sum_left) nl_s = a.node_left[tid];
     }
   }
   const int32_t n = a.counts->n_level;  // <= kPlanThreads (the host bound)
   const int32_t n_leaf_old = a.counts->n_leaf;
   const int32_t n_nodes0 = a.counts->n_nodes;
+  const int32_t n_items = sum_left ? a.counts->n_part[a.depth & 1] : 0;
   const double ug = ldexp(1.0, -a.exps[0]), uh = ldexp(1.0, -a.exps[1]);
+  if (sum_left) s_left[tid] = 0;
   __syncthreads();  // every thread has read the counts before any is rewritten
+  if (sum_left) {  // item k's count goes to its node (four items in flight per thread)
+    for (int32_t k0 = tid; k0 < n_items; k0 += 4 * kPlanThreads) {
+      uint32_t node[4];
+      int64_t v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int32_t k = k0 + u * kPlanThreads < n_items ? k0 + u * kPlanThreads : n_items - 1;
+        node[u] = uint32_t(a.cur_part_work[k].node);
+        v[u] = a.work_left[k];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (k0 + u * kPlanThreads < n_items && node[u] < uint32_t(kPlanThreads))
+          atomicAdd(reinterpret_cast<unsigned long long*>(&s_left[node[u]]),
+                    static_cast<unsigned long long>(v[u]));
+    }
+    __syncthreads();
+    nl_s = s_left[tid];
+  }
   if (n > kPlanThreads) {  // the host chose this kernel on a wrong bound
     if (tid == 0) {
       PlanCounts* c = a.counts;
-      c->n_level = c->n_hist = c->n_reduce = c->n_part = c->n_leaf = c->n_leaf_prev = 0;
+      c->n_level = c->n_hist = c->n_reduce = c->n_leaf = c->n_leaf_prev = 0;
+      c->n_part[(a.depth + 1) & 1] = 0;
       if (!c->error) c->error = 6;
     }
     return;
@@ -518,7 +546,8 @@ __global__ __launch_bounds__(kPlanThreads) void plan_small_kernel(PlanArgs a) {
   if (s_error) {  // inconsistent level or capacity exceeded: stop this tree
     if (tid == 0) {
       PlanCounts* c = a.counts;
-      c->n_level = c->n_hist = c->n_reduce = c->n_part = c->n_leaf = c->n_leaf_prev = 0;
+      c->n_level = c->n_hist = c->n_reduce = c->n_leaf = c->n_leaf_prev = 0;
+      c->n_part[(a.depth + 1) & 1] = 0;
       if (!c->error) c->error = s_error;
     }
     return;
@@ -615,11 +644,29 @@ __global__ __launch_bounds__(kPlanThreads) void plan_small_kernel(PlanArgs a) {
     c->n_nodes = n_nodes0 + n_next;
     c->n_hist = int32_t(n_hist);
     c->n_reduce = n_reduce;
-    c->n_part = int32_t(n_part);
+    c->n_part[(a.depth + 1) & 1] = int32_t(n_part);
     c->n_leaf_prev = n_leaf_old;  // the previous planner's leaves
     c->n_leaf = int32_t(n_leaf);
     if (error && !c->error) c->error = error;
   }
+}
+
+__global__ __launch_bounds__(kPlanThreads) void plan_small_kernel(PlanArgs a) {
+  plan_small_level(a);
+}
+
+// A level's planner (workgroup 0) and its scatter (the other workgroups, four
+// items at a time) in one launch: both read only what the partition count
+// left, and write disjoint buffers (the planner writes the next level's, and
+// the next level's partition count in counts->n_part).
+template <int G>
+__global__ __launch_bounds__(kPlanThreads) void plan_scatter_kernel(PlanArgs a, ScatterArgs sa) {
+  if (blockIdx.x == 0) {
+    plan_small_level(a);
+    return;
+  }
+  scatter_items<G, kPlanThreads / kPartThreads>(sa, int32_t(blockIdx.x) - 1,
+                                                  int32_t(gridDim.x) - 1);
 }
 
 __global__ __launch_bounds__(256) void plan_root_kernel(
@@ -662,7 +709,7 @@ __global__ __launch_bounds__(256) void plan_root_kernel(
     PlanCounts c{};
     c.n_level = 1;
     c.n_nodes = 1;
-    c.n_part = int32_t(chunks);
+    c.n_part[0] = int32_t(chunks);
     *counts = c;
   }
 }
@@ -674,6 +721,19 @@ void launch_plan_level(const PlanArgs& a, int64_t level_bound, hipStream_t s) {
     hipLaunchKernelGGL(plan_small_kernel, dim3(1), dim3(kPlanThreads), 0, s, a);
   else
     hipLaunchKernelGGL(plan_level_kernel, dim3(1), dim3(kPlanThreads), 0, s, a);
+  DP_HIP(hipGetLastError());
+}
+
+void launch_plan_scatter(const PlanArgs& a, const ScatterArgs& sa, int64_t n_rows,
+                         hipStream_t s) {
+  need(a.work_left && a.cur_part_work && a.splits, "the merged planner sums the left counts");
+  need(a.cur_bound <= kPlanThreads, "the merged planner takes levels of at most 1024 nodes");
+  const int32_t items = sa.n_work_host < 2048 ? sa.n_work_host : 2048;
+  constexpr int Q = kPlanThreads / kPartThreads;
+  const int blocks = 1 + (items + Q - 1) / Q;
+  // Four steps per load group on matrices of 4M rows or more, as the partition.
+  auto k = n_rows >= (int64_t(1) << 22) ? plan_scatter_kernel<4> : plan_scatter_kernel<1>;
+  hipLaunchKernelGGL(k, dim3(blocks), dim3(kPlanThreads), 0, s, a, sa);
   DP_HIP(hipGetLastError());
 }
 

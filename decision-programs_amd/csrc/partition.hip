@@ -8,24 +8,23 @@
 //      rows with wavefront ballots and keeps the ballots (one 64-bit mask per
 //      wavefront and 256-row step, 64 per chunk), so the split feature's bins
 //      are gathered once per level;
-//   2. scatter: each chunk sums the counts of its node's chunks (the node's
-//      left total, and its own exclusive offset from the earlier ones; the
-//      node's first chunk publishes the total in node_left), ranks its rows in
-//      position order (an exclusive scan of the chunk's 64 ballot counts, one
-//      per lane, plus the lane's prefix in its ballot) and writes
+//   2. scatter (scatter.hpp): each chunk sums the counts of its node's chunks
+//      (the node's left total, and its own exclusive offset from the earlier
+//      ones; the node's first chunk publishes the total in node_left), ranks
+//      its rows in position order (an exclusive scan of the chunk's 64 ballot
+//      counts, one per lane, plus the lane's prefix in its ballot) and writes
 //      lefts to [begin + left rank) and rights to [begin + n_left + right rank)
-//      of ridx_out.  No atomics: a node can have thousands of chunks.
+//      of ridx_out.  No atomics: a node can have thousands of chunks.  A caller
+//      may take the scatter's arguments instead and launch it beside the level
+//      planner (grow.hip).
 // The row goes left iff its bin of the split feature is <= the split bin, or it
 // is missing and the split's default is left.
 #include "dp_internal.hpp"
+#include "scatter.hpp"
 #include "select.hpp"
 
 namespace dp {
 namespace {
-
-constexpr int kPartThreads = 256;
-constexpr int kPartSteps = int(kPartChunk / kPartThreads);  // 16 rows per lane
-static_assert(kPartSteps * (kPartThreads / 64) == kPartMasks, "one mask per wave and step");
 
 // The split feature's bin of `row`: from the column-major copy when there is
 // one (one byte per row, contiguous within a feature), else from the tiles.
@@ -37,8 +36,6 @@ __device__ __forceinline__ int split_bin_of(const uint8_t* __restrict__ bins, in
   const int within = feature - int(tile) * tile_width;
   return bins[tile * n_rows * tile_width + int64_t(row) * tile_width + within];
 }
-
-__device__ __forceinline__ int popc64(unsigned long long m) { return __popcll(m); }
 
 // The margin (and leaf id) update of one leaf chunk (taken by value: the
 // margin stores cannot alias it).  Row ids are loaded a batch ahead of their
@@ -154,100 +151,9 @@ __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
   }
 }
 
-// Lane l of every wavefront holds ballot l of the item (step l / 4, wavefront
-// l % 4), which is also position order; an exclusive scan of their counts
-// gives each (step, wavefront) its lefts before it in the item, so the steps
-// need no barrier.  The item's barriers share the node-level sums.
 template <int G>
-__global__ __launch_bounds__(kPartThreads) void part_scatter_kernel(
-    const uint32_t* __restrict__ ridx_in, uint32_t* __restrict__ ridx_out,
-    const PartWork* __restrict__ work, int32_t n_work_host,
-    const int32_t* __restrict__ n_work_dev, const dp_split_record* __restrict__ splits,
-    const int64_t* __restrict__ seg_begin, const int32_t* __restrict__ node_first_work,
-    const int64_t* __restrict__ work_left, const unsigned long long* __restrict__ masks,
-    int64_t* __restrict__ node_left) {
-  __shared__ int64_t wave_sum[2][kPartThreads / 64];
-  const PartWork w_first =
-      int32_t(blockIdx.x) < n_work_host ? work[blockIdx.x] : PartWork{0, 0, 0, 0};
-  const int32_t n_work = n_work_dev ? *n_work_dev : n_work_host;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
-  const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int32_t item = blockIdx.x; item < n_work; item += gridDim.x) {
-  const PartWork w = item == int32_t(blockIdx.x) ? w_first : work[item];
-  // Row ids of a group: the first group's are loaded with the item's other
-  // inputs; with G > 1 (large matrices) each later group's while the group
-  // before it is written (measured: no gain with one step per group).
-  uint32_t row[G], nxt[G];
-  auto load_rows = [&](uint32_t (&r)[G], int g0) {
-#pragma unroll
-    for (int k = 0; k < G; ++k) {
-      const int64_t i = w.begin + int64_t(g0 + k) * kPartThreads + threadIdx.x;
-      r[k] = i < w.end ? ridx_in[i] : 0u;
-    }
-  };
-  load_rows(row, 0);
-  const dp_split_record s = splits[w.node];
-  if (!s.expand) continue;
-  const unsigned long long my_mask = masks[int64_t(item) * kPartMasks + lane];
-  const int64_t begin = seg_begin[w.node];
-  // the node's left total and the lefts in its chunks before this one
-  const int32_t first = node_first_work[w.node], last = node_first_work[w.node + 1];
-  long long before = 0, total = 0;
-  for (int32_t k0 = first + threadIdx.x; k0 < last; k0 += 4 * kPartThreads) {
-    int64_t v[4];  // four counts in flight, at indexes clamped below last
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int32_t k = k0 + u * kPartThreads;
-      v[u] = work_left[k < last ? k : last - 1];
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int32_t k = k0 + u * kPartThreads;
-      if (k < last) {
-        total += v[u];
-        if (k < item) before += v[u];
-      }
-    }
-  }
-  before = wave_inclusive_sum(before);
-  total = wave_inclusive_sum(total);
-  if (lane == 63) {
-    wave_sum[0][wave] = before;
-    wave_sum[1][wave] = total;
-  }
-  // lefts before each ballot of the item, in position order
-  const long long c = popc64(my_mask);
-  const int excl = int(wave_inclusive_sum(c) - c);
-  __syncthreads();
-  int64_t lefts_before = 0, n_left = 0;  // lefts before this item; node total
-  for (int k = 0; k < kPartThreads / 64; ++k) {
-    lefts_before += wave_sum[0][k];
-    n_left += wave_sum[1][k];
-  }
-  __syncthreads();  // wave_sum is rewritten by the next item
-  if (item == first && threadIdx.x == 0) node_left[w.node] = n_left;
-#pragma unroll 1
-  for (int g0 = 0; g0 < kPartSteps; g0 += G) {
-    if (w.begin + int64_t(g0) * kPartThreads >= w.end) break;  // uniform per workgroup
-    if (g0 > 0 && G == 1) load_rows(row, g0);
-    if (G > 1 && g0 + G < kPartSteps) load_rows(nxt, g0 + G);
-#pragma unroll
-    for (int k = 0; k < G; ++k) {
-      const int64_t i = w.begin + int64_t(g0 + k) * kPartThreads + threadIdx.x;
-      const int idx = (g0 + k) * (kPartThreads / 64) + wave;
-      const unsigned long long mask = (unsigned long long)readlane64((long long)my_mask, idx);
-      const int64_t prefix =
-          lefts_before + __builtin_amdgcn_readlane(excl, idx) + popc64(mask & below);
-      const int64_t dst = ((mask >> lane) & 1ull) ? begin + prefix
-                                                  : begin + n_left + ((i - begin) - prefix);
-      if (i < w.end) ridx_out[dst] = row[k];
-    }
-    if (G > 1)
-#pragma unroll
-      for (int k = 0; k < G; ++k) row[k] = nxt[k];
-  }
-  }
+__global__ __launch_bounds__(kPartThreads) void part_scatter_kernel(ScatterArgs a) {
+  scatter_items<G, 1>(a, int32_t(blockIdx.x), int32_t(gridDim.x));
 }
 
 // Two leaf lists (the second may be empty): items [0, n0) are list 0's,
@@ -307,7 +213,9 @@ void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_lay
                       dp_split_record* splits, const int32_t* node_first_work,
                       int32_t n_nodes, const int32_t* n_nodes_dev, int64_t* work_left,
                       unsigned long long* masks, int64_t* node_left, bool node_left_zeroed,
-                      hipStream_t s, const LeafPass* leaves, const SplitSelect* select) {
+                      hipStream_t s, const LeafPass* leaves, const SplitSelect* select,
+                      ScatterArgs* deferred) {
+  if (deferred) *deferred = ScatterArgs{};  // nothing to scatter unless filled below
   if (n_nodes <= 0) return;
   (void)n_nodes_dev;
   const int missing = layout.missing_bin;
@@ -327,10 +235,15 @@ void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_lay
                      layout.tile_width, missing, ridx_in, work, n_work, n_work_dev, splits, sel,
                      node_first_work, work_left, masks, lp);
   DP_HIP(hipGetLastError());
+  const ScatterArgs sa{ridx_in, ridx_out,   work,      n_work, n_work_dev, splits,
+                       seg_begin, node_first_work, work_left, masks, node_left};
+  if (deferred) {
+    *deferred = sa;
+    return;
+  }
   if (n_work <= 0) return;
   hipLaunchKernelGGL(wide ? part_scatter_kernel<4> : part_scatter_kernel<1>, dim3(gw),
-                     dim3(kPartThreads), 0, s, ridx_in, ridx_out, work, n_work, n_work_dev,
-                     splits, seg_begin, node_first_work, work_left, masks, node_left);
+                     dim3(kPartThreads), 0, s, sa);
   DP_HIP(hipGetLastError());
 }
 
