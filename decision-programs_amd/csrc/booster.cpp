@@ -438,7 +438,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     a.cur_bound = int32_t(std::min<int64_t>(nb, INT32_MAX));
     if (merged) {
       a.work_left = work_left_.p;
-      a.cur_part_work = part_work_[cur].p;
+      a.part_bound = int32_t(plan_part_capacity(nb, N, chunk_));
       launch_plan_scatter(a, scatter, N, s);
     } else {
       launch_plan_level(a, nb, s);

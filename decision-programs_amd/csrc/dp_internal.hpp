@@ -361,7 +361,8 @@ struct ScatterArgs {
 // Partition: counts, then scatter (which writes the left totals of the
 // expanding nodes into node_left).  cols: column-major copy of the bins
 // (launch_tiles_to_columns) or null to read the tiles.  work_left: one word
-// per work item; masks: kPartMasks words per work item (the count kernel's
+// per work item, the item's node in the upper 32 bits and its left rows in the
+// lower 32 (zero for a node that does not expand); masks: kPartMasks words per work item (the count kernel's
 // ballots, read back by the scatter).  node_left_zeroed: the caller has zeroed
 // node_left[0, nodes) (non-expanding nodes keep 0); else it is cleared here
 // for n_nodes nodes.  deferred: when given, the scatter is not launched; its
@@ -432,10 +433,10 @@ struct PlanArgs {
   // Entries of cur, splits and node_left that may be read before the level's
   // node count is known (the host's bound of this level's size).
   int32_t cur_bound;
-  // Set (with cur_part_work, this level's partition items): left rows are
-  // summed from the partition count's per-item counts instead of node_left.
+  // Set: left rows are summed from the partition count's per-item words (node
+  // << 32 | left rows) instead of read from node_left.
   const int64_t* work_left;
-  const PartWork* cur_part_work;
+  int32_t part_bound;  // host bound of this level's partition items (sizes work_left)
 };
 // level_bound: an upper bound of the level's node count (selects the planner).
 void launch_plan_level(const PlanArgs& a, int64_t level_bound, hipStream_t s);

@@ -396,6 +396,21 @@ __device__ void plan_small_level(const PlanArgs& a) {
   dp_split_record sp_s{};
   int64_t nl_s = 0;
   const bool sum_left = a.splits && a.work_left;
+  // This level's partition item words (node << 32 | left rows), kSumBatch per
+  // thread at a time; the first batch is loaded with the counts (the host
+  // bound keeps the indexes in the buffer, the device count decides which are
+  // used).
+  constexpr int kSumBatch = 4;
+  int64_t item_word[kSumBatch];
+  auto load_items = [&](int32_t k0) {
+#pragma unroll
+    for (int u = 0; u < kSumBatch; ++u) {
+      const int32_t k = k0 + u * kPlanThreads < a.part_bound ? k0 + u * kPlanThreads
+                                                               : a.part_bound - 1;
+      item_word[u] = a.work_left[k];
+    }
+  };
+  if (sum_left && a.part_bound > 0) load_items(tid);
   if (tid < a.cur_bound) {
     nd_s = a.cur[tid];
     if (a.splits) {
@@ -410,21 +425,34 @@ __device__ void plan_small_level(const PlanArgs& a) {
   const double ug = ldexp(1.0, -a.exps[0]), uh = ldexp(1.0, -a.exps[1]);
   if (sum_left) s_left[tid] = 0;
   __syncthreads();  // every thread has read the counts before any is rewritten
-  if (sum_left) {  // item k's count goes to its node (four items in flight per thread)
-    for (int32_t k0 = tid; k0 < n_items; k0 += 4 * kPlanThreads) {
-      uint32_t node[4];
-      int64_t v[4];
+  if (sum_left) {  // item k's count goes to its node
+    // Lanes of a wavefront hold consecutive items, which the partition work
+    // lists by node: each run of one node is summed in the wavefront (its
+    // inclusive prefix minus the prefix before the run's head) and only the
+    // run's last lane adds it to the node, instead of one LDS atomic per item
+    // on a few addresses.
+    const int lane = tid & 63;
+    for (int32_t base = 0; base < a.part_bound; base += kSumBatch * kPlanThreads) {
+      if (base) load_items(base + tid);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int32_t k = k0 + u * kPlanThreads < n_items ? k0 + u * kPlanThreads : n_items - 1;
-        node[u] = uint32_t(a.cur_part_work[k].node);
-        v[u] = a.work_left[k];
+      for (int u = 0; u < kSumBatch; ++u) {
+        if (base + u * kPlanThreads >= n_items) break;  // uniform (the device count)
+        const int32_t k = base + tid + u * kPlanThreads;
+        const uint32_t node = uint32_t(uint64_t(item_word[u]) >> 32);
+        const bool valid = k < n_items && node < uint32_t(kPlanThreads);
+        const int key = valid ? int(node) : -1;
+        const int v = valid ? int(item_word[u] & 0xffffffffll) : 0;  // <= kPartChunk
+        const int prefix = wave_inclusive_sum32(v);                    // <= 64 * kPartChunk
+        const int prev = __shfl_up(key, 1), next = __shfl_down(key, 1);
+        const bool head = lane == 0 || prev != key, tail = lane == 63 || next != key;
+        const unsigned long long heads = __ballot(head);
+        const unsigned long long upto = lane == 63 ? ~0ull : ((2ull << lane) - 1ull);
+        const int h = 63 - __clzll(heads & upto);  // the run's head lane
+        const int before = __shfl(prefix - v, h);  // the prefix before the run
+        if (tail && key >= 0)
+          atomicAdd(reinterpret_cast<unsigned long long*>(&s_left[key]),
+                    static_cast<unsigned long long>(prefix - before));
       }
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-        if (k0 + u * kPlanThreads < n_items && node[u] < uint32_t(kPlanThreads))
-          atomicAdd(reinterpret_cast<unsigned long long*>(&s_left[node[u]]),
-                    static_cast<unsigned long long>(v[u]));
     }
     __syncthreads();
     nl_s = s_left[tid];
@@ -468,6 +496,7 @@ __device__ void plan_small_level(const PlanArgs& a) {
   int64_t off[4], tot[4];
   block_scan_n<4>(cnt, off, tot, scan);  // its barriers also publish s_error = 0
   if (live && a.splits && sp.expand && !e) s_error = 1;
+  if (tid == 0 && n_items > a.part_bound) s_error = 7;  // items beyond the host bound
   const int64_t rank = off[0];
   const int32_t n_expand = int32_t(tot[0]);
   const int32_t n_next = 2 * n_expand;
@@ -726,7 +755,7 @@ void launch_plan_level(const PlanArgs& a, int64_t level_bound, hipStream_t s) {
 
 void launch_plan_scatter(const PlanArgs& a, const ScatterArgs& sa, int64_t n_rows,
                          hipStream_t s) {
-  need(a.work_left && a.cur_part_work && a.splits, "the merged planner sums the left counts");
+  need(a.work_left && a.splits, "the merged planner sums the left counts");
   need(a.cur_bound <= kPlanThreads, "the merged planner takes levels of at most 1024 nodes");
   const int32_t items = sa.n_work_host < 2048 ? sa.n_work_host : 2048;
   constexpr int Q = kPlanThreads / kPartThreads;

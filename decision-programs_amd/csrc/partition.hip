@@ -116,7 +116,7 @@ __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
     s = splits[w.node];
   }
   if (!s.expand) {
-    if (threadIdx.x == 0) work_left[item] = 0;
+    if (threadIdx.x == 0) work_left[item] = int64_t(w.node) << 32;
     continue;
   }
   int count = 0;
@@ -145,7 +145,7 @@ __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
   if (threadIdx.x == 0) {
     int64_t t = 0;
     for (int k = 0; k < kPartThreads / 64; ++k) t += wave_count[k];
-    work_left[item] = t;
+    work_left[item] = (int64_t(w.node) << 32) | t;  // the node, then its left rows
   }
   __syncthreads();
   }

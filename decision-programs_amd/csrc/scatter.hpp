@@ -74,7 +74,7 @@ __device__ void scatter_items(const ScatterArgs& a, int32_t block, int32_t n_blo
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int32_t k = k0 + u * kPartThreads;
-          v[u] = a.work_left[k < last ? k : last - 1];
+          v[u] = a.work_left[k < last ? k : last - 1] & 0xffffffffll;  // the left rows
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {

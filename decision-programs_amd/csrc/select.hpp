@@ -85,6 +85,17 @@ __device__ __forceinline__ long long wave_inclusive_sum(long long x) {
   return x;
 }
 
+// The same scan of 32-bit values (half the lane moves of the 64-bit one).
+__device__ __forceinline__ int wave_inclusive_sum32(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);
+  return x;
+}
+
 // The largest double of the wavefront, returned to every lane.
 __device__ __forceinline__ double wave_max_f64(double v) {
   long long b = __double_as_longlong(v);
