@@ -83,6 +83,46 @@ __device__ void block_scan_n(const int64_t (&v)[V], int64_t (&out)[V], int64_t (
   __syncthreads();  // lds is reused by the next scan
 }
 
+// block_scan_n over the first nw wavefronts only (nw uniform, 1 <= nw <= 16):
+// the others hold no values, skip the scans (a wavefront's VALU work costs the
+// same whether its lanes are live or not) and pass the same two barriers;
+// their out is 0, and every thread gets the totals, through tot_lds.
+template <int V>
+__device__ void block_scan_live(const int64_t (&v)[V], int64_t (&out)[V], int64_t (&total)[V],
+                                int64_t* lds, int64_t* tot_lds, int nw) {
+  constexpr int W = kPlanThreads / 64;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  const bool live = wave < nw;  // uniform per wavefront
+  int64_t x[V];
+  if (live) {
+#pragma unroll
+    for (int k = 0; k < V; ++k) x[k] = wave_inclusive_sum(v[k]);
+    if (lane == 63)
+#pragma unroll
+      for (int k = 0; k < V; ++k) lds[k * W + wave] = x[k];
+  }
+  __syncthreads();
+  if (live) {
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      const int64_t w = wave_inclusive_sum(lane < nw ? lds[k * W + lane] : 0);
+      out[k] = (wave ? readlane64(w, wave - 1) : 0) + x[k] - v[k];
+      total[k] = readlane64(w, nw - 1);
+    }
+    if (wave == 0 && lane == 0)
+#pragma unroll
+      for (int k = 0; k < V; ++k) tot_lds[k] = total[k];
+  }
+  __syncthreads();  // lds is reused by the next scan; tot_lds is read below
+  if (!live)
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      out[k] = 0;
+      total[k] = tot_lds[k];
+    }
+}
+
 // Exclusive scan of one int64 per thread over the workgroup; returns this
 // thread's prefix and writes the total to *total (two barriers).
 __device__ int64_t block_scan(int64_t v, int64_t* lds, int64_t* total) {
@@ -380,6 +420,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
 __device__ void plan_small_level(const PlanArgs& a) {
   __shared__ int64_t scan[2 * (kPlanThreads / 64) * 4];
   __shared__ int64_t s_left[kPlanThreads];      // left rows per node (a.work_left set)
+  __shared__ int64_t s_tot[4];                  // scan totals for wavefronts without nodes
   __shared__ int64_t s_leaf[kPlanThreads + 1];  // first leaf chunk per node
   __shared__ int64_t s_cs[kPlanThreads + 1];    // first histogram chunk per node
   __shared__ int64_t s_ps[kPlanThreads];        // first partial chunk per node
@@ -469,6 +510,10 @@ __device__ void plan_small_level(const PlanArgs& a) {
   if (tid == 0) s_error = 0;
 
   // ---- per-node state and counts ----------------------------------------------
+  // Only the wavefronts that hold nodes run the per-node phases (the item
+  // loops below use every thread).
+  const int n_waves = n > 0 ? (n + 63) >> 6 : 1;
+  const bool wave_live = (tid >> 6) < n_waves;  // uniform per wavefront
   const bool live = tid < n;
   LevelNode nd{};
   dp_split_record sp{};
@@ -487,14 +532,17 @@ __device__ void plan_small_level(const PlanArgs& a) {
   const bool next_hist = a.depth + 1 < a.max_depth;  // children get histograms
   const int64_t rows = nd.end - nd.begin, lrows = nl, rrows = rows - nl;
   const bool right_small = rrows < lrows;
-  int64_t cnt[4] = {e ? 1 : 0,                                                       // expanded
-                    (live && !e) ? ceil_rows(rows, a.leaf_chunk) : 0,                 // leaf chunks
-                    (e && next_hist) ? (right_small ? rrows : lrows) : 0,            // smaller child
-                    (e && next_hist) ? ceil_rows(lrows, a.part_chunk) +               // partition
-                                           ceil_rows(rrows, a.part_chunk)
-                                     : 0};
+  int64_t cnt[4] = {0, 0, 0, 0};
+  if (wave_live) {
+    cnt[0] = e ? 1 : 0;                                                               // expanded
+    cnt[1] = (live && !e) ? ceil_rows(rows, a.leaf_chunk) : 0;                        // leaf chunks
+    cnt[2] = (e && next_hist) ? (right_small ? rrows : lrows) : 0;                    // smaller child
+    cnt[3] = (e && next_hist)                                                         // partition
+                 ? ceil_rows(lrows, a.part_chunk) + ceil_rows(rrows, a.part_chunk)
+                 : 0;
+  }
   int64_t off[4], tot[4];
-  block_scan_n<4>(cnt, off, tot, scan);  // its barriers also publish s_error = 0
+  block_scan_live<4>(cnt, off, tot, scan, s_tot, n_waves);  // its barriers also publish s_error = 0
   if (live && a.splits && sp.expand && !e) s_error = 1;
   if (tid == 0 && n_items > a.part_bound) s_error = 7;  // items beyond the host bound
   const int64_t rank = off[0];
@@ -549,7 +597,7 @@ __device__ void plan_small_level(const PlanArgs& a) {
   // ---- second scan: histogram chunks of the smaller children -----------------
   const int32_t T = a.n_tiles;
   const int64_t chunk = hist_chunk(tot[2], T);
-  const int64_t nc = ceil_rows(cnt[2], chunk);
+  const int64_t nc = wave_live ? ceil_rows(cnt[2], chunk) : 0;
   int64_t cnt2[2] = {nc, nc >= 2 ? nc : 0}, off2[2], tot2[2];
   if (live) {
     s_leaf[tid] = off[1];
@@ -565,7 +613,7 @@ __device__ void plan_small_level(const PlanArgs& a) {
     s_leaf[n] = tot[1];
     s_po[n] = tot[3];
   }
-  block_scan_n<2>(cnt2, off2, tot2, scan);  // its barriers also publish the arrays above
+  block_scan_live<2>(cnt2, off2, tot2, scan, s_tot, n_waves);  // its barriers also publish the arrays above
   if (live) {
     s_cs[tid] = off2[0];
     s_ps[tid] = off2[1];
