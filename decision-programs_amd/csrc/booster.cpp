@@ -321,6 +321,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
                    node_left_[0].p, c, N, root_slots, root_blocks, chunk_, ridx_[0].p, s);
   int64_t nb = 1;  // bound of the current level's node count
   int64_t nb_prev = 0;
+  bool last_level_applied = false;  // level D's leaves went to the margins in the scatter
   for (int32_t d = 0; d <= D; ++d) {
     const int cur = d & 1, nxt = cur ^ 1;
     if (!eager_ && d > 0) {
@@ -436,6 +437,19 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     a.part_capacity = int32_t(part_work_[nxt].n);
     a.leaf_capacity = int32_t(leaf_work_[cur].n);
     a.cur_bound = int32_t(std::min<int64_t>(nb, INT32_MAX));
+    // The last split level's scatter adds the leaf values of its children (all
+    // leaves) to the margins itself, unless leaf ids are wanted too.
+    if (merged && d + 1 == D && margin && !positions) {
+      scatter.margin = margin;
+      scatter.stride = stride;
+      scatter.nodes = level_[cur].p;
+      scatter.exps = exps;
+      scatter.eta = a.eta;
+      scatter.lambda = a.lambda;
+      scatter.alpha = a.alpha;
+      scatter.mcw = a.mcw;
+      last_level_applied = true;
+    }
     if (merged) {
       a.work_left = work_left_.p;
       a.part_bound = int32_t(plan_part_capacity(nb, N, chunk_));
@@ -456,9 +470,13 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
         prev_leaves.n_host = int32_t(plan_leaf_capacity(nb_prev, N, chunk_));
         prev_leaves.n_dev = field(c, &PlanCounts::n_leaf_prev);
       }
-      launch_update_margin(ridx_[cur].p, leaf_work_[cur].p, leaf_bound,
-                           field(c, &PlanCounts::n_leaf), margin, stride, s,
-                           D >= 1 ? &prev_leaves : nullptr);
+      if (last_level_applied)  // only the leaves of level D - 1 are left
+        launch_update_margin(prev_leaves.ridx, prev_leaves.work, prev_leaves.n_host,
+                             prev_leaves.n_dev, margin, stride, s);
+      else
+        launch_update_margin(ridx_[cur].p, leaf_work_[cur].p, leaf_bound,
+                             field(c, &PlanCounts::n_leaf), margin, stride, s,
+                             D >= 1 ? &prev_leaves : nullptr);
       if (positions) {
         if (D >= 1)
           launch_leaf_positions(prev_leaves.ridx, prev_leaves.work, prev_leaves.n_host,

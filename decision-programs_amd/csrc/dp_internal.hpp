@@ -356,6 +356,14 @@ struct ScatterArgs {
   const int64_t* work_left;
   const unsigned long long* masks;
   int64_t* node_left;        // the node's first item writes the node's left total; may be null
+  // Set on the last split level (every child is a leaf): each scattered row
+  // also gets margin[row * stride] += its child's leaf value, eta times the
+  // leaf weight of the child's quantised sums (split record and nodes[node]).
+  float* margin;
+  int64_t stride;
+  const LevelNode* nodes;
+  const int32_t* exps;       // quantiser exponents (gradient, hessian)
+  double eta, lambda, alpha, mcw;
 };
 
 // Partition: counts, then scatter (which writes the left totals of the

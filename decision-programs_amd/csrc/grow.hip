@@ -35,15 +35,8 @@ constexpr int kPlanThreads = 1024;
 // per-item binary searches do not chase dependent global loads.
 constexpr int kLdsOffsets = 4096;
 
-__device__ double plan_threshold_l1(double g, double alpha) {
-  if (g > alpha) return g - alpha;
-  if (g < -alpha) return g + alpha;
-  return 0.0;
-}
-
 __device__ double plan_weight(const PlanArgs& a, double g, double h) {
-  if (h < a.mcw || h <= 0.0) return 0.0;
-  return -plan_threshold_l1(g, a.alpha) / (h + a.lambda);
+  return leaf_weight(g, h, a.lambda, a.alpha, a.mcw);
 }
 
 // ceil(rows / chunk) for 0 <= rows < 2^32 (row ids are 32-bit) and chunk >= 1:
@@ -736,14 +729,14 @@ __global__ __launch_bounds__(kPlanThreads) void plan_small_kernel(PlanArgs a) {
 // items at a time) in one launch: both read only what the partition count
 // left, and write disjoint buffers (the planner writes the next level's, and
 // the next level's partition count in counts->n_part).
-template <int G>
+template <int G, bool MARGIN>
 __global__ __launch_bounds__(kPlanThreads) void plan_scatter_kernel(PlanArgs a, ScatterArgs sa) {
   if (blockIdx.x == 0) {
     plan_small_level(a);
     return;
   }
-  scatter_items<G, kPlanThreads / kPartThreads>(sa, int32_t(blockIdx.x) - 1,
-                                                  int32_t(gridDim.x) - 1);
+  scatter_items<G, kPlanThreads / kPartThreads, MARGIN>(sa, int32_t(blockIdx.x) - 1,
+                                                          int32_t(gridDim.x) - 1);
 }
 
 __global__ __launch_bounds__(256) void plan_root_kernel(
@@ -809,7 +802,9 @@ void launch_plan_scatter(const PlanArgs& a, const ScatterArgs& sa, int64_t n_row
   constexpr int Q = kPlanThreads / kPartThreads;
   const int blocks = 1 + (items + Q - 1) / Q;
   // Four steps per load group on matrices of 4M rows or more, as the partition.
-  auto k = n_rows >= (int64_t(1) << 22) ? plan_scatter_kernel<4> : plan_scatter_kernel<1>;
+  const bool wide = n_rows >= (int64_t(1) << 22);
+  auto k = sa.margin ? (wide ? plan_scatter_kernel<4, true> : plan_scatter_kernel<1, true>)
+                     : (wide ? plan_scatter_kernel<4, false> : plan_scatter_kernel<1, false>);
   hipLaunchKernelGGL(k, dim3(blocks), dim3(kPlanThreads), 0, s, a, sa);
   DP_HIP(hipGetLastError());
 }

@@ -28,10 +28,23 @@ static_assert(kPartSteps * (kPartThreads / 64) == kPartMasks, "one mask per wave
 
 __device__ __forceinline__ int popc64(unsigned long long m) { return __popcll(m); }
 
+// A leaf's weight as the planner records it (upstream's CalcWeight with
+// max_delta_step 0): -T(g) / (h + lambda), T the L1 soft threshold alpha; 0
+// when h < min_child_weight or h <= 0.  Double, compiled without contraction.
+__device__ inline double leaf_weight(double g, double h, double lambda, double alpha,
+                                     double mcw) {
+  if (h < mcw || h <= 0.0) return 0.0;
+  const double t = g > alpha ? g - alpha : (g < -alpha ? g + alpha : 0.0);
+  return -t / (h + lambda);
+}
+
 // Items block * Q + quarter + k * n_blocks * Q.  Rows of a group of G steps:
 // the first group's ids are loaded with the item's other inputs; with G > 1
 // (large matrices) each later group's while the group before it is written.
-template <int G, int Q>
+// MARGIN: the last split level's variant (a.margin set), a separate
+// instantiation so that its registers do not lower the other levels'
+// occupancy.
+template <int G, int Q, bool MARGIN = false>
 __device__ void scatter_items(const ScatterArgs& a, int32_t block, int32_t n_blocks) {
   __shared__ int64_t wave_sum[Q][2][kPartThreads / 64];
   const int q = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kPartThreads);
@@ -104,6 +117,47 @@ __device__ void scatter_items(const ScatterArgs& a, int32_t block, int32_t n_blo
     __syncthreads();  // wave_sum is rewritten by the next items
     if (!act) continue;  // after the barriers every quarter passes
     if (a.node_left && item == first && t == 0) a.node_left[w.node] = n_left;
+    // On the last split level: the children's leaf values, computed as the
+    // next planner computes them from the same quantised sums, are added to the
+    // margins of the rows as they are scattered.
+    if constexpr (MARGIN) {
+      const dp_split_record sp = a.splits[w.node];
+      const LevelNode nd = a.nodes[w.node];
+      const double ug = ldexp(1.0, -a.exps[0]), uh = ldexp(1.0, -a.exps[1]);
+      const float v_left = float(leaf_weight(double(sp.gl) * ug, double(sp.hl) * uh, a.lambda,
+                                             a.alpha, a.mcw) * a.eta);
+      const float v_right = float(leaf_weight(double(nd.g - sp.gl) * ug, double(nd.h - sp.hl) * uh, a.lambda,
+                                  a.alpha, a.mcw) * a.eta);
+      // The row ids of every step of the item, then their margins, then the
+      // stores: two dependent round trips per item instead of two per step.
+      const int n_steps = int((w.end - w.begin + kPartThreads - 1) / kPartThreads);  // uniform
+      uint32_t r[kPartSteps];
+      float m[kPartSteps];
+#pragma unroll
+      for (int st = 0; st < kPartSteps; ++st) {
+        const int64_t i = w.begin + int64_t(st) * kPartThreads + t;
+        r[st] = st < n_steps ? a.ridx_in[i < w.end ? i : w.end - 1] : 0u;
+      }
+#pragma unroll
+      for (int st = 0; st < kPartSteps; ++st)
+        m[st] = st < n_steps ? a.margin[int64_t(r[st]) * a.stride] : 0.0f;
+#pragma unroll
+      for (int st = 0; st < kPartSteps; ++st) {
+        if (st >= n_steps) break;  // uniform per quarter
+        const int64_t i = w.begin + int64_t(st) * kPartThreads + t;
+        const int idx = st * (kPartThreads / 64) + wave;
+        const unsigned long long mask = (unsigned long long)readlane64((long long)my_mask, idx);
+        const int64_t prefix =
+            lefts_before + __builtin_amdgcn_readlane(excl, idx) + popc64(mask & below);
+        const bool left = (mask >> lane) & 1ull;
+        const int64_t dst = left ? begin + prefix : begin + n_left + ((i - begin) - prefix);
+        if (i < w.end) {
+          a.ridx_out[dst] = r[st];
+          a.margin[int64_t(r[st]) * a.stride] = m[st] + (left ? v_left : v_right);
+        }
+      }
+      continue;
+    }
 #pragma unroll 1
     for (int g0 = 0; g0 < kPartSteps; g0 += G) {
       if (w.begin + int64_t(g0) * kPartThreads >= w.end) break;  // uniform per quarter

@@ -289,6 +289,33 @@ def _small_booster(dp, config, n, f, objective, k, rounds, depth=5, seed=7, max_
     return bst, values, labels
 
 
+@pytest.mark.parametrize("config,n,f,objective,k,depth", [(2, 30000, 28, 0, 1, 6),
+                                                           (4, 1500, 784, 1, 10, 4),
+                                                           (5, 4000, 60, 2, 1, 7)])
+def test_margins_without_leaf_ids(dp, device, config, n, f, objective, k, depth):
+    """Without leaf ids recorded, the last split level's scatter adds the leaf values to the
+    margins itself (no separate margin pass for those leaves); margins and models must equal a
+    booster's that records leaf ids, whose margins the oracle tests pin."""
+    from dpgbdt import ops
+
+    values, labels, _, _ = ops.synth(config, n, 11, n_features=f)
+    obj = {0: "binary:logistic", 1: "multi:softmax", 2: "reg:squarederror"}[objective]
+    out = []
+    for record in (0, 1):
+        params = {"objective": obj, "max_depth": depth, "eta": 0.3, "max_bin": 256,
+                  "dp_record_positions": record}
+        if objective == 1:
+            params["num_class"] = k
+        dtrain = dp.DMatrix(values, labels)
+        bst = dp.Booster(params, [dtrain])
+        for r in range(3):
+            bst.update(dtrain, r)
+        model = json.loads(bst.save_raw())["learner"]["gradient_booster"]["model"]
+        out.append((bst.margins(n, k), model))
+    np.testing.assert_array_equal(out[0][0].view(np.uint32), out[1][0].view(np.uint32))
+    assert out[0][1] == out[1][1]
+
+
 @pytest.mark.parametrize("config,n,f,objective,k", [(1, 5000, 8, 0, 1), (4, 1500, 784, 1, 10),
                                                      (5, 4000, 60, 2, 1)])
 def test_prediction_equals_training_margins(dp, device, config, n, f, objective, k):
