@@ -370,8 +370,8 @@ struct ScatterArgs {
 // expanding nodes into node_left).  cols: column-major copy of the bins
 // (launch_tiles_to_columns) or null to read the tiles.  work_left: one word
 // per work item, the item's node in the upper 32 bits and its left rows in the
-// lower 32 (zero for a node that does not expand); masks: kPartMasks words per work item (the count kernel's
-// ballots, read back by the scatter).  node_left_zeroed: the caller has zeroed
+// lower 32 (zero for a node that does not expand); masks: kPartMasks words per
+// work item (the count kernel's ballots, read back by the scatter).  node_left_zeroed: the caller has zeroed
 // node_left[0, nodes) (non-expanding nodes keep 0); else it is cleared here
 // for n_nodes nodes.  deferred: when given, the scatter is not launched; its
 // arguments are written there (n_work_host = 0: nothing to scatter) for

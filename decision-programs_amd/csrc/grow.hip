@@ -408,8 +408,9 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
 // histogram chunk, which depends on the first's totals); the offsets and
 // segments then sit in LDS, read-only, for the item loops.  Its work lists
 // are identical to plan_level_kernel's.  With a.work_left set it sums each
-// node's left rows from the partition count's per-item counts itself, so it
-// can run beside the level's scatter (which publishes them in node_left).
+// node's left rows from the partition count's per-item words (node << 32 |
+// left rows) itself, so it can run beside the level's scatter (which
+// publishes the totals in node_left).
 __device__ void plan_small_level(const PlanArgs& a) {
   __shared__ int64_t scan[2 * (kPlanThreads / 64) * 4];
   __shared__ int64_t s_left[kPlanThreads];      // left rows per node (a.work_left set)
