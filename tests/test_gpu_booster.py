@@ -203,6 +203,18 @@ def test_wide_tree_level_synced(dp, oracle, device):
     assert max(len(t["left"]) for t in o_trees) > 2 ** 12, "tree too small to exercise the path"
 
 
+def test_deep_eager_tree(dp, oracle, device):
+    """Depth 12 over 60,000 rows, enqueued whole: levels whose node bound is at most 1024 run
+    the planner beside the scatter in one launch (level 10 at the 1024 bound), the deeper ones
+    run them as two launches."""
+    p = {"max_depth": 12, "eta": 0.3}
+    print("[booster] C1 60000 x 8, depth 12 (merged and separate planner launches)", flush=True)
+    bst, x, o_trees, o_margin, pos, n = _train_both(dp, oracle, device, 1, 60000, 8, 0, 1, p, 2,
+                                                    20261213)
+    _compare(bst, o_trees, o_margin, pos, n, 1)
+    assert max(len(t["left"]) for t in o_trees) > 2 ** 11, "tree too small to exercise the path"
+
+
 def test_large_matrix_grouped_partition(dp, oracle, device):
     """4,300,000 rows: matrices of 4M rows or more take the partition kernels that
     load four 256-row steps per group (from the column copy of the bins)."""
