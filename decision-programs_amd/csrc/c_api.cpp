@@ -87,7 +87,17 @@ void copy_float_array(const ArrayInterface& a, int64_t n, int64_t k, float* dst)
   int64_t elems = 1;
   for (int64_t s : a.shape) elems *= s;
   dp::need(elems == n * k, "array interface shape differs from the matrix");
-  dp::need(a.strides.empty() || (a.strides.back() == 4), "array interface must be contiguous");
+  // One copy of `elems` floats: the strides, when given, must be the
+  // C-contiguous strides of the whole shape (a column slice of a wider array,
+  // e.g. [n, 1] with row stride 8, is refused rather than read as contiguous).
+  if (!a.strides.empty()) {
+    dp::need(a.strides.size() == a.shape.size(), "array interface strides differ from its shape");
+    int64_t expect = 4;
+    for (size_t d = a.shape.size(); d-- > 0;) {
+      dp::need(a.shape[d] == 1 || a.strides[d] == expect, "array interface must be C-contiguous");
+      expect *= a.shape[d];
+    }
+  }
   DP_HIP(hipMemcpy(dst, reinterpret_cast<const void*>(a.data), sizeof(float) * size_t(elems),
                    hipMemcpyDefault));
 }

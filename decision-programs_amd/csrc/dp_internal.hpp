@@ -323,6 +323,9 @@ void launch_subtract(const int64_t* parent, const int64_t* built, int64_t* sibli
 // the split records were written: always with select; without it, only for
 // matrices few enough features for one workgroup per node -- otherwise the
 // caller selects from the candidates (SplitSelect in launch_partition).
+// With at most kEvalNodeFeatures features the evaluation writes the split
+// records itself (one workgroup per node) and uses no scratch.
+constexpr int kEvalNodeFeatures = 16;
 size_t evaluate_scratch_bytes(int32_t n_nodes, int32_t n_features);
 bool launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_nodes_dev,
                      int32_t n_features, int32_t bin_stride, const int32_t* n_bins,

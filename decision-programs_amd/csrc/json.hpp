@@ -81,11 +81,35 @@ class Parser {
     if (s_.substr(i_, w.size()) == w) { i_ += w.size(); return true; }
     return false;
   }
+  // Objects and arrays nest at most this deep: the descent is recursive, so a
+  // hostile '[[[[...' document is refused before it exhausts the host stack.
+  static constexpr int kMaxDepth = 512;
+  int depth_ = 0;
+  struct Nest {
+    int& d;
+    explicit Nest(int& depth) : d(depth) {
+      need(++d <= kMaxDepth, "JSON nesting deeper than " + std::to_string(kMaxDepth) + " levels");
+    }
+    ~Nest() { --d; }
+  };
   Value value() {
     ws();
     need(i_ < s_.size(), "unexpected end of JSON");
     Value v;
     const char c = s_[i_];
+    if (c == '{' || c == '[') {
+      Nest nest(depth_);
+      return container(c);
+    }
+    if (c == '"') {
+      v.kind = Value::String;
+      v.text = string();
+      return v;
+    }
+    return scalar();
+  }
+  Value container(char c) {
+    Value v;
     if (c == '{') {
       v.kind = Value::Object;
       ++i_;
@@ -122,11 +146,10 @@ class Parser {
         return v;
       }
     }
-    if (c == '"') {
-      v.kind = Value::String;
-      v.text = string();
-      return v;
-    }
+    return v;
+  }
+  Value scalar() {
+    Value v;
     if (lit("true")) { v.kind = Value::Bool; v.boolean = true; return v; }
     if (lit("false")) { v.kind = Value::Bool; v.boolean = false; return v; }
     if (lit("null")) return v;

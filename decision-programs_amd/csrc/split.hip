@@ -311,7 +311,7 @@ __global__ __launch_bounds__(256) void evaluate_features_seg_kernel(
 }
 
 constexpr int kNodeWaves = 16;     // wavefronts per node in evaluate_nodes_kernel
-constexpr int kNodeFeatures = 16;  // feature counts up to this use evaluate_nodes_kernel
+constexpr int kNodeFeatures = kEvalNodeFeatures;  // feature counts up to this use evaluate_nodes_kernel
 
 // Few features: one workgroup per node (looping over nodes); wavefront w
 // scans features w, w + 16, ..., keeps its best, and the workgroup's best is

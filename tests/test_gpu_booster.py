@@ -557,3 +557,105 @@ def test_c5_full_size_layouts_agree(dp, device):
         np.testing.assert_array_equal(a, b)
     np.testing.assert_array_equal(np.asarray(g1).view(np.uint32), np.asarray(g0).view(np.uint32))
     assert len(json.loads(m1)["learner"]["gradient_booster"]["model"]["trees"]) == 2
+
+
+@pytest.mark.parametrize("case", ["level_synced", "large"])
+def test_last_level_margins_synced_and_large(dp, oracle, device, case):
+    """The last split level's margin scatter (taken when leaf ids are not recorded) on the
+    paths the other margin test leaves out: a level-synced tree (depth 17, so the host reads
+    each level's size back) whose levels hold at most 1024 nodes and that reaches its last
+    split level, and a 4,300,000-row matrix (the partition's grouped-load instantiation).
+    Margins and models equal a booster's that records leaf ids; for the level-synced case
+    both also equal the oracle's margins."""
+    import torch
+    from dpgbdt import ops
+
+    if case == "level_synced":
+        n, depth, mcw = 1000, 17, 0.0
+        rng = np.random.default_rng(5)
+        x = rng.random((n, 8), dtype=np.float32)
+        y = (rng.random(n) < 0.5).astype(np.float32)
+        values = torch.as_tensor(x, device=device)
+        labels = torch.as_tensor(y, device=device)
+    else:
+        n, depth, mcw = 4_300_000, 6, 1.0
+        values, labels, _, _ = ops.synth(1, n, 13, n_features=8)
+    print(f"[booster] last-level margins, {case}: {n} rows, depth {depth}", flush=True)
+    out = []
+    for record in (0, 1):
+        dtrain = dp.DMatrix(values, labels)
+        bst = dp.Booster({"objective": "binary:logistic", "max_depth": depth, "eta": 0.3,
+                          "min_child_weight": mcw, "dp_record_positions": record}, [dtrain])
+        for r in range(2):
+            bst.update(dtrain, r)
+        model = json.loads(bst.save_raw())["learner"]["gradient_booster"]["model"]
+        out.append((bst.margins(n, 1), model, bst))
+    np.testing.assert_array_equal(out[0][0].view(np.uint32), out[1][0].view(np.uint32))
+    assert out[0][1] == out[1][1]
+    if case == "level_synced":
+        trees = out[0][1]["trees"]
+        for t in trees:  # the tree reaches its last split level, every level narrow
+            left = np.array(t["left_children"])
+            d = np.zeros(len(left), dtype=np.int64)
+            for i in range(len(left)):
+                if left[i] != -1:
+                    d[left[i]] = d[i] + 1
+                    d[left[i] + 1] = d[i] + 1
+            assert d.max() == depth and np.bincount(d).max() <= 1024
+        cut_ptr, cuts, _ = oracle.compute_cuts(x, 256)
+        bins = oracle.bin_matrix(x, cut_ptr, cuts, -1)
+        p = oracle.params(eta=0.3, min_child_weight=mcw, max_depth=depth)
+        _, o_margin, _ = oracle.train(bins, cut_ptr, cuts, -1, 0, y, 1, p, 2,
+                                      bin_stride=int(np.diff(cut_ptr).max()))
+        np.testing.assert_array_equal(out[0][0].view(np.uint32), o_margin.view(np.uint32))
+
+
+def test_c5_own_parameters(dp, oracle, device):
+    """C5's own parameters against the oracle (200,000 x 1,000, 95 % missing, max_bin 64,
+    depth 10, squared error, two rounds): the evaluation kernel for at most 64 bins, the
+    present-value histograms and the depth-10 planner together, node for node."""
+    p = {"max_depth": 10, "eta": 0.3}
+    print("[booster] C5 200000 x 1000, 64 bins, depth 10 vs the oracle", flush=True)
+    bst, x, o_trees, o_margin, pos, n = _train_both(dp, oracle, device, 5, 200_000, 1000, 2, 1, p,
+                                                    2, 20261201 + 5, max_bin=64)
+    _compare(bst, o_trees, o_margin, pos, n, 1)
+    assert max(len(t["left"]) for t in o_trees) > 500, "trees too small for depth 10"
+    assert any(t["default_left"].any() for t in o_trees), "learned default direction unused"
+
+
+def test_c3_tree_one_million_rows(dp, oracle, device):
+    """C3's tree on 1,000,000 of its rows (128 features, 256 bins, depth 8, injected
+    gradients), one round against the oracle: the gathered row-major histograms at
+    multi-chunk node sizes, subtraction, evaluation and partition at depth 8."""
+    p = {"max_depth": 8, "eta": 0.3}
+    print("[booster] C3 1000000 x 128, depth 8 vs the oracle", flush=True)
+    bst, x, o_trees, o_margin, pos, n = _train_both(dp, oracle, device, 3, 1_000_000, 128, 2, 1, p,
+                                                    1, 20261203, injected=True)
+    _compare(bst, o_trees, o_margin, pos, n, 1)
+
+
+def test_strided_label_interface_is_refused(dp, device):
+    """A label array interface with strides is copied as one contiguous block, so strides must
+    be the C-contiguous ones: a column slice of an [n, 2] array ([n, 1] with a row stride of 8
+    bytes) is refused, a contiguous [n, 1] with explicit strides is accepted."""
+    import ctypes
+
+    import torch
+    from dpgbdt import ops
+
+    n = 1000
+    values, _, _, _ = ops.synth(1, n, 3)
+    both = torch.zeros((n, 2), dtype=torch.float32, device=device)
+    dtrain = dp.DMatrix(values)
+    lib = dp.load()
+
+    def set_labels(ptr, strides):
+        doc = json.dumps({"data": [ptr, True], "shape": [n, 1], "strides": strides,
+                          "typestr": "<f4", "version": 3})
+        return lib.XGDMatrixSetInfoFromInterface(dtrain.handle, b"label", doc.encode())
+
+    assert set_labels(both.data_ptr(), [8, 4]) == -1
+    assert "C-contiguous" in lib.XGBGetLastError().decode()
+    col = torch.zeros((n, 1), dtype=torch.float32, device=device)
+    assert set_labels(col.data_ptr(), [4, 4]) == 0
+    assert ctypes.sizeof(ctypes.c_float) == 4

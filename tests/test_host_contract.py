@@ -61,3 +61,38 @@ def test_sampling_keys_kept_when_given(dp):
                        "eta": 1, "max_bin": 64, "seed": 7}, 10)
     assert hp["subsample"] == 1.0 and hp["colsample_bynode"] == 0.5
     assert (hp["eta"], hp["max_bin"], hp["seed"]) == (1.0, 64, 7)
+
+
+def _raw_validate(dp, text, classes=3):
+    lib = dp.load()
+    n, out = ctypes.c_uint64(), ctypes.c_char_p()
+    lib.DPValidateHyperparameters.argtypes = [ctypes.c_char_p, ctypes.c_uint32,
+                                              ctypes.POINTER(ctypes.c_uint64),
+                                              ctypes.POINTER(ctypes.c_char_p)]
+    rc = lib.DPValidateHyperparameters(text.encode(), classes, ctypes.byref(n), ctypes.byref(out))
+    return rc, lib.XGBGetLastError().decode()
+
+
+@pytest.mark.parametrize("depth,msg", [(100, "eta must be numeric"), (600, "nesting deeper")])
+def test_json_nesting_is_capped(dp, depth, msg):
+    """The JSON reader descends recursively: nesting beyond 512 levels is refused
+    with an error instead of exhausting the host stack."""
+    text = '{"rounds":2,"max_depth":2,"eta":' + "[" * depth + "]" * depth + "}"
+    rc, err = _raw_validate(dp, text)
+    assert rc == -1 and msg in err
+
+
+def test_deeply_nested_model_buffer_is_refused(dp):
+    """XGBoosterLoadModelFromBuffer takes caller bytes: a 100,000-deep array
+    fails with status -1 (the process survives)."""
+    lib = dp.load()
+    h = ctypes.c_void_p()
+    assert lib.XGBoosterCreate(None, 0, ctypes.byref(h)) == 0
+    try:
+        buf = b"[" * 100000 + b"]" * 100000
+        lib.XGBoosterLoadModelFromBuffer.argtypes = [ctypes.c_void_p, ctypes.c_char_p,
+                                                     ctypes.c_uint64]
+        assert lib.XGBoosterLoadModelFromBuffer(h, buf, len(buf)) == -1
+        assert "nesting deeper" in lib.XGBGetLastError().decode()
+    finally:
+        lib.XGBoosterFree(h)
