@@ -615,6 +615,24 @@ int dp_evaluate_splits(dp_workspace ws, const int64_t* hist, int32_t n_nodes,
   });
 }
 
+int dp_evaluate_splits_noalloc(const int64_t* hist, int32_t n_nodes, int32_t n_features,
+                               int32_t bin_stride, const int32_t* n_bins,
+                               const int64_t* node_sums, int32_t exp_g, int32_t exp_h,
+                               const dp_train_param* param, dp_split_record* out, void* stream) {
+  return guarded([&] {
+    dp::need(hist && n_bins && node_sums && param && out, "null argument");
+    dp::need(n_nodes >= 0 && n_features >= 1, "node and feature counts");
+    if (n_nodes == 0) return;
+    // The candidates go to the library's device array: no workspace, no
+    // allocation, no host synchronisation.
+    const size_t bytes =
+        n_features > dp::kEvalNodeFeatures ? dp::evaluate_scratch_bytes(n_nodes, n_features) : 0;
+    void* scratch = dp::noalloc_scratch(bytes);
+    dp::launch_evaluate(hist, n_nodes, nullptr, n_features, bin_stride, n_bins, node_sums, nullptr,
+                        exp_g, exp_h, *param, scratch, out, as_stream(stream));
+  });
+}
+
 int dp_partition(dp_workspace ws, const uint8_t* bins, const dp_bin_layout* layout,
                  const uint32_t* ridx_in, uint32_t* ridx_out, const int64_t* begin,
                  const int64_t* end, const dp_split_record* splits, int32_t n_nodes,

@@ -560,6 +560,13 @@ void sketch_cuts(dp_workspace_s& ws, const float* values, int64_t n_rows, int32_
 void launch_synth(int32_t config, uint64_t seed, int64_t n_rows, int32_t n_features,
                   float* values, float* labels, float* grad, float* hess, hipStream_t s);
 
+// Device memory of the entry points that allocate nothing (noalloc.hip): a
+// file-scope array of this many bytes per GPU.  Returns its device address on
+// the current device (looked up once per device); fails when `bytes` exceeds
+// the array.
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
+void* noalloc_scratch(size_t bytes);
+
 inline int grid_for(int64_t n, int threads, int64_t cap = 65536) {
   int64_t g = (n + threads - 1) / threads;
   if (g < 1) g = 1;

@@ -133,6 +133,9 @@ def load():
         "dp_evaluate_splits": (c_int, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p,
                                        c_int32, c_int32, POINTER(TrainParam), c_void_p,
                                        c_void_p]),
+        "dp_evaluate_splits_noalloc": (c_int, [c_void_p, c_int32, c_int32, c_int32, c_void_p,
+                                               c_void_p, c_int32, c_int32, POINTER(TrainParam),
+                                               c_void_p, c_void_p]),
         "dp_partition": (c_int, [H, c_void_p, POINTER(BinLayout), c_void_p, c_void_p, c_void_p,
                                  c_void_p, c_void_p, c_int32, c_void_p, c_void_p]),
         "dp_update_margin": (c_int, [H, c_void_p, c_void_p, c_void_p, c_void_p, c_int32,

@@ -276,6 +276,19 @@ int dp_evaluate_splits(dp_workspace ws, const int64_t* hist, int32_t n_nodes, in
                        int32_t exp_g, int32_t exp_h, const dp_train_param* param,
                        dp_split_record* out, void* stream);
 
+/* As dp_evaluate_splits, but allocates nothing: no workspace, no hipMalloc,
+ * no host synchronisation.  No counterpart in the reference; it is for
+ * callers that cannot allocate (code under HIP graph capture, serving loops
+ * that forbid hipMalloc).  The per-(node, feature) candidates live in a
+ * library-owned device array of 16 MiB per GPU, so n_nodes * n_features must
+ * not exceed 524,288 when n_features > 16 (with at most 16 features no
+ * scratch is used); larger calls fail with an error.  Calls on one GPU share
+ * that array: calls that overlap on one GPU (two streams or threads) race. */
+int dp_evaluate_splits_noalloc(const int64_t* hist, int32_t n_nodes, int32_t n_features,
+                               int32_t bin_stride, const int32_t* n_bins,
+                               const int64_t* node_sums, int32_t exp_g, int32_t exp_h,
+                               const dp_train_param* param, dp_split_record* out, void* stream);
+
 /* Stable partition: for every node i with splits[i].expand, the rows
  * ridx_in[begin[i], end[i]) are written to ridx_out[begin[i], end[i]) with the
  * left child's rows first.  left_count [n_nodes] (device, int64) receives the
