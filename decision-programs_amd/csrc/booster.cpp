@@ -98,6 +98,8 @@ std::string validate_hyperparameters(const std::string& text, uint32_t classes) 
   };
   const uint64_t max_bin = integer(or_default("max_bin", "256"), "max_bin", INT_MAX);
   need(max_bin >= 2, "max_bin must be at least 2");
+  need(max_bin <= uint64_t(kMaxBins),
+       "max_bin above 256 is not supported by this library: bins are stored as uint8");
   const uint64_t seed = integer(or_default("seed", "0"), "seed", INT_MAX);
   const double eta = numeric(or_default("eta", "0.3"), "eta", 0, 1, true);
   std::string o = "{\"rounds\":" + std::to_string(rounds) + ",\"max_depth\":" +
@@ -223,6 +225,7 @@ void Grower::ensure_level(const Quantized& q, int64_t nb, int32_t d, int32_t D) 
     hist_[cur].reserve(size_t(nb * S));
     splits_.reserve(size_t(nb));
     eval_scratch_.reserve(evaluate_scratch_bytes(int32_t(nb), q.layout.n_features));
+    if (colsample_) fmask_.reserve(size_t(nb) * size_t((q.layout.n_features + 31) / 32));
     work_left_.reserve(size_t(plan_part_capacity(nb, N, chunk_)));
     part_masks_.reserve(size_t(plan_part_capacity(nb, N, chunk_)) * kPartMasks);
   }
@@ -243,6 +246,7 @@ void Grower::prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, b
   const dp_bin_layout& L = q.layout;
   need(sparse ? q.sparse.n_tiles > 0 : q.rows.n > 0, "histogram layout not built");
   sparse_ = sparse;
+  colsample_ = p.colsample();
   tiles_ = sparse ? q.sparse.n_tiles : L.n_tiles;
   const int64_t N = L.n_rows;
   const int32_t D = p.max_depth;
@@ -375,10 +379,18 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
         launch_hist_reduce(partial_.p, reduce_jobs_[cur].p, int32_t(nb / 2 + 1),
                            field(c, &PlanCounts::n_reduce), T, F, B, hist_[nxt].p, h, false, s);
       }
+      // Column sampling: each node's feature sample, read by the evaluation.
+      const uint32_t* fmask = nullptr;
+      if (colsample.active()) {
+        need(colsample_, "column sampling buffers were not prepared");
+        launch_colsample(level_[cur].p, int32_t(nb), field(c, &PlanCounts::n_level), F,
+                         colsample, d, fmask_.p, s);
+        fmask = fmask_.p;
+      }
       // Without records from the evaluation, the count launch selects them.
       const bool records = launch_evaluate(h, int32_t(nb), field(c, &PlanCounts::n_level), F, B,
                                            q.d_nbins.p, sums_[cur].p, exps, 0, 0, dtp,
-                                           eval_scratch_.p, splits_.p, s, false);
+                                           eval_scratch_.p, splits_.p, s, false, fmask);
       SplitSelect sel;
       sel.cand = reinterpret_cast<const FeatCand*>(eval_scratch_.p);
       sel.n_features = F;
@@ -527,8 +539,8 @@ uint64_t Grower::signature() const {
   }
   buf(root_work_); buf(root_job_); buf(partial_); buf(pair_chunk_); buf(work_left_);
   buf(part_masks_);
-  buf(splits_); buf(eval_scratch_); buf(info_); buf(counts_); buf(slots_);
-  mix(uint64_t(eager_)); mix(uint64_t(sparse_)); mix(uint64_t(tiles_));
+  buf(splits_); buf(eval_scratch_); buf(fmask_); buf(info_); buf(counts_); buf(slots_);
+  mix(uint64_t(eager_)); mix(uint64_t(sparse_)); mix(uint64_t(colsample_)); mix(uint64_t(tiles_));
   mix(uint64_t(node_cap_)); mix(uint64_t(chunk_));
   mix(uint64_t(slot_bytes_)); mix(uint64_t(root_rows_)); mix(uint64_t(root_tiles_));
   mix(uint64_t(root_items_));
@@ -682,8 +694,24 @@ void Booster::configure(DMatrix* d) {
        "regularisation parameters must be non-negative");
   need(tp.max_depth >= 1 && tp.max_depth <= 30, "max_depth must be in [1, 30]");
   need(tp.max_bin >= 2, "max_bin must be at least 2");
-  for (const char* k : {"subsample", "colsample_bytree", "colsample_bylevel", "colsample_bynode"})
-    need(parse_float(k, get(k, "1")) == 1.0f, std::string(k) + " other than 1 is not supported");
+  need(tp.max_bin <= kMaxBins, "max_bin above 256 is not supported: bins are stored as uint8");
+  // Row and column sampling (draws defined in sample.hpp).
+  float* fractions[] = {&tp.subsample, &tp.colsample_bytree, &tp.colsample_bylevel,
+                        &tp.colsample_bynode};
+  const char* fraction_keys[] = {"subsample", "colsample_bytree", "colsample_bylevel",
+                                 "colsample_bynode"};
+  for (int i = 0; i < 4; ++i) {
+    *fractions[i] = parse_float(fraction_keys[i], get(fraction_keys[i], "1"));
+    need(*fractions[i] > 0.0f && *fractions[i] <= 1.0f,
+         std::string(fraction_keys[i]) + " must be in (0, 1]");
+  }
+  {
+    const std::string v = get("seed", "0");
+    char* end = nullptr;
+    const long long x = std::strtoll(v.c_str(), &end, 10);
+    need(end && *end == '\0' && !v.empty(), "invalid integer value for seed: " + v);
+    tp.seed = uint64_t(x);
+  }
   const std::string method = get("tree_method", "hist");
   need(method == "hist" || method == "gpu_hist" || method == "auto",
        "tree_method must be hist");
@@ -854,6 +882,7 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
     qp = &d->quantize(tp_.max_bin, scratch, stream_);
   }
   Quantized& q = *qp;
+  effective_max_bin_ = q.max_bin;
   // Histogram layout: the present-value layout for mostly-missing matrices,
   // else the row-major copy of the tiles for gathered rows.
   bool sparse = false;
@@ -909,36 +938,65 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
       reinterpret_cast<uint64_t>(quant_scratch_.p),
       reinterpret_cast<uint64_t>(positions), reinterpret_cast<uint64_t>(q.sparse.ptr.p),
       reinterpret_cast<uint64_t>(q.sparse.entries.p), uint64_t(sparse), uint64_t(S)};
+  // Sampling kernels read the round's index from device memory, stored ahead
+  // of the (possibly replayed) round.
+  RowSample rows;
+  if (tp_.subsample < 1.0f || tp_.colsample()) {
+    round_dev_.reserve(1);
+    launch_store_i32(round_dev_.p, rounds_, stream_);
+    if (tp_.subsample < 1.0f) {
+      rows.seed = tp_.seed;
+      rows.threshold = uint64_t(std::ldexp(double(tp_.subsample), 32));
+      rows.round = round_dev_.p;
+    }
+  }
+  key.push_back(reinterpret_cast<uint64_t>(round_dev_.p));
   for (int32_t l = 0; l < S; ++l) key.push_back(growers_[size_t(l)]->signature());
   words(key, &q.layout, sizeof q.layout);
   words(key, &tp_, sizeof tp_);
   enqueue(key, eager, [&] {
     bool maxima = false;
+    // With row sampling the quantiser takes the maxima over the kept rows.
     if (with_gradients)
       maxima = launch_gradients(objective_id_, margin_.p, d->labels.p, N, K, grad_.p, hess_.p,
-                                quant_scratch_.p, stream_);
+                                rows.active() ? nullptr : quant_scratch_.p, stream_);
     // The per-workgroup sums stay in the quantiser's slots: each tree's first
     // launch adds up its output's.
     launch_quantise(grad_.p, hess_.p, N, K, quant_scratch_.p, maxima, exps_.p, gpair_.p, nullptr,
-                    stream_);
+                    stream_, rows);
     const int32_t blocks = quantise_blocks(N);
     const int64_t* slots = quantise_sum_slots(quant_scratch_.p, N, K);
+    auto sample_columns = [&](Grower& g, int32_t k) {
+      g.colsample = ColSample{};
+      if (tp_.colsample()) {
+        g.colsample.seed = tp_.seed;
+        g.colsample.round = round_dev_.p;
+        g.colsample.output = k;
+        g.colsample.bytree = tp_.colsample_bytree;
+        g.colsample.bylevel = tp_.colsample_bylevel;
+        g.colsample.bynode = tp_.colsample_bynode;
+      }
+    };
     if (S == 1) {
-      for (int32_t k = 0; k < K; ++k)
+      for (int32_t k = 0; k < K; ++k) {
+        sample_columns(*growers_[0], k);
         growers_[0]->grow(q, gpair_.p + int64_t(k) * N * 2, exps_.p + 2 * k,
                           slots + int64_t(k) * blocks * 2, blocks, tp_, margin_.p + k, K,
                           positions, k, stream_);
+      }
       return;
     }
     // Each tree writes its own margin column; only the last writes the row
     // positions (the round's positions are its last tree's).
     DP_HIP(hipEventRecord(fork_, stream_));
     for (int32_t l = 0; l < S; ++l) DP_HIP(hipStreamWaitEvent(tree_streams_[size_t(l)], fork_, 0));
-    for (int32_t k = 0; k < K; ++k)
+    for (int32_t k = 0; k < K; ++k) {
+      sample_columns(*growers_[size_t(k % S)], k);
       growers_[size_t(k % S)]->grow(q, gpair_.p + int64_t(k) * N * 2, exps_.p + 2 * k,
                                     slots + int64_t(k) * blocks * 2, blocks, tp_, margin_.p + k,
                                     K, k == K - 1 ? positions : nullptr, k / S,
                                     tree_streams_[size_t(k % S)]);
+    }
     for (int32_t l = 0; l < S; ++l) {
       DP_HIP(hipEventRecord(tree_done_[size_t(l)], tree_streams_[size_t(l)]));
       DP_HIP(hipStreamWaitEvent(stream_, tree_done_[size_t(l)], 0));
@@ -1124,7 +1182,10 @@ std::string Booster::save_config() const {
        "\"},\"gbtree_train_param\":{\"process_type\":\"default\",\"tree_method\":\"hist\","
        "\"updater\":\"grow_gpu_hist\",\"updater_seq\":\"grow_gpu_hist\"},\"name\":\"gbtree\","
        "\"updater\":[{\"hist_train_param\":{\"max_bin\":\"";
-  o += std::to_string(tp_.max_bin) + "\"},\"name\":\"grow_gpu_hist\",\"train_param\":{";
+  // The bins actually used: a matrix with missing values keeps byte 255 for
+  // them, so max_bin 256 bins it into at most 255 quantiles.
+  o += std::to_string(effective_max_bin_ > 0 ? effective_max_bin_ : tp_.max_bin) +
+       "\"},\"name\":\"grow_gpu_hist\",\"train_param\":{";
   auto kv = [&](const char* k, const std::string& v, bool comma = true) {
     if (comma) o += ',';
     json::put_string(o, k);
@@ -1356,6 +1417,7 @@ std::unique_ptr<Booster> Booster::slice(int begin, int end, int step) const {
   out->n_features_ = n_features_;
   out->base_score_ = base_score_;
   out->tp_ = tp_;
+  out->effective_max_bin_ = effective_max_bin_;
   out->iteration_indptr_ = {0};
   for (int r = begin; r < end; r += step) {
     for (int32_t t = iteration_indptr_[size_t(r)]; t < iteration_indptr_[size_t(r) + 1]; ++t) {

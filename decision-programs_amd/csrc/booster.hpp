@@ -58,6 +58,14 @@ struct Tree {
 struct TrainParam {
   float eta = 0.3f, lambda = 1.0f, alpha = 0.0f, gamma = 0.0f, min_child_weight = 1.0f;
   int32_t max_depth = 6, max_bin = 256;
+  // Sampling (sample.hpp): fractions in (0, 1], 1 = off; seed of the draws.
+  float subsample = 1.0f, colsample_bytree = 1.0f, colsample_bylevel = 1.0f,
+        colsample_bynode = 1.0f;
+  int32_t pad = 0;  // no padding bytes: the struct's words key the cached round graphs
+  uint64_t seed = 0;
+  bool colsample() const {
+    return colsample_bytree < 1.0f || colsample_bylevel < 1.0f || colsample_bynode < 1.0f;
+  }
 };
 
 // Depth-wise tree growth on one quantised matrix (reusable device buffers).
@@ -79,6 +87,9 @@ class Grower {
   // the 16-feature tiles and the row-major copy (which must then be built).
   void prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, bool sparse,
                hipStream_t s);
+  // Column sampling of the trees grow() enqueues next (inactive: every
+  // feature is a candidate at every node); cs.output is set per tree.
+  ColSample colsample;
   // Enqueues one tree.  gpair: [n_rows][2] fixed-point gradients of one output;
   // exps (device): its two quantiser exponents; root_slots (device): the
   // quantiser's root_blocks per-workgroup (g, h) sums of gpair, added up by the
@@ -113,6 +124,7 @@ class Grower {
   PooledBuffer<unsigned long long> part_masks_;  // count ballots, kPartMasks per item
   PooledBuffer<dp_split_record> splits_;
   PooledBuffer<uint8_t> eval_scratch_;
+  PooledBuffer<uint32_t> fmask_;  // column sampling: [level node][ceil(F / 32)] bits
   PooledBuffer<LeafWork> leaf_work_[2];  // by level parity: applied one level later
   PooledBuffer<NodeInfo> info_;
   PooledBuffer<PlanCounts> counts_;
@@ -124,6 +136,7 @@ class Grower {
   std::vector<PlanCounts> spill_counts_;
   bool eager_ = true;
   bool sparse_ = false;  // histograms from the present-value layout
+  bool colsample_ = false;  // column sampling buffers sized (prepare)
   int32_t tiles_ = 0;    // histogram tiles per row chunk (16-feature or sparse tiles)
   int64_t node_cap_ = 0;
   int64_t chunk_ = kPartChunk;  // rows per partition / margin-update item
@@ -202,12 +215,14 @@ class Booster {
   int32_t n_features_ = 0;
   std::vector<float> base_score_;  // as stored in the model (probability for logistic)
   TrainParam tp_;
+  int32_t effective_max_bin_ = 0;  // the quantiser's max_bin of the last round (0: none yet)
   DMatrix* train_ = nullptr;
   // training state
   PooledBuffer<float> margin_, grad_, hess_;
   PooledBuffer<int32_t> gpair_, exps_;
   PooledBuffer<uint8_t> quant_scratch_;  // quantiser reduction slots
   PooledBuffer<int32_t> positions_;
+  PooledBuffer<int32_t> round_dev_;  // the round's index, read by the sampling kernels
   mutable std::vector<int32_t> last_exps_;
   PooledPinnedBuffer exps_host_;  // two buffers, by round parity
   bool record_positions_ = false;

@@ -10,6 +10,7 @@
 #include <vector>
 
 #include "../../include/dpgbdt.h"
+#include "sample.hpp"
 
 namespace dp {
 
@@ -331,7 +332,14 @@ bool launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_node
                      int32_t n_features, int32_t bin_stride, const int32_t* n_bins,
                      const int64_t* node_sums, const int32_t* exps, int32_t exp_g, int32_t exp_h,
                      const dp_train_param& param, void* scratch, dp_split_record* out,
-                     hipStream_t s, bool select = true);
+                     hipStream_t s, bool select = true, const uint32_t* fmask = nullptr);
+// Column sampling of one level (ColSample active): masks[node][ceil(F / 32)]
+// gets each node's feature sample (bit f set: feature f is a candidate), for
+// the node count *n_dev (n_host when null; n_host bounds the grid).  depth is
+// the level's depth; nodes supply the node ids.
+void launch_colsample(const LevelNode* nodes, int32_t n_host, const int32_t* n_dev,
+                      int32_t n_features, const ColSample& cs, int32_t depth, uint32_t* masks,
+                      hipStream_t s);
 
 // Margin (and optional leaf id) update of leaf chunks: margin[ridx[i] *
 // stride] += value, positions[ridx[i]] = leaf id; work count from n_dev when
@@ -507,9 +515,13 @@ int quantise_blocks(int64_t n_rows);
 // (g, h) pairs start at pair k * quantise_blocks(n_rows).
 const int64_t* quantise_sum_slots(const void* scratch, int64_t n_rows, int32_t n_classes);
 size_t quantise_scratch_bytes(int64_t n_rows, int32_t n_classes);
+// rows: row sampling of the round (inactive by default): a dropped row's
+// (g, h) count as zero in the maxima, the pairs and the sums of its class.
 void launch_quantise(const float* grad, const float* hess, int64_t n_rows, int32_t n_classes,
                      void* scratch, bool maxima_ready, int32_t* exps, int32_t* gpair,
-                     int64_t* sums, hipStream_t s);
+                     int64_t* sums, hipStream_t s, const RowSample& rows = RowSample{});
+// *p = value (one thread), e.g. the round index the sampling kernels read.
+void launch_store_i32(int32_t* p, int32_t value, hipStream_t s);
 
 void launch_bin_values(const float* values, const dp_bin_layout& layout, const int32_t* cut_ptr,
                        const float* cut_values, uint8_t* bins, hipStream_t s);

@@ -115,13 +115,26 @@ __global__ __launch_bounds__(kQuantThreads) void gradients_kernel(
 }
 
 // Per-workgroup max|g|, max|h| of class blockIdx.y into its slots.
+// With row sampling, a dropped row's values count as zero.
+__device__ __forceinline__ uint64_t row_prefix(const RowSample& rs, int k) {
+  return rs.active() ? sample_prefix(rs.seed, kRowStream, uint64_t(uint32_t(*rs.round)),
+                                     uint64_t(uint32_t(k)) << 32)
+                     : 0;
+}
+
+__device__ __forceinline__ bool row_kept(const RowSample& rs, uint64_t prefix, int64_t r) {
+  return !rs.active() || uint64_t(sample_draw(prefix, uint64_t(r))) < rs.threshold;
+}
+
 __global__ __launch_bounds__(kQuantThreads) void absmax_kernel(
     const float* __restrict__ grad, const float* __restrict__ hess, int64_t n_rows,
-    int n_classes, unsigned* __restrict__ max_slots) {
+    int n_classes, unsigned* __restrict__ max_slots, RowSample rs) {
   const int k = blockIdx.y;
+  const uint64_t prefix = row_prefix(rs, k);
   unsigned mg = 0, mh = 0;
   for (int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; r < n_rows;
        r += int64_t(blockDim.x) * gridDim.x) {
+    if (!row_kept(rs, prefix, r)) continue;
     mg = max(mg, __float_as_uint(fabsf(grad[r * n_classes + k])));
     mh = max(mh, __float_as_uint(fabsf(hess[r * n_classes + k])));
   }
@@ -146,7 +159,7 @@ __device__ __forceinline__ int quant_exp(unsigned bits) {
 __global__ __launch_bounds__(kQuantThreads) void quantise_kernel(
     const float* __restrict__ grad, const float* __restrict__ hess, int64_t n_rows,
     int n_classes, const unsigned* __restrict__ max_slots, int32_t* __restrict__ exps,
-    int2* __restrict__ gpair, long long* __restrict__ sum_slots) {
+    int2* __restrict__ gpair, long long* __restrict__ sum_slots, RowSample rs) {
   __shared__ long long wave_sum[2][kQuantThreads / 64];
   __shared__ int s_exp[2];
   const int k = blockIdx.y;
@@ -169,10 +182,12 @@ __global__ __launch_bounds__(kQuantThreads) void quantise_kernel(
   const int eg = s_exp[0], eh = s_exp[1];
   long long sg = 0, sh = 0;
   int2* out = gpair + int64_t(k) * n_rows;
+  const uint64_t prefix = row_prefix(rs, k);
   for (int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; r < n_rows;
        r += int64_t(blockDim.x) * gridDim.x) {
-    const int qg = int(rintf(ldexpf(grad[r * n_classes + k], eg)));
-    const int qh = int(rintf(ldexpf(hess[r * n_classes + k], eh)));
+    const bool kept = row_kept(rs, prefix, r);
+    const int qg = kept ? int(rintf(ldexpf(grad[r * n_classes + k], eg))) : 0;
+    const int qh = kept ? int(rintf(ldexpf(hess[r * n_classes + k], eh))) : 0;
     out[r] = make_int2(qg, qh);
     sg += qg;
     sh += qh;
@@ -304,9 +319,18 @@ bool launch_gradients(int32_t objective, const float* margin, const float* label
   return false;
 }
 
+__global__ void store_i32_kernel(int32_t* p, int32_t value) { *p = value; }
+
+void launch_store_i32(int32_t* p, int32_t value, hipStream_t s) {
+  hipLaunchKernelGGL(store_i32_kernel, dim3(1), dim3(1), 0, s, p, value);
+  DP_HIP(hipGetLastError());
+}
+
 void launch_quantise(const float* grad, const float* hess, int64_t n_rows, int32_t n_classes,
                      void* scratch, bool maxima_ready, int32_t* exps, int32_t* gpair,
-                     int64_t* sums, hipStream_t s) {
+                     int64_t* sums, hipStream_t s, const RowSample& rows) {
+  need(!rows.active() || rows.round != nullptr, "row sampling needs the device round index");
+  need(!(rows.active() && maxima_ready), "row sampling needs the sampled maxima");
   need(n_classes >= 1 && n_classes <= 65535, "class count out of range");
   need(n_rows >= 1, "quantiser needs at least one row");
   const int blocks = quantise_blocks(n_rows);
@@ -316,12 +340,12 @@ void launch_quantise(const float* grad, const float* hess, int64_t n_rows, int32
                                                  ((slots * 2 * sizeof(uint32_t) + 255) & ~size_t(255)));
   if (!maxima_ready) {
     hipLaunchKernelGGL(absmax_kernel, dim3(blocks, n_classes), dim3(kQuantThreads), 0, s, grad,
-                       hess, n_rows, n_classes, max_slots);
+                       hess, n_rows, n_classes, max_slots, rows);
     DP_HIP(hipGetLastError());
   }
   hipLaunchKernelGGL(quantise_kernel, dim3(blocks, n_classes), dim3(kQuantThreads), 0, s, grad,
                      hess, n_rows, n_classes, max_slots, exps, reinterpret_cast<int2*>(gpair),
-                     sum_slots);
+                     sum_slots, rows);
   DP_HIP(hipGetLastError());
   if (!sums) return;  // the caller reduces the sum slots itself
   hipLaunchKernelGGL(finish_sums_kernel, dim3(n_classes), dim3(kQuantThreads), 0, s, sum_slots,

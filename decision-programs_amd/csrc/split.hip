@@ -20,6 +20,7 @@
 // All double arithmetic is compiled with -ffp-contract=off so each value
 // rounds exactly as the CPU restatement computes it.
 #include "dp_internal.hpp"
+#include "sample.hpp"
 #include "select.hpp"
 
 #include <cmath>
@@ -54,6 +55,15 @@ __device__ __forceinline__ double split_loss(const Param& p, long long qgl, long
 }
 
 constexpr int kFeatWaves = 4;  // features per workgroup in evaluate_features_kernel
+
+// Column sampling: fmask holds one bit per feature for every node of the
+// level ([node][ceil(F / 32)] words); null when every feature is a candidate.
+__device__ __forceinline__ bool feature_allowed(const uint32_t* __restrict__ fmask, int32_t node,
+                                                int32_t f, int32_t n_features) {
+  if (!fmask) return true;
+  const int64_t words = (n_features + 31) / 32;
+  return (fmask[int64_t(node) * words + (f >> 5)] >> (f & 31)) & 1u;
+}
 
 __device__ __forceinline__ double dpp_f64_bits(long long bits) { return __longlong_as_double(bits); }
 
@@ -174,7 +184,7 @@ __global__ __launch_bounds__(64 * kFeatWaves) void evaluate_features_kernel(
     const int32_t* __restrict__ n_nodes_dev, int32_t n_features, int32_t bin_stride,
     const int32_t* __restrict__ n_bins, const long long* __restrict__ node_sums,
     const int32_t* __restrict__ exps, int32_t exp_g_host, int32_t exp_h_host, Param p,
-    FeatCand* __restrict__ cand) {
+    const uint32_t* __restrict__ fmask, FeatCand* __restrict__ cand) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int32_t n_nodes = n_nodes_dev ? *n_nodes_dev : n_nodes_host;
   const int32_t groups = (n_features + kFeatWaves - 1) / kFeatWaves;
@@ -190,7 +200,9 @@ __global__ __launch_bounds__(64 * kFeatWaves) void evaluate_features_kernel(
     load_feature<BPL>(hist, node, f, n_features, bin_stride, bins);
     const long long gp = node_sums[2 * node], hp = node_sums[2 * node + 1];
     const double parent_gain = calc_gain(p, double(gp) * ug, double(hp) * uh);
-    const Cand c = feature_best<BPL>(bins, f, n_bins[f], gp, hp, parent_gain, ug, uh, p);
+    // A feature outside the node's sample has no bins to split at: loss -inf.
+    const int nb = feature_allowed(fmask, node, f, n_features) ? n_bins[f] : 0;
+    const Cand c = feature_best<BPL>(bins, f, nb, gp, hp, parent_gain, ug, uh, p);
     if (lane == 0) cand[int64_t(node) * n_features + f] = FeatCand{c.loss, c.gl, c.hl, c.bin, c.dl};
   }
 }
@@ -214,7 +226,7 @@ __global__ __launch_bounds__(256) void evaluate_features_seg_kernel(
     const int32_t* __restrict__ n_nodes_dev, int32_t n_features, int32_t bin_stride,
     const int32_t* __restrict__ n_bins, const long long* __restrict__ node_sums,
     const int32_t* __restrict__ exps, int32_t exp_g_host, int32_t exp_h_host, Param p,
-    FeatCand* __restrict__ cand) {
+    const uint32_t* __restrict__ fmask, FeatCand* __restrict__ cand) {
   constexpr int BPL = 4;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int seg = lane >> 4, sub = lane & 15;
@@ -237,7 +249,7 @@ __global__ __launch_bounds__(256) void evaluate_features_seg_kernel(
       dg[j] = live && b < bin_stride ? hf[2 * b] : 0;
       dh[j] = live && b < bin_stride ? hf[2 * b + 1] : 0;
     }
-    const int nb = live ? n_bins[f] : 0;
+    const int nb = live && feature_allowed(fmask, node, f, n_features) ? n_bins[f] : 0;
     const long long gp = node_sums[2 * node], hp = node_sums[2 * node + 1];
     const double parent_gain = calc_gain(p, double(gp) * ug, double(hp) * uh);
     long long sg[BPL], sh[BPL];
@@ -322,7 +334,7 @@ __global__ __launch_bounds__(64 * kNodeWaves) void evaluate_nodes_kernel(
     const int32_t* __restrict__ n_nodes_dev, int32_t n_features, int32_t bin_stride,
     const int32_t* __restrict__ n_bins, const long long* __restrict__ node_sums,
     const int32_t* __restrict__ exps, int32_t exp_g_host, int32_t exp_h_host, Param p,
-    dp_split_record* __restrict__ out) {
+    const uint32_t* __restrict__ fmask, dp_split_record* __restrict__ out) {
   __shared__ Cand wave_best[kNodeWaves];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int32_t n_nodes = n_nodes_dev ? *n_nodes_dev : n_nodes_host;
@@ -344,7 +356,8 @@ __global__ __launch_bounds__(64 * kNodeWaves) void evaluate_nodes_kernel(
     for (int32_t f = wave; f < n_features; f += kNodeWaves) {  // wave-uniform
       if (f + kNodeWaves < n_features)
         load_feature<BPL>(hist, node, f + kNodeWaves, n_features, bin_stride, nxt);
-      const Cand c = feature_best<BPL>(cur, f, n_bins[f], gp, hp, parent_gain, ug, uh, p);
+      const int nb = feature_allowed(fmask, node, f, n_features) ? n_bins[f] : 0;
+      const Cand c = feature_best<BPL>(cur, f, nb, gp, hp, parent_gain, ug, uh, p);
       if (c.loss > -INFINITY && better(c, best)) best = c;
       cur = nxt;
     }
@@ -357,6 +370,117 @@ __global__ __launch_bounds__(64 * kNodeWaves) void evaluate_nodes_kernel(
       out[node] = make_record(r, p.gamma);
     }
     __syncthreads();  // wave_best is reused by the next node
+  }
+}
+
+// ---- column sampling (the draws are defined in sample.hpp) ---------------
+constexpr int kColThreads = 256;
+
+// The nth smallest key (nth >= 1, at most the candidate count) among the
+// features cand(f) admits: radix selection, eight bits at a time from the top,
+// one LDS histogram of the digit per pass.  Keys are distinct, so the result
+// is exactly the key of the nth candidate in key order.  Every thread of the
+// workgroup calls it and gets the same result.
+template <class Cand, class Key>
+__device__ uint32_t select_nth_key(int32_t n_features, uint32_t nth, Cand cand, Key key,
+                                   uint32_t* hist, uint32_t* pick) {
+  const int lane = threadIdx.x & 63;
+  uint32_t prefix = 0, pmask = 0, need = nth;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int i = threadIdx.x; i < 256; i += kColThreads) hist[i] = 0;
+    __syncthreads();
+    for (int32_t f = threadIdx.x; f < n_features; f += kColThreads) {
+      if (!cand(f)) continue;
+      const uint32_t k = key(f);
+      if ((k & pmask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (threadIdx.x < 64) {  // lane l holds digits 4l .. 4l + 3
+      uint32_t c[4], tot = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        c[j] = hist[4 * lane + j];
+        tot += c[j];
+      }
+      uint32_t incl = tot;
+      for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t v = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += v;
+      }
+      const uint32_t excl = incl - tot;
+      if (excl < need && need <= incl) {  // exactly one lane holds the digit
+        uint32_t run = excl;
+        for (int j = 0; j < 4; ++j) {
+          if (run + c[j] >= need) {
+            pick[0] = uint32_t(4 * lane + j);
+            pick[1] = need - run;
+            break;
+          }
+          run += c[j];
+        }
+      }
+    }
+    __syncthreads();
+    prefix |= pick[0] << shift;
+    pmask |= 0xffu << shift;
+    need = pick[1];
+    __syncthreads();  // pick and hist are rewritten by the next pass
+  }
+  return prefix;
+}
+
+// One workgroup per node of the level (looping over nodes): the node's
+// feature sample as a bit mask, masks[node][ceil(F / 32)].  The tree and level
+// stages are the same for every node of the level; each workgroup selects
+// them once, then the node stage per node.
+__global__ __launch_bounds__(kColThreads) void colsample_kernel(
+    const LevelNode* __restrict__ nodes, int32_t n_host, const int32_t* __restrict__ n_dev,
+    int32_t n_features, ColSample cs, int32_t depth, uint32_t* __restrict__ masks) {
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t pick[2];
+  const int32_t n_nodes = n_dev ? *n_dev : n_host;
+  if (int32_t(blockIdx.x) >= n_nodes) return;  // uniform per workgroup
+  const int lane = threadIdx.x & 63;
+  const uint64_t round = uint64_t(uint32_t(*cs.round));
+  const uint64_t out = uint64_t(uint32_t(cs.output)) << 32;
+  const int fbits = feature_bits(n_features);
+  const uint64_t p_tree = sample_prefix(cs.seed, kTreeStream, round, out);
+  const uint64_t p_level = sample_prefix(cs.seed, kLevelStream, round, out | uint32_t(depth));
+  const int32_t n1 = stage_keep(cs.bytree, n_features);
+  const int32_t n2 = stage_keep(cs.bylevel, n1);
+  const int32_t n3 = stage_keep(cs.bynode, n2);
+  auto all = [](int32_t) { return true; };
+  const uint32_t t1 =
+      n1 < n_features
+          ? select_nth_key(n_features, uint32_t(n1), all,
+                           [&](int32_t f) { return feature_key(p_tree, f, fbits); }, hist, pick)
+          : 0xffffffffu;
+  auto in_tree = [&](int32_t f) { return feature_key(p_tree, f, fbits) <= t1; };
+  const uint32_t t2 =
+      n2 < n1 ? select_nth_key(n_features, uint32_t(n2), in_tree,
+                               [&](int32_t f) { return feature_key(p_level, f, fbits); }, hist,
+                               pick)
+              : 0xffffffffu;
+  auto in_level = [&](int32_t f) { return in_tree(f) && feature_key(p_level, f, fbits) <= t2; };
+  const int64_t words = (n_features + 31) / 32;
+  for (int32_t node = blockIdx.x; node < n_nodes; node += gridDim.x) {
+    const uint64_t p_node =
+        sample_prefix(cs.seed, kNodeStream, round, out | uint32_t(nodes[node].nid));
+    const uint32_t t3 =
+        n3 < n2 ? select_nth_key(n_features, uint32_t(n3), in_level,
+                                 [&](int32_t f) { return feature_key(p_node, f, fbits); }, hist,
+                                 pick)
+                : 0xffffffffu;
+    uint32_t* m = masks + int64_t(node) * words;
+    for (int32_t base = int32_t(threadIdx.x >> 6) * 64; base < n_features; base += kColThreads) {
+      const int32_t f = base + lane;
+      const bool in = f < n_features && in_level(f) && feature_key(p_node, f, fbits) <= t3;
+      const unsigned long long b = __ballot(in);
+      if (lane == 0) {
+        m[base >> 5] = uint32_t(b);
+        if ((base >> 5) + 1 < words) m[(base >> 5) + 1] = uint32_t(b >> 32);
+      }
+    }
   }
 }
 
@@ -388,7 +512,7 @@ bool launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_node
                      int32_t n_features, int32_t bin_stride, const int32_t* n_bins,
                      const int64_t* node_sums, const int32_t* exps, int32_t exp_g, int32_t exp_h,
                      const dp_train_param& param, void* scratch, dp_split_record* out,
-                     hipStream_t s, bool select) {
+                     hipStream_t s, bool select, const uint32_t* fmask) {
   if (n_nodes <= 0) return true;
   need(bin_stride >= 1 && bin_stride <= kMaxBins, "split bin stride out of range");
   need(n_features >= 1, "split evaluation needs at least one feature");
@@ -400,13 +524,13 @@ bool launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_node
     const dim3 grid(n_nodes < 2048 ? n_nodes : 2048), block(64 * kNodeWaves);
     if (bin_stride <= 64)
       hipLaunchKernelGGL(evaluate_nodes_kernel<1>, grid, block, 0, s, h, n_nodes, n_nodes_dev,
-                         n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p, out);
+                         n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p, fmask, out);
     else if (bin_stride <= 128)
       hipLaunchKernelGGL(evaluate_nodes_kernel<2>, grid, block, 0, s, h, n_nodes, n_nodes_dev,
-                         n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p, out);
+                         n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p, fmask, out);
     else
       hipLaunchKernelGGL(evaluate_nodes_kernel<4>, grid, block, 0, s, h, n_nodes, n_nodes_dev,
-                         n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p, out);
+                         n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p, fmask, out);
     DP_HIP(hipGetLastError());
     return true;
   }
@@ -415,7 +539,7 @@ bool launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_node
     const int64_t items = int64_t(n_nodes) * ((n_features + kSegFeatures - 1) / kSegFeatures);
     hipLaunchKernelGGL(evaluate_features_seg_kernel, dim3(items < 2048 ? items : 2048), dim3(256),
                        0, s, h, n_nodes, n_nodes_dev, n_features, bin_stride, n_bins, sums, exps,
-                       exp_g, exp_h, p, cand);
+                       exp_g, exp_h, p, fmask, cand);
     DP_HIP(hipGetLastError());
     if (!select) return false;
     hipLaunchKernelGGL(select_splits_kernel, dim3(n_nodes < 1024 ? n_nodes : 1024),
@@ -431,11 +555,11 @@ bool launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_node
   if (bin_stride <= 128)
     hipLaunchKernelGGL(evaluate_features_kernel<2>, dim3(grid), block, 0, s, h, n_nodes,
                        n_nodes_dev, n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p,
-                       cand);
+                       fmask, cand);
   else
     hipLaunchKernelGGL(evaluate_features_kernel<4>, dim3(grid), block, 0, s, h, n_nodes,
                        n_nodes_dev, n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p,
-                       cand);
+                       fmask, cand);
   DP_HIP(hipGetLastError());
   if (!select) return false;
   hipLaunchKernelGGL(select_splits_kernel, dim3(n_nodes < 1024 ? n_nodes : 1024),
@@ -443,6 +567,18 @@ bool launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_node
                      double(param.gamma), out);
   DP_HIP(hipGetLastError());
   return true;
+}
+
+void launch_colsample(const LevelNode* nodes, int32_t n_host, const int32_t* n_dev,
+                      int32_t n_features, const ColSample& cs, int32_t depth, uint32_t* masks,
+                      hipStream_t s) {
+  if (n_host <= 0 || !cs.active()) return;
+  need(n_features >= 1, "column sampling needs at least one feature");
+  need(cs.round != nullptr, "column sampling needs the device round index");
+  const int grid = n_host < 2048 ? n_host : 2048;
+  hipLaunchKernelGGL(colsample_kernel, dim3(grid), dim3(kColThreads), 0, s, nodes, n_host, n_dev,
+                     n_features, cs, depth, masks);
+  DP_HIP(hipGetLastError());
 }
 
 }  // namespace dp

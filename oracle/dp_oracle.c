@@ -315,6 +315,14 @@ static double split_loss(const dpo_params* p, int64_t qgl, int64_t qhl, int64_t 
 void dpo_evaluate_split(const int64_t* hist, int64_t n_features, int32_t bin_stride,
                         const int32_t* n_bins, int64_t gp, int64_t hp, double unscale_g,
                         double unscale_h, const dpo_params* p, dpo_split* out) {
+  dpo_evaluate_split_masked(hist, n_features, bin_stride, n_bins, gp, hp, unscale_g, unscale_h, p,
+                            NULL, out);
+}
+
+void dpo_evaluate_split_masked(const int64_t* hist, int64_t n_features, int32_t bin_stride,
+                               const int32_t* n_bins, int64_t gp, int64_t hp, double unscale_g,
+                               double unscale_h, const dpo_params* p, const uint8_t* allowed,
+                               dpo_split* out) {
   dpo_split best;
   best.loss_chg = -INFINITY;
   best.feature = -1;
@@ -325,6 +333,7 @@ void dpo_evaluate_split(const int64_t* hist, int64_t n_features, int32_t bin_str
   best.hl = 0;
   const double parent_gain = dpo_calc_gain(p, (double)gp * unscale_g, (double)hp * unscale_h);
   for (int64_t f = 0; f < n_features; ++f) {
+    if (allowed && !allowed[f]) continue;  /* outside the node's column sample */
     const int64_t* hf = hist + 2 * f * bin_stride;
     const int32_t nb = n_bins[f];
     int64_t tg = 0, th = 0;
@@ -370,6 +379,104 @@ int64_t dpo_partition(uint32_t* ridx, int64_t begin, int64_t end, const uint8_t*
 }
 
 /* ------------------------------------------------------------------------ */
+/* Row and column sampling (subsample, colsample_by{tree,level,node}; the     */
+/* reference forwards these keys to the trainer unchanged,                    */
+/* native/class_native_training.cuh:30-31, :63).  Upstream draws from a      */
+/* global generator that cannot be reproduced here; this build fixes         */
+/* counter-based draws instead:                                              */
+/*   mix64      SplitMix64's output function (Steele, Lea & Flood 2014)      */
+/*   prefix     mix64(mix64(mix64(seed ^ stream << 56) ^ a) ^ b)             */
+/*   draw       upper 32 bits of mix64(prefix ^ index)                       */
+/* Rows: stream 1, a = round, b = output << 32; row r is kept iff            */
+/* draw < floor(subsample * 2^32), and a dropped row's (g, h) are zero for   */
+/* that tree (before the quantiser).  Columns: stages tree (stream 2,         */
+/* b = output << 32), level (stream 3, b = output << 32 | depth) and node     */
+/* (stream 4, b = output << 32 | node id), a = round.  A stage keeps          */
+/* n = max(1, (int)(fraction * m)) of its m candidates (the product in float, */
+/* as upstream's ColumnSampler forms it), those with the smallest keys,      */
+/* key(f) = draw with its low fbits bits replaced by f (fbits: bits of        */
+/* n_features - 1).  Each stage chooses among the previous stage's features. */
+/* Here the n smallest keys are found by sorting them.                       */
+/* ------------------------------------------------------------------------ */
+uint64_t dpo_mix64(uint64_t z) {
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+uint64_t dpo_sample_prefix(uint64_t seed, uint64_t stream, uint64_t a, uint64_t b) {
+  return dpo_mix64(dpo_mix64(dpo_mix64(seed ^ (stream << 56)) ^ a) ^ b);
+}
+
+uint32_t dpo_sample_draw(uint64_t prefix, uint64_t index) {
+  return (uint32_t)(dpo_mix64(prefix ^ index) >> 32);
+}
+
+int32_t dpo_stage_keep(float fraction, int32_t m) {
+  if (!(fraction < 1.0f)) return m;
+  float x = fraction * (float)m;
+  int32_t n = (int32_t)x;
+  return n < 1 ? 1 : n;
+}
+
+void dpo_sample_rows(const dpo_sampling* s, int64_t n, uint8_t* keep) {
+  if (!(s->subsample < 1.0f)) {
+    memset(keep, 1, (size_t)n);
+    return;
+  }
+  const uint64_t threshold = (uint64_t)ldexp((double)s->subsample, 32);
+  const uint64_t prefix = dpo_sample_prefix(s->seed, 1, (uint64_t)(uint32_t)s->round,
+                                            (uint64_t)(uint32_t)s->output << 32);
+  for (int64_t r = 0; r < n; ++r) keep[r] = (uint64_t)dpo_sample_draw(prefix, (uint64_t)r) < threshold;
+}
+
+static int cmp_u32(const void* a, const void* b) {
+  uint32_t x = *(const uint32_t*)a, y = *(const uint32_t*)b;
+  return (x > y) - (x < y);
+}
+
+static uint32_t feature_key(uint64_t prefix, int64_t f, int fbits) {
+  uint32_t low = fbits >= 32 ? 0xffffffffu : ((1u << fbits) - 1u);
+  return (dpo_sample_draw(prefix, (uint64_t)f) & ~low) | (uint32_t)f;
+}
+
+/* One stage: among the features allowed[] admits, keep the n smallest keys. */
+static void colsample_stage(uint64_t prefix, float fraction, int64_t n_features, int fbits,
+                            uint8_t* allowed, uint32_t* keys) {
+  int32_t m = 0;
+  for (int64_t f = 0; f < n_features; ++f)
+    if (allowed[f]) keys[m++] = feature_key(prefix, f, fbits);
+  const int32_t n = dpo_stage_keep(fraction, m);
+  if (n >= m) return;
+  qsort(keys, (size_t)m, sizeof(uint32_t), cmp_u32);
+  const uint32_t last = keys[n - 1];
+  for (int64_t f = 0; f < n_features; ++f)
+    if (allowed[f]) allowed[f] = feature_key(prefix, f, fbits) <= last;
+}
+
+void dpo_colsample(const dpo_sampling* s, int32_t depth, int32_t nid, int64_t n_features,
+                   uint8_t* allowed) {
+  memset(allowed, 1, (size_t)n_features);
+  if (!s || !(s->colsample_bytree < 1.0f || s->colsample_bylevel < 1.0f ||
+              s->colsample_bynode < 1.0f))
+    return;
+  int fbits = 0;
+  while (fbits < 31 && ((int64_t)1 << fbits) < n_features) ++fbits;
+  uint32_t* keys = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)(n_features > 0 ? n_features : 1));
+  if (!keys) return;
+  const uint64_t round = (uint64_t)(uint32_t)s->round;
+  const uint64_t out = (uint64_t)(uint32_t)s->output << 32;
+  colsample_stage(dpo_sample_prefix(s->seed, 2, round, out), s->colsample_bytree, n_features,
+                  fbits, allowed, keys);
+  colsample_stage(dpo_sample_prefix(s->seed, 3, round, out | (uint32_t)depth),
+                  s->colsample_bylevel, n_features, fbits, allowed, keys);
+  colsample_stage(dpo_sample_prefix(s->seed, 4, round, out | (uint32_t)nid), s->colsample_bynode,
+                  n_features, fbits, allowed, keys);
+  free(keys);
+}
+
+/* ------------------------------------------------------------------------ */
 /* One depth-wise tree.  Nodes are numbered as upstream's depth-wise driver   */
 /* allocates them: level by level, children of the k-th expanded node of a   */
 /* level get the next two ids (left, right), so left > node and right =      */
@@ -384,6 +491,15 @@ int dpo_grow_tree(const uint8_t* bins, int64_t n, int64_t n_features, const int3
                   const float* cut_values, int32_t missing_bin, const int32_t* qg,
                   const int32_t* qh, int32_t exp_g, int32_t exp_h, const dpo_params* p,
                   int32_t bin_stride, uint32_t* ridx, dpo_tree* t) {
+  return dpo_grow_tree_sampled(bins, n, n_features, cut_ptr, cut_values, missing_bin, qg, qh,
+                               exp_g, exp_h, p, bin_stride, NULL, ridx, t);
+}
+
+int dpo_grow_tree_sampled(const uint8_t* bins, int64_t n, int64_t n_features,
+                          const int32_t* cut_ptr, const float* cut_values, int32_t missing_bin,
+                          const int32_t* qg, const int32_t* qh, int32_t exp_g, int32_t exp_h,
+                          const dpo_params* p, int32_t bin_stride, const dpo_sampling* smp,
+                          uint32_t* ridx, dpo_tree* t) {
   const int32_t depth_cap = p->max_depth;
   if (depth_cap < 0 || depth_cap > 20) return -1;
   const int32_t cap = (int32_t)((1u << (depth_cap + 1)) - 1u);
@@ -412,6 +528,7 @@ int dpo_grow_tree(const uint8_t* bins, int64_t n, int64_t n_features, const int3
   uint32_t* scratch = (uint32_t*)xcalloc((size_t)n, 4);
   int32_t* level = (int32_t*)xcalloc((size_t)cap, 4);
   int32_t* next = (int32_t*)xcalloc((size_t)cap, 4);
+  uint8_t* allowed = (uint8_t*)xcalloc((size_t)n_features, 1);
 
   int64_t g0 = 0, h0 = 0;
   for (int64_t r = 0; r < n; ++r) { g0 += qg[r]; h0 += qh[r]; }
@@ -441,8 +558,9 @@ int dpo_grow_tree(const uint8_t* bins, int64_t n, int64_t n_features, const int3
       dpo_split s;
       int expand = 0;
       if (depth < depth_cap) {
-        dpo_evaluate_split(hist[nid], n_features, bin_stride, n_bins, t->sum_qg[nid],
-                           t->sum_qh[nid], ug, uh, p, &s);
+        dpo_colsample(smp, depth, nid, n_features, allowed);
+        dpo_evaluate_split_masked(hist[nid], n_features, bin_stride, n_bins, t->sum_qg[nid],
+                                  t->sum_qh[nid], ug, uh, p, allowed, &s);
         expand = s.valid && s.loss_chg > DPO_RT_EPS && s.loss_chg >= (double)p->gamma;
       }
       if (!expand) {
@@ -496,6 +614,7 @@ int dpo_grow_tree(const uint8_t* bins, int64_t n, int64_t n_features, const int3
   free(level);
   free(next);
   free(n_bins);
+  free(allowed);
   return 0;
 }
 

@@ -83,9 +83,36 @@ double dpo_calc_weight(const dpo_params* p, double g, double h);
 void dpo_evaluate_split(const int64_t* hist, int64_t n_features, int32_t bin_stride,
                         const int32_t* n_bins, int64_t gp, int64_t hp, double unscale_g,
                         double unscale_h, const dpo_params* p, dpo_split* out);
+/* Only features with allowed[f] != 0 are candidates (allowed NULL: all). */
+void dpo_evaluate_split_masked(const int64_t* hist, int64_t n_features, int32_t bin_stride,
+                               const int32_t* n_bins, int64_t gp, int64_t hp, double unscale_g,
+                               double unscale_h, const dpo_params* p, const uint8_t* allowed,
+                               dpo_split* out);
 int64_t dpo_partition(uint32_t* ridx, int64_t begin, int64_t end, const uint8_t* bins,
                       int64_t n_features, int32_t feature, int32_t split_bin,
                       int32_t default_left, int32_t missing_bin, uint32_t* scratch);
+
+/* ---- row and column sampling ------------------------------------------ */
+/* Counter-based draws (see dp_oracle.c): subsample keeps a row of one tree's */
+/* gradients iff its draw falls below floor(subsample * 2^32); the column     */
+/* stages keep the features with the smallest keys.                          */
+typedef struct {
+  uint64_t seed;
+  int32_t round;           /* boosting round index                          */
+  int32_t output;          /* the tree's output (class) index               */
+  float subsample, colsample_bytree, colsample_bylevel, colsample_bynode;
+} dpo_sampling;
+
+uint64_t dpo_mix64(uint64_t z);
+uint64_t dpo_sample_prefix(uint64_t seed, uint64_t stream, uint64_t a, uint64_t b);
+uint32_t dpo_sample_draw(uint64_t prefix, uint64_t index);
+int32_t dpo_stage_keep(float fraction, int32_t m);
+/* keep[r] = 1 when row r's gradient pair is kept for tree (round, output). */
+void dpo_sample_rows(const dpo_sampling* s, int64_t n, uint8_t* keep);
+/* allowed[f] = 1 when feature f is a split candidate at node `nid` of depth */
+/* `depth` (the nested tree, level and node stages).                          */
+void dpo_colsample(const dpo_sampling* s, int32_t depth, int32_t nid, int64_t n_features,
+                   uint8_t* allowed);
 
 /* ---- one tree ----------------------------------------------------------- */
 typedef struct {
@@ -100,6 +127,12 @@ int dpo_grow_tree(const uint8_t* bins, int64_t n, int64_t n_features, const int3
                   const float* cut_values, int32_t missing_bin, const int32_t* qg,
                   const int32_t* qh, int32_t exp_g, int32_t exp_h, const dpo_params* p,
                   int32_t bin_stride, uint32_t* ridx, dpo_tree* out);
+/* As dpo_grow_tree with column sampling (s NULL: every feature everywhere). */
+int dpo_grow_tree_sampled(const uint8_t* bins, int64_t n, int64_t n_features,
+                          const int32_t* cut_ptr, const float* cut_values, int32_t missing_bin,
+                          const int32_t* qg, const int32_t* qh, int32_t exp_g, int32_t exp_h,
+                          const dpo_params* p, int32_t bin_stride, const dpo_sampling* s,
+                          uint32_t* ridx, dpo_tree* out);
 void dpo_tree_free(dpo_tree* t);
 void dpo_tree_update_margin(const dpo_tree* t, const uint32_t* ridx, float* margin,
                             int64_t stride);

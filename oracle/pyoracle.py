@@ -29,6 +29,12 @@ class Split(Structure):
                 ("default_left", c_int32), ("valid", c_int32), ("gl", c_int64), ("hl", c_int64)]
 
 
+class Sampling(Structure):
+    _fields_ = [("seed", ctypes.c_uint64), ("round", c_int32), ("output", c_int32),
+                ("subsample", c_float), ("colsample_bytree", c_float),
+                ("colsample_bylevel", c_float), ("colsample_bynode", c_float)]
+
+
 class Tree(Structure):
     _fields_ = [("n_nodes", c_int32)] + [
         (n, POINTER(c_int32)) for n in ("left", "right", "parent", "feature", "split_bin",
@@ -78,6 +84,23 @@ def load():
         lib.dpo_grow_tree.argtypes = [P, c_int64, c_int64, P, P, c_int32, P, P, c_int32, c_int32,
                                       POINTER(Params), c_int32, P, POINTER(Tree)]
         lib.dpo_grow_tree.restype = c_int32
+        lib.dpo_grow_tree_sampled.argtypes = [P, c_int64, c_int64, P, P, c_int32, P, P, c_int32,
+                                              c_int32, POINTER(Params), c_int32,
+                                              POINTER(Sampling), P, POINTER(Tree)]
+        lib.dpo_grow_tree_sampled.restype = c_int32
+        lib.dpo_evaluate_split_masked.argtypes = [P, c_int64, c_int32, P, c_int64, c_int64,
+                                                  c_double, c_double, POINTER(Params), P,
+                                                  POINTER(Split)]
+        lib.dpo_mix64.argtypes = [ctypes.c_uint64]
+        lib.dpo_mix64.restype = ctypes.c_uint64
+        lib.dpo_sample_prefix.argtypes = [ctypes.c_uint64] * 4
+        lib.dpo_sample_prefix.restype = ctypes.c_uint64
+        lib.dpo_sample_draw.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
+        lib.dpo_sample_draw.restype = ctypes.c_uint32
+        lib.dpo_stage_keep.argtypes = [c_float, c_int32]
+        lib.dpo_stage_keep.restype = c_int32
+        lib.dpo_sample_rows.argtypes = [POINTER(Sampling), c_int64, P]
+        lib.dpo_colsample.argtypes = [POINTER(Sampling), c_int32, c_int32, c_int64, P]
         lib.dpo_tree_free.argtypes = [POINTER(Tree)]
         lib.dpo_tree_update_margin.argtypes = [POINTER(Tree), P, P, c_int64]
         lib.dpo_predict_tree.argtypes = [POINTER(Tree), P]
@@ -209,17 +232,58 @@ def partition(ridx, begin, end, bins, feature, split_bin, default_left, missing_
     return ridx, nl
 
 
-def grow_tree(bins, cut_ptr, cuts, missing_bin, qg, qh, exp_g, exp_h, p, bin_stride=256):
-    """One tree -> (dict of node arrays, final ridx)."""
+def sampling(seed=0, round_=0, output=0, subsample=1.0, bytree=1.0, bylevel=1.0, bynode=1.0):
+    return Sampling(seed, round_, output, subsample, bytree, bylevel, bynode)
+
+
+def mix64(z):
+    return load().dpo_mix64(z)
+
+
+def sample_rows(smp, n):
+    keep = np.zeros(n, dtype=np.uint8)
+    load().dpo_sample_rows(ctypes.byref(smp), n, _p(keep))
+    return keep.astype(bool)
+
+
+def colsample(smp, depth, nid, n_features):
+    allowed = np.zeros(n_features, dtype=np.uint8)
+    load().dpo_colsample(ctypes.byref(smp), depth, nid, n_features, _p(allowed))
+    return allowed.astype(bool)
+
+
+def stage_keep(fraction, m):
+    return load().dpo_stage_keep(fraction, m)
+
+
+def evaluate_split_masked(hist_, n_bins, gp, hp, exp_g, exp_h, p, allowed):
+    hist_ = np.ascontiguousarray(hist_, dtype=np.int64)
+    f, stride, _ = hist_.shape
+    s = Split()
+    a = np.ascontiguousarray(allowed, dtype=np.uint8)
+    load().dpo_evaluate_split_masked(_p(hist_), f, stride,
+                                     _p(np.ascontiguousarray(n_bins, dtype=np.int32)), int(gp),
+                                     int(hp), unscale(exp_g), unscale(exp_h), ctypes.byref(p),
+                                     _p(a), ctypes.byref(s))
+    return {"loss_chg": s.loss_chg, "feature": s.feature, "bin": s.bin,
+            "default_left": s.default_left, "valid": s.valid, "gl": s.gl, "hl": s.hl}
+
+
+def grow_tree(bins, cut_ptr, cuts, missing_bin, qg, qh, exp_g, exp_h, p, bin_stride=256,
+              smp=None):
+    """One tree -> (dict of node arrays, final ridx); smp: column sampling (Sampling)."""
     bins = np.ascontiguousarray(bins, dtype=np.uint8)
     n, f = bins.shape
     ridx = np.arange(n, dtype=np.uint32)
     t = Tree()
-    rc = load().dpo_grow_tree(_p(bins), n, f, _p(np.ascontiguousarray(cut_ptr, dtype=np.int32)),
-                              _p(np.ascontiguousarray(cuts, dtype=np.float32)), missing_bin,
-                              _p(np.ascontiguousarray(qg, dtype=np.int32)),
-                              _p(np.ascontiguousarray(qh, dtype=np.int32)), exp_g, exp_h,
-                              ctypes.byref(p), bin_stride, _p(ridx), ctypes.byref(t))
+    rc = load().dpo_grow_tree_sampled(_p(bins), n, f,
+                                      _p(np.ascontiguousarray(cut_ptr, dtype=np.int32)),
+                                      _p(np.ascontiguousarray(cuts, dtype=np.float32)),
+                                      missing_bin, _p(np.ascontiguousarray(qg, dtype=np.int32)),
+                                      _p(np.ascontiguousarray(qh, dtype=np.int32)), exp_g, exp_h,
+                                      ctypes.byref(p), bin_stride,
+                                      ctypes.byref(smp) if smp is not None else None, _p(ridx),
+                                      ctypes.byref(t))
     assert rc == 0
     k = t.n_nodes
 
@@ -268,10 +332,13 @@ def predict_tree(tree, x):
 
 
 def train(bins, cut_ptr, cuts, missing_bin, objective, labels, n_classes, p, rounds,
-          base_margin=0.0, bin_stride=256, injected=None):
+          base_margin=0.0, bin_stride=256, injected=None, sample=None):
     """Whole booster on the CPU: per round gradients -> quantise -> K trees -> margins.
 
     injected: optional callable(round) -> (g [n,K], h [n,K]) replacing the objective.
+    sample: optional dict(seed, subsample, bytree, bylevel, bynode) of row and column
+    sampling: tree (round r, output k) zeroes the (g, h) of its dropped rows before the
+    quantiser and restricts each node's split candidates to its column sample.
     Returns (trees, margins, per-round gradients)."""
     n = bins.shape[0]
     margin = np.full((n, n_classes), base_margin, dtype=np.float32)
@@ -283,10 +350,22 @@ def train(bins, cut_ptr, cuts, missing_bin, objective, labels, n_classes, p, rou
             g, h = gradients(objective, margin if n_classes > 1 else margin[:, 0], labels,
                              n_classes)
         grads.append((g.copy(), h.copy()))
+        g = np.array(g, dtype=np.float32).reshape(n, -1)
+        h = np.array(h, dtype=np.float32).reshape(n, -1)
+        smps = [None] * n_classes
+        if sample is not None:
+            for k in range(n_classes):
+                smps[k] = sampling(sample.get("seed", 0), r, k, sample.get("subsample", 1.0),
+                                   sample.get("bytree", 1.0), sample.get("bylevel", 1.0),
+                                   sample.get("bynode", 1.0))
+                keep = sample_rows(smps[k], n)
+                g[~keep, k] = 0.0
+                h[~keep, k] = 0.0
         q = quantise(g, h)
         for k in range(n_classes):
             eg, eh, qg, qh = q[k]
-            tree, ridx = grow_tree(bins, cut_ptr, cuts, missing_bin, qg, qh, eg, eh, p, bin_stride)
+            tree, ridx = grow_tree(bins, cut_ptr, cuts, missing_bin, qg, qh, eg, eh, p, bin_stride,
+                                   smp=smps[k])
             col = np.ascontiguousarray(margin[:, k])
             for nid in range(len(tree["left"])):
                 if tree["left"][nid] == -1:

@@ -151,12 +151,16 @@ def test_plan_pin_and_existing_output(tmp_path):
 
 
 @pytest.mark.gpu
-def test_fit_matches_in_process_training(tmp_path, dp, device):
+@pytest.mark.parametrize("sampling", [{}, {"subsample": 0.8, "colsample_bynode": 0.5,
+                                           "colsample_bytree": 0.9, "seed": 12}])
+def test_fit_matches_in_process_training(tmp_path, dp, device, sampling):
+    """dp_model_train fit writes the model the in-process API trains, also with the plan's
+    row and column sampling keys (which the reference forwards to the library)."""
     import torch
 
     x, y, ds = write_dataset(tmp_path)
     hp = {"rounds": 4, "max_depth": 4, "eta": 0.5, "max_bin": 64, "lambda": 2, "alpha": 0.25,
-          "min_child_weight": 0.5}
+          "min_child_weight": 0.5, **sampling}
     plan, pin = write_plan(tmp_path, ds, hp)
     out = tmp_path / "run"
     print(f"[cli] fit {ds['rows']} x {ds['features']} K={ds['classes']}", flush=True)
@@ -178,7 +182,7 @@ def test_fit_matches_in_process_training(tmp_path, dp, device):
     params = {"objective": "multi:softmax", "num_class": 3, "tree_method": "hist",
               "device": "cuda:0", "max_bin": 64, "max_depth": 4, "eta": 0.5, "lambda": 2,
               "alpha": 0.25, "gamma": 0, "min_child_weight": 0.5, "base_score": "[0,0,0]",
-              "boost_from_average": 0, "seed": 0}
+              "boost_from_average": 0, "seed": 0, **sampling}
     bst = dp.Booster(params, [dtrain])
     for r in range(4):
         bst.update(dtrain, r)

@@ -20,11 +20,16 @@ TREE_KEYS_BITS = ["split_condition", "base_weight", "sum_hess"]
 
 
 def _train_both(dp, oracle, device, config, n, f, objective, k, p, rounds, seed, injected=False,
-                max_bin=256, base_score=None, extra=None, mutate=None):
+                max_bin=256, base_score=None, extra=None, mutate=None, sample=None,
+                values_labels=None):
     import torch
     from dpgbdt import ops
 
-    values, labels, g, h = ops.synth(config, n, seed, n_features=f, want_grad=injected)
+    if values_labels is not None:
+        values, labels = values_labels
+        g = h = None
+    else:
+        values, labels, g, h = ops.synth(config, n, seed, n_features=f, want_grad=injected)
     if mutate is not None:
         values = mutate(values)
     obj_name = {0: "binary:logistic", 1: "multi:softmax", 2: "reg:squarederror"}[objective]
@@ -37,6 +42,12 @@ def _train_both(dp, oracle, device, config, n, f, objective, k, p, rounds, seed,
         params["num_class"] = k
     if base_score is not None:
         params["base_score"] = base_score
+    if sample is not None:  # row / column sampling: booster keys and the oracle's draws
+        params["seed"] = sample.get("seed", 0)
+        for key, name in (("subsample", "subsample"), ("bytree", "colsample_bytree"),
+                          ("bylevel", "colsample_bylevel"), ("bynode", "colsample_bynode")):
+            if key in sample:
+                params[name] = sample[key]
     params.update(extra or {})
     bst = dp.Booster(params, [dtrain])
     gpu_positions = []
@@ -66,7 +77,8 @@ def _train_both(dp, oracle, device, config, n, f, objective, k, p, rounds, seed,
         base_margin = float(base_score)
     o_trees, o_margin, _ = oracle.train(bins, cut_ptr, cuts, mb, objective, labels.cpu().numpy(),
                                         k, op, rounds, base_margin=base_margin,
-                                        bin_stride=int(np.diff(cut_ptr).max()), injected=inj)
+                                        bin_stride=int(np.diff(cut_ptr).max()), injected=inj,
+                                        sample=sample)
     return bst, x, o_trees, o_margin, gpu_positions, n
 
 
@@ -659,3 +671,109 @@ def test_strided_label_interface_is_refused(dp, device):
     col = torch.zeros((n, 1), dtype=torch.float32, device=device)
     assert set_labels(col.data_ptr(), [4, 4]) == 0
     assert ctypes.sizeof(ctypes.c_float) == 4
+
+
+
+SAMPLING_CASES = {
+    "subsample": {"seed": 7, "subsample": 0.8},
+    "bytree": {"seed": 7, "bytree": 0.5},
+    "bynode": {"seed": 7, "bynode": 0.5},
+    "bylevel": {"seed": 3, "bylevel": 0.6},
+    "all": {"seed": 11, "subsample": 0.7, "bytree": 0.8, "bylevel": 0.7, "bynode": 0.6},
+}
+
+
+@pytest.mark.parametrize("case", list(SAMPLING_CASES))
+def test_sampling_parity(dp, oracle, device, case):
+    """Row and column sampling (subsample, colsample_by{tree,level,node}, seed) train the
+    same trees, row partitions and margins as the oracle's booster, round after round
+    (the draws depend on the round, read by replayed round graphs from device memory)."""
+    p = {"max_depth": 6, "eta": 0.3}
+    sample = SAMPLING_CASES[case]
+    print(f"[booster] sampling {case}: C2 40000 x 28, depth 6, 4 rounds", flush=True)
+    bst, x, o_trees, o_margin, pos, n = _train_both(dp, oracle, device, 2, 40000, 28, 0, 1, p, 4,
+                                                    20261202, sample=sample)
+    _compare(bst, o_trees, o_margin, pos, n, 1)
+    cfg = json.loads(bst.save_config())
+    tp = cfg["learner"]["gradient_booster"]["updater"][0]["train_param"]
+    assert tp["subsample"] == str(sample.get("subsample", 1))
+
+
+@pytest.mark.parametrize("shape", ["few_features", "softmax", "present_value", "level_synced",
+                                   "injected"])
+def test_sampling_parity_paths(dp, oracle, device, shape):
+    """Sampling on the other evaluation and growth paths: at most 16 features (one workgroup
+    per node), ten concurrent class trees (each its own draws), present-value histograms of
+    a mostly-missing matrix, level-synced growth (depth 17), and caller gradients."""
+    import torch
+
+    if shape == "few_features":
+        p, sample = {"max_depth": 6, "eta": 0.3}, {"seed": 5, "subsample": 0.75, "bytree": 0.5,
+                                                    "bynode": 0.75}
+        args = (1, 10000, 8, 0, 1, p, 3, 20261201)
+        kw = {}
+    elif shape == "softmax":
+        p, sample = {"max_depth": 4, "eta": 0.3}, {"seed": 9, "subsample": 0.8, "bynode": 0.5}
+        args = (4, 2000, 784, 1, 10, p, 2, 20261204)
+        kw = {}
+    elif shape == "present_value":
+        p, sample = {"max_depth": 7, "eta": 0.3}, {"seed": 2, "subsample": 0.9, "bylevel": 0.5,
+                                                    "bynode": 0.8}
+        args = (5, 6000, 120, 2, 1, p, 3, 20261205)
+        kw = {"max_bin": 64, "extra": {"dp_sparse_hist": 1}}
+    elif shape == "level_synced":
+        p, sample = {"max_depth": 17, "eta": 0.3, "min_child_weight": 0.0}, \
+            {"seed": 4, "subsample": 0.9, "bytree": 0.9, "bynode": 0.7}
+        rng = np.random.default_rng(5)
+        xv = rng.random((1000, 8), dtype=np.float32)
+        yv = (rng.random(1000) < 0.5).astype(np.float32)
+        args = (1, 1000, 8, 0, 1, p, 2, 0)
+        kw = {"values_labels": (torch.as_tensor(xv, device=device),
+                                torch.as_tensor(yv, device=device))}
+    else:
+        p, sample = {"max_depth": 8, "eta": 0.3}, {"seed": 6, "subsample": 0.5, "bytree": 0.5}
+        args = (3, 30000, 128, 2, 1, p, 2, 20261203)
+        kw = {"injected": True}
+    print(f"[booster] sampling path {shape}", flush=True)
+    bst, x, o_trees, o_margin, pos, n = _train_both(dp, oracle, device, *args, sample=sample, **kw)
+    _compare(bst, o_trees, o_margin, pos, n, args[4])
+
+
+def test_sampled_graph_replays_equal_direct_launches(dp, device):
+    """With sampling on, rounds replayed from cached graphs equal direct launches (each round
+    stores its index for the sampling kernels before the replay)."""
+    from dpgbdt import ops
+
+    values, labels, _, _ = ops.synth(2, 20000, 5, n_features=28)
+    models = []
+    for graphs in (0, 1):
+        dtrain = dp.DMatrix(values, labels)
+        bst = dp.Booster({"objective": "binary:logistic", "max_depth": 5, "subsample": 0.7,
+                          "colsample_bynode": 0.5, "seed": 3, "dp_graphs": graphs}, [dtrain])
+        for r in range(6):
+            bst.update(dtrain, r)
+        models.append(bst.save_raw())
+    assert models[0] == models[1]
+
+
+def test_max_bin_is_not_changed_silently(dp, device):
+    """max_bin above 256 is refused (bins are uint8); the saved configuration reports the bins
+    actually used: 256 on a matrix without missing values, 255 with them (byte 255 marks a
+    missing value)."""
+    import torch
+    from dpgbdt import ops
+
+    values, labels, _, _ = ops.synth(1, 5000, 7)
+    dtrain = dp.DMatrix(values, labels)
+    bst = dp.Booster({"objective": "binary:logistic", "max_bin": 1024}, [dtrain])
+    with pytest.raises(dp.DPError, match="max_bin above 256"):
+        bst.update(dtrain, 0)
+    for holes, used in ((False, "256"), (True, "255")):
+        v = values.clone()
+        if holes:
+            v[::3, 2] = float("nan")
+        d = dp.DMatrix(v, labels)
+        b = dp.Booster({"objective": "binary:logistic", "max_bin": 256, "max_depth": 3}, [d])
+        b.update(d, 0)
+        cfg = json.loads(b.save_config())
+        assert cfg["learner"]["gradient_booster"]["updater"][0]["hist_train_param"]["max_bin"] == used

@@ -198,9 +198,10 @@ def test_gain_and_weight_minimise_objective(oracle, lam, alpha, mcw):
         assert abs(oracle.calc_weight(p, G, H) - res.x) < 1e-5
 
 
-def _brute_force_split(bins, qg, qh, rows, nb_per_feature, mb, ug, uh, p):
+def _brute_force_split(bins, qg, qh, rows, nb_per_feature, mb, ug, uh, p, allowed=None):
     """Every (feature, bin, missing side) from raw row selections; tie rule:
-    larger loss, then lower feature, then lower bin, then missing-right."""
+    larger loss, then lower feature, then lower bin, then missing-right.
+    allowed: optional boolean mask of the candidate features."""
     lam, alpha, mcw = float(p.lambda_), float(p.alpha), float(p.min_child_weight)
 
     def gain(G, H):
@@ -215,6 +216,8 @@ def _brute_force_split(bins, qg, qh, rows, nb_per_feature, mb, ug, uh, p):
     parent = gain(GP * ug, HP * uh)
     best = (-np.inf, None)
     for f in range(bins.shape[1]):
+        if allowed is not None and not allowed[f]:
+            continue
         col = bins[rows, f].astype(np.int64)
         miss = col == mb
         for b in range(nb_per_feature[f]):
@@ -263,8 +266,9 @@ def test_partition_is_stable(oracle):
         np.testing.assert_array_equal(out[1500:], ridx[1500:])
 
 
-def _reference_tree(bins, qg, qh, cut_ptr, mb, ug, uh, p):
-    """Independent depth-wise builder on raw rows (no histograms, no subtraction)."""
+def _reference_tree(bins, qg, qh, cut_ptr, mb, ug, uh, p, allowed_fn=None):
+    """Independent depth-wise builder on raw rows (no histograms, no subtraction).
+    allowed_fn(depth, nid): optional candidate-feature mask of each node."""
     nbf = np.diff(cut_ptr).astype(np.int32)
     nodes = [{"rows": np.arange(bins.shape[0], dtype=np.uint32), "depth": 0}]
     out = []
@@ -275,7 +279,9 @@ def _reference_tree(bins, qg, qh, cut_ptr, mb, ug, uh, p):
             nd = nodes[nid]
             rec = {"nid": nid, "left": -1}
             if nd["depth"] < p.max_depth:
-                key, val = _brute_force_split(bins, qg, qh, nd["rows"], nbf, mb, ug, uh, p)
+                allowed = allowed_fn(nd["depth"], nid) if allowed_fn else None
+                key, val = _brute_force_split(bins, qg, qh, nd["rows"], nbf, mb, ug, uh, p,
+                                              allowed)
                 if val is not None and key[0] > 1e-6 and key[0] >= p.gamma:
                     f, b, dl, gl, hl = val
                     col = bins[nd["rows"], f].astype(np.int64)
@@ -346,3 +352,140 @@ def test_strided_arguments_stay_alive(oracle):
     np.testing.assert_array_equal(strided, ref)
     np.testing.assert_array_equal(strided[:, :, 0].sum(axis=1),
                                   np.full(f, q[:, 0].astype(np.int64).sum()))
+
+
+# ---- row and column sampling ------------------------------------------------
+def test_mix64_is_splitmix64(oracle):
+    """The draws' mixing function is SplitMix64's output function: seeded with 0,
+    SplitMix64 (state += 0x9E3779B97F4A7C15, then the output function) yields
+    0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F."""
+    golden = 0x9E3779B97F4A7C15
+    got = [oracle.mix64((i * golden) % 2**64) for i in range(3)]
+    assert got == [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F]
+
+
+@pytest.mark.parametrize("subsample", [0.3, 0.8])
+def test_row_sampling_fraction_and_streams(oracle, subsample):
+    """Kept rows are a Bernoulli(subsample) sample: the kept share is within 5 sigma of
+    subsample, rounds and outputs draw independent samples (overlap ~ subsample^2), and
+    subsample 1 keeps every row."""
+    n = 200_000
+    a = oracle.sample_rows(oracle.sampling(7, 0, 0, subsample), n)
+    sigma = np.sqrt(subsample * (1 - subsample) / n)
+    assert abs(a.mean() - subsample) < 5 * sigma
+    for other in (oracle.sampling(7, 1, 0, subsample), oracle.sampling(7, 0, 1, subsample),
+                  oracle.sampling(8, 0, 0, subsample)):
+        b = oracle.sample_rows(other, n)
+        assert abs((a & b).mean() - subsample ** 2) < 6 * np.sqrt(subsample ** 2 / n)
+    assert oracle.sample_rows(oracle.sampling(7, 0, 0, 1.0), 1000).all()
+    # the same key draws the same sample
+    np.testing.assert_array_equal(a, oracle.sample_rows(oracle.sampling(7, 0, 0, subsample), n))
+
+
+def test_stage_count_rule(oracle):
+    """n = max(1, (int)(fraction * m)) with the product formed in float, as upstream's
+    ColumnSampler computes it: 0.7 of 10 keeps 7 (0.7f * 10 rounds to 7.0f), 0.7 of 3
+    keeps 2, 0.01 of 10 keeps 1, 1.0 keeps all."""
+    assert oracle.stage_keep(0.7, 10) == 7
+    assert oracle.stage_keep(0.7, 3) == 2
+    assert oracle.stage_keep(0.01, 10) == 1
+    assert oracle.stage_keep(0.5, 1000) == 500
+    assert oracle.stage_keep(1.0, 37) == 37
+    for m in range(1, 300):
+        for frac in (0.1, 0.25, 0.3, 0.5, 0.7, 0.9):
+            x = np.float32(frac) * np.float32(m)
+            assert oracle.stage_keep(frac, m) == max(1, int(x))
+
+
+@pytest.mark.parametrize("f", [1, 7, 28, 128, 1000])
+def test_colsample_counts_and_nesting(oracle, f):
+    """Each stage keeps exactly its count, chosen among the previous stage's features:
+    tree set (bytree of all), level set (bylevel of the tree set, per depth) and node set
+    (bynode of the level set, per node id)."""
+    bt, bl, bn = 0.7, 0.6, 0.5
+    tree = oracle.colsample(oracle.sampling(3, 4, 1, 1.0, bt), 0, 0, f)
+    n1 = oracle.stage_keep(bt, f)
+    assert tree.sum() == n1
+    for depth in (0, 1, 5):
+        level = oracle.colsample(oracle.sampling(3, 4, 1, 1.0, bt, bl), depth, 99, f)
+        n2 = oracle.stage_keep(bl, n1)
+        assert level.sum() == n2 and not (level & ~tree).any()
+        for nid in (0, 3, 1000):
+            node = oracle.colsample(oracle.sampling(3, 4, 1, 1.0, bt, bl, bn), depth, nid, f)
+            assert node.sum() == oracle.stage_keep(bn, n2)
+            assert not (node & ~level).any()
+
+
+def test_colsample_is_uniform(oracle):
+    """Over 4,000 node draws each of 40 features is kept with frequency n/F (chi-square,
+    39 degrees of freedom, far tail), and different nodes draw different sets."""
+    f, draws = 40, 4000
+    counts = np.zeros(f)
+    sets = set()
+    for nid in range(draws):
+        m = oracle.colsample(oracle.sampling(11, 2, 0, 1.0, 1.0, 1.0, 0.25), 3, nid, f)
+        counts += m
+        sets.add(m.tobytes())
+    expected = draws * 10 / f
+    chi2 = ((counts - expected) ** 2 / expected).sum()
+    assert chi2 < 100  # 39 dof: P(chi2 > 100) < 1e-6
+    assert len(sets) > draws * 0.99
+
+
+def test_sampled_tree_matches_independent_builder(oracle):
+    """A tree grown with row and column sampling equals the independent raw-row builder
+    given the same dropped rows (zero gradient pairs) and, at every node, the same
+    candidate features (the oracle's column sample of that node's depth and id)."""
+    x, bins, cut_ptr, cuts, mb, qg, qh, eg, eh = _quantised_case(oracle, n=500, f=6, nb=8,
+                                                                  seed=31)
+    smp = oracle.sampling(5, 2, 1, 0.7, 0.85, 0.8, 0.5)
+    keep = oracle.sample_rows(smp, bins.shape[0])
+    assert 0 < keep.sum() < keep.size
+    qg = np.where(keep, qg, 0).astype(np.int32)
+    qh = np.where(keep, qh, 0).astype(np.int32)
+    p = oracle.params(max_depth=4, eta=0.5, min_child_weight=0.0)
+    tree, ridx = oracle.grow_tree(bins, cut_ptr, cuts, mb, qg, qh, eg, eh, p, bin_stride=8,
+                                  smp=smp)
+    ref, nodes = _reference_tree(bins, qg, qh, cut_ptr, mb, oracle.unscale(eg),
+                                 oracle.unscale(eh), p,
+                                 lambda depth, nid: oracle.colsample(smp, depth, nid, 6))
+    assert len(ref) == len(tree["left"]) and len(ref) > 7
+    used = set()
+    for r in ref:
+        nid = r["nid"]
+        assert tree["left"][nid] == r["left"]
+        if r["left"] != -1:
+            assert (tree["feature"][nid], tree["split_bin"][nid], tree["default_left"][nid]) == \
+                (r["feature"], r["bin"], r["dl"])
+            used.add(r["feature"])
+    unsampled, _ = oracle.grow_tree(bins, cut_ptr, cuts, mb, qg, qh, eg, eh, p, bin_stride=8)
+    assert not (np.array_equal(unsampled["feature"], tree["feature"]) and
+                np.array_equal(unsampled["left"], tree["left"])), "sampling changed nothing"
+
+
+def test_booster_row_sampling_zeroes_dropped_pairs(oracle):
+    """train(sample=subsample) equals train on caller gradients whose dropped rows are zero
+    before the quantiser (round by round, the tree's own sample)."""
+    x, bins, cut_ptr, cuts, mb, qg, qh, eg, eh = _quantised_case(oracle, n=3000, f=5, nb=16,
+                                                                  seed=41)
+    rng = np.random.default_rng(2)
+    g = rng.normal(size=3000).astype(np.float32)
+    h = rng.uniform(0.1, 0.3, size=3000).astype(np.float32)
+    p = oracle.params(max_depth=4, eta=0.3)
+    inj = lambda r: (np.roll(g, r)[:, None], np.roll(h, r)[:, None])  # noqa: E731
+    sample = {"seed": 4, "subsample": 0.6}
+    t1, m1, _ = oracle.train(bins, cut_ptr, cuts, mb, 3, None, 1, p, 3, bin_stride=16,
+                             injected=inj, sample=sample)
+
+    def masked(r):
+        keep = oracle.sample_rows(oracle.sampling(4, r, 0, 0.6), 3000)
+        gr, hr = inj(r)
+        return np.where(keep[:, None], gr, 0).astype(np.float32), \
+            np.where(keep[:, None], hr, 0).astype(np.float32)
+
+    t2, m2, _ = oracle.train(bins, cut_ptr, cuts, mb, 3, None, 1, p, 3, bin_stride=16,
+                             injected=masked)
+    for a, b in zip(t1, t2):
+        for key in ("left", "feature", "split_bin", "sum_qg", "sum_qh"):
+            np.testing.assert_array_equal(a[key], b[key])
+    np.testing.assert_array_equal(m1.view(np.uint32), m2.view(np.uint32))
