@@ -166,7 +166,7 @@ def cpu_leg(sample, args):
     import pyoracle
 
     bins, qg, qh, stride = sample[:4]
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    threads = host_threads()
     rows, f = bins.shape
     pyoracle.hist_parallel(bins[: min(rows, 4096)], qg[:4096], qh[:4096], stride, -1, threads)
     t0 = time.perf_counter()
@@ -185,36 +185,59 @@ def cpu_leg(sample, args):
             "hardware_concurrency": os.cpu_count(),
             "kind": "port",
             "sample": f"oracle dpo_hist_parallel root pass over the first {rows} rows x {f} "
-                      f"features of the C3 matrix, {reps} passes, {el:.1f} s",
+                      f"features of the C3 matrix (a bounded sample of its 10M rows), "
+                      f"{reps} passes, {el:.1f} s",
+            "sample_rows": rows,
             "gbs": algorithmic_hist_bytes(rows, f, 256) / per_pass / 1e9}
 
 
-def cpu_trees_leg(ops, name, max_rounds):
-    """The oracle's single-threaded booster (same cuts, bins and tree rules) on the
-    configuration's data: trees/s over at most `max_rounds` rounds."""
+def host_threads():
+    """Threads of the CPU legs: OMP_NUM_THREADS when set, else the affinity count."""
+    env = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return env or len(os.sched_getaffinity(0))
+
+
+def cpu_trees_leg(torch, ops, name, max_rounds, threads):
+    """The oracle's booster (same cuts, bins, sampling and tree rules as the GPU path,
+    OpenMP over `threads` host threads; results identical for any count) on the
+    configuration's data: trees/s over at most `max_rounds` rounds.  The cuts and uint8
+    bins come from the GPU (bit-identical to the oracle's, which the GPU tests pin) so
+    the timed CPU work is the boosting rounds, as on the GPU side."""
     import numpy as np
     import pyoracle
 
     config, n, rounds, depth, eta, objective, max_bin, injected = TREE_CONFIGS[name]
     rounds = min(rounds, max_rounds)
-    values, labels, _, _ = ops.synth(config, n, SEED + config)
-    x = values.cpu().numpy()
-    y = labels.cpu().numpy()
-    del values, labels
-    has_missing = bool(np.isnan(x).any())
-    cut_ptr, cuts, _ = pyoracle.compute_cuts(x, pyoracle.effective_max_bin(max_bin, has_missing))
+    values, labels, g, h = ops.synth(config, n, SEED + config, want_grad=injected)
+    f = values.shape[1]
+    ws = ops.Workspace()
+    has_missing = bool(torch.isnan(values).any().item())
+    eff = pyoracle.effective_max_bin(max_bin, has_missing)
+    cut_ptr, cuts, _, _ = ops.sketch_cuts(ws, values, eff)
     mb = 255 if has_missing else -1
-    bins = pyoracle.bin_matrix(x, cut_ptr, cuts, mb)
+    lay = ops.layout(n, f, 0, mb)
+    bins = ops.from_tiles(ops.bin_values(values, lay, cut_ptr, cuts).cpu().numpy(), lay)
+    y = labels.cpu().numpy()
+    inj = None
+    if injected:
+        gn, hn = g.cpu().numpy(), h.cpu().numpy()
+        inj = lambda r: (np.roll(gn, r)[:, None], np.roll(hn, r)[:, None])  # noqa: E731
+    del values, labels, g, h
+    torch.cuda.empty_cache()
     obj = {"binary:logistic": 0, "multi:softprob": 1, "reg:squarederror": 2}[objective]
     k = 10 if obj == 1 else 1
     p = pyoracle.params(eta=eta, max_depth=depth)
-    t0 = time.perf_counter()
-    trees, _, _ = pyoracle.train(bins, cut_ptr, cuts, mb, obj, y, k, p, rounds,
-                                 bin_stride=int(np.diff(cut_ptr).max()))
-    el = time.perf_counter() - t0
-    return {"value": len(trees) / el, "unit": "trees/s", "cores": 1, "kind": "port",
-            "sample": f"oracle booster, {len(trees)} trees of {name} ({n} x {x.shape[1]}, "
-                      f"depth {depth}), {el:.1f} s, one thread"}
+    pyoracle.set_threads(threads)
+    try:
+        t0 = time.perf_counter()
+        trees, _, _ = pyoracle.train(bins, cut_ptr, cuts, mb, obj, y, k, p, rounds,
+                                     bin_stride=int(np.diff(cut_ptr).max()), injected=inj)
+        el = time.perf_counter() - t0
+    finally:
+        pyoracle.set_threads(1)
+    return {"value": len(trees) / el, "unit": "trees/s", "cores": threads, "kind": "port",
+            "sample": f"oracle booster, {len(trees)} trees ({rounds} rounds) of {name} "
+                      f"({n} x {f}, depth {depth}), {el:.1f} s, {threads} threads"}
 
 
 # name: (config, rows, rounds, depth, eta, objective, max_bin, injected gradients)
@@ -225,6 +248,10 @@ TREE_CONFIGS = {
     "C4": (4, 60_000, 50, 6, 0.3, "multi:softprob", 256, False),
     "C5": (5, 2_000_000, 50, 10, 0.3, "reg:squarederror", 64, False),
 }
+
+
+# Rounds of each configuration the CPU baseline times (bounded: about 10-30 s in all).
+CPU_TREE_ROUNDS = (("C1", 10), ("C2", 5), ("C3", 2), ("C4", 2), ("C5", 3))
 
 
 def tree_algorithmic_bytes(t, n_rows, n_features, n_bins, depth, density=None):
@@ -293,6 +320,7 @@ def trees_leg(torch, dp, ops, name, rows=None, warm_rounds=4):
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
     trees = bst.num_trees()
+    tuning = bst.tuning()  # the autotuner's launch shapes for this matrix
     nodes, abytes = 0, 0
     for t in range(trees):
         tr = bst.tree(t)
@@ -304,7 +332,8 @@ def trees_leg(torch, dp, ops, name, rows=None, warm_rounds=4):
     return {"trees": trees, "rounds": rounds, "seconds": el, "value": trees / el,
             "unit": "trees/s", "rows": n, "features": f, "depth": depth, "objective": objective,
             "nodes": nodes, "layout": layout, "algorithmic_bytes_per_tree": abytes / trees,
-            "gbs": gbs, "pct_hbm_peak": 100.0 * gbs / HBM_PEAK_GBS}
+            "gbs": gbs, "pct_hbm_peak": 100.0 * gbs / HBM_PEAK_GBS,
+            "hist_config": tuning.get("chosen", tuning)}
 
 
 def paper_shape_leg(torch, dp, ops):
@@ -356,7 +385,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--rows", type=int, default=10_000_000)
-    ap.add_argument("--mode", choices=["full", "hist", "copy", "c2", "trees", "paper"],
+    ap.add_argument("--mode", choices=["full", "hist", "copy", "c2", "trees", "paper", "cpu"],
                     default="full")
     ap.add_argument("--configs", default="C1,C2,C3,C4,C5",
                     help="tree configurations timed in full/trees mode")
@@ -379,6 +408,13 @@ def main():
         return
     if args.mode == "paper":
         print(json.dumps(paper_shape_leg(torch, dp, ops)), flush=True)
+        return
+    if args.mode == "cpu":  # the CPU baseline's boosters only
+        threads = host_threads()
+        for name, cap in CPU_TREE_ROUNDS:
+            if name in args.configs.split(","):
+                print(json.dumps({name: cpu_trees_leg(torch, ops, name, cap, threads)}),
+                      flush=True)
         return
     names = [c.strip() for c in args.configs.split(",") if c.strip()]
     if args.mode in ("c2", "trees"):  # boosting rounds only (for kernel-trace profiles)
@@ -409,10 +445,15 @@ def main():
         log(f"CPU baseline: oracle histogram, {args.cpu_seconds:.0f} s budget")
         cpu = cpu_leg(sample, args)
         if args.mode == "full":
+            threads = host_threads()
             cpu["trees_per_s"] = {}
+            for name, cap in CPU_TREE_ROUNDS:
+                log(f"CPU baseline: oracle booster on {name}, {threads} threads")
+                cpu["trees_per_s"][name] = cpu_trees_leg(torch, ops, name, cap, threads)
+            cpu["trees_per_s_one_thread"] = {}
             for name, cap in (("C1", 10), ("C2", 2)):
-                log(f"CPU baseline: oracle booster on {name}")
-                cpu["trees_per_s"][name] = cpu_trees_leg(ops, name, cap)
+                log(f"CPU baseline: oracle booster on {name}, one thread")
+                cpu["trees_per_s_one_thread"][name] = cpu_trees_leg(torch, ops, name, cap, 1)
     avg_s = hist["avg_ms"] * 1e-3
     line = {
         "metric": METRIC,

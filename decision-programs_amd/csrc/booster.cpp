@@ -22,6 +22,7 @@
 
 #include "json.hpp"
 #include "predict.hpp"
+#include "tune.hpp"
 
 namespace dp {
 
@@ -218,7 +219,9 @@ void Grower::ensure_level(const Quantized& q, int64_t nb, int32_t d, int32_t D) 
   const int64_t S = int64_t(q.layout.n_features) * q.bin_stride * 2;
   const int cur = d & 1, nxt = cur ^ 1;
   const int64_t nn = d < D ? std::min(2 * nb, N) : 0;  // next level's bound
-  need(plan_hist_capacity(nn, T) < INT32_MAX && plan_part_capacity(nb, N, chunk_) < INT32_MAX &&
+  const int32_t G = (T + level_cfg_.tiles - 1) / level_cfg_.tiles;  // items per row chunk
+  need(plan_hist_capacity(nn, G, level_cfg_.items) < INT32_MAX &&
+           plan_part_capacity(nb, N, chunk_) < INT32_MAX &&
            plan_part_capacity(nn, N, chunk_) < INT32_MAX && plan_leaf_capacity(nb, N, chunk_) < INT32_MAX,
        "tree level too wide for the planner's 32-bit work counts");
   if (d < D) {
@@ -233,7 +236,7 @@ void Grower::ensure_level(const Quantized& q, int64_t nb, int32_t d, int32_t D) 
   level_[nxt].reserve(size_t(std::max<int64_t>(nn, 1)));
   sums_[nxt].reserve(size_t(2 * std::max<int64_t>(nn, 1)));
   seg_begin_[nxt].reserve(size_t(std::max<int64_t>(nn, 1)));
-  hist_work_[nxt].reserve(size_t(plan_hist_capacity(nn, T)));
+  hist_work_[nxt].reserve(size_t(plan_hist_capacity(nn, G, level_cfg_.items)));
   reduce_jobs_[nxt].reserve(size_t(nn / 2 + 1));
   pair_chunk_.reserve(size_t(2 * (std::max(nb, nn) + 1)));
   part_work_[nxt].reserve(size_t(plan_part_capacity(nn, N, chunk_)));
@@ -242,10 +245,13 @@ void Grower::ensure_level(const Quantized& q, int64_t nb, int32_t d, int32_t D) 
 }
 
 void Grower::prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, bool sparse,
-                     hipStream_t s) {
+                     const HistConfig& root_cfg, const HistConfig& level_cfg, hipStream_t s) {
   const dp_bin_layout& L = q.layout;
   need(sparse ? q.sparse.n_tiles > 0 : q.rows.n > 0, "histogram layout not built");
   sparse_ = sparse;
+  root_cfg_ = root_cfg;
+  level_cfg_ = level_cfg;
+  if (sparse) root_cfg_.tiles = level_cfg_.tiles = 1;  // one present-value tile per item
   colsample_ = p.colsample();
   tiles_ = sparse ? q.sparse.n_tiles : L.n_tiles;
   const int64_t N = L.n_rows;
@@ -268,13 +274,16 @@ void Grower::prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, b
   node_left_[0].reserve(1);
   const int64_t slot_words = sparse ? int64_t(q.sparse.tile_features) * q.bin_stride * 2
                                     : int64_t(q.bin_stride) * 32;
-  partial_.reserve(size_t(hist_partial_capacity(tiles_) * slot_words));
-  if (root_rows_ != N || root_tiles_ != tiles_) {
+  partial_.reserve(size_t(std::max(hist_partial_capacity(tiles_, root_cfg_),
+                                    hist_partial_capacity(tiles_, level_cfg_)) *
+                           slot_words));
+  if (root_rows_ != N || root_tiles_ != tiles_ || root_sparse_ != sparse ||
+      root_made_.tiles != root_cfg_.tiles || root_made_.items != root_cfg_.items) {
     const int64_t b = 0, e = N;
     const int32_t slot = 0;
     std::vector<HistWork> w;
     std::vector<HistReduce> j;
-    make_hist_work(L, &b, &e, &slot, 1, true, w, j, tiles_);
+    make_hist_work(L, &b, &e, &slot, 1, true, w, j, sparse ? tiles_ : 0, root_cfg_);
     root_work_.resize(w.size());
     root_job_.resize(j.size());
     DP_HIP(hipMemcpy(root_work_.p, w.data(), sizeof(HistWork) * w.size(), hipMemcpyHostToDevice));
@@ -282,6 +291,8 @@ void Grower::prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, b
     root_items_ = int32_t(w.size());
     root_rows_ = N;
     root_tiles_ = tiles_;
+    root_sparse_ = sparse;
+    root_made_ = root_cfg_;
   }
   const int64_t widest = level_bound(D, N), widest_hist = level_bound(D - 1, N);
   eager_ = widest <= kEagerNodes && 2 * widest_hist * S * int64_t(sizeof(int64_t)) <= kEagerHistBytes;
@@ -364,18 +375,19 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
         launch_hist_reduce_flat(partial_.p, root_job_.p, 1, nullptr, T, tf, F, B, nullptr, h, s);
       } else if (d == 0) {
         launch_hist(q.bins.p, L, gpair, nullptr, root_work_.p, root_items_, nullptr, B, h,
-                    partial_.p, s);
+                    partial_.p, s, nullptr, root_cfg_);
         launch_hist_reduce(partial_.p, root_job_.p, 1, nullptr, T, F, B, nullptr, h, false, s);
       } else if (sparse_) {
         launch_hist_sparse(q.sparse, N, F, gpair, ridx_[cur].p, hist_work_[cur].p,
-                           int32_t(plan_hist_items(nb, N, T)), field(c, &PlanCounts::n_hist), B,
-                           h, partial_.p, s);
+                           int32_t(plan_hist_items(nb, N, T, level_cfg_.items)),
+                           field(c, &PlanCounts::n_hist), B, h, partial_.p, s);
         launch_hist_reduce_flat(partial_.p, reduce_jobs_[cur].p, int32_t(nb / 2 + 1),
                                 field(c, &PlanCounts::n_reduce), T, tf, F, B, hist_[nxt].p, h, s);
       } else {
+        const int32_t G = (T + level_cfg_.tiles - 1) / level_cfg_.tiles;
         launch_hist(q.bins.p, L, gpair, ridx_[cur].p, hist_work_[cur].p,
-                    int32_t(plan_hist_items(nb, N, T)), field(c, &PlanCounts::n_hist), B, h,
-                    partial_.p, s, q.rows.p);
+                    int32_t(plan_hist_items(nb, N, G, level_cfg_.items)),
+                    field(c, &PlanCounts::n_hist), B, h, partial_.p, s, q.rows.p, level_cfg_);
         launch_hist_reduce(partial_.p, reduce_jobs_[cur].p, int32_t(nb / 2 + 1),
                            field(c, &PlanCounts::n_reduce), T, F, B, hist_[nxt].p, h, false, s);
       }
@@ -435,6 +447,8 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     a.depth = d;
     a.max_depth = D;
     a.n_tiles = T;
+    a.hist_tiles = level_cfg_.tiles;
+    a.hist_items = level_cfg_.items;
     a.hist_elems = S;
     a.part_chunk = chunk_;
     a.leaf_chunk = chunk_;
@@ -445,7 +459,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     a.info_capacity = int32_t(eager_ ? node_cap_ : int64_t(info_.n));
     a.level_capacity = int32_t(level_[nxt].n);
     a.hist_capacity = int32_t(hist_work_[nxt].n);
-    a.partial_capacity = int32_t(hist_partial_capacity(T));
+    a.partial_capacity = int32_t(hist_partial_capacity(T, level_cfg_));
     a.part_capacity = int32_t(part_work_[nxt].n);
     a.leaf_capacity = int32_t(leaf_work_[cur].n);
     a.cur_bound = int32_t(std::min<int64_t>(nb, INT32_MAX));
@@ -544,6 +558,11 @@ uint64_t Grower::signature() const {
   mix(uint64_t(node_cap_)); mix(uint64_t(chunk_));
   mix(uint64_t(slot_bytes_)); mix(uint64_t(root_rows_)); mix(uint64_t(root_tiles_));
   mix(uint64_t(root_items_));
+  for (const HistConfig* c : {&root_cfg_, &level_cfg_}) {
+    mix(uint64_t(c->tiles));
+    mix(uint64_t(c->unroll));
+    mix(uint64_t(c->items));
+  }
   return h;
 }
 
@@ -638,7 +657,8 @@ void Booster::set_param(const std::string& key, const std::string& value) {
       "min_split_loss", "min_child_weight", "subsample", "colsample_bytree", "colsample_bylevel",
       "colsample_bynode", "base_score", "boost_from_average", "seed", "seed_per_iteration",
       "nthread", "verbosity", "validate_parameters", "grow_policy", "dp_record_positions",
-      "dp_graphs", "dp_sparse_hist", "dp_concurrent_trees"};
+      "dp_graphs", "dp_sparse_hist", "dp_concurrent_trees", "dp_autotune", "dp_hist_tiles",
+      "dp_hist_unroll", "dp_hist_items"};
   bool ok = false;
   for (const char* k : known) ok = ok || key == k;
   need(ok, "unsupported parameter: " + key);
@@ -661,6 +681,22 @@ void Booster::set_param(const std::string& key, const std::string& value) {
     const int32_t m = parse_int(key, value);
     need(m >= 1 && m <= 8, "dp_concurrent_trees must be in [1, 8]");
     concurrent_trees_ = m;
+  }
+  if (key == "dp_autotune") autotune_ = parse_int(key, value) != 0;
+  if (key == "dp_hist_tiles") {
+    const int32_t m = parse_int(key, value);
+    need(m == 0 || m == 1 || m == 2, "dp_hist_tiles must be 0 (tuned), 1 or 2");
+    forced_hist_.tiles = m;
+  }
+  if (key == "dp_hist_unroll") {
+    const int32_t m = parse_int(key, value);
+    need(m == 0 || m == 1 || m == 2, "dp_hist_unroll must be 0 (tuned), 1 or 2");
+    forced_hist_.unroll = m;
+  }
+  if (key == "dp_hist_items") {
+    const int32_t m = parse_int(key, value);
+    need(m == 0 || (m >= 256 && m <= 4096), "dp_hist_items must be 0 (tuned) or in [256, 4096]");
+    forced_hist_.items = m;
   }
   if (key == "dp_sparse_hist") {
     const int32_t m = parse_int(key, value);
@@ -866,7 +902,9 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
   // collected first, so no buffer it uses moves under it.
   std::vector<uint64_t> inputs = {reinterpret_cast<uint64_t>(d), uint64_t(record_positions_),
                                   uint64_t(n_groups_), uint64_t(sparse_mode_),
-                                  uint64_t(concurrent_trees_)};
+                                  uint64_t(concurrent_trees_), uint64_t(autotune_),
+                                  uint64_t(forced_hist_.tiles), uint64_t(forced_hist_.unroll),
+                                  uint64_t(forced_hist_.items)};
   auto words = [](std::vector<uint64_t>& v, const void* p, size_t n) {
     for (size_t i = 0; i < n; i += 8) {
       uint64_t w = 0;
@@ -899,18 +937,39 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
     launch_tiles_to_rows(q.bins.p, q.layout, q.rows.p, stream_);
   }
   if (record_positions_) positions_.reserve(size_t(N));
+  // Histogram launch shapes: forced by dp_hist_* (0 = default for the rest),
+  // else tuned on this matrix shape (once per process), else the defaults.
+  HistConfig root_cfg, level_cfg;
+  if (forced_hist_.tiles || forced_hist_.unroll || forced_hist_.items) {
+    if (forced_hist_.tiles) root_cfg.tiles = forced_hist_.tiles;
+    if (forced_hist_.unroll) root_cfg.unroll = forced_hist_.unroll;
+    if (forced_hist_.items) root_cfg.items = forced_hist_.items;
+    level_cfg = root_cfg;
+    tuning_report_ = "{\"forced\":true}";
+  } else if (autotune_) {
+    const HistTuning& t =
+        sparse ? tune_sparse_hist(q.sparse, N, q.layout.n_features, q.bin_stride, gpair_.p,
+                                  stream_)
+               : tune_dense_hist(q.layout, q.bins.p, q.rows.p, q.bin_stride, gpair_.p, stream_);
+    root_cfg = t.root;
+    level_cfg = t.level;
+    tuning_report_ = t.report;
+  } else {
+    tuning_report_ = "{\"defaults\":true}";
+  }
   const int32_t K = n_groups_;
   int32_t S = std::min(K, concurrent_trees_);
   while (int32_t(growers_.size()) < S) growers_.push_back(std::make_unique<Grower>());
   if (growers_.empty()) growers_.push_back(std::make_unique<Grower>());
-  growers_[0]->prepare(q, tp_, (K + S - 1) / S, sparse, stream_);
+  growers_[0]->prepare(q, tp_, (K + S - 1) / S, sparse, root_cfg, level_cfg, stream_);
   const bool eager = growers_[0]->eager();
   if (!eager && S > 1) {  // level-synced trees synchronise per level: one at a time
     S = 1;
-    growers_[0]->prepare(q, tp_, K, sparse, stream_);
+    growers_[0]->prepare(q, tp_, K, sparse, root_cfg, level_cfg, stream_);
   }
-  for (int32_t l = 1; l < S; ++l) growers_[size_t(l)]->prepare(q, tp_, (K - l + S - 1) / S, sparse,
-                                                              stream_);
+  for (int32_t l = 1; l < S; ++l)
+    growers_[size_t(l)]->prepare(q, tp_, (K - l + S - 1) / S, sparse, root_cfg, level_cfg,
+                                 stream_);
   while (S > 1 && int32_t(tree_streams_.size()) < S) {
     hipStream_t t;
     DP_HIP(hipStreamCreateWithFlags(&t, hipStreamNonBlocking));

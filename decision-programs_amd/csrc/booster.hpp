@@ -85,8 +85,10 @@ class Grower {
   // trees in flight before the caller synchronises.
   // sparse: build histograms from q.sparse (which must be built) instead of
   // the 16-feature tiles and the row-major copy (which must then be built).
+  // root_cfg / level_cfg: launch shapes of the root (contiguous) and gathered
+  // histogram passes (present-value histograms use their items only).
   void prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, bool sparse,
-               hipStream_t s);
+               const HistConfig& root_cfg, const HistConfig& level_cfg, hipStream_t s);
   // Column sampling of the trees grow() enqueues next (inactive: every
   // feature is a candidate at every node); cs.output is set per tree.
   ColSample colsample;
@@ -143,6 +145,8 @@ class Grower {
   size_t slot_bytes_ = 0;
   int64_t root_rows_ = -1;
   int32_t root_tiles_ = 0, root_items_ = 0;
+  bool root_sparse_ = false;
+  HistConfig root_cfg_, level_cfg_, root_made_;
 };
 
 // Normalised hyperparameter JSON (see DPValidateHyperparameters).
@@ -184,6 +188,9 @@ class Booster {
   void margins(float* out, size_t n) const;
   void last_gradients(float* grad, float* hess, size_t n, int32_t* exps) const;
   void last_positions(int32_t* out, size_t n) const;
+  // JSON of the histogram launch shapes of the last round (the autotuner's
+  // timings and choice, or the forced / default shapes).
+  const std::string& tuning() const { return tuning_report_; }
   // Model from an XGBoost-schema JSON document (prediction / export only).
   void load_model(const std::string& text);
   // Rounds [begin, end) with the given step, as a new prediction-only booster.
@@ -227,6 +234,9 @@ class Booster {
   PooledPinnedBuffer exps_host_;  // two buffers, by round parity
   bool record_positions_ = false;
   bool use_graphs_ = true;
+  bool autotune_ = true;        // dp_autotune: time the histogram launch shapes (tune.cpp)
+  HistConfig forced_hist_{0, 0, 0};  // dp_hist_tiles / _unroll / _items; 0 = not forced
+  std::string tuning_report_ = "{}";
   int32_t sparse_mode_ = 1;  // dp_sparse_hist: 0 never, 1 when <= 1/4 present, 2 with any NaN
   bool labels_checked_ = false;
   std::vector<std::pair<std::vector<uint64_t>, hipGraphExec_t>> graphs_;  // newest last

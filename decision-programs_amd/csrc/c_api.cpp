@@ -13,6 +13,7 @@
 
 #include "booster.hpp"
 #include "json.hpp"
+#include "tune.hpp"
 
 namespace dp {
 void launch_copy_matrix(const float* src, int64_t row_stride, int64_t n_rows, int32_t n_features,
@@ -426,6 +427,16 @@ int DPBoosterGetLastPositions(BoosterHandle handle, int32_t* out, bst_ulong n) {
   return guarded([&] { bo(handle).b->last_positions(out, size_t(n)); });
 }
 
+int DPBoosterGetTuning(BoosterHandle handle, bst_ulong* out_len, const char** out) {
+  return guarded([&] {
+    dp::need(out_len && out, "null argument");
+    BoosterObj& b = bo(handle);
+    b.buffer = b.b->tuning();
+    *out = b.buffer.c_str();
+    *out_len = bst_ulong(b.buffer.size());
+  });
+}
+
 int DPValidateHyperparameters(const char* hyperparameters, uint32_t classes, bst_ulong* out_len,
                               const char** out) {
   static thread_local std::string result;
@@ -549,13 +560,19 @@ void hist_call(dp_workspace ws, const uint8_t* bins, const dp_bin_layout* layout
     total += end[i] - begin[i];
   }
   (void)total;
+  hipStream_t s = as_stream(stream);
+  // Contiguous row ranges take the launch shape the autotuner chose for this
+  // matrix shape (timed on these bins once per process; synchronises the
+  // stream that first time); gathered calls read the tile-major bins and keep
+  // the default shape.
+  dp::HistConfig cfg;
+  if (!ridx) cfg = dp::tune_dense_hist(*layout, bins, nullptr, bin_stride, gpair, s).root;
   std::vector<dp::HistWork> work;
   std::vector<dp::HistReduce> jobs;
   // Overwriting builds let single-chunk nodes store their histogram directly;
   // accumulating calls route every chunk through a partial slot.
-  const int32_t n_partial =
-      dp::make_hist_work(*layout, begin, end, nullptr, n_nodes, !accumulate, work, jobs);
-  hipStream_t s = as_stream(stream);
+  const int32_t n_partial = dp::make_hist_work(*layout, begin, end, nullptr, n_nodes, !accumulate,
+                                               work, jobs, 0, cfg);
   const size_t partial_words = size_t(n_partial) * size_t(bin_stride) * 32;
   ws->begin(sizeof(dp::HistWork) * work.size() + sizeof(dp::HistReduce) * jobs.size() + 512);
   ws->reserve_scratch(sizeof(int64_t) * partial_words + 256);
@@ -566,7 +583,7 @@ void hist_call(dp_workspace ws, const uint8_t* bins, const dp_bin_layout* layout
   ws->commit(s);
   int64_t* partial = partial_words ? ws->take<int64_t>(partial_words) : nullptr;
   dp::launch_hist(bins, *layout, gpair, ridx, d_work, int32_t(work.size()), nullptr, bin_stride,
-                  hist, partial, s);
+                  hist, partial, s, nullptr, cfg);
   dp::launch_hist_reduce(partial, d_jobs, n_nodes, nullptr, layout->n_tiles, layout->n_features,
                          bin_stride, nullptr, hist, accumulate, s);
 }

@@ -268,14 +268,25 @@ void launch_zero_i64_dev(int64_t* p, const int32_t* n_dev, int64_t per, int64_t 
 void launch_fill_u8(uint8_t* p, int64_t n, uint8_t value, hipStream_t s);
 void launch_iota_u32(uint32_t* p, int64_t n, hipStream_t s);
 
+// Launch shape of the dense histogram kernel, chosen per matrix shape by the
+// autotuner (tune.cpp) or forced by booster parameters: 16-feature tiles per
+// work item (1 or 2), rows per lane per pipeline step (1 or 2), and the work
+// items a pass aims at (which sets the rows per item).
+struct HistConfig {
+  int32_t tiles = 1;
+  int32_t unroll = 2;
+  int32_t items = 1024;
+};
+
 // Histograms: every work item accumulates into hist[slot]; hist must be zero.
 // Direct items write hist; the others write partial (int64 [slot][bin_stride * 32]).
 // row_major: optional row-major copy of the bins (launch_tiles_to_rows), read
-// for gathered rows.
+// for gathered rows.  The work items must come from the same cfg.tiles.
 void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t* gpair,
                  const uint32_t* ridx, const HistWork* work, int32_t n_work,
                  const int32_t* n_work_dev, int32_t bin_stride, int64_t* hist,
-                 int64_t* partial, hipStream_t s, const uint8_t* row_major = nullptr);
+                 int64_t* partial, hipStream_t s, const uint8_t* row_major = nullptr,
+                 const HistConfig& cfg = HistConfig{});
 // Completes the histograms of launch_hist: sums partial tiles, writes built
 // and sibling node histograms.  accumulate: add the sums to hist instead of
 // storing them (then no job may rely on a direct item).
@@ -283,38 +294,44 @@ void launch_hist_reduce(const int64_t* partial, const HistReduce* jobs, int32_t 
                         const int32_t* n_jobs_dev, int32_t n_tiles, int32_t n_features,
                         int32_t bin_stride, const int64_t* parent_base, int64_t* hist,
                         bool accumulate, hipStream_t s);
-// Minimum rows per histogram chunk and the chunk size for `rows` rows over
-// `n_tiles` tiles: about 1024 work items in all on large levels.  On smaller
-// levels of matrices with at most four tiles, about k * 256 items (k whole
-// items per CU, k = 1..3), so that no CU is left with one more item after the
-// others finish (with more tiles the item count moves in steps of n_tiles, and
-// the rule measured no better).
+// Minimum rows per histogram chunk and the chunk size for `rows` rows when
+// each row chunk makes `groups` work items: about `items` work items in all on
+// large levels.  On smaller levels of matrices with at most four groups, about
+// k * 256 items (k whole items per CU, k = 1..3), so that no CU is left with
+// one more item after the others finish (with more groups the item count moves
+// in steps of the group count, and the rule measured no better).
 constexpr int64_t kHistMinChunk = 4096;
-__host__ __device__ inline int64_t hist_chunk(int64_t rows, int32_t n_tiles) {
-  const int64_t units = rows * n_tiles;
+__host__ __device__ inline int64_t hist_chunk(int64_t rows, int32_t groups, int32_t items) {
+  const int64_t units = rows * groups;
   int64_t c;
-  if (n_tiles <= 4 && units < 1024 * kHistMinChunk) {  // units < 2^22: 32-bit division
+  if (groups <= 4 && units < int64_t(items) * kHistMinChunk &&
+      units < (int64_t(1) << 31)) {  // 32-bit division
     const uint32_t u = uint32_t(units);
     const uint32_t k = u < 256u * kHistMinChunk ? 1u : u / uint32_t(256 * kHistMinChunk);
     c = int64_t((u + 256u * k - 1u) / (256u * k));
   } else {
-    c = (units + 1023) / 1024;
+    c = (units + items - 1) / items;
   }
   return c < kHistMinChunk ? kHistMinChunk : c;
 }
-// Partial slots needed by one level (chunks of nodes with two or more chunks
-// number at most 2048 / n_tiles, each with n_tiles slots).
-inline int64_t hist_partial_capacity(int32_t n_tiles) { return 2048 + int64_t(n_tiles); }
+// Partial slots needed by one level: the chunks of nodes with two or more
+// chunks number at most 2 * items / groups, each with n_tiles slots, i.e. at
+// most 2 * items * tiles_per_item slots.
+inline int64_t hist_partial_capacity(int32_t n_tiles, const HistConfig& cfg) {
+  return 2 * int64_t(cfg.items) * cfg.tiles + int64_t(n_tiles);
+}
 // Work items and reduce jobs for the histograms of n_nodes row sets (node i:
 // [begin[i], end[i]) of ridx, written to hist slot slots[i], or i when slots
 // is null), chunked and ordered for the XCD-aware dispatch; the work may hold
 // empty padding items.  allow_direct: single-chunk nodes write directly.
 // n_tiles > 0 overrides the layout's tile count (present-value tiles).
 // Returns the number of partial slots used.
+// n_tiles > 0: present-value tiles, one per item; otherwise cfg.tiles of the
+// layout's 16-feature tiles per item.
 int32_t make_hist_work(const dp_bin_layout& layout, const int64_t* begin, const int64_t* end,
                        const int32_t* slots, int32_t n_nodes, bool allow_direct,
                        std::vector<HistWork>& work, std::vector<HistReduce>& jobs,
-                       int32_t n_tiles = 0);
+                       int32_t n_tiles = 0, const HistConfig& cfg = HistConfig{});
 void launch_subtract(const int64_t* parent, const int64_t* built, int64_t* sibling, int64_t n,
                      hipStream_t s);
 
@@ -444,6 +461,8 @@ struct PlanArgs {
   const int32_t* exps;     // quantiser exponents (gradient, hessian)
   int32_t depth, max_depth;
   int32_t n_tiles;
+  int32_t hist_tiles;      // tiles per histogram work item (HistConfig::tiles; 1 for present-value)
+  int32_t hist_items;      // work items a histogram pass aims at (HistConfig::items)
   int64_t hist_elems;      // int64 values per node histogram
   int64_t part_chunk, leaf_chunk;  // rows per partition / margin-update item
   double eta, lambda, alpha, mcw;
@@ -474,8 +493,8 @@ void launch_plan_root(LevelNode* cur, int64_t* sums, int64_t* seg_begin, PartWor
                       int64_t n_rows, const int64_t* root_slots, int32_t root_blocks,
                       int64_t part_chunk, uint32_t* ridx, hipStream_t s);
 // Upper bounds of the planner's outputs for a level of at most `nodes` nodes.
-inline int64_t plan_hist_capacity(int64_t nodes, int32_t n_tiles) {
-  return 1024 + (nodes / 2 + 8) * int64_t(n_tiles);
+inline int64_t plan_hist_capacity(int64_t nodes, int32_t groups, int32_t items) {
+  return items + int64_t(groups) + (nodes / 2 + 8) * int64_t(groups);
 }
 // Rows per partition / margin-update work item of the planner: about 2048
 // items over the matrix, a multiple of 256 in [256, kPartChunk].
@@ -489,11 +508,12 @@ inline int64_t plan_part_capacity(int64_t nodes, int64_t n_rows, int64_t chunk) 
 inline int64_t plan_leaf_capacity(int64_t nodes, int64_t n_rows, int64_t chunk) {
   return n_rows / chunk + 1 + nodes;
 }
-// Histogram work items of a level of at most `nodes` nodes: C <= min(1024 /
-// n_tiles, n_rows / (2 kHistMinChunk)) + nodes / 2 row chunks, padded to 8.
-inline int64_t plan_hist_items(int64_t nodes, int64_t n_rows, int32_t n_tiles) {
-  const int64_t a = 1024 / n_tiles, b = n_rows / (2 * kHistMinChunk);
-  return ((a < b ? a : b) + nodes / 2 + 8) * int64_t(n_tiles);
+// Histogram work items of a level of at most `nodes` nodes with `groups`
+// items per row chunk: C <= min(items / groups + 1, n_rows / (2 kHistMinChunk))
+// + nodes / 2 row chunks, padded to 8.
+inline int64_t plan_hist_items(int64_t nodes, int64_t n_rows, int32_t groups, int32_t items) {
+  const int64_t a = items / groups + 1, b = n_rows / (2 * kHistMinChunk);
+  return ((a < b ? a : b) + nodes / 2 + 8) * int64_t(groups);
 }
 constexpr int64_t kLeafChunk = 16384;  // margin-update items of the operator API
 

@@ -280,7 +280,8 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
     }
     int64_t small_total;
     (void)block_scan(mine, scan, &small_total);
-    const int64_t chunk = hist_chunk(small_total, T);
+    const int32_t TPW = a.hist_tiles, G = (T + TPW - 1) / TPW;  // items per row chunk
+    const int64_t chunk = hist_chunk(small_total, G, a.hist_items);
     int64_t* cstart = a.pair_chunk;                 // [n_expand + 1]
     int64_t* pstart = a.pair_chunk + n_expand + 1;  // [n_expand + 1]
     int64_t pcarry = 0;
@@ -312,7 +313,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
     __syncthreads();
     const int64_t* pair_off = n_expand <= kLdsOffsets ? s_off : cstart;
     const int64_t padded = (C + 7) / 8 * 8;
-    n_hist = padded * T;
+    n_hist = padded * G;
     if (n_hist > a.hist_capacity || pcarry * T > a.partial_capacity) {
       if (tid == 0) s_error = 4;
       n_hist = 0;
@@ -331,10 +332,10 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
                           b + chunk < sm.end ? b + chunk : sm.end, -1, 0};
           if (pair_off[j + 1] - pair_off[j] >= 2) p = (pstart[j] + k) * T;
         }
-        for (int32_t t = 0; t < T; ++t) {
-          item.tile = t;
-          item.partial = p < 0 ? -1 : int32_t(p + t);
-          a.hist_work[((c / 8) * T + t) * 8 + (c % 8)] = item;
+        for (int32_t g = 0; g < G; ++g) {  // tile group g: tiles g * TPW ..
+          item.tile = g * TPW;
+          item.partial = p < 0 ? -1 : int32_t(p + g * TPW);
+          a.hist_work[((c / 8) * G + g) * 8 + (c % 8)] = item;
         }
       }
       for (int32_t j = tid; j < n_expand; j += kPlanThreads) {
@@ -590,7 +591,8 @@ __device__ void plan_small_level(const PlanArgs& a) {
 
   // ---- second scan: histogram chunks of the smaller children -----------------
   const int32_t T = a.n_tiles;
-  const int64_t chunk = hist_chunk(tot[2], T);
+  const int32_t TPW = a.hist_tiles, G = (T + TPW - 1) / TPW;  // items per row chunk
+  const int64_t chunk = hist_chunk(tot[2], G, a.hist_items);
   const int64_t nc = wave_live ? ceil_rows(cnt[2], chunk) : 0;
   int64_t cnt2[2] = {nc, nc >= 2 ? nc : 0}, off2[2], tot2[2];
   if (live) {
@@ -644,7 +646,7 @@ __device__ void plan_small_level(const PlanArgs& a) {
   if (next_hist && n_next > 0) {
     const int64_t C = tot2[0];
     const int64_t padded = (C + 7) / 8 * 8;
-    n_hist = padded * T;
+    n_hist = padded * G;
     if (n_hist > a.hist_capacity || tot2[1] * T > a.partial_capacity) {
       error = 4;
       n_hist = 0;
@@ -661,10 +663,10 @@ __device__ void plan_small_level(const PlanArgs& a) {
           item = HistWork{s_slot[j], 0, b, b + chunk < se ? b + chunk : se, -1, 0};
           if (s_cs[j + 1] - s_cs[j] >= 2) p = (s_ps[j] + k) * T;
         }
-        for (int32_t t = 0; t < T; ++t) {
-          item.tile = t;
-          item.partial = p < 0 ? -1 : int32_t(p + t);
-          a.hist_work[((c / 8) * T + t) * 8 + (c % 8)] = item;
+        for (int32_t g = 0; g < G; ++g) {  // tile group g: tiles g * TPW ..
+          item.tile = g * TPW;
+          item.partial = p < 0 ? -1 : int32_t(p + g * TPW);
+          a.hist_work[((c / 8) * G + g) * 8 + (c % 8)] = item;
         }
       }
       if (e)

@@ -24,6 +24,9 @@
 //    derives the sibling (parent - built) in the same pass.
 #include "dp_internal.hpp"
 
+#include <algorithm>
+#include <mutex>
+
 namespace dp {
 namespace {
 
@@ -70,20 +73,27 @@ __device__ __forceinline__ void lds_add(lds_u64* p, unsigned long long v) {
 }
 
 constexpr int kTile = 16;                // features per tile (bytes per row per tile)
-constexpr int kLdsWords = 256 * 2 * kTile;  // 64 KiB of int64
+constexpr int kLdsWords = 256 * 2 * kTile;  // 64 KiB of int64 per tile
 constexpr int kHistThreads = 1024;
-constexpr int kHistUnroll = 2;           // rows per lane per pipeline stage
 
-// One work item = rows [begin, end) of node `slot` for one 16-feature tile.
-// LDS holds the tile's histogram as 256 rows of 256 bytes:
+// One work item = rows [begin, end) of node `slot` for TPW consecutive
+// 16-feature tiles starting at `tile` (tiles past the matrix's last are
+// skipped).  LDS holds each tile's histogram as 256 rows of 256 bytes:
 //   row b = [ sum qg of features 0..15 | sum qh of features 0..15 ] (int64 each)
-// so the word of (b, f) is at byte b*256 + f*8 (g) and +128 (h).  A lane owns
-// one matrix row per pipeline step: one 128-bit load brings its 16 bin bytes.
-// The bytes are rotated by (lane & 15) so that at every one of the 16 steps the
-// 16 lanes of a group address 16 distinct features, i.e. 16 distinct bank pairs
-// (f*8 mod 128), whatever their bins: the 64-bit LDS atomics are conflict free.
-// The LDS address is assembled by one v_perm_b32: byte 1 = the bin byte, byte 0
-// = the lane's feature offset for that step.
+// so the word of (b, f) is at byte b*256 + f*8 (g) and +128 (h); tile j of
+// the item at j * 64 KiB.  A lane owns one matrix row per pipeline step: one
+// 128-bit load per tile brings its 16 bin bytes.  The bytes are rotated by
+// (lane & 15) so that at every one of the 16 steps the 16 lanes of a group
+// address 16 distinct features, i.e. 16 distinct bank pairs (f*8 mod 128),
+// whatever their bins: the 64-bit LDS atomics are conflict free.  The LDS
+// address is assembled by one v_perm_b32: byte 1 = the bin byte, byte 0 = the
+// lane's feature offset for that step.
+//
+// TPW (tiles per work item, 1 or 2) and U (rows per lane per pipeline step, 1
+// or 2) are the autotuner's choices: two tiles per item read each row's
+// gradient pair once for 32 features (half the re-reads of TPW 1) with 128
+// KiB of LDS and one workgroup per CU; one tile per item fits two workgroups
+// per CU.
 //
 // The row loads have no branches, so the compiler's memory counters see a
 // straight pipeline: indices past `end` are clamped to the last row and their
@@ -91,22 +101,20 @@ constexpr int kHistUnroll = 2;           // rows per lane per pipeline stage
 // matrices have at most 255 bins) skip the atomics by exec mask, which keeps
 // sparse data (C5: 95 % missing) from spending LDS cycles on absent values.
 // Contiguous rows (GATHER false) are loaded and accumulated block by block (the
-// 32 waves of a CU hide the load latency; measured: prefetching a block ahead
-// does not help, the loop is bound by the LDS atomics); gathered rows
-// (GATHER true) load their row ids two blocks ahead and the bins and gradients
-// one block ahead.  At most 64 VGPRs, so two workgroups fit on a CU.
-// Workgroups loop over items (item = blockIdx.x + k * gridDim.x); with a grid
-// that is a multiple of 8, item i still runs on XCD i mod 8.
-template <bool GATHER, bool MISSING>
-__global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8, 8))) void hist_kernel(
-    const uint8_t* __restrict__ bins, int64_t n_rows, int32_t n_features,
+// resident waves of a CU hide the load latency; the loop is bound by the LDS
+// atomics); gathered rows (GATHER true) load their row ids two blocks ahead and
+// the bins and gradients one block ahead.  Workgroups loop over items (item =
+// blockIdx.x + k * gridDim.x); with a grid that is a multiple of 8, item i
+// still runs on XCD i mod 8.
+template <bool GATHER, bool MISSING, int TPW, int U>
+__global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8 / TPW, 8 / TPW))) void hist_kernel(
+    const uint8_t* __restrict__ bins, int64_t n_rows, int32_t n_features, int32_t n_tiles,
     const int2* __restrict__ gpair, const uint32_t* __restrict__ ridx,
     const HistWork* __restrict__ work, int32_t n_work_host,
     const int32_t* __restrict__ n_work_dev, int32_t bin_stride,
     unsigned long long* __restrict__ hist, unsigned long long* __restrict__ partial,
     int64_t tile_step, int64_t row_step) {
-  __shared__ unsigned long long lds[kLdsWords];
-  constexpr int U = kHistUnroll;
+  extern __shared__ unsigned long long lds[];  // TPW * kLdsWords
   constexpr int64_t kStep = int64_t(kHistThreads) * U;
   // The first item is loaded alongside the device count (the host bound keeps
   // it in range), so the two loads overlap instead of chaining.
@@ -126,14 +134,16 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8,
   for (int32_t item = blockIdx.x; item < n_work; item += gridDim.x) {
   const HistWork w = item == int32_t(blockIdx.x) ? w_first : work[item];
   if (w.begin >= w.end) continue;  // padding item (uniform per workgroup)
-  for (int e = threadIdx.x; e < kLdsWords; e += kHistThreads) lds[e] = 0ull;
+  // tiles of this item that exist (uniform per workgroup)
+  const int nt = TPW == 1 ? 1 : (w.tile + TPW <= n_tiles ? TPW : n_tiles - w.tile);
+  for (int e = threadIdx.x; e < nt * kLdsWords; e += kHistThreads) lds[e] = 0ull;
   __syncthreads();
 
   const uint8_t* tile = bins + int64_t(w.tile) * tile_step;  // row r at tile + r * row_step
   const int64_t last = w.end - 1;
   const int64_t lane = threadIdx.x;
   uint32_t rows[2][U];  // GATHER: row ids of the block after the next
-  uint4 v[2][U];
+  uint4 v[2][U][TPW];
   int2 q[2][U];
   auto fetch_rows = [&](int b, int64_t base) {
 #pragma unroll
@@ -147,7 +157,10 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8,
     for (int u = 0; u < U; ++u) {
       const int64_t i = base + int64_t(u) * kHistThreads + lane;
       const uint32_t r = GATHER ? rows[b][u] : uint32_t(i < w.end ? i : last);
-      v[b][u] = *reinterpret_cast<const uint4*>(tile + int64_t(r) * row_step);
+      const uint8_t* src = tile + int64_t(r) * row_step;
+#pragma unroll
+      for (int j = 0; j < TPW; ++j)  // a missing second tile re-reads the first
+        v[b][u][j] = *reinterpret_cast<const uint4*>(src + (j < nt ? j : 0) * tile_step);
       q[b][u] = gpair[r];
     }
   };
@@ -155,18 +168,23 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8,
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const bool ok = base + int64_t(u) * kHistThreads + lane < w.end;
-      uint32_t a[4] = {v[b][u].x, v[b][u].y, v[b][u].z, v[b][u].w};
-      rotate16(a, rot);
       const unsigned long long g = ok ? (unsigned long long)(long long)q[b][u].x : 0ull;
       const unsigned long long h = ok ? (unsigned long long)(long long)q[b][u].y : 0ull;
 #pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        const uint32_t sel = 0x0c0c0000u | ((4u + uint32_t(k & 3)) << 8) | uint32_t(k & 3);
-        const uint32_t off = __builtin_amdgcn_perm(a[k >> 2], slotw[k >> 2], sel);
-        if (MISSING && off >= 255u * 256u) continue;  // byte 255: missing value
-        lds_u64* p = (lds_u64*)(lds_base + off);
-        lds_add(p, g);
-        lds_add(p + 16, h);
+      for (int j = 0; j < TPW; ++j) {
+        if (j >= nt) break;  // uniform per workgroup
+        uint32_t a[4] = {v[b][u][j].x, v[b][u][j].y, v[b][u][j].z, v[b][u][j].w};
+        rotate16(a, rot);
+        lds_u8* const base_j = lds_base + j * (kLdsWords * 8);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          const uint32_t sel = 0x0c0c0000u | ((4u + uint32_t(k & 3)) << 8) | uint32_t(k & 3);
+          const uint32_t off = __builtin_amdgcn_perm(a[k >> 2], slotw[k >> 2], sel);
+          if (MISSING && off >= 255u * 256u) continue;  // byte 255: missing value
+          lds_u64* p = (lds_u64*)(base_j + off);
+          lds_add(p, g);
+          lds_add(p + 16, h);
+        }
       }
     }
   };
@@ -193,16 +211,19 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8,
   __syncthreads();
 
   const int n_words = bin_stride * 32;  // bins < bin_stride, 32 words each
-  if (w.partial >= 0) {
-    unsigned long long* out = partial + int64_t(w.partial) * n_words;
-    for (int e = threadIdx.x; e < n_words; e += kHistThreads) out[e] = lds[e];
-  } else {
-    unsigned long long* out = hist + int64_t(w.slot) * n_features * bin_stride * 2;
-    const int f0 = w.tile * kTile;
-    for (int e = threadIdx.x; e < n_words; e += kHistThreads) {
-      const int bin = e >> 5, within = e & 31;
-      const int f = f0 + (within & 15);
-      if (f < n_features) out[(int64_t(f) * bin_stride + bin) * 2 + (within >> 4)] = lds[e];
+  for (int j = 0; j < nt; ++j) {
+    const unsigned long long* src = lds + j * kLdsWords;
+    if (w.partial >= 0) {  // tile j's partial slot is the item's slot + j
+      unsigned long long* out = partial + int64_t(w.partial + j) * n_words;
+      for (int e = threadIdx.x; e < n_words; e += kHistThreads) out[e] = src[e];
+    } else {
+      unsigned long long* out = hist + int64_t(w.slot) * n_features * bin_stride * 2;
+      const int f0 = (w.tile + j) * kTile;
+      for (int e = threadIdx.x; e < n_words; e += kHistThreads) {
+        const int bin = e >> 5, within = e & 31;
+        const int f = f0 + (within & 15);
+        if (f < n_features) out[(int64_t(f) * bin_stride + bin) * 2 + (within >> 4)] = src[e];
+      }
     }
   }
   __syncthreads();  // the next item clears the LDS this item just read
@@ -422,13 +443,16 @@ void launch_iota_u32(uint32_t* p, int64_t n, hipStream_t s) {
 int32_t make_hist_work(const dp_bin_layout& layout, const int64_t* begin, const int64_t* end,
                        const int32_t* slots, int32_t n_nodes, bool allow_direct,
                        std::vector<HistWork>& work, std::vector<HistReduce>& jobs,
-                       int32_t n_tiles) {
+                       int32_t n_tiles, const HistConfig& cfg) {
   const int64_t T = n_tiles > 0 ? n_tiles : layout.n_tiles;
-  // About 1024 items (two waves of 2 workgroups per CU on 256 CUs), at least
-  // kHistMinChunk rows each, so the per-item LDS clear and store stay small.
+  const int64_t tpw = n_tiles > 0 ? 1 : cfg.tiles;  // present-value tiles: one per item
+  const int64_t G = (T + tpw - 1) / tpw;            // work items per row chunk
+  // About cfg.items items (two waves of resident workgroups on 256 CUs at the
+  // default), at least kHistMinChunk rows each, so the per-item LDS clear and
+  // store stay small.
   int64_t total = 0;
   for (int32_t i = 0; i < n_nodes; ++i) total += end[i] - begin[i];
-  const int64_t chunk = hist_chunk(total, int32_t(T));
+  const int64_t chunk = hist_chunk(total, int32_t(G), cfg.items);
   struct Chunk {
     int32_t slot, partial;
     int64_t b, e;
@@ -448,33 +472,48 @@ int32_t make_hist_work(const dp_bin_layout& layout, const int64_t* begin, const 
     if (!direct) n_partial += nc;
   }
   // Blocks are dispatched round-robin over the 8 XCDs (block id mod 8).  Item
-  // order puts the tiles of one row chunk on the same XCD in consecutive
+  // order puts the tile groups of one row chunk on the same XCD in consecutive
   // dispatch slots, so that chunk's gradient pairs are read from HBM once and
   // then hit that XCD's L2.
   const int64_t groups = (int64_t(chunks.size()) + 7) / 8;
-  work.assign(size_t(groups * T * 8), HistWork{0, 0, 0, 0, -1, 0});
+  work.assign(size_t(groups * G * 8), HistWork{0, 0, 0, 0, -1, 0});
   for (int64_t c = 0; c < int64_t(chunks.size()); ++c)
-    for (int64_t t = 0; t < T; ++t) {
+    for (int64_t g = 0; g < G; ++g) {
       const Chunk& ch = chunks[size_t(c)];
-      const int64_t b = ((c / 8) * T + t) * 8 + (c % 8);
+      const int64_t b = ((c / 8) * G + g) * 8 + (c % 8);
+      const int64_t t = g * tpw;
       work[size_t(b)] = {ch.slot, int32_t(t), ch.b, ch.e,
                          ch.partial < 0 ? -1 : int32_t(ch.partial * T + t), 0};
     }
   return n_partial * int32_t(T);
 }
 
+namespace {
+template <bool GATHER, bool MISSING>
+auto hist_instance(const HistConfig& cfg) {
+  if (cfg.tiles == 2)
+    return cfg.unroll == 1 ? hist_kernel<GATHER, MISSING, 2, 1> : hist_kernel<GATHER, MISSING, 2, 2>;
+  return cfg.unroll == 1 ? hist_kernel<GATHER, MISSING, 1, 1> : hist_kernel<GATHER, MISSING, 1, 2>;
+}
+}  // namespace
+
 void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t* gpair,
                  const uint32_t* ridx, const HistWork* work, int32_t n_work,
                  const int32_t* n_work_dev, int32_t bin_stride, int64_t* hist,
-                 int64_t* partial, hipStream_t s, const uint8_t* row_major) {
+                 int64_t* partial, hipStream_t s, const uint8_t* row_major,
+                 const HistConfig& cfg) {
   if (n_work <= 0) return;
   need(bin_stride >= 1 && bin_stride <= kMaxBins, "histogram bin stride out of range");
   need(layout.tile_width == kTile, "histogram kernel needs 16-feature tiles");
+  need((cfg.tiles == 1 || cfg.tiles == 2) && (cfg.unroll == 1 || cfg.unroll == 2),
+       "histogram configuration out of range");
   auto* out = reinterpret_cast<unsigned long long*>(hist);
   auto* part = reinterpret_cast<unsigned long long*>(partial);
   const auto* gp = reinterpret_cast<const int2*>(gpair);
-  // At most 1024 resident workgroups (2 per CU, two rounds); a multiple of 8.
-  int grid = n_work < 1024 ? n_work : 1024;
+  // At most two rounds of resident workgroups (two per CU with one tile per
+  // item, one with two tiles); a multiple of 8.
+  const int resident = cfg.tiles == 1 ? 512 : 256;
+  int grid = n_work < 2 * resident ? n_work : 2 * resident;
   grid = (grid + 7) / 8 * 8;
   // A missing value's byte 255 must not alias a real bin.
   if (layout.missing_bin >= 0) {
@@ -486,11 +525,23 @@ void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t
   const int64_t tile_step = rows ? kTile : layout.n_rows * kTile;
   const int64_t row_step = rows ? int64_t(layout.n_tiles) * kTile : kTile;
   const bool missing = layout.missing_bin >= 0;
-  auto kernel = ridx ? (missing ? hist_kernel<true, true> : hist_kernel<true, false>)
-                     : (missing ? hist_kernel<false, true> : hist_kernel<false, false>);
-  hipLaunchKernelGGL(kernel, dim3(grid), dim3(kHistThreads), 0, s, src, layout.n_rows,
-                     layout.n_features, gp, ridx, work, n_work, n_work_dev, bin_stride, out, part,
-                     tile_step, row_step);
+  auto kernel = ridx ? (missing ? hist_instance<true, true>(cfg) : hist_instance<true, false>(cfg))
+                     : (missing ? hist_instance<false, true>(cfg)
+                                : hist_instance<false, false>(cfg));
+  const size_t lds = size_t(cfg.tiles) * kLdsWords * sizeof(unsigned long long);
+  if (lds > 65536) {  // beyond the default dynamic LDS limit (once per instantiation)
+    static std::mutex lock;
+    static std::vector<const void*> raised;
+    std::lock_guard<std::mutex> hold(lock);
+    const void* k = reinterpret_cast<const void*>(kernel);
+    if (std::find(raised.begin(), raised.end(), k) == raised.end()) {
+      DP_HIP(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
+      raised.push_back(k);
+    }
+  }
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(kHistThreads), lds, s, src, layout.n_rows,
+                     layout.n_features, layout.n_tiles, gp, ridx, work, n_work, n_work_dev,
+                     bin_stride, out, part, tile_step, row_step);
   DP_HIP(hipGetLastError());
 }
 

@@ -1,0 +1,212 @@
+// Histogram autotuner: the launch shape of the histogram passes of one matrix
+// shape, chosen by timing the candidates on the matrix itself.
+//
+// The reference has no autotuner (its histograms run inside XGBoost); this one
+// re-derives, per (rows, features, bins, layout), the choices the histogram
+// kernel leaves open on gfx950:
+//   tiles per work item   1 (64 KiB of LDS, two workgroups per CU) or 2
+//                         (128 KiB, one per CU; each row's gradient pair is
+//                         read once for 32 features instead of 16);
+//   rows per lane per pipeline step   1 or 2;
+//   work items per pass   512, 1024 or 2048 (fewer, longer row chunks write
+//                         fewer partial tiles; more balance the CUs better).
+// The contiguous (root) pass is timed over the whole matrix; the gathered pass
+// over every other row of it through the row-major copy, as the levels below
+// the root read it.  Present-value histograms time their work-item count only.
+// Every candidate computes the same exact sums, so the choice changes speed,
+// never results.  Choices are cached per process; the timings are kept as a
+// JSON report.
+#include <algorithm>
+#include <cstdio>
+#include <map>
+#include <mutex>
+#include <tuple>
+
+#include "tune.hpp"
+
+namespace dp {
+namespace {
+
+using Key = std::tuple<int64_t, int32_t, int32_t, int32_t, int32_t, int32_t>;
+
+std::mutex g_lock;
+std::map<Key, HistTuning> g_cache;
+
+std::vector<HistConfig> dense_candidates(int32_t n_tiles) {
+  std::vector<HistConfig> c;
+  for (int32_t tiles : {1, 2}) {
+    if (tiles > n_tiles) continue;
+    for (int32_t unroll : {1, 2})
+      for (int32_t items : {512, 1024, 2048}) c.push_back(HistConfig{tiles, unroll, items});
+  }
+  return c;
+}
+
+std::string config_json(const HistConfig& c) {
+  char b[96];
+  std::snprintf(b, sizeof b, "{\"tiles\":%d,\"unroll\":%d,\"items\":%d}", c.tiles, c.unroll,
+                c.items);
+  return b;
+}
+
+// Average milliseconds of `run` over three launches after one warm launch.
+template <class Run>
+double time_ms(Run&& run, hipStream_t s) {
+  hipEvent_t a, b;
+  DP_HIP(hipEventCreate(&a));
+  DP_HIP(hipEventCreate(&b));
+  run();
+  DP_HIP(hipEventRecord(a, s));
+  for (int r = 0; r < 3; ++r) run();
+  DP_HIP(hipEventRecord(b, s));
+  DP_HIP(hipEventSynchronize(b));
+  float ms = 0.0f;
+  DP_HIP(hipEventElapsedTime(&ms, a, b));
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  return double(ms) / 3.0;
+}
+
+// One timed pass: work lists of one node [0, rows) for cfg, hist + reduce.
+struct Pass {
+  const dp_bin_layout* L;
+  const uint8_t* bins;
+  const uint8_t* rows_major;  // gathered pass: row-major copy, ridx every other row
+  const uint32_t* ridx;
+  int64_t rows;
+  int32_t bin_stride;
+  const int32_t* gpair;
+  int64_t* out;  // one node histogram
+};
+
+double time_dense(const Pass& p, const HistConfig& cfg, hipStream_t s) {
+  const int64_t b = 0, e = p.rows;
+  std::vector<HistWork> w;
+  std::vector<HistReduce> j;
+  const int32_t slots = make_hist_work(*p.L, &b, &e, nullptr, 1, true, w, j, 0, cfg);
+  DeviceBuffer<HistWork> dw(w.size());
+  DeviceBuffer<HistReduce> dj(j.size());
+  DeviceBuffer<int64_t> partial(size_t(std::max(slots, 1)) * size_t(p.bin_stride) * 32);
+  DP_HIP(hipMemcpyAsync(dw.p, w.data(), dw.bytes(), hipMemcpyHostToDevice, s));
+  DP_HIP(hipMemcpyAsync(dj.p, j.data(), dj.bytes(), hipMemcpyHostToDevice, s));
+  const double ms = time_ms(
+      [&] {
+        launch_hist(p.bins, *p.L, p.gpair, p.ridx, dw.p, int32_t(w.size()), nullptr,
+                    p.bin_stride, p.out, partial.p, s, p.rows_major, cfg);
+        launch_hist_reduce(partial.p, dj.p, 1, nullptr, p.L->n_tiles, p.L->n_features,
+                           p.bin_stride, nullptr, p.out, false, s);
+      },
+      s);
+  DP_HIP(hipStreamSynchronize(s));  // before the buffers are freed
+  return ms;
+}
+
+template <class Time>
+HistConfig pick(const std::vector<HistConfig>& cands, Time&& time, std::string& report,
+                const char* name) {
+  HistConfig best = cands.front();
+  double best_ms = -1.0;
+  report += std::string("\"") + name + "\":[";
+  for (size_t i = 0; i < cands.size(); ++i) {
+    const double ms = time(cands[i]);
+    char b[64];
+    std::snprintf(b, sizeof b, ",\"ms\":%.5f}", ms);
+    std::string c = config_json(cands[i]);
+    c.pop_back();
+    report += (i ? "," : "") + c + b;
+    if (best_ms < 0.0 || ms < best_ms) {
+      best_ms = ms;
+      best = cands[i];
+    }
+  }
+  report += "]";
+  return best;
+}
+
+}  // namespace
+
+const HistTuning& tune_dense_hist(const dp_bin_layout& L, const uint8_t* bins,
+                                  const uint8_t* rows_major, int32_t bin_stride,
+                                  const int32_t* gpair, hipStream_t s) {
+  const Key key{L.n_rows, L.n_features, bin_stride, L.missing_bin, rows_major ? 1 : 0, 0};
+  std::lock_guard<std::mutex> hold(g_lock);
+  auto it = g_cache.find(key);
+  if (it != g_cache.end()) return it->second;
+  HistTuning t;
+  const auto cands = dense_candidates(L.n_tiles);
+  DeviceBuffer<int64_t> out(size_t(L.n_features) * size_t(bin_stride) * 2);
+  Pass root{&L, bins, nullptr, nullptr, L.n_rows, bin_stride, gpair, out.p};
+  std::string report = "{";
+  t.root = pick(cands, [&](const HistConfig& c) { return time_dense(root, c, s); }, report,
+                "root");
+  t.level = t.root;
+  if (rows_major && L.n_rows >= 2) {
+    // every other row, as one gathered node
+    const int64_t half = L.n_rows / 2;
+    std::vector<uint32_t> ids(static_cast<size_t>(half));
+    for (int64_t i = 0; i < half; ++i) ids[size_t(i)] = uint32_t(2 * i);
+    DeviceBuffer<uint32_t> ridx(ids.size());
+    DP_HIP(hipMemcpyAsync(ridx.p, ids.data(), ridx.bytes(), hipMemcpyHostToDevice, s));
+    Pass level{&L, bins, rows_major, ridx.p, half, bin_stride, gpair, out.p};
+    report += ",";
+    t.level = pick(cands, [&](const HistConfig& c) { return time_dense(level, c, s); }, report,
+                   "gathered");
+    DP_HIP(hipStreamSynchronize(s));
+  }
+  t.tuned = true;
+  report += ",\"chosen\":{\"root\":" + config_json(t.root) + ",\"gathered\":" +
+            config_json(t.level) + "}}";
+  t.report = report;
+  return g_cache.emplace(key, std::move(t)).first->second;
+}
+
+const HistTuning& tune_sparse_hist(const SparseBins& sp, int64_t n_rows, int32_t n_features,
+                                   int32_t bin_stride, const int32_t* gpair, hipStream_t s) {
+  const Key key{n_rows, n_features, bin_stride, sp.tile_features, 2, int32_t(sp.nnz % 1000003)};
+  std::lock_guard<std::mutex> hold(g_lock);
+  auto it = g_cache.find(key);
+  if (it != g_cache.end()) return it->second;
+  HistTuning t;
+  std::vector<HistConfig> cands;
+  for (int32_t items : {512, 1024, 2048}) cands.push_back(HistConfig{1, 2, items});
+  DeviceBuffer<int64_t> out(size_t(n_features) * size_t(bin_stride) * 2);
+  dp_bin_layout L{};
+  L.n_rows = n_rows;
+  L.n_features = n_features;
+  L.tile_width = 16;
+  L.n_tiles = sp.n_tiles;
+  std::string report = "{";
+  t.root = pick(
+      cands,
+      [&](const HistConfig& c) {
+        const int64_t b = 0, e = n_rows;
+        std::vector<HistWork> w;
+        std::vector<HistReduce> j;
+        const int32_t slots = make_hist_work(L, &b, &e, nullptr, 1, true, w, j, sp.n_tiles, c);
+        DeviceBuffer<HistWork> dw(w.size());
+        DeviceBuffer<HistReduce> dj(j.size());
+        DeviceBuffer<int64_t> partial(size_t(std::max(slots, 1)) * size_t(sp.tile_features) *
+                                      size_t(bin_stride) * 2);
+        DP_HIP(hipMemcpyAsync(dw.p, w.data(), dw.bytes(), hipMemcpyHostToDevice, s));
+        DP_HIP(hipMemcpyAsync(dj.p, j.data(), dj.bytes(), hipMemcpyHostToDevice, s));
+        const double ms = time_ms(
+            [&] {
+              launch_hist_sparse(sp, n_rows, n_features, gpair, nullptr, dw.p, int32_t(w.size()),
+                                 nullptr, bin_stride, out.p, partial.p, s);
+              launch_hist_reduce_flat(partial.p, dj.p, 1, nullptr, sp.n_tiles, sp.tile_features,
+                                      n_features, bin_stride, nullptr, out.p, s);
+            },
+            s);
+        DP_HIP(hipStreamSynchronize(s));
+        return ms;
+      },
+      report, "present_value");
+  t.level = t.root;
+  t.tuned = true;
+  report += ",\"chosen\":{\"root\":" + config_json(t.root) + ",\"gathered\":" +
+            config_json(t.level) + "}}";
+  t.report = report;
+  return g_cache.emplace(key, std::move(t)).first->second;
+}
+
+}  // namespace dp

@@ -1,0 +1,29 @@
+// Histogram autotuner (tune.cpp): launch shapes of the histogram passes of one
+// matrix shape, chosen by timing candidates on the matrix itself.
+#pragma once
+
+#include <string>
+
+#include "dp_internal.hpp"
+
+namespace dp {
+
+struct HistTuning {
+  HistConfig root;    // the contiguous root pass
+  HistConfig level;   // the gathered passes of the levels below the root
+  bool tuned = false;
+  std::string report;  // JSON: every candidate's time and the choice
+};
+
+// Dense 16-feature tiles.  rows_major: the row-major copy the gathered passes
+// read (null: only the root pass is tuned; level = root).  gpair: any
+// [n_rows][2] pairs (the timing does not depend on their values).  Cached per
+// process by (rows, features, bins, missing, gathered); synchronises `s`.
+const HistTuning& tune_dense_hist(const dp_bin_layout& layout, const uint8_t* bins,
+                                  const uint8_t* rows_major, int32_t bin_stride,
+                                  const int32_t* gpair, hipStream_t s);
+// Present-value layout: the work-item count of its passes.
+const HistTuning& tune_sparse_hist(const SparseBins& sp, int64_t n_rows, int32_t n_features,
+                                   int32_t bin_stride, const int32_t* gpair, hipStream_t s);
+
+}  // namespace dp

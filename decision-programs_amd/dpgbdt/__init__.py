@@ -112,6 +112,7 @@ def load():
         "DPBoosterGetMargins": (c_int, [H, c_void_p, c_uint64]),
         "DPBoosterGetLastGradients": (c_int, [H, c_void_p, c_void_p, c_uint64, c_void_p]),
         "DPBoosterGetLastPositions": (c_int, [H, c_void_p, c_uint64]),
+        "DPBoosterGetTuning": (c_int, [H, POINTER(c_uint64), POINTER(c_char_p)]),
         "DPDMatrixGetCuts": (c_int, [H, c_int32, c_void_p, c_void_p, c_uint64, POINTER(c_int32)]),
         "dp_workspace_create": (c_int, [POINTER(H)]),
         "dp_workspace_free": (c_int, [H]),
@@ -355,6 +356,12 @@ class Booster:
         out = np.zeros(n_rows, dtype=np.int32)
         check(load().DPBoosterGetLastPositions(self.handle, out.ctypes.data, n_rows))
         return out
+
+    def tuning(self):
+        """The histogram launch shapes of the last round (autotuner report)."""
+        n, out = c_uint64(), c_char_p()
+        check(load().DPBoosterGetTuning(self.handle, ctypes.byref(n), ctypes.byref(out)))
+        return json.loads(ctypes.string_at(out, n.value).decode())
 
     def __del__(self):
         if getattr(self, "handle", None) and _lib is not None:

@@ -162,6 +162,11 @@ int DPBoosterGetLastGradients(BoosterHandle handle, float* grad, float* hess, bs
                               int32_t* exps);
 /* Final node id of every row in the last tree (the row partition). */
 int DPBoosterGetLastPositions(BoosterHandle handle, int32_t* out, bst_ulong n);
+/* JSON of the histogram launch shapes the last round used: the autotuner's
+ * per-candidate timings and its choice for the root and gathered passes (or
+ * {"forced":true} / {"defaults":true} when dp_hist_* / dp_autotune=0 set
+ * them).  Library-owned string, valid until the next call on this booster. */
+int DPBoosterGetTuning(BoosterHandle handle, bst_ulong* out_len, const char** out);
 
 /* Validates and defaults a training-hyperparameter object the way the reference
  * does before training (class_native_training.cuh:16-33, via

@@ -22,6 +22,27 @@
 #include <omp.h>
 #endif
 
+/* Threads of the parallel loops below (dpo_set_threads; 1 = serial).  Every */
+/* parallel result is identical to the serial one: sums are exact integers, */
+/* and every reduction runs in a fixed order.                                */
+static int g_threads = 1;
+
+void dpo_set_threads(int32_t n) { g_threads = n > 0 ? n : 1; }
+int32_t dpo_get_threads(void) { return g_threads; }
+
+/* Threads for `work` items of which each thread should get at least `grain`. */
+static int threads_for(int64_t work, int64_t grain) {
+#ifdef _OPENMP
+  int64_t t = work / (grain > 0 ? grain : 1);
+  if (t > g_threads) t = g_threads;
+  return t < 1 ? 1 : (int)t;
+#else
+  (void)work;
+  (void)grain;
+  return 1;
+#endif
+}
+
 /* ------------------------------------------------------------------------ */
 /* Quantile cuts.                                                            */
 /*                                                                           */
@@ -47,44 +68,73 @@ static int cmp_float(const void* a, const void* b) {
 
 static float end_cut(float max_value) { return max_value + (fabsf(max_value) + 1e-5f); }
 
+/* Cuts of feature f into out (at most max_bin values); returns their count. */
+static int32_t feature_cuts(const float* x, int64_t n, int64_t n_features, int64_t f,
+                            int32_t max_bin, float* v, float* out, float* min_value) {
+  int32_t count = 0;
+  int64_t m_valid = 0;
+  for (int64_t r = 0; r < n; ++r) {
+    float value = x[r * n_features + f];
+    if (isnan(value)) continue;
+    v[m_valid++] = value == 0.0f ? 0.0f : value;
+  }
+  if (m_valid == 0) {
+    out[count++] = end_cut(0.0f);
+    *min_value = 0.0f;
+    return count;
+  }
+  qsort(v, (size_t)m_valid, sizeof(float), cmp_float);
+  int64_t distinct = 1;
+  for (int64_t i = 1; i < m_valid; ++i) distinct += v[i] != v[i - 1];
+  *min_value = v[0];
+  if (distinct <= max_bin) {
+    for (int64_t i = 1; i < m_valid; ++i)
+      if (v[i] != v[i - 1]) out[count++] = v[i];
+  } else {
+    float prev = v[0];
+    for (int64_t i = 1; i < max_bin; ++i) {
+      float c = v[(i * m_valid) / max_bin];
+      if (c > prev) { out[count++] = c; prev = c; }
+    }
+  }
+  out[count++] = end_cut(v[m_valid - 1]);
+  return count;
+}
+
 int dpo_compute_cuts(const float* x, int64_t n, int64_t n_features, int32_t max_bin,
                      int32_t* cut_ptr, float* cut_values, float* min_values) {
   if (max_bin < 2 || max_bin > 256) return -1;
-  float* v = (float*)malloc(sizeof(float) * (size_t)(n > 0 ? n : 1));
-  if (!v) return -2;
+  /* every feature's cuts go to its own max_bin slots, then are packed */
+  float* tmp = (float*)malloc(sizeof(float) * (size_t)(n_features > 0 ? n_features : 1) *
+                              (size_t)max_bin);
+  int32_t* counts = (int32_t*)malloc(sizeof(int32_t) * (size_t)(n_features > 0 ? n_features : 1));
+  if (!tmp || !counts) { free(tmp); free(counts); return -2; }
+  const int threads = threads_for(n_features, 1);
+  int failed = 0;
+#pragma omp parallel num_threads(threads)
+  {
+    float* v = (float*)malloc(sizeof(float) * (size_t)(n > 0 ? n : 1));
+    if (!v) {
+#pragma omp atomic write
+      failed = 1;
+    } else {
+#pragma omp for schedule(dynamic, 1)
+      for (int64_t f = 0; f < n_features; ++f)
+        counts[f] = feature_cuts(x, n, n_features, f, max_bin, v, tmp + f * max_bin,
+                                 min_values + f);
+    }
+    free(v);
+  }
+  if (failed) { free(tmp); free(counts); return -2; }
   int32_t out = 0;
   cut_ptr[0] = 0;
   for (int64_t f = 0; f < n_features; ++f) {
-    int64_t m_valid = 0;
-    for (int64_t r = 0; r < n; ++r) {
-      float value = x[r * n_features + f];
-      if (isnan(value)) continue;
-      v[m_valid++] = value == 0.0f ? 0.0f : value;
-    }
-    if (m_valid == 0) {
-      cut_values[out++] = end_cut(0.0f);
-      min_values[f] = 0.0f;
-      cut_ptr[f + 1] = out;
-      continue;
-    }
-    qsort(v, (size_t)m_valid, sizeof(float), cmp_float);
-    int64_t distinct = 1;
-    for (int64_t i = 1; i < m_valid; ++i) distinct += v[i] != v[i - 1];
-    min_values[f] = v[0];
-    if (distinct <= max_bin) {
-      for (int64_t i = 1; i < m_valid; ++i)
-        if (v[i] != v[i - 1]) cut_values[out++] = v[i];
-    } else {
-      float prev = v[0];
-      for (int64_t i = 1; i < max_bin; ++i) {
-        float c = v[(i * m_valid) / max_bin];
-        if (c > prev) { cut_values[out++] = c; prev = c; }
-      }
-    }
-    cut_values[out++] = end_cut(v[m_valid - 1]);
+    memcpy(cut_values + out, tmp + f * max_bin, sizeof(float) * (size_t)counts[f]);
+    out += counts[f];
     cut_ptr[f + 1] = out;
   }
-  free(v);
+  free(tmp);
+  free(counts);
   return 0;
 }
 
@@ -99,6 +149,8 @@ static int32_t upper_bound(const float* cuts, int32_t count, float value) {
 
 void dpo_bin_matrix(const float* x, int64_t n, int64_t n_features, const int32_t* cut_ptr,
                     const float* cut_values, int32_t missing_bin, uint8_t* bins) {
+  const int threads = threads_for(n * n_features, 1 << 20);
+#pragma omp parallel for num_threads(threads) schedule(static)
   for (int64_t r = 0; r < n; ++r)
     for (int64_t f = 0; f < n_features; ++f) {
       float value = x[r * n_features + f];
@@ -211,11 +263,10 @@ double dpo_unscale(int32_t exp_q) { return ldexp(1.0, -exp_q); }
 /* f is b; missing entries are not accumulated (their stats are the node sum */
 /* minus the bin total, as upstream derives them).                           */
 /* ------------------------------------------------------------------------ */
-void dpo_hist(const uint8_t* bins, int64_t n_features, const int32_t* qg, const int32_t* qh,
-              const uint32_t* rows, int64_t n_rows, int32_t bin_stride, int32_t missing_bin,
-              int64_t* hist) {
-  memset(hist, 0, sizeof(int64_t) * 2 * (size_t)(n_features * bin_stride));
-  for (int64_t i = 0; i < n_rows; ++i) {
+static void hist_rows(const uint8_t* bins, int64_t n_features, const int32_t* qg,
+                      const int32_t* qh, const uint32_t* rows, int64_t i0, int64_t i1,
+                      int32_t bin_stride, int32_t missing_bin, int64_t* hist) {
+  for (int64_t i = i0; i < i1; ++i) {
     int64_t r = rows ? (int64_t)rows[i] : i;
     const uint8_t* row = bins + r * n_features;
     for (int64_t f = 0; f < n_features; ++f) {
@@ -226,6 +277,40 @@ void dpo_hist(const uint8_t* bins, int64_t n_features, const int32_t* qg, const 
       cell[1] += qh[r];
     }
   }
+}
+
+void dpo_hist(const uint8_t* bins, int64_t n_features, const int32_t* qg, const int32_t* qh,
+              const uint32_t* rows, int64_t n_rows, int32_t bin_stride, int32_t missing_bin,
+              int64_t* hist) {
+  const int64_t cells = 2 * n_features * bin_stride;
+  memset(hist, 0, sizeof(int64_t) * (size_t)cells);
+  const int threads = threads_for(n_rows * n_features, 1 << 18);
+  int64_t* priv = threads > 1 ? (int64_t*)calloc((size_t)(cells * threads), sizeof(int64_t))
+                              : NULL;
+  if (!priv) {
+    hist_rows(bins, n_features, qg, qh, rows, 0, n_rows, bin_stride, missing_bin, hist);
+    return;
+  }
+  /* thread t: rows [n t / T, n (t + 1) / T) into its own histogram, then the */
+  /* histograms are added cell by cell (exact integers: any order is equal)  */
+#pragma omp parallel num_threads(threads)
+  {
+#ifdef _OPENMP
+    const int t = omp_get_thread_num();
+#else
+    const int t = 0;
+#endif
+    hist_rows(bins, n_features, qg, qh, rows, n_rows * t / threads, n_rows * (t + 1) / threads,
+              bin_stride, missing_bin, priv + cells * t);
+#pragma omp barrier
+#pragma omp for schedule(static)
+    for (int64_t c = 0; c < cells; ++c) {
+      int64_t acc = 0;
+      for (int u = 0; u < threads; ++u) acc += priv[cells * u + c];
+      hist[c] = acc;
+    }
+  }
+  free(priv);
 }
 
 /* Root-pass histogram with OpenMP: thread-private histograms over row blocks */
@@ -319,6 +404,43 @@ void dpo_evaluate_split(const int64_t* hist, int64_t n_features, int32_t bin_str
                             NULL, out);
 }
 
+/* Best candidate of one feature: the first bin (then missing right before  */
+/* left) with the largest loss; loss -inf when it has none.                  */
+static dpo_split feature_split(const int64_t* hf, int64_t f, int32_t nb, int64_t gp, int64_t hp,
+                               double unscale_g, double unscale_h, const dpo_params* p,
+                               double parent_gain) {
+  dpo_split best;
+  best.loss_chg = -INFINITY;
+  best.feature = (int32_t)f;
+  best.bin = -1;
+  best.default_left = 0;
+  best.valid = 0;
+  best.gl = 0;
+  best.hl = 0;
+  int64_t tg = 0, th = 0;
+  for (int32_t b = 0; b < nb; ++b) { tg += hf[2 * b]; th += hf[2 * b + 1]; }
+  const int64_t mg = gp - tg, mh = hp - th;
+  int64_t lg = 0, lh = 0;
+  for (int32_t b = 0; b < nb; ++b) {
+    lg += hf[2 * b];
+    lh += hf[2 * b + 1];
+    double right_missing = split_loss(p, lg, lh, gp - lg, hp - lh, unscale_g, unscale_h, parent_gain);
+    double left_missing = split_loss(p, lg + mg, lh + mh, gp - lg - mg, hp - lh - mh,
+                                     unscale_g, unscale_h, parent_gain);
+    int dl = left_missing > right_missing;
+    double c = dl ? left_missing : right_missing;
+    if (c > best.loss_chg) {
+      best.loss_chg = c;
+      best.bin = b;
+      best.default_left = dl;
+      best.valid = 1;
+      best.gl = dl ? lg + mg : lg;
+      best.hl = dl ? lh + mh : lh;
+    }
+  }
+  return best;
+}
+
 void dpo_evaluate_split_masked(const int64_t* hist, int64_t n_features, int32_t bin_stride,
                                const int32_t* n_bins, int64_t gp, int64_t hp, double unscale_g,
                                double unscale_h, const dpo_params* p, const uint8_t* allowed,
@@ -332,49 +454,82 @@ void dpo_evaluate_split_masked(const int64_t* hist, int64_t n_features, int32_t 
   best.gl = 0;
   best.hl = 0;
   const double parent_gain = dpo_calc_gain(p, (double)gp * unscale_g, (double)hp * unscale_h);
+  dpo_split* each = (dpo_split*)malloc(sizeof(dpo_split) * (size_t)(n_features > 0 ? n_features : 1));
+  if (!each) { *out = best; return; }
+  const int threads = threads_for(n_features * bin_stride, 1 << 14);
+#pragma omp parallel for num_threads(threads) schedule(static)
   for (int64_t f = 0; f < n_features; ++f) {
-    if (allowed && !allowed[f]) continue;  /* outside the node's column sample */
-    const int64_t* hf = hist + 2 * f * bin_stride;
-    const int32_t nb = n_bins[f];
-    int64_t tg = 0, th = 0;
-    for (int32_t b = 0; b < nb; ++b) { tg += hf[2 * b]; th += hf[2 * b + 1]; }
-    const int64_t mg = gp - tg, mh = hp - th;
-    int64_t lg = 0, lh = 0;
-    for (int32_t b = 0; b < nb; ++b) {
-      lg += hf[2 * b];
-      lh += hf[2 * b + 1];
-      double right_missing = split_loss(p, lg, lh, gp - lg, hp - lh, unscale_g, unscale_h, parent_gain);
-      double left_missing = split_loss(p, lg + mg, lh + mh, gp - lg - mg, hp - lh - mh,
-                                       unscale_g, unscale_h, parent_gain);
-      int dl = left_missing > right_missing;
-      double c = dl ? left_missing : right_missing;
-      if (c > best.loss_chg) {
-        best.loss_chg = c;
-        best.feature = (int32_t)f;
-        best.bin = b;
-        best.default_left = dl;
-        best.valid = 1;
-        best.gl = dl ? lg + mg : lg;
-        best.hl = dl ? lh + mh : lh;
-      }
+    if (allowed && !allowed[f]) {  /* outside the node's column sample */
+      each[f].valid = 0;
+      continue;
     }
+    each[f] = feature_split(hist + 2 * f * bin_stride, f, n_bins[f], gp, hp, unscale_g,
+                            unscale_h, p, parent_gain);
   }
+  /* features in order, strictly larger wins: ties keep the lowest feature */
+  /* (and, within a feature, its lowest bin)                               */
+  for (int64_t f = 0; f < n_features; ++f)
+    if (each[f].valid && each[f].loss_chg > best.loss_chg) best = each[f];
+  free(each);
   *out = best;
 }
 
 /* Stable partition of ridx[begin, end): rows whose bin <= split_bin (or that */
 /* are missing with default_left) first, in their original order.            */
+static int row_left(const uint8_t* bins, int64_t n_features, uint32_t r, int32_t feature,
+                    int32_t split_bin, int32_t default_left, int32_t missing_bin) {
+  uint8_t b = bins[(int64_t)r * n_features + feature];
+  return b == missing_bin ? default_left : (int32_t)b <= split_bin;
+}
+
 int64_t dpo_partition(uint32_t* ridx, int64_t begin, int64_t end, const uint8_t* bins,
                       int64_t n_features, int32_t feature, int32_t split_bin,
                       int32_t default_left, int32_t missing_bin, uint32_t* scratch) {
-  int64_t nl = 0, nr = 0;
-  for (int64_t i = begin; i < end; ++i) {
-    uint32_t r = ridx[i];
-    uint8_t b = bins[(int64_t)r * n_features + feature];
-    int left = b == missing_bin ? default_left : (int32_t)b <= split_bin;
-    if (left) ridx[begin + nl++] = r; else scratch[nr++] = r;
+  const int64_t n = end - begin;
+  const int threads = threads_for(n, 1 << 16);
+  if (threads <= 1) {
+    int64_t nl = 0, nr = 0;
+    for (int64_t i = begin; i < end; ++i) {
+      uint32_t r = ridx[i];
+      if (row_left(bins, n_features, r, feature, split_bin, default_left, missing_bin))
+        ridx[begin + nl++] = r;
+      else
+        scratch[nr++] = r;
+    }
+    memcpy(ridx + begin + nl, scratch, sizeof(uint32_t) * (size_t)nr);
+    return nl;
   }
-  memcpy(ridx + begin + nl, scratch, sizeof(uint32_t) * (size_t)nr);
+  /* blocks of rows: count each block's lefts, then every block writes its    */
+  /* lefts and rights after those of the blocks before it (stable)           */
+  int64_t* lefts = (int64_t*)calloc((size_t)threads + 1, sizeof(int64_t));
+  memcpy(scratch, ridx + begin, sizeof(uint32_t) * (size_t)n);
+#pragma omp parallel num_threads(threads)
+  {
+#ifdef _OPENMP
+    const int t = omp_get_thread_num();
+#else
+    const int t = 0;
+#endif
+    const int64_t b = n * t / threads, e = n * (t + 1) / threads;
+    int64_t c = 0;
+    for (int64_t i = b; i < e; ++i)
+      c += row_left(bins, n_features, scratch[i], feature, split_bin, default_left, missing_bin);
+    lefts[t + 1] = c;
+#pragma omp barrier
+#pragma omp single
+    for (int u = 0; u < threads; ++u) lefts[u + 1] += lefts[u];
+    /* implicit barrier after single */
+    int64_t pl = begin + lefts[t], pr = begin + lefts[threads] + (b - lefts[t]);
+    for (int64_t i = b; i < e; ++i) {
+      uint32_t r = scratch[i];
+      if (row_left(bins, n_features, r, feature, split_bin, default_left, missing_bin))
+        ridx[pl++] = r;
+      else
+        ridx[pr++] = r;
+    }
+  }
+  const int64_t nl = lefts[threads];
+  free(lefts);
   return nl;
 }
 

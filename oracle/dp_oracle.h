@@ -52,6 +52,12 @@ typedef struct {
   int64_t gl, hl;          /* quantised left-child sums                     */
 } dpo_split;
 
+/* ---- threads ----------------------------------------------------------- */
+/* OpenMP threads of the cuts, binning, histograms, split search and         */
+/* partition (1, the default, runs serially).  Results do not depend on it.  */
+void dpo_set_threads(int32_t n);
+int32_t dpo_get_threads(void);
+
 /* ---- quantile cuts and binning ---------------------------------------- */
 int dpo_compute_cuts(const float* x, int64_t n, int64_t n_features, int32_t max_bin,
                      int32_t* cut_ptr, float* cut_values, float* min_values);

@@ -101,6 +101,8 @@ def load():
         lib.dpo_stage_keep.restype = c_int32
         lib.dpo_sample_rows.argtypes = [POINTER(Sampling), c_int64, P]
         lib.dpo_colsample.argtypes = [POINTER(Sampling), c_int32, c_int32, c_int64, P]
+        lib.dpo_set_threads.argtypes = [c_int32]
+        lib.dpo_get_threads.restype = c_int32
         lib.dpo_tree_free.argtypes = [POINTER(Tree)]
         lib.dpo_tree_update_margin.argtypes = [POINTER(Tree), P, P, c_int64]
         lib.dpo_predict_tree.argtypes = [POINTER(Tree), P]
@@ -230,6 +232,16 @@ def partition(ridx, begin, end, bins, feature, split_bin, default_left, missing_
     nl = load().dpo_partition(_p(ridx), begin, end, _p(bins), bins.shape[1], feature, split_bin,
                               default_left, missing_bin, _p(scratch))
     return ridx, nl
+
+
+def set_threads(n):
+    """OpenMP threads of the oracle's cuts, binning, histograms, split search and partition
+    (1: serial); results are identical for any count."""
+    load().dpo_set_threads(int(n))
+
+
+def get_threads():
+    return load().dpo_get_threads()
 
 
 def sampling(seed=0, round_=0, output=0, subsample=1.0, bytree=1.0, bylevel=1.0, bynode=1.0):

@@ -1,0 +1,89 @@
+"""The histogram autotuner (tune.cpp) and the launch shapes it chooses among.
+
+Every launch shape computes the same exact integer sums, so a booster trained
+with any forced shape (tiles per work item, rows per lane per step, work items
+per pass) must save the model, row partition and margins of the default shape,
+which the oracle-parity tests pin.  The autotuner's report names timed
+candidates and picks one of them; dp_autotune=0 keeps the defaults.
+"""
+import itertools
+import json
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [dict(zip(("dp_hist_tiles", "dp_hist_unroll", "dp_hist_items"), c))
+          for c in itertools.product((1, 2), (1, 2), (512, 1024, 2048))]
+
+
+def _train(dp, values, labels, params, rounds, n, k):
+    dtrain = dp.DMatrix(values, labels)
+    bst = dp.Booster(dict(params, dp_record_positions=1), [dtrain])
+    for r in range(rounds):
+        bst.update(dtrain, r)
+    return bst.save_raw(), bst.last_positions(n), bst.margins(n, k), bst
+
+
+@pytest.mark.parametrize("case", ["c2_two_tiles", "c4_odd_tiles", "missing", "present_value"])
+def test_every_launch_shape_trains_the_same_model(dp, device, case):
+    """Trees, partitions and margins are identical under all twelve forced launch shapes
+    (two tiles per item over an odd tile count leaves a one-tile last group; the MISSING
+    kernels; present-value histograms take the work-item count only)."""
+    import torch
+    from dpgbdt import ops
+
+    if case == "c2_two_tiles":
+        values, labels, _, _ = ops.synth(2, 60000, 3, n_features=28)
+        params, k = {"objective": "binary:logistic", "max_depth": 7, "eta": 0.3}, 1
+    elif case == "c4_odd_tiles":
+        values, labels, _, _ = ops.synth(4, 3000, 4, n_features=784)
+        params, k = {"objective": "multi:softprob", "num_class": 10, "max_depth": 4,
+                     "eta": 0.3}, 10
+    elif case == "missing":
+        values, labels, _, _ = ops.synth(1, 50000, 5, n_features=40)
+        g = torch.Generator(device="cpu").manual_seed(3)
+        values[(torch.rand(values.shape, generator=g) < 0.3).to(values.device)] = float("nan")
+        params, k = {"objective": "binary:logistic", "max_depth": 6, "eta": 0.3,
+                     "dp_sparse_hist": 0}, 1
+    else:
+        values, labels, _, _ = ops.synth(5, 40000, 200, n_features=200)
+        params, k = {"objective": "reg:squarederror", "max_depth": 6, "eta": 0.3,
+                     "max_bin": 64}, 1
+    n = values.shape[0]
+    base = _train(dp, values, labels, dict(params, dp_autotune=0), 3, n, k)
+    assert base[3].tuning() == {"defaults": True}
+    for shape in SHAPES:
+        if case == "present_value" and shape["dp_hist_tiles"] == 2:
+            continue  # one present-value tile per item: only the item count applies
+        print(f"[tuning] {case} {shape}", flush=True)
+        got = _train(dp, values, labels, dict(params, **shape), 3, n, k)
+        assert got[3].tuning() == {"forced": True}
+        assert got[0] == base[0], shape
+        np.testing.assert_array_equal(got[1], base[1])
+        np.testing.assert_array_equal(np.asarray(got[2]).view(np.uint32),
+                                      np.asarray(base[2]).view(np.uint32))
+
+
+def test_autotuner_report_and_choice(dp, device):
+    """The autotuned booster reports every timed candidate of the root and gathered passes
+    and chooses the fastest of each; its model equals the default shape's."""
+    from dpgbdt import ops
+
+    values, labels, _, _ = ops.synth(2, 200000, 8, n_features=28)
+    params = {"objective": "binary:logistic", "max_depth": 6, "eta": 0.3}
+    tuned = _train(dp, values, labels, params, 2, 200000, 1)
+    report = tuned[3].tuning()
+    for name in ("root", "gathered"):
+        cands = report[name]
+        assert len(cands) == 12  # 2 tile widths x 2 unrolls x 3 item counts
+        assert all(c["ms"] > 0 for c in cands)
+        best = min(cands, key=lambda c: c["ms"])
+        assert report["chosen"][name] == {key: best[key] for key in ("tiles", "unroll", "items")}
+    base = _train(dp, values, labels, dict(params, dp_autotune=0), 2, 200000, 1)
+    assert tuned[0] == base[0]
+    # the choice is cached per process: a second booster of the shape reports the same
+    again = _train(dp, values, labels, params, 1, 200000, 1)
+    assert again[3].tuning() == report
+    print(json.dumps(report["chosen"]), flush=True)

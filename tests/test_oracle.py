@@ -489,3 +489,36 @@ def test_booster_row_sampling_zeroes_dropped_pairs(oracle):
         for key in ("left", "feature", "split_bin", "sum_qg", "sum_qh"):
             np.testing.assert_array_equal(a[key], b[key])
     np.testing.assert_array_equal(m1.view(np.uint32), m2.view(np.uint32))
+
+
+def test_threads_give_identical_results(oracle):
+    """The oracle's OpenMP loops (cuts, binning, histograms, split search, stable
+    partition) give the serial results bit for bit: the same cuts, bins, trees and
+    margins with 1 and 4 threads, on a matrix large enough to take every parallel path."""
+    rng = np.random.default_rng(8)
+    n, f = 120_000, 12
+    x = rng.normal(size=(n, f)).astype(np.float32)
+    x[rng.random((n, f)) < 0.1] = np.nan
+    y = (rng.random(n) < 1 / (1 + np.exp(-x[:, 0]))).astype(np.float32)
+    out = []
+    try:
+        for threads in (1, 4):
+            oracle.set_threads(threads)
+            cut_ptr, cuts, _ = oracle.compute_cuts(x, 255)
+            bins = oracle.bin_matrix(x, cut_ptr, cuts, 255)
+            trees, margin, _ = oracle.train(bins, cut_ptr, cuts, 255, oracle.OBJ_LOGISTIC, y, 1,
+                                            oracle.params(max_depth=7, eta=0.3), 2,
+                                            bin_stride=int(np.diff(cut_ptr).max()),
+                                            sample={"seed": 1, "bynode": 0.7})
+            out.append((cut_ptr, cuts, bins, trees, margin))
+    finally:
+        oracle.set_threads(1)
+    (c1, v1, b1, t1, m1), (c4, v4, b4, t4, m4) = out
+    np.testing.assert_array_equal(c1, c4)
+    np.testing.assert_array_equal(v1.view(np.uint32), v4.view(np.uint32))
+    np.testing.assert_array_equal(b1, b4)
+    for a, b in zip(t1, t4):
+        for key in ("left", "feature", "split_bin", "default_left", "sum_qg", "sum_qh",
+                    "positions"):
+            np.testing.assert_array_equal(a[key], b[key])
+    np.testing.assert_array_equal(m1.view(np.uint32), m4.view(np.uint32))
