@@ -118,6 +118,7 @@ def hist_leg(args, torch, dp, ops):
         "rows_features_per_s": n * f / (avg_ms * 1e-3),
         "achieved_gbs": achieved, "algorithmic_bytes": abytes,
         "min_ms": min(launch_ms), "max_ms": max(launch_ms),
+        "tuning": ops.hist_tuning(lay, stride),  # the autotuner's launch shape for this pass
     }
     sample = None
     if not args.skip_cpu:
@@ -481,7 +482,8 @@ def main():
                                "dp::hist_reduce_kernel",
                      "algorithmic_bytes_per_launch": hist["algorithmic_bytes"],
                      "lds_atomic_roof": roof,
-                     "avg_launch_ms": hist["avg_ms"]},
+                     "avg_launch_ms": hist["avg_ms"],
+                     "launch_shape": hist["tuning"].get("chosen", {}).get("root")},
         "trees_per_s": trees,
         "cpu_baseline": cpu,
     }

@@ -174,6 +174,37 @@ Quantized& DMatrix::quantize(int32_t max_bin, dp_workspace_s& ws, hipStream_t s)
   return ref;
 }
 
+// Each feature's most frequent bin (ties: the lowest) over all rows, as skip
+// bins per feature and per 16-feature tile (pad features: bin 0, the byte the
+// tiles hold for them), and the mean share of the rows in those bins.
+void build_skip_bins(Quantized& q, hipStream_t s) {
+  const int64_t N = q.layout.n_rows;
+  const int32_t F = q.layout.n_features, T = q.layout.n_tiles;
+  DeviceBuffer<unsigned int> counts(size_t(F) * 256);
+  launch_bin_counts(q.cols.p, N, F, counts.p, s);
+  std::vector<unsigned int> host(counts.n);
+  DP_HIP(hipMemcpyAsync(host.data(), counts.p, counts.bytes(), hipMemcpyDeviceToHost, s));
+  DP_HIP(hipStreamSynchronize(s));
+  std::vector<uint8_t> per_feature(static_cast<size_t>(F), 0);
+  std::vector<uint8_t> per_tile(static_cast<size_t>(T) * 16, 0);
+  double share = 0.0;
+  for (int32_t f = 0; f < F; ++f) {
+    const unsigned int* c = host.data() + size_t(f) * 256;
+    int32_t best = 0;
+    for (int32_t b = 1; b < 256; ++b)
+      if (c[b] > c[best]) best = b;
+    per_feature[size_t(f)] = uint8_t(best);
+    per_tile[size_t(f)] = uint8_t(best);  // tile-major: feature f at byte f
+    share += double(c[best]) / double(N);
+  }
+  q.skip_features.resize(per_feature.size());
+  q.skip_tiles.resize(per_tile.size());
+  DP_HIP(hipMemcpy(q.skip_features.p, per_feature.data(), per_feature.size(),
+                   hipMemcpyHostToDevice));
+  DP_HIP(hipMemcpy(q.skip_tiles.p, per_tile.data(), per_tile.size(), hipMemcpyHostToDevice));
+  q.skip_share = F > 0 ? share / double(F) : 0.0;
+}
+
 int32_t Tree::alloc(int32_t parent_id) {
   const int32_t id = size();
   left.push_back(-1);
@@ -245,10 +276,15 @@ void Grower::ensure_level(const Quantized& q, int64_t nb, int32_t d, int32_t D) 
 }
 
 void Grower::prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, bool sparse,
-                     const HistConfig& root_cfg, const HistConfig& level_cfg, hipStream_t s) {
+                     const HistConfig& root_cfg, const HistConfig& level_cfg, bool skip,
+                     hipStream_t s) {
   const dp_bin_layout& L = q.layout;
   need(sparse ? q.sparse.n_tiles > 0 : q.rows.n > 0, "histogram layout not built");
+  need(!skip || (!sparse && q.skip_tiles.n > 0 && q.skip_features.n > 0),
+       "skip bins not built");
   sparse_ = sparse;
+  skip_tiles_ = skip ? q.skip_tiles.p : nullptr;
+  skip_features_ = skip ? q.skip_features.p : nullptr;
   root_cfg_ = root_cfg;
   level_cfg_ = level_cfg;
   if (sparse) root_cfg_.tiles = level_cfg_.tiles = 1;  // one present-value tile per item
@@ -375,7 +411,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
         launch_hist_reduce_flat(partial_.p, root_job_.p, 1, nullptr, T, tf, F, B, nullptr, h, s);
       } else if (d == 0) {
         launch_hist(q.bins.p, L, gpair, nullptr, root_work_.p, root_items_, nullptr, B, h,
-                    partial_.p, s, nullptr, root_cfg_);
+                    partial_.p, s, nullptr, root_cfg_, skip_tiles_);
         launch_hist_reduce(partial_.p, root_job_.p, 1, nullptr, T, F, B, nullptr, h, false, s);
       } else if (sparse_) {
         launch_hist_sparse(q.sparse, N, F, gpair, ridx_[cur].p, hist_work_[cur].p,
@@ -387,7 +423,8 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
         const int32_t G = (T + level_cfg_.tiles - 1) / level_cfg_.tiles;
         launch_hist(q.bins.p, L, gpair, ridx_[cur].p, hist_work_[cur].p,
                     int32_t(plan_hist_items(nb, N, G, level_cfg_.items)),
-                    field(c, &PlanCounts::n_hist), B, h, partial_.p, s, q.rows.p, level_cfg_);
+                    field(c, &PlanCounts::n_hist), B, h, partial_.p, s, q.rows.p, level_cfg_,
+                    skip_tiles_);
         launch_hist_reduce(partial_.p, reduce_jobs_[cur].p, int32_t(nb / 2 + 1),
                            field(c, &PlanCounts::n_reduce), T, F, B, hist_[nxt].p, h, false, s);
       }
@@ -402,7 +439,8 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
       // Without records from the evaluation, the count launch selects them.
       const bool records = launch_evaluate(h, int32_t(nb), field(c, &PlanCounts::n_level), F, B,
                                            q.d_nbins.p, sums_[cur].p, exps, 0, 0, dtp,
-                                           eval_scratch_.p, splits_.p, s, false, fmask);
+                                           eval_scratch_.p, splits_.p, s, false, fmask,
+                                           skip_features_);
       SplitSelect sel;
       sel.cand = reinterpret_cast<const FeatCand*>(eval_scratch_.p);
       sel.n_features = F;
@@ -555,6 +593,7 @@ uint64_t Grower::signature() const {
   buf(part_masks_);
   buf(splits_); buf(eval_scratch_); buf(fmask_); buf(info_); buf(counts_); buf(slots_);
   mix(uint64_t(eager_)); mix(uint64_t(sparse_)); mix(uint64_t(colsample_)); mix(uint64_t(tiles_));
+  mix(reinterpret_cast<uint64_t>(skip_tiles_)); mix(reinterpret_cast<uint64_t>(skip_features_));
   mix(uint64_t(node_cap_)); mix(uint64_t(chunk_));
   mix(uint64_t(slot_bytes_)); mix(uint64_t(root_rows_)); mix(uint64_t(root_tiles_));
   mix(uint64_t(root_items_));
@@ -562,6 +601,7 @@ uint64_t Grower::signature() const {
     mix(uint64_t(c->tiles));
     mix(uint64_t(c->unroll));
     mix(uint64_t(c->items));
+    mix(uint64_t(c->split));
   }
   return h;
 }
@@ -658,7 +698,7 @@ void Booster::set_param(const std::string& key, const std::string& value) {
       "colsample_bynode", "base_score", "boost_from_average", "seed", "seed_per_iteration",
       "nthread", "verbosity", "validate_parameters", "grow_policy", "dp_record_positions",
       "dp_graphs", "dp_sparse_hist", "dp_concurrent_trees", "dp_autotune", "dp_hist_tiles",
-      "dp_hist_unroll", "dp_hist_items"};
+      "dp_hist_unroll", "dp_hist_items", "dp_hist_split", "dp_skip_bin"};
   bool ok = false;
   for (const char* k : known) ok = ok || key == k;
   need(ok, "unsupported parameter: " + key);
@@ -683,6 +723,11 @@ void Booster::set_param(const std::string& key, const std::string& value) {
     concurrent_trees_ = m;
   }
   if (key == "dp_autotune") autotune_ = parse_int(key, value) != 0;
+  if (key == "dp_skip_bin") {
+    const int32_t m = parse_int(key, value);
+    need(m >= 0 && m <= 2, "dp_skip_bin must be 0, 1 or 2");
+    skip_mode_ = m;
+  }
   if (key == "dp_hist_tiles") {
     const int32_t m = parse_int(key, value);
     need(m == 0 || m == 1 || m == 2, "dp_hist_tiles must be 0 (tuned), 1 or 2");
@@ -697,6 +742,11 @@ void Booster::set_param(const std::string& key, const std::string& value) {
     const int32_t m = parse_int(key, value);
     need(m == 0 || (m >= 256 && m <= 4096), "dp_hist_items must be 0 (tuned) or in [256, 4096]");
     forced_hist_.items = m;
+  }
+  if (key == "dp_hist_split") {
+    const int32_t m = parse_int(key, value);
+    need(m == 0 || m == 4 || m == 5, "dp_hist_split must be 0, 4 or 5");
+    forced_hist_.split = m;
   }
   if (key == "dp_sparse_hist") {
     const int32_t m = parse_int(key, value);
@@ -904,7 +954,8 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
                                   uint64_t(n_groups_), uint64_t(sparse_mode_),
                                   uint64_t(concurrent_trees_), uint64_t(autotune_),
                                   uint64_t(forced_hist_.tiles), uint64_t(forced_hist_.unroll),
-                                  uint64_t(forced_hist_.items)};
+                                  uint64_t(forced_hist_.items), uint64_t(forced_hist_.split),
+                                  uint64_t(skip_mode_)};
   auto words = [](std::vector<uint64_t>& v, const void* p, size_t n) {
     for (size_t i = 0; i < n; i += 8) {
       uint64_t w = 0;
@@ -936,40 +987,59 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
     q.rows.resize(dp_layout_bytes(&q.layout));
     launch_tiles_to_rows(q.bins.p, q.layout, q.rows.p, stream_);
   }
+  // Skip bins (matrices without missing values): counted once per matrix.
+  bool skip = false;
+  if (!sparse && q.layout.missing_bin < 0 && skip_mode_ != 0) {
+    if (q.skip_share < 0.0) build_skip_bins(q, stream_);
+    skip = skip_mode_ == 2 || q.skip_share >= kSkipShare;
+  }
   if (record_positions_) positions_.reserve(size_t(N));
   // Histogram launch shapes: forced by dp_hist_* (0 = default for the rest),
   // else tuned on this matrix shape (once per process), else the defaults.
   HistConfig root_cfg, level_cfg;
-  if (forced_hist_.tiles || forced_hist_.unroll || forced_hist_.items) {
+  if (forced_hist_.tiles || forced_hist_.unroll || forced_hist_.items || forced_hist_.split) {
     if (forced_hist_.tiles) root_cfg.tiles = forced_hist_.tiles;
     if (forced_hist_.unroll) root_cfg.unroll = forced_hist_.unroll;
     if (forced_hist_.items) root_cfg.items = forced_hist_.items;
+    root_cfg.split = forced_hist_.split;
     level_cfg = root_cfg;
     tuning_report_ = "{\"forced\":true}";
   } else if (autotune_) {
     const HistTuning& t =
         sparse ? tune_sparse_hist(q.sparse, N, q.layout.n_features, q.bin_stride, gpair_.p,
                                   stream_)
-               : tune_dense_hist(q.layout, q.bins.p, q.rows.p, q.bin_stride, gpair_.p, stream_);
+               : tune_dense_hist(q.layout, q.bins.p, q.rows.p, q.bin_stride, gpair_.p, stream_,
+                                 skip ? q.skip_tiles.p : nullptr);
     root_cfg = t.root;
     level_cfg = t.level;
     tuning_report_ = t.report;
   } else {
     tuning_report_ = "{\"defaults\":true}";
   }
+  {  // the histogram mode beside the launch shapes
+    std::string mode = "{\"layout\":\"";
+    mode += sparse ? "present-value" : "dense";
+    mode += "\",\"skip_bins\":";
+    mode += skip ? "true" : "false";
+    if (q.skip_share >= 0.0) {
+      mode += ",\"skip_share\":";
+      json::put_double(mode, q.skip_share);
+    }
+    tuning_report_ = mode + "," + tuning_report_.substr(1);
+  }
   const int32_t K = n_groups_;
   int32_t S = std::min(K, concurrent_trees_);
   while (int32_t(growers_.size()) < S) growers_.push_back(std::make_unique<Grower>());
   if (growers_.empty()) growers_.push_back(std::make_unique<Grower>());
-  growers_[0]->prepare(q, tp_, (K + S - 1) / S, sparse, root_cfg, level_cfg, stream_);
+  growers_[0]->prepare(q, tp_, (K + S - 1) / S, sparse, root_cfg, level_cfg, skip, stream_);
   const bool eager = growers_[0]->eager();
   if (!eager && S > 1) {  // level-synced trees synchronise per level: one at a time
     S = 1;
-    growers_[0]->prepare(q, tp_, K, sparse, root_cfg, level_cfg, stream_);
+    growers_[0]->prepare(q, tp_, K, sparse, root_cfg, level_cfg, skip, stream_);
   }
   for (int32_t l = 1; l < S; ++l)
     growers_[size_t(l)]->prepare(q, tp_, (K - l + S - 1) / S, sparse, root_cfg, level_cfg,
-                                 stream_);
+                                 skip, stream_);
   while (S > 1 && int32_t(tree_streams_.size()) < S) {
     hipStream_t t;
     DP_HIP(hipStreamCreateWithFlags(&t, hipStreamNonBlocking));

@@ -24,9 +24,21 @@ struct Quantized {
   DeviceBuffer<uint8_t> cols;  // column-major copy: cols[f * n_rows + r]
   DeviceBuffer<uint8_t> rows;  // row-major copy: rows[(r * n_tiles + t) * 16 + j] (on demand)
   SparseBins sparse;           // present-value layout (on demand, mostly-missing matrices)
+  // Skip bins (matrices without missing values, on demand): each feature's most
+  // frequent bin, per feature and per 16-feature tile, and the mean share of
+  // the rows those bins hold (-1: not counted yet).
+  DeviceBuffer<uint8_t> skip_features, skip_tiles;
+  double skip_share = -1.0;
   double sparse_limit = -1.0;  // largest density limit the layout was tried with
   double density = -1.0;       // share of present values, once counted
 };
+
+// Counts each feature's bins (column copy) and fills q.skip_features,
+// q.skip_tiles and q.skip_share; synchronises the stream.
+void build_skip_bins(Quantized& q, hipStream_t s);
+// dp_skip_bin 1 uses skip bins when they hold at least this share of the rows
+// on average (C4's zero pixels: about 0.8; quantile-binned features: 1 / bins).
+constexpr double kSkipShare = 0.2;
 
 class Booster;
 
@@ -87,8 +99,11 @@ class Grower {
   // the 16-feature tiles and the row-major copy (which must then be built).
   // root_cfg / level_cfg: launch shapes of the root (contiguous) and gathered
   // histogram passes (present-value histograms use their items only).
+  // skip: histograms leave each feature's skip bin out (q.skip_tiles and
+  // q.skip_features, which must be built) and the evaluation restores it.
   void prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, bool sparse,
-               const HistConfig& root_cfg, const HistConfig& level_cfg, hipStream_t s);
+               const HistConfig& root_cfg, const HistConfig& level_cfg, bool skip,
+               hipStream_t s);
   // Column sampling of the trees grow() enqueues next (inactive: every
   // feature is a candidate at every node); cs.output is set per tree.
   ColSample colsample;
@@ -147,6 +162,8 @@ class Grower {
   int32_t root_tiles_ = 0, root_items_ = 0;
   bool root_sparse_ = false;
   HistConfig root_cfg_, level_cfg_, root_made_;
+  const uint8_t* skip_tiles_ = nullptr;     // the matrix's skip bins when in use
+  const uint8_t* skip_features_ = nullptr;
 };
 
 // Normalised hyperparameter JSON (see DPValidateHyperparameters).
@@ -235,9 +252,12 @@ class Booster {
   bool record_positions_ = false;
   bool use_graphs_ = true;
   bool autotune_ = true;        // dp_autotune: time the histogram launch shapes (tune.cpp)
-  HistConfig forced_hist_{0, 0, 0};  // dp_hist_tiles / _unroll / _items; 0 = not forced
+  HistConfig forced_hist_{0, 0, 0, 0};  // dp_hist_tiles / _unroll / _items / _split; 0 = not forced
   std::string tuning_report_ = "{}";
   int32_t sparse_mode_ = 1;  // dp_sparse_hist: 0 never, 1 when <= 1/4 present, 2 with any NaN
+  // dp_skip_bin (matrices without missing values): 0 never, 1 when the skip
+  // bins hold at least kSkipShare of the rows on average, 2 always.
+  int32_t skip_mode_ = 1;
   bool labels_checked_ = false;
   std::vector<std::pair<std::vector<uint64_t>, hipGraphExec_t>> graphs_;  // newest last
   hipStream_t stream_ = nullptr;

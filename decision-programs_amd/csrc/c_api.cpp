@@ -607,6 +607,18 @@ int dp_hist_accumulate(dp_workspace ws, const uint8_t* bins, const dp_bin_layout
   });
 }
 
+int dp_hist_tuning(const dp_bin_layout* layout, int32_t bin_stride, bst_ulong* out_len,
+                   const char** out) {
+  static thread_local std::string result;
+  return guarded([&] {
+    dp::need(layout && out_len && out, "null argument");
+    const dp::HistTuning* t = dp::find_dense_tuning(*layout, bin_stride, false);
+    result = t ? t->report : "{}";
+    *out = result.c_str();
+    *out_len = bst_ulong(result.size());
+  });
+}
+
 int dp_hist_subtract(const int64_t* parent, const int64_t* built, int64_t* sibling, int64_t n,
                      void* stream) {
   return guarded([&] {

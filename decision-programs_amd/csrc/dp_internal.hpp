@@ -270,23 +270,33 @@ void launch_iota_u32(uint32_t* p, int64_t n, hipStream_t s);
 
 // Launch shape of the dense histogram kernel, chosen per matrix shape by the
 // autotuner (tune.cpp) or forced by booster parameters: 16-feature tiles per
-// work item (1 or 2), rows per lane per pipeline step (1 or 2), and the work
-// items a pass aims at (which sets the rows per item).
+// work item (1 or 2), rows per lane per pipeline step (1 or 2), the work
+// items a pass aims at (which sets the rows per item), and with two tiles the
+// lane bit (4 or 5; 0 = none) that swaps a lane's tile order.
 struct HistConfig {
   int32_t tiles = 1;
   int32_t unroll = 2;
   int32_t items = 1024;
+  int32_t split = 0;
 };
 
 // Histograms: every work item accumulates into hist[slot]; hist must be zero.
 // Direct items write hist; the others write partial (int64 [slot][bin_stride * 32]).
 // row_major: optional row-major copy of the bins (launch_tiles_to_rows), read
 // for gathered rows.  The work items must come from the same cfg.tiles.
+// skip (matrices without missing values): per tile, the 16 features' skip
+// bins ([n_tiles][16] bytes); rows in a feature's skip bin add nothing, so that
+// bin's sums stay zero (the split evaluation restores them from the node's
+// totals: launch_evaluate's skip argument).
 void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t* gpair,
                  const uint32_t* ridx, const HistWork* work, int32_t n_work,
                  const int32_t* n_work_dev, int32_t bin_stride, int64_t* hist,
                  int64_t* partial, hipStream_t s, const uint8_t* row_major = nullptr,
-                 const HistConfig& cfg = HistConfig{});
+                 const HistConfig& cfg = HistConfig{}, const uint8_t* skip = nullptr);
+// counts[f][b] = rows whose bin of feature f is b ([n_features][256] uint32),
+// from the column copy cols[f][row].
+void launch_bin_counts(const uint8_t* cols, int64_t n_rows, int32_t n_features,
+                       unsigned int* counts, hipStream_t s);
 // Completes the histograms of launch_hist: sums partial tiles, writes built
 // and sibling node histograms.  accumulate: add the sums to hist instead of
 // storing them (then no job may rely on a direct item).
@@ -349,7 +359,11 @@ bool launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_node
                      int32_t n_features, int32_t bin_stride, const int32_t* n_bins,
                      const int64_t* node_sums, const int32_t* exps, int32_t exp_g, int32_t exp_h,
                      const dp_train_param& param, void* scratch, dp_split_record* out,
-                     hipStream_t s, bool select = true, const uint32_t* fmask = nullptr);
+                     hipStream_t s, bool select = true, const uint32_t* fmask = nullptr,
+                     const uint8_t* skip_bins = nullptr);
+// skip_bins ([n_features] bytes, matrices without missing values): the
+// histograms leave each feature's skip bin at zero (launch_hist's skip); the
+// node's remaining sums (totals minus the bins) are that bin's.
 // Column sampling of one level (ColSample active): masks[node][ceil(F / 32)]
 // gets each node's feature sample (bit f set: feature f is a candidate), for
 // the node count *n_dev (n_host when null; n_host bounds the grid).  depth is
@@ -529,7 +543,9 @@ bool launch_gradients(int32_t objective, const float* margin, const float* label
                       void* quant_scratch, hipStream_t s);
 // Quantiser: exps int32 [n_classes][2]; gpair int32 [n_classes][n_rows][2];
 // sums int64 [n_classes][2]; scratch holds quantise_scratch_bytes.
-constexpr int kQuantBlocks = 512;  // workgroups (and reduction slots) per class
+// Most workgroups (and reduction slots) per class: eight 256-thread workgroups
+// per CU keep enough loads in flight for the streaming passes over 10M rows.
+constexpr int kQuantBlocks = 2048;
 int quantise_blocks(int64_t n_rows);
 // The quantiser's int64 sum slots in its scratch: class k's quantise_blocks
 // (g, h) pairs start at pair k * quantise_blocks(n_rows).

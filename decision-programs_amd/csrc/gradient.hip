@@ -283,7 +283,11 @@ void launch_check_labels(const float* label, int64_t n, int32_t objective, int32
   DP_HIP(hipGetLastError());
 }
 
-int quantise_blocks(int64_t n_rows) { return grid_for(n_rows, kQuantThreads, kQuantBlocks); }
+// At least eight rows per thread: every quantise workgroup re-reads all the
+// maxima slots, so a 1M-row pass keeps about 500 of them, a 10M-row one 2048.
+int quantise_blocks(int64_t n_rows) {
+  return grid_for(n_rows, kQuantThreads * 8, kQuantBlocks);
+}
 
 size_t quantise_scratch_bytes(int64_t n_rows, int32_t n_classes) {
   const size_t slots = size_t(n_classes) * size_t(quantise_blocks(n_rows));

@@ -106,9 +106,24 @@ constexpr int kHistThreads = 1024;
 // the bins and gradients one block ahead.  Workgroups loop over items (item =
 // blockIdx.x + k * gridDim.x); with a grid that is a multiple of 8, item i
 // still runs on XCD i mod 8.
-template <bool GATHER, bool MISSING, int TPW, int U>
+//
+// SPLIT (two tiles per item only; 0, 4 or 5): lanes whose bit SPLIT of the
+// lane index is set take the item's two tiles in the other order.  Each
+// 64-bit atomic instruction then updates 32 features, each from two lanes
+// instead of four, which halves the lanes that can collide on one (feature,
+// bin) -- the same-address conflicts of features with few live bins.  Bit 4
+// alternates 16-lane rows, bit 5 splits the wavefront into halves.
+//
+// MODE 2 (matrices without missing values): `skip` holds, per tile, the 16
+// features' most frequent bins; a lane whose byte equals its feature's skip
+// bin issues no atomics (the bin's sums are the node's totals minus the other
+// bins', which the split evaluation restores).  On data dominated by one value
+// per feature (C4's zero pixels) this removes most atomics and their
+// same-address conflicts.  MODE 1 is the missing-byte skip above; MODE 0 none.
+template <bool GATHER, int MODE, int TPW, int U, int SPLIT = 0>
 __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8 / TPW, 8 / TPW))) void hist_kernel(
-    const uint8_t* __restrict__ bins, int64_t n_rows, int32_t n_features, int32_t n_tiles,
+    const uint8_t* __restrict__ bins, const uint8_t* __restrict__ skip, int64_t n_rows,
+    int32_t n_features, int32_t n_tiles,
     const int2* __restrict__ gpair, const uint32_t* __restrict__ ridx,
     const HistWork* __restrict__ work, int32_t n_work_host,
     const int32_t* __restrict__ n_work_dev, int32_t bin_stride,
@@ -136,6 +151,23 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8 
   if (w.begin >= w.end) continue;  // padding item (uniform per workgroup)
   // tiles of this item that exist (uniform per workgroup)
   const int nt = TPW == 1 ? 1 : (w.tile + TPW <= n_tiles ? TPW : n_tiles - w.tile);
+  // This lane's tile order: swapped when SPLIT applies and both tiles exist.
+  const int swap = (SPLIT > 0 && nt == 2) ? int((threadIdx.x >> SPLIT) & 1u) : 0;
+  // MODE 2: each tile's skip bins, rotated like the row bytes (byte k of the
+  // rotated vector is the skip bin of the feature this lane takes at step k).
+  uint32_t sk[TPW][4];
+  if constexpr (MODE == 2) {
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) {
+      const uint4 s4 =
+          *reinterpret_cast<const uint4*>(skip + int64_t(w.tile + (j < nt ? j ^ swap : 0)) * kTile);
+      sk[j][0] = s4.x;
+      sk[j][1] = s4.y;
+      sk[j][2] = s4.z;
+      sk[j][3] = s4.w;
+      rotate16(sk[j], rot);
+    }
+  }
   for (int e = threadIdx.x; e < nt * kLdsWords; e += kHistThreads) lds[e] = 0ull;
   __syncthreads();
 
@@ -160,7 +192,7 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8 
       const uint8_t* src = tile + int64_t(r) * row_step;
 #pragma unroll
       for (int j = 0; j < TPW; ++j)  // a missing second tile re-reads the first
-        v[b][u][j] = *reinterpret_cast<const uint4*>(src + (j < nt ? j : 0) * tile_step);
+        v[b][u][j] = *reinterpret_cast<const uint4*>(src + (j < nt ? j ^ swap : 0) * tile_step);
       q[b][u] = gpair[r];
     }
   };
@@ -175,12 +207,14 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8 
         if (j >= nt) break;  // uniform per workgroup
         uint32_t a[4] = {v[b][u][j].x, v[b][u][j].y, v[b][u][j].z, v[b][u][j].w};
         rotate16(a, rot);
-        lds_u8* const base_j = lds_base + j * (kLdsWords * 8);
+        lds_u8* const base_j = lds_base + (j ^ swap) * (kLdsWords * 8);
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
           const uint32_t sel = 0x0c0c0000u | ((4u + uint32_t(k & 3)) << 8) | uint32_t(k & 3);
           const uint32_t off = __builtin_amdgcn_perm(a[k >> 2], slotw[k >> 2], sel);
-          if (MISSING && off >= 255u * 256u) continue;  // byte 255: missing value
+          if (MODE == 1 && off >= 255u * 256u) continue;  // byte 255: missing value
+          if (MODE == 2 && off == __builtin_amdgcn_perm(sk[j][k >> 2], slotw[k >> 2], sel))
+            continue;  // the feature's skip bin
           lds_u64* p = (lds_u64*)(base_j + off);
           lds_add(p, g);
           lds_add(p + 16, h);
@@ -489,11 +523,25 @@ int32_t make_hist_work(const dp_bin_layout& layout, const int64_t* begin, const 
 }
 
 namespace {
-template <bool GATHER, bool MISSING>
+template <bool GATHER, int MODE>
 auto hist_instance(const HistConfig& cfg) {
-  if (cfg.tiles == 2)
-    return cfg.unroll == 1 ? hist_kernel<GATHER, MISSING, 2, 1> : hist_kernel<GATHER, MISSING, 2, 2>;
-  return cfg.unroll == 1 ? hist_kernel<GATHER, MISSING, 1, 1> : hist_kernel<GATHER, MISSING, 1, 2>;
+  if (cfg.tiles == 2) {
+    if (cfg.split == 4)
+      return cfg.unroll == 1 ? hist_kernel<GATHER, MODE, 2, 1, 4>
+                             : hist_kernel<GATHER, MODE, 2, 2, 4>;
+    if (cfg.split == 5)
+      return cfg.unroll == 1 ? hist_kernel<GATHER, MODE, 2, 1, 5>
+                             : hist_kernel<GATHER, MODE, 2, 2, 5>;
+    return cfg.unroll == 1 ? hist_kernel<GATHER, MODE, 2, 1, 0>
+                           : hist_kernel<GATHER, MODE, 2, 2, 0>;
+  }
+  return cfg.unroll == 1 ? hist_kernel<GATHER, MODE, 1, 1> : hist_kernel<GATHER, MODE, 1, 2>;
+}
+
+template <bool GATHER>
+auto hist_mode(int mode, const HistConfig& cfg) {
+  return mode == 1 ? hist_instance<GATHER, 1>(cfg)
+                   : (mode == 2 ? hist_instance<GATHER, 2>(cfg) : hist_instance<GATHER, 0>(cfg));
 }
 }  // namespace
 
@@ -501,11 +549,12 @@ void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t
                  const uint32_t* ridx, const HistWork* work, int32_t n_work,
                  const int32_t* n_work_dev, int32_t bin_stride, int64_t* hist,
                  int64_t* partial, hipStream_t s, const uint8_t* row_major,
-                 const HistConfig& cfg) {
+                 const HistConfig& cfg, const uint8_t* skip) {
   if (n_work <= 0) return;
   need(bin_stride >= 1 && bin_stride <= kMaxBins, "histogram bin stride out of range");
   need(layout.tile_width == kTile, "histogram kernel needs 16-feature tiles");
-  need((cfg.tiles == 1 || cfg.tiles == 2) && (cfg.unroll == 1 || cfg.unroll == 2),
+  need((cfg.tiles == 1 || cfg.tiles == 2) && (cfg.unroll == 1 || cfg.unroll == 2) &&
+           (cfg.split == 0 || cfg.split == 4 || cfg.split == 5),
        "histogram configuration out of range");
   auto* out = reinterpret_cast<unsigned long long*>(hist);
   auto* part = reinterpret_cast<unsigned long long*>(partial);
@@ -525,9 +574,9 @@ void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t
   const int64_t tile_step = rows ? kTile : layout.n_rows * kTile;
   const int64_t row_step = rows ? int64_t(layout.n_tiles) * kTile : kTile;
   const bool missing = layout.missing_bin >= 0;
-  auto kernel = ridx ? (missing ? hist_instance<true, true>(cfg) : hist_instance<true, false>(cfg))
-                     : (missing ? hist_instance<false, true>(cfg)
-                                : hist_instance<false, false>(cfg));
+  need(!(missing && skip), "skip bins apply to matrices without missing values");
+  const int mode = missing ? 1 : (skip ? 2 : 0);
+  auto kernel = ridx ? hist_mode<true>(mode, cfg) : hist_mode<false>(mode, cfg);
   const size_t lds = size_t(cfg.tiles) * kLdsWords * sizeof(unsigned long long);
   if (lds > 65536) {  // beyond the default dynamic LDS limit (once per instantiation)
     static std::mutex lock;
@@ -539,7 +588,7 @@ void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t
       raised.push_back(k);
     }
   }
-  hipLaunchKernelGGL(kernel, dim3(grid), dim3(kHistThreads), lds, s, src, layout.n_rows,
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(kHistThreads), lds, s, src, skip, layout.n_rows,
                      layout.n_features, layout.n_tiles, gp, ridx, work, n_work, n_work_dev,
                      bin_stride, out, part, tile_step, row_step);
   DP_HIP(hipGetLastError());

@@ -328,7 +328,44 @@ __global__ void sparse_fill_kernel(const uint8_t* __restrict__ bins, int64_t n_r
   }
 }
 
+// counts[f][b] += rows of this workgroup's row range whose bin of feature f is
+// b, from the column copy.  Workgroup i takes row range i % blocks_per_feature
+// of feature i / blocks_per_feature; each wavefront counts into its own 256 LDS
+// counters, then the counters go to global memory.
+constexpr int kCountThreads = 256;
+__global__ __launch_bounds__(kCountThreads) void bin_counts_kernel(
+    const uint8_t* __restrict__ cols, int64_t n_rows, int64_t rows_per_block,
+    int64_t blocks_per_feature, unsigned int* __restrict__ counts) {
+  __shared__ unsigned int c[kCountThreads / 64][256];
+  const int wave = threadIdx.x >> 6;
+  for (int i = threadIdx.x; i < (kCountThreads / 64) * 256; i += kCountThreads) (&c[0][0])[i] = 0u;
+  __syncthreads();
+  const int64_t f = int64_t(blockIdx.x) / blocks_per_feature;
+  const uint8_t* col = cols + f * n_rows;
+  const int64_t r0 = (int64_t(blockIdx.x) % blocks_per_feature) * rows_per_block;
+  const int64_t r1 = r0 + rows_per_block < n_rows ? r0 + rows_per_block : n_rows;
+  for (int64_t r = r0 + threadIdx.x; r < r1; r += kCountThreads) atomicAdd(&c[wave][col[r]], 1u);
+  __syncthreads();
+  for (int b = threadIdx.x; b < 256; b += kCountThreads) {
+    unsigned int t = 0;
+    for (int w = 0; w < kCountThreads / 64; ++w) t += c[w][b];
+    if (t) atomicAdd(&counts[f * 256 + b], t);
+  }
+}
+
 }  // namespace
+
+void launch_bin_counts(const uint8_t* cols, int64_t n_rows, int32_t n_features,
+                       unsigned int* counts, hipStream_t s) {
+  if (n_rows <= 0 || n_features <= 0) return;
+  launch_fill_u8(reinterpret_cast<uint8_t*>(counts), int64_t(n_features) * 256 * 4, 0, s);
+  const int64_t per = 1 << 16;
+  const int64_t blocks = (n_rows + per - 1) / per;
+  need(blocks * n_features < (int64_t(1) << 31), "bin counts grid too large");
+  hipLaunchKernelGGL(bin_counts_kernel, dim3(unsigned(blocks * n_features)), dim3(kCountThreads),
+                     0, s, cols, n_rows, per, blocks, counts);
+  DP_HIP(hipGetLastError());
+}
 
 void launch_tiles_to_rows(const uint8_t* bins, const dp_bin_layout& layout, uint8_t* rows,
                           hipStream_t s) {

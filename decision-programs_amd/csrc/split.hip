@@ -110,7 +110,7 @@ __device__ __forceinline__ void load_feature(const long long* __restrict__ hist,
 // the bins, both missing directions, and the argmax.  Every lane returns the
 // same result; loss is -inf when the feature has no valid candidate.
 template <int BPL>
-__device__ __forceinline__ Cand feature_best(const FeatBins<BPL>& d, int32_t f, int nb,
+__device__ __forceinline__ Cand feature_best(const FeatBins<BPL>& d, int32_t f, int nb, int skip,
                                              long long gp, long long hp, double parent_gain,
                                              double ug, double uh, const Param& p) {
   const int lane = threadIdx.x & 63;
@@ -127,7 +127,15 @@ __device__ __forceinline__ Cand feature_best(const FeatBins<BPL>& d, int32_t f, 
   const long long ig = wave_inclusive_sum(rg), ih = wave_inclusive_sum(rh);
   const long long total_g = readlane64(ig, 63), total_h = readlane64(ih, 63);
   const long long og = ig - rg, oh = ih - rh;  // exclusive offset of this lane
-  const long long mg = gp - total_g, mh = hp - total_h;
+  // The node's rows the bins do not hold: the missing rows, or (skip >= 0, no
+  // missing values) the rows of the skipped bin, which the prefixes from that
+  // bin on take back.
+  long long mg = gp - total_g, mh = hp - total_h, kg = 0, kh = 0;
+  if (skip >= 0) {
+    kg = mg;
+    kh = mh;
+    mg = mh = 0;
+  }
 
   Cand c;
   c.loss = -INFINITY;
@@ -139,7 +147,8 @@ __device__ __forceinline__ Cand feature_best(const FeatBins<BPL>& d, int32_t f, 
   for (int j = 0; j < BPL; ++j) {
     const int b = lane * BPL + j;
     if (b < nb) {
-      const long long lg = og + sg[j], lh = oh + sh[j];
+      const long long lg = og + sg[j] + (b >= skip && skip >= 0 ? kg : 0);
+      const long long lh = oh + sh[j] + (b >= skip && skip >= 0 ? kh : 0);
       const double right_missing = split_loss(p, lg, lh, gp - lg, hp - lh, ug, uh, parent_gain);
       // Without missing rows both directions are the same candidate.
       const double left_missing =
@@ -184,7 +193,8 @@ __global__ __launch_bounds__(64 * kFeatWaves) void evaluate_features_kernel(
     const int32_t* __restrict__ n_nodes_dev, int32_t n_features, int32_t bin_stride,
     const int32_t* __restrict__ n_bins, const long long* __restrict__ node_sums,
     const int32_t* __restrict__ exps, int32_t exp_g_host, int32_t exp_h_host, Param p,
-    const uint32_t* __restrict__ fmask, FeatCand* __restrict__ cand) {
+    const uint32_t* __restrict__ fmask, const uint8_t* __restrict__ skip_bins,
+    FeatCand* __restrict__ cand) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int32_t n_nodes = n_nodes_dev ? *n_nodes_dev : n_nodes_host;
   const int32_t groups = (n_features + kFeatWaves - 1) / kFeatWaves;
@@ -202,7 +212,8 @@ __global__ __launch_bounds__(64 * kFeatWaves) void evaluate_features_kernel(
     const double parent_gain = calc_gain(p, double(gp) * ug, double(hp) * uh);
     // A feature outside the node's sample has no bins to split at: loss -inf.
     const int nb = feature_allowed(fmask, node, f, n_features) ? n_bins[f] : 0;
-    const Cand c = feature_best<BPL>(bins, f, nb, gp, hp, parent_gain, ug, uh, p);
+    const int skip = skip_bins ? int(skip_bins[f]) : -1;
+    const Cand c = feature_best<BPL>(bins, f, nb, skip, gp, hp, parent_gain, ug, uh, p);
     if (lane == 0) cand[int64_t(node) * n_features + f] = FeatCand{c.loss, c.gl, c.hl, c.bin, c.dl};
   }
 }
@@ -226,7 +237,8 @@ __global__ __launch_bounds__(256) void evaluate_features_seg_kernel(
     const int32_t* __restrict__ n_nodes_dev, int32_t n_features, int32_t bin_stride,
     const int32_t* __restrict__ n_bins, const long long* __restrict__ node_sums,
     const int32_t* __restrict__ exps, int32_t exp_g_host, int32_t exp_h_host, Param p,
-    const uint32_t* __restrict__ fmask, FeatCand* __restrict__ cand) {
+    const uint32_t* __restrict__ fmask, const uint8_t* __restrict__ skip_bins,
+    FeatCand* __restrict__ cand) {
   constexpr int BPL = 4;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int seg = lane >> 4, sub = lane & 15;
@@ -273,7 +285,14 @@ __global__ __launch_bounds__(256) void evaluate_features_seg_kernel(
     ih += dpp64<0x118>(ih, 0);
     const long long total_g = row_shuffle64(ig, row_last), total_h = row_shuffle64(ih, row_last);
     const long long og = ig - rg, oh = ih - rh;
-    const long long mg = gp - total_g, mh = hp - total_h;
+    // as feature_best: a skipped bin's rows return at the prefixes from that bin
+    const int skip = live && skip_bins ? int(skip_bins[f]) : -1;
+    long long mg = gp - total_g, mh = hp - total_h, kg = 0, kh = 0;
+    if (skip >= 0) {
+      kg = mg;
+      kh = mh;
+      mg = mh = 0;
+    }
 
     Cand c;
     c.loss = -INFINITY;
@@ -285,7 +304,8 @@ __global__ __launch_bounds__(256) void evaluate_features_seg_kernel(
     for (int j = 0; j < BPL; ++j) {
       const int b = sub * BPL + j;
       if (b < nb) {
-        const long long lg = og + sg[j], lh = oh + sh[j];
+        const long long lg = og + sg[j] + (b >= skip && skip >= 0 ? kg : 0);
+        const long long lh = oh + sh[j] + (b >= skip && skip >= 0 ? kh : 0);
         const double right_missing = split_loss(p, lg, lh, gp - lg, hp - lh, ug, uh, parent_gain);
         const double left_missing =
             (mg == 0 && mh == 0)
@@ -334,7 +354,8 @@ __global__ __launch_bounds__(64 * kNodeWaves) void evaluate_nodes_kernel(
     const int32_t* __restrict__ n_nodes_dev, int32_t n_features, int32_t bin_stride,
     const int32_t* __restrict__ n_bins, const long long* __restrict__ node_sums,
     const int32_t* __restrict__ exps, int32_t exp_g_host, int32_t exp_h_host, Param p,
-    const uint32_t* __restrict__ fmask, dp_split_record* __restrict__ out) {
+    const uint32_t* __restrict__ fmask, const uint8_t* __restrict__ skip_bins,
+    dp_split_record* __restrict__ out) {
   __shared__ Cand wave_best[kNodeWaves];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int32_t n_nodes = n_nodes_dev ? *n_nodes_dev : n_nodes_host;
@@ -357,7 +378,8 @@ __global__ __launch_bounds__(64 * kNodeWaves) void evaluate_nodes_kernel(
       if (f + kNodeWaves < n_features)
         load_feature<BPL>(hist, node, f + kNodeWaves, n_features, bin_stride, nxt);
       const int nb = feature_allowed(fmask, node, f, n_features) ? n_bins[f] : 0;
-      const Cand c = feature_best<BPL>(cur, f, nb, gp, hp, parent_gain, ug, uh, p);
+      const int skip = skip_bins ? int(skip_bins[f]) : -1;
+      const Cand c = feature_best<BPL>(cur, f, nb, skip, gp, hp, parent_gain, ug, uh, p);
       if (c.loss > -INFINITY && better(c, best)) best = c;
       cur = nxt;
     }
@@ -512,7 +534,8 @@ bool launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_node
                      int32_t n_features, int32_t bin_stride, const int32_t* n_bins,
                      const int64_t* node_sums, const int32_t* exps, int32_t exp_g, int32_t exp_h,
                      const dp_train_param& param, void* scratch, dp_split_record* out,
-                     hipStream_t s, bool select, const uint32_t* fmask) {
+                     hipStream_t s, bool select, const uint32_t* fmask,
+                     const uint8_t* skip_bins) {
   if (n_nodes <= 0) return true;
   need(bin_stride >= 1 && bin_stride <= kMaxBins, "split bin stride out of range");
   need(n_features >= 1, "split evaluation needs at least one feature");
@@ -524,13 +547,13 @@ bool launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_node
     const dim3 grid(n_nodes < 2048 ? n_nodes : 2048), block(64 * kNodeWaves);
     if (bin_stride <= 64)
       hipLaunchKernelGGL(evaluate_nodes_kernel<1>, grid, block, 0, s, h, n_nodes, n_nodes_dev,
-                         n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p, fmask, out);
+                         n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p, fmask, skip_bins, out);
     else if (bin_stride <= 128)
       hipLaunchKernelGGL(evaluate_nodes_kernel<2>, grid, block, 0, s, h, n_nodes, n_nodes_dev,
-                         n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p, fmask, out);
+                         n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p, fmask, skip_bins, out);
     else
       hipLaunchKernelGGL(evaluate_nodes_kernel<4>, grid, block, 0, s, h, n_nodes, n_nodes_dev,
-                         n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p, fmask, out);
+                         n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p, fmask, skip_bins, out);
     DP_HIP(hipGetLastError());
     return true;
   }
@@ -539,7 +562,7 @@ bool launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_node
     const int64_t items = int64_t(n_nodes) * ((n_features + kSegFeatures - 1) / kSegFeatures);
     hipLaunchKernelGGL(evaluate_features_seg_kernel, dim3(items < 2048 ? items : 2048), dim3(256),
                        0, s, h, n_nodes, n_nodes_dev, n_features, bin_stride, n_bins, sums, exps,
-                       exp_g, exp_h, p, fmask, cand);
+                       exp_g, exp_h, p, fmask, skip_bins, cand);
     DP_HIP(hipGetLastError());
     if (!select) return false;
     hipLaunchKernelGGL(select_splits_kernel, dim3(n_nodes < 1024 ? n_nodes : 1024),
@@ -555,11 +578,11 @@ bool launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_node
   if (bin_stride <= 128)
     hipLaunchKernelGGL(evaluate_features_kernel<2>, dim3(grid), block, 0, s, h, n_nodes,
                        n_nodes_dev, n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p,
-                       fmask, cand);
+                       fmask, skip_bins, cand);
   else
     hipLaunchKernelGGL(evaluate_features_kernel<4>, dim3(grid), block, 0, s, h, n_nodes,
                        n_nodes_dev, n_features, bin_stride, n_bins, sums, exps, exp_g, exp_h, p,
-                       fmask, cand);
+                       fmask, skip_bins, cand);
   DP_HIP(hipGetLastError());
   if (!select) return false;
   hipLaunchKernelGGL(select_splits_kernel, dim3(n_nodes < 1024 ? n_nodes : 1024),

@@ -8,6 +8,8 @@
 //                         (128 KiB, one per CU; each row's gradient pair is
 //                         read once for 32 features instead of 16);
 //   rows per lane per pipeline step   1 or 2;
+//   with two tiles, the lane bit (4, 5 or none) that swaps a lane's tile
+//                         order (fewer lanes per (feature, bin) per atomic);
 //   work items per pass   512, 1024 or 2048 (fewer, longer row chunks write
 //                         fewer partial tiles; more balance the CUs better).
 // The contiguous (root) pass is timed over the whole matrix; the gathered pass
@@ -36,16 +38,20 @@ std::vector<HistConfig> dense_candidates(int32_t n_tiles) {
   std::vector<HistConfig> c;
   for (int32_t tiles : {1, 2}) {
     if (tiles > n_tiles) continue;
-    for (int32_t unroll : {1, 2})
-      for (int32_t items : {512, 1024, 2048}) c.push_back(HistConfig{tiles, unroll, items});
+    for (int32_t split : {0, 4, 5}) {
+      if (tiles == 1 && split) continue;
+      for (int32_t unroll : {1, 2})
+        for (int32_t items : {512, 1024, 2048})
+          c.push_back(HistConfig{tiles, unroll, items, split});
+    }
   }
   return c;
 }
 
 std::string config_json(const HistConfig& c) {
-  char b[96];
-  std::snprintf(b, sizeof b, "{\"tiles\":%d,\"unroll\":%d,\"items\":%d}", c.tiles, c.unroll,
-                c.items);
+  char b[112];
+  std::snprintf(b, sizeof b, "{\"tiles\":%d,\"unroll\":%d,\"items\":%d,\"split\":%d}", c.tiles,
+                c.unroll, c.items, c.split);
   return b;
 }
 
@@ -72,6 +78,7 @@ struct Pass {
   const dp_bin_layout* L;
   const uint8_t* bins;
   const uint8_t* rows_major;  // gathered pass: row-major copy, ridx every other row
+  const uint8_t* skip;        // skip bins per tile, or null
   const uint32_t* ridx;
   int64_t rows;
   int32_t bin_stride;
@@ -92,7 +99,7 @@ double time_dense(const Pass& p, const HistConfig& cfg, hipStream_t s) {
   const double ms = time_ms(
       [&] {
         launch_hist(p.bins, *p.L, p.gpair, p.ridx, dw.p, int32_t(w.size()), nullptr,
-                    p.bin_stride, p.out, partial.p, s, p.rows_major, cfg);
+                    p.bin_stride, p.out, partial.p, s, p.rows_major, cfg, p.skip);
         launch_hist_reduce(partial.p, dj.p, 1, nullptr, p.L->n_tiles, p.L->n_features,
                            p.bin_stride, nullptr, p.out, false, s);
       },
@@ -127,15 +134,16 @@ HistConfig pick(const std::vector<HistConfig>& cands, Time&& time, std::string& 
 
 const HistTuning& tune_dense_hist(const dp_bin_layout& L, const uint8_t* bins,
                                   const uint8_t* rows_major, int32_t bin_stride,
-                                  const int32_t* gpair, hipStream_t s) {
-  const Key key{L.n_rows, L.n_features, bin_stride, L.missing_bin, rows_major ? 1 : 0, 0};
+                                  const int32_t* gpair, hipStream_t s, const uint8_t* skip) {
+  const Key key{L.n_rows, L.n_features, bin_stride, L.missing_bin, rows_major ? 1 : 0,
+                skip ? 1 : 0};
   std::lock_guard<std::mutex> hold(g_lock);
   auto it = g_cache.find(key);
   if (it != g_cache.end()) return it->second;
   HistTuning t;
   const auto cands = dense_candidates(L.n_tiles);
   DeviceBuffer<int64_t> out(size_t(L.n_features) * size_t(bin_stride) * 2);
-  Pass root{&L, bins, nullptr, nullptr, L.n_rows, bin_stride, gpair, out.p};
+  Pass root{&L, bins, nullptr, skip, nullptr, L.n_rows, bin_stride, gpair, out.p};
   std::string report = "{";
   t.root = pick(cands, [&](const HistConfig& c) { return time_dense(root, c, s); }, report,
                 "root");
@@ -147,7 +155,7 @@ const HistTuning& tune_dense_hist(const dp_bin_layout& L, const uint8_t* bins,
     for (int64_t i = 0; i < half; ++i) ids[size_t(i)] = uint32_t(2 * i);
     DeviceBuffer<uint32_t> ridx(ids.size());
     DP_HIP(hipMemcpyAsync(ridx.p, ids.data(), ridx.bytes(), hipMemcpyHostToDevice, s));
-    Pass level{&L, bins, rows_major, ridx.p, half, bin_stride, gpair, out.p};
+    Pass level{&L, bins, rows_major, skip, ridx.p, half, bin_stride, gpair, out.p};
     report += ",";
     t.level = pick(cands, [&](const HistConfig& c) { return time_dense(level, c, s); }, report,
                    "gathered");
@@ -158,6 +166,13 @@ const HistTuning& tune_dense_hist(const dp_bin_layout& L, const uint8_t* bins,
             config_json(t.level) + "}}";
   t.report = report;
   return g_cache.emplace(key, std::move(t)).first->second;
+}
+
+const HistTuning* find_dense_tuning(const dp_bin_layout& L, int32_t bin_stride, bool gathered) {
+  const Key key{L.n_rows, L.n_features, bin_stride, L.missing_bin, gathered ? 1 : 0, 0};
+  std::lock_guard<std::mutex> hold(g_lock);
+  auto it = g_cache.find(key);
+  return it == g_cache.end() ? nullptr : &it->second;
 }
 
 const HistTuning& tune_sparse_hist(const SparseBins& sp, int64_t n_rows, int32_t n_features,

@@ -19,9 +19,14 @@ struct HistTuning {
 // read (null: only the root pass is tuned; level = root).  gpair: any
 // [n_rows][2] pairs (the timing does not depend on their values).  Cached per
 // process by (rows, features, bins, missing, gathered); synchronises `s`.
+// skip: the matrix's skip bins per tile when the histograms leave them out.
 const HistTuning& tune_dense_hist(const dp_bin_layout& layout, const uint8_t* bins,
                                   const uint8_t* rows_major, int32_t bin_stride,
-                                  const int32_t* gpair, hipStream_t s);
+                                  const int32_t* gpair, hipStream_t s,
+                                  const uint8_t* skip = nullptr);
+// The cached dense tuning of a shape, or null when it has not been tuned.
+const HistTuning* find_dense_tuning(const dp_bin_layout& layout, int32_t bin_stride,
+                                    bool gathered);
 // Present-value layout: the work-item count of its passes.
 const HistTuning& tune_sparse_hist(const SparseBins& sp, int64_t n_rows, int32_t n_features,
                                    int32_t bin_stride, const int32_t* gpair, hipStream_t s);

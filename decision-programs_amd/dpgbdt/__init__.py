@@ -131,6 +131,8 @@ def load():
         "dp_hist_accumulate": (c_int, [H, c_void_p, POINTER(BinLayout), c_void_p, c_void_p,
                                        c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p]),
         "dp_hist_subtract": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
+        "dp_hist_tuning": (c_int, [POINTER(BinLayout), c_int32, POINTER(c_uint64),
+                                   POINTER(c_char_p)]),
         "dp_evaluate_splits": (c_int, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p,
                                        c_int32, c_int32, POINTER(TrainParam), c_void_p,
                                        c_void_p]),

@@ -149,6 +149,16 @@ def hist_accumulate(ws, bins, lay, gpair, segments, hist, ridx=None):
     return hist
 
 
+def hist_tuning(lay, bin_stride):
+    """The autotuner's report for contiguous histograms of this layout ({} before tuning)."""
+    import json
+
+    n, out = ctypes.c_uint64(), ctypes.c_char_p()
+    check(load().dp_hist_tuning(ctypes.byref(lay), bin_stride, ctypes.byref(n),
+                                ctypes.byref(out)))
+    return json.loads(ctypes.string_at(out, n.value).decode())
+
+
 def hist_subtract(parent, built):
     import torch
 

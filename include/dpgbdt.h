@@ -254,6 +254,14 @@ int dp_hist_accumulate(dp_workspace ws, const uint8_t* bins, const dp_bin_layout
                        const int64_t* end, int32_t n_nodes, int32_t bin_stride, int64_t* hist,
                        void* stream);
 
+/* The launch shape the autotuner chose for contiguous histograms of this
+ * layout and bin stride (JSON: every candidate's time and the choice; "{}"
+ * before the first contiguous dp_hist_build / dp_hist_accumulate of the
+ * shape, which tunes it).  No counterpart in the reference.  Thread-local
+ * string, valid until the next call on this thread. */
+int dp_hist_tuning(const dp_bin_layout* layout, int32_t bin_stride, bst_ulong* out_len,
+                   const char** out);
+
 /* sibling = parent - built, element-wise over n int64 values. */
 int dp_hist_subtract(const int64_t* parent, const int64_t* built, int64_t* sibling, int64_t n,
                      void* stream);

@@ -14,8 +14,9 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = [dict(zip(("dp_hist_tiles", "dp_hist_unroll", "dp_hist_items"), c))
-          for c in itertools.product((1, 2), (1, 2), (512, 1024, 2048))]
+SHAPES = [dict(zip(("dp_hist_tiles", "dp_hist_unroll", "dp_hist_items", "dp_hist_split"), c))
+          for c in itertools.product((1, 2), (1, 2), (512, 1024, 2048), (0, 4, 5))
+          if c[0] == 2 or c[3] == 0]
 
 
 def _train(dp, values, labels, params, rounds, n, k):
@@ -28,9 +29,10 @@ def _train(dp, values, labels, params, rounds, n, k):
 
 @pytest.mark.parametrize("case", ["c2_two_tiles", "c4_odd_tiles", "missing", "present_value"])
 def test_every_launch_shape_trains_the_same_model(dp, device, case):
-    """Trees, partitions and margins are identical under all twelve forced launch shapes
-    (two tiles per item over an odd tile count leaves a one-tile last group; the MISSING
-    kernels; present-value histograms take the work-item count only)."""
+    """Trees, partitions and margins are identical under all 24 forced launch shapes
+    (two tiles per item over an odd tile count leaves a one-tile last group, with and without
+    the lanes' swapped tile order; the MISSING kernels; present-value histograms take the
+    work-item count only)."""
     import torch
     from dpgbdt import ops
 
@@ -53,13 +55,13 @@ def test_every_launch_shape_trains_the_same_model(dp, device, case):
                      "max_bin": 64}, 1
     n = values.shape[0]
     base = _train(dp, values, labels, dict(params, dp_autotune=0), 3, n, k)
-    assert base[3].tuning() == {"defaults": True}
+    assert base[3].tuning()["defaults"] is True
     for shape in SHAPES:
         if case == "present_value" and shape["dp_hist_tiles"] == 2:
             continue  # one present-value tile per item: only the item count applies
         print(f"[tuning] {case} {shape}", flush=True)
         got = _train(dp, values, labels, dict(params, **shape), 3, n, k)
-        assert got[3].tuning() == {"forced": True}
+        assert got[3].tuning()["forced"] is True
         assert got[0] == base[0], shape
         np.testing.assert_array_equal(got[1], base[1])
         np.testing.assert_array_equal(np.asarray(got[2]).view(np.uint32),
@@ -77,13 +79,45 @@ def test_autotuner_report_and_choice(dp, device):
     report = tuned[3].tuning()
     for name in ("root", "gathered"):
         cands = report[name]
-        assert len(cands) == 12  # 2 tile widths x 2 unrolls x 3 item counts
+        assert len(cands) == 24  # (1 tile + 2 tiles x 3 orders) x 2 unrolls x 3 item counts
         assert all(c["ms"] > 0 for c in cands)
         best = min(cands, key=lambda c: c["ms"])
-        assert report["chosen"][name] == {key: best[key] for key in ("tiles", "unroll", "items")}
+        assert report["chosen"][name] == {key: best[key]
+                                          for key in ("tiles", "unroll", "items", "split")}
     base = _train(dp, values, labels, dict(params, dp_autotune=0), 2, 200000, 1)
     assert tuned[0] == base[0]
     # the choice is cached per process: a second booster of the shape reports the same
     again = _train(dp, values, labels, params, 1, 200000, 1)
     assert again[3].tuning() == report
     print(json.dumps(report["chosen"]), flush=True)
+
+
+@pytest.mark.parametrize("case", ["c4_zero_pixels", "c1_few_features", "c2_wide_bins",
+                                  "le64_bins"])
+def test_skip_bins_train_the_oracle_model(dp, oracle, device, case):
+    """Skip bins (each feature's most frequent bin left out of the histograms and restored
+    from the node totals by the evaluation) train the oracle's trees, partitions and
+    margins bit for bit, forced on (dp_skip_bin 2) for every evaluation kernel: at most 16
+    features (one workgroup per node), 256 bins (one feature per wavefront), at most 64
+    bins (four features per wavefront), and C4's zero-dominated pixels, where the automatic
+    rule takes them; dp_skip_bin 0 gives the same model."""
+    import test_gpu_booster as tb
+
+    if case == "c4_zero_pixels":
+        args, p, kw = (4, 3000, 784, 1, 10), {"max_depth": 5, "eta": 0.3}, {}
+    elif case == "c1_few_features":
+        args, p, kw = (1, 20000, 8, 0, 1), {"max_depth": 6, "eta": 0.3}, {}
+    elif case == "c2_wide_bins":
+        args, p, kw = (2, 30000, 28, 0, 1), {"max_depth": 6, "eta": 0.3}, {}
+    else:
+        args, p, kw = (1, 20000, 40, 0, 1), {"max_depth": 6, "eta": 0.3}, {"max_bin": 64}
+    config, n, f, objective, k = args
+    models = []
+    for mode in (2, 0):
+        print(f"[skip] {case} dp_skip_bin={mode}", flush=True)
+        bst, x, o_trees, o_margin, pos, n = tb._train_both(
+            dp, oracle, device, config, n, f, objective, k, p, 2, 20261230, **kw,
+            extra={"dp_skip_bin": mode})
+        tb._compare(bst, o_trees, o_margin, pos, n, k)
+        models.append(bst.save_raw())
+    assert models[0] == models[1]
