@@ -60,15 +60,20 @@ def algorithmic_hist_bytes(n_rows, n_features, n_bins, gathered=False):
 
 def read_traffic():
     """HBM bytes per C3 root histogram call (hist_kernel + hist_reduce_kernel) from the
-    committed PMC summary."""
-    path = os.path.join(ROOT, "profiles", "hist_c3_root_pmc.md")
+    committed PMC summary, and where they come from: the summary's path and the commit
+    whose kernels its counter runs measured (its `measured_at_commit:` line), so that a
+    figure older than the kernels shows as such."""
+    rel = os.path.join("profiles", "hist_c3_root_pmc.md")
+    value, commit = None, "unknown"
     try:
-        for line in open(path):
+        for line in open(os.path.join(ROOT, rel)):
             if line.startswith("traffic_bytes_per_launch:"):
-                return float(line.split(":", 1)[1])
+                value = float(line.split(":", 1)[1])
+            elif line.startswith("measured_at_commit:"):
+                commit = line.split(":", 1)[1].strip()
     except OSError:
-        pass
-    return None
+        return None, None
+    return value, f"{rel}@{commit}"
 
 
 def hist_leg(args, torch, dp, ops):
@@ -149,7 +154,10 @@ def lds_roof_leg(torch, elements):
     probe_elements = grid * 1024 * rows * 16
     out = torch.empty(grid * 1024, dtype=torch.int64, device="cuda:0")
     stream = torch.cuda.current_stream().cuda_stream
-    names = ["two_u64", "one_u64", "two_u32", "one_u32", "no_lds"]
+    # modes 5-9: lane aggregation (xor-32 partner) on conflict-free, 16-value and
+    # 80 %-zero bins, beside the same bins without it
+    names = ["two_u64", "one_u64", "two_u32", "one_u32", "no_lds", "two_u64_16bins",
+             "two_u64_16bins_agg", "two_u64_agg", "two_u64_zeros", "two_u64_zeros_agg"]
     res = {}
     for mode, name in enumerate(names):
         ms = ctypes.c_float()
@@ -455,7 +463,7 @@ def main():
             for name, cap in (("C1", 10), ("C2", 2)):
                 log(f"CPU baseline: oracle booster on {name}, one thread")
                 cpu["trees_per_s_one_thread"][name] = cpu_trees_leg(torch, ops, name, cap, 1)
-    avg_s = hist["avg_ms"] * 1e-3
+    traffic, traffic_source = read_traffic()
     line = {
         "metric": METRIC,
         "value": hist["rows_features_per_s"],
@@ -477,9 +485,10 @@ def main():
         "pct_hbm_peak": 100.0 * hist["achieved_gbs"] / HBM_PEAK_GBS,
         "roofline": {"bound": "hbm", "achieved": hist["achieved_gbs"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": hist["achieved_gbs"] / HBM_PEAK_GBS,
-                     "traffic": read_traffic(),
-                     "kernel": "dp_hist_accumulate = dp::hist_kernel<false, false> + "
-                               "dp::hist_reduce_kernel",
+                     "traffic": traffic,
+                     "traffic_source": traffic_source,
+                     "kernel": "dp_hist_accumulate = dp::hist_kernel<false, 0, tiles, unroll, "
+                               "split> + dp::hist_reduce_kernel",
                      "algorithmic_bytes_per_launch": hist["algorithmic_bytes"],
                      "lds_atomic_roof": roof,
                      "avg_launch_ms": hist["avg_ms"],
