@@ -372,7 +372,9 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
                    node_left_[0].p, c, N, root_slots, root_blocks, chunk_, ridx_[0].p, s);
   int64_t nb = 1;  // bound of the current level's node count
   int64_t nb_prev = 0;
-  bool last_level_applied = false;  // level D's leaves went to the margins in the scatter
+  // The last split level's count launch adds every leaf value of levels D - 1
+  // and D to the margins (rows of expanding nodes and of D - 1's leaves).
+  bool last_level_applied = false;
   for (int32_t d = 0; d <= D; ++d) {
     const int cur = d & 1, nxt = cur ^ 1;
     if (!eager_ && d > 0) {
@@ -381,8 +383,9 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
       nb = host_counts->n_level;
       if (nb == 0) {  // the tree ended: apply the previous level's deferred leaves
         const int32_t bound = int32_t(plan_leaf_capacity(nb_prev, N, chunk_));
-        launch_update_margin(ridx_[nxt].p, leaf_work_[nxt].p, bound,
-                             field(c, &PlanCounts::n_leaf), margin, stride, s);
+        if (!last_level_applied)  // else the last split level's count launch did
+          launch_update_margin(ridx_[nxt].p, leaf_work_[nxt].p, bound,
+                               field(c, &PlanCounts::n_leaf), margin, stride, s);
         if (positions)
           launch_leaf_positions(ridx_[nxt].p, leaf_work_[nxt].p, bound,
                                 field(c, &PlanCounts::n_leaf), positions, s);
@@ -401,6 +404,10 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     // A split level of at most 1024 nodes runs its planner and its partition
     // scatter in one launch.
     const bool merged = split && nb <= 1024;
+    // On the last split level of such a tree the rows need no new order: the
+    // count launch updates the margins and the planner runs alone (unless leaf
+    // ids are wanted, which the scatter's segments give).
+    const bool fuse_last = merged && d + 1 == D && margin && !positions;
     ScatterArgs scatter{};
     int64_t* h = hist_[cur].p;
     if (split) {
@@ -458,12 +465,25 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
         prev.stride = stride;
         prev.positions = positions;
       }
+      LastLevel ll{};
+      if (fuse_last) {
+        ll.margin = margin;
+        ll.stride = stride;
+        ll.nodes = level_[cur].p;
+        ll.exps = exps;
+        ll.eta = double(p.eta);
+        ll.lambda = double(p.lambda);
+        ll.alpha = double(p.alpha);
+        ll.mcw = double(p.min_child_weight);
+        last_level_applied = true;
+      }
       launch_partition(q.bins.p, q.cols.p, L, ridx_[cur].p, ridx_[nxt].p, part_work_[cur].p,
                        int32_t(plan_part_capacity(nb, N, chunk_)), &c->n_part[d & 1],
                        seg_begin_[cur].p, splits_.p, part_first_[cur].p, int32_t(nb),
                        field(c, &PlanCounts::n_level), work_left_.p, part_masks_.p,
                        node_left_[cur].p, true, s, d > 0 ? &prev : nullptr,
-                       records ? nullptr : &sel, merged ? &scatter : nullptr);
+                       records ? nullptr : &sel, merged && !fuse_last ? &scatter : nullptr,
+                       fuse_last ? &ll : nullptr);
     }
     PlanArgs a{};
     a.cur = level_[cur].p;
@@ -501,26 +521,15 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     a.part_capacity = int32_t(part_work_[nxt].n);
     a.leaf_capacity = int32_t(leaf_work_[cur].n);
     a.cur_bound = int32_t(std::min<int64_t>(nb, INT32_MAX));
-    // The last split level's scatter adds the leaf values of its children (all
-    // leaves) to the margins itself, unless leaf ids are wanted too.
-    if (merged && d + 1 == D && margin && !positions) {
-      scatter.margin = margin;
-      scatter.stride = stride;
-      scatter.nodes = level_[cur].p;
-      scatter.exps = exps;
-      scatter.eta = a.eta;
-      scatter.lambda = a.lambda;
-      scatter.alpha = a.alpha;
-      scatter.mcw = a.mcw;
-      last_level_applied = true;
-    }
-    if (merged) {
+    if (merged) {  // the planner sums the count launch's left counts itself
       a.work_left = work_left_.p;
       a.part_bound = int32_t(plan_part_capacity(nb, N, chunk_));
-      launch_plan_scatter(a, scatter, N, s);
-    } else {
-      launch_plan_level(a, nb, s);
     }
+    // The last split level's planner also writes its children's records (all
+    // leaves, their values already in the margins): no planner for level D.
+    a.leaf_children = fuse_last ? 1 : 0;
+    if (merged && !fuse_last) launch_plan_scatter(a, scatter, N, s);
+    else if (!(d == D && last_level_applied)) launch_plan_level(a, nb, s);
     // No later count launch carries the leaves of the last two levels: level
     // D - 1's are applied with level D's, in one launch after the last planner
     // (which keeps their count in n_leaf_prev).  A level-synced tree that ends
@@ -534,10 +543,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
         prev_leaves.n_host = int32_t(plan_leaf_capacity(nb_prev, N, chunk_));
         prev_leaves.n_dev = field(c, &PlanCounts::n_leaf_prev);
       }
-      if (last_level_applied)  // only the leaves of level D - 1 are left
-        launch_update_margin(prev_leaves.ridx, prev_leaves.work, prev_leaves.n_host,
-                             prev_leaves.n_dev, margin, stride, s);
-      else
+      if (!last_level_applied)
         launch_update_margin(ridx_[cur].p, leaf_work_[cur].p, leaf_bound,
                              field(c, &PlanCounts::n_leaf), margin, stride, s,
                              D >= 1 ? &prev_leaves : nullptr);

@@ -136,11 +136,15 @@ void dp_workspace_s::grow_staging(size_t bytes) {
   while (cap < bytes) cap <<= 1;
   staged_host.reserve(cap);
   staged_dev.reserve(cap);
+  committed_.clear();  // the device area is new
 }
 
 void dp_workspace_s::commit(hipStream_t stream) {
-  if (staged_used)
+  if (staged_used && !(staged_used == committed_.size() &&
+                       std::memcmp(staged_host.p, committed_.data(), staged_used) == 0)) {
     DP_HIP(hipMemcpyAsync(staged_dev.p, staged_host.p, staged_used, hipMemcpyHostToDevice, stream));
+    committed_.assign(staged_host.p, staged_host.p + staged_used);
+  }
   DP_HIP(hipEventRecord(staged_done, stream));
 }
 

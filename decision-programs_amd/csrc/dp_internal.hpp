@@ -236,7 +236,9 @@ struct dp_workspace_s {
     *device_ptr = reinterpret_cast<T*>(staged_dev.p + offset);
     return reinterpret_cast<T*>(staged_host.p + offset);
   }
-  // Copies everything staged since begin() to the device on `stream`.
+  // Copies everything staged since begin() to the device on `stream`, unless
+  // the device area already holds exactly these bytes from the previous
+  // commit (a repeated call with the same work lists issues no copy).
   void commit(hipStream_t stream);
   // Device-only scratch, valid until the next begin().
   template <class T>
@@ -252,6 +254,7 @@ struct dp_workspace_s {
   void reserve_scratch(size_t bytes);
 
  private:
+  std::vector<uint8_t> committed_;  // the bytes the device staging area holds
   void grow_staging(size_t bytes);
   [[noreturn]] void need_scratch(size_t bytes);
 };
@@ -398,13 +401,18 @@ struct ScatterArgs {
   const int64_t* work_left;
   const unsigned long long* masks;
   int64_t* node_left;        // the node's first item writes the node's left total; may be null
-  // Set on the last split level (every child is a leaf): each scattered row
-  // also gets margin[row * stride] += its child's leaf value, eta times the
-  // leaf weight of the child's quantised sums (split record and nodes[node]).
+};
+
+// The last split level's margin update, done by its count launch (every child
+// is a leaf, so the rows need no new order): a row of an expanding node gets
+// margin[row * stride] += its child's leaf value, eta times the leaf weight of
+// the child's quantised sums (split record and nodes[node]); a row of a node
+// that does not expand gets the node's own leaf value.
+struct LastLevel {
   float* margin;
   int64_t stride;
   const LevelNode* nodes;
-  const int32_t* exps;       // quantiser exponents (gradient, hessian)
+  const int32_t* exps;  // quantiser exponents (gradient, hessian)
   double eta, lambda, alpha, mcw;
 };
 
@@ -417,7 +425,9 @@ struct ScatterArgs {
 // node_left[0, nodes) (non-expanding nodes keep 0); else it is cleared here
 // for n_nodes nodes.  deferred: when given, the scatter is not launched; its
 // arguments are written there (n_work_host = 0: nothing to scatter) for
-// launch_plan_scatter.
+// launch_plan_scatter.  last: the last split level's margin update is done by
+// the count launch, and no scatter is launched or deferred (ridx_out is not
+// written; the count still writes work_left for the level's planner).
 // Per-feature candidates left by launch_evaluate(..., select = false): the
 // partition count selects each node's split from them and writes the records.
 struct SplitSelect {
@@ -432,7 +442,8 @@ void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_lay
                       int32_t n_nodes, const int32_t* n_nodes_dev, int64_t* work_left,
                       unsigned long long* masks, int64_t* node_left, bool node_left_zeroed,
                       hipStream_t s, const LeafPass* leaves = nullptr,
-                      const SplitSelect* select = nullptr, ScatterArgs* deferred = nullptr);
+                      const SplitSelect* select = nullptr, ScatterArgs* deferred = nullptr,
+                      const LastLevel* last = nullptr);
 constexpr int64_t kPartChunk = 4096;
 constexpr int kPartMasks = 64;  // ballot words per partition work item (kPartChunk / 64)
 
@@ -489,6 +500,9 @@ struct PlanArgs {
   // << 32 | left rows) instead of read from node_left.
   const int64_t* work_left;
   int32_t part_bound;  // host bound of this level's partition items (sizes work_left)
+  // Set on the last split level when no planner runs for the next level: the
+  // children's node records are written here, as leaves (the small planner).
+  int32_t leaf_children;
 };
 // level_bound: an upper bound of the level's node count (selects the planner).
 void launch_plan_level(const PlanArgs& a, int64_t level_bound, hipStream_t s);

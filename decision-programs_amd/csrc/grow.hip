@@ -577,6 +577,25 @@ __device__ void plan_small_level(const PlanArgs& a) {
         a.next_seg_begin[slot + 1] = nd.begin + nl;
         a.next_node_left[slot] = 0;
         a.next_node_left[slot + 1] = 0;
+        if (a.leaf_children) {  // the children's records, as the next level's planner writes leaves
+          for (int c = 0; c < 2; ++c) {
+            const LevelNode ch = a.next[slot + c];
+            NodeInfo li{};
+            li.g = ch.g;
+            li.h = ch.h;
+            li.begin = ch.begin;
+            li.end = ch.end;
+            li.parity = (a.depth + 1) & 1;
+            const double cg = double(ch.g) * ug, chh = double(ch.h) * uh;
+            const double cw = plan_weight(a, cg, chh);
+            li.base_weight = float(cw);
+            li.sum_hess = float(chh);
+            li.bin = -1;
+            li.left = -1;
+            li.leaf_value = float(cw * a.eta);
+            a.info[left + c] = li;
+          }
+        }
       } else {
         s_error = 2;
       }
@@ -732,14 +751,14 @@ __global__ __launch_bounds__(kPlanThreads) void plan_small_kernel(PlanArgs a) {
 // items at a time) in one launch: both read only what the partition count
 // left, and write disjoint buffers (the planner writes the next level's, and
 // the next level's partition count in counts->n_part).
-template <int G, bool MARGIN>
+template <int G>
 __global__ __launch_bounds__(kPlanThreads) void plan_scatter_kernel(PlanArgs a, ScatterArgs sa) {
   if (blockIdx.x == 0) {
     plan_small_level(a);
     return;
   }
-  scatter_items<G, kPlanThreads / kPartThreads, MARGIN>(sa, int32_t(blockIdx.x) - 1,
-                                                          int32_t(gridDim.x) - 1);
+  scatter_items<G, kPlanThreads / kPartThreads>(sa, int32_t(blockIdx.x) - 1,
+                                                int32_t(gridDim.x) - 1);
 }
 
 __global__ __launch_bounds__(256) void plan_root_kernel(
@@ -790,6 +809,8 @@ __global__ __launch_bounds__(256) void plan_root_kernel(
 }  // namespace
 
 void launch_plan_level(const PlanArgs& a, int64_t level_bound, hipStream_t s) {
+  need(!a.leaf_children || level_bound <= kPlanThreads,
+       "the children's leaf records are written by the small planner only");
   if (level_bound <= kPlanThreads)
     hipLaunchKernelGGL(plan_small_kernel, dim3(1), dim3(kPlanThreads), 0, s, a);
   else
@@ -806,8 +827,7 @@ void launch_plan_scatter(const PlanArgs& a, const ScatterArgs& sa, int64_t n_row
   const int blocks = 1 + (items + Q - 1) / Q;
   // Four steps per load group on matrices of 4M rows or more, as the partition.
   const bool wide = n_rows >= (int64_t(1) << 22);
-  auto k = sa.margin ? (wide ? plan_scatter_kernel<4, true> : plan_scatter_kernel<1, true>)
-                     : (wide ? plan_scatter_kernel<4, false> : plan_scatter_kernel<1, false>);
+  auto k = wide ? plan_scatter_kernel<4> : plan_scatter_kernel<1>;
   hipLaunchKernelGGL(k, dim3(blocks), dim3(kPlanThreads), 0, s, a, sa);
   DP_HIP(hipGetLastError());
 }

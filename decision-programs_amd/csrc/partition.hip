@@ -73,13 +73,17 @@ __device__ __forceinline__ void apply_leaf(const LeafPass& lp, const LeafWork w)
 // groups of G steps whose row ids, then bins, are loaded together.  G = 4
 // keeps more loads in flight and pays on large levels; on levels of about a
 // million rows or fewer (data in cache) G = 1 measured faster.
-template <bool COLS, int G>
+// MARGIN (the last split level, LastLevel): each row's margin is loaded with
+// its bin and stored with its child's leaf value added once the side is known;
+// the rows of a node that does not expand get the node's own leaf value.
+template <bool COLS, int G, bool MARGIN>
 __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
     const uint8_t* __restrict__ bins, int64_t n_rows, int tile_width, int missing_bin,
     const uint32_t* __restrict__ ridx, const PartWork* __restrict__ work, int32_t n_work_host,
     const int32_t* __restrict__ n_work_dev, dp_split_record* __restrict__ splits,
     SplitSelect sel, const int32_t* __restrict__ node_first_work,
-    int64_t* __restrict__ work_left, unsigned long long* __restrict__ masks, LeafPass lp) {
+    int64_t* __restrict__ work_left, unsigned long long* __restrict__ masks, LeafPass lp,
+    LastLevel ll) {
   __shared__ int wave_count[kPartThreads / 64];
   __shared__ Cand wave_best[kPartThreads / 64];
   __shared__ dp_split_record sel_rec;
@@ -115,8 +119,27 @@ __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
   } else {
     s = splits[w.node];
   }
+  // MARGIN: the leaf values of this item's rows (uniform per workgroup), in
+  // the level planner's arithmetic (double, rounded to float once).
+  float v_left = 0.0f, v_right = 0.0f;
+  if constexpr (MARGIN) {
+    const LevelNode nd = ll.nodes[w.node];
+    const double ug = ldexp(1.0, -ll.exps[0]), uh = ldexp(1.0, -ll.exps[1]);
+    if (s.expand) {
+      v_left = float(leaf_weight(double(s.gl) * ug, double(s.hl) * uh, ll.lambda, ll.alpha,
+                                 ll.mcw) * ll.eta);
+      v_right = float(leaf_weight(double(nd.g - s.gl) * ug, double(nd.h - s.hl) * uh, ll.lambda,
+                                  ll.alpha, ll.mcw) * ll.eta);
+    } else {
+      v_left = float(leaf_weight(double(nd.g) * ug, double(nd.h) * uh, ll.lambda, ll.alpha,
+                                 ll.mcw) * ll.eta);
+    }
+  }
   if (!s.expand) {
     if (threadIdx.x == 0) work_left[item] = int64_t(w.node) << 32;
+    if constexpr (MARGIN)  // the node is a leaf: its rows get its own value
+      apply_leaf(LeafPass{ridx, nullptr, nullptr, 0, ll.margin, ll.stride, nullptr},
+                 LeafWork{v_left, 0, w.begin, w.end});
     continue;
   }
   int count = 0;
@@ -125,10 +148,16 @@ __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
   for (int g0 = 0; g0 < kPartSteps; g0 += G) {
     if (w.begin + int64_t(g0) * kPartThreads >= w.end) break;  // uniform per workgroup
     int bin[G];
+    uint32_t mrow[G];  // MARGIN: this group's rows (row[] is refilled below)
+    float mval[G];
 #pragma unroll
     for (int k = 0; k < G; ++k) {
       const int64_t i = w.begin + int64_t(g0 + k) * kPartThreads + threadIdx.x;
       bin[k] = i < w.end ? split_bin_of<COLS>(bins, n_rows, tile_width, row[k], s.feature) : -1;
+      if constexpr (MARGIN) {
+        mrow[k] = row[k];
+        mval[k] = i < w.end ? ll.margin[int64_t(row[k]) * ll.stride] : 0.0f;
+      }
     }
     if (g0 + G < kPartSteps) load_rows(g0 + G);
 #pragma unroll
@@ -138,6 +167,9 @@ __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
       const unsigned long long m = __ballot(left);
       if (lane == 0) item_masks[(g0 + k) * (kPartThreads / 64)] = m;
       count += popc64(m);
+      if constexpr (MARGIN) {
+        if (b >= 0) ll.margin[int64_t(mrow[k]) * ll.stride] = mval[k] + (left ? v_left : v_right);
+      }
     }
   }
   if (lane == 0) wave_count[wave] = count;
@@ -214,7 +246,7 @@ void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_lay
                       int32_t n_nodes, const int32_t* n_nodes_dev, int64_t* work_left,
                       unsigned long long* masks, int64_t* node_left, bool node_left_zeroed,
                       hipStream_t s, const LeafPass* leaves, const SplitSelect* select,
-                      ScatterArgs* deferred) {
+                      ScatterArgs* deferred, const LastLevel* last) {
   if (deferred) *deferred = ScatterArgs{};  // nothing to scatter unless filled below
   if (n_nodes <= 0) return;
   (void)n_nodes_dev;
@@ -229,12 +261,20 @@ void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_lay
   const SplitSelect sel = select ? *select : SplitSelect{};
   // Four steps per load group on matrices of 4M rows or more, else one.
   const bool wide = layout.n_rows >= (int64_t(1) << 22);
-  auto count = cols ? (wide ? part_count_kernel<true, 4> : part_count_kernel<true, 1>)
-                    : (wide ? part_count_kernel<false, 4> : part_count_kernel<false, 1>);
+  const LastLevel ll = last ? *last : LastLevel{};
+  need(!last || (ll.margin && ll.nodes && ll.exps), "last-level margin update arguments");
+  auto pick = [&](auto c1, auto c4, auto t1, auto t4) {
+    return cols ? (wide ? c4 : c1) : (wide ? t4 : t1);
+  };
+  auto count = last ? pick(part_count_kernel<true, 1, true>, part_count_kernel<true, 4, true>,
+                           part_count_kernel<false, 1, true>, part_count_kernel<false, 4, true>)
+                    : pick(part_count_kernel<true, 1, false>, part_count_kernel<true, 4, false>,
+                           part_count_kernel<false, 1, false>, part_count_kernel<false, 4, false>);
   hipLaunchKernelGGL(count, dim3(gc), dim3(kPartThreads), 0, s, src, layout.n_rows,
                      layout.tile_width, missing, ridx_in, work, n_work, n_work_dev, splits, sel,
-                     node_first_work, work_left, masks, lp);
+                     node_first_work, work_left, masks, lp, ll);
   DP_HIP(hipGetLastError());
+  if (last) return;  // every child is a leaf: no new row order
   const ScatterArgs sa{ridx_in, ridx_out,   work,      n_work, n_work_dev, splits,
                        seg_begin, node_first_work, work_left, masks, node_left};
   if (deferred) {

@@ -41,10 +41,7 @@ __device__ inline double leaf_weight(double g, double h, double lambda, double a
 // Items block * Q + quarter + k * n_blocks * Q.  Rows of a group of G steps:
 // the first group's ids are loaded with the item's other inputs; with G > 1
 // (large matrices) each later group's while the group before it is written.
-// MARGIN: the last split level's variant (a.margin set), a separate
-// instantiation so that its registers do not lower the other levels'
-// occupancy.
-template <int G, int Q, bool MARGIN = false>
+template <int G, int Q>
 __device__ void scatter_items(const ScatterArgs& a, int32_t block, int32_t n_blocks) {
   __shared__ int64_t wave_sum[Q][2][kPartThreads / 64];
   const int q = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kPartThreads);
@@ -55,51 +52,6 @@ __device__ void scatter_items(const ScatterArgs& a, int32_t block, int32_t n_blo
   const int32_t item0 = block * Q + q;
   const PartWork w_first = item0 < a.n_work_host ? a.work[item0] : PartWork{0, 0, 0, 0};
   const int32_t n_work = a.n_work_dev ? *a.n_work_dev : a.n_work_host;
-  // On the last split level: every child is a leaf, so the rows need no new
-  // order (no later launch reads this level's row ids) and no node totals --
-  // only each row's side.  The children's leaf values, computed as the next
-  // planner computes them from the same quantised sums, are added to the
-  // margins of the item's rows.  No barriers: MARGIN is uniform per launch.
-  if constexpr (MARGIN) {
-    for (int32_t base = block * Q; base < n_work; base += n_blocks * Q) {
-      const int32_t item = base + q;
-      if (item >= n_work) continue;  // uniform per quarter
-      const PartWork w = item == item0 ? w_first : a.work[item];
-      const dp_split_record sp = a.splits[w.node];
-      if (!sp.expand) continue;
-      const unsigned long long my_mask = a.masks[int64_t(item) * kPartMasks + lane];
-      const LevelNode nd = a.nodes[w.node];
-      const double ug = ldexp(1.0, -a.exps[0]), uh = ldexp(1.0, -a.exps[1]);
-      const float v_left = float(leaf_weight(double(sp.gl) * ug, double(sp.hl) * uh, a.lambda,
-                                             a.alpha, a.mcw) * a.eta);
-      const float v_right = float(leaf_weight(double(nd.g - sp.gl) * ug,
-                                              double(nd.h - sp.hl) * uh, a.lambda, a.alpha,
-                                              a.mcw) * a.eta);
-      // The row ids of every step of the item, then their margins, then the
-      // stores: two dependent round trips per item instead of two per step.
-      const int n_steps = int((w.end - w.begin + kPartThreads - 1) / kPartThreads);  // uniform
-      uint32_t r[kPartSteps];
-      float m[kPartSteps];
-#pragma unroll
-      for (int st = 0; st < kPartSteps; ++st) {
-        const int64_t i = w.begin + int64_t(st) * kPartThreads + t;
-        r[st] = st < n_steps ? a.ridx_in[i < w.end ? i : w.end - 1] : 0u;
-      }
-#pragma unroll
-      for (int st = 0; st < kPartSteps; ++st)
-        m[st] = st < n_steps ? a.margin[int64_t(r[st]) * a.stride] : 0.0f;
-#pragma unroll
-      for (int st = 0; st < kPartSteps; ++st) {
-        if (st >= n_steps) break;  // uniform per quarter
-        const int64_t i = w.begin + int64_t(st) * kPartThreads + t;
-        const int idx = st * (kPartThreads / 64) + wave;
-        const unsigned long long mask = (unsigned long long)readlane64((long long)my_mask, idx);
-        if (i < w.end)
-          a.margin[int64_t(r[st]) * a.stride] = m[st] + (((mask >> lane) & 1ull) ? v_left : v_right);
-      }
-    }
-    return;
-  }
   for (int32_t base = block * Q; base < n_work; base += n_blocks * Q) {
     const int32_t item = base + q;
     const bool have = item < n_work;  // uniform per quarter (always true for Q = 1)

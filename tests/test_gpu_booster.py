@@ -313,13 +313,17 @@ def _small_booster(dp, config, n, f, objective, k, rounds, depth=5, seed=7, max_
     return bst, values, labels
 
 
-@pytest.mark.parametrize("config,n,f,objective,k,depth", [(2, 30000, 28, 0, 1, 6),
-                                                           (4, 1500, 784, 1, 10, 4),
-                                                           (5, 4000, 60, 2, 1, 7)])
-def test_margins_without_leaf_ids(dp, device, config, n, f, objective, k, depth):
-    """Without leaf ids recorded, the last split level's scatter adds the leaf values to the
-    margins itself (no separate margin pass for those leaves); margins and models must equal a
-    booster's that records leaf ids, whose margins the oracle tests pin."""
+@pytest.mark.parametrize("config,n,f,objective,k,depth,mcw", [(2, 30000, 28, 0, 1, 6, 1.0),
+                                                               (4, 1500, 784, 1, 10, 4, 1.0),
+                                                               (5, 4000, 60, 2, 1, 7, 1.0),
+                                                               (1, 3000, 8, 0, 1, 1, 1.0),
+                                                               (1, 3000, 8, 0, 1, 8, 4.0),
+                                                               (1, 3000, 8, 0, 1, 8, 40.0)])
+def test_margins_without_leaf_ids(dp, device, config, n, f, objective, k, depth, mcw):
+    """Without leaf ids recorded, the last split level's count launch adds the leaf values of
+    its children and of that level's own leaves to the margins (no scatter and no separate
+    margin pass there); margins and models must equal a booster's that records leaf ids, whose
+    margins the oracle tests pin."""
     from dpgbdt import ops
 
     values, labels, _, _ = ops.synth(config, n, 11, n_features=f)
@@ -327,7 +331,7 @@ def test_margins_without_leaf_ids(dp, device, config, n, f, objective, k, depth)
     out = []
     for record in (0, 1):
         params = {"objective": obj, "max_depth": depth, "eta": 0.3, "max_bin": 256,
-                  "dp_record_positions": record}
+                  "min_child_weight": mcw, "dp_record_positions": record}
         if objective == 1:
             params["num_class"] = k
         dtrain = dp.DMatrix(values, labels)
@@ -338,6 +342,19 @@ def test_margins_without_leaf_ids(dp, device, config, n, f, objective, k, depth)
         out.append((bst.margins(n, k), model))
     np.testing.assert_array_equal(out[0][0].view(np.uint32), out[1][0].view(np.uint32))
     assert out[0][1] == out[1][1]
+    # leaves by depth: with a larger min_child_weight, nodes stop at the last split level
+    # (their own leaf values come from the count launch) or trees end before it
+    depths = []
+    for t in out[0][1]["trees"]:
+        left = np.array(t["left_children"])
+        d = np.zeros(len(left), dtype=np.int64)
+        for i in range(len(left)):
+            if left[i] != -1:
+                d[left[i]] = d[i] + 1
+                d[left[i] + 1] = d[i] + 1
+        depths.extend(d[left == -1].tolist())
+    print(f"[margins] depth {depth} mcw {mcw}: leaves by depth "
+          f"{np.bincount(depths).tolist()}", flush=True)
 
 
 @pytest.mark.parametrize("config,n,f,objective,k", [(1, 5000, 8, 0, 1), (4, 1500, 784, 1, 10),
