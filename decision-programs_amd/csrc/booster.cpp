@@ -176,7 +176,8 @@ Quantized& DMatrix::quantize(int32_t max_bin, dp_workspace_s& ws, hipStream_t s)
 
 // Each feature's most frequent bin (ties: the lowest) over all rows, as skip
 // bins per feature and per 16-feature tile (pad features: bin 0, the byte the
-// tiles hold for them), and the mean share of the rows in those bins.
+// tiles hold for them, so their atomics are skipped too), and the share of
+// the element atomics skipped: the rows in those bins plus the pad features.
 void build_skip_bins(Quantized& q, hipStream_t s) {
   const int64_t N = q.layout.n_rows;
   const int32_t F = q.layout.n_features, T = q.layout.n_tiles;
@@ -202,7 +203,8 @@ void build_skip_bins(Quantized& q, hipStream_t s) {
   DP_HIP(hipMemcpy(q.skip_features.p, per_feature.data(), per_feature.size(),
                    hipMemcpyHostToDevice));
   DP_HIP(hipMemcpy(q.skip_tiles.p, per_tile.data(), per_tile.size(), hipMemcpyHostToDevice));
-  q.skip_share = F > 0 ? share / double(F) : 0.0;
+  const double slots = double(T) * 16.0;
+  q.skip_share = T > 0 ? (share + (slots - double(F))) / slots : 0.0;
 }
 
 int32_t Tree::alloc(int32_t parent_id) {

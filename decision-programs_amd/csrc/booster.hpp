@@ -25,8 +25,9 @@ struct Quantized {
   DeviceBuffer<uint8_t> rows;  // row-major copy: rows[(r * n_tiles + t) * 16 + j] (on demand)
   SparseBins sparse;           // present-value layout (on demand, mostly-missing matrices)
   // Skip bins (matrices without missing values, on demand): each feature's most
-  // frequent bin, per feature and per 16-feature tile, and the mean share of
-  // the rows those bins hold (-1: not counted yet).
+  // frequent bin, per feature and per 16-feature tile, and the share of the
+  // histogram's element atomics they remove: the rows in those bins plus the
+  // last tile's padding features, over n_tiles * 16 (-1: not counted yet).
   DeviceBuffer<uint8_t> skip_features, skip_tiles;
   double skip_share = -1.0;
   double sparse_limit = -1.0;  // largest density limit the layout was tried with
@@ -36,8 +37,9 @@ struct Quantized {
 // Counts each feature's bins (column copy) and fills q.skip_features,
 // q.skip_tiles and q.skip_share; synchronises the stream.
 void build_skip_bins(Quantized& q, hipStream_t s);
-// dp_skip_bin 1 uses skip bins when they hold at least this share of the rows
-// on average (C4's zero pixels: about 0.8; quantile-binned features: 1 / bins).
+// dp_skip_bin 1 uses skip bins when they remove at least this share of the
+// element atomics (C4's zero pixels: about 0.8; C1's 8 features in a 16-wide
+// tile: 0.5; quantile-binned features filling their tiles: about 1 / bins).
 constexpr double kSkipShare = 0.2;
 
 class Booster;
@@ -256,7 +258,7 @@ class Booster {
   std::string tuning_report_ = "{}";
   int32_t sparse_mode_ = 1;  // dp_sparse_hist: 0 never, 1 when <= 1/4 present, 2 with any NaN
   // dp_skip_bin (matrices without missing values): 0 never, 1 when the skip
-  // bins hold at least kSkipShare of the rows on average, 2 always.
+  // bins remove at least kSkipShare of the element atomics, 2 always.
   int32_t skip_mode_ = 1;
   bool labels_checked_ = false;
   std::vector<std::pair<std::vector<uint64_t>, hipGraphExec_t>> graphs_;  // newest last

@@ -530,6 +530,13 @@ inline int64_t row_chunk(int64_t n_rows) {
   const int64_t c = (n_rows / 2048 + 255) / 256 * 256;
   return c < 256 ? 256 : (c > kPartChunk ? kPartChunk : c);
 }
+// 256-row steps whose row ids, then bins, a partition lane loads together
+// (count and scatter): four on matrices of 4M rows or more (more loads in
+// flight); below that the steps of one row_chunk item, at most two.
+inline int part_group(int64_t n_rows) {
+  if (n_rows >= (int64_t(1) << 22)) return 4;
+  return row_chunk(n_rows) >= 512 ? 2 : 1;
+}
 inline int64_t plan_part_capacity(int64_t nodes, int64_t n_rows, int64_t chunk) {
   return n_rows / chunk + 1 + nodes;
 }

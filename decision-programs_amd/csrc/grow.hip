@@ -825,9 +825,9 @@ void launch_plan_scatter(const PlanArgs& a, const ScatterArgs& sa, int64_t n_row
   const int32_t items = sa.n_work_host < 2048 ? sa.n_work_host : 2048;
   constexpr int Q = kPlanThreads / kPartThreads;
   const int blocks = 1 + (items + Q - 1) / Q;
-  // Four steps per load group on matrices of 4M rows or more, as the partition.
-  const bool wide = n_rows >= (int64_t(1) << 22);
-  auto k = wide ? plan_scatter_kernel<4> : plan_scatter_kernel<1>;
+  const int group = part_group(n_rows);  // load groups as the partition's
+  auto k = group == 4 ? plan_scatter_kernel<4>
+                      : (group == 2 ? plan_scatter_kernel<2> : plan_scatter_kernel<1>);
   hipLaunchKernelGGL(k, dim3(blocks), dim3(kPlanThreads), 0, s, a, sa);
   DP_HIP(hipGetLastError());
 }

@@ -70,9 +70,9 @@ __device__ __forceinline__ void apply_leaf(const LeafPass& lp, const LeafWork w)
 // its node's split from the per-feature candidates (every chunk of a node gets
 // the same record) and the node's first item writes it to splits.
 // A lane handles rows begin + step * 256 + threadIdx.x, step = 0..15, in
-// groups of G steps whose row ids, then bins, are loaded together.  G = 4
-// keeps more loads in flight and pays on large levels; on levels of about a
-// million rows or fewer (data in cache) G = 1 measured faster.
+// groups of G steps whose row ids, then bins, are loaded together
+// (part_group: G = 4 keeps more loads in flight and pays on large levels;
+// smaller matrices take the steps of one item).
 // MARGIN (the last split level, LastLevel): each row's margin is loaded with
 // its bin and stored with its child's leaf value added once the side is known;
 // the rows of a node that does not expand get the node's own leaf value.
@@ -259,17 +259,19 @@ void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_lay
   if (!node_left_zeroed) launch_fill_i64(node_left, n_nodes, 0, s);
   if (items <= 0) return;
   const SplitSelect sel = select ? *select : SplitSelect{};
-  // Four steps per load group on matrices of 4M rows or more, else one.
-  const bool wide = layout.n_rows >= (int64_t(1) << 22);
+  const int group = part_group(layout.n_rows);
   const LastLevel ll = last ? *last : LastLevel{};
   need(!last || (ll.margin && ll.nodes && ll.exps), "last-level margin update arguments");
-  auto pick = [&](auto c1, auto c4, auto t1, auto t4) {
-    return cols ? (wide ? c4 : c1) : (wide ? t4 : t1);
-  };
-  auto count = last ? pick(part_count_kernel<true, 1, true>, part_count_kernel<true, 4, true>,
-                           part_count_kernel<false, 1, true>, part_count_kernel<false, 4, true>)
-                    : pick(part_count_kernel<true, 1, false>, part_count_kernel<true, 4, false>,
-                           part_count_kernel<false, 1, false>, part_count_kernel<false, 4, false>);
+  auto pick = [&](auto k1, auto k2, auto k4) { return group == 4 ? k4 : (group == 2 ? k2 : k1); };
+  auto count =
+      cols ? (last ? pick(part_count_kernel<true, 1, true>, part_count_kernel<true, 2, true>,
+                          part_count_kernel<true, 4, true>)
+                   : pick(part_count_kernel<true, 1, false>, part_count_kernel<true, 2, false>,
+                          part_count_kernel<true, 4, false>))
+           : (last ? pick(part_count_kernel<false, 1, true>, part_count_kernel<false, 2, true>,
+                          part_count_kernel<false, 4, true>)
+                   : pick(part_count_kernel<false, 1, false>, part_count_kernel<false, 2, false>,
+                          part_count_kernel<false, 4, false>));
   hipLaunchKernelGGL(count, dim3(gc), dim3(kPartThreads), 0, s, src, layout.n_rows,
                      layout.tile_width, missing, ridx_in, work, n_work, n_work_dev, splits, sel,
                      node_first_work, work_left, masks, lp, ll);
@@ -282,8 +284,8 @@ void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_lay
     return;
   }
   if (n_work <= 0) return;
-  hipLaunchKernelGGL(wide ? part_scatter_kernel<4> : part_scatter_kernel<1>, dim3(gw),
-                     dim3(kPartThreads), 0, s, sa);
+  hipLaunchKernelGGL(pick(part_scatter_kernel<1>, part_scatter_kernel<2>, part_scatter_kernel<4>),
+                     dim3(gw), dim3(kPartThreads), 0, s, sa);
   DP_HIP(hipGetLastError());
 }
 

@@ -121,3 +121,22 @@ def test_skip_bins_train_the_oracle_model(dp, oracle, device, case):
         tb._compare(bst, o_trees, o_margin, pos, n, k)
         models.append(bst.save_raw())
     assert models[0] == models[1]
+
+
+def test_automatic_skip_rule_counts_padding(dp, device):
+    """dp_skip_bin=1 takes skip bins when they remove at least 20 % of the element atomics,
+    counting the last tile's padding features: 8 features in a 16-wide tile qualify (share
+    >= 0.5), 28 quantile-binned features in two tiles (4 padding slots of 32) do not."""
+    from dpgbdt import ops
+
+    for config, f, expect in ((1, 8, True), (2, 28, False)):
+        values, labels, _, _ = ops.synth(config, 20000, 3, n_features=f)
+        dtrain = dp.DMatrix(values, labels)
+        bst = dp.Booster({"objective": "binary:logistic", "max_depth": 4}, [dtrain])
+        bst.update(dtrain, 0)
+        report = bst.tuning()
+        print(f"[skip rule] {f} features: skip_bins {report['skip_bins']}, "
+              f"share {report.get('skip_share')}", flush=True)
+        assert report["skip_bins"] is expect
+        slots = 16 * ((f + 15) // 16)
+        assert report["skip_share"] >= (slots - f) / slots
