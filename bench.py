@@ -293,6 +293,24 @@ def tree_algorithmic_bytes(t, n_rows, n_features, n_bins, depth, density=None):
     return total
 
 
+def tree_hist_elements(t, n_rows, n_features, depth):
+    """(row, feature) elements the dense histogram passes of one tree accumulate: the root
+    over all rows, then the smaller child of every pair that gets a histogram (its sibling
+    comes from subtraction).  Two 64-bit LDS atomics each: with the LDS roof's rate this
+    gives the tree's histogram time at the roof."""
+    left, right, rows = t["left"], t["right"], t["rows"]
+    dep = [0] * len(left)
+    total = n_rows * n_features
+    for v in range(len(left)):
+        if left[v] < 0:
+            continue
+        a, b = int(left[v]), int(right[v])
+        dep[a] = dep[b] = dep[v] + 1
+        if dep[v] + 1 < depth:
+            total += min(int(rows[a]), int(rows[b])) * n_features
+    return total
+
+
 def trees_leg(torch, dp, ops, name, rows=None, warm_rounds=4):
     """Wall time of the configuration's boosting rounds on a fresh booster (the
     matrix is quantised and the kernels warmed by a previous booster).  The warm
@@ -330,17 +348,20 @@ def trees_leg(torch, dp, ops, name, rows=None, warm_rounds=4):
     el = time.perf_counter() - t0
     trees = bst.num_trees()
     tuning = bst.tuning()  # the autotuner's launch shapes for this matrix
-    nodes, abytes = 0, 0
+    nodes, abytes, helems = 0, 0, 0
     for t in range(trees):
         tr = bst.tree(t)
         nodes += len(tr["left"])
         abytes += tree_algorithmic_bytes(tr, n, f, max_bin, depth, density)
+        helems += tree_hist_elements(tr, n, f, depth)
     del bst, dtrain
     torch.cuda.empty_cache()
     gbs = abytes / el / 1e9
     return {"trees": trees, "rounds": rounds, "seconds": el, "value": trees / el,
             "unit": "trees/s", "rows": n, "features": f, "depth": depth, "objective": objective,
             "nodes": nodes, "layout": layout, "algorithmic_bytes_per_tree": abytes / trees,
+            # dense layouts: (row, feature) elements of the histogram passes per tree
+            "hist_elements_per_tree": None if density else helems / trees,
             "gbs": gbs, "pct_hbm_peak": 100.0 * gbs / HBM_PEAK_GBS,
             "hist_config": tuning.get("chosen", tuning)}
 
@@ -433,6 +454,9 @@ def main():
         return
     hist, sample, *_ = hist_leg(args, torch, dp, ops)
     log(f"hist: {hist['avg_ms']:.3f} ms/launch, {hist['achieved_gbs']:.0f} GB/s algorithmic")
+    cands = sorted(hist["tuning"].get("root", []), key=lambda c: c["ms"])
+    log("autotuner, fastest root shapes (hist + reduce ms): " + ", ".join(
+        f"{c['tiles']}t/{c['unroll']}u/{c['items']}i/s{c['split']} {c['ms']:.3f}" for c in cands[:8]))
     roof = lds_roof_leg(torch, hist["n"] * hist["f"])
     if roof:
         roof["frac"] = roof["two_u64_ms"] / hist["avg_ms"]
@@ -448,6 +472,10 @@ def main():
             time.sleep(LEG_GAP_S)
             trees[name] = trees_leg(torch, dp, ops, name,
                                     rows=args.rows if name == "C3" else None)
+            el = trees[name]["hist_elements_per_tree"]
+            if roof and el:  # the tree's histogram passes at the LDS roof's rate
+                trees[name]["hist_lds_roof_ms_per_tree"] = \
+                    roof["two_u64_ms"] * el / (hist["n"] * hist["f"])
             log(f"{name}: {trees[name]['value']:.1f} trees/s")
     cpu = None
     if sample is not None:
