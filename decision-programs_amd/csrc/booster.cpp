@@ -414,10 +414,26 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     int64_t* h = hist_[cur].p;
     if (split) {
       const int32_t tf = q.sparse.tile_features;
+      // Column sampling: each node's feature sample, read by the evaluation.
+      const uint32_t* fmask = nullptr;
+      if (colsample.active()) {
+        need(colsample_, "column sampling buffers were not prepared");
+        launch_colsample(level_[cur].p, int32_t(nb), field(c, &PlanCounts::n_level), F,
+                         colsample, d, fmask_.p, s);
+        fmask = fmask_.p;
+      }
+      // The present-value layout's partial slots hold node-histogram words: its
+      // levels reduce and evaluate in one launch (up to 64 bins).
+      const bool fused = sparse_ && B <= 64 && tf % 16 == 0 && exps;
       if (d == 0 && sparse_) {
         launch_hist_sparse(q.sparse, N, F, gpair, nullptr, root_work_.p, root_items_, nullptr, B,
                            h, partial_.p, s);
-        launch_hist_reduce_flat(partial_.p, root_job_.p, 1, nullptr, T, tf, F, B, nullptr, h, s);
+        if (fused)
+          launch_reduce_evaluate_flat(partial_.p, root_job_.p, 1, nullptr, T, tf, F, B, nullptr, h,
+                                      q.d_nbins.p, sums_[cur].p, exps, dtp, fmask,
+                                      skip_features_, eval_scratch_.p, s);
+        else
+          launch_hist_reduce_flat(partial_.p, root_job_.p, 1, nullptr, T, tf, F, B, nullptr, h, s);
       } else if (d == 0) {
         launch_hist(q.bins.p, L, gpair, nullptr, root_work_.p, root_items_, nullptr, B, h,
                     partial_.p, s, nullptr, root_cfg_, skip_tiles_);
@@ -426,8 +442,15 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
         launch_hist_sparse(q.sparse, N, F, gpair, ridx_[cur].p, hist_work_[cur].p,
                            int32_t(plan_hist_items(nb, N, T, level_cfg_.items)),
                            field(c, &PlanCounts::n_hist), B, h, partial_.p, s);
-        launch_hist_reduce_flat(partial_.p, reduce_jobs_[cur].p, int32_t(nb / 2 + 1),
-                                field(c, &PlanCounts::n_reduce), T, tf, F, B, hist_[nxt].p, h, s);
+        if (fused)
+          launch_reduce_evaluate_flat(partial_.p, reduce_jobs_[cur].p, int32_t(nb / 2 + 1),
+                                      field(c, &PlanCounts::n_reduce), T, tf, F, B, hist_[nxt].p,
+                                      h, q.d_nbins.p, sums_[cur].p, exps, dtp, fmask,
+                                      skip_features_, eval_scratch_.p, s);
+        else
+          launch_hist_reduce_flat(partial_.p, reduce_jobs_[cur].p, int32_t(nb / 2 + 1),
+                                  field(c, &PlanCounts::n_reduce), T, tf, F, B, hist_[nxt].p, h,
+                                  s);
       } else {
         const int32_t G = (T + level_cfg_.tiles - 1) / level_cfg_.tiles;
         launch_hist(q.bins.p, L, gpair, ridx_[cur].p, hist_work_[cur].p,
@@ -437,19 +460,12 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
         launch_hist_reduce(partial_.p, reduce_jobs_[cur].p, int32_t(nb / 2 + 1),
                            field(c, &PlanCounts::n_reduce), T, F, B, hist_[nxt].p, h, false, s);
       }
-      // Column sampling: each node's feature sample, read by the evaluation.
-      const uint32_t* fmask = nullptr;
-      if (colsample.active()) {
-        need(colsample_, "column sampling buffers were not prepared");
-        launch_colsample(level_[cur].p, int32_t(nb), field(c, &PlanCounts::n_level), F,
-                         colsample, d, fmask_.p, s);
-        fmask = fmask_.p;
-      }
       // Without records from the evaluation, the count launch selects them.
-      const bool records = launch_evaluate(h, int32_t(nb), field(c, &PlanCounts::n_level), F, B,
-                                           q.d_nbins.p, sums_[cur].p, exps, 0, 0, dtp,
-                                           eval_scratch_.p, splits_.p, s, false, fmask,
-                                           skip_features_);
+      const bool records =
+          fused ? false
+                : launch_evaluate(h, int32_t(nb), field(c, &PlanCounts::n_level), F, B,
+                                  q.d_nbins.p, sums_[cur].p, exps, 0, 0, dtp, eval_scratch_.p,
+                                  splits_.p, s, false, fmask, skip_features_);
       SplitSelect sel;
       sel.cand = reinterpret_cast<const FeatCand*>(eval_scratch_.p);
       sel.n_features = F;

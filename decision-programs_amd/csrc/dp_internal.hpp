@@ -367,6 +367,18 @@ bool launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_node
 // skip_bins ([n_features] bytes, matrices without missing values): the
 // histograms leave each feature's skip bin at zero (launch_hist's skip); the
 // node's remaining sums (totals minus the bins) are that bin's.
+// Present-value layout (at most 64 bins, tiles of a multiple of 16 features):
+// launch_hist_reduce_flat and launch_evaluate(..., select = false) in one
+// launch -- the same node histograms (built and sibling) and the same
+// per-feature candidates in scratch.  exps: the quantiser exponents in device
+// memory.
+void launch_reduce_evaluate_flat(const int64_t* partial, const HistReduce* jobs, int32_t n_jobs,
+                                 const int32_t* n_jobs_dev, int32_t n_tiles, int32_t tile_features,
+                                 int32_t n_features, int32_t bin_stride,
+                                 const int64_t* parent_base, int64_t* hist, const int32_t* n_bins,
+                                 const int64_t* node_sums, const int32_t* exps,
+                                 const dp_train_param& param, const uint32_t* fmask,
+                                 const uint8_t* skip_bins, void* scratch, hipStream_t s);
 // Column sampling of one level (ColSample active): masks[node][ceil(F / 32)]
 // gets each node's feature sample (bit f set: feature f is a candidate), for
 // the node count *n_dev (n_host when null; n_host bounds the grid).  depth is

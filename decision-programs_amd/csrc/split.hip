@@ -218,12 +218,6 @@ __global__ __launch_bounds__(64 * kFeatWaves) void evaluate_features_kernel(
   }
 }
 
-// Up to 64 bins: four features per wavefront, one per 16-lane row, four bins
-// per lane (bin 4 * (lane % 16) + j).  The row's prefix scan and argmax take
-// the row_shr steps of the full-wave ones; the row total and the winner's
-// fields come by lane permutes.  Same per-bin arithmetic and tie rule as
-// feature_best, with a quarter of the wavefronts and of their fixed costs.
-// Workgroups loop over (node, group of 16 features) items.
 constexpr int kSegFeatures = 16;  // features per workgroup (four per wavefront)
 
 __device__ __forceinline__ long long row_shuffle64(long long v, int src) {
@@ -232,6 +226,107 @@ __device__ __forceinline__ long long row_shuffle64(long long v, int src) {
   return (long long)((uint64_t(uint32_t(hi)) << 32) | uint32_t(lo));
 }
 
+// The evaluation of four features per wavefront, one per 16-lane row, four bins
+// per lane (bins 4 * (lane % 16) + j in dg, dh): the row's prefix scan and
+// argmax take the row_shr steps of the full-wave ones; the row total and the
+// winner's fields come by lane permutes.  Same per-bin arithmetic and tie rule
+// as feature_best, with a quarter of the wavefronts and of their fixed costs.
+// The row's first lane writes feature f's best candidate of `node` (live: the
+// row's feature exists; every lane takes part in the row steps).
+__device__ __forceinline__ void seg_evaluate(const long long (&dg)[4], const long long (&dh)[4],
+                                             int32_t node, int32_t f, bool live,
+                                             int32_t n_features, const int32_t* __restrict__ n_bins,
+                                             const long long* __restrict__ node_sums, double ug,
+                                             double uh, const Param& p,
+                                             const uint32_t* __restrict__ fmask,
+                                             const uint8_t* __restrict__ skip_bins,
+                                             FeatCand* __restrict__ cand) {
+  constexpr int BPL = 4;
+  const int lane = threadIdx.x & 63;
+  const int seg = lane >> 4, sub = lane & 15;
+  const int row_last = lane | 15;
+  const int nb = live && feature_allowed(fmask, node, f, n_features) ? n_bins[f] : 0;
+  const long long gp = node_sums[2 * node], hp = node_sums[2 * node + 1];
+  const double parent_gain = calc_gain(p, double(gp) * ug, double(hp) * uh);
+  long long sg[BPL], sh[BPL];
+  long long rg = 0, rh = 0;
+#pragma unroll
+  for (int j = 0; j < BPL; ++j) {
+    rg += dg[j];
+    rh += dh[j];
+    sg[j] = rg;
+    sh[j] = rh;
+  }
+  // inclusive scan of the lane totals within the 16-lane row
+  long long ig = rg, ih = rh;
+  ig += dpp64<0x111>(ig, 0);
+  ih += dpp64<0x111>(ih, 0);
+  ig += dpp64<0x112>(ig, 0);
+  ih += dpp64<0x112>(ih, 0);
+  ig += dpp64<0x114>(ig, 0);
+  ih += dpp64<0x114>(ih, 0);
+  ig += dpp64<0x118>(ig, 0);
+  ih += dpp64<0x118>(ih, 0);
+  const long long total_g = row_shuffle64(ig, row_last), total_h = row_shuffle64(ih, row_last);
+  const long long og = ig - rg, oh = ih - rh;
+  // as feature_best: a skipped bin's rows return at the prefixes from that bin
+  const int skip = live && skip_bins ? int(skip_bins[f]) : -1;
+  long long mg = gp - total_g, mh = hp - total_h, kg = 0, kh = 0;
+  if (skip >= 0) {
+    kg = mg;
+    kh = mh;
+    mg = mh = 0;
+  }
+
+  Cand c;
+  c.loss = -INFINITY;
+  c.gl = c.hl = 0;
+  c.feature = f;
+  c.bin = -1;
+  c.dl = 0;
+#pragma unroll
+  for (int j = 0; j < BPL; ++j) {
+    const int b = sub * BPL + j;
+    if (b < nb) {
+      const long long lg = og + sg[j] + (b >= skip && skip >= 0 ? kg : 0);
+      const long long lh = oh + sh[j] + (b >= skip && skip >= 0 ? kh : 0);
+      const double right_missing = split_loss(p, lg, lh, gp - lg, hp - lh, ug, uh, parent_gain);
+      const double left_missing =
+          (mg == 0 && mh == 0)
+              ? right_missing
+              : split_loss(p, lg + mg, lh + mh, gp - lg - mg, hp - lh - mh, ug, uh, parent_gain);
+      const int dl = left_missing > right_missing;
+      const double loss = dl ? left_missing : right_missing;
+      if (loss > c.loss) {
+        c.loss = loss;
+        c.bin = b;
+        c.dl = dl;
+        c.gl = dl ? lg + mg : lg;
+        c.hl = dl ? lh + mh : lh;
+      }
+    }
+  }
+  // Row argmax: the largest loss, then the lowest lane holding it (lanes hold
+  // increasing bins and each kept its lowest bin on ties).
+  long long bb = __double_as_longlong(c.loss);
+  auto step = [&](long long o) {
+    if (dpp_f64_bits(o) > dpp_f64_bits(bb)) bb = o;
+  };
+  step(dpp64<0x111>(bb, bb));
+  step(dpp64<0x112>(bb, bb));
+  step(dpp64<0x114>(bb, bb));
+  step(dpp64<0x118>(bb, bb));
+  const double best = dpp_f64_bits(row_shuffle64(bb, row_last));
+  const unsigned long long hit = __ballot(c.loss == best);
+  const int winner = seg * 16 + __builtin_ctzll((hit >> (seg * 16)) & 0xffffull);
+  const long long w_gl = row_shuffle64(c.gl, winner), w_hl = row_shuffle64(c.hl, winner);
+  const int w_bin = __shfl(c.bin, winner, 64), w_dl = __shfl(c.dl, winner, 64);
+  if (live && sub == 0)
+    cand[int64_t(node) * n_features + f] = FeatCand{best, w_gl, w_hl, w_bin, w_dl};
+}
+
+// Up to 64 bins: four features per wavefront (seg_evaluate).  Workgroups loop
+// over (node, group of 16 features) items.
 __global__ __launch_bounds__(256) void evaluate_features_seg_kernel(
     const long long* __restrict__ hist, int32_t n_nodes_host,
     const int32_t* __restrict__ n_nodes_dev, int32_t n_features, int32_t bin_stride,
@@ -248,7 +343,6 @@ __global__ __launch_bounds__(256) void evaluate_features_seg_kernel(
   const int exp_g = exps ? exps[0] : exp_g_host;
   const int exp_h = exps ? exps[1] : exp_h_host;
   const double ug = ldexp(1.0, -exp_g), uh = ldexp(1.0, -exp_h);
-  const int row_last = lane | 15;
   for (int64_t item = blockIdx.x; item < n_items; item += gridDim.x) {
     const int32_t node = int32_t(item / groups);
     const int32_t f = int32_t(item % groups) * kSegFeatures + wave * 4 + seg;
@@ -261,84 +355,95 @@ __global__ __launch_bounds__(256) void evaluate_features_seg_kernel(
       dg[j] = live && b < bin_stride ? hf[2 * b] : 0;
       dh[j] = live && b < bin_stride ? hf[2 * b + 1] : 0;
     }
-    const int nb = live && feature_allowed(fmask, node, f, n_features) ? n_bins[f] : 0;
-    const long long gp = node_sums[2 * node], hp = node_sums[2 * node + 1];
-    const double parent_gain = calc_gain(p, double(gp) * ug, double(hp) * uh);
-    long long sg[BPL], sh[BPL];
-    long long rg = 0, rh = 0;
-#pragma unroll
-    for (int j = 0; j < BPL; ++j) {
-      rg += dg[j];
-      rh += dh[j];
-      sg[j] = rg;
-      sh[j] = rh;
-    }
-    // inclusive scan of the lane totals within the 16-lane row
-    long long ig = rg, ih = rh;
-    ig += dpp64<0x111>(ig, 0);
-    ih += dpp64<0x111>(ih, 0);
-    ig += dpp64<0x112>(ig, 0);
-    ih += dpp64<0x112>(ih, 0);
-    ig += dpp64<0x114>(ig, 0);
-    ih += dpp64<0x114>(ih, 0);
-    ig += dpp64<0x118>(ig, 0);
-    ih += dpp64<0x118>(ih, 0);
-    const long long total_g = row_shuffle64(ig, row_last), total_h = row_shuffle64(ih, row_last);
-    const long long og = ig - rg, oh = ih - rh;
-    // as feature_best: a skipped bin's rows return at the prefixes from that bin
-    const int skip = live && skip_bins ? int(skip_bins[f]) : -1;
-    long long mg = gp - total_g, mh = hp - total_h, kg = 0, kh = 0;
-    if (skip >= 0) {
-      kg = mg;
-      kh = mh;
-      mg = mh = 0;
-    }
+    seg_evaluate(dg, dh, node, f, live, n_features, n_bins, node_sums, ug, uh, p, fmask,
+                 skip_bins, cand);
+  }
+}
 
-    Cand c;
-    c.loss = -INFINITY;
-    c.gl = c.hl = 0;
-    c.feature = f;
-    c.bin = -1;
-    c.dl = 0;
+// Reduce and evaluate in one launch for the present-value layout, whose
+// partial slots already hold the node histogram's [feature][bin][g, h] words
+// (word e of tile t's slot is word t * tile_features * bin_stride * 2 + e of a
+// node histogram).  A 256-thread workgroup per (reduce job, 16 features): each
+// lane owns four bins of one feature, as seg_evaluate holds them, sums the
+// job's partial slots of its 64 contiguous bytes (or takes what the node's
+// only chunk wrote), writes the built and sibling words, and evaluates both
+// nodes' feature from its registers.  No barriers, and no second pass over the
+// level's histograms: the words and candidates are those of
+// hist_reduce_flat_kernel followed by evaluate_features_seg_kernel.
+__global__ __launch_bounds__(256) void reduce_evaluate_flat_kernel(
+    const long long* __restrict__ partial, const HistReduce* __restrict__ jobs,
+    int32_t n_jobs_host, const int32_t* __restrict__ n_jobs_dev, int32_t n_tiles,
+    int32_t tile_features, int32_t n_features, int32_t bin_stride,
+    const long long* __restrict__ parent_base, long long* __restrict__ hist,
+    const int32_t* __restrict__ n_bins, const long long* __restrict__ node_sums,
+    const int32_t* __restrict__ exps, Param p, const uint32_t* __restrict__ fmask,
+    const uint8_t* __restrict__ skip_bins, FeatCand* __restrict__ cand) {
+  constexpr int BPL = 4;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int seg = lane >> 4, sub = lane & 15;
+  const int32_t f = int32_t(blockIdx.x) * kSegFeatures + wave * 4 + seg;
+  const bool live = f < n_features;
+  const int32_t fl = live ? f : 0;
+  const int32_t t = fl / tile_features;
+  const int64_t slot_words = int64_t(tile_features) * bin_stride * 2;
+  const int64_t node_elems = int64_t(n_features) * bin_stride * 2;
+  const int64_t feat_at = int64_t(fl) * bin_stride * 2 + 2 * (sub * BPL);  // this lane's first bin
+  const int64_t slot_at = int64_t(fl - t * tile_features) * bin_stride * 2 + 2 * (sub * BPL);
+  // bins of this lane that exist (the lane's bins are sub * 4 + j)
+  const int rest = bin_stride - sub * BPL;
+  const int nbl = !live || rest < 0 ? 0 : (rest > BPL ? BPL : rest);
+  const int32_t n_jobs = n_jobs_dev ? *n_jobs_dev : n_jobs_host;
+  const double ug = ldexp(1.0, -exps[0]), uh = ldexp(1.0, -exps[1]);
+  for (int32_t jb = blockIdx.y; jb < n_jobs; jb += gridDim.y) {
+    const HistReduce j = jobs[jb];
+    long long bg[BPL] = {0, 0, 0, 0}, bh[BPL] = {0, 0, 0, 0};
+    long long* built = hist + int64_t(j.slot) * node_elems + feat_at;
+    if (j.nc == 1 && j.p0 < 0) {  // written directly by the node's only chunk
 #pragma unroll
-    for (int j = 0; j < BPL; ++j) {
-      const int b = sub * BPL + j;
-      if (b < nb) {
-        const long long lg = og + sg[j] + (b >= skip && skip >= 0 ? kg : 0);
-        const long long lh = oh + sh[j] + (b >= skip && skip >= 0 ? kh : 0);
-        const double right_missing = split_loss(p, lg, lh, gp - lg, hp - lh, ug, uh, parent_gain);
-        const double left_missing =
-            (mg == 0 && mh == 0)
-                ? right_missing
-                : split_loss(p, lg + mg, lh + mh, gp - lg - mg, hp - lh - mh, ug, uh, parent_gain);
-        const int dl = left_missing > right_missing;
-        const double loss = dl ? left_missing : right_missing;
-        if (loss > c.loss) {
-          c.loss = loss;
-          c.bin = b;
-          c.dl = dl;
-          c.gl = dl ? lg + mg : lg;
-          c.hl = dl ? lh + mh : lh;
+      for (int k = 0; k < BPL; ++k) {
+        if (k < nbl) {
+          bg[k] = built[2 * k];
+          bh[k] = built[2 * k + 1];
+        }
+      }
+    } else {
+      const long long* src = partial + (int64_t(j.p0) * n_tiles + t) * slot_words + slot_at;
+      const int64_t step = int64_t(n_tiles) * slot_words;
+      for (int32_t c = 0; c < j.nc; ++c) {
+#pragma unroll
+        for (int k = 0; k < BPL; ++k) {
+          if (k < nbl) {
+            bg[k] += src[c * step + 2 * k];
+            bh[k] += src[c * step + 2 * k + 1];
+          }
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < BPL; ++k) {
+        if (k < nbl) {
+          built[2 * k] = bg[k];
+          built[2 * k + 1] = bh[k];
         }
       }
     }
-    // Row argmax: the largest loss, then the lowest lane holding it (lanes hold
-    // increasing bins and each kept its lowest bin on ties).
-    long long bb = __double_as_longlong(c.loss);
-    auto step = [&](long long o) {
-      if (dpp_f64_bits(o) > dpp_f64_bits(bb)) bb = o;
-    };
-    step(dpp64<0x111>(bb, bb));
-    step(dpp64<0x112>(bb, bb));
-    step(dpp64<0x114>(bb, bb));
-    step(dpp64<0x118>(bb, bb));
-    const double best = dpp_f64_bits(row_shuffle64(bb, row_last));
-    const unsigned long long hit = __ballot(c.loss == best);
-    const int winner = seg * 16 + __builtin_ctzll((hit >> (seg * 16)) & 0xffffull);
-    const long long w_gl = row_shuffle64(c.gl, winner), w_hl = row_shuffle64(c.hl, winner);
-    const int w_bin = __shfl(c.bin, winner, 64), w_dl = __shfl(c.dl, winner, 64);
-    if (live && sub == 0)
-      cand[int64_t(node) * n_features + f] = FeatCand{best, w_gl, w_hl, w_bin, w_dl};
+    seg_evaluate(bg, bh, j.slot, f, live, n_features, n_bins, node_sums, ug, uh, p, fmask,
+                 skip_bins, cand);
+    if (j.sibling >= 0) {  // uniform per workgroup
+      long long sg[BPL] = {0, 0, 0, 0}, sh[BPL] = {0, 0, 0, 0};
+      const long long* par = parent_base + j.parent + feat_at;
+      long long* sib = hist + int64_t(j.sibling) * node_elems + feat_at;
+#pragma unroll
+      for (int k = 0; k < BPL; ++k) {
+        if (k < nbl) {
+          sg[k] = par[2 * k] - bg[k];
+          sh[k] = par[2 * k + 1] - bh[k];
+          sib[2 * k] = sg[k];
+          sib[2 * k + 1] = sh[k];
+        }
+      }
+      seg_evaluate(sg, sh, j.sibling, f, live, n_features, n_bins, node_sums, ug, uh, p, fmask,
+                   skip_bins, cand);
+    }
   }
 }
 
@@ -590,6 +695,33 @@ bool launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_node
                      double(param.gamma), out);
   DP_HIP(hipGetLastError());
   return true;
+}
+
+void launch_reduce_evaluate_flat(const int64_t* partial, const HistReduce* jobs, int32_t n_jobs,
+                                 const int32_t* n_jobs_dev, int32_t n_tiles, int32_t tile_features,
+                                 int32_t n_features, int32_t bin_stride,
+                                 const int64_t* parent_base, int64_t* hist, const int32_t* n_bins,
+                                 const int64_t* node_sums, const int32_t* exps,
+                                 const dp_train_param& param, const uint32_t* fmask,
+                                 const uint8_t* skip_bins, void* scratch, hipStream_t s) {
+  if (n_jobs <= 0) return;
+  need(bin_stride >= 1 && bin_stride <= 64, "the present-value reduce-evaluate takes <= 64 bins");
+  need(tile_features >= kSegFeatures && tile_features % kSegFeatures == 0,
+       "present-value tiles must hold whole groups of 16 features");
+  need(n_tiles == (n_features + tile_features - 1) / tile_features, "tile count");
+  need(exps && scratch, "reduce-evaluate needs the quantiser exponents and candidate scratch");
+  Param p{double(param.lambda), double(param.alpha), double(param.min_child_weight),
+          double(param.gamma)};
+  const dim3 grid(unsigned((n_features + kSegFeatures - 1) / kSegFeatures),
+                  unsigned(n_jobs < 256 ? n_jobs : 256));
+  hipLaunchKernelGGL(reduce_evaluate_flat_kernel, grid, dim3(256), 0, s,
+                     reinterpret_cast<const long long*>(partial), jobs, n_jobs, n_jobs_dev,
+                     n_tiles, tile_features, n_features, bin_stride,
+                     reinterpret_cast<const long long*>(parent_base),
+                     reinterpret_cast<long long*>(hist), n_bins,
+                     reinterpret_cast<const long long*>(node_sums), exps, p, fmask, skip_bins,
+                     static_cast<FeatCand*>(scratch));
+  DP_HIP(hipGetLastError());
 }
 
 void launch_colsample(const LevelNode* nodes, int32_t n_host, const int32_t* n_dev,
