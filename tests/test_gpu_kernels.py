@@ -236,6 +236,37 @@ def test_gathered_histograms_and_subtraction(dp, oracle, ws, device):
     np.testing.assert_array_equal(sib.cpu().numpy(), hn_[4])
 
 
+def test_workspace_staging_reuse(dp, oracle, ws, device):
+    """A workspace skips re-uploading work lists identical to its last upload: calls with
+    lists A, A (no upload), B, A (uploads again), and accumulating calls on A, each give the
+    oracle's histograms."""
+    import torch
+    from dpgbdt import ops
+
+    n, f = 30000, 40
+    values, _, g, h = _synth(ops, 1, n, 9, f, grad=True)
+    lay, bins, o_bins, cut_ptr, cuts, n_bins, mb = _prepare(dp, oracle, ws, values)
+    stride = int(n_bins.max())
+    gn, hn = g.cpu().numpy(), h.cpu().numpy()
+    _, gpair, _ = _gpair(ws, device, gn, hn)
+    q = oracle.quantise(gn, hn)[0]
+    ridx = np.random.default_rng(4).permutation(n).astype(np.uint32)
+    d_ridx = torch.as_tensor(ridx.view(np.int32), device=device)
+    lists = {"A": [(0, 9000), (9000, 30000)], "B": [(0, 17), (17, 25000), (25000, 30000)]}
+    refs = {k: [oracle.hist(o_bins, q[2], q[3], rows=ridx[b:e], bin_stride=stride, missing_bin=mb)
+                for b, e in segs] for k, segs in lists.items()}
+    for name in ("A", "A", "B", "A"):
+        got = ops.hist_build(ws, bins, lay, gpair, lists[name], stride, ridx=d_ridx).cpu().numpy()
+        for i, ref in enumerate(refs[name]):
+            np.testing.assert_array_equal(got[i], ref, err_msg=f"list {name}, segment {i}")
+    acc = torch.zeros((2, f, stride, 2), dtype=torch.int64, device=device)
+    for _ in range(3):
+        ops.hist_accumulate(ws, bins, lay, gpair, lists["A"], acc, ridx=d_ridx)
+    got = acc.cpu().numpy()
+    for i, ref in enumerate(refs["A"]):
+        np.testing.assert_array_equal(got[i], 3 * ref)
+
+
 # 128 features: feature-parallel items (256 bins: one feature per wavefront),
 # then a select kernel; up to 64 bins: four features per wavefront (40 features:
 # the last group holds unused rows); 8 features: one workgroup per node.
