@@ -299,6 +299,11 @@ void Grower::prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, b
   need(N <= int64_t(UINT32_MAX), "row ids are 32-bit");
   need(D >= 1 && D <= 30, "max_depth out of supported range");
   chunk_ = row_chunk(N);
+  if (cus_ == 0) {
+    int dev = 0;
+    DP_HIP(hipGetDevice(&dev));
+    DP_HIP(hipDeviceGetAttribute(&cus_, hipDeviceAttributeMultiprocessorCount, dev));
+  }
   ridx_[0].reserve(size_t(N));
   ridx_[1].reserve(size_t(N));
   counts_.reserve(1);
@@ -525,6 +530,9 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     a.n_tiles = T;
     a.hist_tiles = level_cfg_.tiles;
     a.hist_items = level_cfg_.items;
+    // Dense histogram workgroups resident at once: two per CU with one 64 KiB
+    // tile per item, one with two (the present-value passes keep hist_chunk's).
+    a.hist_slots = sparse_ ? 0 : cus_ * (level_cfg_.tiles == 1 ? 2 : 1);
     a.hist_elems = S;
     a.part_chunk = chunk_;
     a.leaf_chunk = chunk_;

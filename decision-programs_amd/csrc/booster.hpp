@@ -159,6 +159,7 @@ class Grower {
   int32_t tiles_ = 0;    // histogram tiles per row chunk (16-feature or sparse tiles)
   int64_t node_cap_ = 0;
   int64_t chunk_ = kPartChunk;  // rows per partition / margin-update item
+  int32_t cus_ = 0;             // compute units of the device (histogram slots per round)
   size_t slot_bytes_ = 0;
   int64_t root_rows_ = -1;
   int32_t root_tiles_ = 0, root_items_ = 0;

@@ -327,6 +327,29 @@ __host__ __device__ inline int64_t hist_chunk(int64_t rows, int32_t groups, int3
   }
   return c < kHistMinChunk ? kHistMinChunk : c;
 }
+// A level's chunk: hist_chunk's, enlarged when that moves the level's items
+// into one round fewer of the `slots` workgroups the chip holds at once (the
+// last round of items, if only partly filled, takes as long as a full one:
+// measured on C3's gathered passes, 264-276 items on 256 slots took two rounds
+// for one round's work).  The items are at most (ceil(rows / chunk) + nodes) *
+// groups (rows: the built nodes' rows, nodes: their count); the larger chunk
+// keeps that bound within (rounds - 1) * slots, and only replaces hist_chunk's
+// when (rounds - 1) * chunk is the shorter time.  It is never smaller, so the
+// level's items and partial slots stay within hist_chunk's capacity bounds.
+// slots <= 0: hist_chunk's chunk.
+__host__ __device__ inline int64_t hist_chunk_fit(int64_t rows, int64_t nodes, int32_t groups,
+                                                  int32_t items, int32_t slots) {
+  const int64_t c = hist_chunk(rows, groups, items);
+  if (slots <= 0 || rows <= 0 || groups <= 0) return c;
+  const int64_t per_round = slots / groups;  // chunks that fit one round
+  const int64_t bound = (rows + c - 1) / c + nodes;
+  const int64_t rounds = (bound * groups + slots - 1) / slots;
+  if (rounds < 2) return c;
+  const int64_t avail = (rounds - 1) * per_round - nodes;
+  if (avail <= 0) return c;
+  const int64_t c2 = (rows + avail - 1) / avail;
+  return c2 > c && (rounds - 1) * c2 < rounds * c ? c2 : c;
+}
 // Partial slots needed by one level: the chunks of nodes with two or more
 // chunks number at most 2 * items / groups, each with n_tiles slots, i.e. at
 // most 2 * items * tiles_per_item slots.
@@ -500,6 +523,7 @@ struct PlanArgs {
   int32_t n_tiles;
   int32_t hist_tiles;      // tiles per histogram work item (HistConfig::tiles; 1 for present-value)
   int32_t hist_items;      // work items a histogram pass aims at (HistConfig::items)
+  int32_t hist_slots;      // histogram workgroups the chip holds at once (hist_chunk_fit; 0: off)
   int64_t hist_elems;      // int64 values per node histogram
   int64_t part_chunk, leaf_chunk;  // rows per partition / margin-update item
   double eta, lambda, alpha, mcw;

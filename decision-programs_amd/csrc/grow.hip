@@ -281,7 +281,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
     int64_t small_total;
     (void)block_scan(mine, scan, &small_total);
     const int32_t TPW = a.hist_tiles, G = (T + TPW - 1) / TPW;  // items per row chunk
-    const int64_t chunk = hist_chunk(small_total, G, a.hist_items);
+    const int64_t chunk = hist_chunk_fit(small_total, n_expand, G, a.hist_items, a.hist_slots);
     int64_t* cstart = a.pair_chunk;                 // [n_expand + 1]
     int64_t* pstart = a.pair_chunk + n_expand + 1;  // [n_expand + 1]
     int64_t pcarry = 0;
@@ -611,7 +611,7 @@ __device__ void plan_small_level(const PlanArgs& a) {
   // ---- second scan: histogram chunks of the smaller children -----------------
   const int32_t T = a.n_tiles;
   const int32_t TPW = a.hist_tiles, G = (T + TPW - 1) / TPW;  // items per row chunk
-  const int64_t chunk = hist_chunk(tot[2], G, a.hist_items);
+  const int64_t chunk = hist_chunk_fit(tot[2], tot[0], G, a.hist_items, a.hist_slots);
   const int64_t nc = wave_live ? ceil_rows(cnt[2], chunk) : 0;
   int64_t cnt2[2] = {nc, nc >= 2 ? nc : 0}, off2[2], tot2[2];
   if (live) {
