@@ -530,9 +530,9 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     a.n_tiles = T;
     a.hist_tiles = level_cfg_.tiles;
     a.hist_items = level_cfg_.items;
-    // Dense histogram workgroups resident at once: two per CU with one 64 KiB
-    // tile per item, one with two (the present-value passes keep hist_chunk's).
-    a.hist_slots = sparse_ ? 0 : cus_ * (level_cfg_.tiles == 1 ? 2 : 1);
+    // Histogram workgroups resident at once: two per CU with one 64 KiB tile
+    // per item (dense or present-value), one with two dense tiles.
+    a.hist_slots = cus_ * (sparse_ || level_cfg_.tiles == 1 ? 2 : 1);
     a.hist_elems = S;
     a.part_chunk = chunk_;
     a.leaf_chunk = chunk_;
