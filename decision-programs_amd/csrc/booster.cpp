@@ -430,13 +430,16 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
       // The present-value layout's partial slots hold node-histogram words: its
       // levels reduce and evaluate in one launch (up to 64 bins).
       const bool fused = sparse_ && B <= 64 && tf % 16 == 0 && exps;
+      // The last split level's histograms have no readers: a fused launch
+      // evaluates them without storing them.
+      const bool keep = d + 1 < D;
       if (d == 0 && sparse_) {
         launch_hist_sparse(q.sparse, N, F, gpair, nullptr, root_work_.p, root_items_, nullptr, B,
                            h, partial_.p, s);
         if (fused)
           launch_reduce_evaluate_flat(partial_.p, root_job_.p, 1, nullptr, T, tf, F, B, nullptr, h,
                                       q.d_nbins.p, sums_[cur].p, exps, dtp, fmask,
-                                      skip_features_, eval_scratch_.p, s);
+                                      skip_features_, eval_scratch_.p, keep, s);
         else
           launch_hist_reduce_flat(partial_.p, root_job_.p, 1, nullptr, T, tf, F, B, nullptr, h, s);
       } else if (d == 0) {
@@ -451,7 +454,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
           launch_reduce_evaluate_flat(partial_.p, reduce_jobs_[cur].p, int32_t(nb / 2 + 1),
                                       field(c, &PlanCounts::n_reduce), T, tf, F, B, hist_[nxt].p,
                                       h, q.d_nbins.p, sums_[cur].p, exps, dtp, fmask,
-                                      skip_features_, eval_scratch_.p, s);
+                                      skip_features_, eval_scratch_.p, keep, s);
         else
           launch_hist_reduce_flat(partial_.p, reduce_jobs_[cur].p, int32_t(nb / 2 + 1),
                                   field(c, &PlanCounts::n_reduce), T, tf, F, B, hist_[nxt].p, h,

@@ -401,7 +401,8 @@ void launch_reduce_evaluate_flat(const int64_t* partial, const HistReduce* jobs,
                                  const int64_t* parent_base, int64_t* hist, const int32_t* n_bins,
                                  const int64_t* node_sums, const int32_t* exps,
                                  const dp_train_param& param, const uint32_t* fmask,
-                                 const uint8_t* skip_bins, void* scratch, hipStream_t s);
+                                 const uint8_t* skip_bins, void* scratch, bool store,
+                                 hipStream_t s);
 // Column sampling of one level (ColSample active): masks[node][ceil(F / 32)]
 // gets each node's feature sample (bit f set: feature f is a candidate), for
 // the node count *n_dev (n_host when null; n_host bounds the grid).  depth is

@@ -369,7 +369,9 @@ __global__ __launch_bounds__(256) void evaluate_features_seg_kernel(
 // only chunk wrote), writes the built and sibling words, and evaluates both
 // nodes' feature from its registers.  No barriers, and no second pass over the
 // level's histograms: the words and candidates are those of
-// hist_reduce_flat_kernel followed by evaluate_features_seg_kernel.
+// hist_reduce_flat_kernel followed by evaluate_features_seg_kernel.  With
+// store == 0 (the tree's last split level, whose histograms no later level
+// reads) the built and sibling words are evaluated but not written.
 __global__ __launch_bounds__(256) void reduce_evaluate_flat_kernel(
     const long long* __restrict__ partial, const HistReduce* __restrict__ jobs,
     int32_t n_jobs_host, const int32_t* __restrict__ n_jobs_dev, int32_t n_tiles,
@@ -377,7 +379,7 @@ __global__ __launch_bounds__(256) void reduce_evaluate_flat_kernel(
     const long long* __restrict__ parent_base, long long* __restrict__ hist,
     const int32_t* __restrict__ n_bins, const long long* __restrict__ node_sums,
     const int32_t* __restrict__ exps, Param p, const uint32_t* __restrict__ fmask,
-    const uint8_t* __restrict__ skip_bins, FeatCand* __restrict__ cand) {
+    const uint8_t* __restrict__ skip_bins, FeatCand* __restrict__ cand, int32_t store) {
   constexpr int BPL = 4;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int seg = lane >> 4, sub = lane & 15;
@@ -418,11 +420,13 @@ __global__ __launch_bounds__(256) void reduce_evaluate_flat_kernel(
           }
         }
       }
+      if (store) {
 #pragma unroll
-      for (int k = 0; k < BPL; ++k) {
-        if (k < nbl) {
-          built[2 * k] = bg[k];
-          built[2 * k + 1] = bh[k];
+        for (int k = 0; k < BPL; ++k) {
+          if (k < nbl) {
+            built[2 * k] = bg[k];
+            built[2 * k + 1] = bh[k];
+          }
         }
       }
     }
@@ -437,8 +441,10 @@ __global__ __launch_bounds__(256) void reduce_evaluate_flat_kernel(
         if (k < nbl) {
           sg[k] = par[2 * k] - bg[k];
           sh[k] = par[2 * k + 1] - bh[k];
-          sib[2 * k] = sg[k];
-          sib[2 * k + 1] = sh[k];
+          if (store) {
+            sib[2 * k] = sg[k];
+            sib[2 * k + 1] = sh[k];
+          }
         }
       }
       seg_evaluate(sg, sh, j.sibling, f, live, n_features, n_bins, node_sums, ug, uh, p, fmask,
@@ -703,7 +709,8 @@ void launch_reduce_evaluate_flat(const int64_t* partial, const HistReduce* jobs,
                                  const int64_t* parent_base, int64_t* hist, const int32_t* n_bins,
                                  const int64_t* node_sums, const int32_t* exps,
                                  const dp_train_param& param, const uint32_t* fmask,
-                                 const uint8_t* skip_bins, void* scratch, hipStream_t s) {
+                                 const uint8_t* skip_bins, void* scratch, bool store,
+                                 hipStream_t s) {
   if (n_jobs <= 0) return;
   need(bin_stride >= 1 && bin_stride <= 64, "the present-value reduce-evaluate takes <= 64 bins");
   need(tile_features >= kSegFeatures && tile_features % kSegFeatures == 0,
@@ -720,7 +727,7 @@ void launch_reduce_evaluate_flat(const int64_t* partial, const HistReduce* jobs,
                      reinterpret_cast<const long long*>(parent_base),
                      reinterpret_cast<long long*>(hist), n_bins,
                      reinterpret_cast<const long long*>(node_sums), exps, p, fmask, skip_bins,
-                     static_cast<FeatCand*>(scratch));
+                     static_cast<FeatCand*>(scratch), store ? 1 : 0);
   DP_HIP(hipGetLastError());
 }
 
