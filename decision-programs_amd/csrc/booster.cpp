@@ -7,9 +7,10 @@
 //   histogram build of the smaller child of every pair (gather by row ids)
 //   -> sibling = parent - built -> split evaluation -> stable partition
 //   -> planner (node records, child numbering, next level's work, leaf work)
-//   -> margin update of the level's leaves
+//   -> the leaf values of the level's leaves, stored per row
 // with every count read from device memory, so a round's trees are enqueued
-// back to back and the host reads the node records once per round.
+// back to back and the host reads the node records once per round.  The round
+// ends by adding its trees' per-row leaf values to the margins in row order.
 #include "booster.hpp"
 
 #include <algorithm>
@@ -361,8 +362,7 @@ void Grower::prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, b
 
 void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
                   const int64_t* root_slots, int32_t root_blocks, const TrainParam& p,
-                  float* margin, int64_t stride,
-                  int32_t* positions, int32_t slot, hipStream_t s) {
+                  float* values, int32_t* positions, int32_t slot, hipStream_t s) {
   const dp_bin_layout& L = q.layout;
   const int64_t N = L.n_rows;
   const int32_t F = L.n_features, B = q.bin_stride, T = tiles_, D = p.max_depth;
@@ -379,8 +379,9 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
                    node_left_[0].p, c, N, root_slots, root_blocks, chunk_, ridx_[0].p, s);
   int64_t nb = 1;  // bound of the current level's node count
   int64_t nb_prev = 0;
-  // The last split level's count launch adds every leaf value of levels D - 1
-  // and D to the margins (rows of expanding nodes and of D - 1's leaves).
+  // The last split level's count launch stores every leaf value of levels
+  // D - 1 and D (rows of expanding nodes and of D - 1's leaves).  Every leaf
+  // pass stores into the leaf-value plane: no margin is read here.
   bool last_level_applied = false;
   for (int32_t d = 0; d <= D; ++d) {
     const int cur = d & 1, nxt = cur ^ 1;
@@ -392,7 +393,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
         const int32_t bound = int32_t(plan_leaf_capacity(nb_prev, N, chunk_));
         if (!last_level_applied)  // else the last split level's count launch did
           launch_update_margin(ridx_[nxt].p, leaf_work_[nxt].p, bound,
-                               field(c, &PlanCounts::n_leaf), margin, stride, s);
+                               field(c, &PlanCounts::n_leaf), values, 1, s, nullptr, true);
         if (positions)
           launch_leaf_positions(ridx_[nxt].p, leaf_work_[nxt].p, bound,
                                 field(c, &PlanCounts::n_leaf), positions, s);
@@ -412,9 +413,9 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     // scatter in one launch.
     const bool merged = split && nb <= 1024;
     // On the last split level of such a tree the rows need no new order: the
-    // count launch updates the margins and the planner runs alone (unless leaf
+    // count launch stores the leaf values and the planner runs alone (unless leaf
     // ids are wanted, which the scatter's segments give).
-    const bool fuse_last = merged && d + 1 == D && margin && !positions;
+    const bool fuse_last = merged && d + 1 == D && values && !positions;
     ScatterArgs scatter{};
     int64_t* h = hist_[cur].p;
     if (split) {
@@ -487,14 +488,14 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
         prev.work = leaf_work_[nxt].p;
         prev.n_dev = field(c, &PlanCounts::n_leaf);
         prev.n_host = int32_t(plan_leaf_capacity(nb_prev, N, chunk_));
-        prev.margin = margin;
-        prev.stride = stride;
+        prev.margin = values;
+        prev.stride = 1;
+        prev.store = true;
         prev.positions = positions;
       }
       LastLevel ll{};
       if (fuse_last) {
-        ll.margin = margin;
-        ll.stride = stride;
+        ll.values = values;
         ll.nodes = level_[cur].p;
         ll.exps = exps;
         ll.eta = double(p.eta);
@@ -555,7 +556,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
       a.part_bound = int32_t(plan_part_capacity(nb, N, chunk_));
     }
     // The last split level's planner also writes its children's records (all
-    // leaves, their values already in the margins): no planner for level D.
+    // leaves, their values already stored): no planner for level D.
     a.leaf_children = fuse_last ? 1 : 0;
     if (merged && !fuse_last) launch_plan_scatter(a, scatter, N, s);
     else if (!(d == D && last_level_applied)) launch_plan_level(a, nb, s);
@@ -574,8 +575,8 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
       }
       if (!last_level_applied)
         launch_update_margin(ridx_[cur].p, leaf_work_[cur].p, leaf_bound,
-                             field(c, &PlanCounts::n_leaf), margin, stride, s,
-                             D >= 1 ? &prev_leaves : nullptr);
+                             field(c, &PlanCounts::n_leaf), values, 1, s,
+                             D >= 1 ? &prev_leaves : nullptr, true);
       if (positions) {
         if (D >= 1)
           launch_leaf_positions(prev_leaves.ridx, prev_leaves.work, prev_leaves.n_host,
@@ -882,6 +883,7 @@ void Booster::configure(DMatrix* d) {
   const int64_t N = d->n_rows;
   DP_HIP(hipStreamCreateWithFlags(&stream_, hipStreamDefault));  // orders with the null stream
   margin_.resize(size_t(N) * n_groups_);
+  leaf_values_.resize(size_t(N) * n_groups_);
   grad_.resize(size_t(N) * n_groups_);
   hess_.resize(size_t(N) * n_groups_);
   gpair_.resize(size_t(N) * n_groups_ * 2);
@@ -1097,6 +1099,7 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
       reinterpret_cast<uint64_t>(q.rows.p), reinterpret_cast<uint64_t>(q.d_nbins.p),
       uint64_t(q.bin_stride), uint64_t(N), reinterpret_cast<uint64_t>(d->labels.p),
       uint64_t(objective_id_), uint64_t(n_groups_), reinterpret_cast<uint64_t>(margin_.p),
+      reinterpret_cast<uint64_t>(leaf_values_.p),
       reinterpret_cast<uint64_t>(grad_.p), reinterpret_cast<uint64_t>(hess_.p),
       reinterpret_cast<uint64_t>(gpair_.p), reinterpret_cast<uint64_t>(exps_.p),
       reinterpret_cast<uint64_t>(quant_scratch_.p),
@@ -1145,26 +1148,29 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
       for (int32_t k = 0; k < K; ++k) {
         sample_columns(*growers_[0], k);
         growers_[0]->grow(q, gpair_.p + int64_t(k) * N * 2, exps_.p + 2 * k,
-                          slots + int64_t(k) * blocks * 2, blocks, tp_, margin_.p + k, K,
-                          positions, k, stream_);
+                          slots + int64_t(k) * blocks * 2, blocks, tp_,
+                          leaf_values_.p + int64_t(k) * N, positions, k, stream_);
       }
+      launch_add_leaf_values(margin_.p, K, leaf_values_.p, N, stream_);
       return;
     }
-    // Each tree writes its own margin column; only the last writes the row
+    // Each tree stores its own leaf-value plane; only the last writes the row
     // positions (the round's positions are its last tree's).
     DP_HIP(hipEventRecord(fork_, stream_));
     for (int32_t l = 0; l < S; ++l) DP_HIP(hipStreamWaitEvent(tree_streams_[size_t(l)], fork_, 0));
     for (int32_t k = 0; k < K; ++k) {
       sample_columns(*growers_[size_t(k % S)], k);
       growers_[size_t(k % S)]->grow(q, gpair_.p + int64_t(k) * N * 2, exps_.p + 2 * k,
-                                    slots + int64_t(k) * blocks * 2, blocks, tp_, margin_.p + k,
-                                    K, k == K - 1 ? positions : nullptr, k / S,
+                                    slots + int64_t(k) * blocks * 2, blocks, tp_,
+                                    leaf_values_.p + int64_t(k) * N,
+                                    k == K - 1 ? positions : nullptr, k / S,
                                     tree_streams_[size_t(k % S)]);
     }
     for (int32_t l = 0; l < S; ++l) {
       DP_HIP(hipEventRecord(tree_done_[size_t(l)], tree_streams_[size_t(l)]));
       DP_HIP(hipStreamWaitEvent(stream_, tree_done_[size_t(l)], 0));
     }
+    launch_add_leaf_values(margin_.p, K, leaf_values_.p, N, stream_);
   });
   // This round's records go to the buffer the round in flight does not use.
   const int32_t buffer = pending_ ? 1 - pending_buffer_ : 0;

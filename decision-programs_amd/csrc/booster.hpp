@@ -112,11 +112,12 @@ class Grower {
   // Enqueues one tree.  gpair: [n_rows][2] fixed-point gradients of one output;
   // exps (device): its two quantiser exponents; root_slots (device): the
   // quantiser's root_blocks per-workgroup (g, h) sums of gpair, added up by the
-  // tree's first launch.  Adds the leaf values to margin[r * stride] and, when
-  // `positions` is set, writes each row's leaf id.
+  // tree's first launch.  Stores each row's leaf value into values[row] (every
+  // row once; the caller adds the plane to the margins) and, when `positions`
+  // is set, writes each row's leaf id.
   void grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
-            const int64_t* root_slots, int32_t root_blocks, const TrainParam& p, float* margin,
-            int64_t stride, int32_t* positions, int32_t slot, hipStream_t s);
+            const int64_t* root_slots, int32_t root_blocks, const TrainParam& p, float* values,
+            int32_t* positions, int32_t slot, hipStream_t s);
   // Copies the node records of slots [0, n_slots) to host buffer `buffer`
   // (0 or 1; one copy; eager trees only, level-synced trees were copied by
   // grow).
@@ -246,6 +247,9 @@ class Booster {
   DMatrix* train_ = nullptr;
   // training state
   PooledBuffer<float> margin_, grad_, hess_;
+  // The round's leaf-value planes, [n_groups][n_rows]: tree k stores each
+  // row's leaf value in plane k; the round ends by adding them to margin_.
+  PooledBuffer<float> leaf_values_;
   PooledBuffer<int32_t> gpair_, exps_;
   PooledBuffer<uint8_t> quant_scratch_;  // quantiser reduction slots
   PooledBuffer<int32_t> positions_;

@@ -413,7 +413,9 @@ void launch_colsample(const LevelNode* nodes, int32_t n_host, const int32_t* n_d
 
 // Margin (and optional leaf id) update of leaf chunks: margin[ridx[i] *
 // stride] += value, positions[ridx[i]] = leaf id; work count from n_dev when
-// set, else n_host (an upper bound for grid sizing either way).
+// set, else n_host (an upper bound for grid sizing either way).  With store
+// set, margin[ridx[i] * stride] = value instead: `margin` is then the tree's
+// leaf-value plane, which launch_add_leaf_values adds to the margins.
 struct LeafPass {
   const uint32_t* ridx = nullptr;
   const LeafWork* work = nullptr;
@@ -422,6 +424,7 @@ struct LeafPass {
   float* margin = nullptr;
   int64_t stride = 1;
   int32_t* positions = nullptr;
+  bool store = false;
 };
 
 // The partition scatter's arguments (scatter.hpp).
@@ -439,14 +442,13 @@ struct ScatterArgs {
   int64_t* node_left;        // the node's first item writes the node's left total; may be null
 };
 
-// The last split level's margin update, done by its count launch (every child
+// The last split level's leaf values, stored by its count launch (every child
 // is a leaf, so the rows need no new order): a row of an expanding node gets
-// margin[row * stride] += its child's leaf value, eta times the leaf weight of
-// the child's quantised sums (split record and nodes[node]); a row of a node
-// that does not expand gets the node's own leaf value.
+// values[row] = its child's leaf value, eta times the leaf weight of the
+// child's quantised sums (split record and nodes[node]); a row of a node that
+// does not expand gets the node's own leaf value.
 struct LastLevel {
-  float* margin;
-  int64_t stride;
+  float* values;  // the tree's leaf-value plane, one float per row
   const LevelNode* nodes;
   const int32_t* exps;  // quantiser exponents (gradient, hessian)
   double eta, lambda, alpha, mcw;
@@ -492,10 +494,16 @@ struct LeafList {
   const int32_t* n_dev = nullptr;
 };
 // margin[ridx[i] * stride] += value for the chunks of the list (ridx, work,
-// n_work, n_work_dev) and, in the same launch, of `second` when given.
+// n_work, n_work_dev) and, in the same launch, of `second` when given; with
+// store, margin[ridx[i] * stride] = value (a leaf-value plane).
 void launch_update_margin(const uint32_t* ridx, const LeafWork* work, int32_t n_work,
                           const int32_t* n_work_dev, float* margin, int64_t stride, hipStream_t s,
-                          const LeafList* second = nullptr);
+                          const LeafList* second = nullptr, bool store = false);
+// margin[row * n_groups + k] += values[k * n_rows + row] for every row and
+// output group k: a round's trees' leaf-value planes (each row of each plane
+// stored once by its tree's leaf passes) added to the margins in row order.
+void launch_add_leaf_values(float* margin, int32_t n_groups, const float* values, int64_t n_rows,
+                            hipStream_t s);
 void launch_leaf_positions(const uint32_t* ridx, const LeafWork* work, int32_t n_work,
                            const int32_t* n_work_dev, int32_t* positions, hipStream_t s);
 

@@ -12,7 +12,7 @@
 //     per tile writes its histogram directly, larger ones use partial slots),
 //     the reduce jobs that finish the built histograms and derive each
 //     sibling, and the partition work;
-//   * the margin-update work of this level's leaves.
+//   * the leaf-value work of this level's leaves.
 // Counts are scanned over the workgroup and every work item is then written
 // by its own thread, which finds its node by binary search over the offsets.
 // Nothing goes back to the host until the tree is complete, so a whole tree

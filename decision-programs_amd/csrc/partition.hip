@@ -41,7 +41,9 @@ __device__ __forceinline__ int split_bin_of(const uint8_t* __restrict__ bins, in
 // margin stores cannot alias it).  Row ids are loaded a batch ahead of their
 // margins, at indexes clamped into the chunk (i0 < end), so the loads need no
 // branch and overlap; a chunk's rows are distinct, so all margins of a batch
-// are read before any is written.
+// are read before any is written.  With lp.store (uniform) the value is
+// stored into the leaf-value plane and nothing is read: a row's scattered
+// access is then one write instead of a read and a write of its sector.
 __device__ __forceinline__ void apply_leaf(const LeafPass& lp, const LeafWork w) {
   constexpr int kBatch = 8;
   for (int64_t i0 = w.begin + threadIdx.x; i0 < w.end; i0 += int64_t(kBatch) * blockDim.x) {
@@ -53,11 +55,12 @@ __device__ __forceinline__ void apply_leaf(const LeafPass& lp, const LeafWork w)
     }
     float m[kBatch];
 #pragma unroll
-    for (int k = 0; k < kBatch; ++k) m[k] = lp.margin[int64_t(row[k]) * lp.stride];
+    for (int k = 0; k < kBatch; ++k)
+      m[k] = lp.store ? 0.0f : lp.margin[int64_t(row[k]) * lp.stride];
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
       if (i0 + int64_t(k) * blockDim.x >= w.end) break;
-      lp.margin[int64_t(row[k]) * lp.stride] = m[k] + w.value;
+      lp.margin[int64_t(row[k]) * lp.stride] = lp.store ? w.value : m[k] + w.value;
       if (lp.positions) lp.positions[row[k]] = w.pad;
     }
   }
@@ -73,9 +76,9 @@ __device__ __forceinline__ void apply_leaf(const LeafPass& lp, const LeafWork w)
 // groups of G steps whose row ids, then bins, are loaded together
 // (part_group: G = 4 keeps more loads in flight and pays on large levels;
 // smaller matrices take the steps of one item).
-// MARGIN (the last split level, LastLevel): each row's margin is loaded with
-// its bin and stored with its child's leaf value added once the side is known;
-// the rows of a node that does not expand get the node's own leaf value.
+// MARGIN (the last split level, LastLevel): each row's child leaf value is
+// stored into the leaf-value plane once the side is known; the rows of a node
+// that does not expand get the node's own leaf value.
 template <bool COLS, int G, bool MARGIN>
 __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
     const uint8_t* __restrict__ bins, int64_t n_rows, int tile_width, int missing_bin,
@@ -138,7 +141,7 @@ __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
   if (!s.expand) {
     if (threadIdx.x == 0) work_left[item] = int64_t(w.node) << 32;
     if constexpr (MARGIN)  // the node is a leaf: its rows get its own value
-      apply_leaf(LeafPass{ridx, nullptr, nullptr, 0, ll.margin, ll.stride, nullptr},
+      apply_leaf(LeafPass{ridx, nullptr, nullptr, 0, ll.values, 1, nullptr, true},
                  LeafWork{v_left, 0, w.begin, w.end});
     continue;
   }
@@ -149,15 +152,11 @@ __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
     if (w.begin + int64_t(g0) * kPartThreads >= w.end) break;  // uniform per workgroup
     int bin[G];
     uint32_t mrow[G];  // MARGIN: this group's rows (row[] is refilled below)
-    float mval[G];
 #pragma unroll
     for (int k = 0; k < G; ++k) {
       const int64_t i = w.begin + int64_t(g0 + k) * kPartThreads + threadIdx.x;
       bin[k] = i < w.end ? split_bin_of<COLS>(bins, n_rows, tile_width, row[k], s.feature) : -1;
-      if constexpr (MARGIN) {
-        mrow[k] = row[k];
-        mval[k] = i < w.end ? ll.margin[int64_t(row[k]) * ll.stride] : 0.0f;
-      }
+      if constexpr (MARGIN) mrow[k] = row[k];
     }
     if (g0 + G < kPartSteps) load_rows(g0 + G);
 #pragma unroll
@@ -168,7 +167,7 @@ __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
       if (lane == 0) item_masks[(g0 + k) * (kPartThreads / 64)] = m;
       count += popc64(m);
       if constexpr (MARGIN) {
-        if (b >= 0) ll.margin[int64_t(mrow[k]) * ll.stride] = mval[k] + (left ? v_left : v_right);
+        if (b >= 0) ll.values[mrow[k]] = left ? v_left : v_right;
       }
     }
   }
@@ -189,9 +188,10 @@ __global__ __launch_bounds__(kPartThreads) void part_scatter_kernel(ScatterArgs 
 }
 
 // Two leaf lists (the second may be empty): items [0, n0) are list 0's,
-// [n0, n0 + n1) list 1's, each list with its own row-id buffer.
+// [n0, n0 + n1) list 1's, each list with its own row-id buffer.  store: the
+// values are stored (a leaf-value plane) rather than added.
 __global__ void update_margin_kernel(LeafList l0, LeafList l1, float* __restrict__ margin,
-                                     int64_t stride) {
+                                     int64_t stride, int32_t store) {
   const int32_t n0 = l0.n_dev ? *l0.n_dev : l0.n_host;
   const int32_t n1 = l1.work ? (l1.n_dev ? *l1.n_dev : l1.n_host) : 0;
   constexpr int kBatch = 8;  // as apply_leaf: row ids, then margins, then stores
@@ -209,12 +209,41 @@ __global__ void update_margin_kernel(LeafList l0, LeafList l1, float* __restrict
       // A leaf's rows are distinct: all margins are read before any is written.
       float m[kBatch];
 #pragma unroll
-      for (int k = 0; k < kBatch; ++k) m[k] = margin[int64_t(row[k]) * stride];
+      for (int k = 0; k < kBatch; ++k) m[k] = store ? 0.0f : margin[int64_t(row[k]) * stride];
 #pragma unroll
       for (int k = 0; k < kBatch; ++k)
-        if (i0 + int64_t(k) * blockDim.x < w.end) margin[int64_t(row[k]) * stride] = m[k] + w.value;
+        if (i0 + int64_t(k) * blockDim.x < w.end)
+          margin[int64_t(row[k]) * stride] = store ? w.value : m[k] + w.value;
     }
   }
+}
+
+// margin[row * K + k] += values[k * n + row]: one thread per row (grid-stride),
+// the K planes read in row order, so every access is coalesced (K = 1: a
+// float4 of rows per thread).
+__global__ void add_leaf_values_kernel(float* __restrict__ margin, int32_t n_groups,
+                                       const float* __restrict__ values, int64_t n) {
+  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  const int64_t t0 = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (n_groups == 1) {
+    const int64_t n4 = n / 4;
+    auto* m4 = reinterpret_cast<float4*>(margin);
+    const auto* v4 = reinterpret_cast<const float4*>(values);
+    for (int64_t i = t0; i < n4; i += stride) {
+      float4 m = m4[i];
+      const float4 v = v4[i];
+      m.x = m.x + v.x;
+      m.y = m.y + v.y;
+      m.z = m.z + v.z;
+      m.w = m.w + v.w;
+      m4[i] = m;
+    }
+    for (int64_t r = n4 * 4 + t0; r < n; r += stride) margin[r] = margin[r] + values[r];
+    return;
+  }
+  for (int64_t r = t0; r < n; r += stride)
+    for (int32_t k = 0; k < n_groups; ++k)
+      margin[r * n_groups + k] = margin[r * n_groups + k] + values[int64_t(k) * n + r];
 }
 
 __global__ void leaf_positions_kernel(const uint32_t* __restrict__ ridx,
@@ -261,7 +290,7 @@ void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_lay
   const SplitSelect sel = select ? *select : SplitSelect{};
   const int group = part_group(layout.n_rows);
   const LastLevel ll = last ? *last : LastLevel{};
-  need(!last || (ll.margin && ll.nodes && ll.exps), "last-level margin update arguments");
+  need(!last || (ll.values && ll.nodes && ll.exps), "last-level leaf value arguments");
   auto pick = [&](auto k1, auto k2, auto k4) { return group == 4 ? k4 : (group == 2 ? k2 : k1); };
   auto count =
       cols ? (last ? pick(part_count_kernel<true, 1, true>, part_count_kernel<true, 2, true>,
@@ -291,13 +320,27 @@ void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_lay
 
 void launch_update_margin(const uint32_t* ridx, const LeafWork* work, int32_t n_work,
                           const int32_t* n_work_dev, float* margin, int64_t stride,
-                          hipStream_t s, const LeafList* second) {
+                          hipStream_t s, const LeafList* second, bool store) {
   const LeafList l1 = second ? *second : LeafList{};
   const int64_t items = int64_t(n_work) + (l1.work ? l1.n_host : 0);
   if (items <= 0) return;
   const LeafList l0{ridx, work, n_work, n_work_dev};
   hipLaunchKernelGGL(update_margin_kernel, dim3(items < 2048 ? items : 2048), dim3(256), 0, s, l0,
-                     l1, margin, stride);
+                     l1, margin, stride, store ? 1 : 0);
+  DP_HIP(hipGetLastError());
+}
+
+void launch_add_leaf_values(float* margin, int32_t n_groups, const float* values, int64_t n_rows,
+                            hipStream_t s) {
+  if (n_rows <= 0 || n_groups <= 0) return;
+  need(margin && values, "leaf-value addition needs the margins and the planes");
+  need(n_groups > 1 || (reinterpret_cast<uintptr_t>(margin) % 16 == 0 &&
+                        reinterpret_cast<uintptr_t>(values) % 16 == 0),
+       "single-output margins and leaf values must be 16-byte aligned");
+  const int64_t per = n_groups == 1 ? (n_rows + 3) / 4 : n_rows;
+  const int64_t blocks = (per + 255) / 256;
+  hipLaunchKernelGGL(add_leaf_values_kernel, dim3(unsigned(blocks < 2048 ? blocks : 2048)),
+                     dim3(256), 0, s, margin, n_groups, values, n_rows);
   DP_HIP(hipGetLastError());
 }
 
