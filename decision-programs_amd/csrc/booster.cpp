@@ -920,6 +920,7 @@ void Booster::update_one_iter(int iter, DMatrix* d) {
                                                            : "labels must be finite");
     labels_checked_ = true;
   }
+  caller_gradients_ = false;
   run_round(d, true);
 }
 
@@ -930,9 +931,18 @@ void Booster::train_one_iter(DMatrix* d, int iter, const float* grad, const floa
   need(iter == rounds_, "iteration index must equal the number of boosted rounds");
   configure(d);
   need(n == d->n_rows && k == n_groups_, "gradient shape differs from [rows, outputs]");
-  // Keep a copy so the parity hook can report the gradients of this round.
-  DP_HIP(hipMemcpyAsync(grad_.p, grad, grad_.bytes(), hipMemcpyDeviceToDevice, stream_));
-  DP_HIP(hipMemcpyAsync(hess_.p, hess, hess_.bytes(), hipMemcpyDeviceToDevice, stream_));
+  need(grad && hess, "null gradient buffer");
+  // The round's quantiser reads the caller's buffers (their pointers go to
+  // device memory ahead of the round, so its graph is the same every round);
+  // like every launch of the round they are read in stream order.
+  const uint64_t src[2] = {reinterpret_cast<uint64_t>(grad), reinterpret_cast<uint64_t>(hess)};
+  if (!gradient_src_.p || src[0] != gradient_src_host_[0] || src[1] != gradient_src_host_[1]) {
+    gradient_src_.reserve(2);
+    launch_store_u64x2(gradient_src_.p, src[0], src[1], stream_);
+    gradient_src_host_[0] = src[0];
+    gradient_src_host_[1] = src[1];
+  }
+  caller_gradients_ = true;
   run_round(d, false);
 }
 
@@ -1099,7 +1109,7 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
       reinterpret_cast<uint64_t>(q.rows.p), reinterpret_cast<uint64_t>(q.d_nbins.p),
       uint64_t(q.bin_stride), uint64_t(N), reinterpret_cast<uint64_t>(d->labels.p),
       uint64_t(objective_id_), uint64_t(n_groups_), reinterpret_cast<uint64_t>(margin_.p),
-      reinterpret_cast<uint64_t>(leaf_values_.p),
+      reinterpret_cast<uint64_t>(leaf_values_.p), reinterpret_cast<uint64_t>(gradient_src_.p),
       reinterpret_cast<uint64_t>(grad_.p), reinterpret_cast<uint64_t>(hess_.p),
       reinterpret_cast<uint64_t>(gpair_.p), reinterpret_cast<uint64_t>(exps_.p),
       reinterpret_cast<uint64_t>(quant_scratch_.p),
@@ -1130,7 +1140,7 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
     // The per-workgroup sums stay in the quantiser's slots: each tree's first
     // launch adds up its output's.
     launch_quantise(grad_.p, hess_.p, N, K, quant_scratch_.p, maxima, exps_.p, gpair_.p, nullptr,
-                    stream_, rows);
+                    stream_, rows, with_gradients ? nullptr : gradient_src_.p);
     const int32_t blocks = quantise_blocks(N);
     const int64_t* slots = quantise_sum_slots(quant_scratch_.p, N, K);
     auto sample_columns = [&](Grower& g, int32_t k) {
@@ -1230,6 +1240,8 @@ void Booster::margins(float* out, size_t n) const {
 void Booster::last_gradients(float* grad, float* hess, size_t n, int32_t* exps) const {
   flush();
   need(configured_, "booster has not been trained");
+  need(!caller_gradients_,
+       "the last round's gradients were supplied by the caller (XGBoosterTrainOneIter)");
   need(n == grad_.n, "gradient buffer size differs");
   if (grad) DP_HIP(hipMemcpy(grad, grad_.p, grad_.bytes(), hipMemcpyDeviceToHost));
   if (hess) DP_HIP(hipMemcpy(hess, hess_.p, hess_.bytes(), hipMemcpyDeviceToHost));

@@ -254,6 +254,11 @@ class Booster {
   PooledBuffer<uint8_t> quant_scratch_;  // quantiser reduction slots
   PooledBuffer<int32_t> positions_;
   PooledBuffer<int32_t> round_dev_;  // the round's index, read by the sampling kernels
+  // The caller's (grad, hess) pointers of an XGBoosterTrainOneIter round,
+  // stored before the round and read by its quantiser (no copy is made).
+  PooledBuffer<uint64_t> gradient_src_;
+  uint64_t gradient_src_host_[2] = {0, 0};  // what gradient_src_ holds (stored in stream order)
+  bool caller_gradients_ = false;  // the last round's gradients came from the caller
   mutable std::vector<int32_t> last_exps_;
   PooledPinnedBuffer exps_host_;  // two buffers, by round parity
   bool record_positions_ = false;
