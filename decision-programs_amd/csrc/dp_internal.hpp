@@ -569,18 +569,21 @@ void launch_plan_root(LevelNode* cur, int64_t* sums, int64_t* seg_begin, PartWor
 inline int64_t plan_hist_capacity(int64_t nodes, int32_t groups, int32_t items) {
   return items + int64_t(groups) + (nodes / 2 + 8) * int64_t(groups);
 }
-// Rows per partition / margin-update work item of the planner: about 2048
-// items over the matrix, a multiple of 256 in [256, kPartChunk].
+// Rows per partition / leaf-value work item of the planner: about 1024 items
+// over the matrix, a multiple of 256 in [256, kPartChunk] (measured against
+// about 2048, 1536 and 768 items: C2 at 1M rows 2,290 / 2,414 / 2,449 against
+// 2,460 trees/s here, C5 at 2M rows 615 / 630 / 627 against 634).
 inline int64_t row_chunk(int64_t n_rows) {
-  const int64_t c = (n_rows / 2048 + 255) / 256 * 256;
+  const int64_t c = (n_rows / 1024 + 255) / 256 * 256;
   return c < 256 ? 256 : (c > kPartChunk ? kPartChunk : c);
 }
 // 256-row steps whose row ids, then bins, a partition lane loads together
-// (count and scatter): four on matrices of 4M rows or more (more loads in
-// flight); below that the steps of one row_chunk item, at most two.
+// (count and scatter): four once items have 1024 rows or more (more loads in
+// flight; C2 2,460 -> 2,483 trees/s against two), else the steps of one
+// row_chunk item, at most two.
 inline int part_group(int64_t n_rows) {
-  if (n_rows >= (int64_t(1) << 22)) return 4;
-  return row_chunk(n_rows) >= 512 ? 2 : 1;
+  const int64_t c = row_chunk(n_rows);
+  return c >= 1024 ? 4 : (c >= 512 ? 2 : 1);
 }
 inline int64_t plan_part_capacity(int64_t nodes, int64_t n_rows, int64_t chunk) {
   return n_rows / chunk + 1 + nodes;
