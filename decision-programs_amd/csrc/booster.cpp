@@ -448,14 +448,31 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
                     partial_.p, s, nullptr, root_cfg_, skip_tiles_);
         launch_hist_reduce(partial_.p, root_job_.p, 1, nullptr, T, F, B, nullptr, h, false, s);
       } else if (sparse_) {
+        // On the last split level of a fused tree, the nodes built in one chunk
+        // are evaluated by the histogram pass itself, from LDS, and are never
+        // stored; the reduce-evaluate takes the rest.  (On earlier levels the
+        // pass's 512-thread workgroups accumulate the multi-chunk items more
+        // slowly than the evaluation saves: measured on C5.)
+        const bool in_pass = fused && !keep;
+        SparseEval ev;
+        ev.parent_base = hist_[nxt].p;
+        ev.n_bins = q.d_nbins.p;
+        ev.node_sums = sums_[cur].p;
+        ev.exps = exps;
+        ev.param = dtp;
+        ev.fmask = fmask;
+        ev.skip_bins = skip_features_;
+        ev.cand = eval_scratch_.p;
+        ev.store = keep;
         launch_hist_sparse(q.sparse, N, F, gpair, ridx_[cur].p, hist_work_[cur].p,
                            int32_t(plan_hist_items(nb, N, T, level_cfg_.items)),
-                           field(c, &PlanCounts::n_hist), B, h, partial_.p, s);
+                           field(c, &PlanCounts::n_hist), B, h, partial_.p, s,
+                           in_pass ? &ev : nullptr);
         if (fused)
           launch_reduce_evaluate_flat(partial_.p, reduce_jobs_[cur].p, int32_t(nb / 2 + 1),
                                       field(c, &PlanCounts::n_reduce), T, tf, F, B, hist_[nxt].p,
                                       h, q.d_nbins.p, sums_[cur].p, exps, dtp, fmask,
-                                      skip_features_, eval_scratch_.p, keep, s);
+                                      skip_features_, eval_scratch_.p, keep, s, in_pass);
         else
           launch_hist_reduce_flat(partial_.p, reduce_jobs_[cur].p, int32_t(nb / 2 + 1),
                                   field(c, &PlanCounts::n_reduce), T, tf, F, B, hist_[nxt].p, h,

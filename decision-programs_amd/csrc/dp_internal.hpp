@@ -133,14 +133,16 @@ constexpr int kMaxBins = 256;
 // One histogram work item: rows [begin, end) of node `slot` for one tile.
 // partial >= 0: the workgroup stores its tile histogram in partial slot
 // `partial` (summed later by the reduce pass); partial < 0: the item is the
-// node's only chunk and writes the node histogram's tile directly.
+// node's only chunk and writes the node histogram's tile directly.  parent:
+// the parent's histogram slot in the previous level (the node's sibling is
+// slot ^ 1), or -1 when the node has no sibling (the root).
 struct HistWork {
   int32_t slot;
   int32_t tile;
   int64_t begin;
   int64_t end;
   int32_t partial;
-  int32_t pad;
+  int32_t parent;
 };
 
 // One reduce job (all tiles of one built node): node histogram `slot` = sum
@@ -394,7 +396,8 @@ bool launch_evaluate(const int64_t* hist, int32_t n_nodes, const int32_t* n_node
 // launch_hist_reduce_flat and launch_evaluate(..., select = false) in one
 // launch -- the same node histograms (built and sibling) and the same
 // per-feature candidates in scratch.  exps: the quantiser exponents in device
-// memory.
+// memory.  skip_direct: jobs whose node was built by one direct item are left
+// alone (launch_hist_sparse's evaluation did them).
 void launch_reduce_evaluate_flat(const int64_t* partial, const HistReduce* jobs, int32_t n_jobs,
                                  const int32_t* n_jobs_dev, int32_t n_tiles, int32_t tile_features,
                                  int32_t n_features, int32_t bin_stride,
@@ -402,7 +405,7 @@ void launch_reduce_evaluate_flat(const int64_t* partial, const HistReduce* jobs,
                                  const int64_t* node_sums, const int32_t* exps,
                                  const dp_train_param& param, const uint32_t* fmask,
                                  const uint8_t* skip_bins, void* scratch, bool store,
-                                 hipStream_t s);
+                                 hipStream_t s, bool skip_direct = false);
 // Column sampling of one level (ColSample active): masks[node][ceil(F / 32)]
 // gets each node's feature sample (bit f set: feature f is a candidate), for
 // the node count *n_dev (n_host when null; n_host bounds the grid).  depth is
@@ -660,10 +663,29 @@ double build_sparse_bins(const uint8_t* bins, const dp_bin_layout& layout, int32
 // Histograms from the present-value layout: work items as for launch_hist,
 // with `tile` a sparse tile; partial slots of tile_features * bin_stride * 2
 // words in the node histogram's layout.  Finished by launch_hist_reduce_flat.
+// The evaluation a present-value pass does for the nodes it builds in one
+// chunk (HistWork::partial < 0; HistWork::parent names the sibling): the
+// node's and its sibling's words and per-feature candidates of
+// launch_reduce_evaluate_flat, computed from the LDS tile; that launch then
+// skips these jobs (skip_direct).
+// store false: nothing is written but the candidates (no later level reads
+// the histograms).  At most 64 bins.
+struct SparseEval {
+  const int64_t* parent_base = nullptr;  // previous level's node histograms
+  const int32_t* n_bins = nullptr;
+  const int64_t* node_sums = nullptr;
+  const int32_t* exps = nullptr;  // quantiser exponents, device memory
+  dp_train_param param{};
+  const uint32_t* fmask = nullptr;
+  const uint8_t* skip_bins = nullptr;
+  void* cand = nullptr;  // evaluate_scratch_bytes of per-feature candidates
+  bool store = true;
+};
 void launch_hist_sparse(const SparseBins& sp, int64_t n_rows, int32_t n_features,
                         const int32_t* gpair, const uint32_t* ridx, const HistWork* work,
                         int32_t n_work, const int32_t* n_work_dev, int32_t bin_stride,
-                        int64_t* hist, int64_t* partial, hipStream_t s);
+                        int64_t* hist, int64_t* partial, hipStream_t s,
+                        const SparseEval* eval = nullptr);
 void launch_hist_reduce_flat(const int64_t* partial, const HistReduce* jobs, int32_t n_jobs,
                              const int32_t* n_jobs_dev, int32_t n_tiles, int32_t tile_features,
                              int32_t n_features, int32_t bin_stride, const int64_t* parent_base,

@@ -329,7 +329,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
           const int64_t k = c - pair_off[j];
           const int64_t b = sm.begin + k * chunk;
           item = HistWork{2 * j + (right_small ? 1 : 0), 0, b,
-                          b + chunk < sm.end ? b + chunk : sm.end, -1, 0};
+                          b + chunk < sm.end ? b + chunk : sm.end, -1, l.parent_slot};
           if (pair_off[j + 1] - pair_off[j] >= 2) p = (pstart[j] + k) * T;
         }
         for (int32_t g = 0; g < G; ++g) {  // tile group g: tiles g * TPW ..
@@ -679,7 +679,7 @@ __device__ void plan_small_level(const PlanArgs& a) {
           const bool rs = s_slot[j] & 1;
           const int64_t sb = rs ? s_mid[j] : s_begin[j], se = rs ? s_end[j] : s_mid[j];
           const int64_t b = sb + k * chunk;
-          item = HistWork{s_slot[j], 0, b, b + chunk < se ? b + chunk : se, -1, 0};
+          item = HistWork{s_slot[j], 0, b, b + chunk < se ? b + chunk : se, -1, j};
           if (s_cs[j + 1] - s_cs[j] >= 2) p = (s_ps[j] + k) * T;
         }
         for (int32_t g = 0; g < G; ++g) {  // tile group g: tiles g * TPW ..

@@ -23,6 +23,7 @@
 //    slot, and hist_reduce_kernel sums the partial slots of each node and
 //    derives the sibling (parent - built) in the same pass.
 #include "dp_internal.hpp"
+#include "gain.hpp"
 
 #include <algorithm>
 #include <mutex>
@@ -264,6 +265,84 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8 
   }
 }
 
+// The evaluation a present-value pass does for its single-chunk nodes (EVAL).
+struct SparseEvalArgs {
+  const long long* parent_base;  // previous level's node histograms
+  const int32_t* n_bins;
+  const long long* node_sums;
+  const int32_t* exps;
+  Param p;
+  const uint32_t* fmask;
+  const uint8_t* skip_bins;
+  FeatCand* cand;
+  int32_t store;  // 0: the level's histograms have no readers (nothing stored)
+};
+
+// EVAL's epilogue (see hist_sparse_kernel): node w.slot's features f0 .. f0 +
+// nf from the LDS tile ([feature][bin][g, h] words), and its sibling's from
+// the parent's words minus them; every thread of the workgroup takes part.
+template <int THREADS>
+__device__ __forceinline__ void evaluate_tile(const SparseEvalArgs& ev, const HistWork& w,
+                                              int32_t f0, int32_t nf, int32_t n_features,
+                                              int32_t bin_stride, const unsigned long long* lds,
+                                              unsigned long long* __restrict__ hist) {
+  constexpr int BPL = 4;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int seg = lane >> 4, sub = lane & 15;
+  const double ug = ldexp(1.0, -ev.exps[0]), uh = ldexp(1.0, -ev.exps[1]);
+  const int64_t node_elems = int64_t(n_features) * bin_stride * 2;
+  const bool sib = w.parent >= 0;  // uniform per workgroup
+  // This lane's four bins of feature fl from the LDS tile (zero past the bins).
+  auto load = [&](int32_t fl, bool live, long long (&g)[BPL], long long (&h)[BPL]) {
+#pragma unroll
+    for (int k = 0; k < BPL; ++k) {
+      const int b = sub * BPL + k;
+      const bool ok = live && b < bin_stride;
+      const int e = ((live ? fl : 0) * bin_stride + (ok ? b : 0)) * 2;
+      g[k] = ok ? (long long)lds[e] : 0;
+      h[k] = ok ? (long long)lds[e + 1] : 0;
+    }
+  };
+  for (int32_t fb = 0; fb < nf; fb += (THREADS / 64) * 4) {
+    const int32_t fl = fb + wave * 4 + seg;
+    const bool live = fl < nf;
+    const int64_t at = (int64_t(f0 + (live ? fl : 0)) * bin_stride + sub * BPL) * 2;
+    // The parent's words are loaded first, so that their latency is hidden by
+    // the node's evaluation.
+    long long pg[BPL], ph[BPL];
+    if (sib) {
+      const long long* par = ev.parent_base + int64_t(w.parent) * node_elems + at;
+#pragma unroll
+      for (int k = 0; k < BPL; ++k) {
+        const bool ok = live && sub * BPL + k < bin_stride;
+        pg[k] = ok ? par[2 * k] : 0;
+        ph[k] = ok ? par[2 * k + 1] : 0;
+      }
+    }
+    long long g[BPL], h[BPL];
+    load(fl, live, g, h);
+    seg_evaluate(g, h, w.slot, f0 + fl, live, n_features, ev.n_bins, ev.node_sums, ug, uh, ev.p,
+                 ev.fmask, ev.skip_bins, ev.cand);
+    if (!sib) continue;
+    // The sibling: the parent's words minus the node's (read again from LDS,
+    // so that they are not held across the evaluation above).
+    load(fl, live, g, h);
+    long long* so = reinterpret_cast<long long*>(hist) + int64_t(w.slot ^ 1) * node_elems + at;
+#pragma unroll
+    for (int k = 0; k < BPL; ++k) {
+      const bool ok = live && sub * BPL + k < bin_stride;
+      g[k] = ok ? pg[k] - g[k] : 0;
+      h[k] = ok ? ph[k] - h[k] : 0;
+      if (ok && ev.store) {
+        so[2 * k] = g[k];
+        so[2 * k + 1] = h[k];
+      }
+    }
+    seg_evaluate(g, h, w.slot ^ 1, f0 + fl, live, n_features, ev.n_bins, ev.node_sums, ug, uh,
+                 ev.p, ev.fmask, ev.skip_bins, ev.cand);
+  }
+}
+
 // Histograms from the present-value layout (SparseBins): one work item = rows
 // [begin, end) of node `slot` for one sparse tile of tile_features features.
 // The tile's histogram lives in LDS as the node histogram's own layout,
@@ -274,15 +353,28 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8 
 // software-pipelined: while row i's entries are accumulated, the row id of
 // row i + 2 * 1024 and the entry range and (g, h) of row i + 1024 are in
 // flight.  Per-lane trip counts differ; no barrier sits inside the row loop.
+//
+// EVAL: an item that is its node's only chunk (partial < 0) also evaluates
+// the node from the LDS tile, and its sibling (parent >= 0; the sibling is
+// slot ^ 1) as the parent's tile minus it --
+// the words and per-feature candidates of reduce_evaluate_flat_kernel, which
+// then skips the node's job.  Sixteen wavefronts take 64 of the tile's
+// features per step, one per 16-lane row with four bins per lane
+// (seg_evaluate).  The node's words (and the sibling's) are stored only with
+// ev.store, so on the tree's last split level such a node never leaves LDS.
 constexpr int kSparseBatch = 4;
+// EVAL's workgroups: 512 threads, so that the evaluation's double arithmetic
+// has 128 registers without spilling while two workgroups share a CU.
+constexpr int kSparseEvalThreads = 512;
 
-template <bool GATHER>
-__global__ __launch_bounds__(kHistThreads) void hist_sparse_kernel(
+template <bool GATHER, bool EVAL, int THREADS>
+__global__ __launch_bounds__(THREADS) void hist_sparse_kernel(
     const uint32_t* __restrict__ ptr, const uint16_t* __restrict__ entries, int64_t n_rows,
     int32_t n_features, int32_t tile_features, const int2* __restrict__ gpair,
     const uint32_t* __restrict__ ridx, const HistWork* __restrict__ work, int32_t n_work_host,
     const int32_t* __restrict__ n_work_dev, int32_t bin_stride,
-    unsigned long long* __restrict__ hist, unsigned long long* __restrict__ partial) {
+    unsigned long long* __restrict__ hist, unsigned long long* __restrict__ partial,
+    SparseEvalArgs ev) {
   extern __shared__ unsigned long long lds_tile[];
   const int32_t n_work = n_work_dev ? *n_work_dev : n_work_host;
   const int64_t slot_words = int64_t(tile_features) * bin_stride * 2;
@@ -293,7 +385,7 @@ __global__ __launch_bounds__(kHistThreads) void hist_sparse_kernel(
     const int32_t f0 = w.tile * tile_features;
     const int32_t nf = f0 + tile_features < n_features ? tile_features : n_features - f0;
     const int32_t words = nf * bin_stride * 2;
-    for (int e = threadIdx.x; e < words; e += kHistThreads) lds_tile[e] = 0ull;
+    for (int e = threadIdx.x; e < words; e += THREADS) lds_tile[e] = 0ull;
     __syncthreads();
     const uint32_t* tp = ptr + int64_t(w.tile) * n_rows;
     auto row_of = [&](int64_t i) -> uint32_t {
@@ -309,9 +401,9 @@ __global__ __launch_bounds__(kHistThreads) void hist_sparse_kernel(
       e = tp[r + 1];
       q = gpair[r];
     }
-    uint32_t r1 = i + kHistThreads < w.end ? row_of(i + kHistThreads) : 0;
-    for (; i < w.end; i += kHistThreads) {
-      const int64_t i1 = i + kHistThreads, i2 = i + 2 * kHistThreads;
+    uint32_t r1 = i + THREADS < w.end ? row_of(i + THREADS) : 0;
+    for (; i < w.end; i += THREADS) {
+      const int64_t i1 = i + THREADS, i2 = i + 2 * THREADS;
       const uint32_t r2 = i2 < w.end ? row_of(i2) : 0;
       uint32_t b1 = 0, e1 = 0;
       int2 q1 = make_int2(0, 0);
@@ -341,10 +433,15 @@ __global__ __launch_bounds__(kHistThreads) void hist_sparse_kernel(
       r1 = r2;
     }
     __syncthreads();
+    const bool direct = w.partial < 0;  // uniform per workgroup
     unsigned long long* out =
-        w.partial >= 0 ? partial + int64_t(w.partial) * slot_words
-                       : hist + (int64_t(w.slot) * n_features + f0) * bin_stride * 2;
-    for (int k = threadIdx.x; k < words; k += kHistThreads) out[k] = lds_tile[k];
+        !direct ? partial + int64_t(w.partial) * slot_words
+                : hist + (int64_t(w.slot) * n_features + f0) * bin_stride * 2;
+    if (!(EVAL && direct && !ev.store))
+      for (int k = threadIdx.x; k < words; k += THREADS) out[k] = lds_tile[k];
+    if constexpr (EVAL) {
+      if (direct) evaluate_tile<THREADS>(ev, w, f0, nf, n_features, bin_stride, lds_tile, hist);
+    }
     __syncthreads();  // the next item clears the LDS this item just read
   }
 }
@@ -454,6 +551,49 @@ __global__ __launch_bounds__(256) void hist_reduce_kernel(
   }
 }
 
+// One reduce job with many partial slots (a root pass: every chunk of the
+// matrix): hist_reduce_kernel's sums with four times the loads in flight.
+// Each 1024-thread workgroup takes 256 words of one tile; thread group q
+// (256 threads) sums slots q, q + 4, ... of its word, and group 0 adds the
+// four sums (exact in int64, so the order does not matter).
+constexpr int kWideGroups = 4;
+__global__ __launch_bounds__(256 * kWideGroups) void hist_reduce_wide_kernel(
+    const long long* __restrict__ partial, const HistReduce* __restrict__ jobs, int32_t n_tiles,
+    int32_t n_features, int32_t bin_stride, const long long* __restrict__ parent_base,
+    long long* __restrict__ hist, int32_t accumulate) {
+  __shared__ long long part[kWideGroups - 1][256];
+  const HistReduce j = jobs[0];
+  const int q = threadIdx.x >> 8, t = threadIdx.x & 255;
+  const int n_words = bin_stride * 32;
+  const int e = blockIdx.x * 256 + t;
+  const int tile = blockIdx.y;
+  const int within = e & 31, bin = e >> 5;
+  const int f = tile * kTile + (within & 15);
+  const bool live = e < n_words && f < n_features;
+  const bool direct = j.nc == 1 && j.p0 < 0;  // uniform: the node's only chunk wrote it
+  long long sum = 0;
+  if (live && !direct && q < j.nc) {
+    const int32_t nq = (j.nc - q + kWideGroups - 1) / kWideGroups;  // slots q, q + 4, ...
+    sum = sum_slots(partial + (int64_t(j.p0 + q) * n_tiles + tile) * n_words + e,
+                    int64_t(kWideGroups) * n_tiles * n_words, nq);
+  }
+  if (q > 0) part[q - 1][t] = sum;
+  __syncthreads();
+  if (q > 0 || !live) return;  // no barriers below
+  const int64_t node_elems = int64_t(n_features) * bin_stride * 2;
+  const int64_t at = (int64_t(f) * bin_stride + bin) * 2 + (within >> 4);
+  long long* built = hist + int64_t(j.slot) * node_elems + at;
+  if (direct) {
+    sum = *built;
+  } else {
+#pragma unroll
+    for (int k = 0; k < kWideGroups - 1; ++k) sum += part[k][t];
+    if (accumulate) sum += *built;
+    *built = sum;
+  }
+  if (j.sibling >= 0) hist[int64_t(j.sibling) * node_elems + at] = parent_base[j.parent + at] - sum;
+}
+
 }  // namespace
 
 void launch_fill_i64(int64_t* p, int64_t n, int64_t value, hipStream_t s) {
@@ -517,7 +657,7 @@ int32_t make_hist_work(const dp_bin_layout& layout, const int64_t* begin, const 
       const int64_t b = ((c / 8) * G + g) * 8 + (c % 8);
       const int64_t t = g * tpw;
       work[size_t(b)] = {ch.slot, int32_t(t), ch.b, ch.e,
-                         ch.partial < 0 ? -1 : int32_t(ch.partial * T + t), 0};
+                         ch.partial < 0 ? -1 : int32_t(ch.partial * T + t), -1};
     }
   return n_partial * int32_t(T);
 }
@@ -616,6 +756,16 @@ void launch_hist_reduce(const int64_t* partial, const HistReduce* jobs, int32_t 
                         bool accumulate, hipStream_t s) {
   if (n_jobs <= 0) return;
   need(bin_stride >= 1 && bin_stride <= kMaxBins, "histogram bin stride out of range");
+  if (n_jobs == 1 && !n_jobs_dev) {  // one node (a root pass): the wide reduce
+    hipLaunchKernelGGL(hist_reduce_wide_kernel,
+                       dim3(unsigned(bin_stride * 32 + 255) / 256, unsigned(n_tiles)),
+                       dim3(256 * kWideGroups), 0, s, reinterpret_cast<const long long*>(partial),
+                       jobs, n_tiles, n_features, bin_stride,
+                       reinterpret_cast<const long long*>(parent_base),
+                       reinterpret_cast<long long*>(hist), accumulate ? 1 : 0);
+    DP_HIP(hipGetLastError());
+    return;
+  }
   const dim3 grid(unsigned(bin_stride * 32 + 255) / 256, unsigned(n_tiles),
                   unsigned(n_jobs < 64 ? n_jobs : 64));
   hipLaunchKernelGGL(hist_reduce_kernel, grid, dim3(256), 0, s,
@@ -629,27 +779,43 @@ void launch_hist_reduce(const int64_t* partial, const HistReduce* jobs, int32_t 
 void launch_hist_sparse(const SparseBins& sp, int64_t n_rows, int32_t n_features,
                         const int32_t* gpair, const uint32_t* ridx, const HistWork* work,
                         int32_t n_work, const int32_t* n_work_dev, int32_t bin_stride,
-                        int64_t* hist, int64_t* partial, hipStream_t s) {
+                        int64_t* hist, int64_t* partial, hipStream_t s, const SparseEval* eval) {
   if (n_work <= 0) return;
   need(sp.n_tiles > 0, "present-value layout not built");
   need(bin_stride >= 1 && bin_stride <= kMaxBins, "histogram bin stride out of range");
   const size_t lds = size_t(sp.tile_features) * size_t(bin_stride) * 16;
   need(lds <= size_t(kSparseLdsBytes), "sparse tile exceeds its LDS budget");
-  auto kernel = ridx ? hist_sparse_kernel<true> : hist_sparse_kernel<false>;
-  static bool attr_set[2] = {false, false};
-  if (!attr_set[ridx ? 1 : 0]) {
+  SparseEvalArgs ev{};
+  if (eval) {
+    need(bin_stride <= 64, "evaluation in the present-value pass needs at most 64 bins");
+    need(eval->parent_base && eval->n_bins && eval->node_sums && eval->exps && eval->cand,
+         "evaluation in the present-value pass needs its inputs");
+    const dp_train_param& q = eval->param;
+    ev = SparseEvalArgs{reinterpret_cast<const long long*>(eval->parent_base), eval->n_bins,
+                        reinterpret_cast<const long long*>(eval->node_sums), eval->exps,
+                        Param{double(q.lambda), double(q.alpha), double(q.min_child_weight),
+                              double(q.gamma)},
+                        eval->fmask, eval->skip_bins, static_cast<FeatCand*>(eval->cand),
+                        eval->store ? 1 : 0};
+  }
+  auto kernel = ridx ? (eval ? hist_sparse_kernel<true, true, kSparseEvalThreads>
+                             : hist_sparse_kernel<true, false, kHistThreads>)
+                     : (eval ? hist_sparse_kernel<false, true, kSparseEvalThreads>
+                             : hist_sparse_kernel<false, false, kHistThreads>);
+  static std::once_flag attr_once[4];
+  std::call_once(attr_once[(ridx ? 1 : 0) + (eval ? 2 : 0)], [kernel] {
     DP_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                hipFuncAttributeMaxDynamicSharedMemorySize, int(kSparseLdsBytes)));
-    attr_set[ridx ? 1 : 0] = true;
-  }
-  // One workgroup per CU (the tile's LDS), a multiple of 8 for the XCD order.
+  });
+  // Two workgroups per CU (64 KiB of LDS each), a multiple of 8 for the XCD order.
   int grid = n_work < 1024 ? n_work : 1024;
   grid = (grid + 7) / 8 * 8;
-  hipLaunchKernelGGL(kernel, dim3(grid), dim3(kHistThreads), lds, s, sp.ptr.p, sp.entries.p,
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(eval ? kSparseEvalThreads : kHistThreads), lds, s,
+                     sp.ptr.p, sp.entries.p,
                      n_rows, n_features, sp.tile_features, reinterpret_cast<const int2*>(gpair),
                      ridx, work, n_work, n_work_dev, bin_stride,
                      reinterpret_cast<unsigned long long*>(hist),
-                     reinterpret_cast<unsigned long long*>(partial));
+                     reinterpret_cast<unsigned long long*>(partial), ev);
   DP_HIP(hipGetLastError());
 }
 

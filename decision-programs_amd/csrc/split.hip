@@ -22,50 +22,14 @@
 #include "dp_internal.hpp"
 #include "sample.hpp"
 #include "select.hpp"
+#include "gain.hpp"
 
 #include <cmath>
 
 namespace dp {
 namespace {
 
-struct Param {
-  double lambda, alpha, mcw, gamma;
-};
-
-__device__ __forceinline__ double threshold_l1(double g, double alpha) {
-  if (g > alpha) return g - alpha;
-  if (g < -alpha) return g + alpha;
-  return 0.0;
-}
-
-__device__ __forceinline__ double calc_gain(const Param& p, double g, double h) {
-  if (h < p.mcw || h <= 0.0) return 0.0;
-  const double t = threshold_l1(g, p.alpha);
-  return (t * t) / (h + p.lambda);
-}
-
-__device__ __forceinline__ double split_loss(const Param& p, long long qgl, long long qhl,
-                                             long long qgr, long long qhr, double ug, double uh,
-                                             double parent_gain) {
-  if (qhl <= 0 || qhr <= 0) return -INFINITY;
-  const double gl = double(qgl) * ug, hl = double(qhl) * uh;
-  const double gr = double(qgr) * ug, hr = double(qhr) * uh;
-  if (hl < p.mcw || hr < p.mcw) return -INFINITY;
-  return (calc_gain(p, gl, hl) + calc_gain(p, gr, hr)) - parent_gain;
-}
-
 constexpr int kFeatWaves = 4;  // features per workgroup in evaluate_features_kernel
-
-// Column sampling: fmask holds one bit per feature for every node of the
-// level ([node][ceil(F / 32)] words); null when every feature is a candidate.
-__device__ __forceinline__ bool feature_allowed(const uint32_t* __restrict__ fmask, int32_t node,
-                                                int32_t f, int32_t n_features) {
-  if (!fmask) return true;
-  const int64_t words = (n_features + 31) / 32;
-  return (fmask[int64_t(node) * words + (f >> 5)] >> (f & 31)) & 1u;
-}
-
-__device__ __forceinline__ double dpp_f64_bits(long long bits) { return __longlong_as_double(bits); }
 
 // The largest value of the wavefront, in lane 63 (the same steps as the scan).
 __device__ __forceinline__ double wave_max_to_last(double v) {
@@ -218,113 +182,6 @@ __global__ __launch_bounds__(64 * kFeatWaves) void evaluate_features_kernel(
   }
 }
 
-constexpr int kSegFeatures = 16;  // features per workgroup (four per wavefront)
-
-__device__ __forceinline__ long long row_shuffle64(long long v, int src) {
-  const int lo = __shfl(int(v), src, 64);
-  const int hi = __shfl(int(v >> 32), src, 64);
-  return (long long)((uint64_t(uint32_t(hi)) << 32) | uint32_t(lo));
-}
-
-// The evaluation of four features per wavefront, one per 16-lane row, four bins
-// per lane (bins 4 * (lane % 16) + j in dg, dh): the row's prefix scan and
-// argmax take the row_shr steps of the full-wave ones; the row total and the
-// winner's fields come by lane permutes.  Same per-bin arithmetic and tie rule
-// as feature_best, with a quarter of the wavefronts and of their fixed costs.
-// The row's first lane writes feature f's best candidate of `node` (live: the
-// row's feature exists; every lane takes part in the row steps).
-__device__ __forceinline__ void seg_evaluate(const long long (&dg)[4], const long long (&dh)[4],
-                                             int32_t node, int32_t f, bool live,
-                                             int32_t n_features, const int32_t* __restrict__ n_bins,
-                                             const long long* __restrict__ node_sums, double ug,
-                                             double uh, const Param& p,
-                                             const uint32_t* __restrict__ fmask,
-                                             const uint8_t* __restrict__ skip_bins,
-                                             FeatCand* __restrict__ cand) {
-  constexpr int BPL = 4;
-  const int lane = threadIdx.x & 63;
-  const int seg = lane >> 4, sub = lane & 15;
-  const int row_last = lane | 15;
-  const int nb = live && feature_allowed(fmask, node, f, n_features) ? n_bins[f] : 0;
-  const long long gp = node_sums[2 * node], hp = node_sums[2 * node + 1];
-  const double parent_gain = calc_gain(p, double(gp) * ug, double(hp) * uh);
-  long long sg[BPL], sh[BPL];
-  long long rg = 0, rh = 0;
-#pragma unroll
-  for (int j = 0; j < BPL; ++j) {
-    rg += dg[j];
-    rh += dh[j];
-    sg[j] = rg;
-    sh[j] = rh;
-  }
-  // inclusive scan of the lane totals within the 16-lane row
-  long long ig = rg, ih = rh;
-  ig += dpp64<0x111>(ig, 0);
-  ih += dpp64<0x111>(ih, 0);
-  ig += dpp64<0x112>(ig, 0);
-  ih += dpp64<0x112>(ih, 0);
-  ig += dpp64<0x114>(ig, 0);
-  ih += dpp64<0x114>(ih, 0);
-  ig += dpp64<0x118>(ig, 0);
-  ih += dpp64<0x118>(ih, 0);
-  const long long total_g = row_shuffle64(ig, row_last), total_h = row_shuffle64(ih, row_last);
-  const long long og = ig - rg, oh = ih - rh;
-  // as feature_best: a skipped bin's rows return at the prefixes from that bin
-  const int skip = live && skip_bins ? int(skip_bins[f]) : -1;
-  long long mg = gp - total_g, mh = hp - total_h, kg = 0, kh = 0;
-  if (skip >= 0) {
-    kg = mg;
-    kh = mh;
-    mg = mh = 0;
-  }
-
-  Cand c;
-  c.loss = -INFINITY;
-  c.gl = c.hl = 0;
-  c.feature = f;
-  c.bin = -1;
-  c.dl = 0;
-#pragma unroll
-  for (int j = 0; j < BPL; ++j) {
-    const int b = sub * BPL + j;
-    if (b < nb) {
-      const long long lg = og + sg[j] + (b >= skip && skip >= 0 ? kg : 0);
-      const long long lh = oh + sh[j] + (b >= skip && skip >= 0 ? kh : 0);
-      const double right_missing = split_loss(p, lg, lh, gp - lg, hp - lh, ug, uh, parent_gain);
-      const double left_missing =
-          (mg == 0 && mh == 0)
-              ? right_missing
-              : split_loss(p, lg + mg, lh + mh, gp - lg - mg, hp - lh - mh, ug, uh, parent_gain);
-      const int dl = left_missing > right_missing;
-      const double loss = dl ? left_missing : right_missing;
-      if (loss > c.loss) {
-        c.loss = loss;
-        c.bin = b;
-        c.dl = dl;
-        c.gl = dl ? lg + mg : lg;
-        c.hl = dl ? lh + mh : lh;
-      }
-    }
-  }
-  // Row argmax: the largest loss, then the lowest lane holding it (lanes hold
-  // increasing bins and each kept its lowest bin on ties).
-  long long bb = __double_as_longlong(c.loss);
-  auto step = [&](long long o) {
-    if (dpp_f64_bits(o) > dpp_f64_bits(bb)) bb = o;
-  };
-  step(dpp64<0x111>(bb, bb));
-  step(dpp64<0x112>(bb, bb));
-  step(dpp64<0x114>(bb, bb));
-  step(dpp64<0x118>(bb, bb));
-  const double best = dpp_f64_bits(row_shuffle64(bb, row_last));
-  const unsigned long long hit = __ballot(c.loss == best);
-  const int winner = seg * 16 + __builtin_ctzll((hit >> (seg * 16)) & 0xffffull);
-  const long long w_gl = row_shuffle64(c.gl, winner), w_hl = row_shuffle64(c.hl, winner);
-  const int w_bin = __shfl(c.bin, winner, 64), w_dl = __shfl(c.dl, winner, 64);
-  if (live && sub == 0)
-    cand[int64_t(node) * n_features + f] = FeatCand{best, w_gl, w_hl, w_bin, w_dl};
-}
-
 // Up to 64 bins: four features per wavefront (seg_evaluate).  Workgroups loop
 // over (node, group of 16 features) items.
 __global__ __launch_bounds__(256) void evaluate_features_seg_kernel(
@@ -371,7 +228,9 @@ __global__ __launch_bounds__(256) void evaluate_features_seg_kernel(
 // level's histograms: the words and candidates are those of
 // hist_reduce_flat_kernel followed by evaluate_features_seg_kernel.  With
 // store == 0 (the tree's last split level, whose histograms no later level
-// reads) the built and sibling words are evaluated but not written.
+// reads) the built and sibling words are evaluated but not written.  With
+// skip_direct, jobs whose node was built by its only chunk are left alone:
+// the present-value histogram pass evaluated them from LDS.
 __global__ __launch_bounds__(256) void reduce_evaluate_flat_kernel(
     const long long* __restrict__ partial, const HistReduce* __restrict__ jobs,
     int32_t n_jobs_host, const int32_t* __restrict__ n_jobs_dev, int32_t n_tiles,
@@ -379,7 +238,8 @@ __global__ __launch_bounds__(256) void reduce_evaluate_flat_kernel(
     const long long* __restrict__ parent_base, long long* __restrict__ hist,
     const int32_t* __restrict__ n_bins, const long long* __restrict__ node_sums,
     const int32_t* __restrict__ exps, Param p, const uint32_t* __restrict__ fmask,
-    const uint8_t* __restrict__ skip_bins, FeatCand* __restrict__ cand, int32_t store) {
+    const uint8_t* __restrict__ skip_bins, FeatCand* __restrict__ cand, int32_t store,
+    int32_t skip_direct) {
   constexpr int BPL = 4;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int seg = lane >> 4, sub = lane & 15;
@@ -398,6 +258,7 @@ __global__ __launch_bounds__(256) void reduce_evaluate_flat_kernel(
   const double ug = ldexp(1.0, -exps[0]), uh = ldexp(1.0, -exps[1]);
   for (int32_t jb = blockIdx.y; jb < n_jobs; jb += gridDim.y) {
     const HistReduce j = jobs[jb];
+    if (skip_direct && j.nc == 1 && j.p0 < 0) continue;  // uniform per workgroup
     long long bg[BPL] = {0, 0, 0, 0}, bh[BPL] = {0, 0, 0, 0};
     long long* built = hist + int64_t(j.slot) * node_elems + feat_at;
     if (j.nc == 1 && j.p0 < 0) {  // written directly by the node's only chunk
@@ -710,7 +571,7 @@ void launch_reduce_evaluate_flat(const int64_t* partial, const HistReduce* jobs,
                                  const int64_t* node_sums, const int32_t* exps,
                                  const dp_train_param& param, const uint32_t* fmask,
                                  const uint8_t* skip_bins, void* scratch, bool store,
-                                 hipStream_t s) {
+                                 hipStream_t s, bool skip_direct) {
   if (n_jobs <= 0) return;
   need(bin_stride >= 1 && bin_stride <= 64, "the present-value reduce-evaluate takes <= 64 bins");
   need(tile_features >= kSegFeatures && tile_features % kSegFeatures == 0,
@@ -727,7 +588,8 @@ void launch_reduce_evaluate_flat(const int64_t* partial, const HistReduce* jobs,
                      reinterpret_cast<const long long*>(parent_base),
                      reinterpret_cast<long long*>(hist), n_bins,
                      reinterpret_cast<const long long*>(node_sums), exps, p, fmask, skip_bins,
-                     static_cast<FeatCand*>(scratch), store ? 1 : 0);
+                     static_cast<FeatCand*>(scratch), store ? 1 : 0,
+                     skip_direct ? 1 : 0);
   DP_HIP(hipGetLastError());
 }
 
