@@ -434,6 +434,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
       // The last split level's histograms have no readers: a fused launch
       // evaluates them without storing them.
       const bool keep = d + 1 < D;
+      bool dense_fused = false;  // set below for dense levels below the root
       if (d == 0 && sparse_) {
         launch_hist_sparse(q.sparse, N, F, gpair, nullptr, root_work_.p, root_items_, nullptr, B,
                            h, partial_.p, s);
@@ -479,19 +480,34 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
                                   s);
       } else {
         const int32_t G = (T + level_cfg_.tiles - 1) / level_cfg_.tiles;
+        // Levels below the root of wide matrices: feature-major partial slots,
+        // and the reduce and the evaluation in one launch (four features per
+        // workgroup, so at least 64 workgroups per node).  Measured: C4 (784
+        // features) 3,303 -> 3,815 trees/s; on C3 (128) and C2 (28) slower
+        // (394 against 437, 2,256 against 2,471): their nodes' many partial
+        // slots are summed by a few wavefronts per feature, and the
+        // feature-major flush scatters each item's stores over 16 rows.
+        dense_fused = F >= kDenseFuseFeatures && B <= 256 && exps;
         launch_hist(q.bins.p, L, gpair, ridx_[cur].p, hist_work_[cur].p,
                     int32_t(plan_hist_items(nb, N, G, level_cfg_.items)),
                     field(c, &PlanCounts::n_hist), B, h, partial_.p, s, q.rows.p, level_cfg_,
-                    skip_tiles_);
-        launch_hist_reduce(partial_.p, reduce_jobs_[cur].p, int32_t(nb / 2 + 1),
-                           field(c, &PlanCounts::n_reduce), T, F, B, hist_[nxt].p, h, false, s);
+                    skip_tiles_, dense_fused);
+        if (dense_fused)
+          launch_reduce_evaluate_dense(partial_.p, reduce_jobs_[cur].p, int32_t(nb / 2 + 1),
+                                       field(c, &PlanCounts::n_reduce), T, F, B, hist_[nxt].p, h,
+                                       q.d_nbins.p, sums_[cur].p, exps, dtp, fmask,
+                                       skip_features_, eval_scratch_.p, keep, s);
+        else
+          launch_hist_reduce(partial_.p, reduce_jobs_[cur].p, int32_t(nb / 2 + 1),
+                             field(c, &PlanCounts::n_reduce), T, F, B, hist_[nxt].p, h, false, s);
       }
       // Without records from the evaluation, the count launch selects them.
       const bool records =
-          fused ? false
-                : launch_evaluate(h, int32_t(nb), field(c, &PlanCounts::n_level), F, B,
-                                  q.d_nbins.p, sums_[cur].p, exps, 0, 0, dtp, eval_scratch_.p,
-                                  splits_.p, s, false, fmask, skip_features_);
+          fused || dense_fused
+              ? false
+              : launch_evaluate(h, int32_t(nb), field(c, &PlanCounts::n_level), F, B,
+                                q.d_nbins.p, sums_[cur].p, exps, 0, 0, dtp, eval_scratch_.p,
+                                splits_.p, s, false, fmask, skip_features_);
       SplitSelect sel;
       sel.cand = reinterpret_cast<const FeatCand*>(eval_scratch_.p);
       sel.n_features = F;

@@ -292,12 +292,16 @@ struct HistConfig {
 // skip (matrices without missing values): per tile, the 16 features' skip
 // bins ([n_tiles][16] bytes); rows in a feature's skip bin add nothing, so that
 // bin's sums stay zero (the split evaluation restores them from the node's
-// totals: launch_evaluate's skip argument).
+// totals: launch_evaluate's skip argument).  fmaj: partial slots are stored
+// feature-major, [16 features][bin_stride][g, h] (the node histogram's layout
+// restricted to the tile), for launch_reduce_evaluate_dense; otherwise as the
+// LDS image [bin][g of 16 features, h of 16 features] (launch_hist_reduce).
 void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t* gpair,
                  const uint32_t* ridx, const HistWork* work, int32_t n_work,
                  const int32_t* n_work_dev, int32_t bin_stride, int64_t* hist,
                  int64_t* partial, hipStream_t s, const uint8_t* row_major = nullptr,
-                 const HistConfig& cfg = HistConfig{}, const uint8_t* skip = nullptr);
+                 const HistConfig& cfg = HistConfig{}, const uint8_t* skip = nullptr,
+                 bool fmaj = false);
 // counts[f][b] = rows whose bin of feature f is b ([n_features][256] uint32),
 // from the column copy cols[f][row].
 void launch_bin_counts(const uint8_t* cols, int64_t n_rows, int32_t n_features,
@@ -406,6 +410,20 @@ void launch_reduce_evaluate_flat(const int64_t* partial, const HistReduce* jobs,
                                  const dp_train_param& param, const uint32_t* fmask,
                                  const uint8_t* skip_bins, void* scratch, bool store,
                                  hipStream_t s, bool skip_direct = false);
+// Feature count from which the booster's dense levels below the root use
+// feature-major partial slots and launch_reduce_evaluate_dense.
+constexpr int32_t kDenseFuseFeatures = 256;
+// Dense levels whose partial slots are feature-major (launch_hist's fmaj):
+// launch_hist_reduce and launch_evaluate(..., select = false) in one launch --
+// the same node histograms (built and sibling; none stored when !store) and the
+// same per-feature candidates in scratch.  At most 256 bins.
+void launch_reduce_evaluate_dense(const int64_t* partial, const HistReduce* jobs, int32_t n_jobs,
+                                  const int32_t* n_jobs_dev, int32_t n_tiles, int32_t n_features,
+                                  int32_t bin_stride, const int64_t* parent_base, int64_t* hist,
+                                  const int32_t* n_bins, const int64_t* node_sums,
+                                  const int32_t* exps, const dp_train_param& param,
+                                  const uint32_t* fmask, const uint8_t* skip_bins, void* scratch,
+                                  bool store, hipStream_t s);
 // Column sampling of one level (ColSample active): masks[node][ceil(F / 32)]
 // gets each node's feature sample (bit f set: feature f is a candidate), for
 // the node count *n_dev (n_host when null; n_host bounds the grid).  depth is

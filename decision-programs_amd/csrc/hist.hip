@@ -129,7 +129,7 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8 
     const HistWork* __restrict__ work, int32_t n_work_host,
     const int32_t* __restrict__ n_work_dev, int32_t bin_stride,
     unsigned long long* __restrict__ hist, unsigned long long* __restrict__ partial,
-    int64_t tile_step, int64_t row_step) {
+    int64_t tile_step, int64_t row_step, int32_t fmaj) {
   extern __shared__ unsigned long long lds[];  // TPW * kLdsWords
   constexpr int64_t kStep = int64_t(kHistThreads) * U;
   // The first item is loaded alongside the device count (the host bound keeps
@@ -248,7 +248,24 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8 
   const int n_words = bin_stride * 32;  // bins < bin_stride, 32 words each
   for (int j = 0; j < nt; ++j) {
     const unsigned long long* src = lds + j * kLdsWords;
-    if (w.partial >= 0) {  // tile j's partial slot is the item's slot + j
+    if (w.partial >= 0 && fmaj) {  // feature-major partial slot: [16][bin_stride][g, h]
+      // Thread k takes feature k % 16 and four bins: eight LDS words (lanes of
+      // one feature in four bin groups share a bank pair: 4-way at most), one
+      // 64-byte run of the slot.
+      unsigned long long* out = partial + int64_t(w.partial + j) * n_words;
+      const int chunks = 16 * ((bin_stride + 3) >> 2);
+      for (int k = threadIdx.x; k < chunks; k += kHistThreads) {
+        const int fl = k & 15, b0 = (k >> 4) * 4;
+        unsigned long long* o = out + (int64_t(fl) * bin_stride + b0) * 2;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (b0 + i < bin_stride) {
+            o[2 * i] = src[(b0 + i) * 32 + fl];
+            o[2 * i + 1] = src[(b0 + i) * 32 + 16 + fl];
+          }
+        }
+      }
+    } else if (w.partial >= 0) {  // tile j's partial slot is the item's slot + j (LDS image)
       unsigned long long* out = partial + int64_t(w.partial + j) * n_words;
       for (int e = threadIdx.x; e < n_words; e += kHistThreads) out[e] = src[e];
     } else {
@@ -689,7 +706,7 @@ void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t
                  const uint32_t* ridx, const HistWork* work, int32_t n_work,
                  const int32_t* n_work_dev, int32_t bin_stride, int64_t* hist,
                  int64_t* partial, hipStream_t s, const uint8_t* row_major,
-                 const HistConfig& cfg, const uint8_t* skip) {
+                 const HistConfig& cfg, const uint8_t* skip, bool fmaj) {
   if (n_work <= 0) return;
   need(bin_stride >= 1 && bin_stride <= kMaxBins, "histogram bin stride out of range");
   need(layout.tile_width == kTile, "histogram kernel needs 16-feature tiles");
@@ -730,7 +747,7 @@ void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t
   }
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(kHistThreads), lds, s, src, skip, layout.n_rows,
                      layout.n_features, layout.n_tiles, gp, ridx, work, n_work, n_work_dev,
-                     bin_stride, out, part, tile_step, row_step);
+                     bin_stride, out, part, tile_step, row_step, fmaj ? 1 : 0);
   DP_HIP(hipGetLastError());
 }
 

@@ -314,6 +314,127 @@ __global__ __launch_bounds__(256) void reduce_evaluate_flat_kernel(
   }
 }
 
+// Reduce and evaluate in one launch for dense levels whose partial slots are
+// feature-major ([16 features][bin_stride][g, h] per tile: hist_kernel's fmaj
+// flush, so a feature's words in a slot are contiguous).  One wavefront per
+// feature, four per 256-thread workgroup, lane l holding bins 4l .. 4l + 3 as
+// evaluate_features_kernel<4> does: the lane sums the job's partial slots of
+// its 64 contiguous bytes (or reads what the node's only chunk wrote), writes
+// the built and sibling words (with store), and evaluates both nodes' feature
+// from its registers -- the words and candidates of hist_reduce_kernel
+// followed by evaluate_features_kernel<4>, with one launch and one pass over
+// the level's histograms fewer.  Bins past bin_stride read the feature's last
+// bin and are masked (branch-free loads).  No barriers.
+constexpr int kDenseEvalWaves = 4;
+__global__ __launch_bounds__(64 * kDenseEvalWaves) void reduce_evaluate_dense_kernel(
+    const long long* __restrict__ partial, const HistReduce* __restrict__ jobs,
+    int32_t n_jobs_host, const int32_t* __restrict__ n_jobs_dev, int32_t n_tiles,
+    int32_t n_features, int32_t bin_stride, const long long* __restrict__ parent_base,
+    long long* __restrict__ hist, const int32_t* __restrict__ n_bins,
+    const long long* __restrict__ node_sums, const int32_t* __restrict__ exps, Param p,
+    const uint32_t* __restrict__ fmask, const uint8_t* __restrict__ skip_bins,
+    FeatCand* __restrict__ cand, int32_t store) {
+  constexpr int BPL = 4;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int32_t f = int32_t(blockIdx.x) * kDenseEvalWaves + wave;
+  if (f >= n_features) return;  // wave-uniform; no barriers in this kernel
+  const HistReduce j_first = int32_t(blockIdx.y) < n_jobs_host ? jobs[blockIdx.y] : HistReduce{};
+  const int32_t n_jobs = n_jobs_dev ? *n_jobs_dev : n_jobs_host;
+  const int32_t tile = f >> 4, fl = f & 15;
+  const int64_t slot_words = int64_t(bin_stride) * 32;  // a tile's partial slot
+  const int64_t node_elems = int64_t(n_features) * bin_stride * 2;
+  bool ok[BPL];
+  int64_t at[BPL], pat[BPL];  // word of bin (g; h is + 1): node histogram, partial slot
+#pragma unroll
+  for (int k = 0; k < BPL; ++k) {
+    const int b = lane * BPL + k;
+    ok[k] = b < bin_stride;
+    const int bc = ok[k] ? b : bin_stride - 1;
+    at[k] = (int64_t(f) * bin_stride + bc) * 2;
+    pat[k] = (int64_t(fl) * bin_stride + bc) * 2;
+  }
+  const int nbf = n_bins[f];
+  const int skip = skip_bins ? int(skip_bins[f]) : -1;
+  const double ug = ldexp(1.0, -exps[0]), uh = ldexp(1.0, -exps[1]);
+  auto evaluate = [&](const FeatBins<BPL>& d, int32_t node) {
+    const long long gp = node_sums[2 * node], hp = node_sums[2 * node + 1];
+    const double parent_gain = calc_gain(p, double(gp) * ug, double(hp) * uh);
+    const int nb = feature_allowed(fmask, node, f, n_features) ? nbf : 0;
+    const Cand c = feature_best<BPL>(d, f, nb, skip, gp, hp, parent_gain, ug, uh, p);
+    if (lane == 0) cand[int64_t(node) * n_features + f] = FeatCand{c.loss, c.gl, c.hl, c.bin, c.dl};
+  };
+  for (int32_t jb = blockIdx.y; jb < n_jobs; jb += gridDim.y) {
+    const HistReduce j = jb == int32_t(blockIdx.y) ? j_first : jobs[jb];
+    const bool direct = j.nc == 1 && j.p0 < 0;  // uniform: the node's only chunk wrote it
+    FeatBins<BPL> d;
+    long long pg[BPL] = {}, ph[BPL] = {};
+    if (j.sibling >= 0)  // uniform; issued first, used last
+#pragma unroll
+      for (int k = 0; k < BPL; ++k) {
+        pg[k] = parent_base[j.parent + at[k]];
+        ph[k] = parent_base[j.parent + at[k] + 1];
+      }
+    long long* built = hist + int64_t(j.slot) * node_elems;
+    if (direct) {
+#pragma unroll
+      for (int k = 0; k < BPL; ++k) {
+        const long long g = built[at[k]], h = built[at[k] + 1];
+        d.g[k] = ok[k] ? g : 0;
+        d.h[k] = ok[k] ? h : 0;
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < BPL; ++k) d.g[k] = d.h[k] = 0;
+      const long long* src = partial + (int64_t(j.p0) * n_tiles + tile) * slot_words;
+      const int64_t step = int64_t(n_tiles) * slot_words;
+      int32_t c = 0;
+      for (; c + 2 <= j.nc; c += 2) {  // two slots' sixteen words in flight
+        long long v[2][2 * BPL];
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int k = 0; k < BPL; ++k) {
+            v[u][2 * k] = src[(c + u) * step + pat[k]];
+            v[u][2 * k + 1] = src[(c + u) * step + pat[k] + 1];
+          }
+#pragma unroll
+        for (int k = 0; k < BPL; ++k) {
+          d.g[k] += v[0][2 * k] + v[1][2 * k];
+          d.h[k] += v[0][2 * k + 1] + v[1][2 * k + 1];
+        }
+      }
+      if (c < j.nc)
+#pragma unroll
+        for (int k = 0; k < BPL; ++k) {
+          d.g[k] += src[c * step + pat[k]];
+          d.h[k] += src[c * step + pat[k] + 1];
+        }
+#pragma unroll
+      for (int k = 0; k < BPL; ++k) {
+        if (!ok[k]) d.g[k] = d.h[k] = 0;
+        if (ok[k] && store) {
+          built[at[k]] = d.g[k];
+          built[at[k] + 1] = d.h[k];
+        }
+      }
+    }
+    evaluate(d, j.slot);
+    if (j.sibling >= 0) {  // uniform
+      long long* sib = hist + int64_t(j.sibling) * node_elems;
+#pragma unroll
+      for (int k = 0; k < BPL; ++k) {
+        d.g[k] = ok[k] ? pg[k] - d.g[k] : 0;
+        d.h[k] = ok[k] ? ph[k] - d.h[k] : 0;
+        if (ok[k] && store) {
+          sib[at[k]] = d.g[k];
+          sib[at[k] + 1] = d.h[k];
+        }
+      }
+      evaluate(d, j.sibling);
+    }
+  }
+}
+
 constexpr int kNodeWaves = 16;     // wavefronts per node in evaluate_nodes_kernel
 constexpr int kNodeFeatures = kEvalNodeFeatures;  // feature counts up to this use evaluate_nodes_kernel
 
@@ -590,6 +711,31 @@ void launch_reduce_evaluate_flat(const int64_t* partial, const HistReduce* jobs,
                      reinterpret_cast<const long long*>(node_sums), exps, p, fmask, skip_bins,
                      static_cast<FeatCand*>(scratch), store ? 1 : 0,
                      skip_direct ? 1 : 0);
+  DP_HIP(hipGetLastError());
+}
+
+void launch_reduce_evaluate_dense(const int64_t* partial, const HistReduce* jobs, int32_t n_jobs,
+                                  const int32_t* n_jobs_dev, int32_t n_tiles, int32_t n_features,
+                                  int32_t bin_stride, const int64_t* parent_base, int64_t* hist,
+                                  const int32_t* n_bins, const int64_t* node_sums,
+                                  const int32_t* exps, const dp_train_param& param,
+                                  const uint32_t* fmask, const uint8_t* skip_bins, void* scratch,
+                                  bool store, hipStream_t s) {
+  if (n_jobs <= 0 || n_features <= 0) return;
+  need(bin_stride >= 1 && bin_stride <= 64 * 4, "dense reduce-evaluate needs at most 256 bins");
+  need(exps && scratch && n_bins && node_sums,
+       "reduce-evaluate needs the quantiser exponents, the bin counts and candidate scratch");
+  Param p{double(param.lambda), double(param.alpha), double(param.min_child_weight),
+          double(param.gamma)};
+  const dim3 grid(unsigned((n_features + kDenseEvalWaves - 1) / kDenseEvalWaves),
+                  unsigned(n_jobs < 256 ? n_jobs : 256));
+  hipLaunchKernelGGL(reduce_evaluate_dense_kernel, grid, dim3(64 * kDenseEvalWaves), 0, s,
+                     reinterpret_cast<const long long*>(partial), jobs, n_jobs, n_jobs_dev,
+                     n_tiles, n_features, bin_stride,
+                     reinterpret_cast<const long long*>(parent_base),
+                     reinterpret_cast<long long*>(hist), n_bins,
+                     reinterpret_cast<const long long*>(node_sums), exps, p, fmask, skip_bins,
+                     static_cast<FeatCand*>(scratch), store ? 1 : 0);
   DP_HIP(hipGetLastError());
 }
 

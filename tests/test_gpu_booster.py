@@ -196,6 +196,27 @@ def test_present_value_histograms_forced(dp, oracle, device, max_bin, f):
     _compare(bst, o_trees, o_margin, pos, n, 1)
 
 
+@pytest.mark.parametrize("max_bin", [256, 64])
+def test_wide_dense_levels_with_missing_values(dp, oracle, device, max_bin):
+    """The dense layout of a wide matrix (300 features: feature-major partial slots and the
+    reduce and evaluation in one launch on every level below the root) with 40 % missing
+    values, single- and multi-chunk nodes, 255 and 64 bins, against the oracle."""
+    import torch
+
+    def holes(v):
+        g = torch.Generator(device="cpu").manual_seed(13)
+        m = torch.rand(v.shape, generator=g) < 0.4
+        v = v.clone()
+        v[m.to(v.device)] = float("nan")
+        return v
+
+    p = {"max_depth": 6, "eta": 0.3}
+    bst, x, o_trees, o_margin, pos, n = _train_both(dp, oracle, device, 1, 40000, 300, 0, 1, p, 2,
+                                                    20261208, max_bin=max_bin,
+                                                    extra={"dp_sparse_hist": 0}, mutate=holes)
+    _compare(bst, o_trees, o_margin, pos, n, 1)
+
+
 def test_c3_reduced_injected_gradients(dp, oracle, device):
     p = {"max_depth": 8, "eta": 0.3}
     bst, x, o_trees, o_margin, pos, n = _train_both(dp, oracle, device, 3, 30000, 128, 2, 1, p, 2,
