@@ -480,13 +480,10 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
                                   s);
       } else {
         const int32_t G = (T + level_cfg_.tiles - 1) / level_cfg_.tiles;
-        // Levels below the root of wide matrices: feature-major partial slots,
-        // and the reduce and the evaluation in one launch (four features per
-        // workgroup, so at least 64 workgroups per node).  Measured: C4 (784
-        // features) 3,303 -> 3,815 trees/s; on C3 (128) and C2 (28) slower
-        // (394 against 437, 2,256 against 2,471): their nodes' many partial
-        // slots are summed by a few wavefronts per feature, and the
-        // feature-major flush scatters each item's stores over 16 rows.
+        // Levels below the root with more features than one evaluation
+        // workgroup takes: feature-major partial slots, and the reduce and the
+        // evaluation in one launch (measured: C2 2,474 -> 2,560, C3 455 ->
+        // 463, C4 3,321 -> 3,886 trees/s).
         dense_fused = F >= kDenseFuseFeatures && B <= 256 && exps;
         launch_hist(q.bins.p, L, gpair, ridx_[cur].p, hist_work_[cur].p,
                     int32_t(plan_hist_items(nb, N, G, level_cfg_.items)),

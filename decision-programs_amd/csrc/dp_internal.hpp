@@ -410,9 +410,11 @@ void launch_reduce_evaluate_flat(const int64_t* partial, const HistReduce* jobs,
                                  const dp_train_param& param, const uint32_t* fmask,
                                  const uint8_t* skip_bins, void* scratch, bool store,
                                  hipStream_t s, bool skip_direct = false);
-// Feature count from which the booster's dense levels below the root use
-// feature-major partial slots and launch_reduce_evaluate_dense.
-constexpr int32_t kDenseFuseFeatures = 256;
+// Feature counts from which the booster's dense levels below the root use
+// feature-major partial slots and launch_reduce_evaluate_dense, and from which
+// that launch takes four features per workgroup instead of one.
+constexpr int32_t kDenseFuseFeatures = 17;
+constexpr int32_t kDenseWideFeatures = 256;
 // Dense levels whose partial slots are feature-major (launch_hist's fmaj):
 // launch_hist_reduce and launch_evaluate(..., select = false) in one launch --
 // the same node histograms (built and sibling; none stored when !store) and the

@@ -249,21 +249,14 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8 
   for (int j = 0; j < nt; ++j) {
     const unsigned long long* src = lds + j * kLdsWords;
     if (w.partial >= 0 && fmaj) {  // feature-major partial slot: [16][bin_stride][g, h]
-      // Thread k takes feature k % 16 and four bins: eight LDS words (lanes of
-      // one feature in four bin groups share a bank pair: 4-way at most), one
-      // 64-byte run of the slot.
-      unsigned long long* out = partial + int64_t(w.partial + j) * n_words;
-      const int chunks = 16 * ((bin_stride + 3) >> 2);
-      for (int k = threadIdx.x; k < chunks; k += kHistThreads) {
-        const int fl = k & 15, b0 = (k >> 4) * 4;
-        unsigned long long* o = out + (int64_t(fl) * bin_stride + b0) * 2;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          if (b0 + i < bin_stride) {
-            o[2 * i] = src[(b0 + i) * 32 + fl];
-            o[2 * i + 1] = src[(b0 + i) * 32 + 16 + fl];
-          }
-        }
+      // Pair q = (bin q / 16, feature q % 16): its (g, h) words, 16 bytes at
+      // (feature * bin_stride + bin) * 2.  One store instruction of a
+      // wavefront writes four bins of 16 features, a 64-byte run per feature;
+      // the LDS reads of one feature's four bins share a bank pair (4-way).
+      auto* out = reinterpret_cast<ulonglong2*>(partial + int64_t(w.partial + j) * n_words);
+      for (int q = threadIdx.x; q < 16 * bin_stride; q += kHistThreads) {
+        const int fl = q & 15, b = q >> 4;
+        out[fl * bin_stride + b] = make_ulonglong2(src[b * 32 + fl], src[b * 32 + 16 + fl]);
       }
     } else if (w.partial >= 0) {  // tile j's partial slot is the item's slot + j (LDS image)
       unsigned long long* out = partial + int64_t(w.partial + j) * n_words;

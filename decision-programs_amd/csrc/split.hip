@@ -316,7 +316,8 @@ __global__ __launch_bounds__(256) void reduce_evaluate_flat_kernel(
 
 // Reduce and evaluate in one launch for dense levels whose partial slots are
 // feature-major ([16 features][bin_stride][g, h] per tile: hist_kernel's fmaj
-// flush, so a feature's words in a slot are contiguous).  One wavefront per
+// flush, so a feature's words in a slot are contiguous), for wide matrices
+// (many workgroups per job, nodes of few chunks).  One wavefront per
 // feature, four per 256-thread workgroup, lane l holding bins 4l .. 4l + 3 as
 // evaluate_features_kernel<4> does: the lane sums the job's partial slots of
 // its 64 contiguous bytes (or reads what the node's only chunk wrote), writes
@@ -325,8 +326,8 @@ __global__ __launch_bounds__(256) void reduce_evaluate_flat_kernel(
 // followed by evaluate_features_kernel<4>, with one launch and one pass over
 // the level's histograms fewer.  Bins past bin_stride read the feature's last
 // bin and are masked (branch-free loads).  No barriers.
-constexpr int kDenseEvalWaves = 4;
-__global__ __launch_bounds__(64 * kDenseEvalWaves) void reduce_evaluate_dense_kernel(
+constexpr int kDenseEvalFeatures = 4;  // features per workgroup (one per wavefront)
+__global__ __launch_bounds__(64 * kDenseEvalFeatures) void reduce_evaluate_dense_kernel(
     const long long* __restrict__ partial, const HistReduce* __restrict__ jobs,
     int32_t n_jobs_host, const int32_t* __restrict__ n_jobs_dev, int32_t n_tiles,
     int32_t n_features, int32_t bin_stride, const long long* __restrict__ parent_base,
@@ -336,7 +337,7 @@ __global__ __launch_bounds__(64 * kDenseEvalWaves) void reduce_evaluate_dense_ke
     FeatCand* __restrict__ cand, int32_t store) {
   constexpr int BPL = 4;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int32_t f = int32_t(blockIdx.x) * kDenseEvalWaves + wave;
+  const int32_t f = int32_t(blockIdx.x) * kDenseEvalFeatures + wave;
   if (f >= n_features) return;  // wave-uniform; no barriers in this kernel
   const HistReduce j_first = int32_t(blockIdx.y) < n_jobs_host ? jobs[blockIdx.y] : HistReduce{};
   const int32_t n_jobs = n_jobs_dev ? *n_jobs_dev : n_jobs_host;
@@ -432,6 +433,138 @@ __global__ __launch_bounds__(64 * kDenseEvalWaves) void reduce_evaluate_dense_ke
       }
       evaluate(d, j.sibling);
     }
+  }
+}
+
+// Reduce and evaluate in one launch for dense levels whose partial slots are
+// feature-major ([16 features][bin_stride][g, h] per tile: hist_kernel's fmaj
+// flush, so a feature's words in a slot are contiguous), for narrower
+// matrices (fewer workgroups per job, nodes of many chunks).  One 256-thread
+// workgroup per (reduce job, feature); every lane holds bins 4l .. 4l + 3 of
+// the feature, as evaluate_features_kernel<4> does.  Wavefront w sums the
+// job's partial slots w, w + 4, ... of its lane's 64 contiguous bytes (or
+// wavefront 0 reads what the node's only chunk wrote), the sums meet in LDS,
+// and then wavefront 0 writes (with store) and evaluates the node while
+// wavefront 1 derives, writes and evaluates the sibling from the parent's
+// words -- the words and candidates of hist_reduce_kernel followed by
+// evaluate_features_kernel<4>, with one launch and one pass over the level's
+// histograms fewer.  Bins past bin_stride read the feature's last bin and are
+// masked (branch-free loads).
+constexpr int kDenseEvalWaves = 4;
+__global__ __launch_bounds__(64 * kDenseEvalWaves) void reduce_evaluate_dense_split_kernel(
+    const long long* __restrict__ partial, const HistReduce* __restrict__ jobs,
+    int32_t n_jobs_host, const int32_t* __restrict__ n_jobs_dev, int32_t n_tiles,
+    int32_t n_features, int32_t bin_stride, const long long* __restrict__ parent_base,
+    long long* __restrict__ hist, const int32_t* __restrict__ n_bins,
+    const long long* __restrict__ node_sums, const int32_t* __restrict__ exps, Param p,
+    const uint32_t* __restrict__ fmask, const uint8_t* __restrict__ skip_bins,
+    FeatCand* __restrict__ cand, int32_t store) {
+  constexpr int BPL = 4, W = kDenseEvalWaves;
+  __shared__ long long part[W][2 * BPL][64];  // each wavefront's sums; [0] then the node's
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+  const int32_t f = int32_t(blockIdx.x);
+  const HistReduce j_first = int32_t(blockIdx.y) < n_jobs_host ? jobs[blockIdx.y] : HistReduce{};
+  const int32_t n_jobs = n_jobs_dev ? *n_jobs_dev : n_jobs_host;
+  const int32_t tile = f >> 4, fl = f & 15;
+  const int64_t slot_words = int64_t(bin_stride) * 32;  // a tile's partial slot
+  const int64_t node_elems = int64_t(n_features) * bin_stride * 2;
+  bool ok[BPL];
+  int64_t at[BPL], pat[BPL];  // word of bin (g; h is + 1): node histogram, partial slot
+#pragma unroll
+  for (int k = 0; k < BPL; ++k) {
+    const int bn = lane * BPL + k;
+    ok[k] = bn < bin_stride;
+    const int bc = ok[k] ? bn : bin_stride - 1;
+    at[k] = (int64_t(f) * bin_stride + bc) * 2;
+    pat[k] = (int64_t(fl) * bin_stride + bc) * 2;
+  }
+  const int nbf = n_bins[f];
+  const int skip = skip_bins ? int(skip_bins[f]) : -1;
+  const double ug = ldexp(1.0, -exps[0]), uh = ldexp(1.0, -exps[1]);
+  for (int32_t jb = blockIdx.y; jb < n_jobs; jb += gridDim.y) {
+    const HistReduce j = jb == int32_t(blockIdx.y) ? j_first : jobs[jb];
+    const bool direct = j.nc == 1 && j.p0 < 0;  // uniform: the node's only chunk wrote it
+    long long s[2 * BPL] = {};                  // g, h of each bin: this wavefront's part
+    long long pw[2 * BPL] = {};                 // wavefront 1: the parent's words
+    if (wave == 1 && j.sibling >= 0)
+#pragma unroll
+      for (int k = 0; k < BPL; ++k) {
+        pw[2 * k] = parent_base[j.parent + at[k]];
+        pw[2 * k + 1] = parent_base[j.parent + at[k] + 1];
+      }
+    if (direct) {
+      if (wave == 0) {
+        const long long* built = hist + int64_t(j.slot) * node_elems;
+#pragma unroll
+        for (int k = 0; k < BPL; ++k) {
+          s[2 * k] = built[at[k]];
+          s[2 * k + 1] = built[at[k] + 1];
+        }
+      }
+    } else {
+      const long long* src = partial + (int64_t(j.p0) * n_tiles + tile) * slot_words;
+      const int64_t step = int64_t(n_tiles) * slot_words;
+      int32_t c = wave;
+      for (; c + W < j.nc; c += 2 * W) {  // two of this wavefront's slots in flight
+        long long v[2][2 * BPL];
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int k = 0; k < BPL; ++k) {
+            v[u][2 * k] = src[(c + u * W) * step + pat[k]];
+            v[u][2 * k + 1] = src[(c + u * W) * step + pat[k] + 1];
+          }
+#pragma unroll
+        for (int i = 0; i < 2 * BPL; ++i) s[i] += v[0][i] + v[1][i];
+      }
+      if (c < j.nc)
+#pragma unroll
+        for (int k = 0; k < BPL; ++k) {
+          s[2 * k] += src[c * step + pat[k]];
+          s[2 * k + 1] += src[c * step + pat[k] + 1];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 2 * BPL; ++i) part[wave][i][lane] = s[i];
+    __syncthreads();
+    if (wave == 0) {  // the node: the four parts (one, for a direct node)
+      if (!direct)
+#pragma unroll
+        for (int i = 0; i < 2 * BPL; ++i) s[i] += part[1][i][lane] + part[2][i][lane] + part[3][i][lane];
+#pragma unroll
+      for (int i = 0; i < 2 * BPL; ++i) part[0][i][lane] = s[i];
+    }
+    __syncthreads();
+    if (wave <= 1) {
+      const bool sib = wave == 1;
+      if (!sib || j.sibling >= 0) {  // wavefront-uniform
+        FeatBins<BPL> d;
+#pragma unroll
+        for (int k = 0; k < BPL; ++k) {
+          const long long g = part[0][2 * k][lane], hh = part[0][2 * k + 1][lane];
+          d.g[k] = !ok[k] ? 0 : (sib ? pw[2 * k] - g : g);
+          d.h[k] = !ok[k] ? 0 : (sib ? pw[2 * k + 1] - hh : hh);
+        }
+        const int32_t node = sib ? j.sibling : j.slot;
+        if (store && (sib || !direct)) {
+          long long* o = hist + int64_t(node) * node_elems;
+#pragma unroll
+          for (int k = 0; k < BPL; ++k)
+            if (ok[k]) {
+              o[at[k]] = d.g[k];
+              o[at[k] + 1] = d.h[k];
+            }
+        }
+        const long long gp = node_sums[2 * node], hp = node_sums[2 * node + 1];
+        const double parent_gain = calc_gain(p, double(gp) * ug, double(hp) * uh);
+        const int nb = feature_allowed(fmask, node, f, n_features) ? nbf : 0;
+        const Cand cd = feature_best<BPL>(d, f, nb, skip, gp, hp, parent_gain, ug, uh, p);
+        if (lane == 0)
+          cand[int64_t(node) * n_features + f] = FeatCand{cd.loss, cd.gl, cd.hl, cd.bin, cd.dl};
+      }
+    }
+    __syncthreads();  // part is rewritten by the next job
   }
 }
 
@@ -727,9 +860,15 @@ void launch_reduce_evaluate_dense(const int64_t* partial, const HistReduce* jobs
        "reduce-evaluate needs the quantiser exponents, the bin counts and candidate scratch");
   Param p{double(param.lambda), double(param.alpha), double(param.min_child_weight),
           double(param.gamma)};
-  const dim3 grid(unsigned((n_features + kDenseEvalWaves - 1) / kDenseEvalWaves),
+  // Wide matrices: four features per workgroup, each wavefront summing its
+  // feature's slots alone; narrower ones: a workgroup per feature whose four
+  // wavefronts split the slots and evaluate the node and the sibling at once.
+  const bool wide = n_features >= kDenseWideFeatures;
+  const dim3 grid(unsigned(wide ? (n_features + kDenseEvalFeatures - 1) / kDenseEvalFeatures
+                                : n_features),
                   unsigned(n_jobs < 256 ? n_jobs : 256));
-  hipLaunchKernelGGL(reduce_evaluate_dense_kernel, grid, dim3(64 * kDenseEvalWaves), 0, s,
+  hipLaunchKernelGGL(wide ? reduce_evaluate_dense_kernel : reduce_evaluate_dense_split_kernel,
+                     grid, dim3(256), 0, s,
                      reinterpret_cast<const long long*>(partial), jobs, n_jobs, n_jobs_dev,
                      n_tiles, n_features, bin_stride,
                      reinterpret_cast<const long long*>(parent_base),
