@@ -1161,12 +1161,19 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
   for (int32_t l = 0; l < S; ++l) key.push_back(growers_[size_t(l)]->signature());
   words(key, &q.layout, sizeof q.layout);
   words(key, &tp_, sizeof tp_);
+  // A round that computes gradients leaves its leaf values for the next round's
+  // gradient kernel to add to the margins (one launch fewer per round);
+  // values_pending_ says so, and margins() adds them when asked first.
+  const bool add_first = values_pending_ && !with_gradients;  // caller gradients follow
+  key.push_back(uint64_t(values_pending_) | uint64_t(with_gradients) << 1);
   enqueue(key, eager, [&] {
     bool maxima = false;
+    if (add_first) launch_add_leaf_values(margin_.p, K, leaf_values_.p, N, stream_);
     // With row sampling the quantiser takes the maxima over the kept rows.
     if (with_gradients)
       maxima = launch_gradients(objective_id_, margin_.p, d->labels.p, N, K, grad_.p, hess_.p,
-                                rows.active() ? nullptr : quant_scratch_.p, stream_);
+                                rows.active() ? nullptr : quant_scratch_.p, stream_,
+                                values_pending_ ? leaf_values_.p : nullptr);
     // The per-workgroup sums stay in the quantiser's slots: each tree's first
     // launch adds up its output's.
     launch_quantise(grad_.p, hess_.p, N, K, quant_scratch_.p, maxima, exps_.p, gpair_.p, nullptr,
@@ -1191,7 +1198,7 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
                           slots + int64_t(k) * blocks * 2, blocks, tp_,
                           leaf_values_.p + int64_t(k) * N, positions, k, stream_);
       }
-      launch_add_leaf_values(margin_.p, K, leaf_values_.p, N, stream_);
+      if (!with_gradients) launch_add_leaf_values(margin_.p, K, leaf_values_.p, N, stream_);
       return;
     }
     // Each tree stores its own leaf-value plane; only the last writes the row
@@ -1210,8 +1217,9 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
       DP_HIP(hipEventRecord(tree_done_[size_t(l)], tree_streams_[size_t(l)]));
       DP_HIP(hipStreamWaitEvent(stream_, tree_done_[size_t(l)], 0));
     }
-    launch_add_leaf_values(margin_.p, K, leaf_values_.p, N, stream_);
+    if (!with_gradients) launch_add_leaf_values(margin_.p, K, leaf_values_.p, N, stream_);
   });
+  values_pending_ = with_gradients;
   // This round's records go to the buffer the round in flight does not use.
   const int32_t buffer = pending_ ? 1 - pending_buffer_ : 0;
   for (int32_t l = 0; l < S; ++l)
@@ -1264,6 +1272,11 @@ void Booster::margins(float* out, size_t n) const {
   flush();
   need(configured_, "booster has not been trained");
   need(n == margin_.n, "margin buffer size differs");
+  if (values_pending_) {  // the last round's leaf values, left for the next gradients
+    launch_add_leaf_values(margin_.p, n_groups_, leaf_values_.p, train_->n_rows, stream_);
+    values_pending_ = false;
+  }
+  DP_HIP(hipStreamSynchronize(stream_));
   DP_HIP(hipMemcpy(out, margin_.p, margin_.bytes(), hipMemcpyDeviceToHost));
 }
 

@@ -247,8 +247,12 @@ class Booster {
   DMatrix* train_ = nullptr;
   // training state
   PooledBuffer<float> margin_, grad_, hess_;
+  // The last round's leaf values are not in margin_ yet: the next round's
+  // gradient kernel (or margins()) adds them.
+  mutable bool values_pending_ = false;
   // The round's leaf-value planes, [n_groups][n_rows]: tree k stores each
-  // row's leaf value in plane k; the round ends by adding them to margin_.
+  // row's leaf value in plane k; they are added to margin_ by the next round's
+  // gradient kernel, or at the end of a round of caller-supplied gradients.
   PooledBuffer<float> leaf_values_;
   PooledBuffer<int32_t> gpair_, exps_;
   PooledBuffer<uint8_t> quant_scratch_;  // quantiser reduction slots

@@ -528,8 +528,9 @@ int dp_objective_gradients(int32_t objective, const float* margin, const float* 
     dp::need(n_classes >= 1, "n_classes must be positive");
     dp::need(objective != DP_OBJ_SOFTPROB || n_classes >= 2, "softprob needs 2+ classes");
     dp::need(objective == DP_OBJ_SOFTPROB || n_classes == 1, "single-output objective");
-    dp::launch_gradients(objective, margin, label, n_rows, n_classes, grad, hess, nullptr,
-                         as_stream(stream));
+    // No leaf values: the margins are only read.
+    dp::launch_gradients(objective, const_cast<float*>(margin), label, n_rows, n_classes, grad,
+                         hess, nullptr, as_stream(stream));
   });
 }
 

@@ -630,9 +630,13 @@ void launch_init_margin(float* margin, int64_t n_rows, int32_t n_outputs, const 
 // Objective gradients.  With quant_scratch (quantise_scratch_bytes) and one
 // output, the per-workgroup maxima the quantiser needs are written too and
 // true is returned (pass maxima_ready to launch_quantise).
-bool launch_gradients(int32_t objective, const float* margin, const float* label,
+// values (optional, planes [n_classes][n_rows]): leaf values added to the
+// margins first (margin[r * n_classes + k] += values[k * n_rows + r], stored),
+// as launch_add_leaf_values would, so a round's add rides in the next round's
+// gradients.
+bool launch_gradients(int32_t objective, float* margin, const float* label,
                       int64_t n_rows, int32_t n_classes, float* grad, float* hess,
-                      void* quant_scratch, hipStream_t s);
+                      void* quant_scratch, hipStream_t s, const float* values = nullptr);
 // Quantiser: exps int32 [n_classes][2]; gpair int32 [n_classes][n_rows][2];
 // sums int64 [n_classes][2]; scratch holds quantise_scratch_bytes.
 // Most workgroups (and reduction slots) per class: eight 256-thread workgroups

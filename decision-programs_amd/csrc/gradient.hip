@@ -72,12 +72,17 @@ __device__ __forceinline__ void block_max2(unsigned& a, unsigned& b) {
 // bit patterns to max_slots[2 * blockIdx.x ..].
 template <bool MAXIMA>
 __global__ __launch_bounds__(kQuantThreads) void gradients_kernel(
-    int objective, const float* __restrict__ margin, const float* __restrict__ label,
+    int objective, float* __restrict__ margin, const float* __restrict__ label,
     int64_t n_rows, int n_classes, float* __restrict__ grad, float* __restrict__ hess,
-    unsigned* __restrict__ max_slots) {
+    unsigned* __restrict__ max_slots, const float* __restrict__ values) {
   unsigned mg = 0, mh = 0;
   for (int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; r < n_rows;
        r += int64_t(blockDim.x) * gridDim.x) {
+    // The previous round's leaf values first (values: planes [n_classes][n_rows]):
+    // margin + value, the add add_leaf_values_kernel would have made.
+    if (values)
+      for (int k = 0; k < n_classes; ++k)
+        margin[r * n_classes + k] = margin[r * n_classes + k] + values[int64_t(k) * n_rows + r];
     if (objective == DP_OBJ_LOGISTIC) {
       const float p = 1.0f / (1.0f + dp_expf(-margin[r]));
       const float g = p - label[r], h = fmaxf(p * (1.0f - p), 1e-16f);
@@ -314,9 +319,9 @@ void launch_init_margin(float* margin, int64_t n_rows, int32_t n_outputs, const 
   DP_HIP(hipGetLastError());
 }
 
-bool launch_gradients(int32_t objective, const float* margin, const float* label,
+bool launch_gradients(int32_t objective, float* margin, const float* label,
                       int64_t n_rows, int32_t n_classes, float* grad, float* hess,
-                      void* quant_scratch, hipStream_t s) {
+                      void* quant_scratch, hipStream_t s, const float* values) {
   if (n_rows <= 0) return false;
   need(objective == DP_OBJ_LOGISTIC || objective == DP_OBJ_SOFTPROB ||
            objective == DP_OBJ_SQUARED,
@@ -324,13 +329,13 @@ bool launch_gradients(int32_t objective, const float* margin, const float* label
   if (quant_scratch && n_classes == 1) {
     hipLaunchKernelGGL(gradients_kernel<true>, dim3(quantise_blocks(n_rows)), dim3(kQuantThreads),
                        0, s, objective, margin, label, n_rows, n_classes, grad, hess,
-                       static_cast<unsigned*>(quant_scratch));
+                       static_cast<unsigned*>(quant_scratch), values);
     DP_HIP(hipGetLastError());
     return true;
   }
   hipLaunchKernelGGL(gradients_kernel<false>, dim3(grid_for(n_rows, kQuantThreads, 8192)),
                      dim3(kQuantThreads), 0, s, objective, margin, label, n_rows, n_classes, grad,
-                     hess, nullptr);
+                     hess, nullptr, values);
   DP_HIP(hipGetLastError());
   return false;
 }
