@@ -376,7 +376,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
   auto* host_counts = reinterpret_cast<PlanCounts*>(level_count_.p);
 
   launch_plan_root(level_[0].p, sums_[0].p, seg_begin_[0].p, part_work_[0].p, part_first_[0].p,
-                   node_left_[0].p, c, N, root_slots, root_blocks, chunk_, ridx_[0].p, s);
+                   node_left_[0].p, c, N, root_slots, root_blocks, chunk_, ridx_[0].p, s, exps);
   int64_t nb = 1;  // bound of the current level's node count
   int64_t nb_prev = 0;
   // The last split level's count launch stores every leaf value of levels
@@ -670,6 +670,16 @@ uint64_t Grower::signature() const {
     mix(uint64_t(c->split));
   }
   return h;
+}
+
+void Grower::exponents(int32_t slot, int32_t buffer, int32_t* out) const {
+  const PlanCounts* c =
+      eager_ ? reinterpret_cast<const PlanCounts*>(
+                   readback_.p +
+                   slot_bytes_ * (size_t(buffer) * size_t(readback_slots_) + size_t(slot)))
+             : &spill_counts_[size_t(slot)];
+  out[0] = c->exps[0];
+  out[1] = c->exps[1];
 }
 
 void Grower::collect(const Quantized& q, int32_t slot, int32_t buffer, Tree& tree) const {
@@ -1224,9 +1234,6 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
   const int32_t buffer = pending_ ? 1 - pending_buffer_ : 0;
   for (int32_t l = 0; l < S; ++l)
     growers_[size_t(l)]->readback(S == 1 ? K : (K - l + S - 1) / S, buffer, stream_);
-  exps_host_.reserve(2 * exps_.bytes());
-  DP_HIP(hipMemcpyAsync(exps_host_.p + size_t(buffer) * exps_.bytes(), exps_.p, exps_.bytes(),
-                        hipMemcpyDeviceToHost, stream_));
   if (!round_done_[buffer])
     DP_HIP(hipEventCreateWithFlags(&round_done_[buffer], hipEventDisableTiming));
   DP_HIP(hipEventRecord(round_done_[buffer], stream_));
@@ -1250,8 +1257,11 @@ void Booster::flush() const {
   }
   const int32_t b = pending_buffer_;
   DP_HIP(hipEventSynchronize(round_done_[b]));
-  const auto* e = reinterpret_cast<const int32_t*>(exps_host_.p + size_t(b) * exps_.bytes());
-  last_exps_.assign(e, e + 2 * n_groups_);
+  // Each tree's records carry its output's quantiser exponents.
+  last_exps_.assign(size_t(2 * n_groups_), 0);
+  for (int32_t k = 0; k < n_groups_; ++k)
+    growers_[size_t(k % pending_lanes_)]->exponents(k / pending_lanes_, b,
+                                                   &last_exps_[2 * size_t(k)]);
   std::vector<Tree> round(static_cast<size_t>(n_groups_));
   try {
     const int32_t S = pending_lanes_;

@@ -124,6 +124,8 @@ class Grower {
   void readback(int32_t n_slots, int32_t buffer, hipStream_t s);
   // The tree grown into `slot`; readback() into `buffer` has completed.
   void collect(const Quantized& q, int32_t slot, int32_t buffer, Tree& tree) const;
+  // The quantiser exponents (g, h) of the tree in `slot`, as collect() finds it.
+  void exponents(int32_t slot, int32_t buffer, int32_t* out) const;
   // False when trees are grown level-synced (grow() then synchronises).
   bool eager() const { return eager_; }
   // Changes whenever a buffer that grow() passes to a kernel moves or resizes.
@@ -264,7 +266,6 @@ class Booster {
   uint64_t gradient_src_host_[2] = {0, 0};  // what gradient_src_ holds (stored in stream order)
   bool caller_gradients_ = false;  // the last round's gradients came from the caller
   mutable std::vector<int32_t> last_exps_;
-  PooledPinnedBuffer exps_host_;  // two buffers, by round parity
   bool record_positions_ = false;
   bool use_graphs_ = true;
   bool autotune_ = true;        // dp_autotune: time the histogram launch shapes (tune.cpp)

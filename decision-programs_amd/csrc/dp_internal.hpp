@@ -202,6 +202,7 @@ struct PlanCounts {
   int32_t error;       // nonzero: inconsistent partition counts
   int32_t n_leaf_prev; // leaf work items of the planner run before the last
   int32_t pad;
+  int32_t exps[2];     // the tree's quantiser exponents (g, h), stored by its root planner
   // Partition work items of the level of depth d in n_part[d & 1]: the planner
   // of level d writes level d + 1's while that level's scatter, in the same
   // launch, still reads level d's.
@@ -587,7 +588,8 @@ void launch_plan_scatter(const PlanArgs& a, const ScatterArgs& sa, int64_t n_row
 void launch_plan_root(LevelNode* cur, int64_t* sums, int64_t* seg_begin, PartWork* part_work,
                       int32_t* part_first, int64_t* node_left, PlanCounts* counts,
                       int64_t n_rows, const int64_t* root_slots, int32_t root_blocks,
-                      int64_t part_chunk, uint32_t* ridx, hipStream_t s);
+                      int64_t part_chunk, uint32_t* ridx, hipStream_t s,
+                      const int32_t* exps = nullptr);
 // Upper bounds of the planner's outputs for a level of at most `nodes` nodes.
 inline int64_t plan_hist_capacity(int64_t nodes, int32_t groups, int32_t items) {
   return items + int64_t(groups) + (nodes / 2 + 8) * int64_t(groups);

@@ -764,7 +764,8 @@ __global__ __launch_bounds__(kPlanThreads) void plan_scatter_kernel(PlanArgs a, 
 __global__ __launch_bounds__(256) void plan_root_kernel(
     LevelNode* cur, int64_t* sums, int64_t* seg_begin, PartWork* part_work, int32_t* part_first,
     int64_t* node_left, PlanCounts* counts, int64_t n_rows, const int64_t* __restrict__ root_slots,
-    int32_t root_blocks, int64_t part_chunk, uint32_t* __restrict__ ridx) {
+    int32_t root_blocks, int64_t part_chunk, uint32_t* __restrict__ ridx,
+    const int32_t* __restrict__ exps) {
   __shared__ int64_t part[2][4];
   const int64_t chunks = (n_rows + part_chunk - 1) / part_chunk;
   const int64_t stride = int64_t(blockDim.x) * gridDim.x;
@@ -802,6 +803,10 @@ __global__ __launch_bounds__(256) void plan_root_kernel(
     c.n_level = 1;
     c.n_nodes = 1;
     c.n_part[0] = int32_t(chunks);
+    if (exps) {  // the tree's records then carry its exponents to the host
+      c.exps[0] = exps[0];
+      c.exps[1] = exps[1];
+    }
     *counts = c;
   }
 }
@@ -835,12 +840,13 @@ void launch_plan_scatter(const PlanArgs& a, const ScatterArgs& sa, int64_t n_row
 void launch_plan_root(LevelNode* cur, int64_t* sums, int64_t* seg_begin, PartWork* part_work,
                       int32_t* part_first, int64_t* node_left, PlanCounts* counts,
                       int64_t n_rows, const int64_t* root_slots, int32_t root_blocks,
-                      int64_t part_chunk, uint32_t* ridx, hipStream_t s) {
+                      int64_t part_chunk, uint32_t* ridx, hipStream_t s,
+                      const int32_t* exps) {
   need(part_chunk >= 1 && part_chunk <= kPartChunk, "partition chunk out of range");
   need(root_blocks >= 1, "root sums need at least one slot");
   hipLaunchKernelGGL(plan_root_kernel, dim3(grid_for(n_rows, 256, 1024)), dim3(256), 0, s, cur,
                      sums, seg_begin, part_work, part_first, node_left, counts, n_rows, root_slots,
-                     root_blocks, part_chunk, ridx);
+                     root_blocks, part_chunk, ridx, exps);
   DP_HIP(hipGetLastError());
 }
 
