@@ -236,6 +236,10 @@ namespace {
 constexpr int64_t kEagerNodes = int64_t(1) << 16;
 constexpr int64_t kEagerHistBytes = int64_t(8) << 30;
 
+// Present-value levels of at least this many nodes evaluate their single-chunk
+// nodes in the histogram pass (Grower::grow).
+constexpr int64_t kInPassNodes = 128;
+
 int64_t level_bound(int32_t depth, int64_t n_rows) {
   return depth >= 62 ? n_rows : std::min<int64_t>(int64_t(1) << depth, n_rows);
 }
@@ -449,12 +453,14 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
                     partial_.p, s, nullptr, root_cfg_, skip_tiles_);
         launch_hist_reduce(partial_.p, root_job_.p, 1, nullptr, T, F, B, nullptr, h, false, s);
       } else if (sparse_) {
-        // On the last split level of a fused tree, the nodes built in one chunk
-        // are evaluated by the histogram pass itself, from LDS, and are never
-        // stored; the reduce-evaluate takes the rest.  (On earlier levels the
-        // pass's 512-thread workgroups accumulate the multi-chunk items more
-        // slowly than the evaluation saves: measured on C5.)
-        const bool in_pass = fused && !keep;
+        // On the last split level of a fused tree, and on levels of at least
+        // kInPassNodes nodes (mostly small ones), the nodes built in one chunk
+        // are evaluated by the histogram pass itself, from LDS (on the last
+        // level never stored); the reduce-evaluate takes the rest.  (On
+        // levels of fewer, larger nodes the pass's 512-thread workgroups
+        // accumulate the multi-chunk items more slowly than the evaluation
+        // saves: measured on C5.)
+        const bool in_pass = fused && (!keep || nb >= kInPassNodes);
         SparseEval ev;
         ev.parent_base = hist_[nxt].p;
         ev.n_bins = q.d_nbins.p;
