@@ -91,6 +91,7 @@ struct Pass {
   int32_t bin_stride;
   const int32_t* gpair;
   int64_t* out;  // `nodes` node histograms
+  bool fmaj;     // the levels' feature-major partial slots (launch_hist's fmaj)
 };
 
 double time_dense(const Pass& p, const HistConfig& cfg, hipStream_t s) {
@@ -110,8 +111,10 @@ double time_dense(const Pass& p, const HistConfig& cfg, hipStream_t s) {
   DP_HIP(hipMemcpyAsync(dj.p, j.data(), dj.bytes(), hipMemcpyHostToDevice, s));
   const double ms = time_ms(
       [&] {
+        // With fmaj the reduce below reads the slots in the other layout: its
+        // sums are discarded, its time stands for the levels' reduce.
         launch_hist(p.bins, *p.L, p.gpair, p.ridx, dw.p, int32_t(w.size()), nullptr,
-                    p.bin_stride, p.out, partial.p, s, p.rows_major, cfg, p.skip);
+                    p.bin_stride, p.out, partial.p, s, p.rows_major, cfg, p.skip, p.fmaj);
         launch_hist_reduce(partial.p, dj.p, p.nodes, nullptr, p.L->n_tiles, p.L->n_features,
                            p.bin_stride, nullptr, p.out, false, s);
       },
@@ -159,7 +162,7 @@ const HistTuning& tune_dense_hist(const dp_bin_layout& L, const uint8_t* bins,
   const auto cands = dense_candidates(L.n_tiles);
   constexpr int32_t kStride = 32, kNodes = 12;  // the gathered pass's nodes (see above)
   DeviceBuffer<int64_t> out(size_t(kNodes) * size_t(L.n_features) * size_t(bin_stride) * 2);
-  Pass root{&L, bins, nullptr, skip, nullptr, L.n_rows, 1, bin_stride, gpair, out.p};
+  Pass root{&L, bins, nullptr, skip, nullptr, L.n_rows, 1, bin_stride, gpair, out.p, false};
   std::string report = "{";
   t.root = pick(cands, [&](const HistConfig& c) { return time_dense(root, c, s); }, report,
                 "root");
@@ -173,7 +176,10 @@ const HistTuning& tune_dense_hist(const dp_bin_layout& L, const uint8_t* bins,
         ids[size_t(k) * size_t(per) + size_t(i)] = uint32_t(i * kStride + k);
     DeviceBuffer<uint32_t> ridx(ids.size());
     DP_HIP(hipMemcpyAsync(ridx.p, ids.data(), ridx.bytes(), hipMemcpyHostToDevice, s));
-    Pass level{&L, bins, rows_major, skip, ridx.p, per, kNodes, bin_stride, gpair, out.p};
+    // The levels' flush layout: feature-major where the booster fuses the
+    // reduce and the evaluation (it costs more per item than the LDS image).
+    const bool fmaj = L.n_features >= kDenseFuseFeatures && bin_stride <= 256;
+    Pass level{&L, bins, rows_major, skip, ridx.p, per, kNodes, bin_stride, gpair, out.p, fmaj};
     report += ",";
     t.level = pick(cands, [&](const HistConfig& c) { return time_dense(level, c, s); }, report,
                    "gathered");
