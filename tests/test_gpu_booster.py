@@ -456,7 +456,9 @@ def test_graph_replays_equal_direct_launches(dp, device, objective, k):
     """Rounds replayed from cached HIP graphs give the same model, margins and row positions
     as rounds launched directly; a parameter change between rounds captures a new graph, and
     caller gradients (a graph without the objective kernel) replay the same way.  Rounds left
-    in flight back to back (trees collected one call later) give the same model too."""
+    in flight back to back (trees collected one call later, each round's leaf values added by
+    the next round's gradient kernel instead of a margin read) give the same model and the
+    same final margins too."""
     import torch
     from dpgbdt import ops
 
@@ -490,13 +492,19 @@ def test_graph_replays_equal_direct_launches(dp, device, objective, k):
                 positions.append(bst.last_positions(n))
                 margins.append(bst.margins(n, k))
         assert bst.num_boosted_rounds() == 9
-        return bst.save_raw(), positions, margins
+        # the last rounds' leaf values are in the margins however the rounds were read
+        return bst.save_raw(), positions, margins, bst.margins(n, k)
 
-    raw_direct, pos_direct, m_direct = train(0)
-    raw_graph, pos_graph, m_graph = train(1)
+    raw_direct, pos_direct, m_direct, end_direct = train(0)
+    raw_graph, pos_graph, m_graph, end_graph = train(1)
     assert raw_graph == raw_direct
-    assert train(1, inspect=False)[0] == raw_direct
-    assert train(0, inspect=False)[0] == raw_direct
+    for graphs in (1, 0):
+        raw, _, _, end = train(graphs, inspect=False)
+        assert raw == raw_direct
+        np.testing.assert_array_equal(np.asarray(end).view(np.uint32),
+                                      np.asarray(end_direct).view(np.uint32))
+    np.testing.assert_array_equal(np.asarray(end_graph).view(np.uint32),
+                                  np.asarray(end_direct).view(np.uint32))
     for r, (a, b) in enumerate(zip(pos_graph, pos_direct)):
         np.testing.assert_array_equal(a, b, err_msg=f"round {r} positions")
     for r, (a, b) in enumerate(zip(m_graph, m_direct)):
