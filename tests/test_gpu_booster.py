@@ -692,6 +692,48 @@ def test_c3_tree_one_million_rows(dp, oracle, device):
     _compare(bst, o_trees, o_margin, pos, n, 1)
 
 
+def test_c3_full_size_tree(dp, oracle, device):
+    """C3 at its full size -- 10,000,000 rows x 128 features, 256 bins, depth 8, injected
+    gradients -- one round against the oracle's booster on all host cores: every split record,
+    row count, leaf value, the 10M row positions and the margins.  The oracle takes the GPU's
+    cuts and uint8 bins (bit-identical to its own on every configuration's shape,
+    test_gpu_kernels.py::test_cuts_and_bins_bit_exact), as the bench's CPU leg does, so the
+    check covers the boosting round: the root pass over all rows, the gathered passes with
+    their fitted chunks, the fused reduce-evaluate over many-chunk nodes and the partition of
+    10M rows at every level."""
+    import os
+
+    import torch
+    from dpgbdt import ops
+
+    n, f = 10_000_000, 128
+    print("[booster] C3 10000000 x 128, depth 8 vs the oracle (host threads)", flush=True)
+    values, labels, g, h = ops.synth(3, n, 20261204, want_grad=True)
+    dtrain = dp.DMatrix(values, labels)
+    bst = dp.Booster({"objective": "reg:squarederror", "max_depth": 8, "eta": 0.3,
+                      "max_bin": 256, "dp_record_positions": 1}, [dtrain])
+    bst.boost(dtrain, 0, g.reshape(-1, 1).contiguous(), h.reshape(-1, 1).contiguous())
+    gpu_positions = [bst.last_positions(n)]
+    assert not bool(torch.isnan(values).any().item())  # C3 has no missing values
+    ws = ops.Workspace()
+    cut_ptr, cuts, _, _ = ops.sketch_cuts(ws, values, 256)
+    lay = ops.layout(n, f, 0, -1)
+    bins = ops.from_tiles(ops.bin_values(values, lay, cut_ptr, cuts).cpu().numpy(), lay)
+    gn, hn = g.cpu().numpy()[:, None], h.cpu().numpy()[:, None]
+    y = labels.cpu().numpy()
+    del values, labels, g, h
+    torch.cuda.empty_cache()
+    oracle.set_threads(len(os.sched_getaffinity(0)))
+    try:
+        o_trees, o_margin, _ = oracle.train(bins, cut_ptr, cuts, -1, 2, y, 1,
+                                            oracle.params(eta=0.3, max_depth=8), 1,
+                                            bin_stride=int(np.diff(cut_ptr).max()),
+                                            injected=lambda r: (gn, hn))
+    finally:
+        oracle.set_threads(1)
+    _compare(bst, o_trees, o_margin, gpu_positions, n, 1)
+
+
 def test_strided_label_interface_is_refused(dp, device):
     """A label array interface with strides is copied as one contiguous block, so strides must
     be the C-contiguous ones: a column slice of an [n, 2] array ([n, 1] with a row stride of 8
