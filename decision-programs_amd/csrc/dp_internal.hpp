@@ -679,6 +679,10 @@ struct SparseBins {
   DeviceBuffer<uint16_t> entries;  // [nnz]
 };
 constexpr int64_t kSparseLdsBytes = 64 * 1024;
+// LDS of one present-value tile in the histogram kernel: g and h in planes of
+// their own, each feature's bins padded by one word (tile_features *
+// (bin_stride + 1) * 16 bytes, at most kSparseLdsBytes + 4 KiB).
+constexpr int64_t kSparseLdsAlloc = kSparseLdsBytes + 4 * 1024;
 constexpr double kSparseDensity = 0.25;  // automatic use: at most this share present
 int32_t sparse_tile_features(int32_t bin_stride);
 // Counts the present values of `bins` (16-feature tiles, missing byte 255) and

@@ -289,12 +289,13 @@ struct SparseEvalArgs {
 };
 
 // EVAL's epilogue (see hist_sparse_kernel): node w.slot's features f0 .. f0 +
-// nf from the LDS tile ([feature][bin][g, h] words), and its sibling's from
+// nf from the LDS planes (g, h: [feature][bin_stride + 1] words), and its sibling's from
 // the parent's words minus them; every thread of the workgroup takes part.
 template <int THREADS>
 __device__ __forceinline__ void evaluate_tile(const SparseEvalArgs& ev, const HistWork& w,
                                               int32_t f0, int32_t nf, int32_t n_features,
                                               int32_t bin_stride, const unsigned long long* lds,
+                                              uint32_t ps, uint32_t hoff,
                                               unsigned long long* __restrict__ hist) {
   constexpr int BPL = 4;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -302,15 +303,15 @@ __device__ __forceinline__ void evaluate_tile(const SparseEvalArgs& ev, const Hi
   const double ug = ldexp(1.0, -ev.exps[0]), uh = ldexp(1.0, -ev.exps[1]);
   const int64_t node_elems = int64_t(n_features) * bin_stride * 2;
   const bool sib = w.parent >= 0;  // uniform per workgroup
-  // This lane's four bins of feature fl from the LDS tile (zero past the bins).
+  // This lane's four bins of feature fl from the LDS planes (zero past the bins).
   auto load = [&](int32_t fl, bool live, long long (&g)[BPL], long long (&h)[BPL]) {
 #pragma unroll
     for (int k = 0; k < BPL; ++k) {
       const int b = sub * BPL + k;
       const bool ok = live && b < bin_stride;
-      const int e = ((live ? fl : 0) * bin_stride + (ok ? b : 0)) * 2;
-      g[k] = ok ? (long long)lds[e] : 0;
-      h[k] = ok ? (long long)lds[e + 1] : 0;
+      const uint32_t a = uint32_t(live ? fl : 0) * ps + uint32_t(ok ? b : 0);
+      g[k] = ok ? (long long)lds[a] : 0;
+      h[k] = ok ? (long long)lds[a + hoff] : 0;
     }
   };
   for (int32_t fb = 0; fb < nf; fb += (THREADS / 64) * 4) {
@@ -355,14 +356,24 @@ __device__ __forceinline__ void evaluate_tile(const SparseEvalArgs& ev, const Hi
 
 // Histograms from the present-value layout (SparseBins): one work item = rows
 // [begin, end) of node `slot` for one sparse tile of tile_features features.
-// The tile's histogram lives in LDS as the node histogram's own layout,
-// [feature][bin][g, h] int64 (tile_features * bin_stride * 16 bytes, dynamic
-// LDS), so the store is one contiguous copy.  A lane takes one row at a time
+// The tile's histogram lives in LDS as two planes, g then h, each
+// [feature][bin_stride + 1] int64 (dynamic LDS): a plane's words of one
+// feature are adjacent, so the 64-bit atomics of a wavefront spread over the
+// banks by bin, and the one-word pad per feature shifts each feature's bins by
+// one bank pair, so that features spread them too (interleaved (g, h) pairs
+// put a feature's g words 16 bytes apart, on half the bank pairs, and every
+// feature on the same ones: measured 2.2 LDS cycles per atomic instruction of
+// the dense layout's).  The store interleaves the planes into the node
+// histogram's [feature][bin][g, h] layout.  A lane takes one row at a time
 // and walks the row's present values in the tile (two 64-bit LDS atomics
-// each), loading kSparseBatch entries at once.  The lane's rows are
-// software-pipelined: while row i's entries are accumulated, the row id of
-// row i + 2 * 1024 and the entry range and (g, h) of row i + 1024 are in
-// flight.  Per-lane trip counts differ; no barrier sits inside the row loop.
+// each).  The lane's rows are software-pipelined three deep (loads of row
+// i + THREADS's first kSparsePre entries, row i + 2 * THREADS's entry range
+// and (g, h), row i + 3 * THREADS's row id in flight while row i is
+// accumulated), so that a row's dependent loads (row id -> range -> entries)
+// are never waited for in sequence: the row loop is bound by memory latency
+// otherwise (measured on C5's root pass: 75 % of wave cycles waiting, the LDS
+// far from its atomic roof).  Entries past kSparsePre are loaded kSparseBatch
+// at a time.  Per-lane trip counts differ; no barrier sits inside the row loop.
 //
 // EVAL: an item that is its node's only chunk (partial < 0) also evaluates
 // the node from the LDS tile, and its sibling (parent >= 0; the sibling is
@@ -373,6 +384,10 @@ __device__ __forceinline__ void evaluate_tile(const SparseEvalArgs& ev, const Hi
 // (seg_evaluate).  The node's words (and the sibling's) are stored only with
 // ev.store, so on the tree's last split level such a node never leaves LDS.
 constexpr int kSparseBatch = 4;
+// Entries of a row loaded one row ahead: at C5's density (64-feature tiles, 5 %
+// present) a row holds more than 12 present values of a tile in about one
+// wavefront-row in a thousand.
+constexpr int kSparsePre = 12;
 // EVAL's workgroups: 512 threads, so that the evaluation's double arithmetic
 // has 128 registers without spilling while two workgroups share a CU.
 constexpr int kSparseEvalThreads = 512;
@@ -385,62 +400,82 @@ __global__ __launch_bounds__(THREADS) void hist_sparse_kernel(
     const int32_t* __restrict__ n_work_dev, int32_t bin_stride,
     unsigned long long* __restrict__ hist, unsigned long long* __restrict__ partial,
     SparseEvalArgs ev) {
-  extern __shared__ unsigned long long lds_tile[];
+  extern __shared__ unsigned long long lds_tile[];  // g plane, then h plane
   const int32_t n_work = n_work_dev ? *n_work_dev : n_work_host;
   const int64_t slot_words = int64_t(tile_features) * bin_stride * 2;
-  const uint32_t stride = uint32_t(bin_stride);
+  const uint32_t ps = uint32_t(bin_stride) + 1u;        // plane words per feature
+  const uint32_t hoff = uint32_t(tile_features) * ps;  // the h plane's offset
+  const unsigned long long* const lds_h = lds_tile + hoff;
   for (int32_t item = blockIdx.x; item < n_work; item += gridDim.x) {
     const HistWork w = work[item];
     if (w.begin >= w.end) continue;  // padding item (uniform per workgroup)
     const int32_t f0 = w.tile * tile_features;
     const int32_t nf = f0 + tile_features < n_features ? tile_features : n_features - f0;
-    const int32_t words = nf * bin_stride * 2;
-    for (int e = threadIdx.x; e < words; e += THREADS) lds_tile[e] = 0ull;
+    for (int e = threadIdx.x; e < int32_t(2 * hoff); e += THREADS) lds_tile[e] = 0ull;
     __syncthreads();
     const uint32_t* tp = ptr + int64_t(w.tile) * n_rows;
     auto row_of = [&](int64_t i) -> uint32_t {
       return GATHER ? ridx[i] : uint32_t(i);
     };
-    // stage 0: row id of row i2 = i + 2 * 1024; stage 1: range and (g, h) of i1 = i + 1024
-    int64_t i = w.begin + threadIdx.x;
-    uint32_t b = 0, e = 0;
-    int2 q = make_int2(0, 0);
-    if (i < w.end) {
-      const uint32_t r = row_of(i);
-      b = tp[r];
-      e = tp[r + 1];
-      q = gpair[r];
-    }
-    uint32_t r1 = i + THREADS < w.end ? row_of(i + THREADS) : 0;
-    for (; i < w.end; i += THREADS) {
-      const int64_t i1 = i + THREADS, i2 = i + 2 * THREADS;
-      const uint32_t r2 = i2 < w.end ? row_of(i2) : 0;
-      uint32_t b1 = 0, e1 = 0;
-      int2 q1 = make_int2(0, 0);
-      if (i1 < w.end) {
-        b1 = tp[r1];
-        e1 = tp[r1 + 1];
-        q1 = gpair[r1];
+    auto range = [&](int64_t ii, uint32_t r, uint32_t& b, uint32_t& e, int2& q) {
+      if (ii < w.end) {
+        b = tp[r];
+        e = tp[r + 1];
+        q = gpair[r];
+      } else {
+        b = e = 0;
+        q = make_int2(0, 0);
       }
-      const unsigned long long g = (unsigned long long)(long long)q.x;
-      const unsigned long long h = (unsigned long long)(long long)q.y;
-      for (uint32_t j = b; j < e; j += kSparseBatch) {
+    };
+    auto first = [&](uint32_t b, uint32_t e, uint32_t (&v)[kSparsePre]) {
+#pragma unroll
+      for (int k = 0; k < kSparsePre; ++k) v[k] = b + k < e ? entries[b + k] : 0u;
+    };
+    auto add = [&](uint32_t v, unsigned long long g, unsigned long long h) {
+      lds_u64* p = (lds_u64*)lds_tile + ((v >> 8) * ps + (v & 0xffu));
+      lds_add(p, g);
+      lds_add(p + hoff, h);
+    };
+    // Rows i, i + THREADS, ... of this lane, pipelined: while row i is
+    // accumulated, the first entries of row i + THREADS, the range and (g, h)
+    // of row i + 2 * THREADS and the row id of row i + 3 * THREADS are loaded.
+    int64_t i = w.begin + threadIdx.x;
+    uint32_t b0, e0, b1, e1, v0[kSparsePre];
+    int2 q0, q1;
+    range(i, i < w.end ? row_of(i) : 0u, b0, e0, q0);
+    first(b0, e0, v0);
+    range(i + THREADS, i + THREADS < w.end ? row_of(i + THREADS) : 0u, b1, e1, q1);
+    uint32_t r2 = i + 2 * THREADS < w.end ? row_of(i + 2 * THREADS) : 0u;
+    for (; i < w.end; i += THREADS) {
+      const int64_t i2 = i + 2 * THREADS, i3 = i + 3 * THREADS;
+      const uint32_t r3 = i3 < w.end ? row_of(i3) : 0u;
+      uint32_t b2, e2, v1[kSparsePre];
+      int2 q2;
+      range(i2, r2, b2, e2, q2);
+      first(b1, e1, v1);
+      const unsigned long long g = (unsigned long long)(long long)q0.x;
+      const unsigned long long h = (unsigned long long)(long long)q0.y;
+#pragma unroll
+      for (int k = 0; k < kSparsePre; ++k)
+        if (b0 + k < e0) add(v0[k], g, h);
+      // A row with more than kSparsePre present values in the tile: the rest.
+      for (uint32_t j = b0 + kSparsePre; j < e0; j += kSparseBatch) {
         uint32_t v[kSparseBatch];
 #pragma unroll
-        for (int k = 0; k < kSparseBatch; ++k) v[k] = j + k < e ? entries[j + k] : 0u;
+        for (int k = 0; k < kSparseBatch; ++k) v[k] = j + k < e0 ? entries[j + k] : 0u;
 #pragma unroll
-        for (int k = 0; k < kSparseBatch; ++k) {
-          if (j + k < e) {
-            lds_u64* p = (lds_u64*)lds_tile + ((v[k] >> 8) * stride + (v[k] & 0xffu)) * 2u;
-            lds_add(p, g);
-            lds_add(p + 1, h);
-          }
-        }
+        for (int k = 0; k < kSparseBatch; ++k)
+          if (j + k < e0) add(v[k], g, h);
       }
-      b = b1;
-      e = e1;
-      q = q1;
-      r1 = r2;
+      b0 = b1;
+      e0 = e1;
+      q0 = q1;
+#pragma unroll
+      for (int k = 0; k < kSparsePre; ++k) v0[k] = v1[k];
+      b1 = b2;
+      e1 = e2;
+      q1 = q2;
+      r2 = r3;
     }
     __syncthreads();
     const bool direct = w.partial < 0;  // uniform per workgroup
@@ -448,9 +483,13 @@ __global__ __launch_bounds__(THREADS) void hist_sparse_kernel(
         !direct ? partial + int64_t(w.partial) * slot_words
                 : hist + (int64_t(w.slot) * n_features + f0) * bin_stride * 2;
     if (!(EVAL && direct && !ev.store))
-      for (int k = threadIdx.x; k < words; k += THREADS) out[k] = lds_tile[k];
+      for (int k = threadIdx.x; k < nf * bin_stride; k += THREADS) {  // (feature, bin) pairs
+        const int32_t f = k / bin_stride, a = f * int32_t(ps) + (k - f * bin_stride);
+        reinterpret_cast<ulonglong2*>(out)[k] = make_ulonglong2(lds_tile[a], lds_h[a]);
+      }
     if constexpr (EVAL) {
-      if (direct) evaluate_tile<THREADS>(ev, w, f0, nf, n_features, bin_stride, lds_tile, hist);
+      if (direct)
+        evaluate_tile<THREADS>(ev, w, f0, nf, n_features, bin_stride, lds_tile, ps, hoff, hist);
     }
     __syncthreads();  // the next item clears the LDS this item just read
   }
@@ -793,8 +832,8 @@ void launch_hist_sparse(const SparseBins& sp, int64_t n_rows, int32_t n_features
   if (n_work <= 0) return;
   need(sp.n_tiles > 0, "present-value layout not built");
   need(bin_stride >= 1 && bin_stride <= kMaxBins, "histogram bin stride out of range");
-  const size_t lds = size_t(sp.tile_features) * size_t(bin_stride) * 16;
-  need(lds <= size_t(kSparseLdsBytes), "sparse tile exceeds its LDS budget");
+  const size_t lds = size_t(sp.tile_features) * size_t(bin_stride + 1) * 16;  // two planes
+  need(lds <= size_t(kSparseLdsAlloc), "sparse tile exceeds its LDS budget");
   SparseEvalArgs ev{};
   if (eval) {
     need(bin_stride <= 64, "evaluation in the present-value pass needs at most 64 bins");
@@ -815,9 +854,9 @@ void launch_hist_sparse(const SparseBins& sp, int64_t n_rows, int32_t n_features
   static std::once_flag attr_once[4];
   std::call_once(attr_once[(ridx ? 1 : 0) + (eval ? 2 : 0)], [kernel] {
     DP_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, int(kSparseLdsBytes)));
+                               hipFuncAttributeMaxDynamicSharedMemorySize, int(kSparseLdsAlloc)));
   });
-  // Two workgroups per CU (64 KiB of LDS each), a multiple of 8 for the XCD order.
+  // Two workgroups per CU (at most 68 KiB of LDS each), a multiple of 8 for the XCD order.
   int grid = n_work < 1024 ? n_work : 1024;
   grid = (grid + 7) / 8 * 8;
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(eval ? kSparseEvalThreads : kHistThreads), lds, s,
