@@ -734,6 +734,87 @@ def test_c3_full_size_tree(dp, oracle, device):
     _compare(bst, o_trees, o_margin, gpu_positions, n, 1)
 
 
+def _random_case(rng):
+    """One random training problem: matrix shape, value kinds per column (continuous, few
+    distinct integers, constant, mostly zero), missing share, bins, objective, tree and
+    regularisation parameters, rounds, sampling, histogram layout and launch shape."""
+    n = int(rng.choice([1, 2, 3, 17, 100, 640, 2000, 5000, 9000, 40000, 120000]))
+    f = int(rng.choice([1, 2, 5, 15, 16, 17, 33, 70, 130, 300]))
+    if n * f > 1_500_000:
+        f = max(1, 1_500_000 // n)
+    x = np.empty((n, f), dtype=np.float32)
+    for j in range(f):
+        kind = rng.choice(["normal", "ints", "const", "zeros"], p=[0.5, 0.3, 0.05, 0.15])
+        if kind == "normal":
+            x[:, j] = rng.normal(size=n) * rng.choice([1e-3, 1.0, 1e3])
+        elif kind == "ints":
+            x[:, j] = rng.integers(0, int(rng.integers(2, 40)), size=n)
+        elif kind == "const":
+            x[:, j] = 0.5
+        else:
+            x[:, j] = np.where(rng.random(n) < 0.8, 0.0, rng.random(n))
+    missing = float(rng.choice([0.0, 0.0, 0.1, 0.5, 0.95]))
+    if missing > 0:
+        x[rng.random((n, f)) < missing] = np.nan
+    objective = int(rng.integers(0, 3))
+    k = int(rng.integers(2, 5)) if objective == 1 else 1
+    z = np.nan_to_num(x, nan=0.0) @ rng.normal(size=(f, k)).astype(np.float32)
+    z = z / (np.abs(z).max() + 1e-6) * 3 + rng.normal(size=(n, k)).astype(np.float32)
+    if objective == 0:
+        y = (z[:, 0] > 0).astype(np.float32)
+    elif objective == 1:
+        y = z.argmax(axis=1).astype(np.float32)
+    else:
+        y = z[:, 0].astype(np.float32)
+    p = {"max_depth": int(rng.integers(1, 11)), "eta": float(rng.choice([0.1, 0.3, 1.0])),
+         "lam": float(rng.choice([0.0, 1.0, 5.0])), "alpha": float(rng.choice([0.0, 0.5])),
+         "gamma": float(rng.choice([0.0, 0.2])),
+         "min_child_weight": float(rng.choice([0.0, 1.0, 4.0]))}
+    extra = {"dp_graphs": int(rng.integers(0, 2)),
+             "dp_sparse_hist": int(rng.choice([0, 1, 2])) if missing > 0 else 0,
+             "dp_hist_tiles": int(rng.choice([0, 1, 2])),
+             "dp_hist_unroll": int(rng.choice([0, 1, 2])),
+             "dp_hist_split": int(rng.choice([0, 4, 5]))}
+    if missing == 0:
+        extra["dp_skip_bin"] = int(rng.choice([0, 1, 2]))
+    if objective == 1:
+        extra["dp_concurrent_trees"] = int(rng.choice([1, 3]))
+    sample = None
+    if rng.random() < 0.3:
+        sample = {"seed": int(rng.integers(0, 1000))}
+        for key in ("subsample", "bytree", "bylevel", "bynode"):
+            if rng.random() < 0.5:
+                sample[key] = float(rng.choice([0.5, 0.8]))
+    case = {"n": n, "f": f, "missing": missing, "objective": objective, "k": k,
+            "max_bin": int(rng.choice([2, 3, 7, 16, 63, 64, 65, 128, 255, 256])),
+            "rounds": int(rng.integers(1, 4)), "p": p, "extra": extra, "sample": sample}
+    return x, y, case
+
+
+def test_random_problems_match_the_oracle(dp, oracle, device):
+    """A hundred seeded random problems -- 1 to 120,000 rows, 1 to 300 features of mixed kinds
+    (tied integers, constants, mostly-zero columns), 0-95 % missing, 2-256 bins, every
+    objective, depth 1-10, random regularisation, sampling, histogram layout, skip bins,
+    launch shape and graph use -- each trained for 1-3 rounds against the oracle's booster:
+    split records, row counts, leaf values, row positions and margins, bit for bit."""
+    import torch
+
+    rng = np.random.default_rng(20261202)
+    grown = 0
+    for t in range(100):
+        x, y, case = _random_case(rng)
+        print(f"[booster] random problem {t}: {case}", flush=True)
+        values = torch.from_numpy(x).to(device)
+        labels = torch.from_numpy(y).to(device)
+        bst, _, o_trees, o_margin, pos, n = _train_both(
+            dp, oracle, device, 1, case["n"], case["f"], case["objective"], case["k"], case["p"],
+            case["rounds"], 0, max_bin=case["max_bin"], extra=case["extra"],
+            sample=case["sample"], values_labels=(values, labels))
+        _compare(bst, o_trees, o_margin, pos, n, case["k"])
+        grown += any(bool((ot["left"] != -1).any()) for ot in o_trees)
+    assert grown >= 60, f"only {grown} of 100 problems grew a split"
+
+
 def test_strided_label_interface_is_refused(dp, device):
     """A label array interface with strides is copied as one contiguous block, so strides must
     be the C-contiguous ones: a column slice of an [n, 2] array ([n, 1] with a row stride of 8
