@@ -796,7 +796,8 @@ def test_random_problems_match_the_oracle(dp, oracle, device):
     (tied integers, constants, mostly-zero columns), 0-95 % missing, 2-256 bins, every
     objective, depth 1-10, random regularisation, sampling, histogram layout, skip bins,
     launch shape and graph use -- each trained for 1-3 rounds against the oracle's booster:
-    split records, row counts, leaf values, row positions and margins, bit for bit."""
+    split records, row counts, leaf values, row positions and margins, bit for bit, and the
+    predictor's margins over the raw values equal to them."""
     import torch
 
     rng = np.random.default_rng(20261202)
@@ -811,6 +812,10 @@ def test_random_problems_match_the_oracle(dp, oracle, device):
             case["rounds"], 0, max_bin=case["max_bin"], extra=case["extra"],
             sample=case["sample"], values_labels=(values, labels))
         _compare(bst, o_trees, o_margin, pos, n, case["k"])
+        # the predictor, walking the saved trees on the raw values, gives the same margins
+        pm = bst.predict(values, margin=True).cpu().numpy()
+        np.testing.assert_array_equal(pm.reshape(o_margin.shape).view(np.uint32),
+                                      o_margin.view(np.uint32))
         grown += any(bool((ot["left"] != -1).any()) for ot in o_trees)
     assert grown >= 60, f"only {grown} of 100 problems grew a split"
 
