@@ -308,6 +308,91 @@ def test_split_evaluation_bit_exact(dp, oracle, ws, device, config, f, max_bin):
             assert (rec[i]["gl"], rec[i]["hl"]) == (o["gl"], o["hl"])
 
 
+def test_random_operator_calls_match_the_oracle(dp, oracle, ws, device):
+    """Forty seeded random inputs through the C ABI, one operator after another, each against
+    the oracle: cuts and bins (mixed value kinds, missing values, 2-256 bins), the quantiser,
+    histograms of random row sets (contiguous or gathered, empty sets included),
+    accumulation, subtraction, split evaluation under random regularisation, and the
+    partition of every row set by its own chosen split."""
+    import torch
+    from dpgbdt import ops
+
+    rng = np.random.default_rng(20261203)
+    for t in range(40):
+        n = int(rng.choice([1, 5, 100, 3000, 20000, 70000]))
+        f = int(rng.choice([1, 3, 16, 17, 40, 130]))
+        max_bin = int(rng.choice([2, 16, 64, 200, 256]))
+        missing = float(rng.choice([0.0, 0.0, 0.3]))
+        gather = bool(rng.integers(0, 2))
+        print(f"[kernels] random call {t}: {n} x {f}, max_bin {max_bin}, missing {missing}, "
+              f"gather {gather}", flush=True)
+        x = np.empty((n, f), dtype=np.float32)
+        for j in range(f):
+            if rng.random() < 0.5:
+                x[:, j] = rng.normal(size=n)
+            else:
+                x[:, j] = rng.integers(0, int(rng.integers(1, 30)), size=n)
+        if missing > 0:
+            x[rng.random((n, f)) < missing] = np.nan
+        values = torch.as_tensor(x, device=device)
+        lay, bins, o_bins, cut_ptr, cuts, n_bins, mb = _prepare(dp, oracle, ws, values, max_bin)
+        stride = max(1, int(n_bins.max()))
+        g = (rng.normal(size=n) * rng.choice([1e-4, 1.0, 1e4])).astype(np.float32)
+        h = (rng.random(size=n) * rng.choice([1e-3, 1.0, 50.0])).astype(np.float32)
+        (eg, eh), gpair, _ = _gpair(ws, device, g, h)
+        q = oracle.quantise(g, h)[0]
+        assert (eg, eh) == (q[0], q[1])
+        gp = gpair.cpu().numpy().reshape(n, 2)
+        np.testing.assert_array_equal(gp[:, 0], q[2])
+        np.testing.assert_array_equal(gp[:, 1], q[3])
+        ridx = rng.permutation(n).astype(np.uint32) if gather else np.arange(n, dtype=np.uint32)
+        d_ridx = torch.as_tensor(ridx.view(np.int32), device=device)
+        bounds = [0, *sorted(int(v) for v in rng.integers(0, n + 1, size=int(rng.integers(1, 6)))), n]
+        segs = [(bounds[i], bounds[i + 1]) for i in range(len(bounds) - 1)]
+        hist = ops.hist_build(ws, bins, lay, gpair, segs, stride, ridx=d_ridx if gather else None)
+        hn_ = hist.cpu().numpy()
+        refs = [oracle.hist(o_bins, q[2], q[3], rows=ridx[b:e], bin_stride=stride, missing_bin=mb)
+                for b, e in segs]
+        for i in range(len(segs)):
+            np.testing.assert_array_equal(hn_[i], refs[i], err_msg=f"histogram {i} of {segs}")
+        twice = ops.hist_accumulate(ws, bins, lay, gpair, segs, hist.clone(),
+                                    ridx=d_ridx if gather else None)
+        np.testing.assert_array_equal(twice.cpu().numpy(), 2 * hn_)
+        parent = ops.hist_build(ws, bins, lay, gpair, [(0, n)], stride)
+        rest = oracle.hist(o_bins, q[2], q[3], rows=ridx[segs[0][1]:], bin_stride=stride,
+                           missing_bin=mb)
+        np.testing.assert_array_equal(ops.hist_subtract(parent[0], hist[0]).cpu().numpy(), rest)
+        sums = [(int(q[2][ridx[b:e]].astype(np.int64).sum()),
+                 int(q[3][ridx[b:e]].astype(np.int64).sum())) for b, e in segs]
+        prm = {"lam": float(rng.choice([0.0, 1.0, 3.0])), "alpha": float(rng.choice([0.0, 0.3])),
+               "gamma": float(rng.choice([0.0, 0.5])),
+               "min_child_weight": float(rng.choice([0.0, 1.0, 5.0]))}
+        d_rec = ops.evaluate_splits(ws, hist, torch.as_tensor(n_bins, device=device),
+                                    torch.as_tensor(np.array(sums, dtype=np.int64), device=device),
+                                    eg, eh, ops.train_param(**prm))
+        rec = ops.splits_to_numpy(d_rec)
+        p = oracle.params(**prm)
+        for i in range(len(segs)):
+            o = oracle.evaluate_split(refs[i], n_bins, sums[i][0], sums[i][1], eg, eh, p)
+            assert rec[i]["valid"] == o["valid"], f"split {i}"
+            if not o["valid"]:
+                continue
+            assert (rec[i]["feature"], rec[i]["bin"], rec[i]["default_left"]) == \
+                (o["feature"], o["bin"], o["default_left"]), f"split {i}"
+            assert np.float64(rec[i]["loss_chg"]).tobytes() == np.float64(o["loss_chg"]).tobytes()
+            assert (rec[i]["gl"], rec[i]["hl"]) == (o["gl"], o["hl"])
+        out, left = ops.partition(ws, bins, lay, d_ridx, segs, d_rec)
+        out, left = out.cpu().numpy().view(np.uint32), left.cpu().numpy()
+        for i, (b, e) in enumerate(segs):
+            if not rec[i]["expand"]:
+                assert left[i] == 0
+                continue
+            part, nl = oracle.partition(ridx, b, e, o_bins, int(rec[i]["feature"]),
+                                        int(rec[i]["bin"]), int(rec[i]["default_left"]), mb)
+            assert left[i] == nl, f"partition {i}"
+            np.testing.assert_array_equal(out[b:e], part[b:e], err_msg=f"partition {i}")
+
+
 # 4,300,000 rows: matrices of 4M rows or more take the partition kernels that
 # load four 256-row steps per group (one step per group below).
 @pytest.mark.parametrize("n,f", [(30000, 200), (4_300_000, 24)])
