@@ -734,12 +734,18 @@ def test_c3_full_size_tree(dp, oracle, device):
     _compare(bst, o_trees, o_margin, gpu_positions, n, 1)
 
 
-def _random_case(rng):
+def _random_case(rng, large=False):
     """One random training problem: matrix shape, value kinds per column (continuous, few
     distinct integers, constant, mostly zero), missing share, bins, objective, tree and
-    regularisation parameters, rounds, sampling, histogram layout and launch shape."""
-    n = int(rng.choice([1, 2, 3, 17, 100, 640, 2000, 5000, 9000, 40000, 120000]))
-    f = int(rng.choice([1, 2, 5, 15, 16, 17, 33, 70, 130, 300]))
+    regularisation parameters, rounds, sampling, histogram layout and launch shape.  large:
+    200,000 to 1,000,000 rows of at most 40 features, depth up to 17 (level-synced growth
+    past the device planner's levels), up to 10 classes."""
+    if large:
+        n = int(rng.choice([200000, 500000, 1000000]))
+        f = int(rng.choice([1, 5, 17, 28, 40]))
+    else:
+        n = int(rng.choice([1, 2, 3, 17, 100, 640, 2000, 5000, 9000, 40000, 120000]))
+        f = int(rng.choice([1, 2, 5, 15, 16, 17, 33, 70, 130, 300]))
     if n * f > 1_500_000:
         f = max(1, 1_500_000 // n)
     x = np.empty((n, f), dtype=np.float32)
@@ -757,7 +763,7 @@ def _random_case(rng):
     if missing > 0:
         x[rng.random((n, f)) < missing] = np.nan
     objective = int(rng.integers(0, 3))
-    k = int(rng.integers(2, 5)) if objective == 1 else 1
+    k = int(rng.integers(2, 11 if large else 5)) if objective == 1 else 1
     z = np.nan_to_num(x, nan=0.0) @ rng.normal(size=(f, k)).astype(np.float32)
     z = z / (np.abs(z).max() + 1e-6) * 3 + rng.normal(size=(n, k)).astype(np.float32)
     if objective == 0:
@@ -766,7 +772,8 @@ def _random_case(rng):
         y = z.argmax(axis=1).astype(np.float32)
     else:
         y = z[:, 0].astype(np.float32)
-    p = {"max_depth": int(rng.integers(1, 11)), "eta": float(rng.choice([0.1, 0.3, 1.0])),
+    p = {"max_depth": int(rng.integers(1, 18 if large else 11)),
+         "eta": float(rng.choice([0.1, 0.3, 1.0])),
          "lam": float(rng.choice([0.0, 1.0, 5.0])), "alpha": float(rng.choice([0.0, 0.5])),
          "gamma": float(rng.choice([0.0, 0.2])),
          "min_child_weight": float(rng.choice([0.0, 1.0, 4.0]))}
@@ -791,19 +798,14 @@ def _random_case(rng):
     return x, y, case
 
 
-def test_random_problems_match_the_oracle(dp, oracle, device):
-    """A hundred seeded random problems -- 1 to 120,000 rows, 1 to 300 features of mixed kinds
-    (tied integers, constants, mostly-zero columns), 0-95 % missing, 2-256 bins, every
-    objective, depth 1-10, random regularisation, sampling, histogram layout, skip bins,
-    launch shape and graph use -- each trained for 1-3 rounds against the oracle's booster:
-    split records, row counts, leaf values, row positions and margins, bit for bit, and the
-    predictor's margins over the raw values equal to them."""
+def _random_problems(dp, oracle, device, seed, count, large=False):
+    """Trains `count` random problems against the oracle; returns how many grew a split."""
     import torch
 
-    rng = np.random.default_rng(20261202)
+    rng = np.random.default_rng(seed)
     grown = 0
-    for t in range(100):
-        x, y, case = _random_case(rng)
+    for t in range(count):
+        x, y, case = _random_case(rng, large)
         print(f"[booster] random problem {t}: {case}", flush=True)
         values = torch.from_numpy(x).to(device)
         labels = torch.from_numpy(y).to(device)
@@ -817,7 +819,32 @@ def test_random_problems_match_the_oracle(dp, oracle, device):
         np.testing.assert_array_equal(pm.reshape(o_margin.shape).view(np.uint32),
                                       o_margin.view(np.uint32))
         grown += any(bool((ot["left"] != -1).any()) for ot in o_trees)
+    return grown
+
+
+def test_random_problems_match_the_oracle(dp, oracle, device):
+    """A hundred seeded random problems -- 1 to 120,000 rows, 1 to 300 features of mixed kinds
+    (tied integers, constants, mostly-zero columns), 0-95 % missing, 2-256 bins, every
+    objective, depth 1-10, random regularisation, sampling, histogram layout, skip bins,
+    launch shape and graph use -- each trained for 1-3 rounds against the oracle's booster:
+    split records, row counts, leaf values, row positions and margins, bit for bit, and the
+    predictor's margins over the raw values equal to them."""
+    grown = _random_problems(dp, oracle, device, 20261202, 100)
     assert grown >= 60, f"only {grown} of 100 problems grew a split"
+
+
+def test_random_large_problems_match_the_oracle(dp, oracle, device):
+    """Twenty seeded random problems of 200,000 to 1,000,000 rows, depth up to 17 and up to
+    10 classes (the rest as in the small ones), against the oracle's booster on all host
+    threads."""
+    import os
+
+    oracle.set_threads(len(os.sched_getaffinity(0)))
+    try:
+        grown = _random_problems(dp, oracle, device, 4242, 20, large=True)
+    finally:
+        oracle.set_threads(1)
+    assert grown >= 15, f"only {grown} of 20 problems grew a split"
 
 
 def test_strided_label_interface_is_refused(dp, device):
