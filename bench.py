@@ -511,8 +511,11 @@ def main():
                    "rows": hist["n"], "features": hist["f"], "max_bin": 256,
                    "bin_stride": hist["stride"], "parallelism": "single GPU"},
         "pct_hbm_peak": 100.0 * hist["achieved_gbs"] / HBM_PEAK_GBS,
-        "roofline": {"bound": "hbm", "achieved": hist["achieved_gbs"], "peak": HBM_PEAK_GBS,
+        "roofline": {"bound": "lds", "achieved": hist["achieved_gbs"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": hist["achieved_gbs"] / HBM_PEAK_GBS,
+                     "bound_note": "the kernel is bound by its LDS atomics (two exact int64 "
+                                   "adds per element; lds_atomic_roof below); achieved, peak "
+                                   "and frac are its HBM figures",
                      "traffic": traffic,
                      "traffic_source": traffic_source,
                      "kernel": "dp_hist_accumulate = dp::hist_kernel<false, 0, tiles, unroll, "

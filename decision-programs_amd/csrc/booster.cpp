@@ -764,6 +764,7 @@ Booster::~Booster() {
   for (hipStream_t t : tree_streams_) (void)hipStreamDestroy(t);
   for (hipEvent_t e : tree_done_) (void)hipEventDestroy(e);
   if (fork_) (void)hipEventDestroy(fork_);
+  if (caller_read_) (void)hipEventDestroy(caller_read_);
   if (stream_) (void)hipStreamDestroy(stream_);
 }
 
@@ -933,6 +934,10 @@ void Booster::configure(DMatrix* d) {
   grad_.resize(size_t(N) * n_groups_);
   hess_.resize(size_t(N) * n_groups_);
   gpair_.resize(size_t(N) * n_groups_ * 2);
+  // The autotuner times the first round's histogram passes on gpair_ before
+  // that round's quantiser writes it: zero it once so the timing passes read
+  // defined values (their sums are discarded either way).
+  launch_fill_u8(reinterpret_cast<uint8_t*>(gpair_.p), int64_t(gpair_.bytes()), 0, stream_);
   exps_.resize(size_t(2 * n_groups_));
   quant_scratch_.resize(quantise_scratch_bytes(N, n_groups_));
   std::vector<float> init(static_cast<size_t>(n_groups_));
@@ -978,18 +983,16 @@ void Booster::train_one_iter(DMatrix* d, int iter, const float* grad, const floa
   configure(d);
   need(n == d->n_rows && k == n_groups_, "gradient shape differs from [rows, outputs]");
   need(grad && hess, "null gradient buffer");
-  // The round's quantiser reads the caller's buffers (their pointers go to
-  // device memory ahead of the round, so its graph is the same every round);
-  // like every launch of the round they are read in stream order.
-  const uint64_t src[2] = {reinterpret_cast<uint64_t>(grad), reinterpret_cast<uint64_t>(hess)};
-  if (!gradient_src_.p || src[0] != gradient_src_host_[0] || src[1] != gradient_src_host_[1]) {
-    gradient_src_.reserve(2);
-    launch_store_u64x2(gradient_src_.p, src[0], src[1], stream_);
-    gradient_src_host_[0] = src[0];
-    gradient_src_host_[1] = src[1];
-  }
+  // The round's quantiser reads the caller's buffers in place, in stream
+  // order after the previous round, and the call returns once it has run: the
+  // caller may then overwrite them from any stream, as upstream's call, which
+  // consumes the gradients before it returns, allows.
+  caller_grad_ = grad;
+  caller_hess_ = hess;
   caller_gradients_ = true;
+  if (!caller_read_) DP_HIP(hipEventCreateWithFlags(&caller_read_, hipEventDisableTiming));
   run_round(d, false);
+  DP_HIP(hipEventSynchronize(caller_read_));
 }
 
 void Booster::enqueue(const std::vector<uint64_t>& key, bool capturable,
@@ -1155,8 +1158,7 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
       reinterpret_cast<uint64_t>(q.rows.p), reinterpret_cast<uint64_t>(q.d_nbins.p),
       uint64_t(q.bin_stride), uint64_t(N), reinterpret_cast<uint64_t>(d->labels.p),
       uint64_t(objective_id_), uint64_t(n_groups_), reinterpret_cast<uint64_t>(margin_.p),
-      reinterpret_cast<uint64_t>(leaf_values_.p), reinterpret_cast<uint64_t>(gradient_src_.p),
-      reinterpret_cast<uint64_t>(grad_.p), reinterpret_cast<uint64_t>(hess_.p),
+      reinterpret_cast<uint64_t>(leaf_values_.p), reinterpret_cast<uint64_t>(grad_.p), reinterpret_cast<uint64_t>(hess_.p),
       reinterpret_cast<uint64_t>(gpair_.p), reinterpret_cast<uint64_t>(exps_.p),
       reinterpret_cast<uint64_t>(quant_scratch_.p),
       reinterpret_cast<uint64_t>(positions), reinterpret_cast<uint64_t>(q.sparse.ptr.p),
@@ -1182,18 +1184,26 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
   // values_pending_ says so, and margins() adds them when asked first.
   const bool add_first = values_pending_ && !with_gradients;  // caller gradients follow
   key.push_back(uint64_t(values_pending_) | uint64_t(with_gradients) << 1);
+  // The per-workgroup sums stay in the quantiser's slots: each tree's first
+  // launch adds up its output's.  Caller gradients are quantised by direct
+  // launches ahead of the round's graph, so that the call can wait for their
+  // last read (caller_read_) without waiting for the trees.
+  if (!with_gradients) {
+    launch_quantise(caller_grad_, caller_hess_, N, K, quant_scratch_.p, false, exps_.p,
+                    gpair_.p, nullptr, stream_, rows);
+    DP_HIP(hipEventRecord(caller_read_, stream_));
+  }
   enqueue(key, eager, [&] {
-    bool maxima = false;
     if (add_first) launch_add_leaf_values(margin_.p, K, leaf_values_.p, N, stream_);
-    // With row sampling the quantiser takes the maxima over the kept rows.
-    if (with_gradients)
-      maxima = launch_gradients(objective_id_, margin_.p, d->labels.p, N, K, grad_.p, hess_.p,
-                                rows.active() ? nullptr : quant_scratch_.p, stream_,
-                                values_pending_ ? leaf_values_.p : nullptr);
-    // The per-workgroup sums stay in the quantiser's slots: each tree's first
-    // launch adds up its output's.
-    launch_quantise(grad_.p, hess_.p, N, K, quant_scratch_.p, maxima, exps_.p, gpair_.p, nullptr,
-                    stream_, rows, with_gradients ? nullptr : gradient_src_.p);
+    if (with_gradients) {
+      // With row sampling the quantiser takes the maxima over the kept rows.
+      const bool maxima =
+          launch_gradients(objective_id_, margin_.p, d->labels.p, N, K, grad_.p, hess_.p,
+                           rows.active() ? nullptr : quant_scratch_.p, stream_,
+                           values_pending_ ? leaf_values_.p : nullptr);
+      launch_quantise(grad_.p, hess_.p, N, K, quant_scratch_.p, maxima, exps_.p, gpair_.p,
+                      nullptr, stream_, rows);
+    }
     const int32_t blocks = quantise_blocks(N);
     const int64_t* slots = quantise_sum_slots(quant_scratch_.p, N, K);
     auto sample_columns = [&](Grower& g, int32_t k) {

@@ -199,6 +199,12 @@ class Booster {
     flush();
     return rounds_;
   }
+  // num_feature of the trained or loaded model, else of the first training
+  // matrix (XGBoosterGetNumFeature); 0 with neither.
+  int64_t num_features() const {
+    if (configured_ || model_only_) return n_features_;
+    return cache_.empty() || !cache_[0] ? 0 : cache_[0]->n_features;
+  }
   std::string save_config() const;
   std::string save_model() const;
   const std::vector<Tree>& trees() const {
@@ -260,10 +266,12 @@ class Booster {
   PooledBuffer<uint8_t> quant_scratch_;  // quantiser reduction slots
   PooledBuffer<int32_t> positions_;
   PooledBuffer<int32_t> round_dev_;  // the round's index, read by the sampling kernels
-  // The caller's (grad, hess) pointers of an XGBoosterTrainOneIter round,
-  // stored before the round and read by its quantiser (no copy is made).
-  PooledBuffer<uint64_t> gradient_src_;
-  uint64_t gradient_src_host_[2] = {0, 0};  // what gradient_src_ holds (stored in stream order)
+  // The caller's (grad, hess) buffers of an XGBoosterTrainOneIter round: its
+  // quantiser reads them in place, launched outside the round's graph, and
+  // caller_read_ (recorded after it) is waited on before the call returns.
+  const float* caller_grad_ = nullptr;
+  const float* caller_hess_ = nullptr;
+  hipEvent_t caller_read_ = nullptr;
   bool caller_gradients_ = false;  // the last round's gradients came from the caller
   mutable std::vector<int32_t> last_exps_;
   bool record_positions_ = false;

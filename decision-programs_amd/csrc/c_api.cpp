@@ -82,6 +82,35 @@ BoosterObj& bo(BoosterHandle h) {
 
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Kernels read these caller arrays in place, so a host, freed or foreign
+// pointer would fault the GPU instead of failing the call: the array must be
+// device memory of the current device (or managed memory), and `bytes` from p
+// must lie inside its allocation.  The errors the queries leave on a refused
+// pointer are cleared, so no later call reports them.
+void require_device_array(uintptr_t p, size_t bytes, const char* what) {
+  dp::need(p != 0, std::string(what) + " is a null pointer");
+  hipPointerAttribute_t attr{};
+  const hipError_t e = hipPointerGetAttributes(&attr, reinterpret_cast<const void*>(p));
+  if (e != hipSuccess) (void)hipGetLastError();
+  const bool managed = e == hipSuccess && (attr.type == hipMemoryTypeManaged || attr.isManaged);
+  dp::need(e == hipSuccess && (attr.type == hipMemoryTypeDevice || managed),
+           std::string(what) + " must be device memory (a HIP device or managed allocation)");
+  if (managed) return;
+  int device = 0;
+  DP_HIP(hipGetDevice(&device));
+  dp::need(attr.device == device, std::string(what) + " belongs to device " +
+                                      std::to_string(attr.device) + ", not the current device " +
+                                      std::to_string(device));
+  hipDeviceptr_t base = nullptr;
+  size_t size = 0;
+  const hipError_t r = hipMemGetAddressRange(&base, &size, reinterpret_cast<hipDeviceptr_t>(p));
+  if (r != hipSuccess) (void)hipGetLastError();
+  const uintptr_t b = reinterpret_cast<uintptr_t>(base);
+  dp::need(r == hipSuccess && p >= b && p - b <= size && bytes <= size - (p - b),
+           std::string(what) + ": " + std::to_string(bytes) +
+               " bytes from the pointer exceed its device allocation");
+}
+
 // Copies a float32 device array interface of shape [n] or [n, k] into dst.
 void copy_float_array(const ArrayInterface& a, int64_t n, int64_t k, float* dst) {
   dp::need(a.typestr == "<f4", "array interface must be little-endian float32 (<f4)");
@@ -206,6 +235,7 @@ int XGDMatrixCreateFromCudaArrayInterface(const char* data, const char* config,
                "unsupported matrix strides");
       row_stride = a.strides[0] / 4;
     }
+    require_device_array(a.data, sizeof(float) * size_t((n - 1) * row_stride + f), "matrix data");
     auto obj = std::make_unique<DMatrixObj>();
     obj->m.n_rows = n;
     obj->m.n_features = int32_t(f);
@@ -284,6 +314,10 @@ int XGBoosterTrainOneIter(BoosterHandle handle, DMatrixHandle dtrain, int iter, 
     dp::need(g.strides.empty() && h.strides.empty(), "gradients must be C-contiguous");
     const int64_t n = g.shape[0];
     const int32_t k = g.shape.size() == 2 ? int32_t(g.shape[1]) : 1;
+    dp::need(n > 0 && k > 0 && n <= INT64_MAX / 4 / k, "gradient shape out of range");
+    // The round's quantiser reads both arrays in place.
+    require_device_array(g.data, sizeof(float) * size_t(n) * size_t(k), "grad");
+    require_device_array(h.data, sizeof(float) * size_t(n) * size_t(k), "hess");
     bo(handle).b->train_one_iter(&dm(dtrain), iter, reinterpret_cast<const float*>(g.data),
                                  reinterpret_cast<const float*>(h.data), n, k);
   });
@@ -356,6 +390,10 @@ int XGBoosterPredictFromCudaArray(BoosterHandle handle, const char* values, cons
       if (const auto* v = c.find("strict_shape")) req.strict_shape = v->boolean;
       if (const auto* v = c.find("missing")) req.missing = float(v->number());
     }
+    if (req.rows > 0 && req.features > 0)
+      require_device_array(a.data,
+                           sizeof(float) * size_t((req.rows - 1) * req.row_stride + req.features),
+                           "prediction input");
     std::vector<uint64_t> shape;
     *out_result = b.b->predict(req, shape);
     b.shape.assign(shape.begin(), shape.end());
@@ -378,6 +416,13 @@ int XGBoosterLoadModel(BoosterHandle handle, const char* fname) {
     dp::need(bool(f), std::string("cannot open ") + fname);
     std::string text((std::istreambuf_iterator<char>(f)), std::istreambuf_iterator<char>());
     bo(handle).b->load_model(text);
+  });
+}
+
+int XGBoosterGetNumFeature(BoosterHandle handle, bst_ulong* out) {
+  return guarded([&] {
+    dp::need(out != nullptr, "null output pointer");
+    *out = bst_ulong(bo(handle).b->num_features());
   });
 }
 
@@ -564,14 +609,21 @@ void hist_call(dp_workspace ws, const uint8_t* bins, const dp_bin_layout* layout
     dp::need(ridx != nullptr || end[i] <= layout->n_rows, "row range beyond the matrix");
     total += end[i] - begin[i];
   }
-  (void)total;
   hipStream_t s = as_stream(stream);
   // Contiguous row ranges take the launch shape the autotuner chose for this
-  // matrix shape (timed on these bins once per process; synchronises the
-  // stream that first time); gathered calls read the tile-major bins and keep
-  // the default shape.
+  // matrix shape.  The first such call of a shape that covers at least
+  // kTuneMinRows rows times the candidates on these bins (once per process:
+  // it allocates, launches about 200 timing passes and synchronises the
+  // stream); smaller calls use the shape tuned already, else the defaults.
+  // Gathered calls read the tile-major bins and keep the default shape.
+  constexpr int64_t kTuneMinRows = int64_t(1) << 18;
   dp::HistConfig cfg;
-  if (!ridx) cfg = dp::tune_dense_hist(*layout, bins, nullptr, bin_stride, gpair, s).root;
+  if (!ridx) {
+    if (const dp::HistTuning* t = dp::find_dense_tuning(*layout, bin_stride, false))
+      cfg = t->root;
+    else if (total >= kTuneMinRows)
+      cfg = dp::tune_dense_hist(*layout, bins, nullptr, bin_stride, gpair, s).root;
+  }
   std::vector<dp::HistWork> work;
   std::vector<dp::HistReduce> jobs;
   // Overwriting builds let single-chunk nodes store their histogram directly;

@@ -651,17 +651,11 @@ const int64_t* quantise_sum_slots(const void* scratch, int64_t n_rows, int32_t n
 size_t quantise_scratch_bytes(int64_t n_rows, int32_t n_classes);
 // rows: row sampling of the round (inactive by default): a dropped row's
 // (g, h) count as zero in the maxima, the pairs and the sums of its class.
-// src: when set (device memory holding two pointers, stored before the
-// launch), the gradients are read from src[0] and src[1] instead of grad and
-// hess, so a captured quantiser reads whatever buffers the round's caller gave.
 void launch_quantise(const float* grad, const float* hess, int64_t n_rows, int32_t n_classes,
                      void* scratch, bool maxima_ready, int32_t* exps, int32_t* gpair,
-                     int64_t* sums, hipStream_t s, const RowSample& rows = RowSample{},
-                     const uint64_t* src = nullptr);
+                     int64_t* sums, hipStream_t s, const RowSample& rows = RowSample{});
 // *p = value (one thread), e.g. the round index the sampling kernels read.
 void launch_store_i32(int32_t* p, int32_t value, hipStream_t s);
-// p[0] = a, p[1] = b (one thread), e.g. the gradient pointers of a round.
-void launch_store_u64x2(uint64_t* p, uint64_t a, uint64_t b, hipStream_t s);
 
 void launch_bin_values(const float* values, const dp_bin_layout& layout, const int32_t* cut_ptr,
                        const float* cut_values, uint8_t* bins, hipStream_t s);

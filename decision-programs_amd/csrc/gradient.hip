@@ -131,19 +131,9 @@ __device__ __forceinline__ bool row_kept(const RowSample& rs, uint64_t prefix, i
   return !rs.active() || uint64_t(sample_draw(prefix, uint64_t(r))) < rs.threshold;
 }
 
-// src: when set, the (grad, hess) pointers are read from it (device memory
-// the host stores before the launch), so a captured launch serves any buffers.
-__device__ __forceinline__ void gradient_source(const uint64_t* src, const float*& grad,
-                                                const float*& hess) {
-  if (!src) return;
-  grad = reinterpret_cast<const float*>(src[0]);
-  hess = reinterpret_cast<const float*>(src[1]);
-}
-
 __global__ __launch_bounds__(kQuantThreads) void absmax_kernel(
-    const float* grad, const float* hess, int64_t n_rows, int n_classes,
-    unsigned* __restrict__ max_slots, RowSample rs, const uint64_t* __restrict__ src) {
-  gradient_source(src, grad, hess);
+    const float* __restrict__ grad, const float* __restrict__ hess, int64_t n_rows,
+    int n_classes, unsigned* __restrict__ max_slots, RowSample rs) {
   const int k = blockIdx.y;
   const uint64_t prefix = row_prefix(rs, k);
   unsigned mg = 0, mh = 0;
@@ -172,13 +162,11 @@ __device__ __forceinline__ int quant_exp(unsigned bits) {
 // Reduces class blockIdx.y's maxima slots, quantises its rows and writes this
 // workgroup's sums to the sum slots.
 __global__ __launch_bounds__(kQuantThreads) void quantise_kernel(
-    const float* grad, const float* hess, int64_t n_rows, int n_classes,
-    const unsigned* __restrict__ max_slots, int32_t* __restrict__ exps,
-    int2* __restrict__ gpair, long long* __restrict__ sum_slots, RowSample rs,
-    const uint64_t* __restrict__ src) {
+    const float* __restrict__ grad, const float* __restrict__ hess, int64_t n_rows,
+    int n_classes, const unsigned* __restrict__ max_slots, int32_t* __restrict__ exps,
+    int2* __restrict__ gpair, long long* __restrict__ sum_slots, RowSample rs) {
   __shared__ long long wave_sum[2][kQuantThreads / 64];
   __shared__ int s_exp[2];
-  gradient_source(src, grad, hess);
   const int k = blockIdx.y;
   unsigned mg = 0, mh = 0;
   const unsigned* slots = max_slots + int64_t(k) * gridDim.x * 2;
@@ -348,22 +336,10 @@ void launch_store_i32(int32_t* p, int32_t value, hipStream_t s) {
   DP_HIP(hipGetLastError());
 }
 
-__global__ void store_u64x2_kernel(uint64_t* p, uint64_t a, uint64_t b) {
-  p[0] = a;
-  p[1] = b;
-}
-
-void launch_store_u64x2(uint64_t* p, uint64_t a, uint64_t b, hipStream_t s) {
-  hipLaunchKernelGGL(store_u64x2_kernel, dim3(1), dim3(1), 0, s, p, a, b);
-  DP_HIP(hipGetLastError());
-}
-
 void launch_quantise(const float* grad, const float* hess, int64_t n_rows, int32_t n_classes,
                      void* scratch, bool maxima_ready, int32_t* exps, int32_t* gpair,
-                     int64_t* sums, hipStream_t s, const RowSample& rows,
-                     const uint64_t* src) {
+                     int64_t* sums, hipStream_t s, const RowSample& rows) {
   need(!rows.active() || rows.round != nullptr, "row sampling needs the device round index");
-  need(!(src && maxima_ready), "gradients read through src take their maxima here");
   need(!(rows.active() && maxima_ready), "row sampling needs the sampled maxima");
   need(n_classes >= 1 && n_classes <= 65535, "class count out of range");
   need(n_rows >= 1, "quantiser needs at least one row");
@@ -374,12 +350,12 @@ void launch_quantise(const float* grad, const float* hess, int64_t n_rows, int32
                                                  ((slots * 2 * sizeof(uint32_t) + 255) & ~size_t(255)));
   if (!maxima_ready) {
     hipLaunchKernelGGL(absmax_kernel, dim3(blocks, n_classes), dim3(kQuantThreads), 0, s, grad,
-                       hess, n_rows, n_classes, max_slots, rows, src);
+                       hess, n_rows, n_classes, max_slots, rows);
     DP_HIP(hipGetLastError());
   }
   hipLaunchKernelGGL(quantise_kernel, dim3(blocks, n_classes), dim3(kQuantThreads), 0, s, grad,
                      hess, n_rows, n_classes, max_slots, exps, reinterpret_cast<int2*>(gpair),
-                     sum_slots, rows, src);
+                     sum_slots, rows);
   DP_HIP(hipGetLastError());
   if (!sums) return;  // the caller reduces the sum slots itself
   hipLaunchKernelGGL(finish_sums_kernel, dim3(n_classes), dim3(kQuantThreads), 0, s, sum_slots,

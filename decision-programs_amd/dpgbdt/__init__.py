@@ -105,6 +105,7 @@ def load():
         "XGBoosterLoadModelFromBuffer": (c_int, [H, c_void_p, c_uint64]),
         "XGBoosterLoadModel": (c_int, [H, c_char_p]),
         "XGBoosterSlice": (c_int, [H, c_int, c_int, c_int, POINTER(H)]),
+        "XGBoosterGetNumFeature": (c_int, [H, POINTER(c_uint64)]),
         "DPValidateHyperparameters": (c_int, [c_char_p, ctypes.c_uint32, POINTER(c_uint64),
                                               POINTER(c_char_p)]),
         "DPBoosterNumTrees": (c_int, [H, POINTER(c_int)]),
@@ -245,6 +246,11 @@ class Booster:
         check(load().XGBoosterTrainOneIter(self.handle, dtrain.handle, iteration,
                                            array_interface(grad).encode(),
                                            array_interface(hess).encode()))
+
+    def num_features(self):
+        out = c_uint64()
+        check(load().XGBoosterGetNumFeature(self.handle, ctypes.byref(out)))
+        return out.value
 
     def num_boosted_rounds(self):
         out = c_int()

@@ -129,6 +129,13 @@ int XGBoosterPredictFromCudaArray(BoosterHandle handle, const char* values, cons
 int XGBoosterLoadModelFromBuffer(BoosterHandle handle, const void* buf, bst_ulong len);
 int XGBoosterLoadModel(BoosterHandle handle, const char* fname);
 
+/* Feature count of the booster's model: num_feature of a trained or loaded
+ * model, else of the first training matrix it was created with (0 with
+ * neither).  The converter's native oracle checks it right after loading a
+ * model (native/class_model_convert.cpp:112), as does the RL oracle
+ * (native/rl/class_xgboost.hpp:64). */
+int XGBoosterGetNumFeature(BoosterHandle handle, bst_ulong* out);
+
 /* Rounds [begin_layer, end_layer) with step as a new booster (end 0 = all),
  * as the reference uses to clone a full-round view (class_study_train.cu:132). */
 int XGBoosterSlice(BoosterHandle handle, int begin_layer, int end_layer, int step,
@@ -241,7 +248,15 @@ int dp_quantise_gradients(dp_workspace ws, const float* grad, const float* hess,
 /* Histograms of n_nodes row sets: node i covers ridx[begin[i], end[i]) (row
  * ids begin[i]..end[i]-1 when ridx is NULL).  begin/end are host arrays.
  * hist [n_nodes][n_features][bin_stride][2] is overwritten.  bin_stride >= the
- * largest bin index + 1 and <= 256. */
+ * largest bin index + 1 and <= 256.
+ * Launch shape: calls with contiguous rows (ridx NULL) use the shape the
+ * autotuner chose for this layout and bin stride.  The first such call of a
+ * shape whose nodes hold at least 262,144 rows in all tunes it: once per
+ * process, that call allocates device memory, times about 200 passes over the
+ * matrix and synchronises `stream` before it returns.  Smaller calls never
+ * tune (they take the tuned shape when there is one, else the defaults), nor
+ * do gathered calls, so a caller that must not block can make its first large
+ * call ahead of time. */
 int dp_hist_build(dp_workspace ws, const uint8_t* bins, const dp_bin_layout* layout,
                   const int32_t* gpair, const uint32_t* ridx, const int64_t* begin,
                   const int64_t* end, int32_t n_nodes, int32_t bin_stride, int64_t* hist,

@@ -6,7 +6,7 @@
  * trainer (native/class_native_training.cuh:47-70, native/class_model_train.cu:48).
  * Where upstream behaviour cannot be checked here (its library is absent) the
  * choice made is stated at the function that makes it.  Every function below is
- * pinned by tests/test_oracle_*.py against numpy closed forms, brute force or the
+ * pinned by tests/test_oracle.py against numpy closed forms, brute force or the
  * reference's fixtures; see the header of each test for what it pins.
  *
  * Compile with -ffp-contract=off: every float/double operation here must round

@@ -21,7 +21,12 @@ TREE_KEYS_BITS = ["split_condition", "base_weight", "sum_hess"]
 
 def _train_both(dp, oracle, device, config, n, f, objective, k, p, rounds, seed, injected=False,
                 max_bin=256, base_score=None, extra=None, mutate=None, sample=None,
-                values_labels=None):
+                values_labels=None, record=1):
+    """Trains the booster and the oracle's booster on the same inputs.  record: the
+    booster's dp_record_positions.  With 1 the row positions are read back after every
+    round; with 0 (the default training path, the one the bench and the trainer process
+    run) the last split level's count launch stores the leaf values and no scatter or
+    level-D planner runs, and no positions are returned (gpu_positions is None)."""
     import torch
     from dpgbdt import ops
 
@@ -37,7 +42,8 @@ def _train_both(dp, oracle, device, config, n, f, objective, k, p, rounds, seed,
     params = {"objective": obj_name, "tree_method": "hist", "device": "cuda:0", "max_bin": max_bin,
               "max_depth": p["max_depth"], "eta": p["eta"], "lambda": p.get("lam", 1.0),
               "alpha": p.get("alpha", 0.0), "gamma": p.get("gamma", 0.0),
-              "min_child_weight": p.get("min_child_weight", 1.0), "dp_record_positions": 1}
+              "min_child_weight": p.get("min_child_weight", 1.0),
+              "dp_record_positions": int(record)}
     if objective == 1:
         params["num_class"] = k
     if base_score is not None:
@@ -50,7 +56,7 @@ def _train_both(dp, oracle, device, config, n, f, objective, k, p, rounds, seed,
                 params[name] = sample[key]
     params.update(extra or {})
     bst = dp.Booster(params, [dtrain])
-    gpu_positions = []
+    gpu_positions = [] if record else None
     for r in range(rounds):
         if injected:
             gr = torch.roll(g, shifts=r).contiguous()
@@ -58,7 +64,8 @@ def _train_both(dp, oracle, device, config, n, f, objective, k, p, rounds, seed,
             bst.boost(dtrain, r, gr, hr)
         else:
             bst.update(dtrain, r)
-        gpu_positions.append(bst.last_positions(n))
+        if record:
+            gpu_positions.append(bst.last_positions(n))
     x = values.cpu().numpy()
     has_missing = bool(np.isnan(x).any())
     eff = oracle.effective_max_bin(max_bin, has_missing)
@@ -83,6 +90,8 @@ def _train_both(dp, oracle, device, config, n, f, objective, k, p, rounds, seed,
 
 
 def _compare(bst, o_trees, o_margin, gpu_positions, n, k):
+    """Trees node for node, row counts, margins bit for bit, and the row positions of every
+    round unless gpu_positions is None (a booster that did not record them)."""
     assert bst.num_trees() == len(o_trees)
     for t, ot in enumerate(o_trees):
         gt = bst.tree(t)
@@ -101,7 +110,7 @@ def _compare(bst, o_trees, o_margin, gpu_positions, n, k):
         np.testing.assert_array_equal(gt["rows"][inner],
                                       gt["rows"][ot["left"][inner]] + gt["rows"][ot["right"][inner]])
         assert gt["rows"][0] == n
-    for r, pos in enumerate(gpu_positions):
+    for r, pos in enumerate(gpu_positions or []):
         np.testing.assert_array_equal(pos, o_trees[(r + 1) * k - 1]["positions"],
                                       err_msg=f"round {r} positions")
     np.testing.assert_array_equal(bst.margins(n, k).view(np.uint32), o_margin.view(np.uint32))
@@ -258,24 +267,28 @@ def test_large_matrix_grouped_partition(dp, oracle, device):
     _compare(bst, o_trees, o_margin, pos, n, 1)
 
 
-def test_c2_full_size(dp, oracle, device):
+@pytest.mark.parametrize("record", [0, 1])
+def test_c2_full_size(dp, oracle, device, record):
     """C2 at its benchmark size and parameters (1,000,000 x 28, depth 8, eta 0.1,
-    logistic): two rounds, every tree, the row partition and the margins
-    bit-exact against the oracle."""
+    logistic): two rounds, every tree, the margins (and, recording them, the row
+    partition) bit-exact against the oracle.  record 0 is the path the bench times."""
     p = {"max_depth": 8, "eta": 0.1}
-    print("[booster] C2 1000000 x 28, depth 8 (benchmark size)", flush=True)
+    print(f"[booster] C2 1000000 x 28, depth 8 (benchmark size), record {record}", flush=True)
     bst, x, o_trees, o_margin, pos, n = _train_both(dp, oracle, device, 2, 1_000_000, 28, 0, 1, p, 2,
-                                                    20261201 + 2)
+                                                    20261201 + 2, record=record)
     _compare(bst, o_trees, o_margin, pos, n, 1)
 
 
-def test_c4_full_size(dp, oracle, device):
-    """C4 at its benchmark size (60,000 x 784, 10 classes, depth 6, eta 0.3): one
-    round of ten trees, grown concurrently on four streams, against the oracle."""
+@pytest.mark.parametrize("record", [0, 1])
+def test_c4_full_size(dp, oracle, device, record):
+    """C4 at its benchmark size (60,000 x 784, 10 classes, depth 6, eta 0.3): two
+    rounds of ten trees, grown concurrently on four streams, against the oracle (the
+    second round's gradients add the first round's leaf values when record is 0)."""
     p = {"max_depth": 6, "eta": 0.3}
-    print("[booster] C4 60000 x 784, 10 classes, depth 6 (benchmark size)", flush=True)
-    bst, x, o_trees, o_margin, pos, n = _train_both(dp, oracle, device, 4, 60_000, 784, 1, 10, p, 1,
-                                                    20261201 + 4)
+    print(f"[booster] C4 60000 x 784, 10 classes, depth 6 (benchmark size), record {record}",
+          flush=True)
+    bst, x, o_trees, o_margin, pos, n = _train_both(dp, oracle, device, 4, 60_000, 784, 1, 10, p, 2,
+                                                    20261201 + 4, record=record)
     _compare(bst, o_trees, o_margin, pos, n, 10)
 
 
@@ -668,14 +681,17 @@ def test_last_level_margins_synced_and_large(dp, oracle, device, case):
         np.testing.assert_array_equal(out[0][0].view(np.uint32), o_margin.view(np.uint32))
 
 
-def test_c5_own_parameters(dp, oracle, device):
+@pytest.mark.parametrize("record", [0, 1])
+def test_c5_own_parameters(dp, oracle, device, record):
     """C5's own parameters against the oracle (200,000 x 1,000, 95 % missing, max_bin 64,
     depth 10, squared error, two rounds): the evaluation kernel for at most 64 bins, the
-    present-value histograms and the depth-10 planner together, node for node."""
+    present-value histograms and the depth-10 planner together, node for node; record 0 is
+    the path the bench times."""
     p = {"max_depth": 10, "eta": 0.3}
-    print("[booster] C5 200000 x 1000, 64 bins, depth 10 vs the oracle", flush=True)
+    print(f"[booster] C5 200000 x 1000, 64 bins, depth 10 vs the oracle, record {record}",
+          flush=True)
     bst, x, o_trees, o_margin, pos, n = _train_both(dp, oracle, device, 5, 200_000, 1000, 2, 1, p,
-                                                    2, 20261201 + 5, max_bin=64)
+                                                    2, 20261201 + 5, max_bin=64, record=record)
     _compare(bst, o_trees, o_margin, pos, n, 1)
     assert max(len(t["left"]) for t in o_trees) > 500, "trees too small for depth 10"
     assert any(t["default_left"].any() for t in o_trees), "learned default direction unused"
@@ -695,7 +711,8 @@ def test_c3_tree_one_million_rows(dp, oracle, device):
 def test_c3_full_size_tree(dp, oracle, device):
     """C3 at its full size -- 10,000,000 rows x 128 features, 256 bins, depth 8, injected
     gradients -- one round against the oracle's booster on all host cores: every split record,
-    row count, leaf value, the 10M row positions and the margins.  The oracle takes the GPU's
+    row count, leaf value and the margins of a booster without row positions recorded (the
+    bench's path) and of one with them, whose 10M row positions are compared too.  The oracle takes the GPU's
     cuts and uint8 bins (bit-identical to its own on every configuration's shape,
     test_gpu_kernels.py::test_cuts_and_bins_bit_exact), as the bench's CPU leg does, so the
     check covers the boosting round: the root pass over all rows, the gathered passes with
@@ -710,10 +727,12 @@ def test_c3_full_size_tree(dp, oracle, device):
     print("[booster] C3 10000000 x 128, depth 8 vs the oracle (host threads)", flush=True)
     values, labels, g, h = ops.synth(3, n, 20261204, want_grad=True)
     dtrain = dp.DMatrix(values, labels)
-    bst = dp.Booster({"objective": "reg:squarederror", "max_depth": 8, "eta": 0.3,
-                      "max_bin": 256, "dp_record_positions": 1}, [dtrain])
-    bst.boost(dtrain, 0, g.reshape(-1, 1).contiguous(), h.reshape(-1, 1).contiguous())
-    gpu_positions = [bst.last_positions(n)]
+    boosters = []
+    for record in (0, 1):  # 0: the path the bench times; 1: also the row positions
+        bst = dp.Booster({"objective": "reg:squarederror", "max_depth": 8, "eta": 0.3,
+                          "max_bin": 256, "dp_record_positions": record}, [dtrain])
+        bst.boost(dtrain, 0, g.reshape(-1, 1).contiguous(), h.reshape(-1, 1).contiguous())
+        boosters.append((bst, [bst.last_positions(n)] if record else None))
     assert not bool(torch.isnan(values).any().item())  # C3 has no missing values
     ws = ops.Workspace()
     cut_ptr, cuts, _, _ = ops.sketch_cuts(ws, values, 256)
@@ -731,7 +750,8 @@ def test_c3_full_size_tree(dp, oracle, device):
                                             injected=lambda r: (gn, hn))
     finally:
         oracle.set_threads(1)
-    _compare(bst, o_trees, o_margin, gpu_positions, n, 1)
+    for bst, gpu_positions in boosters:
+        _compare(bst, o_trees, o_margin, gpu_positions, n, 1)
 
 
 def _random_case(rng, large=False):
@@ -803,16 +823,20 @@ def _random_problems(dp, oracle, device, seed, count, large=False):
     import torch
 
     rng = np.random.default_rng(seed)
+    # dp_record_positions per problem from a generator of its own, so the problems
+    # themselves stay the ones the seed has always drawn
+    record_rng = np.random.default_rng(seed + 1)
     grown = 0
     for t in range(count):
         x, y, case = _random_case(rng, large)
-        print(f"[booster] random problem {t}: {case}", flush=True)
+        record = int(record_rng.integers(0, 2))
+        print(f"[booster] random problem {t} (record {record}): {case}", flush=True)
         values = torch.from_numpy(x).to(device)
         labels = torch.from_numpy(y).to(device)
         bst, _, o_trees, o_margin, pos, n = _train_both(
             dp, oracle, device, 1, case["n"], case["f"], case["objective"], case["k"], case["p"],
             case["rounds"], 0, max_bin=case["max_bin"], extra=case["extra"],
-            sample=case["sample"], values_labels=(values, labels))
+            sample=case["sample"], values_labels=(values, labels), record=record)
         _compare(bst, o_trees, o_margin, pos, n, case["k"])
         # the predictor, walking the saved trees on the raw values, gives the same margins
         pm = bst.predict(values, margin=True).cpu().numpy()
@@ -827,8 +851,10 @@ def test_random_problems_match_the_oracle(dp, oracle, device):
     (tied integers, constants, mostly-zero columns), 0-95 % missing, 2-256 bins, every
     objective, depth 1-10, random regularisation, sampling, histogram layout, skip bins,
     launch shape and graph use -- each trained for 1-3 rounds against the oracle's booster:
-    split records, row counts, leaf values, row positions and margins, bit for bit, and the
-    predictor's margins over the raw values equal to them."""
+    split records, row counts, leaf values, margins and (for the problems drawn to record
+    them) row positions, bit for bit, and the predictor's margins over the raw values equal
+    to them.  About half the problems run without row positions recorded, the default
+    training path."""
     grown = _random_problems(dp, oracle, device, 20261202, 100)
     assert grown >= 60, f"only {grown} of 100 problems grew a split"
 
@@ -978,3 +1004,174 @@ def test_max_bin_is_not_changed_silently(dp, device):
         b.update(d, 0)
         cfg = json.loads(b.save_config())
         assert cfg["learner"]["gradient_booster"]["updater"][0]["hist_train_param"]["max_bin"] == used
+
+
+@pytest.mark.parametrize("objective", ["multi:softprob", "multi:softmax"])
+def test_resident_model_sequence(dp, oracle, device, objective):
+    """The converter's native oracle (ResidentModel, native/class_model_convert.cpp:96-156)
+    replayed call for call on a model this library trained: XGBoostVersion and XGBuildInfo
+    checks, XGBoosterCreate(NULL, 0), XGBoosterLoadModelFromBuffer, SetParam device and
+    nthread, XGBoosterGetNumFeature against the source's feature count, the
+    XGBoosterSaveJsonConfig field checks, then XGBoosterPredictFromCudaArray with
+    strict_shape and "missing":NaN for margins and values.  The margins must equal the
+    oracle's training margins bit for bit."""
+    import ctypes
+
+    import torch
+
+    rng = np.random.default_rng(31)
+    n, f, k = 3000, 6, 3
+    x = rng.normal(size=(n, f)).astype(np.float32)
+    x[rng.random((n, f)) < 0.1] = np.nan
+    y = (np.nan_to_num(x[:, 0]) + np.nan_to_num(x[:, 1]) > 0).astype(np.float32) + \
+        (np.nan_to_num(x[:, 2]) > 0.5).astype(np.float32)
+    values = torch.from_numpy(x).to(device)
+    labels = torch.from_numpy(y).to(device)
+    p = {"max_depth": 4, "eta": 0.3}
+    bst, _, o_trees, o_margin, _, _ = _train_both(dp, oracle, device, 1, n, f, 1, k, p, 3, 0,
+                                                 values_labels=(values, labels), record=0)
+    # trained as multi:softmax (the reference trainer's objective); the softprob case
+    # names the other objective the converter accepts in the saved model
+    doc = json.loads(bst.save_raw())
+    assert doc["learner"]["objective"]["name"] == "multi:softmax"
+    doc["learner"]["objective"]["name"] = objective
+    model = json.dumps(doc).encode()
+
+    lib = dp.load()
+    H = ctypes.c_void_p
+    major, minor, patch = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    lib.XGBoostVersion(ctypes.byref(major), ctypes.byref(minor), ctypes.byref(patch))
+    assert (major.value, minor.value, patch.value) == (3, 4, 1)
+    info = ctypes.c_char_p()
+    assert lib.XGBuildInfo(ctypes.byref(info)) == 0
+    assert json.loads(info.value.decode())["USE_CUDA"] is True
+    h = H()
+    assert lib.XGBoosterCreate(None, 0, ctypes.byref(h)) == 0, lib.XGBGetLastError()
+    try:
+        buf = ctypes.create_string_buffer(model, len(model))
+        assert lib.XGBoosterLoadModelFromBuffer(h, buf, len(model)) == 0, lib.XGBGetLastError()
+        assert lib.XGBoosterSetParam(h, b"device", b"cuda:0") == 0
+        assert lib.XGBoosterSetParam(h, b"nthread", b"4") == 0
+        features = ctypes.c_uint64()
+        assert lib.XGBoosterGetNumFeature(h, ctypes.byref(features)) == 0
+        assert features.value == f
+        size, text = ctypes.c_uint64(), ctypes.c_char_p()
+        assert lib.XGBoosterSaveJsonConfig(h, ctypes.byref(size), ctypes.byref(text)) == 0
+        cfg = json.loads(ctypes.string_at(text, size.value).decode())["learner"]
+        assert cfg["generic_param"]["device"] == "cuda:0"
+        assert cfg["gradient_booster"]["name"] == "gbtree"
+        assert cfg["objective"]["name"] == objective
+        assert int(cfg["learner_model_param"]["num_class"]) == k
+        torch.cuda.synchronize()
+        array = json.dumps({"data": [values.data_ptr(), True], "shape": [n, f], "strides": None,
+                            "typestr": "<f4", "version": 3, "stream": 1})
+        for margin in (True, False):
+            options = json.dumps({"type": 1 if margin else 0, "training": False,
+                                  "iteration_begin": 0, "iteration_end": 0,
+                                  "strict_shape": True, "cache_id": 0})[:-1] + ',"missing":NaN}'
+            shape = ctypes.POINTER(ctypes.c_uint64)()
+            dims = ctypes.c_uint64()
+            out = ctypes.POINTER(ctypes.c_float)()
+            assert lib.XGBoosterPredictFromCudaArray(
+                h, array.encode(), options.encode(), None, ctypes.byref(shape),
+                ctypes.byref(dims), ctypes.byref(out)) == 0, lib.XGBGetLastError()
+            columns = k if margin or objective == "multi:softprob" else 1
+            assert dims.value == 2 and (shape[0], shape[1]) == (n, columns)
+            got = torch.empty((n, columns), dtype=torch.float32, device=device)
+            from dpgbdt import _hip_memcpy
+            _hip_memcpy()(ctypes.c_void_p(got.data_ptr()),
+                          ctypes.c_void_p(ctypes.addressof(out.contents)), n * columns * 4)
+            torch.cuda.synchronize()
+            got = got.cpu().numpy()
+            if margin:
+                np.testing.assert_array_equal(got.view(np.uint32), o_margin.view(np.uint32))
+            elif objective == "multi:softmax":
+                np.testing.assert_array_equal(got[:, 0],
+                                              np.argmax(o_margin, axis=1).astype(np.float32))
+            else:
+                m = o_margin.astype(np.float64)
+                prob = np.exp(m - m.max(axis=1, keepdims=True))
+                prob /= prob.sum(axis=1, keepdims=True)
+                np.testing.assert_allclose(got, prob, rtol=1e-5, atol=1e-7)
+    finally:
+        lib.XGBoosterFree(h)
+
+
+def test_caller_gradients_may_be_overwritten_after_return(dp, device):
+    """XGBoosterTrainOneIter returns only once its quantiser has read the caller's arrays:
+    overwriting them from a non-blocking stream right after each call (with nothing ordering
+    that stream after the library's) leaves the model and margins equal to a run whose
+    buffers stay untouched."""
+    import torch
+    from dpgbdt import ops
+
+    n = 200_000
+    values, labels, g, h = ops.synth(1, n, 7, n_features=16, want_grad=True)
+    g, h = g.reshape(-1, 1).contiguous(), h.reshape(-1, 1).contiguous()
+    dtrain = dp.DMatrix(values, labels)
+    params = {"objective": "reg:squarederror", "max_depth": 6, "eta": 0.3}
+    side = torch.cuda.Stream(device=device)  # non-blocking with respect to the null stream
+    out = []
+    for overwrite in (False, True):
+        bst = dp.Booster(params, [dtrain])
+        gb, hb = g.clone(), h.clone()
+        for r in range(3):
+            torch.cuda.synchronize()
+            gb.copy_(torch.roll(g, r))
+            hb.copy_(torch.roll(h, r))
+            torch.cuda.synchronize()
+            bst.boost(dtrain, r, gb, hb)
+            if overwrite:
+                with torch.cuda.stream(side):
+                    gb.fill_(1e6)
+                    hb.fill_(-3.0)
+        torch.cuda.synchronize()
+        out.append((bst.save_raw(), bst.margins(n, 1)))
+    assert out[0][0] == out[1][0]
+    np.testing.assert_array_equal(out[0][1].view(np.uint32), out[1][1].view(np.uint32))
+
+
+def test_train_one_iter_refuses_foreign_arrays(dp, device):
+    """Gradient arrays the quantiser could not read in bounds are refused with an error: host
+    memory, and a device allocation shorter than the declared shape."""
+    import ctypes
+
+    import torch
+    from dpgbdt import ops
+
+    n = 4096
+    values, labels, _, _ = ops.synth(1, n, 3)
+    dtrain = dp.DMatrix(values, labels)
+    bst = dp.Booster({"objective": "reg:squarederror", "max_depth": 3}, [dtrain])
+    lib = dp.load()
+
+    def iface(ptr, rows):
+        return json.dumps({"data": [ptr, True], "shape": [rows, 1], "strides": None,
+                           "typestr": "<f4", "version": 3}).encode()
+
+    ok = torch.zeros((n, 1), dtype=torch.float32, device=device)
+    host = np.zeros(n, dtype=np.float32)
+    assert lib.XGBoosterTrainOneIter(bst.handle, dtrain.handle, 0, iface(host.ctypes.data, n),
+                                     iface(ok.data_ptr(), n)) == -1
+    assert "grad must be device memory" in lib.XGBGetLastError().decode()
+    # a hipMalloc allocation declared one float longer than the runtime says it is
+    rt = ctypes.CDLL("libamdhip64.so.7")
+    rt.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+    rt.hipFree.argtypes = [ctypes.c_void_p]
+    rt.hipMemGetAddressRange.argtypes = [ctypes.POINTER(ctypes.c_void_p),
+                                         ctypes.POINTER(ctypes.c_size_t), ctypes.c_void_p]
+    p = ctypes.c_void_p()
+    assert rt.hipMalloc(ctypes.byref(p), 1 << 20) == 0
+    try:
+        base, size = ctypes.c_void_p(), ctypes.c_size_t()
+        assert rt.hipMemGetAddressRange(ctypes.byref(base), ctypes.byref(size), p) == 0
+        assert base.value == p.value and size.value >= 1 << 20
+        rows = size.value // 4 + 1
+        assert lib.XGBoosterTrainOneIter(bst.handle, dtrain.handle, 0, iface(p.value, rows),
+                                         iface(p.value, rows)) == -1
+        assert "exceed its device allocation" in lib.XGBGetLastError().decode()
+    finally:
+        rt.hipFree(p)
+    # the booster is unharmed: a valid round still trains
+    bst.boost(dtrain, 0, ok.clone(), torch.ones((n, 1), dtype=torch.float32, device=device))
+    assert bst.num_boosted_rounds() == 1

@@ -105,6 +105,32 @@ def test_quantise_bit_exact(dp, oracle, ws, device):
         assert np.abs(qg).max() <= 2 ** 30 and np.abs(qh).max() <= 2 ** 30
 
 
+def _check_float_sums(oracle, hist, o_bins, gn, hn, eg, eh, missing_bin, features):
+    """The histogram's sums as floats (the fixed-point sums times 2^-exp) against the float64
+    sums of the raw float32 gradients, for g and for h, per (feature, bin): within 1e-5
+    relative wherever the bin's |sum| is at least 1e-3 of its sum of magnitudes, and within
+    1e-5 of that sum of magnitudes in the cancelling bins (where a relative bound on a sum
+    near zero means nothing).  The quantiser's step is 2^-30 of max|x| per item, so the
+    bound holds with a margin of about 20x on these inputs."""
+    stride = hist.shape[1]
+    checked = 0
+    for c, (x, e) in enumerate(((gn, eg), (hn, eh))):
+        got = hist[..., c] * oracle.unscale(e)
+        for feat in features:
+            col = o_bins[:, feat]
+            keep = col != missing_bin if missing_bin >= 0 else slice(None)
+            cb, xv = col[keep], x[keep].astype(np.float64)
+            exact = np.bincount(cb, weights=xv, minlength=stride)[:stride]
+            mass = np.bincount(cb, weights=np.abs(xv), minlength=stride)[:stride]
+            err = np.abs(got[feat] - exact)
+            live = np.abs(exact) >= 1e-3 * mass
+            bad = live & (err > 1e-5 * np.abs(exact))
+            assert not bad.any(), (c, feat, np.nonzero(bad)[0][:5], err[bad][:5], exact[bad][:5])
+            assert np.all(err[~live] <= 1e-5 * mass[~live]), (c, feat)
+            checked += int(live.sum())
+    return checked
+
+
 def _gpair(ws, device, g, h):
     import torch
     from dpgbdt import ops
@@ -136,14 +162,8 @@ def test_root_histogram_bit_exact(dp, oracle, ws, device, config, n, f):
         col = o_bins[:, feat]
         col = col[col != 255] if mb == 255 else col
         np.testing.assert_array_equal(counts[feat, :, 0], np.bincount(col, minlength=stride)[:stride])
-    # float sums within 1e-5 of the float64 sums of the raw gradients
-    gsum = hist[..., 0] * oracle.unscale(eg)
-    for feat in range(0, f, max(1, f // 8)):
-        col = o_bins[:, feat]
-        keep = col != 255 if mb == 255 else np.ones(n, bool)
-        exact = np.bincount(col[keep], weights=gn[keep].astype(np.float64), minlength=stride)[:stride]
-        mass = np.bincount(col[keep], weights=np.abs(gn[keep]).astype(np.float64), minlength=stride)[:stride]
-        assert np.all(np.abs(gsum[feat] - exact) <= 1e-5 * np.maximum(mass, 1e-30))
+    # g and h sums as floats within 1e-5 relative of the float64 sums of the raw gradients
+    assert _check_float_sums(oracle, hist, o_bins, gn, hn, eg, eh, mb, range(f)) > 0
 
 
 def test_c3_root_histogram_full_size(dp, oracle, ws, device):
@@ -173,6 +193,35 @@ def test_c3_root_histogram_full_size(dp, oracle, ws, device):
     del bins
     ref = oracle.hist_parallel(host_bins, qgqh[:, 0], qgqh[:, 1], bin_stride=stride)
     np.testing.assert_array_equal(hist, ref)
+    # every feature's g and h sums as floats, within 1e-5 relative of float64 sums
+    live = _check_float_sums(oracle, hist, host_bins, g.cpu().numpy(), h.cpu().numpy(), eg, eh,
+                             -1, range(f))
+    print(f"[kernels] C3 float sums: {live} (feature, bin, g|h) sums within 1e-5 relative",
+          flush=True)
+
+
+def test_c5_float_sums(dp, oracle, ws, device):
+    """C5's shape at 200,000 x 1,000 (95 % missing, 64 bins plus the missing byte): the root
+    histogram's g and h sums as floats, for every feature, within 1e-5 relative of the float64
+    sums of the raw gradients over the present values (bit-exact fixed point against the
+    oracle first)."""
+    from dpgbdt import ops
+
+    n, f = 200_000, 1000
+    print(f"[kernels] C5 float sums {n} x {f}", flush=True)
+    values, _, g, h = _synth(ops, 5, n, 20261201 + 5, f, grad=True)
+    lay, bins, o_bins, cut_ptr, cuts, n_bins, mb = _prepare(dp, oracle, ws, values, 64)
+    assert mb == 255
+    stride = int(n_bins.max())
+    gn, hn = g.cpu().numpy(), h.cpu().numpy()
+    (eg, eh), gpair, _ = _gpair(ws, device, gn, hn)
+    hist = ops.hist_build(ws, bins, lay, gpair, [(0, n)], stride).cpu().numpy()[0]
+    q = oracle.quantise(gn, hn)[0]
+    np.testing.assert_array_equal(hist, oracle.hist(o_bins, q[2], q[3], bin_stride=stride,
+                                                    missing_bin=mb))
+    live = _check_float_sums(oracle, hist, o_bins, gn, hn, eg, eh, mb, range(f))
+    print(f"[kernels] C5 float sums: {live} (feature, bin, g|h) sums within 1e-5 relative",
+          flush=True)
 
 
 @pytest.mark.parametrize("max_bin", [64, 128])

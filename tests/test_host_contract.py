@@ -96,3 +96,26 @@ def test_deeply_nested_model_buffer_is_refused(dp):
         assert "nesting deeper" in lib.XGBGetLastError().decode()
     finally:
         lib.XGBoosterFree(h)
+
+
+def test_train_one_iter_refuses_host_gradients(dp):
+    """XGBoosterTrainOneIter's quantiser reads the caller's gradient arrays in place on the
+    device, so a host pointer is refused with an error before any launch (without a GPU the
+    pointer cannot be device memory either)."""
+    import numpy as np
+
+    lib = dp.load()
+    h = ctypes.c_void_p()
+    assert lib.XGBoosterCreate(None, 0, ctypes.byref(h)) == 0
+    try:
+        g = np.zeros(16, dtype=np.float32)
+
+        def iface(a):
+            return json.dumps({"data": [a.ctypes.data, True], "shape": [16], "strides": None,
+                               "typestr": "<f4", "version": 3}).encode()
+
+        rc = lib.XGBoosterTrainOneIter(h, None, 0, iface(g), iface(g))
+        assert rc == -1
+        assert "grad must be device memory" in lib.XGBGetLastError().decode()
+    finally:
+        lib.XGBoosterFree(h)

@@ -138,3 +138,20 @@ def test_errors_are_reported_not_raised(dp):
     assert lib.XGBGetLastError()
     rc = lib.XGBoosterSetParam(None, b"eta", b"0.3")
     assert rc == -1 and b"null" in lib.XGBGetLastError()
+
+
+def test_num_feature_of_an_empty_booster(dp):
+    """XGBoosterGetNumFeature, which the converter's native oracle calls right after
+    loading a model (native/class_model_convert.cpp:112): 0 for a booster with neither a
+    model nor a training matrix, and a null output pointer is an error.  A loaded model's
+    count is checked on the GPU (test_gpu_booster.py::test_resident_model_sequence)."""
+    lib = dp.load()
+    h = ctypes.c_void_p()
+    assert lib.XGBoosterCreate(None, 0, ctypes.byref(h)) == 0
+    try:
+        n = ctypes.c_uint64(99)
+        assert lib.XGBoosterGetNumFeature(h, ctypes.byref(n)) == 0 and n.value == 0
+        assert lib.XGBoosterGetNumFeature(h, None) == -1
+        assert b"null" in lib.XGBGetLastError()
+    finally:
+        lib.XGBoosterFree(h)

@@ -97,3 +97,46 @@ def test_noalloc_refuses_beyond_its_array(dp, device):
                                         ops._ptr(out), ops._stream())
     assert rc == -1
     assert "exceeds" in lib.XGBGetLastError().decode()
+
+
+def test_noalloc_inside_graph_capture(dp, ws, device):
+    """The callers it is for: one warm call (the per-device array address is looked up
+    then), then the call captured into a HIP graph with torch.cuda.graph and replayed on new
+    histograms copied into the captured input buffers.  Every replay, with eager work and
+    synchronisations between replays, must equal dp_evaluate_splits on the same inputs."""
+    import torch
+    from dpgbdt import SplitRecord, ops
+
+    lib = dp.load()
+    rng = np.random.default_rng(23)
+    n_nodes, f, stride = 40, 120, 256
+    param = ops.train_param()
+    hist, n_bins, sums = _inputs(rng, n_nodes, f, stride, device)
+    out = torch.empty((n_nodes, ctypes.sizeof(SplitRecord)), dtype=torch.uint8, device=device)
+
+    def call():
+        return lib.dp_evaluate_splits_noalloc(ops._ptr(hist), n_nodes, f, stride,
+                                              ops._ptr(n_bins), ops._ptr(sums), 26, 24,
+                                              ctypes.byref(param), ops._ptr(out), ops._stream())
+
+    assert call() == 0  # warm: the array's device address is known from here on
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        assert call() == 0, lib.XGBGetLastError().decode()
+    valid = 0
+    for replay in range(4):
+        h2, b2, s2 = _inputs(rng, n_nodes, f, stride, device)
+        torch.cuda.synchronize()
+        hist.copy_(h2)
+        n_bins.copy_(b2)
+        sums.copy_(s2)
+        want = ops.splits_to_numpy(ops.evaluate_splits(ws, hist, n_bins, sums, 26, 24, param))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = ops.splits_to_numpy(out)
+        print(f"noalloc graph replay {replay}", flush=True)
+        assert got.tobytes() == want.tobytes(), f"replay {replay}"
+        valid += int(np.sum(got["valid"] == 1))
+    assert valid > 0
