@@ -221,7 +221,8 @@ def cpu_trees_leg(torch, ops, name, max_rounds, threads):
     f = values.shape[1]
     ws = ops.Workspace()
     has_missing = bool(torch.isnan(values).any().item())
-    eff = pyoracle.effective_max_bin(max_bin, has_missing)
+    # the CPU legs read the device's uint8 bins: byte 255 marks missing values
+    eff = min(max_bin, 255) if has_missing else min(max_bin, 256)
     cut_ptr, cuts, _, _ = ops.sketch_cuts(ws, values, eff)
     mb = 255 if has_missing else -1
     lay = ops.layout(n, f, 0, mb)

@@ -138,8 +138,10 @@ Quantized& DMatrix::quantize(int32_t max_bin, dp_workspace_s& ws, hipStream_t s)
   int32_t has_nan = 0;
   DP_HIP(hipMemcpyAsync(&has_nan, flag.p, sizeof(int32_t), hipMemcpyDeviceToHost, s));
   DP_HIP(hipStreamSynchronize(s));
-  // uint8 storage: with NaN present byte 255 marks missing, leaving 255 bins.
-  const int32_t eff = std::min(max_bin, has_nan ? 255 : 256);
+  // Cuts for up to 256 bins, with or without missing values.  uint8 bins keep
+  // byte 255 for missing values, so a matrix with NaN whose features use all
+  // 256 bins keeps 16-bit columns instead (below).
+  const int32_t eff = std::min(max_bin, kMaxBins);
   q->max_bin = eff;
   q->cut_ptr.assign(size_t(n_features) + 1, 0);
   q->cut_values.assign(size_t(n_features) * eff, 0.0f);
@@ -155,8 +157,10 @@ Quantized& DMatrix::quantize(int32_t max_bin, dp_workspace_s& ws, hipStream_t s)
     widest = std::max(widest, nbins[size_t(f)]);
   }
   q->bin_stride = widest;
+  const bool wide = has_nan && widest > 255;
   need(dp_layout_init(n_rows, n_features, 0, has_nan ? 255 : -1, &q->layout) == 0,
        "bin layout");
+  if (wide) q->layout.missing_bin = kWideMissing;
   q->d_cut_ptr.resize(q->cut_ptr.size());
   q->d_cut_values.resize(std::max<size_t>(q->cut_values.size(), 1));
   q->d_nbins.resize(nbins.size());
@@ -165,10 +169,16 @@ Quantized& DMatrix::quantize(int32_t max_bin, dp_workspace_s& ws, hipStream_t s)
   DP_HIP(hipMemcpyAsync(q->d_cut_values.p, q->cut_values.data(),
                         sizeof(float) * q->cut_values.size(), hipMemcpyHostToDevice, s));
   DP_HIP(hipMemcpyAsync(q->d_nbins.p, nbins.data(), q->d_nbins.bytes(), hipMemcpyHostToDevice, s));
-  q->bins.resize(dp_layout_bytes(&q->layout));
-  launch_bin_values(values.p, q->layout, q->d_cut_ptr.p, q->d_cut_values.p, q->bins.p, s);
-  q->cols.resize(size_t(n_rows) * size_t(n_features));
-  launch_tiles_to_columns(q->bins.p, q->layout, q->cols.p, s);
+  if (wide) {
+    q->cols16.resize(size_t(n_rows) * size_t(n_features));
+    launch_bin_columns16(values.p, n_rows, n_features, q->d_cut_ptr.p, q->d_cut_values.p,
+                         q->cols16.p, s);
+  } else {
+    q->bins.resize(dp_layout_bytes(&q->layout));
+    launch_bin_values(values.p, q->layout, q->d_cut_ptr.p, q->d_cut_values.p, q->bins.p, s);
+    q->cols.resize(size_t(n_rows) * size_t(n_features));
+    launch_tiles_to_columns(q->bins.p, q->layout, q->cols.p, s);
+  }
   DP_HIP(hipStreamSynchronize(s));
   auto& ref = *q;
   quantized.emplace(max_bin, std::move(q));
@@ -540,7 +550,10 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
         ll.mcw = double(p.min_child_weight);
         last_level_applied = true;
       }
-      launch_partition(q.bins.p, q.cols.p, L, ridx_[cur].p, ridx_[nxt].p, part_work_[cur].p,
+      launch_partition(q.bins.p,
+                       L.missing_bin == kWideMissing ? static_cast<const void*>(q.cols16.p)
+                                                     : static_cast<const void*>(q.cols.p),
+                       L, ridx_[cur].p, ridx_[nxt].p, part_work_[cur].p,
                        int32_t(plan_part_capacity(nb, N, chunk_)), &c->n_part[d & 1],
                        seg_begin_[cur].p, splits_.p, part_first_[cur].p, int32_t(nb),
                        field(c, &PlanCounts::n_level), work_left_.p, part_masks_.p,
@@ -1071,7 +1084,15 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
   // Histogram layout: the present-value layout for mostly-missing matrices,
   // else the row-major copy of the tiles for gathered rows.
   bool sparse = false;
-  if (sparse_mode_ != 0 && q.layout.missing_bin >= 0) {
+  if (q.layout.missing_bin == kWideMissing) {
+    // 16-bit symbols: the present-value layout is the only histogram layout
+    // (whatever dp_sparse_hist says), built from the columns.
+    if (q.sparse.n_tiles == 0) {
+      build_sparse_bins_wide(q.cols16.p, N, q.layout.n_features, q.bin_stride, q.sparse, stream_);
+      q.sparse_limit = 1.0;
+    }
+    sparse = true;
+  } else if (sparse_mode_ != 0 && q.layout.missing_bin >= 0) {
     const double limit = sparse_mode_ == 2 ? 1.0 : kSparseDensity;
     if (q.sparse.n_tiles == 0 && q.sparse_limit < limit) {
       q.density = build_sparse_bins(q.bins.p, q.layout, q.bin_stride, limit, q.sparse, stream_);
@@ -1155,6 +1176,7 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
   std::vector<uint64_t> key = {
       uint64_t(with_gradients), reinterpret_cast<uint64_t>(d), reinterpret_cast<uint64_t>(&q),
       reinterpret_cast<uint64_t>(q.bins.p), reinterpret_cast<uint64_t>(q.cols.p),
+      reinterpret_cast<uint64_t>(q.cols16.p),
       reinterpret_cast<uint64_t>(q.rows.p), reinterpret_cast<uint64_t>(q.d_nbins.p),
       uint64_t(q.bin_stride), uint64_t(N), reinterpret_cast<uint64_t>(d->labels.p),
       uint64_t(objective_id_), uint64_t(n_groups_), reinterpret_cast<uint64_t>(margin_.p),
@@ -1433,8 +1455,8 @@ std::string Booster::save_config() const {
        "\"},\"gbtree_train_param\":{\"process_type\":\"default\",\"tree_method\":\"hist\","
        "\"updater\":\"grow_gpu_hist\",\"updater_seq\":\"grow_gpu_hist\"},\"name\":\"gbtree\","
        "\"updater\":[{\"hist_train_param\":{\"max_bin\":\"";
-  // The bins actually used: a matrix with missing values keeps byte 255 for
-  // them, so max_bin 256 bins it into at most 255 quantiles.
+  // The bins the cuts were computed with (max_bin, at most 256, also with
+  // missing values).
   o += std::to_string(effective_max_bin_ > 0 ? effective_max_bin_ : tp_.max_bin) +
        "\"},\"name\":\"grow_gpu_hist\",\"train_param\":{";
   auto kv = [&](const char* k, const std::string& v, bool comma = true) {

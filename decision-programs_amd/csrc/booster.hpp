@@ -22,6 +22,11 @@ struct Quantized {
   DeviceBuffer<float> d_cut_values;
   DeviceBuffer<uint8_t> bins;
   DeviceBuffer<uint8_t> cols;  // column-major copy: cols[f * n_rows + r]
+  // A matrix with missing values some of whose features use all 256 bins
+  // (layout.missing_bin == kWideMissing): no uint8 bins; 16-bit columns
+  // (missing: kWideMissing) for the partition, and every histogram from the
+  // present-value layout built from them.
+  DeviceBuffer<uint16_t> cols16;
   DeviceBuffer<uint8_t> rows;  // row-major copy: rows[(r * n_tiles + t) * 16 + j] (on demand)
   SparseBins sparse;           // present-value layout (on demand, mostly-missing matrices)
   // Skip bins (matrices without missing values, on demand): each feature's most

@@ -129,6 +129,11 @@ struct FeatCand {
   int32_t bin, dl;
 };
 constexpr int kMaxBins = 256;
+// Missing symbol of 16-bit bins: a matrix with missing values some of whose
+// features use all 256 bins keeps 16-bit columns (the layout's missing_bin is
+// then kWideMissing) and histograms from the present-value layout, which
+// stores no missing values.
+constexpr int32_t kWideMissing = 256;
 
 // One histogram work item: rows [begin, end) of node `slot` for one tile.
 // partial >= 0: the workgroup stores its tile histogram in partial slot
@@ -497,7 +502,9 @@ struct SplitSelect {
   int32_t n_features = 0;
   double gamma = 0.0;
 };
-void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_layout& layout,
+// cols: the column copy, uint8 symbols, or uint16 when layout.missing_bin is
+// kWideMissing (such a layout has no tile-major bins: cols is required).
+void launch_partition(const uint8_t* bins, const void* cols, const dp_bin_layout& layout,
                       const uint32_t* ridx_in, uint32_t* ridx_out, const PartWork* work,
                       int32_t n_work, const int32_t* n_work_dev, const int64_t* seg_begin,
                       dp_split_record* splits, const int32_t* node_first_work,
@@ -684,6 +691,16 @@ int32_t sparse_tile_features(int32_t bin_stride);
 // 32-bit offsets); returns the share.  Synchronises the stream.
 double build_sparse_bins(const uint8_t* bins, const dp_bin_layout& layout, int32_t bin_stride,
                          double max_density, SparseBins& out, hipStream_t s);
+// The same layout from 16-bit columns (cols[f * n_rows + r], kWideMissing for
+// missing values), whatever the density; fails when the present values do not
+// fit 32-bit offsets.  Synchronises the stream.
+void build_sparse_bins_wide(const uint16_t* cols, int64_t n_rows, int32_t n_features,
+                            int32_t bin_stride, SparseBins& out, hipStream_t s);
+// cols[f * n_rows + r] = bin of values[r * n_features + f] (first cut > x,
+// clamped), kWideMissing for NaN: the 16-bit columns of such a matrix.
+void launch_bin_columns16(const float* values, int64_t n_rows, int32_t n_features,
+                          const int32_t* cut_ptr, const float* cut_values, uint16_t* cols,
+                          hipStream_t s);
 // Histograms from the present-value layout: work items as for launch_hist,
 // with `tile` a sparse tile; partial slots of tile_features * bin_stride * 2
 // words in the node histogram's layout.  Finished by launch_hist_reduce_flat.

@@ -27,9 +27,10 @@ namespace dp {
 namespace {
 
 // The split feature's bin of `row`: from the column-major copy when there is
-// one (one byte per row, contiguous within a feature), else from the tiles.
-template <bool COLS>
-__device__ __forceinline__ int split_bin_of(const uint8_t* __restrict__ bins, int64_t n_rows,
+// one (one symbol per row, contiguous within a feature; uint16 symbols for
+// matrices whose missing marker is kWideMissing), else from the tiles.
+template <bool COLS, typename SYM>
+__device__ __forceinline__ int split_bin_of(const SYM* __restrict__ bins, int64_t n_rows,
                                             int tile_width, uint32_t row, int feature) {
   if (COLS) return bins[int64_t(feature) * n_rows + row];
   const int64_t tile = feature / tile_width;
@@ -79,9 +80,9 @@ __device__ __forceinline__ void apply_leaf(const LeafPass& lp, const LeafWork w)
 // MARGIN (the last split level, LastLevel): each row's child leaf value is
 // stored into the leaf-value plane once the side is known; the rows of a node
 // that does not expand get the node's own leaf value.
-template <bool COLS, int G, bool MARGIN>
+template <bool COLS, int G, bool MARGIN, typename SYM = uint8_t>
 __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
-    const uint8_t* __restrict__ bins, int64_t n_rows, int tile_width, int missing_bin,
+    const SYM* __restrict__ bins, int64_t n_rows, int tile_width, int missing_bin,
     const uint32_t* __restrict__ ridx, const PartWork* __restrict__ work, int32_t n_work_host,
     const int32_t* __restrict__ n_work_dev, dp_split_record* __restrict__ splits,
     SplitSelect sel, const int32_t* __restrict__ node_first_work,
@@ -155,7 +156,8 @@ __global__ __launch_bounds__(kPartThreads) void part_count_kernel(
 #pragma unroll
     for (int k = 0; k < G; ++k) {
       const int64_t i = w.begin + int64_t(g0 + k) * kPartThreads + threadIdx.x;
-      bin[k] = i < w.end ? split_bin_of<COLS>(bins, n_rows, tile_width, row[k], s.feature) : -1;
+      bin[k] = i < w.end ? split_bin_of<COLS, SYM>(bins, n_rows, tile_width, row[k], s.feature)
+                         : -1;
       if constexpr (MARGIN) mrow[k] = row[k];
     }
     if (g0 + G < kPartSteps) load_rows(g0 + G);
@@ -268,7 +270,7 @@ void launch_leaf_positions(const uint32_t* ridx, const LeafWork* work, int32_t n
   DP_HIP(hipGetLastError());
 }
 
-void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_layout& layout,
+void launch_partition(const uint8_t* bins, const void* cols, const dp_bin_layout& layout,
                       const uint32_t* ridx_in, uint32_t* ridx_out, const PartWork* work,
                       int32_t n_work, const int32_t* n_work_dev, const int64_t* seg_begin,
                       dp_split_record* splits, const int32_t* node_first_work,
@@ -284,7 +286,8 @@ void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_lay
   const int64_t items = int64_t(n_work) + (lp.work ? lp.n_host : 0);
   const int gc = int(items < 2048 ? items : 2048);
   const int gw = n_work < 2048 ? n_work : 2048;
-  const uint8_t* src = cols ? cols : bins;
+  const bool wide = missing == kWideMissing;
+  need(!wide || cols, "16-bit symbols are read from the column copy");
   if (!node_left_zeroed) launch_fill_i64(node_left, n_nodes, 0, s);
   if (items <= 0) return;
   const SplitSelect sel = select ? *select : SplitSelect{};
@@ -292,18 +295,32 @@ void launch_partition(const uint8_t* bins, const uint8_t* cols, const dp_bin_lay
   const LastLevel ll = last ? *last : LastLevel{};
   need(!last || (ll.values && ll.nodes && ll.exps), "last-level leaf value arguments");
   auto pick = [&](auto k1, auto k2, auto k4) { return group == 4 ? k4 : (group == 2 ? k2 : k1); };
-  auto count =
-      cols ? (last ? pick(part_count_kernel<true, 1, true>, part_count_kernel<true, 2, true>,
-                          part_count_kernel<true, 4, true>)
-                   : pick(part_count_kernel<true, 1, false>, part_count_kernel<true, 2, false>,
-                          part_count_kernel<true, 4, false>))
-           : (last ? pick(part_count_kernel<false, 1, true>, part_count_kernel<false, 2, true>,
-                          part_count_kernel<false, 4, true>)
-                   : pick(part_count_kernel<false, 1, false>, part_count_kernel<false, 2, false>,
-                          part_count_kernel<false, 4, false>));
-  hipLaunchKernelGGL(count, dim3(gc), dim3(kPartThreads), 0, s, src, layout.n_rows,
-                     layout.tile_width, missing, ridx_in, work, n_work, n_work_dev, splits, sel,
-                     node_first_work, work_left, masks, lp, ll);
+  if (wide) {
+    auto count = last ? pick(part_count_kernel<true, 1, true, uint16_t>,
+                             part_count_kernel<true, 2, true, uint16_t>,
+                             part_count_kernel<true, 4, true, uint16_t>)
+                      : pick(part_count_kernel<true, 1, false, uint16_t>,
+                             part_count_kernel<true, 2, false, uint16_t>,
+                             part_count_kernel<true, 4, false, uint16_t>);
+    hipLaunchKernelGGL(count, dim3(gc), dim3(kPartThreads), 0, s,
+                       static_cast<const uint16_t*>(cols), layout.n_rows, layout.tile_width,
+                       missing, ridx_in, work, n_work, n_work_dev, splits, sel, node_first_work,
+                       work_left, masks, lp, ll);
+  } else {
+    const uint8_t* src = cols ? static_cast<const uint8_t*>(cols) : bins;
+    auto count =
+        cols ? (last ? pick(part_count_kernel<true, 1, true>, part_count_kernel<true, 2, true>,
+                            part_count_kernel<true, 4, true>)
+                     : pick(part_count_kernel<true, 1, false>, part_count_kernel<true, 2, false>,
+                            part_count_kernel<true, 4, false>))
+             : (last ? pick(part_count_kernel<false, 1, true>, part_count_kernel<false, 2, true>,
+                            part_count_kernel<false, 4, true>)
+                     : pick(part_count_kernel<false, 1, false>, part_count_kernel<false, 2, false>,
+                            part_count_kernel<false, 4, false>));
+    hipLaunchKernelGGL(count, dim3(gc), dim3(kPartThreads), 0, s, src, layout.n_rows,
+                       layout.tile_width, missing, ridx_in, work, n_work, n_work_dev, splits,
+                       sel, node_first_work, work_left, masks, lp, ll);
+  }
   DP_HIP(hipGetLastError());
   if (last) return;  // every child is a leaf: no new row order
   const ScatterArgs sa{ridx_in, ridx_out,   work,      n_work, n_work_dev, splits,

@@ -328,6 +328,83 @@ __global__ void sparse_fill_kernel(const uint8_t* __restrict__ bins, int64_t n_r
   }
 }
 
+// 16-bit column copy of a matrix whose missing values need a symbol beside 256
+// bins: cols[f * n_rows + r] = the bin of (r, f), kWideMissing for NaN.  A
+// thread bins one row of one 16-feature tile (the tile's cuts staged in LDS)
+// and stores its 16 symbols, so that for each feature a wavefront stores 64
+// adjacent symbols.
+__global__ __launch_bounds__(256) void bin_columns16_kernel(const float* __restrict__ values,
+                                                            int64_t n_rows, int32_t n_features,
+                                                            const int32_t* __restrict__ cut_ptr,
+                                                            const float* __restrict__ cut_values,
+                                                            uint16_t* __restrict__ cols) {
+  __shared__ float s_cuts[16 * kMaxBins];
+  __shared__ int s_count[16];
+  const int f0 = blockIdx.y * 16;
+  if (threadIdx.x < 16) {
+    const int f = f0 + int(threadIdx.x);
+    s_count[threadIdx.x] = f < n_features ? cut_ptr[f + 1] - cut_ptr[f] : 0;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < 16 * kMaxBins; e += blockDim.x) {
+    const int jf = e / kMaxBins, b = e % kMaxBins;
+    s_cuts[e] = b < s_count[jf] ? cut_values[cut_ptr[f0 + jf] + b] : 0.0f;
+  }
+  __syncthreads();
+  for (int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; r < n_rows;
+       r += int64_t(gridDim.x) * blockDim.x) {
+    for (int k = 0; k < 16 && f0 + k < n_features; ++k) {
+      const float x = values[r * n_features + f0 + k];
+      uint32_t b = uint32_t(kWideMissing);
+      if (x == x) {
+        const float* c = s_cuts + k * kMaxBins;
+        int lo = 0, hi = s_count[k];
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (c[mid] > x) hi = mid; else lo = mid + 1;
+        }
+        b = uint32_t(lo < s_count[k] ? lo : s_count[k] - 1);
+      }
+      cols[int64_t(f0 + k) * n_rows + r] = uint16_t(b);
+    }
+  }
+}
+
+// The present-value layout from 16-bit columns (missing: kWideMissing); one
+// thread per (sparse tile, row) as sparse_count_kernel / sparse_fill_kernel,
+// reading the tile's features of its row from the columns (adjacent threads,
+// adjacent rows).
+__global__ void sparse_count16_kernel(const uint16_t* __restrict__ cols, int64_t n_rows,
+                                      int32_t n_features, int32_t tile_features, int64_t n,
+                                      uint32_t* __restrict__ counts) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += int64_t(blockDim.x) * gridDim.x) {
+    int64_t r;
+    int32_t fb, fe;
+    sparse_tile_row(i, n_rows, n_features, tile_features, r, fb, fe);
+    uint32_t c = 0;
+    for (int32_t f = fb; f < fe; ++f) c += cols[int64_t(f) * n_rows + r] != kWideMissing ? 1u : 0u;
+    counts[i] = c;
+  }
+}
+
+__global__ void sparse_fill16_kernel(const uint16_t* __restrict__ cols, int64_t n_rows,
+                                     int32_t n_features, int32_t tile_features, int64_t n,
+                                     const uint32_t* __restrict__ ptr,
+                                     uint16_t* __restrict__ entries) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += int64_t(blockDim.x) * gridDim.x) {
+    int64_t r;
+    int32_t fb, fe;
+    sparse_tile_row(i, n_rows, n_features, tile_features, r, fb, fe);
+    uint32_t o = ptr[i];
+    for (int32_t f = fb; f < fe; ++f) {
+      const uint32_t b = cols[int64_t(f) * n_rows + r];
+      if (b != uint32_t(kWideMissing)) entries[o++] = uint16_t(uint32_t(f - fb) << 8 | b);
+    }
+  }
+}
+
 // counts[f][b] += rows of this workgroup's row range whose bin of feature f is
 // b, from the column copy.  Workgroup i takes row range i % blocks_per_feature
 // of feature i / blocks_per_feature; each wavefront counts into its own 256 LDS
@@ -393,19 +470,22 @@ int32_t sparse_tile_features(int32_t bin_stride) {
   return t < 16 ? 16 : t;
 }
 
-double build_sparse_bins(const uint8_t* bins, const dp_bin_layout& layout, int32_t bin_stride,
-                         double max_density, SparseBins& out, hipStream_t s) {
-  need(layout.tile_width == 16, "present-value layout needs 16-feature tiles");
-  need(layout.missing_bin == 255, "present-value layout needs missing values");
-  const int64_t N = layout.n_rows;
+namespace {
+
+// The present-value layout of an n_rows x n_features matrix in tiles of
+// sparse_tile_features(bin_stride): count(counts, n) writes the present
+// values of every (tile, row), fill(ptr, entries, n) writes the entries.
+// Built when their share is at most max_density (and the count fits 32-bit
+// offsets); returns the share.  Synchronises the stream.
+template <class Count, class Fill>
+double build_sparse(int64_t N, int32_t n_features, int32_t bin_stride, double max_density,
+                    SparseBins& out, hipStream_t s, Count count, Fill fill) {
   const int32_t tf = sparse_tile_features(bin_stride);
-  const int32_t T = (layout.n_features + tf - 1) / tf;
+  const int32_t T = (n_features + tf - 1) / tf;
   const int64_t n = N * T;
   DeviceBuffer<uint32_t> counts(size_t(n + 1)), ptr(size_t(n + 1));
   launch_fill_u8(reinterpret_cast<uint8_t*>(counts.p + n), sizeof(uint32_t), 0, s);
-  const dim3 grid(grid_for(n, 256, 16384));
-  hipLaunchKernelGGL(sparse_count_kernel, grid, dim3(256), 0, s, bins, N, layout.n_features, tf,
-                     n, layout.missing_bin, counts.p);
+  count(counts.p, tf, n);
   DP_HIP(hipGetLastError());
   // Exclusive scan over n + 1 counts (the last is 0): ptr[n] is the total.  A
   // 64-bit accumulator catches totals that do not fit 32-bit offsets.
@@ -426,11 +506,10 @@ double build_sparse_bins(const uint8_t* bins, const dp_bin_layout& layout, int32
   unsigned long long nnz = 0;
   DP_HIP(hipMemcpyAsync(&nnz, total.p, sizeof nnz, hipMemcpyDeviceToHost, s));
   DP_HIP(hipStreamSynchronize(s));
-  const double density = double(nnz) / (double(N) * double(layout.n_features));
+  const double density = double(nnz) / (double(N) * double(n_features));
   if (density > max_density || nnz >= (1ull << 32)) return density;
   DeviceBuffer<uint16_t> entries(size_t(nnz ? nnz : 1));
-  hipLaunchKernelGGL(sparse_fill_kernel, grid, dim3(256), 0, s, bins, N, layout.n_features, tf, n,
-                     layout.missing_bin, ptr.p, entries.p);
+  fill(ptr.p, entries.p, tf, n);
   DP_HIP(hipGetLastError());
   DP_HIP(hipStreamSynchronize(s));
   out.tile_features = tf;
@@ -439,6 +518,57 @@ double build_sparse_bins(const uint8_t* bins, const dp_bin_layout& layout, int32
   out.ptr = std::move(ptr);
   out.entries = std::move(entries);
   return density;
+}
+
+}  // namespace
+
+double build_sparse_bins(const uint8_t* bins, const dp_bin_layout& layout, int32_t bin_stride,
+                         double max_density, SparseBins& out, hipStream_t s) {
+  need(layout.tile_width == 16, "present-value layout needs 16-feature tiles");
+  need(layout.missing_bin == 255, "present-value layout needs missing values");
+  const int64_t N = layout.n_rows;
+  const int32_t F = layout.n_features;
+  const dim3 grid(grid_for(N * ((F + sparse_tile_features(bin_stride) - 1) /
+                                sparse_tile_features(bin_stride)), 256, 16384));
+  return build_sparse(
+      N, F, bin_stride, max_density, out, s,
+      [&](uint32_t* counts, int32_t tf, int64_t n) {
+        hipLaunchKernelGGL(sparse_count_kernel, grid, dim3(256), 0, s, bins, N, F, tf, n,
+                           layout.missing_bin, counts);
+      },
+      [&](const uint32_t* ptr, uint16_t* entries, int32_t tf, int64_t n) {
+        hipLaunchKernelGGL(sparse_fill_kernel, grid, dim3(256), 0, s, bins, N, F, tf, n,
+                           layout.missing_bin, ptr, entries);
+      });
+}
+
+void build_sparse_bins_wide(const uint16_t* cols, int64_t n_rows, int32_t n_features,
+                            int32_t bin_stride, SparseBins& out, hipStream_t s) {
+  const int32_t tf = sparse_tile_features(bin_stride);
+  const dim3 grid(grid_for(n_rows * ((n_features + tf - 1) / tf), 256, 16384));
+  const double density = build_sparse(
+      n_rows, n_features, bin_stride, 1.0, out, s,
+      [&](uint32_t* counts, int32_t t, int64_t n) {
+        hipLaunchKernelGGL(sparse_count16_kernel, grid, dim3(256), 0, s, cols, n_rows,
+                           n_features, t, n, counts);
+      },
+      [&](const uint32_t* ptr, uint16_t* entries, int32_t t, int64_t n) {
+        hipLaunchKernelGGL(sparse_fill16_kernel, grid, dim3(256), 0, s, cols, n_rows,
+                           n_features, t, n, ptr, entries);
+      });
+  need(out.n_tiles > 0,
+       "matrix has " + std::to_string(int64_t(density * double(n_rows) * double(n_features))) +
+           " present values: more than the 2^32 the present-value layout of a matrix with "
+           "missing values and 256 bins holds (use max_bin 255 or less)");
+}
+
+void launch_bin_columns16(const float* values, int64_t n_rows, int32_t n_features,
+                          const int32_t* cut_ptr, const float* cut_values, uint16_t* cols,
+                          hipStream_t s) {
+  if (n_rows <= 0 || n_features <= 0) return;
+  hipLaunchKernelGGL(bin_columns16_kernel, dim3(grid_for(n_rows, 256, 4096), (n_features + 15) / 16),
+                     dim3(256), 0, s, values, n_rows, n_features, cut_ptr, cut_values, cols);
+  DP_HIP(hipGetLastError());
 }
 
 void launch_any_nan(const float* values, int64_t n, int32_t* flag, hipStream_t s) {

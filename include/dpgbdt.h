@@ -188,7 +188,11 @@ int DPBoosterGetTuning(BoosterHandle handle, bst_ulong* out_len, const char** ou
 int DPValidateHyperparameters(const char* hyperparameters, uint32_t classes, bst_ulong* out_len,
                               const char** out);
 
-/* Quantile cuts and bins the booster trained on (built at first use). */
+/* Quantile cuts and bins the booster trained on (built at first use).
+ * *missing_bin: -1 without missing values, 255 when every feature has at most
+ * 255 bins (uint8 symbols, byte 255 = missing), 256 when the matrix has
+ * missing values and some feature uses all 256 bins (16-bit symbols, 256 =
+ * missing; the booster then builds every histogram from its present values). */
 int DPDMatrixGetCuts(DMatrixHandle handle, int32_t max_bin, int32_t* cut_ptr,
                      float* cut_values, bst_ulong capacity, int32_t* missing_bin);
 
@@ -226,7 +230,8 @@ int dp_sketch_cuts(dp_workspace ws, const float* values, int64_t n_rows, int32_t
                    int32_t* has_missing, void* stream);
 
 /* bins[r][f] = index of the first cut > x (clamped), missing_bin for NaN.
- * cut_ptr and cut_values are device arrays. */
+ * cut_ptr and cut_values are device arrays.  With missing_bin 255 every
+ * feature must have at most 255 bins (byte 255 is the missing marker). */
 int dp_bin_values(const float* values, const dp_bin_layout* layout, const int32_t* cut_ptr,
                   const float* cut_values, uint8_t* bins, void* stream);
 

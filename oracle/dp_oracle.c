@@ -147,22 +147,32 @@ static int32_t upper_bound(const float* cuts, int32_t count, float value) {
   return lo;
 }
 
+/* Bin symbols: uint8, or uint16 when missing_bin > 255 (a matrix with missing  */
+/* values some of whose features use all 256 bins: missing is then symbol 256). */
+static inline int32_t bin_at(const void* bins, int32_t missing_bin, int64_t i) {
+  return missing_bin > 255 ? (int32_t)((const uint16_t*)bins)[i]
+                           : (int32_t)((const uint8_t*)bins)[i];
+}
+
 void dpo_bin_matrix(const float* x, int64_t n, int64_t n_features, const int32_t* cut_ptr,
-                    const float* cut_values, int32_t missing_bin, uint8_t* bins) {
+                    const float* cut_values, int32_t missing_bin, void* bins) {
   const int threads = threads_for(n * n_features, 1 << 20);
 #pragma omp parallel for num_threads(threads) schedule(static)
   for (int64_t r = 0; r < n; ++r)
     for (int64_t f = 0; f < n_features; ++f) {
       float value = x[r * n_features + f];
-      uint8_t b;
+      int32_t b;
       if (isnan(value)) {
-        b = (uint8_t)missing_bin;
+        b = missing_bin;
       } else {
         int32_t count = cut_ptr[f + 1] - cut_ptr[f];
         int32_t idx = upper_bound(cut_values + cut_ptr[f], count, value);
-        b = (uint8_t)(idx < count ? idx : count - 1);
+        b = idx < count ? idx : count - 1;
       }
-      bins[r * n_features + f] = b;
+      if (missing_bin > 255)
+        ((uint16_t*)bins)[r * n_features + f] = (uint16_t)b;
+      else
+        ((uint8_t*)bins)[r * n_features + f] = (uint8_t)b;
     }
 }
 
@@ -263,14 +273,13 @@ double dpo_unscale(int32_t exp_q) { return ldexp(1.0, -exp_q); }
 /* f is b; missing entries are not accumulated (their stats are the node sum */
 /* minus the bin total, as upstream derives them).                           */
 /* ------------------------------------------------------------------------ */
-static void hist_rows(const uint8_t* bins, int64_t n_features, const int32_t* qg,
+static void hist_rows(const void* bins, int64_t n_features, const int32_t* qg,
                       const int32_t* qh, const uint32_t* rows, int64_t i0, int64_t i1,
                       int32_t bin_stride, int32_t missing_bin, int64_t* hist) {
   for (int64_t i = i0; i < i1; ++i) {
     int64_t r = rows ? (int64_t)rows[i] : i;
-    const uint8_t* row = bins + r * n_features;
     for (int64_t f = 0; f < n_features; ++f) {
-      uint8_t b = row[f];
+      int32_t b = bin_at(bins, missing_bin, r * n_features + f);
       if (b == missing_bin) continue;
       int64_t* cell = hist + 2 * (f * bin_stride + b);
       cell[0] += qg[r];
@@ -279,7 +288,7 @@ static void hist_rows(const uint8_t* bins, int64_t n_features, const int32_t* qg
   }
 }
 
-void dpo_hist(const uint8_t* bins, int64_t n_features, const int32_t* qg, const int32_t* qh,
+void dpo_hist(const void* bins, int64_t n_features, const int32_t* qg, const int32_t* qh,
               const uint32_t* rows, int64_t n_rows, int32_t bin_stride, int32_t missing_bin,
               int64_t* hist) {
   const int64_t cells = 2 * n_features * bin_stride;
@@ -476,13 +485,13 @@ void dpo_evaluate_split_masked(const int64_t* hist, int64_t n_features, int32_t 
 
 /* Stable partition of ridx[begin, end): rows whose bin <= split_bin (or that */
 /* are missing with default_left) first, in their original order.            */
-static int row_left(const uint8_t* bins, int64_t n_features, uint32_t r, int32_t feature,
+static int row_left(const void* bins, int64_t n_features, uint32_t r, int32_t feature,
                     int32_t split_bin, int32_t default_left, int32_t missing_bin) {
-  uint8_t b = bins[(int64_t)r * n_features + feature];
-  return b == missing_bin ? default_left : (int32_t)b <= split_bin;
+  const int32_t b = bin_at(bins, missing_bin, (int64_t)r * n_features + feature);
+  return b == missing_bin ? default_left : b <= split_bin;
 }
 
-int64_t dpo_partition(uint32_t* ridx, int64_t begin, int64_t end, const uint8_t* bins,
+int64_t dpo_partition(uint32_t* ridx, int64_t begin, int64_t end, const void* bins,
                       int64_t n_features, int32_t feature, int32_t split_bin,
                       int32_t default_left, int32_t missing_bin, uint32_t* scratch) {
   const int64_t n = end - begin;
@@ -642,7 +651,7 @@ void dpo_colsample(const dpo_sampling* s, int32_t depth, int32_t nid, int64_t n_
 /* ------------------------------------------------------------------------ */
 static void* xcalloc(size_t n, size_t s) { return calloc(n ? n : 1, s); }
 
-int dpo_grow_tree(const uint8_t* bins, int64_t n, int64_t n_features, const int32_t* cut_ptr,
+int dpo_grow_tree(const void* bins, int64_t n, int64_t n_features, const int32_t* cut_ptr,
                   const float* cut_values, int32_t missing_bin, const int32_t* qg,
                   const int32_t* qh, int32_t exp_g, int32_t exp_h, const dpo_params* p,
                   int32_t bin_stride, uint32_t* ridx, dpo_tree* t) {
@@ -650,7 +659,7 @@ int dpo_grow_tree(const uint8_t* bins, int64_t n, int64_t n_features, const int3
                                exp_g, exp_h, p, bin_stride, NULL, ridx, t);
 }
 
-int dpo_grow_tree_sampled(const uint8_t* bins, int64_t n, int64_t n_features,
+int dpo_grow_tree_sampled(const void* bins, int64_t n, int64_t n_features,
                           const int32_t* cut_ptr, const float* cut_values, int32_t missing_bin,
                           const int32_t* qg, const int32_t* qh, int32_t exp_g, int32_t exp_h,
                           const dpo_params* p, int32_t bin_stride, const dpo_sampling* smp,

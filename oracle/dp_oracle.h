@@ -13,7 +13,10 @@
  * open fixed explicitly (quantile definition, fixed-point rounding, tie rules).
  *
  * Layout conventions (shared with the HIP library through the C ABI):
- *   bins      : uint8, row-major [n_rows][n_features]; `missing_bin` marks NaN
+ *   bins      : row-major [n_rows][n_features] symbols; `missing_bin` marks NaN.
+ *               uint8 (missing_bin -1 or 255), or uint16 with missing_bin 256
+ *               for a matrix with missing values some of whose features use
+ *               all 256 bins (dpo_hist_parallel takes uint8 only)
  *   cut_ptr   : int32 [n_features + 1]; feature f owns cut_values[cut_ptr[f],
  *               cut_ptr[f+1]); its bin b holds x in [cut[b-1], cut[b])
  *   hist      : int64 [n_features][n_bins_stride][2] = (sum qg, sum qh)
@@ -62,7 +65,7 @@ int32_t dpo_get_threads(void);
 int dpo_compute_cuts(const float* x, int64_t n, int64_t n_features, int32_t max_bin,
                      int32_t* cut_ptr, float* cut_values, float* min_values);
 void dpo_bin_matrix(const float* x, int64_t n, int64_t n_features, const int32_t* cut_ptr,
-                    const float* cut_values, int32_t missing_bin, uint8_t* bins);
+                    const float* cut_values, int32_t missing_bin, void* bins);
 
 /* ---- objective gradients and the fixed-point quantiser ----------------- */
 float dpo_expf(float x);
@@ -75,7 +78,7 @@ void dpo_quantise(const float* g, const float* h, int64_t n, int64_t stride, int
 double dpo_unscale(int32_t exp_q);
 
 /* ---- histogram, subtraction ------------------------------------------- */
-void dpo_hist(const uint8_t* bins, int64_t n_features, const int32_t* qg, const int32_t* qh,
+void dpo_hist(const void* bins, int64_t n_features, const int32_t* qg, const int32_t* qh,
               const uint32_t* rows, int64_t n_rows, int32_t bin_stride, int32_t missing_bin,
               int64_t* hist);
 void dpo_hist_parallel(const uint8_t* bins, int64_t n_features, const int32_t* qg,
@@ -94,7 +97,7 @@ void dpo_evaluate_split_masked(const int64_t* hist, int64_t n_features, int32_t 
                                const int32_t* n_bins, int64_t gp, int64_t hp, double unscale_g,
                                double unscale_h, const dpo_params* p, const uint8_t* allowed,
                                dpo_split* out);
-int64_t dpo_partition(uint32_t* ridx, int64_t begin, int64_t end, const uint8_t* bins,
+int64_t dpo_partition(uint32_t* ridx, int64_t begin, int64_t end, const void* bins,
                       int64_t n_features, int32_t feature, int32_t split_bin,
                       int32_t default_left, int32_t missing_bin, uint32_t* scratch);
 
@@ -129,12 +132,12 @@ typedef struct {
   int32_t *seg_begin, *seg_end;   /* row segment of every node in ridx     */
 } dpo_tree;
 
-int dpo_grow_tree(const uint8_t* bins, int64_t n, int64_t n_features, const int32_t* cut_ptr,
+int dpo_grow_tree(const void* bins, int64_t n, int64_t n_features, const int32_t* cut_ptr,
                   const float* cut_values, int32_t missing_bin, const int32_t* qg,
                   const int32_t* qh, int32_t exp_g, int32_t exp_h, const dpo_params* p,
                   int32_t bin_stride, uint32_t* ridx, dpo_tree* out);
 /* As dpo_grow_tree with column sampling (s NULL: every feature everywhere). */
-int dpo_grow_tree_sampled(const uint8_t* bins, int64_t n, int64_t n_features,
+int dpo_grow_tree_sampled(const void* bins, int64_t n, int64_t n_features,
                           const int32_t* cut_ptr, const float* cut_values, int32_t missing_bin,
                           const int32_t* qg, const int32_t* qh, int32_t exp_g, int32_t exp_h,
                           const dpo_params* p, int32_t bin_stride, const dpo_sampling* s,

@@ -123,7 +123,27 @@ def params(eta=0.3, lam=1.0, alpha=0.0, gamma=0.0, min_child_weight=1.0, max_dep
 
 
 def effective_max_bin(max_bin, has_missing):
-    return min(max_bin, 255 if has_missing else 256)
+    """The bins the cuts are computed with: max_bin (at most 256) whether or not values are
+    missing (the missing marker gets a symbol of its own; see missing_symbol)."""
+    del has_missing
+    return min(max_bin, 256)
+
+
+def missing_symbol(cut_ptr, has_missing):
+    """The bin symbol that marks a missing value: -1 without missing values, 255 when every
+    feature has at most 255 bins (uint8 symbols), else 256 (uint16 symbols: some feature uses
+    all 256 bins and values are missing)."""
+    if not has_missing:
+        return -1
+    return 256 if int(np.diff(np.asarray(cut_ptr)).max()) > 255 else 255
+
+
+def _bins(bins, missing_bin):
+    """Contiguous symbols of the width missing_bin implies (uint16 for 256)."""
+    wide = missing_bin > 255
+    if not wide:
+        assert bins.dtype == np.uint8, "uint8 symbols expected"
+    return np.ascontiguousarray(bins, dtype=np.uint16 if wide else np.uint8)
 
 
 def compute_cuts(x, max_bin):
@@ -140,7 +160,7 @@ def compute_cuts(x, max_bin):
 def bin_matrix(x, cut_ptr, cuts, missing_bin):
     x = np.ascontiguousarray(x, dtype=np.float32)
     n, f = x.shape
-    bins = np.zeros((n, f), dtype=np.uint8)
+    bins = np.zeros((n, f), dtype=np.uint16 if missing_bin > 255 else np.uint8)
     load().dpo_bin_matrix(_p(x), n, f, _p(np.ascontiguousarray(cut_ptr, dtype=np.int32)),
                           _p(np.ascontiguousarray(cuts, dtype=np.float32)), missing_bin, _p(bins))
     return bins
@@ -185,7 +205,7 @@ def unscale(e):
 
 
 def hist(bins, qg, qh, rows=None, bin_stride=256, missing_bin=-1):
-    bins = np.ascontiguousarray(bins, dtype=np.uint8)
+    bins = _bins(bins, missing_bin)
     n, f = bins.shape
     out = np.zeros((f, bin_stride, 2), dtype=np.int64)
     r = None if rows is None else np.ascontiguousarray(rows, dtype=np.uint32)
@@ -227,7 +247,7 @@ def evaluate_split(hist_, n_bins, gp, hp, exp_g, exp_h, p):
 
 def partition(ridx, begin, end, bins, feature, split_bin, default_left, missing_bin):
     ridx = np.array(ridx, dtype=np.uint32, copy=True)
-    bins = np.ascontiguousarray(bins, dtype=np.uint8)
+    bins = _bins(bins, missing_bin)
     scratch = np.zeros(max(1, end - begin), dtype=np.uint32)
     nl = load().dpo_partition(_p(ridx), begin, end, _p(bins), bins.shape[1], feature, split_bin,
                               default_left, missing_bin, _p(scratch))
@@ -284,7 +304,7 @@ def evaluate_split_masked(hist_, n_bins, gp, hp, exp_g, exp_h, p, allowed):
 def grow_tree(bins, cut_ptr, cuts, missing_bin, qg, qh, exp_g, exp_h, p, bin_stride=256,
               smp=None):
     """One tree -> (dict of node arrays, final ridx); smp: column sampling (Sampling)."""
-    bins = np.ascontiguousarray(bins, dtype=np.uint8)
+    bins = _bins(bins, missing_bin)
     n, f = bins.shape
     ridx = np.arange(n, dtype=np.uint32)
     t = Tree()

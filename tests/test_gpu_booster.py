@@ -70,7 +70,7 @@ def _train_both(dp, oracle, device, config, n, f, objective, k, p, rounds, seed,
     has_missing = bool(np.isnan(x).any())
     eff = oracle.effective_max_bin(max_bin, has_missing)
     cut_ptr, cuts, _ = oracle.compute_cuts(x, eff)
-    mb = 255 if has_missing else -1
+    mb = oracle.missing_symbol(cut_ptr, has_missing)
     bins = oracle.bin_matrix(x, cut_ptr, cuts, mb)
     op = oracle.params(eta=p["eta"], lam=p.get("lam", 1.0), alpha=p.get("alpha", 0.0),
                        gamma=p.get("gamma", 0.0), min_child_weight=p.get("min_child_weight", 1.0),
@@ -984,9 +984,10 @@ def test_sampled_graph_replays_equal_direct_launches(dp, device):
 
 
 def test_max_bin_is_not_changed_silently(dp, device):
-    """max_bin above 256 is refused (bins are uint8); the saved configuration reports the bins
-    actually used: 256 on a matrix without missing values, 255 with them (byte 255 marks a
-    missing value)."""
+    """max_bin above 256 is refused; the saved configuration reports the bins used: 256 with
+    and without missing values (with them, a matrix some of whose features use all 256 bins
+    keeps 16-bit symbols, missing = 256), and a matrix whose features have fewer bins keeps
+    uint8 symbols with byte 255 for missing values."""
     import torch
     from dpgbdt import ops
 
@@ -995,15 +996,19 @@ def test_max_bin_is_not_changed_silently(dp, device):
     bst = dp.Booster({"objective": "binary:logistic", "max_bin": 1024}, [dtrain])
     with pytest.raises(dp.DPError, match="max_bin above 256"):
         bst.update(dtrain, 0)
-    for holes, used in ((False, "256"), (True, "255")):
+    for holes, max_bin, symbol in ((False, 256, -1), (True, 256, 256), (True, 200, 255)):
         v = values.clone()
         if holes:
             v[::3, 2] = float("nan")
         d = dp.DMatrix(v, labels)
-        b = dp.Booster({"objective": "binary:logistic", "max_bin": 256, "max_depth": 3}, [d])
+        b = dp.Booster({"objective": "binary:logistic", "max_bin": max_bin, "max_depth": 3}, [d])
         b.update(d, 0)
         cfg = json.loads(b.save_config())
-        assert cfg["learner"]["gradient_booster"]["updater"][0]["hist_train_param"]["max_bin"] == used
+        used = cfg["learner"]["gradient_booster"]["updater"][0]["hist_train_param"]["max_bin"]
+        assert used == str(max_bin)
+        cut_ptr, _, missing = d.cuts(max_bin)
+        assert missing == symbol and np.diff(cut_ptr).max() == max_bin
+
 
 
 @pytest.mark.parametrize("objective", ["multi:softprob", "multi:softmax"])
@@ -1175,3 +1180,36 @@ def test_train_one_iter_refuses_foreign_arrays(dp, device):
     # the booster is unharmed: a valid round still trains
     bst.boost(dtrain, 0, ok.clone(), torch.ones((n, 1), dtype=torch.float32, device=device))
     assert bst.num_boosted_rounds() == 1
+
+
+@pytest.mark.parametrize("record", [0, 1])
+def test_256_bins_with_missing_values(dp, oracle, device, record):
+    """The reference's default max_bin (256) on data with missing values
+    (native/class_native_training.cuh:24, :51): a C5-shaped matrix (200,000 x 1,000, N(0,1)
+    values, 10 % missing, squared error on the sum of 20 features) trains 256 bins per
+    feature, with the missing marker a symbol of its own, bit-exact against the oracle; the
+    saved configuration reports 256."""
+    import torch
+
+    n, f = 200_000, 1000
+    print(f"[booster] 256 bins with 10 % missing values, {n} x {f}, record {record}", flush=True)
+    g = torch.Generator(device="cpu").manual_seed(97)
+    x = torch.randn((n, f), generator=g)
+    x[torch.rand((n, f), generator=g) < 0.1] = float("nan")
+    cols = torch.randperm(f, generator=g)[:20]
+    y = torch.nan_to_num(x[:, cols], nan=0.0).sum(dim=1) + 0.1 * torch.randn(n, generator=g)
+    values, labels = x.to(device), y.to(device)
+    del x
+    p = {"max_depth": 6, "eta": 0.3}
+    bst, xs, o_trees, o_margin, pos, n = _train_both(dp, oracle, device, 5, n, f, 2, 1, p, 2, 0,
+                                                     values_labels=(values, labels),
+                                                     record=record)
+    _compare(bst, o_trees, o_margin, pos, n, 1)
+    cfg = json.loads(bst.save_config())
+    assert cfg["learner"]["gradient_booster"]["updater"][0]["hist_train_param"]["max_bin"] == "256"
+    assert bst.tuning()["layout"] == "present-value"
+    assert any(t["default_left"].any() for t in o_trees), "learned default direction unused"
+    # every feature has 256 bins, so missing values take symbol 256 (16-bit symbols)
+    cut_ptr, _, _ = oracle.compute_cuts(xs, 256)
+    assert np.diff(cut_ptr).min() == 256
+    assert oracle.missing_symbol(cut_ptr, True) == 256

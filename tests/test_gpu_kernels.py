@@ -23,7 +23,8 @@ def _prepare(dp, oracle, ws, values, max_bin=256):
 
     x = values.cpu().numpy()
     has_missing = bool(np.isnan(x).any())
-    eff = oracle.effective_max_bin(max_bin, has_missing)
+    # the operator API's uint8 bins keep byte 255 for missing values: at most 255 bins then
+    eff = min(max_bin, 255) if has_missing else min(max_bin, 256)
     cut_ptr, cuts, mins, gpu_missing = ops.sketch_cuts(ws, values, eff)
     o_ptr, o_cuts, o_mins = oracle.compute_cuts(x, eff)
     assert gpu_missing == has_missing

@@ -323,6 +323,77 @@ def test_tree_matches_independent_builder(oracle):
     np.testing.assert_array_equal(pred, np.array([leaf_of[i] for i in pos], np.float32))
 
 
+def _wide_case(oracle, n=600, seed=4):
+    """Missing values beside features that use all 256 bins: missing is symbol 256."""
+    rng = np.random.default_rng(seed)
+    x = np.stack([rng.normal(size=n), rng.permutation(n).astype(np.float64),
+                  rng.integers(0, 7, n)], axis=1).astype(np.float32)
+    x[rng.random(n) < 0.2, 0] = np.nan
+    x[rng.random(n) < 0.1, 1] = np.nan
+    cut_ptr, cuts, _ = oracle.compute_cuts(x, 256)
+    mb = oracle.missing_symbol(cut_ptr, True)
+    bins = oracle.bin_matrix(x, cut_ptr, cuts, mb)
+    g = rng.normal(size=n).astype(np.float32)
+    h = rng.uniform(0.05, 1.0, n).astype(np.float32)
+    eg, eh, qg, qh = oracle.quantise(g, h)[0]
+    return x, bins, cut_ptr, cuts, mb, qg, qh, eg, eh
+
+
+def test_wide_symbols_for_256_bins_with_missing(oracle):
+    """max_bin 256 on a matrix with missing values: features with more than 256 distinct
+    values get 256 bins, so the missing marker is symbol 256 in uint16 bins; the bins equal
+    searchsorted on the cuts, the histogram leaves missing rows out and puts bin 255's rows
+    in slot 255, and the partition at bin 255 sends every present row left and the missing
+    rows to the default side."""
+    x, bins, cut_ptr, cuts, mb, qg, qh, eg, eh = _wide_case(oracle)
+    nbf = np.diff(cut_ptr)
+    assert mb == 256 and bins.dtype == np.uint16 and nbf.max() == 256
+    assert oracle.missing_symbol(cut_ptr, False) == -1
+    assert oracle.missing_symbol(np.array([0, 255, 300]), True) == 255
+    for f in range(x.shape[1]):
+        c = cuts[cut_ptr[f]:cut_ptr[f + 1]]
+        ok = ~np.isnan(x[:, f])
+        np.testing.assert_array_equal(bins[ok, f],
+                                      np.minimum(np.searchsorted(c, x[ok, f], side="right"),
+                                                 c.size - 1))
+        assert np.all(bins[~ok, f] == 256)
+    assert (bins[:, 1] == 255).any()  # the top bin is used beside the missing marker
+    hist = oracle.hist(bins, qg, qh, bin_stride=256, missing_bin=mb)
+    for f in range(x.shape[1]):
+        keep = bins[:, f] != mb
+        ref = np.zeros((256, 2), np.int64)
+        np.add.at(ref[:, 0], bins[keep, f], qg[keep].astype(np.int64))
+        np.add.at(ref[:, 1], bins[keep, f], qh[keep].astype(np.int64))
+        np.testing.assert_array_equal(hist[f], ref)
+    ridx = np.arange(x.shape[0], dtype=np.uint32)
+    for dl in (0, 1):
+        out, nl = oracle.partition(ridx, 0, x.shape[0], bins, 1, 255, dl, mb)
+        present = ~np.isnan(x[:, 1])
+        left = present | (bool(dl) & ~present)
+        np.testing.assert_array_equal(out, np.concatenate([ridx[left], ridx[~left]]))
+        assert nl == left.sum()
+
+
+def test_wide_tree_matches_independent_builder(oracle):
+    """A tree over 256-bin features with missing values (uint16 symbols) equals the
+    independent brute-force builder's, node for node."""
+    x, bins, cut_ptr, cuts, mb, qg, qh, eg, eh = _wide_case(oracle, n=300, seed=7)
+    p = oracle.params(max_depth=3, eta=0.5)
+    tree, ridx = oracle.grow_tree(bins, cut_ptr, cuts, mb, qg, qh, eg, eh, p, bin_stride=256)
+    ref, nodes = _reference_tree(bins, qg, qh, cut_ptr, mb, oracle.unscale(eg), oracle.unscale(eh), p)
+    assert len(ref) == len(tree["left"]) > 1
+    for r in ref:
+        nid = r["nid"]
+        assert tree["left"][nid] == r["left"]
+        if r["left"] != -1:
+            assert (tree["right"][nid], tree["feature"][nid], tree["split_bin"][nid],
+                    tree["default_left"][nid]) == (r["right"], r["feature"], r["bin"], r["dl"])
+    pos = oracle.positions(tree, ridx, bins.shape[0])
+    leaf_of = {nid: tree["leaf_value"][nid] for nid in range(len(tree["left"]))}
+    np.testing.assert_array_equal(oracle.predict_tree(tree, x),
+                                  np.array([leaf_of[i] for i in pos], np.float32))
+
+
 def test_booster_reduces_logloss(oracle):
     rng = np.random.default_rng(0)
     n = 3000
