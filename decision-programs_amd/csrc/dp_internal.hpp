@@ -672,18 +672,32 @@ void launch_bin_values(const float* values, const dp_bin_layout& layout, const i
 // tile's histogram fills kSparseLdsBytes of LDS).  For tile t and row r the
 // row's present values in the tile are
 //   entries[ptr[t * n_rows + r] .. ptr[t * n_rows + r + 1])
-// in feature order, each (feature - t * tile_features) << 8 | bin.
+// in feature order, each the word index of its (feature, bin) in one LDS plane
+// of the tile's histogram: (feature - t * tile_features) * (bin_stride + 1) +
+// bin (one word of pad per feature; see hist_sparse_kernel).
 struct SparseBins {
   int32_t tile_features = 0, n_tiles = 0;  // n_tiles 0: not built
+  int32_t bin_stride = 0;                  // the stride the entries' indexes use
   int64_t nnz = 0;
   DeviceBuffer<uint32_t> ptr;      // [n_tiles * n_rows + 1]
   DeviceBuffer<uint16_t> entries;  // [nnz]
 };
 constexpr int64_t kSparseLdsBytes = 64 * 1024;
 // LDS of one present-value tile in the histogram kernel: g and h in planes of
-// their own, each feature's bins padded by one word (tile_features *
-// (bin_stride + 1) * 16 bytes, at most kSparseLdsBytes + 4 KiB).
-constexpr int64_t kSparseLdsAlloc = kSparseLdsBytes + 4 * 1024;
+// their own, each feature's bins padded by one word.  A plane holds
+// tile_features * (bin_stride + 1) words, at most kSparsePlaneWords for every
+// tile sparse_tile_features makes (tile_features * bin_stride <= 4096 and
+// tile_features <= 256), followed by kSparseTrashWords words that the
+// histogram kernel adds its masked lanes' values to (never read); the h plane
+// starts at word kSparsePlaneStride, so an entry's h address is its g address
+// plus an instruction offset.
+constexpr int64_t kSparsePlaneWords = 4352;
+constexpr int64_t kSparseTrashWords = 64;
+constexpr int64_t kSparsePlaneStride = kSparsePlaneWords + kSparseTrashWords;
+constexpr int64_t kSparseLdsAlloc = 2 * kSparsePlaneStride * 8;
+// Entries past the last one that the histogram kernel's aligned 8-byte loads
+// may read (their values are not used).
+constexpr int64_t kSparseEntryPad = 4;
 constexpr double kSparseDensity = 0.25;  // automatic use: at most this share present
 int32_t sparse_tile_features(int32_t bin_stride);
 // Counts the present values of `bins` (16-feature tiles, missing byte 255) and

@@ -357,23 +357,33 @@ __device__ __forceinline__ void evaluate_tile(const SparseEvalArgs& ev, const Hi
 // Histograms from the present-value layout (SparseBins): one work item = rows
 // [begin, end) of node `slot` for one sparse tile of tile_features features.
 // The tile's histogram lives in LDS as two planes, g then h, each
-// [feature][bin_stride + 1] int64 (dynamic LDS): a plane's words of one
-// feature are adjacent, so the 64-bit atomics of a wavefront spread over the
-// banks by bin, and the one-word pad per feature shifts each feature's bins by
-// one bank pair, so that features spread them too (interleaved (g, h) pairs
-// put a feature's g words 16 bytes apart, on half the bank pairs, and every
-// feature on the same ones: measured 2.2 LDS cycles per atomic instruction of
-// the dense layout's).  The store interleaves the planes into the node
-// histogram's [feature][bin][g, h] layout.  A lane takes one row at a time
-// and walks the row's present values in the tile (two 64-bit LDS atomics
-// each).  The lane's rows are software-pipelined three deep (loads of row
-// i + THREADS's first kSparsePre entries, row i + 2 * THREADS's entry range
-// and (g, h), row i + 3 * THREADS's row id in flight while row i is
-// accumulated), so that a row's dependent loads (row id -> range -> entries)
-// are never waited for in sequence: the row loop is bound by memory latency
-// otherwise (measured on C5's root pass: 75 % of wave cycles waiting, the LDS
-// far from its atomic roof).  Entries past kSparsePre are loaded kSparseBatch
-// at a time.  Per-lane trip counts differ; no barrier sits inside the row loop.
+// [feature][bin_stride + 1] int64 (dynamic LDS; the h plane at the fixed word
+// kSparsePlaneWords): a plane's words of one feature are adjacent, so the
+// 64-bit atomics of a wavefront spread over the banks by bin, and the one-word
+// pad per feature shifts each feature's bins by one bank pair, so that
+// features spread them too.  An entry is its word's index in a plane, so its
+// two atomics need one address.  The store interleaves the planes into the
+// node histogram's [feature][bin][g, h] layout.
+//
+// The entries are spread over the lanes, not the rows: a wavefront takes 64
+// rows at a time (rows begin + 64 (k * waves + wave) + lane), loads their
+// entry ranges and (g, h), and scans the ranges' lengths (a DPP scan) into
+// each row's first position in the rows' concatenated entries.  It then
+// takes those entries 128 positions per round, two adjacent ones per lane:
+// the rows whose first position falls in the round's window write their lane
+// into the wavefront's map (one word per position, tagged with the round so
+// that stale words from earlier rounds are ignored and nothing needs
+// clearing), every lane reads its two positions' words, and a DPP max-scan
+// carries each row to the positions after its first (rows increase with
+// position).  The lane then takes (g, h), and for gathered rows the entry
+// range's start, from the row's lane (ds_bpermute) and adds its entries.
+// Every lane thus does the same work whatever the rows' lengths (a per-row
+// walk runs at the pace of the wavefront's fullest row: 3.2 present values
+// per 64-feature tile on average at C5's density, up to 12), and on the root
+// pass the rows' entries are one contiguous run, read with coalesced loads.
+// LDS operations of one wavefront execute in order, so a lane reads the map
+// words other lanes wrote just before.  Per-lane trip counts are uniform; no
+// barrier sits inside the row loop.
 //
 // EVAL: an item that is its node's only chunk (partial < 0) also evaluates
 // the node from the LDS tile, and its sibling (parent >= 0; the sibling is
@@ -383,14 +393,30 @@ __device__ __forceinline__ void evaluate_tile(const SparseEvalArgs& ev, const Hi
 // features per step, one per 16-lane row with four bins per lane
 // (seg_evaluate).  The node's words (and the sibling's) are stored only with
 // ev.store, so on the tree's last split level such a node never leaves LDS.
-constexpr int kSparseBatch = 4;
-// Entries of a row loaded one row ahead: at C5's density (64-feature tiles, 5 %
-// present) a row holds more than 12 present values of a tile in about one
-// wavefront-row in a thousand.
-constexpr int kSparsePre = 12;
+// Entry positions per lane and round: four on contiguous rows (one aligned
+// 8-byte load), two on gathered rows (each position its own load and row base).
+template <bool GATHER>
+constexpr int kPosPerLane = GATHER ? 2 : 4;
+constexpr int kMapSlotsMax = 64 * 4;  // positions per round and wavefront, at most
+// Map word (16 bits): round tag << 8 | lane.  Tags run 0 .. kMapTagWrap - 1;
+// 0xffff marks a word no round has written.
+constexpr uint32_t kMapTagWrap = 255;
 // EVAL's workgroups: 512 threads, so that the evaluation's double arithmetic
 // has 128 registers without spilling while two workgroups share a CU.
 constexpr int kSparseEvalThreads = 512;
+
+// Inclusive max over the wavefront's lanes of non-negative values (row_shr 1,
+// 2, 4, 8, then row_bcast15 and row_bcast31; a lane without a source takes 0,
+// the identity, so each step is one max with a DPP operand).
+__device__ __forceinline__ uint32_t wave_inclusive_umax(uint32_t x) {
+  x = max(x, uint32_t(__builtin_amdgcn_update_dpp(0, int(x), 0x111, 0xf, 0xf, false)));
+  x = max(x, uint32_t(__builtin_amdgcn_update_dpp(0, int(x), 0x112, 0xf, 0xf, false)));
+  x = max(x, uint32_t(__builtin_amdgcn_update_dpp(0, int(x), 0x114, 0xf, 0xf, false)));
+  x = max(x, uint32_t(__builtin_amdgcn_update_dpp(0, int(x), 0x118, 0xf, 0xf, false)));
+  x = max(x, uint32_t(__builtin_amdgcn_update_dpp(0, int(x), 0x142, 0xa, 0xf, false)));
+  x = max(x, uint32_t(__builtin_amdgcn_update_dpp(0, int(x), 0x143, 0xc, 0xf, false)));
+  return x;
+}
 
 template <bool GATHER, bool EVAL, int THREADS>
 __global__ __launch_bounds__(THREADS) void hist_sparse_kernel(
@@ -401,81 +427,147 @@ __global__ __launch_bounds__(THREADS) void hist_sparse_kernel(
     unsigned long long* __restrict__ hist, unsigned long long* __restrict__ partial,
     SparseEvalArgs ev) {
   extern __shared__ unsigned long long lds_tile[];  // g plane, then h plane
+  constexpr int P = kPosPerLane<GATHER>;
+  constexpr int kMapSlots = 64 * P;  // positions per round
+  // Each wavefront's map of one round's kMapSlots positions (16-bit words,
+  // 8-byte aligned for the lanes' wide reads).
+  __shared__ uint2 lds_map[THREADS / 64][kMapSlotsMax / 4];
   const int32_t n_work = n_work_dev ? *n_work_dev : n_work_host;
   const int64_t slot_words = int64_t(tile_features) * bin_stride * 2;
-  const uint32_t ps = uint32_t(bin_stride) + 1u;        // plane words per feature
-  const uint32_t hoff = uint32_t(tile_features) * ps;  // the h plane's offset
+  const uint32_t ps = uint32_t(bin_stride) + 1u;         // plane words per feature
+  constexpr uint32_t hoff = uint32_t(kSparsePlaneStride);  // the h plane's offset
   const unsigned long long* const lds_h = lds_tile + hoff;
+  const uint32_t plane = uint32_t(tile_features) * ps;   // live words of a plane
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // lane l's words: positions P l .. P l + P - 1
+  uint16_t* const map = reinterpret_cast<uint16_t*>(lds_map[wave]);
+  // This lane's P words, read and cleared as one 4- or 8-byte access.
+  auto read_words = [&](uint32_t (&word)[4]) {
+    if constexpr (P == 4) {
+      const uint2 m = reinterpret_cast<const uint2*>(map)[lane];
+      word[0] = m.x & 0xffffu;
+      word[1] = m.x >> 16;
+      word[2] = m.y & 0xffffu;
+      word[3] = m.y >> 16;
+    } else {
+      const uint32_t m = reinterpret_cast<const uint32_t*>(map)[lane];
+      word[0] = m & 0xffffu;
+      word[1] = m >> 16;
+    }
+  };
+  auto clear_words = [&] {
+    if constexpr (P == 4) reinterpret_cast<uint2*>(map)[lane] = make_uint2(~0u, ~0u);
+    else reinterpret_cast<uint32_t*>(map)[lane] = ~0u;
+  };
+  clear_words();  // no round has written a word yet
+  uint32_t tag = 0;
+  // A masked position adds its values to the trash word of its lane.
+  const uint32_t trash = uint32_t(kSparsePlaneWords) + uint32_t(lane);
   for (int32_t item = blockIdx.x; item < n_work; item += gridDim.x) {
     const HistWork w = work[item];
     if (w.begin >= w.end) continue;  // padding item (uniform per workgroup)
     const int32_t f0 = w.tile * tile_features;
     const int32_t nf = f0 + tile_features < n_features ? tile_features : n_features - f0;
-    for (int e = threadIdx.x; e < int32_t(2 * hoff); e += THREADS) lds_tile[e] = 0ull;
+    for (uint32_t e = threadIdx.x; e < plane; e += THREADS) {
+      lds_tile[e] = 0ull;
+      lds_tile[hoff + e] = 0ull;
+    }
     __syncthreads();
     const uint32_t* tp = ptr + int64_t(w.tile) * n_rows;
-    auto row_of = [&](int64_t i) -> uint32_t {
-      return GATHER ? ridx[i] : uint32_t(i);
+    // The rows of block i0 (rows i0 + lane): entry range start, length and
+    // (g, h), loaded one block ahead (gathered row ids two blocks ahead).
+    // Loads are branch-free (indexes past the item clamped, their values
+    // masked), so that the compiler counts them and waits only for the ones a
+    // step needs.
+    struct Rows {
+      uint32_t b, c;
+      int2 q;
     };
-    auto range = [&](int64_t ii, uint32_t r, uint32_t& b, uint32_t& e, int2& q) {
-      if (ii < w.end) {
-        b = tp[r];
-        e = tp[r + 1];
-        q = gpair[r];
-      } else {
-        b = e = 0;
-        q = make_int2(0, 0);
+    auto row_id = [&](int64_t i0) -> uint32_t {
+      const int64_t i = i0 + lane;
+      return GATHER ? ridx[i < w.end ? i : w.end - 1] : uint32_t(i < w.end ? i : w.end - 1);
+    };
+    auto load_rows = [&](int64_t i0, uint32_t r) -> Rows {
+      const bool valid = i0 + lane < w.end;
+      const uint32_t b = tp[r], e = tp[r + 1];
+      const int2 q = gpair[r];
+      return Rows{b, valid ? e - b : 0u, valid ? q : make_int2(0, 0)};
+    };
+    int64_t i0 = w.begin + int64_t(wave) * 64;
+    uint32_t r_ahead = GATHER ? row_id(i0 + THREADS) : 0u;
+    Rows cur = load_rows(i0, row_id(i0));
+    for (; i0 < w.end; i0 += THREADS) {
+      const Rows nxt = load_rows(i0 + THREADS, GATHER ? r_ahead : row_id(i0 + THREADS));
+      if (GATHER) r_ahead = row_id(i0 + 2 * THREADS);
+      const int c = int(cur.c);
+      const int incl = wave_inclusive_sum32(c);
+      uint32_t first = uint32_t(incl - c);  // the row's first position
+      uint32_t total = uint32_t(__builtin_amdgcn_readlane(incl, 63));
+      // Gathered rows: position p of row v is entry base_v + p.
+      const uint32_t base = cur.b - first;
+      // Contiguous rows: the block's entries are one run from lane 0's b.
+      // Positions count from that entry rounded down to a multiple of 4
+      // (`shift` positions of the block before, masked), so that a lane's
+      // four positions are one aligned 8-byte load.
+      uint32_t shift = 0, a0 = 0;
+      if (!GATHER) {
+        const uint32_t b0 = uint32_t(__builtin_amdgcn_readfirstlane(cur.b));
+        shift = b0 & 3u;
+        a0 = b0 - shift;
+        first += shift;
+        total = total ? total + shift : 0u;
       }
-    };
-    auto first = [&](uint32_t b, uint32_t e, uint32_t (&v)[kSparsePre]) {
+      uint32_t carry = 0;  // the row of the position before the round's window
+      for (uint32_t j = 0; j < total; j += kMapSlots) {
+        // Rows whose first position falls in [j, j + kMapSlots) mark it.
+        if (c > 0 && first - j < uint32_t(kMapSlots)) map[first - j] = uint16_t(tag << 8 | lane);
+        __builtin_amdgcn_wave_barrier();
+        uint32_t word[4];
+        read_words(word);
+        __builtin_amdgcn_wave_barrier();
+        uint32_t run = 0, row[P];
 #pragma unroll
-      for (int k = 0; k < kSparsePre; ++k) v[k] = b + k < e ? entries[b + k] : 0u;
-    };
-    auto add = [&](uint32_t v, unsigned long long g, unsigned long long h) {
-      lds_u64* p = (lds_u64*)lds_tile + ((v >> 8) * ps + (v & 0xffu));
-      lds_add(p, g);
-      lds_add(p + hoff, h);
-    };
-    // Rows i, i + THREADS, ... of this lane, pipelined: while row i is
-    // accumulated, the first entries of row i + THREADS, the range and (g, h)
-    // of row i + 2 * THREADS and the row id of row i + 3 * THREADS are loaded.
-    int64_t i = w.begin + threadIdx.x;
-    uint32_t b0, e0, b1, e1, v0[kSparsePre];
-    int2 q0, q1;
-    range(i, i < w.end ? row_of(i) : 0u, b0, e0, q0);
-    first(b0, e0, v0);
-    range(i + THREADS, i + THREADS < w.end ? row_of(i + THREADS) : 0u, b1, e1, q1);
-    uint32_t r2 = i + 2 * THREADS < w.end ? row_of(i + 2 * THREADS) : 0u;
-    for (; i < w.end; i += THREADS) {
-      const int64_t i2 = i + 2 * THREADS, i3 = i + 3 * THREADS;
-      const uint32_t r3 = i3 < w.end ? row_of(i3) : 0u;
-      uint32_t b2, e2, v1[kSparsePre];
-      int2 q2;
-      range(i2, r2, b2, e2, q2);
-      first(b1, e1, v1);
-      const unsigned long long g = (unsigned long long)(long long)q0.x;
-      const unsigned long long h = (unsigned long long)(long long)q0.y;
+        for (int k = 0; k < P; ++k) {
+          run = max(run, (word[k] >> 8) == tag ? (word[k] & 63u) : 0u);
+          row[k] = run;
+        }
+        const uint32_t scan = wave_inclusive_umax(max(run, carry));
+        // the lanes before's rows (lane 0: the carry) bound this lane's
+        const uint32_t before =
+            uint32_t(__builtin_amdgcn_update_dpp(int(carry), int(scan), 0x138, 0xf, 0xf, false));
+        carry = uint32_t(__builtin_amdgcn_readlane(int(scan), 63));
+        if (++tag == kMapTagWrap) {  // uniform: start the tags again on a clean map
+          clear_words();
+          tag = 0;
+        }
+        const uint32_t p = j + uint32_t(P * lane);  // this lane's first position
+        uint32_t x[P];
+        if constexpr (!GATHER) {  // one aligned load of the four entries (past the end: a0's)
+          const uint2 v = *reinterpret_cast<const uint2*>(entries + a0 + (p < total ? p : 0u));
+          x[0] = v.x & 0xffffu;
+          x[1] = v.x >> 16;
+          x[2] = v.y & 0xffffu;
+          x[3] = v.y >> 16;
+        }
 #pragma unroll
-      for (int k = 0; k < kSparsePre; ++k)
-        if (b0 + k < e0) add(v0[k], g, h);
-      // A row with more than kSparsePre present values in the tile: the rest.
-      for (uint32_t j = b0 + kSparsePre; j < e0; j += kSparseBatch) {
-        uint32_t v[kSparseBatch];
-#pragma unroll
-        for (int k = 0; k < kSparseBatch; ++k) v[k] = j + k < e0 ? entries[j + k] : 0u;
-#pragma unroll
-        for (int k = 0; k < kSparseBatch; ++k)
-          if (j + k < e0) add(v[k], g, h);
+        for (int k = 0; k < P; ++k) {
+          const int vk = int(max(row[k], before));
+          const uint32_t pk = p + uint32_t(k);
+          const bool in = pk < total && pk >= shift;
+          // Every lane takes part in the row lane reads (a lane reads the value
+          // of another lane only while both are active), so they come before
+          // any masking.
+          const int g = __shfl(cur.q.x, vk, 64), h = __shfl(cur.q.y, vk, 64);
+          if (GATHER) {
+            const uint32_t bv = uint32_t(__shfl(int(base), vk, 64));
+            x[k] = entries[in ? bv + pk : 0u];
+          }
+          lds_u64* const at = (lds_u64*)lds_tile + (in ? x[k] : trash);
+          lds_add(at, (unsigned long long)(long long)g);
+          lds_add(at + hoff, (unsigned long long)(long long)h);
+        }
       }
-      b0 = b1;
-      e0 = e1;
-      q0 = q1;
-#pragma unroll
-      for (int k = 0; k < kSparsePre; ++k) v0[k] = v1[k];
-      b1 = b2;
-      e1 = e2;
-      q1 = q2;
-      r2 = r3;
+      cur = nxt;
     }
     __syncthreads();
     const bool direct = w.partial < 0;  // uniform per workgroup
@@ -832,8 +924,10 @@ void launch_hist_sparse(const SparseBins& sp, int64_t n_rows, int32_t n_features
   if (n_work <= 0) return;
   need(sp.n_tiles > 0, "present-value layout not built");
   need(bin_stride >= 1 && bin_stride <= kMaxBins, "histogram bin stride out of range");
-  const size_t lds = size_t(sp.tile_features) * size_t(bin_stride + 1) * 16;  // two planes
-  need(lds <= size_t(kSparseLdsAlloc), "sparse tile exceeds its LDS budget");
+  need(int64_t(sp.tile_features) * (bin_stride + 1) <= kSparsePlaneWords,
+       "sparse tile exceeds its LDS plane");
+  need(sp.bin_stride == bin_stride, "present-value entries were built for another bin stride");
+  const size_t lds = size_t(kSparseLdsAlloc);  // two planes at fixed offsets
   SparseEvalArgs ev{};
   if (eval) {
     need(bin_stride <= 64, "evaluation in the present-value pass needs at most 64 bins");

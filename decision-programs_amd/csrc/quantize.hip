@@ -305,9 +305,15 @@ __global__ void sparse_count_kernel(const uint8_t* __restrict__ bins, int64_t n_
   }
 }
 
+// An entry: the LDS plane word of (feature offset fo, bin b) with ps words per
+// feature (see SparseBins).
+__device__ __forceinline__ uint16_t sparse_entry(int32_t fo, uint32_t b, uint32_t ps) {
+  return uint16_t(uint32_t(fo) * ps + b);
+}
+
 __global__ void sparse_fill_kernel(const uint8_t* __restrict__ bins, int64_t n_rows,
                                    int32_t n_features, int32_t tile_features, int64_t n,
-                                   int32_t missing_bin, const uint32_t* __restrict__ ptr,
+                                   int32_t missing_bin, uint32_t ps, const uint32_t* __restrict__ ptr,
                                    uint16_t* __restrict__ entries) {
   for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
        i += int64_t(blockDim.x) * gridDim.x) {
@@ -322,7 +328,7 @@ __global__ void sparse_fill_kernel(const uint8_t* __restrict__ bins, int64_t n_r
       for (int k = 0; k < 16; ++k) {
         const int32_t f = d * 16 + k;
         const uint32_t b = (w[k >> 2] >> (8 * (k & 3))) & 0xffu;
-        if (f < fe && int32_t(b) != missing_bin) entries[o++] = uint16_t(uint32_t(f - fb) << 8 | b);
+        if (f < fe && int32_t(b) != missing_bin) entries[o++] = sparse_entry(f - fb, b, ps);
       }
     }
   }
@@ -390,7 +396,7 @@ __global__ void sparse_count16_kernel(const uint16_t* __restrict__ cols, int64_t
 
 __global__ void sparse_fill16_kernel(const uint16_t* __restrict__ cols, int64_t n_rows,
                                      int32_t n_features, int32_t tile_features, int64_t n,
-                                     const uint32_t* __restrict__ ptr,
+                                     uint32_t ps, const uint32_t* __restrict__ ptr,
                                      uint16_t* __restrict__ entries) {
   for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
        i += int64_t(blockDim.x) * gridDim.x) {
@@ -400,7 +406,7 @@ __global__ void sparse_fill16_kernel(const uint16_t* __restrict__ cols, int64_t 
     uint32_t o = ptr[i];
     for (int32_t f = fb; f < fe; ++f) {
       const uint32_t b = cols[int64_t(f) * n_rows + r];
-      if (b != uint32_t(kWideMissing)) entries[o++] = uint16_t(uint32_t(f - fb) << 8 | b);
+      if (b != uint32_t(kWideMissing)) entries[o++] = sparse_entry(f - fb, b, ps);
     }
   }
 }
@@ -508,12 +514,13 @@ double build_sparse(int64_t N, int32_t n_features, int32_t bin_stride, double ma
   DP_HIP(hipStreamSynchronize(s));
   const double density = double(nnz) / (double(N) * double(n_features));
   if (density > max_density || nnz >= (1ull << 32)) return density;
-  DeviceBuffer<uint16_t> entries(size_t(nnz ? nnz : 1));
+  DeviceBuffer<uint16_t> entries(size_t(nnz + kSparseEntryPad));
   fill(ptr.p, entries.p, tf, n);
   DP_HIP(hipGetLastError());
   DP_HIP(hipStreamSynchronize(s));
   out.tile_features = tf;
   out.n_tiles = T;
+  out.bin_stride = bin_stride;
   out.nnz = int64_t(nnz);
   out.ptr = std::move(ptr);
   out.entries = std::move(entries);
@@ -538,7 +545,7 @@ double build_sparse_bins(const uint8_t* bins, const dp_bin_layout& layout, int32
       },
       [&](const uint32_t* ptr, uint16_t* entries, int32_t tf, int64_t n) {
         hipLaunchKernelGGL(sparse_fill_kernel, grid, dim3(256), 0, s, bins, N, F, tf, n,
-                           layout.missing_bin, ptr, entries);
+                           layout.missing_bin, uint32_t(bin_stride + 1), ptr, entries);
       });
 }
 
@@ -554,7 +561,7 @@ void build_sparse_bins_wide(const uint16_t* cols, int64_t n_rows, int32_t n_feat
       },
       [&](const uint32_t* ptr, uint16_t* entries, int32_t t, int64_t n) {
         hipLaunchKernelGGL(sparse_fill16_kernel, grid, dim3(256), 0, s, cols, n_rows,
-                           n_features, t, n, ptr, entries);
+                           n_features, t, n, uint32_t(bin_stride + 1), ptr, entries);
       });
   need(out.n_tiles > 0,
        "matrix has " + std::to_string(int64_t(density * double(n_rows) * double(n_features))) +
