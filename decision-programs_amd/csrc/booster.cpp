@@ -583,9 +583,11 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     a.n_tiles = T;
     a.hist_tiles = level_cfg_.tiles;
     a.hist_items = level_cfg_.items;
-    // Histogram workgroups resident at once: two per CU with one 64 KiB tile
-    // per item (dense or present-value), one with two dense tiles.
-    a.hist_slots = cus_ * (sparse_ || level_cfg_.tiles == 1 ? 2 : 1);
+    // Histogram workgroups resident at once: two per CU for present-value
+    // tiles; for dense tiles, what the level kernel's LDS and registers allow.
+    a.hist_slots = sparse_ ? cus_ * 2
+                           : hist_resident(true, L.missing_bin >= 0, skip_tiles_ != nullptr,
+                                           level_cfg_);
     a.hist_elems = S;
     a.part_chunk = chunk_;
     a.leaf_chunk = chunk_;
@@ -794,7 +796,7 @@ void Booster::set_param(const std::string& key, const std::string& value) {
       "colsample_bynode", "base_score", "boost_from_average", "seed", "seed_per_iteration",
       "nthread", "verbosity", "validate_parameters", "grow_policy", "dp_record_positions",
       "dp_graphs", "dp_sparse_hist", "dp_concurrent_trees", "dp_autotune", "dp_hist_tiles",
-      "dp_hist_unroll", "dp_hist_items", "dp_hist_split", "dp_skip_bin"};
+      "dp_hist_unroll", "dp_hist_items", "dp_hist_split", "dp_hist_deep", "dp_skip_bin"};
   bool ok = false;
   for (const char* k : known) ok = ok || key == k;
   need(ok, "unsupported parameter: " + key);
@@ -843,6 +845,11 @@ void Booster::set_param(const std::string& key, const std::string& value) {
     const int32_t m = parse_int(key, value);
     need(m == 0 || m == 4 || m == 5, "dp_hist_split must be 0, 4 or 5");
     forced_hist_.split = m;
+  }
+  if (key == "dp_hist_deep") {
+    const int32_t m = parse_int(key, value);
+    need(m == 0 || m == 1, "dp_hist_deep must be 0 or 1");
+    forced_hist_.deep = m;
   }
   if (key == "dp_sparse_hist") {
     const int32_t m = parse_int(key, value);
@@ -1064,7 +1071,7 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
                                   uint64_t(concurrent_trees_), uint64_t(autotune_),
                                   uint64_t(forced_hist_.tiles), uint64_t(forced_hist_.unroll),
                                   uint64_t(forced_hist_.items), uint64_t(forced_hist_.split),
-                                  uint64_t(skip_mode_)};
+                                  uint64_t(forced_hist_.deep), uint64_t(skip_mode_)};
   auto words = [](std::vector<uint64_t>& v, const void* p, size_t n) {
     for (size_t i = 0; i < n; i += 8) {
       uint64_t w = 0;
@@ -1114,11 +1121,14 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
   // Histogram launch shapes: forced by dp_hist_* (0 = default for the rest),
   // else tuned on this matrix shape (once per process), else the defaults.
   HistConfig root_cfg, level_cfg;
-  if (forced_hist_.tiles || forced_hist_.unroll || forced_hist_.items || forced_hist_.split) {
+  if (forced_hist_.tiles || forced_hist_.unroll || forced_hist_.items || forced_hist_.split ||
+      forced_hist_.deep) {
+    need(!(forced_hist_.deep && forced_hist_.split), "dp_hist_deep 1 needs dp_hist_split 0");
     if (forced_hist_.tiles) root_cfg.tiles = forced_hist_.tiles;
     if (forced_hist_.unroll) root_cfg.unroll = forced_hist_.unroll;
     if (forced_hist_.items) root_cfg.items = forced_hist_.items;
     root_cfg.split = forced_hist_.split;
+    root_cfg.deep = forced_hist_.deep;
     level_cfg = root_cfg;
     tuning_report_ = "{\"forced\":true}";
   } else if (autotune_) {

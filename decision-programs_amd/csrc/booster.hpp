@@ -282,7 +282,7 @@ class Booster {
   bool record_positions_ = false;
   bool use_graphs_ = true;
   bool autotune_ = true;        // dp_autotune: time the histogram launch shapes (tune.cpp)
-  HistConfig forced_hist_{0, 0, 0, 0};  // dp_hist_tiles / _unroll / _items / _split; 0 = not forced
+  HistConfig forced_hist_{0, 0, 0, 0, 0};  // dp_hist_tiles / _unroll / _items / _split / _deep; 0 = not forced
   std::string tuning_report_ = "{}";
   int32_t sparse_mode_ = 1;  // dp_sparse_hist: 0 never, 1 when <= 1/4 present, 2 with any NaN
   // dp_skip_bin (matrices without missing values): 0 never, 1 when the skip

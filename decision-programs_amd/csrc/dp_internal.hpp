@@ -289,6 +289,7 @@ struct HistConfig {
   int32_t unroll = 2;
   int32_t items = 1024;
   int32_t split = 0;
+  int32_t deep = 0;  // 1: three blocks of rows in flight per workgroup (split 0 only)
 };
 
 // Histograms: every work item accumulates into hist[slot]; hist must be zero.
@@ -302,6 +303,9 @@ struct HistConfig {
 // feature-major, [16 features][bin_stride][g, h] (the node histogram's layout
 // restricted to the tile), for launch_reduce_evaluate_dense; otherwise as the
 // LDS image [bin][g of 16 features, h of 16 features] (launch_hist_reduce).
+// Histogram workgroups the device holds at once for launch_hist's kernel of
+// this configuration (gathered or contiguous rows; missing values; skip bins).
+int hist_resident(bool gather, bool missing, bool skip, const HistConfig& cfg);
 void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t* gpair,
                  const uint32_t* ridx, const HistWork* work, int32_t n_work,
                  const int32_t* n_work_dev, int32_t bin_stride, int64_t* hist,

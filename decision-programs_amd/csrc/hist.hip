@@ -101,12 +101,24 @@ constexpr int kHistThreads = 1024;
 // (g, h) masked to zero.  With MISSING, lanes whose byte is 255 (missing; such
 // matrices have at most 255 bins) skip the atomics by exec mask, which keeps
 // sparse data (C5: 95 % missing) from spending LDS cycles on absent values.
-// Contiguous rows (GATHER false) are loaded and accumulated block by block (the
-// resident waves of a CU hide the load latency; the loop is bound by the LDS
-// atomics); gathered rows (GATHER true) load their row ids two blocks ahead and
-// the bins and gradients one block ahead.  Workgroups loop over items (item =
-// blockIdx.x + k * gridDim.x); with a grid that is a multiple of 8, item i
-// still runs on XCD i mod 8.
+// The rows of an item are taken in blocks of kHistThreads * U, through a ring
+// of PD + 1 register buffers: while a block is accumulated, the bins and
+// gradients of the next PD blocks are in flight (PD: the prefetch depth), and
+// gathered rows (GATHER) load their row ids PD + 1 blocks ahead of their data.
+// Loads return in order for the memory counter, so waiting for a row id also
+// waits for every older load; the row id of block j is issued after the data
+// of block j - PD - 1, which is accumulated before block j's data is issued,
+// so that wait costs nothing.  DEEP false: PD 1 for gathered rows, 0 for
+// contiguous rows (loaded and accumulated block by block; with two resident
+// workgroups per CU the other workgroup's waves hide the load latency).  DEEP
+// true: PD 3, which keeps about 3 * 1024 rows of loads in flight per workgroup
+// -- what the measured load latency of the gathered levels needs at the LDS
+// rate when a level has fewer items than CUs (one workgroup per CU, nothing
+// else to hide the latency).  DEEP costs registers (two workgroups per CU may
+// no longer fit; the launcher reads the occupancy).  Blocks past the item's
+// end are loaded clamped (in bounds) and not accumulated.  Workgroups loop
+// over items (item = blockIdx.x + k * gridDim.x); with a grid that is a
+// multiple of 8, item i still runs on XCD i mod 8.
 //
 // SPLIT (two tiles per item only; 0, 4 or 5): lanes whose bit SPLIT of the
 // lane index is set take the item's two tiles in the other order.  Each
@@ -121,8 +133,8 @@ constexpr int kHistThreads = 1024;
 // bins', which the split evaluation restores).  On data dominated by one value
 // per feature (C4's zero pixels) this removes most atomics and their
 // same-address conflicts.  MODE 1 is the missing-byte skip above; MODE 0 none.
-template <bool GATHER, int MODE, int TPW, int U, int SPLIT = 0>
-__global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8 / TPW, 8 / TPW))) void hist_kernel(
+template <bool GATHER, int MODE, int TPW, int U, int SPLIT = 0, bool DEEP = false>
+__global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(DEEP ? 4 : 8 / TPW, 8 / TPW))) void hist_kernel(
     const uint8_t* __restrict__ bins, const uint8_t* __restrict__ skip, int64_t n_rows,
     int32_t n_features, int32_t n_tiles,
     const int2* __restrict__ gpair, const uint32_t* __restrict__ ridx,
@@ -132,6 +144,8 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8 
     int64_t tile_step, int64_t row_step, int32_t fmaj) {
   extern __shared__ unsigned long long lds[];  // TPW * kLdsWords
   constexpr int64_t kStep = int64_t(kHistThreads) * U;
+  constexpr int PD = DEEP ? 3 : (GATHER ? 1 : 0);  // prefetch depth (blocks)
+  constexpr int R = PD + 1;                         // ring buffers
   // The first item is loaded alongside the device count (the host bound keeps
   // it in range), so the two loads overlap instead of chaining.
   const HistWork w_first =
@@ -175,9 +189,9 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8 
   const uint8_t* tile = bins + int64_t(w.tile) * tile_step;  // row r at tile + r * row_step
   const int64_t last = w.end - 1;
   const int64_t lane = threadIdx.x;
-  uint32_t rows[2][U];  // GATHER: row ids of the block after the next
-  uint4 v[2][U][TPW];
-  int2 q[2][U];
+  uint32_t rows[R][U];  // GATHER: row ids
+  uint4 v[R][U][TPW];
+  int2 q[R][U];
   auto fetch_rows = [&](int b, int64_t base) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -223,24 +237,28 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(8 
       }
     }
   };
-  // The loop bound is uniform per workgroup; buffer indices are static.
+  // The loop bound and the block guards are uniform per workgroup; buffer
+  // indices are static (buffer j % R holds block j of the item).
   const int64_t b0 = w.begin;
   if (GATHER) {
-    fetch_rows(0, b0);
-    fetch_rows(1, b0 + kStep);
-    fetch_data(0, b0);
-    for (int64_t blk = b0; blk < w.end; blk += 2 * kStep) {
-      fetch_rows(0, blk + 2 * kStep);
-      fetch_data(1, blk + kStep);
-      process(0, blk);
-      fetch_rows(1, blk + 3 * kStep);
-      fetch_data(0, blk + 2 * kStep);
-      process(1, blk + kStep);
+#pragma unroll
+    for (int j = 0; j < R; ++j) fetch_rows(j, b0 + j * kStep);
+#pragma unroll
+    for (int j = 0; j < PD; ++j) {
+      fetch_data(j, b0 + j * kStep);
+      fetch_rows(j, b0 + (j + R) * kStep);
     }
   } else {
-    for (int64_t blk = b0; blk < w.end; blk += kStep) {
-      fetch_data(0, blk);
-      process(0, blk);
+#pragma unroll
+    for (int j = 0; j < PD; ++j) fetch_data(j, b0 + j * kStep);
+  }
+  for (int64_t blk = b0; blk < w.end; blk += R * kStep) {
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      const int n = (k + PD) % R;  // the buffer of block k + PD
+      fetch_data(n, blk + (k + PD) * kStep);
+      if (GATHER) fetch_rows(n, blk + (k + PD + R) * kStep);
+      if (k == 0 || blk + k * kStep < w.end) process(k, blk + k * kStep);
     }
   }
   __syncthreads();
@@ -806,6 +824,12 @@ int32_t make_hist_work(const dp_bin_layout& layout, const int64_t* begin, const 
 namespace {
 template <bool GATHER, int MODE>
 auto hist_instance(const HistConfig& cfg) {
+  if (cfg.deep)
+    return cfg.tiles == 2
+               ? (cfg.unroll == 1 ? hist_kernel<GATHER, MODE, 2, 1, 0, true>
+                                  : hist_kernel<GATHER, MODE, 2, 2, 0, true>)
+               : (cfg.unroll == 1 ? hist_kernel<GATHER, MODE, 1, 1, 0, true>
+                                  : hist_kernel<GATHER, MODE, 1, 2, 0, true>);
   if (cfg.tiles == 2) {
     if (cfg.split == 4)
       return cfg.unroll == 1 ? hist_kernel<GATHER, MODE, 2, 1, 4>
@@ -824,7 +848,46 @@ auto hist_mode(int mode, const HistConfig& cfg) {
   return mode == 1 ? hist_instance<GATHER, 1>(cfg)
                    : (mode == 2 ? hist_instance<GATHER, 2>(cfg) : hist_instance<GATHER, 0>(cfg));
 }
+
+// Raises the kernel's dynamic LDS limit when it needs more than the default
+// 64 KiB, and returns how many of its workgroups one CU holds at once (LDS
+// and registers); once per kernel.
+int prepare_hist_kernel(const void* k, size_t lds) {
+  static std::mutex lock;
+  static std::vector<std::pair<const void*, int>> known;
+  std::lock_guard<std::mutex> hold(lock);
+  for (const auto& e : known)
+    if (e.first == k) return e.second;
+  if (lds > 65536)
+    DP_HIP(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
+  int per_cu = 0;
+  DP_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, kHistThreads, lds));
+  need(per_cu >= 1, "histogram kernel does not fit a CU");
+  known.emplace_back(k, per_cu);
+  return per_cu;
+}
+
+int device_cus() {
+  static std::mutex lock;
+  static int cached[64] = {};
+  int dev = 0;
+  DP_HIP(hipGetDevice(&dev));
+  need(dev >= 0 && dev < 64, "device index out of range");
+  std::lock_guard<std::mutex> hold(lock);
+  if (cached[dev] == 0)
+    DP_HIP(hipDeviceGetAttribute(&cached[dev], hipDeviceAttributeMultiprocessorCount, dev));
+  return cached[dev];
+}
+
+int mode_of(bool missing, bool skip) { return missing ? 1 : (skip ? 2 : 0); }
 }  // namespace
+
+int hist_resident(bool gather, bool missing, bool skip, const HistConfig& cfg) {
+  const int mode = mode_of(missing, skip);
+  auto kernel = gather ? hist_mode<true>(mode, cfg) : hist_mode<false>(mode, cfg);
+  const size_t lds = size_t(cfg.tiles) * kLdsWords * sizeof(unsigned long long);
+  return prepare_hist_kernel(reinterpret_cast<const void*>(kernel), lds) * device_cus();
+}
 
 void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t* gpair,
                  const uint32_t* ridx, const HistWork* work, int32_t n_work,
@@ -835,16 +898,12 @@ void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t
   need(bin_stride >= 1 && bin_stride <= kMaxBins, "histogram bin stride out of range");
   need(layout.tile_width == kTile, "histogram kernel needs 16-feature tiles");
   need((cfg.tiles == 1 || cfg.tiles == 2) && (cfg.unroll == 1 || cfg.unroll == 2) &&
-           (cfg.split == 0 || cfg.split == 4 || cfg.split == 5),
+           (cfg.split == 0 || cfg.split == 4 || cfg.split == 5) &&
+           (cfg.deep == 0 || (cfg.deep == 1 && cfg.split == 0)),
        "histogram configuration out of range");
   auto* out = reinterpret_cast<unsigned long long*>(hist);
   auto* part = reinterpret_cast<unsigned long long*>(partial);
   const auto* gp = reinterpret_cast<const int2*>(gpair);
-  // At most two rounds of resident workgroups (two per CU with one tile per
-  // item, one with two tiles); a multiple of 8.
-  const int resident = cfg.tiles == 1 ? 512 : 256;
-  int grid = n_work < 2 * resident ? n_work : 2 * resident;
-  grid = (grid + 7) / 8 * 8;
   // A missing value's byte 255 must not alias a real bin.
   if (layout.missing_bin >= 0) {
     need(layout.missing_bin == 255, "missing bin must be 255");
@@ -856,19 +915,14 @@ void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t
   const int64_t row_step = rows ? int64_t(layout.n_tiles) * kTile : kTile;
   const bool missing = layout.missing_bin >= 0;
   need(!(missing && skip), "skip bins apply to matrices without missing values");
-  const int mode = missing ? 1 : (skip ? 2 : 0);
+  const int mode = mode_of(missing, skip != nullptr);
   auto kernel = ridx ? hist_mode<true>(mode, cfg) : hist_mode<false>(mode, cfg);
   const size_t lds = size_t(cfg.tiles) * kLdsWords * sizeof(unsigned long long);
-  if (lds > 65536) {  // beyond the default dynamic LDS limit (once per instantiation)
-    static std::mutex lock;
-    static std::vector<const void*> raised;
-    std::lock_guard<std::mutex> hold(lock);
-    const void* k = reinterpret_cast<const void*>(kernel);
-    if (std::find(raised.begin(), raised.end(), k) == raised.end()) {
-      DP_HIP(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
-      raised.push_back(k);
-    }
-  }
+  // At most two rounds of resident workgroups; a multiple of 8.
+  const int resident =
+      prepare_hist_kernel(reinterpret_cast<const void*>(kernel), lds) * device_cus();
+  int grid = n_work < 2 * resident ? n_work : 2 * resident;
+  grid = (grid + 7) / 8 * 8;
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(kHistThreads), lds, s, src, skip, layout.n_rows,
                      layout.n_features, layout.n_tiles, gp, ridx, work, n_work, n_work_dev,
                      bin_stride, out, part, tile_step, row_step, fmaj ? 1 : 0);

@@ -10,6 +10,10 @@
 //   rows per lane per pipeline step   1 or 2;
 //   with two tiles, the lane bit (4, 5 or none) that swaps a lane's tile
 //                         order (fewer lanes per (feature, bin) per atomic);
+//   without that swap, the prefetch depth: one block of rows in flight per
+//                         workgroup (gathered rows; none for contiguous rows)
+//                         or three (more registers, possibly fewer resident
+//                         workgroups; for passes with few items per CU);
 //   work items per pass   512, 1024 or 2048 (fewer, longer row chunks write
 //                         fewer partial tiles; more balance the CUs better).
 // The contiguous (root) pass is timed over the whole matrix; the gathered pass
@@ -45,18 +49,22 @@ std::vector<HistConfig> dense_candidates(int32_t n_tiles) {
     if (tiles > n_tiles) continue;
     for (int32_t split : {0, 4, 5}) {
       if (tiles == 1 && split) continue;
-      for (int32_t unroll : {1, 2})
-        for (int32_t items : {512, 1024, 2048})
-          c.push_back(HistConfig{tiles, unroll, items, split});
+      for (int32_t deep : {0, 1}) {
+        if (deep && split) continue;
+        for (int32_t unroll : {1, 2})
+          for (int32_t items : {512, 1024, 2048})
+            c.push_back(HistConfig{tiles, unroll, items, split, deep});
+      }
     }
   }
   return c;
 }
 
 std::string config_json(const HistConfig& c) {
-  char b[112];
-  std::snprintf(b, sizeof b, "{\"tiles\":%d,\"unroll\":%d,\"items\":%d,\"split\":%d}", c.tiles,
-                c.unroll, c.items, c.split);
+  char b[128];
+  std::snprintf(b, sizeof b,
+                "{\"tiles\":%d,\"unroll\":%d,\"items\":%d,\"split\":%d,\"deep\":%d}", c.tiles,
+                c.unroll, c.items, c.split, c.deep);
   return b;
 }
 

@@ -14,9 +14,10 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = [dict(zip(("dp_hist_tiles", "dp_hist_unroll", "dp_hist_items", "dp_hist_split"), c))
-          for c in itertools.product((1, 2), (1, 2), (512, 1024, 2048), (0, 4, 5))
-          if c[0] == 2 or c[3] == 0]
+SHAPES = [dict(zip(("dp_hist_tiles", "dp_hist_unroll", "dp_hist_items", "dp_hist_split",
+                    "dp_hist_deep"), c))
+          for c in itertools.product((1, 2), (1, 2), (512, 1024, 2048), (0, 4, 5), (0, 1))
+          if (c[0] == 2 or c[3] == 0) and (c[3] == 0 or c[4] == 0)]
 
 
 def _train(dp, values, labels, params, rounds, n, k):
@@ -29,10 +30,10 @@ def _train(dp, values, labels, params, rounds, n, k):
 
 @pytest.mark.parametrize("case", ["c2_two_tiles", "c4_odd_tiles", "missing", "present_value"])
 def test_every_launch_shape_trains_the_same_model(dp, device, case):
-    """Trees, partitions and margins are identical under all 24 forced launch shapes
+    """Trees, partitions and margins are identical under all 36 forced launch shapes
     (two tiles per item over an odd tile count leaves a one-tile last group, with and without
-    the lanes' swapped tile order; the MISSING kernels; present-value histograms take the
-    work-item count only)."""
+    the lanes' swapped tile order; one or three blocks of rows in flight; the MISSING
+    kernels; present-value histograms take the work-item count only)."""
     import torch
     from dpgbdt import ops
 
@@ -57,7 +58,7 @@ def test_every_launch_shape_trains_the_same_model(dp, device, case):
     base = _train(dp, values, labels, dict(params, dp_autotune=0), 3, n, k)
     assert base[3].tuning()["defaults"] is True
     for shape in SHAPES:
-        if case == "present_value" and shape["dp_hist_tiles"] == 2:
+        if case == "present_value" and (shape["dp_hist_tiles"] == 2 or shape["dp_hist_deep"]):
             continue  # one present-value tile per item: only the item count applies
         print(f"[tuning] {case} {shape}", flush=True)
         got = _train(dp, values, labels, dict(params, **shape), 3, n, k)
@@ -80,13 +81,14 @@ def test_autotuner_report_and_choice(dp, device):
     report = tuned[3].tuning()
     for name in ("root", "gathered"):
         cands = report[name]
-        assert len(cands) == 24  # (1 tile + 2 tiles x 3 orders) x 2 unrolls x 3 item counts
+        # (1 tile x 2 depths + 2 tiles x (2 depths + 2 swapped orders)) x 2 unrolls x 3 items
+        assert len(cands) == 36
         assert all(c["ms"] > 0 for c in cands)
         fastest = min(c["ms"] for c in cands)
         near = [c for c in cands if c["ms"] <= fastest * 1.01]
         best = min(near, key=lambda c: (c["items"], c["ms"]))
         assert report["chosen"][name] == {key: best[key]
-                                          for key in ("tiles", "unroll", "items", "split")}
+                                          for key in ("tiles", "unroll", "items", "split", "deep")}
     base = _train(dp, values, labels, dict(params, dp_autotune=0), 2, 200000, 1)
     assert tuned[0] == base[0]
     # the choice is cached per process: a second booster of the shape reports the same
