@@ -24,6 +24,7 @@
 #include "select.hpp"
 #include "gain.hpp"
 
+#include <algorithm>
 #include <cmath>
 
 namespace dp {
@@ -327,6 +328,7 @@ __global__ __launch_bounds__(256) void reduce_evaluate_flat_kernel(
 // the level's histograms fewer.  Bins past bin_stride read the feature's last
 // bin and are masked (branch-free loads).  No barriers.
 constexpr int kDenseEvalFeatures = 4;  // features per workgroup (one per wavefront)
+constexpr int64_t kDenseOneRound = 1024;  // four-wave reduce-evaluate workgroups 256 CUs hold at once
 __global__ __launch_bounds__(64 * kDenseEvalFeatures) void reduce_evaluate_dense_kernel(
     const long long* __restrict__ partial, const HistReduce* __restrict__ jobs,
     int32_t n_jobs_host, const int32_t* __restrict__ n_jobs_dev, int32_t n_tiles,
@@ -449,9 +451,14 @@ __global__ __launch_bounds__(64 * kDenseEvalFeatures) void reduce_evaluate_dense
 // words -- the words and candidates of hist_reduce_kernel followed by
 // evaluate_features_kernel<4>, with one launch and one pass over the level's
 // histograms fewer.  Bins past bin_stride read the feature's last bin and are
-// masked (branch-free loads).
-constexpr int kDenseEvalWaves = 4;
-__global__ __launch_bounds__(64 * kDenseEvalWaves) void reduce_evaluate_dense_split_kernel(
+// masked (branch-free loads).  W wavefronts per workgroup: 4, or 2 (the node
+// and the sibling only) when the launch has more workgroups than the chip holds
+// at once with four wavefronts each (the kernel's registers allow four
+// wavefronts per SIMD, 1,024 such workgroups on 256 CUs): two-wave workgroups
+// fit twice as many, and such levels have mostly one chunk per node (C2's last
+// split level: 12.0 -> 10.0 us; with fewer workgroups two waves measured slower).
+template <int W>
+__global__ __launch_bounds__(64 * W) void reduce_evaluate_dense_split_kernel(
     const long long* __restrict__ partial, const HistReduce* __restrict__ jobs,
     int32_t n_jobs_host, const int32_t* __restrict__ n_jobs_dev, int32_t n_tiles,
     int32_t n_features, int32_t bin_stride, const long long* __restrict__ parent_base,
@@ -459,7 +466,7 @@ __global__ __launch_bounds__(64 * kDenseEvalWaves) void reduce_evaluate_dense_sp
     const long long* __restrict__ node_sums, const int32_t* __restrict__ exps, Param p,
     const uint32_t* __restrict__ fmask, const uint8_t* __restrict__ skip_bins,
     FeatCand* __restrict__ cand, int32_t store) {
-  constexpr int BPL = 4, W = kDenseEvalWaves;
+  constexpr int BPL = 4;
   __shared__ long long part[W][2 * BPL][64];  // each wavefront's sums; [0] then the node's
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
@@ -531,7 +538,9 @@ __global__ __launch_bounds__(64 * kDenseEvalWaves) void reduce_evaluate_dense_sp
     if (wave == 0) {  // the node: the four parts (one, for a direct node)
       if (!direct)
 #pragma unroll
-        for (int i = 0; i < 2 * BPL; ++i) s[i] += part[1][i][lane] + part[2][i][lane] + part[3][i][lane];
+        for (int w = 1; w < W; ++w)
+#pragma unroll
+          for (int i = 0; i < 2 * BPL; ++i) s[i] += part[w][i][lane];
 #pragma unroll
       for (int i = 0; i < 2 * BPL; ++i) part[0][i][lane] = s[i];
     }
@@ -861,14 +870,18 @@ void launch_reduce_evaluate_dense(const int64_t* partial, const HistReduce* jobs
   Param p{double(param.lambda), double(param.alpha), double(param.min_child_weight),
           double(param.gamma)};
   // Wide matrices: four features per workgroup, each wavefront summing its
-  // feature's slots alone; narrower ones: a workgroup per feature whose four
-  // wavefronts split the slots and evaluate the node and the sibling at once.
+  // feature's slots alone; narrower ones: a workgroup per feature whose
+  // wavefronts split the slots and evaluate the node and the sibling at once
+  // (two wavefronts when the grid exceeds kDenseOneRound four-wave workgroups).
   const bool wide = n_features >= kDenseWideFeatures;
+  const bool many = !wide && int64_t(n_features) * std::min(n_jobs, 256) > kDenseOneRound;
   const dim3 grid(unsigned(wide ? (n_features + kDenseEvalFeatures - 1) / kDenseEvalFeatures
                                 : n_features),
                   unsigned(n_jobs < 256 ? n_jobs : 256));
-  hipLaunchKernelGGL(wide ? reduce_evaluate_dense_kernel : reduce_evaluate_dense_split_kernel,
-                     grid, dim3(256), 0, s,
+  hipLaunchKernelGGL(wide   ? reduce_evaluate_dense_kernel
+                     : many ? reduce_evaluate_dense_split_kernel<2>
+                            : reduce_evaluate_dense_split_kernel<4>,
+                     grid, dim3(many ? 128 : 256), 0, s,
                      reinterpret_cast<const long long*>(partial), jobs, n_jobs, n_jobs_dev,
                      n_tiles, n_features, bin_stride,
                      reinterpret_cast<const long long*>(parent_base),

@@ -131,7 +131,7 @@ double time_dense(const Pass& p, const HistConfig& cfg, hipStream_t s) {
   return ms;
 }
 
-constexpr double kTieShare = 0.01;
+constexpr double kTieShare = 0.03;
 
 template <class Time>
 HistConfig pick(const std::vector<HistConfig>& cands, Time&& time, std::string& report,

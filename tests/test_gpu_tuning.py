@@ -71,7 +71,7 @@ def test_every_launch_shape_trains_the_same_model(dp, device, case):
 
 def test_autotuner_report_and_choice(dp, device):
     """The autotuned booster reports every timed candidate of the root and gathered passes
-    and chooses, of the candidates within 1 % of the fastest, the one with the fewest work
+    and chooses, of the candidates within 3 % of the fastest, the one with the fewest work
     items (then the fastest); its model equals the default shape's."""
     from dpgbdt import ops
 
@@ -85,7 +85,7 @@ def test_autotuner_report_and_choice(dp, device):
         assert len(cands) == 36
         assert all(c["ms"] > 0 for c in cands)
         fastest = min(c["ms"] for c in cands)
-        near = [c for c in cands if c["ms"] <= fastest * 1.01]
+        near = [c for c in cands if c["ms"] <= fastest * 1.03]
         best = min(near, key=lambda c: (c["items"], c["ms"]))
         assert report["chosen"][name] == {key: best[key]
                                           for key in ("tiles", "unroll", "items", "split", "deep")}
