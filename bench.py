@@ -312,6 +312,28 @@ def tree_hist_elements(t, n_rows, n_features, depth):
     return total
 
 
+def quantum_ratio(g, h, exps):
+    """log2 of this build's per-item fixed-point step over upstream's, per output, for one
+    round's gradients.  Here the step is 2^-exps (exps = 30 - the frexp exponent of max|x|).
+    Upstream's GradientQuantiser (XGBoost 3.4.1, as published; not checkable here) rounds
+    max(sum of positive x, sum of |negative x|) / (1 - 2 n eps) up to a power of two R and
+    uses the step R / 2^62.  A ratio of k means the step here is 2^k times upstream's."""
+    import math
+    import numpy as np
+
+    n = g.shape[0]
+    out = {"g": [], "h": []}
+    for k in range(g.shape[1]):
+        for key, x, e in (("g", g[:, k], exps[k][0]), ("h", h[:, k], exps[k][1])):
+            x = x.astype(np.float64)
+            big = max(float(x[x > 0].sum()), float(-x[x < 0].sum()))
+            if big <= 0.0:
+                continue
+            rounding_exp = math.frexp(big / (1.0 - 2.0 * n * np.finfo(np.float64).eps))[1]
+            out[key].append(62 - int(e) - rounding_exp)
+    return {key: (v[0] if len(set(v)) == 1 else [min(v), max(v)]) for key, v in out.items() if v}
+
+
 def trees_leg(torch, dp, ops, name, rows=None, warm_rounds=4):
     """Wall time of the configuration's boosting rounds on a fresh booster (the
     matrix is quantised and the kernels warmed by a previous booster).  The warm
@@ -335,9 +357,13 @@ def trees_leg(torch, dp, ops, name, rows=None, warm_rounds=4):
         params["num_class"] = 10
     g1 = g.reshape(-1, 1).contiguous() if injected else None
     h1 = h.reshape(-1, 1).contiguous() if injected else None
+    k_out = 10 if objective == "multi:softprob" else 1
     warm = dp.Booster(params, [dtrain])  # quantises the matrix, warms kernels
+    quantum = {}
     for r in range(warm_rounds):
         warm.boost(dtrain, r, g1, h1) if injected else warm.update(dtrain, r)
+        if r == 0 and not injected:  # the first round's gradients (untimed)
+            quantum["round_0"] = quantum_ratio(*warm.last_gradients(n, k_out))
     del warm
     bst = dp.Booster(params, [dtrain])
     torch.cuda.synchronize()
@@ -349,6 +375,14 @@ def trees_leg(torch, dp, ops, name, rows=None, warm_rounds=4):
     el = time.perf_counter() - t0
     trees = bst.num_trees()
     tuning = bst.tuning()  # the autotuner's launch shapes for this matrix
+    if injected:  # the caller's gradients, the same every round
+        import math
+
+        gi, hi = g1.cpu().numpy(), h1.cpu().numpy()
+        exps = [[30 - math.frexp(float(abs(x).max()))[1] for x in (gi[:, 0], hi[:, 0])]]
+        quantum["every_round"] = quantum_ratio(gi, hi, exps)
+    else:
+        quantum["last_round"] = quantum_ratio(*bst.last_gradients(n, k_out))
     nodes, abytes, helems = 0, 0, 0
     for t in range(trees):
         tr = bst.tree(t)
@@ -364,7 +398,10 @@ def trees_leg(torch, dp, ops, name, rows=None, warm_rounds=4):
             # dense layouts: (row, feature) elements of the histogram passes per tree
             "hist_elements_per_tree": None if density else helems / trees,
             "gbs": gbs, "pct_hbm_peak": 100.0 * gbs / HBM_PEAK_GBS,
-            "hist_config": tuning.get("chosen", tuning)}
+            "hist_config": tuning.get("chosen", tuning),
+            # log2 (this build's fixed-point step / upstream's) for g and h (a [min, max]
+            # range over the outputs of multi-output rounds)
+            "quantum_log2_ratio": quantum}
 
 
 def paper_shape_leg(torch, dp, ops):

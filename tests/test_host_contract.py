@@ -119,3 +119,34 @@ def test_train_one_iter_refuses_host_gradients(dp):
         assert "grad must be device memory" in lib.XGBGetLastError().decode()
     finally:
         lib.XGBoosterFree(h)
+
+
+def test_quantum_ratio_closed_forms():
+    """bench.py's report of this build's fixed-point step against upstream's: for n rows of
+    g = +-1/2 (half each) and h = 1/4, the step here is 2^-30 (g) and 2^-31 (h); upstream
+    rounds sum(g > 0) = n/4 and sum(h) = n/4 up to powers of two and divides by 2^62, so with
+    n = 2^14 both sums are 2^12 (exactly, so the (1 - 2 n eps) guard lifts them to 2^13)
+    and the ratios are 62 - 30 - 13 = 19 and 62 - 31 - 13 = 18.  A sign mix that makes the
+    negative sum the larger one must give the same g ratio, and a [min, max] pair is
+    reported when outputs differ."""
+    import os
+    import sys
+
+    import numpy as np
+
+    sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    import bench
+
+    n = 1 << 14
+    g = np.where(np.arange(n) % 2 == 0, 0.5, -0.5).astype(np.float32).reshape(-1, 1)
+    h = np.full((n, 1), 0.25, dtype=np.float32)
+    assert bench.quantum_ratio(g, h, [[30, 31]]) == {"g": 19, "h": 18}
+    flipped = np.where(np.arange(n) % 4 == 0, 0.5, -0.5).astype(np.float32).reshape(-1, 1)
+    # negative sum 3n/8 = 6144: frexp exponent 13 -> the same ratio
+    assert bench.quantum_ratio(flipped, h, [[30, 31]])["g"] == 19
+    # second output: one row at 2 (max|g| = 2, step 2^-28), the sums still below 2^13
+    outlier = g.copy()
+    outlier[0, 0] = 2.0
+    r = bench.quantum_ratio(np.concatenate([g, outlier], axis=1),
+                            np.concatenate([h, h], axis=1), [[30, 31], [28, 31]])
+    assert r == {"g": [19, 21], "h": 18}
