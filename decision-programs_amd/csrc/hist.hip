@@ -183,9 +183,6 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(DE
       rotate16(sk[j], rot);
     }
   }
-  for (int e = threadIdx.x; e < nt * kLdsWords; e += kHistThreads) lds[e] = 0ull;
-  __syncthreads();
-
   const uint8_t* tile = bins + int64_t(w.tile) * tile_step;  // row r at tile + r * row_step
   const int64_t last = w.end - 1;
   const int64_t lane = threadIdx.x;
@@ -238,11 +235,17 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(DE
     }
   };
   // The loop bound and the block guards are uniform per workgroup; buffer
-  // indices are static (buffer j % R holds block j of the item).
+  // indices are static (buffer j % R holds block j of the item).  The item's
+  // first loads are issued before the LDS clear and its barrier, which they
+  // do not depend on (a barrier waits for LDS operations only), so the clear
+  // runs while they are in flight.
   const int64_t b0 = w.begin;
   if (GATHER) {
 #pragma unroll
     for (int j = 0; j < R; ++j) fetch_rows(j, b0 + j * kStep);
+  }
+  for (int e = threadIdx.x; e < nt * kLdsWords; e += kHistThreads) lds[e] = 0ull;
+  if (GATHER) {
 #pragma unroll
     for (int j = 0; j < PD; ++j) {
       fetch_data(j, b0 + j * kStep);
@@ -252,6 +255,7 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(DE
 #pragma unroll
     for (int j = 0; j < PD; ++j) fetch_data(j, b0 + j * kStep);
   }
+  __syncthreads();
   for (int64_t blk = b0; blk < w.end; blk += R * kStep) {
 #pragma unroll
     for (int k = 0; k < R; ++k) {
