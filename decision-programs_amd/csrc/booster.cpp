@@ -448,7 +448,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
       // The last split level's histograms have no readers: a fused launch
       // evaluates them without storing them.
       const bool keep = d + 1 < D;
-      bool dense_fused = false;  // set below for dense levels below the root
+      bool dense_fused = false;  // set below for dense passes with at least kDenseFuseFeatures features
       if (d == 0 && sparse_) {
         launch_hist_sparse(q.sparse, N, F, gpair, nullptr, root_work_.p, root_items_, nullptr, B,
                            h, partial_.p, s);
@@ -459,9 +459,17 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
         else
           launch_hist_reduce_flat(partial_.p, root_job_.p, 1, nullptr, T, tf, F, B, nullptr, h, s);
       } else if (d == 0) {
+        // The root, as the levels below it: feature-major partial slots, and
+        // the reduce and the evaluation in one launch (one job, no sibling).
+        dense_fused = F >= kDenseFuseFeatures && B <= 256 && exps;
         launch_hist(q.bins.p, L, gpair, nullptr, root_work_.p, root_items_, nullptr, B, h,
-                    partial_.p, s, nullptr, root_cfg_, skip_tiles_);
-        launch_hist_reduce(partial_.p, root_job_.p, 1, nullptr, T, F, B, nullptr, h, false, s);
+                    partial_.p, s, nullptr, root_cfg_, skip_tiles_, dense_fused);
+        if (dense_fused)
+          launch_reduce_evaluate_dense(partial_.p, root_job_.p, 1, nullptr, T, F, B, nullptr, h,
+                                       q.d_nbins.p, sums_[cur].p, exps, dtp, fmask,
+                                       skip_features_, eval_scratch_.p, keep, s);
+        else
+          launch_hist_reduce(partial_.p, root_job_.p, 1, nullptr, T, F, B, nullptr, h, false, s);
       } else if (sparse_) {
         // On the last split level of a fused tree, and on levels of at least
         // kInPassNodes nodes (mostly small ones), the nodes built in one chunk
