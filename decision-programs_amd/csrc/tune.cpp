@@ -10,10 +10,9 @@
 //   rows per lane per pipeline step   1 or 2;
 //   with two tiles, the lane bit (4, 5 or none) that swaps a lane's tile
 //                         order (fewer lanes per (feature, bin) per atomic);
-//   without that swap, the prefetch depth: one block of rows in flight per
-//                         workgroup (gathered rows; none for contiguous rows)
-//                         or three (more registers, possibly fewer resident
-//                         workgroups; for passes with few items per CU);
+//   without that swap, on the contiguous (root) pass, the prefetch depth: none
+//                         or three blocks of rows in flight per workgroup (more
+//                         registers, possibly fewer resident workgroups);
 //   work items per pass   512, 1024 or 2048 (fewer, longer row chunks write
 //                         fewer partial tiles; more balance the CUs better).
 // The contiguous (root) pass is timed over the whole matrix; the gathered pass
@@ -43,14 +42,17 @@ using Key = std::tuple<int64_t, int32_t, int32_t, int32_t, int32_t, int32_t>;
 std::mutex g_lock;
 std::map<Key, HistTuning> g_cache;
 
-std::vector<HistConfig> dense_candidates(int32_t n_tiles) {
+// contiguous: the root pass's candidates, which include the three-block
+// prefetch; the gathered passes' do not (it was slower on C2's levels, whose
+// small items the timed pass does not have, and tied on C3's).
+std::vector<HistConfig> dense_candidates(int32_t n_tiles, bool contiguous) {
   std::vector<HistConfig> c;
   for (int32_t tiles : {1, 2}) {
     if (tiles > n_tiles) continue;
     for (int32_t split : {0, 4, 5}) {
       if (tiles == 1 && split) continue;
       for (int32_t deep : {0, 1}) {
-        if (deep && split) continue;
+        if (deep && (split || !contiguous)) continue;
         for (int32_t unroll : {1, 2})
           for (int32_t items : {512, 1024, 2048})
             c.push_back(HistConfig{tiles, unroll, items, split, deep});
@@ -181,7 +183,7 @@ const HistTuning& tune_dense_hist(const dp_bin_layout& L, const uint8_t* bins,
   auto it = g_cache.find(key);
   if (it != g_cache.end()) return it->second;
   HistTuning t;
-  const auto cands = dense_candidates(L.n_tiles);
+  const auto cands = dense_candidates(L.n_tiles, true);
   constexpr int32_t kStride = 32, kNodes = 12;  // the gathered pass's nodes (see above)
   DeviceBuffer<int64_t> out(size_t(kNodes) * size_t(L.n_features) * size_t(bin_stride) * 2);
   Pass root{&L, bins, nullptr, skip, nullptr, L.n_rows, 1, bin_stride, gpair, out.p, false};
@@ -203,7 +205,8 @@ const HistTuning& tune_dense_hist(const dp_bin_layout& L, const uint8_t* bins,
     const bool fmaj = L.n_features >= kDenseFuseFeatures && bin_stride <= 256;
     Pass level{&L, bins, rows_major, skip, ridx.p, per, kNodes, bin_stride, gpair, out.p, fmaj};
     report += ",";
-    t.level = pick(cands, [&](const HistConfig& c) { return time_dense(level, c, s); }, report,
+    t.level = pick(dense_candidates(L.n_tiles, false),
+                   [&](const HistConfig& c) { return time_dense(level, c, s); }, report,
                    "gathered");
     DP_HIP(hipStreamSynchronize(s));
   }
