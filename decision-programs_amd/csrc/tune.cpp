@@ -152,20 +152,19 @@ HistConfig pick(const std::vector<HistConfig>& cands, Time&& time, std::string& 
   }
   report += "]";
   // Near-ties (within kTieShare of the fastest) go to the fewest work items,
-  // then to the one-block prefetch, then to one row per lane per step, then
-  // the faster: fewer items write fewer partial slots, which a tree's levels
-  // pay for in their reduce more than the timed passes show (measured on C3:
-  // the gathered shapes within 2 % of each other here trained at 438 to 469
-  // trees/s, the fewer items faster); the three-block prefetch and two rows
-  // per step were slower on the small items of C2's levels (by about 1 us per
-  // level each), which the timed pass's larger items do not show.
+  // then to one row per lane per step, then the faster: fewer items write
+  // fewer partial slots, which a tree's levels pay for in their reduce more
+  // than the timed passes show (measured on C3: the gathered shapes within 2 %
+  // of each other here trained at 438 to 469 trees/s, the fewer items
+  // faster); two rows per step were slower on the small items of C2's levels
+  // (about 1 us per level), which the timed pass's larger items do not show.
   const double fastest = *std::min_element(ms.begin(), ms.end());
   size_t best = 0;
   bool have = false;
   for (size_t i = 0; i < cands.size(); ++i) {
     if (ms[i] > fastest * (1.0 + kTieShare)) continue;
     const HistConfig &c = cands[i], &b = cands[best];
-    const auto rank = [](const HistConfig& x) { return std::tuple(x.items, x.deep, x.unroll); };
+    const auto rank = [](const HistConfig& x) { return std::tuple(x.items, x.unroll); };
     if (!have || rank(c) < rank(b) || (rank(c) == rank(b) && ms[i] < ms[best])) best = i;
     have = true;
   }
