@@ -4,7 +4,9 @@
 Headline (`value`): histogram build throughput in rows*features/s on the C3
 workload -- 10,000,000 rows x 128 features, 256 quantile bins, uint8 bins,
 fixed-point (g, h) -- with everything resident in HBM.  One step is one
-histogram pass over all 10M rows (one launch of the histogram kernel).
+histogram pass over all 10M rows (one launch of the histogram kernel).  The
+layout pairs the two tiles of C3's 16-value features (dp_layout_pair_tiles, as
+the booster does); the unpaired pass is timed beside it.
 
 The same JSON line carries
   roofline      the histogram operation's algorithmic bytes per launch over
@@ -86,7 +88,11 @@ def hist_leg(args, torch, dp, ops):
     cut_ptr, cuts, _, missing = ops.sketch_cuts(ws, values, 256)
     import numpy as np
 
-    lay = ops.layout(n, f, 0, -1)
+    # features 96-127 take 16 values: tiles 6 and 7 are paired (their joint tile, one
+    # byte per feature pair, follows the 8 tiles), as the booster pairs them; the
+    # unpaired layout is timed beside it on the same buffer
+    lay = ops.layout_pair_tiles(ops.layout(n, f, 0, -1), cut_ptr)
+    plain = ops.layout(n, f, 0, -1)
     bins = ops.bin_values(values, lay, cut_ptr, cuts)
     del values
     n_bins = np.diff(cut_ptr)
@@ -110,6 +116,20 @@ def hist_leg(args, torch, dp, ops):
     wall = time.perf_counter() - t0
     launch_ms = [ev[k].elapsed_time(ev[k + 1]) for k in range(args.steps)]
     avg_ms = sum(launch_ms) / len(launch_ms)
+    # the same pass without paired tiles (tuned on first use), for comparison
+    unpaired = torch.zeros_like(hist)
+    ops.hist_accumulate(ws, bins, plain, gp, [(0, n)], unpaired)
+    torch.cuda.synchronize()
+    ev_u = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    ev_u[0].record(stream)
+    for k in range(args.steps):
+        ops.hist_accumulate(ws, bins, plain, gp, [(0, n)], unpaired)
+        ev_u[k + 1].record(stream)
+    torch.cuda.synchronize()
+    unpaired_ms = sum(ev_u[k].elapsed_time(ev_u[k + 1]) for k in range(args.steps)) / args.steps
+    assert bool((unpaired[0] * (args.warmup + args.steps) == hist[0] * (args.steps + 1)).all()), \
+        "paired and unpaired histograms differ"
+    del unpaired
     # size-independent check: every feature's bins sum to the root totals
     h0 = hist[0].sum(dim=1)  # [F, 2]
     reps = args.warmup + args.steps
@@ -124,11 +144,15 @@ def hist_leg(args, torch, dp, ops):
         "achieved_gbs": achieved, "algorithmic_bytes": abytes,
         "min_ms": min(launch_ms), "max_ms": max(launch_ms),
         "tuning": ops.hist_tuning(lay, stride),  # the autotuner's launch shape for this pass
+        "paired_tiles": int(lay.paired_tiles),
+        "issued_elements": n * (f - 16 * bin(int(lay.paired_tiles)).count("1")),
+        "unpaired_avg_ms": unpaired_ms,
+        "unpaired_launch_shape": ops.hist_tuning(plain, stride).get("chosen", {}).get("root"),
     }
     sample = None
     if not args.skip_cpu:
         rows = min(n, args.cpu_rows)
-        tiles = bins.view(lay.n_tiles, n, lay.tile_width)[:, :rows, :]
+        tiles = bins[: ops.layout_bytes(plain)].view(lay.n_tiles, n, lay.tile_width)[:, :rows, :]
         sample_bins = tiles.permute(1, 0, 2).reshape(rows, -1)[:, :f].contiguous().cpu().numpy()
         gq = gp[:rows].cpu().numpy()
         sample = (sample_bins, np.ascontiguousarray(gq[:, 0]), np.ascontiguousarray(gq[:, 1]),
@@ -495,10 +519,13 @@ def main():
     cands = sorted(hist["tuning"].get("root", []), key=lambda c: c["ms"])
     log("autotuner, fastest root shapes (hist + reduce ms): " + ", ".join(
         f"{c['tiles']}t/{c['unroll']}u/{c['items']}i/s{c['split']} {c['ms']:.3f}" for c in cands[:8]))
-    roof = lds_roof_leg(torch, hist["n"] * hist["f"])
+    issued = hist["issued_elements"]
+    roof = lds_roof_leg(torch, issued)
     if roof:
         roof["frac"] = roof["two_u64_ms"] / hist["avg_ms"]
-        roof["note"] = ("LDS atomic roof at this pass's row-features: the histogram's exact "
+        roof["elements"] = issued
+        roof["note"] = ("LDS atomic roof at the elements this pass accumulates (rows x "
+                        "features, a paired tile pair counting once): the histogram's exact "
                         "accumulation (two 64-bit LDS atomics per element) with no global "
                         "loads; frac = roof time / measured launch time")
         log(f"LDS roof (two 64-bit atomics): {roof['two_u64_ms']:.3f} ms, "
@@ -512,8 +539,7 @@ def main():
                                     rows=args.rows if name == "C3" else None)
             el = trees[name]["hist_elements_per_tree"]
             if roof and el:  # the tree's histogram passes at the LDS roof's rate
-                trees[name]["hist_lds_roof_ms_per_tree"] = \
-                    roof["two_u64_ms"] * el / (hist["n"] * hist["f"])
+                trees[name]["hist_lds_roof_ms_per_tree"] = roof["two_u64_ms"] * el / issued
             log(f"{name}: {trees[name]['value']:.1f} trees/s")
     cpu = None
     if sample is not None:
@@ -561,7 +587,10 @@ def main():
                      "algorithmic_bytes_per_launch": hist["algorithmic_bytes"],
                      "lds_atomic_roof": roof,
                      "avg_launch_ms": hist["avg_ms"],
-                     "launch_shape": hist["tuning"].get("chosen", {}).get("root")},
+                     "launch_shape": hist["tuning"].get("chosen", {}).get("root"),
+                     "paired_tiles": hist["paired_tiles"],
+                     "unpaired_avg_launch_ms": hist["unpaired_avg_ms"],
+                     "unpaired_launch_shape": hist["unpaired_launch_shape"]},
         "trees_per_s": trees,
         "cpu_baseline": cpu,
     }

@@ -17,6 +17,7 @@
 #include <climits>
 #include <cmath>
 #include <charconv>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <limits>
@@ -174,8 +175,15 @@ Quantized& DMatrix::quantize(int32_t max_bin, dp_workspace_s& ws, hipStream_t s)
     launch_bin_columns16(values.p, n_rows, n_features, q->d_cut_ptr.p, q->d_cut_values.p,
                          q->cols16.p, s);
   } else {
-    q->bins.resize(dp_layout_bytes(&q->layout));
+    // The tiles whose features all have at most 16 bins are paired: their
+    // joint tiles follow the matrix's tiles in q->bins (the histograms use
+    // them unless the round's histograms skip bins or pairing is off).
+    dp_bin_layout paired = q->layout;
+    paired.paired_tiles = pair_tiles(nbins.data(), n_features, q->layout.n_tiles, has_nan);
+    q->pairs = paired.paired_tiles;
+    q->bins.resize(dp_layout_bytes(&paired));
     launch_bin_values(values.p, q->layout, q->d_cut_ptr.p, q->d_cut_values.p, q->bins.p, s);
+    launch_join_tiles(q->bins.p, paired, s);
     q->cols.resize(size_t(n_rows) * size_t(n_features));
     launch_tiles_to_columns(q->bins.p, q->layout, q->cols.p, s);
   }
@@ -267,7 +275,8 @@ void Grower::ensure_level(const Quantized& q, int64_t nb, int32_t d, int32_t D) 
   const int64_t S = int64_t(q.layout.n_features) * q.bin_stride * 2;
   const int cur = d & 1, nxt = cur ^ 1;
   const int64_t nn = d < D ? std::min(2 * nb, N) : 0;  // next level's bound
-  const int32_t G = (T + level_cfg_.tiles - 1) / level_cfg_.tiles;  // items per row chunk
+  // items per row chunk
+  const int32_t G = hist_groups(T, level_cfg_.tiles, hist_pairs(lay_.paired_tiles, level_cfg_.tiles));
   need(plan_hist_capacity(nn, G, level_cfg_.items) < INT32_MAX &&
            plan_part_capacity(nb, N, chunk_) < INT32_MAX &&
            plan_part_capacity(nn, N, chunk_) < INT32_MAX && plan_leaf_capacity(nb, N, chunk_) < INT32_MAX,
@@ -294,11 +303,17 @@ void Grower::ensure_level(const Quantized& q, int64_t nb, int32_t d, int32_t D) 
 
 void Grower::prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, bool sparse,
                      const HistConfig& root_cfg, const HistConfig& level_cfg, bool skip,
-                     hipStream_t s) {
+                     uint64_t pairs, hipStream_t s) {
   const dp_bin_layout& L = q.layout;
   need(sparse ? q.sparse.n_tiles > 0 : q.rows.n > 0, "histogram layout not built");
   need(!skip || (!sparse && q.skip_tiles.n > 0 && q.skip_features.n > 0),
        "skip bins not built");
+  need(!pairs || (!sparse && !skip && (pairs & ~q.pairs) == 0), "tile pairs out of place");
+  need(sparse || q.rows_pairs == hist_pairs(pairs, level_cfg.tiles),
+       "row-major copy out of step with the tile pairs");
+  lay_ = L;
+  lay_.paired_tiles = pairs;
+  check_pairs(lay_);
   sparse_ = sparse;
   skip_tiles_ = skip ? q.skip_tiles.p : nullptr;
   skip_features_ = skip ? q.skip_features.p : nullptr;
@@ -332,16 +347,17 @@ void Grower::prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, b
   node_left_[0].reserve(1);
   const int64_t slot_words = sparse ? int64_t(q.sparse.tile_features) * q.bin_stride * 2
                                     : int64_t(q.bin_stride) * 32;
-  partial_.reserve(size_t(std::max(hist_partial_capacity(tiles_, root_cfg_),
-                                    hist_partial_capacity(tiles_, level_cfg_)) *
+  partial_.reserve(size_t(std::max(hist_partial_capacity(tiles_, root_cfg_, pairs),
+                                    hist_partial_capacity(tiles_, level_cfg_, pairs)) *
                            slot_words));
   if (root_rows_ != N || root_tiles_ != tiles_ || root_sparse_ != sparse ||
-      root_made_.tiles != root_cfg_.tiles || root_made_.items != root_cfg_.items) {
+      root_made_.tiles != root_cfg_.tiles || root_made_.items != root_cfg_.items ||
+      root_pairs_ != pairs) {
     const int64_t b = 0, e = N;
     const int32_t slot = 0;
     std::vector<HistWork> w;
     std::vector<HistReduce> j;
-    make_hist_work(L, &b, &e, &slot, 1, true, w, j, sparse ? tiles_ : 0, root_cfg_);
+    make_hist_work(lay_, &b, &e, &slot, 1, true, w, j, sparse ? tiles_ : 0, root_cfg_);
     root_work_.resize(w.size());
     root_job_.resize(j.size());
     DP_HIP(hipMemcpy(root_work_.p, w.data(), sizeof(HistWork) * w.size(), hipMemcpyHostToDevice));
@@ -351,6 +367,7 @@ void Grower::prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, b
     root_tiles_ = tiles_;
     root_sparse_ = sparse;
     root_made_ = root_cfg_;
+    root_pairs_ = pairs;
   }
   const int64_t widest = level_bound(D, N), widest_hist = level_bound(D - 1, N);
   eager_ = widest <= kEagerNodes && 2 * widest_hist * S * int64_t(sizeof(int64_t)) <= kEagerHistBytes;
@@ -462,7 +479,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
         // The root, as the levels below it: feature-major partial slots, and
         // the reduce and the evaluation in one launch (one job, no sibling).
         dense_fused = F >= kDenseFuseFeatures && B <= 256 && exps;
-        launch_hist(q.bins.p, L, gpair, nullptr, root_work_.p, root_items_, nullptr, B, h,
+        launch_hist(q.bins.p, lay_, gpair, nullptr, root_work_.p, root_items_, nullptr, B, h,
                     partial_.p, s, nullptr, root_cfg_, skip_tiles_, dense_fused);
         if (dense_fused)
           launch_reduce_evaluate_dense(partial_.p, root_job_.p, 1, nullptr, T, F, B, nullptr, h,
@@ -503,13 +520,14 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
                                   field(c, &PlanCounts::n_reduce), T, tf, F, B, hist_[nxt].p, h,
                                   s);
       } else {
-        const int32_t G = (T + level_cfg_.tiles - 1) / level_cfg_.tiles;
+        const int32_t G =
+            hist_groups(T, level_cfg_.tiles, hist_pairs(lay_.paired_tiles, level_cfg_.tiles));
         // Levels below the root with more features than one evaluation
         // workgroup takes: feature-major partial slots, and the reduce and the
         // evaluation in one launch (measured: C2 2,474 -> 2,560, C3 455 ->
         // 463, C4 3,321 -> 3,886 trees/s).
         dense_fused = F >= kDenseFuseFeatures && B <= 256 && exps;
-        launch_hist(q.bins.p, L, gpair, ridx_[cur].p, hist_work_[cur].p,
+        launch_hist(q.bins.p, lay_, gpair, ridx_[cur].p, hist_work_[cur].p,
                     int32_t(plan_hist_items(nb, N, G, level_cfg_.items)),
                     field(c, &PlanCounts::n_hist), B, h, partial_.p, s, q.rows.p, level_cfg_,
                     skip_tiles_, dense_fused);
@@ -590,6 +608,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     a.max_depth = D;
     a.n_tiles = T;
     a.hist_tiles = level_cfg_.tiles;
+    a.hist_pairs = hist_pairs(lay_.paired_tiles, level_cfg_.tiles);
     a.hist_items = level_cfg_.items;
     // Histogram workgroups resident at once: two per CU for present-value
     // tiles; for dense tiles, what the level kernel's LDS and registers allow.
@@ -606,7 +625,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     a.info_capacity = int32_t(eager_ ? node_cap_ : int64_t(info_.n));
     a.level_capacity = int32_t(level_[nxt].n);
     a.hist_capacity = int32_t(hist_work_[nxt].n);
-    a.partial_capacity = int32_t(hist_partial_capacity(T, level_cfg_));
+    a.partial_capacity = int32_t(hist_partial_capacity(T, level_cfg_, lay_.paired_tiles));
     a.part_capacity = int32_t(part_work_[nxt].n);
     a.leaf_capacity = int32_t(leaf_work_[cur].n);
     a.cur_bound = int32_t(std::min<int64_t>(nb, INT32_MAX));
@@ -697,7 +716,9 @@ uint64_t Grower::signature() const {
     mix(uint64_t(c->unroll));
     mix(uint64_t(c->items));
     mix(uint64_t(c->split));
+    mix(uint64_t(c->deep));
   }
+  mix(lay_.paired_tiles);
   return h;
 }
 
@@ -804,7 +825,8 @@ void Booster::set_param(const std::string& key, const std::string& value) {
       "colsample_bynode", "base_score", "boost_from_average", "seed", "seed_per_iteration",
       "nthread", "verbosity", "validate_parameters", "grow_policy", "dp_record_positions",
       "dp_graphs", "dp_sparse_hist", "dp_concurrent_trees", "dp_autotune", "dp_hist_tiles",
-      "dp_hist_unroll", "dp_hist_items", "dp_hist_split", "dp_hist_deep", "dp_skip_bin"};
+      "dp_hist_unroll", "dp_hist_items", "dp_hist_split", "dp_hist_deep", "dp_hist_pair",
+      "dp_skip_bin"};
   bool ok = false;
   for (const char* k : known) ok = ok || key == k;
   need(ok, "unsupported parameter: " + key);
@@ -858,6 +880,11 @@ void Booster::set_param(const std::string& key, const std::string& value) {
     const int32_t m = parse_int(key, value);
     need(m == 0 || m == 1, "dp_hist_deep must be 0 or 1");
     forced_hist_.deep = m;
+  }
+  if (key == "dp_hist_pair") {
+    const int32_t m = parse_int(key, value);
+    need(m == 0 || m == 1, "dp_hist_pair must be 0 or 1");
+    pair_tiles_ = m != 0;
   }
   if (key == "dp_sparse_hist") {
     const int32_t m = parse_int(key, value);
@@ -1115,16 +1142,16 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
     }
     sparse = q.sparse.n_tiles > 0;
   }
-  if (!sparse && q.rows.n == 0) {
-    q.rows.resize(dp_layout_bytes(&q.layout));
-    launch_tiles_to_rows(q.bins.p, q.layout, q.rows.p, stream_);
-  }
   // Skip bins (matrices without missing values): counted once per matrix.
   bool skip = false;
   if (!sparse && q.layout.missing_bin < 0 && skip_mode_ != 0) {
     if (q.skip_share < 0.0) build_skip_bins(q, stream_);
     skip = skip_mode_ == 2 || q.skip_share >= kSkipShare;
   }
+  // Paired tiles (dense histograms without skip bins): the tuner times and the
+  // growers launch with this layout.
+  dp_bin_layout hl = q.layout;
+  hl.paired_tiles = !sparse && !skip && pair_tiles_ ? q.pairs : 0;
   if (record_positions_) positions_.reserve(size_t(N));
   // Histogram launch shapes: forced by dp_hist_* (0 = default for the rest),
   // else tuned on this matrix shape (once per process), else the defaults.
@@ -1143,7 +1170,7 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
     const HistTuning& t =
         sparse ? tune_sparse_hist(q.sparse, N, q.layout.n_features, q.bin_stride, gpair_.p,
                                   stream_)
-               : tune_dense_hist(q.layout, q.bins.p, q.rows.p, q.bin_stride, gpair_.p, stream_,
+               : tune_dense_hist(hl, q.bins.p, true, q.bin_stride, gpair_.p, stream_,
                                  skip ? q.skip_tiles.p : nullptr);
     root_cfg = t.root;
     level_cfg = t.level;
@@ -1151,11 +1178,28 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
   } else {
     tuning_report_ = "{\"defaults\":true}";
   }
+  // The gathered passes' row-major copy: with the pairs' joint tiles in place
+  // of their first tiles when the level shape uses the pairs (one tile per
+  // item), else plain; rebuilt only when that changes.
+  if (!sparse) {
+    const uint64_t rp = hist_pairs(hl.paired_tiles, level_cfg.tiles);
+    if (q.rows.n == 0 || q.rows_pairs != rp) {
+      dp_bin_layout rl = q.layout;
+      rl.paired_tiles = rp;
+      q.rows.resize(dp_layout_bytes(&q.layout));
+      launch_tiles_to_rows(q.bins.p, rl, q.rows.p, stream_);
+      q.rows_pairs = rp;
+    }
+  }
   {  // the histogram mode beside the launch shapes
     std::string mode = "{\"layout\":\"";
     mode += sparse ? "present-value" : "dense";
     mode += "\",\"skip_bins\":";
     mode += skip ? "true" : "false";
+    char pairs[40];
+    std::snprintf(pairs, sizeof pairs, ",\"paired_tiles\":%llu",
+                  static_cast<unsigned long long>(hl.paired_tiles));
+    mode += pairs;
     if (q.skip_share >= 0.0) {
       mode += ",\"skip_share\":";
       json::put_double(mode, q.skip_share);
@@ -1166,15 +1210,17 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
   int32_t S = std::min(K, concurrent_trees_);
   while (int32_t(growers_.size()) < S) growers_.push_back(std::make_unique<Grower>());
   if (growers_.empty()) growers_.push_back(std::make_unique<Grower>());
-  growers_[0]->prepare(q, tp_, (K + S - 1) / S, sparse, root_cfg, level_cfg, skip, stream_);
+  growers_[0]->prepare(q, tp_, (K + S - 1) / S, sparse, root_cfg, level_cfg, skip,
+                       hl.paired_tiles, stream_);
   const bool eager = growers_[0]->eager();
   if (!eager && S > 1) {  // level-synced trees synchronise per level: one at a time
     S = 1;
-    growers_[0]->prepare(q, tp_, K, sparse, root_cfg, level_cfg, skip, stream_);
+    growers_[0]->prepare(q, tp_, K, sparse, root_cfg, level_cfg, skip, hl.paired_tiles,
+                         stream_);
   }
   for (int32_t l = 1; l < S; ++l)
     growers_[size_t(l)]->prepare(q, tp_, (K - l + S - 1) / S, sparse, root_cfg, level_cfg,
-                                 skip, stream_);
+                                 skip, hl.paired_tiles, stream_);
   while (S > 1 && int32_t(tree_streams_.size()) < S) {
     hipStream_t t;
     DP_HIP(hipStreamCreateWithFlags(&t, hipStreamNonBlocking));

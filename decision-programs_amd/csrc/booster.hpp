@@ -27,7 +27,10 @@ struct Quantized {
   // (missing: kWideMissing) for the partition, and every histogram from the
   // present-value layout built from them.
   DeviceBuffer<uint16_t> cols16;
-  DeviceBuffer<uint8_t> rows;  // row-major copy: rows[(r * n_tiles + t) * 16 + j] (on demand)
+  // row-major copy: rows[(r * n_tiles + t) * 16 + j] (on demand); the first
+  // tile of each pair of rows_pairs holds the pair's joint tile instead
+  DeviceBuffer<uint8_t> rows;
+  uint64_t rows_pairs = 0;
   SparseBins sparse;           // present-value layout (on demand, mostly-missing matrices)
   // Skip bins (matrices without missing values, on demand): each feature's most
   // frequent bin, per feature and per 16-feature tile, and the share of the
@@ -37,6 +40,10 @@ struct Quantized {
   double skip_share = -1.0;
   double sparse_limit = -1.0;  // largest density limit the layout was tried with
   double density = -1.0;       // share of present values, once counted
+  // Tiles the dense histograms may pair (dp_bin_layout::paired_tiles, from
+  // pair_tiles: none with missing values); their joint tiles follow the
+  // n_tiles tiles in `bins`.
+  uint64_t pairs = 0;
 };
 
 // Counts each feature's bins (column copy) and fills q.skip_features,
@@ -108,9 +115,11 @@ class Grower {
   // histogram passes (present-value histograms use their items only).
   // skip: histograms leave each feature's skip bin out (q.skip_tiles and
   // q.skip_features, which must be built) and the evaluation restores it.
+  // pairs: the paired tiles of the dense histograms (a subset of q.pairs; 0
+  // with sparse or skip).
   void prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, bool sparse,
                const HistConfig& root_cfg, const HistConfig& level_cfg, bool skip,
-               hipStream_t s);
+               uint64_t pairs, hipStream_t s);
   // Column sampling of the trees grow() enqueues next (inactive: every
   // feature is a candidate at every node); cs.output is set per tree.
   ColSample colsample;
@@ -173,6 +182,8 @@ class Grower {
   int32_t root_tiles_ = 0, root_items_ = 0;
   bool root_sparse_ = false;
   HistConfig root_cfg_, level_cfg_, root_made_;
+  uint64_t root_pairs_ = 0;                 // the paired tiles root_work_ was made for
+  dp_bin_layout lay_{};                     // the matrix's layout with the pairs in use
   const uint8_t* skip_tiles_ = nullptr;     // the matrix's skip bins when in use
   const uint8_t* skip_features_ = nullptr;
 };
@@ -283,6 +294,7 @@ class Booster {
   bool use_graphs_ = true;
   bool autotune_ = true;        // dp_autotune: time the histogram launch shapes (tune.cpp)
   HistConfig forced_hist_{0, 0, 0, 0, 0};  // dp_hist_tiles / _unroll / _items / _split / _deep; 0 = not forced
+  bool pair_tiles_ = true;      // dp_hist_pair: pair the tiles whose features have <= 16 bins
   std::string tuning_report_ = "{}";
   int32_t sparse_mode_ = 1;  // dp_sparse_hist: 0 never, 1 when <= 1/4 present, 2 with any NaN
   // dp_skip_bin (matrices without missing values): 0 never, 1 when the skip

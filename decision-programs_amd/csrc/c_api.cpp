@@ -539,12 +539,37 @@ int dp_layout_init(int64_t n_rows, int32_t n_features, int32_t tile_width, int32
     out->tile_width = tile_width;
     out->n_tiles = (n_features + tile_width - 1) / tile_width;
     out->missing_bin = missing_bin;
+    out->paired_tiles = 0;
+  });
+}
+
+int dp_layout_pair_tiles(dp_bin_layout* layout, const int32_t* cut_ptr) {
+  return guarded([&] {
+    dp::need(layout && cut_ptr, "null argument");
+    dp::need(layout->n_features > 0 && layout->tile_width == 16 &&
+                 layout->n_tiles == (layout->n_features + 15) / 16,
+             "layout not initialised");
+    std::vector<int32_t> n_bins(size_t(layout->n_features));
+    for (int32_t f = 0; f < layout->n_features; ++f) {
+      n_bins[size_t(f)] = cut_ptr[f + 1] - cut_ptr[f];
+      dp::need(n_bins[size_t(f)] >= 0, "cut_ptr must not decrease");
+    }
+    layout->paired_tiles = dp::pair_tiles(n_bins.data(), layout->n_features, layout->n_tiles,
+                                          layout->missing_bin >= 0);
   });
 }
 
 size_t dp_layout_bytes(const dp_bin_layout* layout) {
   if (!layout) return 0;
-  return size_t(layout->n_tiles) * size_t(layout->n_rows) * size_t(layout->tile_width);
+  const size_t tiles = size_t(layout->n_tiles) + size_t(__builtin_popcountll(layout->paired_tiles));
+  return tiles * size_t(layout->n_rows) * size_t(layout->tile_width);
+}
+
+int dp_join_tiles(uint8_t* bins, const dp_bin_layout* layout, void* stream) {
+  return guarded([&] {
+    dp::need(bins && layout, "null argument");
+    dp::launch_join_tiles(bins, *layout, as_stream(stream));
+  });
 }
 
 int dp_sketch_cuts(dp_workspace ws, const float* values, int64_t n_rows, int32_t n_features,
@@ -562,6 +587,7 @@ int dp_bin_values(const float* values, const dp_bin_layout* layout, const int32_
   return guarded([&] {
     dp::need(values && layout && cut_ptr && cut_values && bins, "null argument");
     dp::launch_bin_values(values, *layout, cut_ptr, cut_values, bins, as_stream(stream));
+    dp::launch_join_tiles(bins, *layout, as_stream(stream));
   });
 }
 
@@ -622,7 +648,7 @@ void hist_call(dp_workspace ws, const uint8_t* bins, const dp_bin_layout* layout
     if (const dp::HistTuning* t = dp::find_dense_tuning(*layout, bin_stride, false))
       cfg = t->root;
     else if (total >= kTuneMinRows)
-      cfg = dp::tune_dense_hist(*layout, bins, nullptr, bin_stride, gpair, s).root;
+      cfg = dp::tune_dense_hist(*layout, bins, false, bin_stride, gpair, s).root;
   }
   std::vector<dp::HistWork> work;
   std::vector<dp::HistReduce> jobs;

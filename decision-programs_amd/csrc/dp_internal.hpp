@@ -292,10 +292,35 @@ struct HistConfig {
   int32_t deep = 0;  // 1: three blocks of rows in flight per workgroup (split 0 only)
 };
 
+// Paired tiles (dp_bin_layout::paired_tiles): bit t joins tiles t and t + 1
+// into one work item whose rows add one joint byte per feature pair.  Only
+// one-tile items pair; hist_pairs gives the pairs a configuration uses.
+__host__ __device__ inline uint64_t hist_pairs(uint64_t paired_tiles, int32_t tiles) {
+  return tiles == 1 ? paired_tiles : 0;
+}
+// Work items per row chunk: tile groups of `tiles` tiles, less one per pair.
+__host__ __device__ inline int32_t hist_groups(int32_t n_tiles, int32_t tiles, uint64_t pairs) {
+  return (n_tiles + tiles - 1) / tiles - __builtin_popcountll(pairs);
+}
+// Tile t is the second of a pair (its rows go with tile t - 1's item).
+__host__ __device__ inline bool pair_second(uint64_t pairs, int32_t t) {
+  return t >= 1 && t <= 64 && ((pairs >> (t - 1)) & 1ull);
+}
+// The pairs of a matrix: tiles t, t + 1 (left to right, t < 63) whose
+// features all have at most 16 bins (n_bins[f], f < n_features; pad features
+// count as such); none when the matrix has missing values.
+uint64_t pair_tiles(const int32_t* n_bins, int32_t n_features, int32_t n_tiles, bool missing);
+// Rejects a layout whose paired_tiles the histogram kernel cannot take.
+void check_pairs(const dp_bin_layout& layout);
+
 // Histograms: every work item accumulates into hist[slot]; hist must be zero.
 // Direct items write hist; the others write partial (int64 [slot][bin_stride * 32]).
 // row_major: optional row-major copy of the bins (launch_tiles_to_rows), read
-// for gathered rows.  The work items must come from the same cfg.tiles.
+// for gathered rows; when the configuration uses the layout's pairs (one tile
+// per item), it must be the copy that holds each pair's joint tile in place of
+// its first tile (launch_tiles_to_rows with that layout), else the plain copy.
+// The work items must come from the same cfg.tiles and layout (its
+// paired_tiles: launch_hist pairs what make_hist_work paired).
 // skip (matrices without missing values): per tile, the 16 features' skip
 // bins ([n_tiles][16] bytes); rows in a feature's skip bin add nothing, so that
 // bin's sums stay zero (the split evaluation restores them from the node's
@@ -324,11 +349,16 @@ void launch_hist_reduce(const int64_t* partial, const HistReduce* jobs, int32_t 
                         int32_t bin_stride, const int64_t* parent_base, int64_t* hist,
                         bool accumulate, hipStream_t s);
 // Minimum rows per histogram chunk and the chunk size for `rows` rows when
-// each row chunk makes `groups` work items: about `items` work items in all on
-// large levels.  On smaller levels of matrices with at most four groups, about
-// k * 256 items (k whole items per CU, k = 1..3), so that no CU is left with
-// one more item after the others finish (with more groups the item count moves
-// in steps of the group count, and the rule measured no better).
+// each row chunk makes `groups` work items: at most `items` work items in all
+// on large levels (items / groups row chunks, rounded down to a multiple of 8,
+// the XCD interleave's unit, so that a group count that does not divide
+// `items` -- seven with one pair of eight tiles -- leaves no real item behind
+// the padding of a last partial block of 8 chunks, past the workgroups the
+// chip holds at once).  On smaller levels of matrices
+// with at most four groups, about k * 256 items (k whole items per CU, k =
+// 1..3), so that no CU is left with one more item after the others finish
+// (with more groups the item count moves in steps of the group count, and the
+// rule measured no better).
 constexpr int64_t kHistMinChunk = 4096;
 __host__ __device__ inline int64_t hist_chunk(int64_t rows, int32_t groups, int32_t items) {
   const int64_t units = rows * groups;
@@ -339,7 +369,9 @@ __host__ __device__ inline int64_t hist_chunk(int64_t rows, int32_t groups, int3
     const uint32_t k = u < 256u * kHistMinChunk ? 1u : u / uint32_t(256 * kHistMinChunk);
     c = int64_t((u + 256u * k - 1u) / (256u * k));
   } else {
-    c = (units + items - 1) / items;
+    int64_t per = items >= groups ? items / groups : 1;  // row chunks
+    if (per >= 8) per = per / 8 * 8;
+    c = (rows + per - 1) / per;
   }
   return c < kHistMinChunk ? kHistMinChunk : c;
 }
@@ -367,10 +399,11 @@ __host__ __device__ inline int64_t hist_chunk_fit(int64_t rows, int64_t nodes, i
   return c2 > c && (rounds - 1) * c2 < rounds * c ? c2 : c;
 }
 // Partial slots needed by one level: the chunks of nodes with two or more
-// chunks number at most 2 * items / groups, each with n_tiles slots, i.e. at
-// most 2 * items * tiles_per_item slots.
-inline int64_t hist_partial_capacity(int32_t n_tiles, const HistConfig& cfg) {
-  return 2 * int64_t(cfg.items) * cfg.tiles + int64_t(n_tiles);
+// chunks number at most 2 * items / groups, each with n_tiles slots (groups:
+// hist_groups, at least n_tiles / 2 with pairs).
+inline int64_t hist_partial_capacity(int32_t n_tiles, const HistConfig& cfg, uint64_t pairs) {
+  const int64_t g = hist_groups(n_tiles, cfg.tiles, hist_pairs(pairs, cfg.tiles));
+  return (2 * int64_t(cfg.items) * n_tiles + g - 1) / g + int64_t(n_tiles);
 }
 // Work items and reduce jobs for the histograms of n_nodes row sets (node i:
 // [begin[i], end[i]) of ridx, written to hist slot slots[i], or i when slots
@@ -379,7 +412,8 @@ inline int64_t hist_partial_capacity(int32_t n_tiles, const HistConfig& cfg) {
 // n_tiles > 0 overrides the layout's tile count (present-value tiles).
 // Returns the number of partial slots used.
 // n_tiles > 0: present-value tiles, one per item; otherwise cfg.tiles of the
-// layout's 16-feature tiles per item.
+// layout's 16-feature tiles per item, and with one tile per item one item for
+// each pair of paired_tiles (its partial slots stay one per tile).
 int32_t make_hist_work(const dp_bin_layout& layout, const int64_t* begin, const int64_t* end,
                        const int32_t* slots, int32_t n_nodes, bool allow_direct,
                        std::vector<HistWork>& work, std::vector<HistReduce>& jobs,
@@ -566,6 +600,7 @@ struct PlanArgs {
   int32_t depth, max_depth;
   int32_t n_tiles;
   int32_t hist_tiles;      // tiles per histogram work item (HistConfig::tiles; 1 for present-value)
+  uint64_t hist_pairs;     // paired tiles of the level's items (hist_pairs; 0 for present-value)
   int32_t hist_items;      // work items a histogram pass aims at (HistConfig::items)
   int32_t hist_slots;      // histogram workgroups the chip holds at once (hist_chunk_fit; 0: off)
   int64_t hist_elems;      // int64 values per node histogram
@@ -752,9 +787,16 @@ void launch_hist_reduce_flat(const int64_t* partial, const HistReduce* jobs, int
 
 void launch_tiles_to_columns(const uint8_t* bins, const dp_bin_layout& layout, uint8_t* cols,
                              hipStream_t s);
-// rows[r * n_tiles * 16 + t * 16 + j] = tile t's byte j of row r.
+// rows[r * n_tiles * 16 + t * 16 + j] = tile t's byte j of row r; for the
+// first tile t of each of the layout's pairs, the pair's joint tile instead
+// (from the tile-major bins, which hold it): the copy the gathered passes of
+// one-tile items read with the pairs in use (launch_hist).
 void launch_tiles_to_rows(const uint8_t* bins, const dp_bin_layout& layout, uint8_t* rows,
                           hipStream_t s);
+// Writes the joint tiles of the layout's pairs (after its n_tiles tiles) from
+// the tiles they pair: per row and feature slot i, the byte (tile t's bin <<
+// 4) | (tile t + 1's bin & 15).
+void launch_join_tiles(uint8_t* bins, const dp_bin_layout& layout, hipStream_t s);
 
 // Quantile cuts on the device; host outputs as in dp_sketch_cuts.
 void sketch_cuts(dp_workspace_s& ws, const float* values, int64_t n_rows, int32_t n_features,

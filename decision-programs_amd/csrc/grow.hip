@@ -280,7 +280,8 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
     }
     int64_t small_total;
     (void)block_scan(mine, scan, &small_total);
-    const int32_t TPW = a.hist_tiles, G = (T + TPW - 1) / TPW;  // items per row chunk
+    const int32_t TPW = a.hist_tiles;
+    const int32_t G = hist_groups(T, TPW, a.hist_pairs);  // items per row chunk
     const int64_t chunk = hist_chunk_fit(small_total, n_expand, G, a.hist_items, a.hist_slots);
     int64_t* cstart = a.pair_chunk;                 // [n_expand + 1]
     int64_t* pstart = a.pair_chunk + n_expand + 1;  // [n_expand + 1]
@@ -332,10 +333,13 @@ __global__ __launch_bounds__(kPlanThreads) void plan_level_kernel(PlanArgs a) {
                           b + chunk < sm.end ? b + chunk : sm.end, -1, l.parent_slot};
           if (pair_off[j + 1] - pair_off[j] >= 2) p = (pstart[j] + k) * T;
         }
-        for (int32_t g = 0; g < G; ++g) {  // tile group g: tiles g * TPW ..
-          item.tile = g * TPW;
-          item.partial = p < 0 ? -1 : int32_t(p + g * TPW);
+        int32_t g = 0;  // tile group g: its first tile t
+        for (int32_t t = 0; t < T; t += TPW) {
+          if (pair_second(a.hist_pairs, t)) continue;
+          item.tile = t;
+          item.partial = p < 0 ? -1 : int32_t(p + t);
           a.hist_work[((c / 8) * G + g) * 8 + (c % 8)] = item;
+          ++g;
         }
       }
       for (int32_t j = tid; j < n_expand; j += kPlanThreads) {
@@ -610,7 +614,8 @@ __device__ void plan_small_level(const PlanArgs& a) {
 
   // ---- second scan: histogram chunks of the smaller children -----------------
   const int32_t T = a.n_tiles;
-  const int32_t TPW = a.hist_tiles, G = (T + TPW - 1) / TPW;  // items per row chunk
+  const int32_t TPW = a.hist_tiles;
+  const int32_t G = hist_groups(T, TPW, a.hist_pairs);  // items per row chunk
   const int64_t chunk = hist_chunk_fit(tot[2], tot[0], G, a.hist_items, a.hist_slots);
   const int64_t nc = wave_live ? ceil_rows(cnt[2], chunk) : 0;
   int64_t cnt2[2] = {nc, nc >= 2 ? nc : 0}, off2[2], tot2[2];
@@ -682,10 +687,13 @@ __device__ void plan_small_level(const PlanArgs& a) {
           item = HistWork{s_slot[j], 0, b, b + chunk < se ? b + chunk : se, -1, j};
           if (s_cs[j + 1] - s_cs[j] >= 2) p = (s_ps[j] + k) * T;
         }
-        for (int32_t g = 0; g < G; ++g) {  // tile group g: tiles g * TPW ..
-          item.tile = g * TPW;
-          item.partial = p < 0 ? -1 : int32_t(p + g * TPW);
+        int32_t g = 0;  // tile group g: its first tile t
+        for (int32_t t = 0; t < T; t += TPW) {
+          if (pair_second(a.hist_pairs, t)) continue;
+          item.tile = t;
+          item.partial = p < 0 ? -1 : int32_t(p + t);
           a.hist_work[((c / 8) * G + g) * 8 + (c % 8)] = item;
+          ++g;
         }
       }
       if (e)

@@ -133,39 +133,42 @@ constexpr int kHistThreads = 1024;
 // bins', which the split evaluation restores).  On data dominated by one value
 // per feature (C4's zero pixels) this removes most atomics and their
 // same-address conflicts.  MODE 1 is the missing-byte skip above; MODE 0 none.
-template <bool GATHER, int MODE, int TPW, int U, int SPLIT = 0, bool DEEP = false>
-__global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(DEEP ? 4 : 8 / TPW, 8 / TPW))) void hist_kernel(
-    const uint8_t* __restrict__ bins, const uint8_t* __restrict__ skip, int64_t n_rows,
-    int32_t n_features, int32_t n_tiles,
-    const int2* __restrict__ gpair, const uint32_t* __restrict__ ridx,
-    const HistWork* __restrict__ work, int32_t n_work_host,
-    const int32_t* __restrict__ n_work_dev, int32_t bin_stride,
-    unsigned long long* __restrict__ hist, unsigned long long* __restrict__ partial,
-    int64_t tile_step, int64_t row_step, int32_t fmaj) {
-  extern __shared__ unsigned long long lds[];  // TPW * kLdsWords
+// PAIR (one-tile items without missing values or skip bins): the item covers
+// tiles t and t + 1 of dp_bin_layout::paired_tiles, whose bins are all below
+// 16, and reads their joint tile (per row and feature slot i the byte tile
+// t's bin << 4 | tile t + 1's bin: stored after the matrix's tiles, and in
+// place of tile t in the row-major copy of gathered passes), so the
+// row's 32 features cost one 16-byte load and the 16 atomic pairs of one tile:
+// an ordinary item's work.  The flush takes the marginals: tile t's bin a is
+// the sum of joint bins 16 a .. 16 a + 15, tile t + 1's bin b the sum of joint
+// bins b, b + 16, ... (one word per thread, 16 LDS reads), and bins 16 and up
+// of both tiles are zero.  Both tiles' outputs have the layout of two ordinary
+// items.
+struct HistPass {
+  const uint8_t* bins;
+  const uint8_t* skip;
+  int32_t n_features, n_tiles;
+  const int2* gpair;
+  const uint32_t* ridx;
+  int32_t bin_stride;
+  unsigned long long* hist;
+  unsigned long long* partial;
+  int64_t tile_step, row_step;
+  int32_t fmaj;
+};
+
+// src_tile: the tile whose bytes the item reads (w.tile, or a pair's joint tile).
+template <bool GATHER, int MODE, int TPW, int U, int SPLIT, bool DEEP, bool PAIR>
+__device__ __forceinline__ void hist_item(const HistPass& a, const HistWork& w, int32_t src_tile,
+                                          unsigned long long* lds, const uint32_t (&slotw)[4],
+                                          uint32_t rot) {
+  static_assert(!PAIR || (TPW == 1 && MODE == 0), "pairs take one-tile items without skips");
   constexpr int64_t kStep = int64_t(kHistThreads) * U;
   constexpr int PD = DEEP ? 3 : (GATHER ? 1 : 0);  // prefetch depth (blocks)
   constexpr int R = PD + 1;                         // ring buffers
-  // The first item is loaded alongside the device count (the host bound keeps
-  // it in range), so the two loads overlap instead of chaining.
-  const HistWork w_first =
-      int32_t(blockIdx.x) < n_work_host ? work[blockIdx.x] : HistWork{0, 0, 0, 0, -1, 0};
-  const int32_t n_work = n_work_dev ? *n_work_dev : n_work_host;
-  const uint32_t rot = threadIdx.x & 15u;
-  uint32_t slotw[4];  // byte i of slotw[m]: feature offset (bytes) of step 4m+i
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    uint32_t v = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v |= (((uint32_t(4 * m + i) + rot) & 15u) * 8u) << (8 * i);
-    slotw[m] = v;
-  }
   lds_u8* const lds_base = (lds_u8*)lds;
-  for (int32_t item = blockIdx.x; item < n_work; item += gridDim.x) {
-  const HistWork w = item == int32_t(blockIdx.x) ? w_first : work[item];
-  if (w.begin >= w.end) continue;  // padding item (uniform per workgroup)
-  // tiles of this item that exist (uniform per workgroup)
-  const int nt = TPW == 1 ? 1 : (w.tile + TPW <= n_tiles ? TPW : n_tiles - w.tile);
+  // tiles of this item that exist (uniform per workgroup); a pair fills one LDS tile
+  const int nt = TPW == 1 ? 1 : (w.tile + TPW <= a.n_tiles ? TPW : a.n_tiles - w.tile);
   // This lane's tile order: swapped when SPLIT applies and both tiles exist.
   const int swap = (SPLIT > 0 && nt == 2) ? int((threadIdx.x >> SPLIT) & 1u) : 0;
   // MODE 2: each tile's skip bins, rotated like the row bytes (byte k of the
@@ -174,8 +177,8 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(DE
   if constexpr (MODE == 2) {
 #pragma unroll
     for (int j = 0; j < TPW; ++j) {
-      const uint4 s4 =
-          *reinterpret_cast<const uint4*>(skip + int64_t(w.tile + (j < nt ? j ^ swap : 0)) * kTile);
+      const uint4 s4 = *reinterpret_cast<const uint4*>(
+          a.skip + int64_t(w.tile + (j < nt ? j ^ swap : 0)) * kTile);
       sk[j][0] = s4.x;
       sk[j][1] = s4.y;
       sk[j][2] = s4.z;
@@ -183,7 +186,7 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(DE
       rotate16(sk[j], rot);
     }
   }
-  const uint8_t* tile = bins + int64_t(w.tile) * tile_step;  // row r at tile + r * row_step
+  const uint8_t* tile = a.bins + int64_t(src_tile) * a.tile_step;  // row r at tile + r * row_step
   const int64_t last = w.end - 1;
   const int64_t lane = threadIdx.x;
   uint32_t rows[R][U];  // GATHER: row ids
@@ -193,7 +196,7 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(DE
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t i = base + int64_t(u) * kHistThreads + lane;
-      rows[b][u] = ridx[i < w.end ? i : last];
+      rows[b][u] = a.ridx[i < w.end ? i : last];
     }
   };
   auto fetch_data = [&](int b, int64_t base) {
@@ -201,11 +204,11 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(DE
     for (int u = 0; u < U; ++u) {
       const int64_t i = base + int64_t(u) * kHistThreads + lane;
       const uint32_t r = GATHER ? rows[b][u] : uint32_t(i < w.end ? i : last);
-      const uint8_t* src = tile + int64_t(r) * row_step;
+      const uint8_t* src = tile + int64_t(r) * a.row_step;
 #pragma unroll
       for (int j = 0; j < TPW; ++j)  // a missing second tile re-reads the first
-        v[b][u][j] = *reinterpret_cast<const uint4*>(src + (j < nt ? j ^ swap : 0) * tile_step);
-      q[b][u] = gpair[r];
+        v[b][u][j] = *reinterpret_cast<const uint4*>(src + (j < nt ? j ^ swap : 0) * a.tile_step);
+      q[b][u] = a.gpair[r];
     }
   };
   auto process = [&](int b, int64_t base) {
@@ -217,13 +220,13 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(DE
 #pragma unroll
       for (int j = 0; j < TPW; ++j) {
         if (j >= nt) break;  // uniform per workgroup
-        uint32_t a[4] = {v[b][u][j].x, v[b][u][j].y, v[b][u][j].z, v[b][u][j].w};
-        rotate16(a, rot);
+        uint32_t x[4] = {v[b][u][j].x, v[b][u][j].y, v[b][u][j].z, v[b][u][j].w};
+        rotate16(x, rot);
         lds_u8* const base_j = lds_base + (j ^ swap) * (kLdsWords * 8);
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
           const uint32_t sel = 0x0c0c0000u | ((4u + uint32_t(k & 3)) << 8) | uint32_t(k & 3);
-          const uint32_t off = __builtin_amdgcn_perm(a[k >> 2], slotw[k >> 2], sel);
+          const uint32_t off = __builtin_amdgcn_perm(x[k >> 2], slotw[k >> 2], sel);
           if (MODE == 1 && off >= 255u * 256u) continue;  // byte 255: missing value
           if (MODE == 2 && off == __builtin_amdgcn_perm(sk[j][k >> 2], slotw[k >> 2], sel))
             continue;  // the feature's skip bin
@@ -267,33 +270,120 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(DE
   }
   __syncthreads();
 
-  const int n_words = bin_stride * 32;  // bins < bin_stride, 32 words each
-  for (int j = 0; j < nt; ++j) {
-    const unsigned long long* src = lds + j * kLdsWords;
-    if (w.partial >= 0 && fmaj) {  // feature-major partial slot: [16][bin_stride][g, h]
-      // Pair q = (bin q / 16, feature q % 16): its (g, h) words, 16 bytes at
-      // (feature * bin_stride + bin) * 2.  One store instruction of a
-      // wavefront writes four bins of 16 features, a 64-byte run per feature;
-      // the LDS reads of one feature's four bins share a bank pair (4-way).
-      auto* out = reinterpret_cast<ulonglong2*>(partial + int64_t(w.partial + j) * n_words);
-      for (int q = threadIdx.x; q < 16 * bin_stride; q += kHistThreads) {
-        const int fl = q & 15, b = q >> 4;
-        out[fl * bin_stride + b] = make_ulonglong2(src[b * 32 + fl], src[b * 32 + 16 + fl]);
+  const int n_words = a.bin_stride * 32;  // bins < bin_stride, 32 words each
+  if constexpr (PAIR) {
+    static_assert(kHistThreads == 1024, "one marginal word per thread");
+    // Thread e: output tile jj = e / 512 (0: tile t, 1: tile t + 1), bin x,
+    // word c of the LDS row layout (g of the 16 features, then h).  e is
+    // opaque to the compiler here, so that nothing derived from it is hoisted
+    // out of the item loop and held in registers across the row loop.
+    int e = int(threadIdx.x);
+    __asm__ volatile("" : "+v"(e));
+    const int jj = e >> 9, x = (e >> 5) & 15, c = e & 31;
+    unsigned long long m = 0;
+#pragma unroll 2
+    for (int y = 0; y < 16; ++y) m += lds[(jj ? 16 * y + x : 16 * x + y) * 32 + c];
+    // Tile jj's output: the partial slot w.partial + jj (LDS image or
+    // feature-major) or, for a direct item, its features of node w.slot.
+    const bool image = w.partial >= 0 && !a.fmaj;
+    const int64_t node_words = int64_t(a.n_features) * a.bin_stride * 2;
+    // off: the word within the image, else within feature fi's bins.
+    auto put = [&](int t, int fi, int off, unsigned long long val) {
+      if (image) {
+        a.partial[int64_t(w.partial + t) * n_words + off] = val;
+      } else if (w.partial >= 0) {
+        a.partial[int64_t(w.partial + t) * n_words + int64_t(fi) * a.bin_stride * 2 + off] = val;
+      } else {
+        const int f = (w.tile + t) * kTile + fi;
+        if (f < a.n_features)
+          a.hist[int64_t(w.slot) * node_words + int64_t(f) * a.bin_stride * 2 + off] = val;
       }
-    } else if (w.partial >= 0) {  // tile j's partial slot is the item's slot + j (LDS image)
-      unsigned long long* out = partial + int64_t(w.partial + j) * n_words;
-      for (int e = threadIdx.x; e < n_words; e += kHistThreads) out[e] = src[e];
-    } else {
-      unsigned long long* out = hist + int64_t(w.slot) * n_features * bin_stride * 2;
-      const int f0 = (w.tile + j) * kTile;
-      for (int e = threadIdx.x; e < n_words; e += kHistThreads) {
-        const int bin = e >> 5, within = e & 31;
-        const int f = f0 + (within & 15);
-        if (f < n_features) out[(int64_t(f) * bin_stride + bin) * 2 + (within >> 4)] = src[e];
+    };
+    if (x < a.bin_stride) put(jj, c & 15, image ? x * 32 + c : x * 2 + (c >> 4), m);
+    // bins 16 .. bin_stride - 1 of both tiles: zero
+    const int zb = a.bin_stride > 16 ? a.bin_stride - 16 : 0;
+    if (image) {  // rows 16 and up: one run of zb * 32 words per tile
+      for (int z = e; z < 2 * zb * 32; z += kHistThreads) {
+        const int t = z >= zb * 32 ? 1 : 0;
+        put(t, 0, 16 * 32 + (z - t * zb * 32), 0ull);
+      }
+    } else {  // per feature: a run of zb * 2 words from bin 16
+      const int per = zb * 2;
+      for (int z = e; z < 2 * 16 * per; z += kHistThreads) {
+        const int t = z >= 16 * per ? 1 : 0, r = z - t * 16 * per, fi = r / per;
+        put(t, fi, 32 + (r - fi * per), 0ull);
+      }
+    }
+  } else {
+    for (int j = 0; j < nt; ++j) {
+      const unsigned long long* src = lds + j * kLdsWords;
+      if (w.partial >= 0 && a.fmaj) {  // feature-major partial slot: [16][bin_stride][g, h]
+        // Pair q = (bin q / 16, feature q % 16): its (g, h) words, 16 bytes at
+        // (feature * bin_stride + bin) * 2.  One store instruction of a
+        // wavefront writes four bins of 16 features, a 64-byte run per feature;
+        // the LDS reads of one feature's four bins share a bank pair (4-way).
+        auto* out = reinterpret_cast<ulonglong2*>(a.partial + int64_t(w.partial + j) * n_words);
+        for (int q = threadIdx.x; q < 16 * a.bin_stride; q += kHistThreads) {
+          const int fl = q & 15, b = q >> 4;
+          out[fl * a.bin_stride + b] = make_ulonglong2(src[b * 32 + fl], src[b * 32 + 16 + fl]);
+        }
+      } else if (w.partial >= 0) {  // tile j's partial slot is the item's slot + j (LDS image)
+        unsigned long long* out = a.partial + int64_t(w.partial + j) * n_words;
+        for (int e = threadIdx.x; e < n_words; e += kHistThreads) out[e] = src[e];
+      } else {
+        unsigned long long* out = a.hist + int64_t(w.slot) * a.n_features * a.bin_stride * 2;
+        const int f0 = (w.tile + j) * kTile;
+        for (int e = threadIdx.x; e < n_words; e += kHistThreads) {
+          const int bin = e >> 5, within = e & 31;
+          const int f = f0 + (within & 15);
+          if (f < a.n_features)
+            out[(int64_t(f) * a.bin_stride + bin) * 2 + (within >> 4)] = src[e];
+        }
       }
     }
   }
   __syncthreads();  // the next item clears the LDS this item just read
+}
+
+template <bool GATHER, int MODE, int TPW, int U, int SPLIT = 0, bool DEEP = false>
+__global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(DEEP && (U == 2 || MODE != 0) ? 4 : 8 / TPW, 8 / TPW))) void hist_kernel(
+    const uint8_t* __restrict__ bins, const uint8_t* __restrict__ skip, int64_t n_rows,
+    int32_t n_features, int32_t n_tiles,
+    const int2* __restrict__ gpair, const uint32_t* __restrict__ ridx,
+    const HistWork* __restrict__ work, int32_t n_work_host,
+    const int32_t* __restrict__ n_work_dev, int32_t bin_stride,
+    unsigned long long* __restrict__ hist, unsigned long long* __restrict__ partial,
+    int64_t tile_step, int64_t row_step, int32_t fmaj, uint64_t pairs, int32_t joint_first) {
+  extern __shared__ unsigned long long lds[];  // TPW * kLdsWords
+  // The first item is loaded alongside the device count (the host bound keeps
+  // it in range), so the two loads overlap instead of chaining.
+  const HistWork w_first =
+      int32_t(blockIdx.x) < n_work_host ? work[blockIdx.x] : HistWork{0, 0, 0, 0, -1, 0};
+  const int32_t n_work = n_work_dev ? *n_work_dev : n_work_host;
+  const uint32_t rot = threadIdx.x & 15u;
+  uint32_t slotw[4];  // byte i of slotw[m]: feature offset (bytes) of step 4m+i
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    uint32_t v = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v |= (((uint32_t(4 * m + i) + rot) & 15u) * 8u) << (8 * i);
+    slotw[m] = v;
+  }
+  (void)n_rows;
+  const HistPass a{bins, skip, n_features, n_tiles, gpair, ridx, bin_stride, hist, partial,
+                   tile_step, row_step, fmaj};
+  for (int32_t item = blockIdx.x; item < n_work; item += gridDim.x) {
+    const HistWork w = item == int32_t(blockIdx.x) ? w_first : work[item];
+    if (w.begin >= w.end) continue;  // padding item (uniform per workgroup)
+    if constexpr (TPW == 1 && MODE == 0) {
+      if (pair_second(pairs, w.tile + 1)) {  // w.tile is the first of pair k
+        const int32_t k = __builtin_popcountll(pairs & ((1ull << w.tile) - 1ull));
+        const int32_t jt = joint_first < 0 ? w.tile : joint_first + k;  // its joint tile
+        hist_item<GATHER, MODE, TPW, U, SPLIT, DEEP, true>(a, w, jt, lds, slotw, rot);
+        continue;
+      }
+    }
+    hist_item<GATHER, MODE, TPW, U, SPLIT, DEEP, false>(a, w, w.tile, lds, slotw, rot);
   }
 }
 
@@ -783,7 +873,9 @@ int32_t make_hist_work(const dp_bin_layout& layout, const int64_t* begin, const 
                        int32_t n_tiles, const HistConfig& cfg) {
   const int64_t T = n_tiles > 0 ? n_tiles : layout.n_tiles;
   const int64_t tpw = n_tiles > 0 ? 1 : cfg.tiles;  // present-value tiles: one per item
-  const int64_t G = (T + tpw - 1) / tpw;            // work items per row chunk
+  const uint64_t pairs = n_tiles > 0 ? 0 : hist_pairs(layout.paired_tiles, cfg.tiles);
+  if (pairs) check_pairs(layout);
+  const int64_t G = hist_groups(int32_t(T), int32_t(tpw), pairs);  // work items per row chunk
   // About cfg.items items (two waves of resident workgroups on 256 CUs at the
   // default), at least kHistMinChunk rows each, so the per-item LDS clear and
   // store stay small.
@@ -814,15 +906,46 @@ int32_t make_hist_work(const dp_bin_layout& layout, const int64_t* begin, const 
   // then hit that XCD's L2.
   const int64_t groups = (int64_t(chunks.size()) + 7) / 8;
   work.assign(size_t(groups * G * 8), HistWork{0, 0, 0, 0, -1, 0});
-  for (int64_t c = 0; c < int64_t(chunks.size()); ++c)
-    for (int64_t g = 0; g < G; ++g) {
-      const Chunk& ch = chunks[size_t(c)];
+  for (int64_t c = 0; c < int64_t(chunks.size()); ++c) {
+    const Chunk& ch = chunks[size_t(c)];
+    int64_t g = 0;  // tile group g: its first tile t
+    for (int64_t t = 0; t < T; t += tpw) {
+      if (pair_second(pairs, int32_t(t))) continue;
       const int64_t b = ((c / 8) * G + g) * 8 + (c % 8);
-      const int64_t t = g * tpw;
       work[size_t(b)] = {ch.slot, int32_t(t), ch.b, ch.e,
                          ch.partial < 0 ? -1 : int32_t(ch.partial * T + t), -1};
+      ++g;
     }
+  }
   return n_partial * int32_t(T);
+}
+
+uint64_t pair_tiles(const int32_t* n_bins, int32_t n_features, int32_t n_tiles, bool missing) {
+  if (missing) return 0;
+  auto narrow = [&](int32_t t) {  // every feature of tile t has at most 16 bins
+    for (int32_t f = t * kTile; f < std::min((t + 1) * kTile, n_features); ++f)
+      if (n_bins[f] > 16) return false;
+    return true;
+  };
+  uint64_t m = 0;
+  for (int32_t t = 0; t + 1 < n_tiles && t < 63;) {
+    if (narrow(t) && narrow(t + 1)) {
+      m |= 1ull << t;
+      t += 2;
+    } else {
+      t += 1;
+    }
+  }
+  return m;
+}
+
+void check_pairs(const dp_bin_layout& layout) {
+  const uint64_t p = layout.paired_tiles;
+  if (!p) return;
+  need(layout.missing_bin < 0, "paired tiles need a matrix without missing values");
+  need((p & (p << 1)) == 0, "a tile belongs to at most one pair");
+  const int32_t last = std::min(layout.n_tiles - 1, 63);  // bit t needs tile t + 1
+  need(last > 0 && (p >> last) == 0, "paired tile beyond the matrix");
 }
 
 namespace {
@@ -917,8 +1040,14 @@ void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t
   const uint8_t* src = rows ? row_major : bins;
   const int64_t tile_step = rows ? kTile : layout.n_rows * kTile;
   const int64_t row_step = rows ? int64_t(layout.n_tiles) * kTile : kTile;
+  // A pair's joint tile: tile n_tiles + k of the tile-major bins, or in place
+  // of the pair's first tile in the row-major copy (joint_first -1).
+  const int32_t joint_first = rows ? -1 : layout.n_tiles;
   const bool missing = layout.missing_bin >= 0;
   need(!(missing && skip), "skip bins apply to matrices without missing values");
+  const uint64_t pairs = hist_pairs(layout.paired_tiles, cfg.tiles);
+  check_pairs(layout);
+  need(!(pairs && skip), "paired tiles and skip bins do not combine");
   const int mode = mode_of(missing, skip != nullptr);
   auto kernel = ridx ? hist_mode<true>(mode, cfg) : hist_mode<false>(mode, cfg);
   const size_t lds = size_t(cfg.tiles) * kLdsWords * sizeof(unsigned long long);
@@ -929,7 +1058,8 @@ void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t
   grid = (grid + 7) / 8 * 8;
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(kHistThreads), lds, s, src, skip, layout.n_rows,
                      layout.n_features, layout.n_tiles, gp, ridx, work, n_work, n_work_dev,
-                     bin_stride, out, part, tile_step, row_step, fmaj ? 1 : 0);
+                     bin_stride, out, part, tile_step, row_step, fmaj ? 1 : 0, pairs,
+                     joint_first);
   DP_HIP(hipGetLastError());
 }
 

@@ -257,15 +257,46 @@ __global__ __launch_bounds__(256) void tiles_to_columns_kernel(const uint8_t* __
   }
 }
 
-// Row-major copy of tile-major bins: one 16-byte piece per thread.
+// Joint tiles of the paired tiles (dp_bin_layout::paired_tiles): joint tile
+// n_tiles + k, for the k-th pair (tiles t, t + 1; blockIdx.y = k), holds per
+// row and feature slot i the byte (tile t's bin << 4) | (tile t + 1's bin &
+// 15).  One row per thread: two 16-byte loads, one store.
+__global__ void join_tiles_kernel(uint8_t* __restrict__ bins, int64_t n_rows, int32_t n_tiles,
+                                  uint64_t pairs) {
+  const int32_t k = int32_t(blockIdx.y);
+  uint64_t m = pairs;
+  for (int32_t j = 0; j < k; ++j) m &= m - 1ull;  // drop the first k pairs
+  const int64_t t = __builtin_ctzll(m);
+  const uint8_t* hi = bins + t * n_rows * 16;
+  const uint8_t* lo = hi + n_rows * 16;
+  uint8_t* out = bins + int64_t(n_tiles + k) * n_rows * 16;
+  for (int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; r < n_rows;
+       r += int64_t(blockDim.x) * gridDim.x) {
+    const uint4 x = *reinterpret_cast<const uint4*>(hi + r * 16);
+    const uint4 y = *reinterpret_cast<const uint4*>(lo + r * 16);
+    uint4 z;
+    z.x = ((x.x << 4) & 0xf0f0f0f0u) | (y.x & 0x0f0f0f0fu);
+    z.y = ((x.y << 4) & 0xf0f0f0f0u) | (y.y & 0x0f0f0f0fu);
+    z.z = ((x.z << 4) & 0xf0f0f0f0u) | (y.z & 0x0f0f0f0fu);
+    z.w = ((x.w << 4) & 0xf0f0f0f0u) | (y.w & 0x0f0f0f0fu);
+    *reinterpret_cast<uint4*>(out + r * 16) = z;
+  }
+}
+
+// Row-major copy of tile-major bins: one 16-byte piece per thread.  The first
+// tile of each pair takes the pair's joint tile (tile n_tiles + k of the
+// tile-major bins for the k-th pair).
 __global__ void tiles_to_rows_kernel(const uint8_t* __restrict__ bins, int64_t n_rows,
-                                     int32_t n_tiles, uint8_t* __restrict__ rows) {
+                                     int32_t n_tiles, uint64_t pairs, uint8_t* __restrict__ rows) {
   const int64_t n = n_rows * n_tiles;
   for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
        i += int64_t(blockDim.x) * gridDim.x) {
     const int64_t t = i / n_rows, r = i - t * n_rows;
+    const int64_t src = t < 63 && ((pairs >> t) & 1ull)
+                            ? n_tiles + __builtin_popcountll(pairs & ((1ull << t) - 1ull))
+                            : t;
     *reinterpret_cast<uint4*>(rows + (r * n_tiles + t) * 16) =
-        *reinterpret_cast<const uint4*>(bins + i * 16);
+        *reinterpret_cast<const uint4*>(bins + (src * n_rows + r) * 16);
   }
 }
 
@@ -454,8 +485,19 @@ void launch_tiles_to_rows(const uint8_t* bins, const dp_bin_layout& layout, uint
                           hipStream_t s) {
   if (layout.n_rows <= 0) return;
   need(layout.tile_width == 16, "row copy needs 16-feature tiles");
-  hipLaunchKernelGGL(tiles_to_rows_kernel, dim3(grid_for(layout.n_rows * layout.n_tiles, 256, 8192)),
-                     dim3(256), 0, s, bins, layout.n_rows, layout.n_tiles, rows);
+  check_pairs(layout);
+  hipLaunchKernelGGL(tiles_to_rows_kernel,
+                     dim3(grid_for(layout.n_rows * layout.n_tiles, 256, 8192)), dim3(256), 0, s,
+                     bins, layout.n_rows, layout.n_tiles, layout.paired_tiles, rows);
+  DP_HIP(hipGetLastError());
+}
+
+void launch_join_tiles(uint8_t* bins, const dp_bin_layout& layout, hipStream_t s) {
+  if (!layout.paired_tiles || layout.n_rows <= 0) return;
+  check_pairs(layout);
+  const int32_t pairs = __builtin_popcountll(layout.paired_tiles);
+  hipLaunchKernelGGL(join_tiles_kernel, dim3(grid_for(layout.n_rows, 256, 4096), pairs),
+                     dim3(256), 0, s, bins, layout.n_rows, layout.n_tiles, layout.paired_tiles);
   DP_HIP(hipGetLastError());
 }
 

@@ -15,6 +15,9 @@
 //                         registers, possibly fewer resident workgroups);
 //   work items per pass   512, 1024 or 2048 (fewer, longer row chunks write
 //                         fewer partial tiles; more balance the CUs better).
+// A layout with paired tiles (tiles whose features all have at most 16 bins)
+// is tuned as such: one-tile candidates pair them, two-tile candidates do not,
+// and the timings decide between them.
 // The contiguous (root) pass is timed over the whole matrix; the gathered pass
 // through the row-major copy, as the levels below the root read it, over 12
 // nodes whose rows are strided over the matrix (node k: rows k, k + 32, ...),
@@ -37,7 +40,7 @@
 namespace dp {
 namespace {
 
-using Key = std::tuple<int64_t, int32_t, int32_t, int32_t, int32_t, int32_t>;
+using Key = std::tuple<int64_t, int32_t, int32_t, int32_t, int32_t, int32_t, uint64_t>;
 
 std::mutex g_lock;
 std::map<Key, HistTuning> g_cache;
@@ -173,11 +176,11 @@ HistConfig pick(const std::vector<HistConfig>& cands, Time&& time, std::string& 
 
 }  // namespace
 
-const HistTuning& tune_dense_hist(const dp_bin_layout& L, const uint8_t* bins,
-                                  const uint8_t* rows_major, int32_t bin_stride,
-                                  const int32_t* gpair, hipStream_t s, const uint8_t* skip) {
-  const Key key{L.n_rows, L.n_features, bin_stride, L.missing_bin, rows_major ? 1 : 0,
-                skip ? 1 : 0};
+const HistTuning& tune_dense_hist(const dp_bin_layout& L, const uint8_t* bins, bool gathered,
+                                  int32_t bin_stride, const int32_t* gpair, hipStream_t s,
+                                  const uint8_t* skip) {
+  const Key key{L.n_rows, L.n_features, bin_stride, L.missing_bin, gathered ? 1 : 0,
+                skip ? 1 : 0, L.paired_tiles};
   std::lock_guard<std::mutex> hold(g_lock);
   auto it = g_cache.find(key);
   if (it != g_cache.end()) return it->second;
@@ -190,7 +193,7 @@ const HistTuning& tune_dense_hist(const dp_bin_layout& L, const uint8_t* bins,
   t.root = pick(cands, [&](const HistConfig& c) { return time_dense(root, c, s); }, report,
                 "root");
   t.level = t.root;
-  if (rows_major && L.n_rows >= kStride) {
+  if (gathered && L.n_rows >= kStride) {
     // node k: rows k, k + kStride, k + 2 kStride, ... (k < kNodes)
     const int64_t per = L.n_rows / kStride;
     std::vector<uint32_t> ids(size_t(per) * kNodes);
@@ -199,14 +202,28 @@ const HistTuning& tune_dense_hist(const dp_bin_layout& L, const uint8_t* bins,
         ids[size_t(k) * size_t(per) + size_t(i)] = uint32_t(i * kStride + k);
     DeviceBuffer<uint32_t> ridx(ids.size());
     DP_HIP(hipMemcpyAsync(ridx.p, ids.data(), ridx.bytes(), hipMemcpyHostToDevice, s));
+    // The row-major copies: plain, and with the pairs' joint tiles in place
+    // of their first tiles (what one-tile items read with the pairs in use).
+    dp_bin_layout plain = L;
+    plain.paired_tiles = 0;
+    DeviceBuffer<uint8_t> rows_plain(size_t(L.n_rows) * size_t(L.n_tiles) * 16), rows_paired;
+    launch_tiles_to_rows(bins, plain, rows_plain.p, s);
+    if (L.paired_tiles) {
+      rows_paired.resize(rows_plain.n);
+      launch_tiles_to_rows(bins, L, rows_paired.p, s);
+    }
     // The levels' flush layout: feature-major where the booster fuses the
     // reduce and the evaluation (it costs more per item than the LDS image).
     const bool fmaj = L.n_features >= kDenseFuseFeatures && bin_stride <= 256;
-    Pass level{&L, bins, rows_major, skip, ridx.p, per, kNodes, bin_stride, gpair, out.p, fmaj};
     report += ",";
-    t.level = pick(dense_candidates(L.n_tiles, false),
-                   [&](const HistConfig& c) { return time_dense(level, c, s); }, report,
-                   "gathered");
+    t.level = pick(
+        dense_candidates(L.n_tiles, false),
+        [&](const HistConfig& c) {
+          const uint8_t* rm = hist_pairs(L.paired_tiles, c.tiles) ? rows_paired.p : rows_plain.p;
+          Pass level{&L, bins, rm, skip, ridx.p, per, kNodes, bin_stride, gpair, out.p, fmaj};
+          return time_dense(level, c, s);
+        },
+        report, "gathered");
     DP_HIP(hipStreamSynchronize(s));
   }
   t.tuned = true;
@@ -217,7 +234,8 @@ const HistTuning& tune_dense_hist(const dp_bin_layout& L, const uint8_t* bins,
 }
 
 const HistTuning* find_dense_tuning(const dp_bin_layout& L, int32_t bin_stride, bool gathered) {
-  const Key key{L.n_rows, L.n_features, bin_stride, L.missing_bin, gathered ? 1 : 0, 0};
+  const Key key{L.n_rows, L.n_features, bin_stride, L.missing_bin, gathered ? 1 : 0, 0,
+                L.paired_tiles};
   std::lock_guard<std::mutex> hold(g_lock);
   auto it = g_cache.find(key);
   return it == g_cache.end() ? nullptr : &it->second;
@@ -225,7 +243,8 @@ const HistTuning* find_dense_tuning(const dp_bin_layout& L, int32_t bin_stride, 
 
 const HistTuning& tune_sparse_hist(const SparseBins& sp, int64_t n_rows, int32_t n_features,
                                    int32_t bin_stride, const int32_t* gpair, hipStream_t s) {
-  const Key key{n_rows, n_features, bin_stride, sp.tile_features, 2, int32_t(sp.nnz % 1000003)};
+  const Key key{n_rows, n_features, bin_stride, sp.tile_features, 2, int32_t(sp.nnz % 1000003),
+                0};
   std::lock_guard<std::mutex> hold(g_lock);
   auto it = g_cache.find(key);
   if (it != g_cache.end()) return it->second;

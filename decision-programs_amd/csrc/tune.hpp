@@ -15,15 +15,17 @@ struct HistTuning {
   std::string report;  // JSON: every candidate's time and the choice
 };
 
-// Dense 16-feature tiles.  rows_major: the row-major copy the gathered passes
-// read (null: only the root pass is tuned; level = root).  gpair: any
-// [n_rows][2] pairs (the timing does not depend on their values).  Cached per
-// process by (rows, features, bins, missing, gathered); synchronises `s`.
-// skip: the matrix's skip bins per tile when the histograms leave them out.
+// Dense 16-feature tiles (bins: tile-major, with the joint tiles of the
+// layout's pairs).  gathered: also tune the gathered passes, which read a
+// row-major copy (made here for the timing: the plain copy, and the one with
+// the pairs' joint tiles for one-tile candidates); otherwise level = root.
+// gpair: any [n_rows][2] pairs (the timing does not depend on their values).
+// Cached per process by (rows, features, bins, missing, gathered, skip,
+// pairs); synchronises `s`.  skip: the matrix's skip bins per tile when the
+// histograms leave them out.
 const HistTuning& tune_dense_hist(const dp_bin_layout& layout, const uint8_t* bins,
-                                  const uint8_t* rows_major, int32_t bin_stride,
-                                  const int32_t* gpair, hipStream_t s,
-                                  const uint8_t* skip = nullptr);
+                                  bool gathered, int32_t bin_stride, const int32_t* gpair,
+                                  hipStream_t s, const uint8_t* skip = nullptr);
 // The cached dense tuning of a shape, or null when it has not been tuned.
 const HistTuning* find_dense_tuning(const dp_bin_layout& layout, int32_t bin_stride,
                                     bool gathered);

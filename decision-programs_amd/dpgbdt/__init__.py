@@ -35,7 +35,7 @@ class DPError(RuntimeError):
 
 class BinLayout(Structure):
     _fields_ = [("n_rows", c_int64), ("n_features", c_int32), ("tile_width", c_int32),
-                ("n_tiles", c_int32), ("missing_bin", c_int32)]
+                ("n_tiles", c_int32), ("missing_bin", c_int32), ("paired_tiles", c_uint64)]
 
 
 class TrainParam(Structure):
@@ -119,6 +119,8 @@ def load():
         "dp_workspace_free": (c_int, [H]),
         "dp_layout_init": (c_int, [c_int64, c_int32, c_int32, c_int32, POINTER(BinLayout)]),
         "dp_layout_bytes": (c_size_t, [POINTER(BinLayout)]),
+        "dp_layout_pair_tiles": (c_int, [POINTER(BinLayout), c_void_p]),
+        "dp_join_tiles": (c_int, [c_void_p, POINTER(BinLayout), c_void_p]),
         "dp_sketch_cuts": (c_int, [H, c_void_p, c_int64, c_int32, c_int32, c_void_p, c_void_p,
                                    c_void_p, POINTER(c_int32), c_void_p]),
         "dp_bin_values": (c_int, [c_void_p, POINTER(BinLayout), c_void_p, c_void_p, c_void_p,

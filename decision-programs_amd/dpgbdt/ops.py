@@ -49,6 +49,20 @@ def layout(n_rows, n_features, tile_width=0, missing_bin=-1):
     return out
 
 
+def layout_pair_tiles(lay, cut_ptr):
+    """Pairs the layout's tiles whose features all have at most 16 bins (host cut_ptr, as
+    sketch_cuts returns it); returns the layout (changed in place)."""
+    ptr = np.ascontiguousarray(cut_ptr, dtype=np.int32)
+    check(load().dp_layout_pair_tiles(ctypes.byref(lay), ptr.ctypes.data))
+    return lay
+
+
+def join_tiles(bins, lay):
+    """Writes the joint tiles of a paired layout into device bins (after its n_tiles tiles)."""
+    check(load().dp_join_tiles(_ptr(bins), ctypes.byref(lay), _stream()))
+    return bins
+
+
 def layout_bytes(lay):
     return load().dp_layout_bytes(ctypes.byref(lay))
 

@@ -25,7 +25,8 @@
  *   values     float32 row-major [n_rows][n_features]; NaN = missing
  *   bins       uint8 tile-major: element (r, f) at
  *              bins[(f / tile_width) * n_rows * tile_width + r * tile_width
- *                   + f % tile_width]; `missing_bin` (-1 = none) marks NaN
+ *                   + f % tile_width]; `missing_bin` (-1 = none) marks NaN;
+ *              a paired layout's joint tiles follow (dp_bin_layout)
  *   gpair      int32 [n_rows][2] = (qg, qh), gradients in fixed point:
  *              q = rint(x * 2^exp), |q| <= 2^30 (see dp_quantise_gradients)
  *   hist       int64 [node][n_features][bin_stride][2] = (sum qg, sum qh)
@@ -214,12 +215,36 @@ typedef struct {
   int32_t tile_width;   /* features per tile: 16 */
   int32_t n_tiles;
   int32_t missing_bin;  /* -1 when the matrix holds no NaN, else 255 */
+  /* Bit t set: tiles t and t + 1 (t < 63) hold only bins below 16 and are
+   * histogrammed together from their joint tile; no two set bits adjacent.
+   * The k-th pair's joint tile is tile n_tiles + k of the bins buffer: per row
+   * and feature slot i the byte (tile t's bin << 4) | tile t + 1's bin.
+   * 0 from dp_layout_init; set by dp_layout_pair_tiles.  Histograms are the
+   * same either way. */
+  uint64_t paired_tiles;
 } dp_bin_layout;
 
 /* Fills `out`; tile_width 0 selects the default (16). */
 int dp_layout_init(int64_t n_rows, int32_t n_features, int32_t tile_width, int32_t missing_bin,
                    dp_bin_layout* out);
+/* Bytes of the bins buffer: n_tiles tiles of n_rows * 16 bytes (tile-major:
+ * tile t holds 16 bytes per row), plus one joint tile per pair. */
 size_t dp_layout_bytes(const dp_bin_layout* layout);
+
+/* Sets layout->paired_tiles from the cuts (host cut_ptr [n_features + 1], as
+ * dp_sketch_cuts returns): tiles are paired left to right, t with t + 1, when
+ * every feature of both has at most 16 bins (pad features count as such); a
+ * matrix with missing values gets none.  Call it before sizing the bins buffer
+ * (dp_layout_bytes counts the joint tiles); dp_bin_values then writes the
+ * joint tiles too.  The bins must come from these cuts (every byte of a paired
+ * tile below 16; a larger byte gives wrong sums, never an access out of
+ * bounds).  No counterpart in the reference: a layout choice of this library
+ * (two tiles' histograms for the LDS atomics of one). */
+int dp_layout_pair_tiles(dp_bin_layout* layout, const int32_t* cut_ptr);
+
+/* Writes the joint tiles of layout->paired_tiles from the tiles they pair,
+ * for bins made without dp_bin_values.  No counterpart in the reference. */
+int dp_join_tiles(uint8_t* bins, const dp_bin_layout* layout, void* stream);
 
 /* Exact quantile cuts of every feature (the definition is stated in the
  * implementation).  Host outputs: cut_ptr [n_features + 1], cut_values
@@ -229,7 +254,8 @@ int dp_sketch_cuts(dp_workspace ws, const float* values, int64_t n_rows, int32_t
                    int32_t max_bin, int32_t* cut_ptr, float* cut_values, float* min_values,
                    int32_t* has_missing, void* stream);
 
-/* bins[r][f] = index of the first cut > x (clamped), missing_bin for NaN.
+/* bins[r][f] = index of the first cut > x (clamped), missing_bin for NaN, in
+ * the tile-major layout (and the joint tiles of a paired layout).
  * cut_ptr and cut_values are device arrays.  With missing_bin 255 every
  * feature must have at most 255 bins (byte 255 is the missing marker). */
 int dp_bin_values(const float* values, const dp_bin_layout* layout, const int32_t* cut_ptr,

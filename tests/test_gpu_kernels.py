@@ -171,9 +171,9 @@ def test_c3_root_histogram_full_size(dp, oracle, ws, device):
     """The benchmark's C3 root pass at its size (10,000,000 x 128, 256 bins): the
     device bins (whose cuts and binning the tests above pin against the oracle
     at smaller sizes) are read back and histogrammed by the oracle's parallel
-    histogram; the GPU histogram must equal it bit for bit, and every feature's
-    sums must equal the sums of the quantised gradients (no row lost or counted
-    twice)."""
+    histogram; the GPU histogram, with and without paired tiles, must equal it
+    bit for bit, and every feature's sums must equal the sums of the quantised
+    gradients (no row lost or counted twice)."""
     from dpgbdt import ops
 
     n, f = 10_000_000, 128
@@ -182,7 +182,11 @@ def test_c3_root_histogram_full_size(dp, oracle, ws, device):
     cut_ptr, cuts, _, missing = ops.sketch_cuts(ws, values, 256)
     assert not missing
     lay = ops.layout(n, f, 0, -1)
-    bins = ops.bin_values(values, lay, cut_ptr, cuts)
+    # features 96-127 take 16 values: tiles 6 and 7 pair, as in the benchmark's pass
+    # (the bins buffer: the 8 tiles, then the pair's joint tile)
+    paired = ops.layout_pair_tiles(ops.layout(n, f, 0, -1), cut_ptr)
+    assert paired.paired_tiles == 1 << 6
+    bins = ops.bin_values(values, paired, cut_ptr, cuts)
     del values
     stride = int(np.diff(cut_ptr).max())
     (eg, eh), gpair, sums = _gpair(ws, device, g.cpu().numpy(), h.cpu().numpy())
@@ -190,10 +194,12 @@ def test_c3_root_histogram_full_size(dp, oracle, ws, device):
     qgqh = gpair.cpu().numpy()
     np.testing.assert_array_equal(hist[:, :, 0].sum(axis=1), np.full(f, sums[0]))
     np.testing.assert_array_equal(hist[:, :, 1].sum(axis=1), np.full(f, sums[1]))
-    host_bins = ops.from_tiles(bins.cpu().numpy(), lay)
+    hist_paired = ops.hist_build(ws, bins, paired, gpair, [(0, n)], stride).cpu().numpy()[0]
+    host_bins = ops.from_tiles(bins[: ops.layout_bytes(lay)].cpu().numpy(), lay)
     del bins
     ref = oracle.hist_parallel(host_bins, qgqh[:, 0], qgqh[:, 1], bin_stride=stride)
     np.testing.assert_array_equal(hist, ref)
+    np.testing.assert_array_equal(hist_paired, ref)
     # every feature's g and h sums as floats, within 1e-5 relative of float64 sums
     live = _check_float_sums(oracle, hist, host_bins, g.cpu().numpy(), h.cpu().numpy(), eg, eh,
                              -1, range(f))

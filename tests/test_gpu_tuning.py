@@ -28,18 +28,23 @@ def _train(dp, values, labels, params, rounds, n, k):
     return bst.save_raw(), bst.last_positions(n), bst.margins(n, k), bst
 
 
-@pytest.mark.parametrize("case", ["c2_two_tiles", "c4_odd_tiles", "missing", "present_value"])
+@pytest.mark.parametrize("case", ["c2_two_tiles", "c3_paired_tiles", "c4_odd_tiles", "missing",
+                                  "present_value"])
 def test_every_launch_shape_trains_the_same_model(dp, device, case):
     """Trees, partitions and margins are identical under all 36 forced launch shapes
     (two tiles per item over an odd tile count leaves a one-tile last group, with and without
-    the lanes' swapped tile order; one or three blocks of rows in flight; the MISSING
-    kernels; present-value histograms take the work-item count only)."""
+    the lanes' swapped tile order; one or three blocks of rows in flight; C3's tiles 6 and 7
+    paired by the one-tile shapes; the MISSING kernels; present-value histograms take the
+    work-item count only)."""
     import torch
     from dpgbdt import ops
 
     if case == "c2_two_tiles":
         values, labels, _, _ = ops.synth(2, 60000, 3, n_features=28)
         params, k = {"objective": "binary:logistic", "max_depth": 7, "eta": 0.3}, 1
+    elif case == "c3_paired_tiles":
+        values, labels, _, _ = ops.synth(3, 40000, 6, n_features=128)
+        params, k = {"objective": "binary:logistic", "max_depth": 6, "eta": 0.3}, 1
     elif case == "c4_odd_tiles":
         values, labels, _, _ = ops.synth(4, 3000, 4, n_features=784)
         params, k = {"objective": "multi:softprob", "num_class": 10, "max_depth": 4,

@@ -150,3 +150,35 @@ def test_quantum_ratio_closed_forms():
     r = bench.quantum_ratio(np.concatenate([g, outlier], axis=1),
                             np.concatenate([h, h], axis=1), [[30, 31], [28, 31]])
     assert r == {"g": [19, 21], "h": 18}
+
+
+def test_layout_pair_tiles(dp):
+    """dp_layout_pair_tiles: adjacent 16-feature tiles are paired left to right when every
+    feature of both has at most 16 bins (pad features count as such); a 17-bin feature breaks
+    a pair, a matrix with missing values gets none, and bit 62 is the last pair's."""
+    import numpy as np
+    from dpgbdt import ops
+
+    def pairs(n_bins, missing_bin=-1):
+        lay = ops.layout(100, len(n_bins), 0, missing_bin)
+        ptr = np.concatenate([[0], np.cumsum(n_bins)]).astype(np.int32)
+        return ops.layout_pair_tiles(lay, ptr).paired_tiles
+
+    nb = np.full(90, 16)  # six tiles, the last with 10 features and 6 pad features
+    nb[50] = 17           # tile 3 is wide
+    assert pairs(nb) == (1 << 0) | (1 << 4)  # (0, 1), then 2 alone, 3 wide, (4, 5)
+    nb[50] = 16
+    assert pairs(nb) == (1 << 0) | (1 << 2) | (1 << 4)
+    nb[5] = 256           # tile 0 wide: (1, 2), (3, 4), 5 alone
+    assert pairs(nb) == (1 << 1) | (1 << 3)
+    assert pairs(np.full(90, 2), missing_bin=255) == 0
+    assert pairs(np.full(16, 3)) == 0  # one tile: nothing to pair with
+    assert pairs(np.full(70 * 16, 8)) == int("01" * 32, 2)  # tiles 0..63 in 32 pairs
+    assert ctypes.sizeof(dp.BinLayout) == 32
+    lay = ops.layout(100, 90, 0, -1)
+    assert ops.layout_bytes(lay) == 6 * 100 * 16
+    ops.layout_pair_tiles(lay, np.concatenate([[0], np.cumsum(np.full(90, 16))]))
+    assert ops.layout_bytes(lay) == (6 + 3) * 100 * 16  # three joint tiles follow
+    lay = ops.layout(100, 40, 0, -1)
+    with pytest.raises(dp.DPError, match="cut_ptr must not decrease"):
+        ops.layout_pair_tiles(lay, np.array([0, 5, 3] + [3] * 38, dtype=np.int32))
