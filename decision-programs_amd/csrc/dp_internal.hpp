@@ -293,14 +293,17 @@ struct HistConfig {
 };
 
 // Paired tiles (dp_bin_layout::paired_tiles): bit t joins tiles t and t + 1
-// into one work item whose rows add one joint byte per feature pair.  Only
-// one-tile items pair; hist_pairs gives the pairs a configuration uses.
+// into one work item whose rows add one joint byte per feature pair.
+// hist_pairs gives the pairs a configuration uses: with one tile per item
+// every pair (the pair's item replaces two), with two every pair that is an
+// item's two tiles (t even).
 __host__ __device__ inline uint64_t hist_pairs(uint64_t paired_tiles, int32_t tiles) {
-  return tiles == 1 ? paired_tiles : 0;
+  return tiles == 1 ? paired_tiles : paired_tiles & 0x5555555555555555ull;
 }
-// Work items per row chunk: tile groups of `tiles` tiles, less one per pair.
+// Work items per row chunk: tile groups of `tiles` tiles (one tile: less one
+// per pair).
 __host__ __device__ inline int32_t hist_groups(int32_t n_tiles, int32_t tiles, uint64_t pairs) {
-  return (n_tiles + tiles - 1) / tiles - __builtin_popcountll(pairs);
+  return tiles == 1 ? n_tiles - __builtin_popcountll(pairs) : (n_tiles + tiles - 1) / tiles;
 }
 // Tile t is the second of a pair (its rows go with tile t - 1's item).
 __host__ __device__ inline bool pair_second(uint64_t pairs, int32_t t) {

@@ -133,7 +133,8 @@ constexpr int kHistThreads = 1024;
 // bins', which the split evaluation restores).  On data dominated by one value
 // per feature (C4's zero pixels) this removes most atomics and their
 // same-address conflicts.  MODE 1 is the missing-byte skip above; MODE 0 none.
-// PAIR (one-tile items without missing values or skip bins): the item covers
+// PAIR (items without missing values or skip bins; one tile per item, or two
+// whose tiles are the pair): the item covers
 // tiles t and t + 1 of dp_bin_layout::paired_tiles, whose bins are all below
 // 16, and reads their joint tile (per row and feature slot i the byte tile
 // t's bin << 4 | tile t + 1's bin: stored after the matrix's tiles, and in
@@ -162,13 +163,14 @@ template <bool GATHER, int MODE, int TPW, int U, int SPLIT, bool DEEP, bool PAIR
 __device__ __forceinline__ void hist_item(const HistPass& a, const HistWork& w, int32_t src_tile,
                                           unsigned long long* lds, const uint32_t (&slotw)[4],
                                           uint32_t rot) {
-  static_assert(!PAIR || (TPW == 1 && MODE == 0), "pairs take one-tile items without skips");
+  static_assert(!PAIR || MODE == 0, "pairs take items without skips");
   constexpr int64_t kStep = int64_t(kHistThreads) * U;
   constexpr int PD = DEEP ? 3 : (GATHER ? 1 : 0);  // prefetch depth (blocks)
   constexpr int R = PD + 1;                         // ring buffers
+  constexpr int TW = PAIR ? 1 : TPW;                // tiles read per row (a pair: its joint tile)
   lds_u8* const lds_base = (lds_u8*)lds;
   // tiles of this item that exist (uniform per workgroup); a pair fills one LDS tile
-  const int nt = TPW == 1 ? 1 : (w.tile + TPW <= a.n_tiles ? TPW : a.n_tiles - w.tile);
+  const int nt = TW == 1 ? 1 : (w.tile + TPW <= a.n_tiles ? TPW : a.n_tiles - w.tile);
   // This lane's tile order: swapped when SPLIT applies and both tiles exist.
   const int swap = (SPLIT > 0 && nt == 2) ? int((threadIdx.x >> SPLIT) & 1u) : 0;
   // MODE 2: each tile's skip bins, rotated like the row bytes (byte k of the
@@ -190,7 +192,7 @@ __device__ __forceinline__ void hist_item(const HistPass& a, const HistWork& w, 
   const int64_t last = w.end - 1;
   const int64_t lane = threadIdx.x;
   uint32_t rows[R][U];  // GATHER: row ids
-  uint4 v[R][U][TPW];
+  uint4 v[R][U][TW];
   int2 q[R][U];
   auto fetch_rows = [&](int b, int64_t base) {
 #pragma unroll
@@ -206,7 +208,7 @@ __device__ __forceinline__ void hist_item(const HistPass& a, const HistWork& w, 
       const uint32_t r = GATHER ? rows[b][u] : uint32_t(i < w.end ? i : last);
       const uint8_t* src = tile + int64_t(r) * a.row_step;
 #pragma unroll
-      for (int j = 0; j < TPW; ++j)  // a missing second tile re-reads the first
+      for (int j = 0; j < TW; ++j)  // a missing second tile re-reads the first
         v[b][u][j] = *reinterpret_cast<const uint4*>(src + (j < nt ? j ^ swap : 0) * a.tile_step);
       q[b][u] = a.gpair[r];
     }
@@ -218,7 +220,7 @@ __device__ __forceinline__ void hist_item(const HistPass& a, const HistWork& w, 
       const unsigned long long g = ok ? (unsigned long long)(long long)q[b][u].x : 0ull;
       const unsigned long long h = ok ? (unsigned long long)(long long)q[b][u].y : 0ull;
 #pragma unroll
-      for (int j = 0; j < TPW; ++j) {
+      for (int j = 0; j < TW; ++j) {
         if (j >= nt) break;  // uniform per workgroup
         uint32_t x[4] = {v[b][u][j].x, v[b][u][j].y, v[b][u][j].z, v[b][u][j].w};
         rotate16(x, rot);
@@ -353,7 +355,8 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(DE
     const HistWork* __restrict__ work, int32_t n_work_host,
     const int32_t* __restrict__ n_work_dev, int32_t bin_stride,
     unsigned long long* __restrict__ hist, unsigned long long* __restrict__ partial,
-    int64_t tile_step, int64_t row_step, int32_t fmaj, uint64_t pairs, int32_t joint_first) {
+    int64_t tile_step, int64_t row_step, int32_t fmaj, uint64_t pairs, uint64_t joint_pairs,
+    int32_t joint_first) {
   extern __shared__ unsigned long long lds[];  // TPW * kLdsWords
   // The first item is loaded alongside the device count (the host bound keeps
   // it in range), so the two loads overlap instead of chaining.
@@ -375,9 +378,9 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(DE
   for (int32_t item = blockIdx.x; item < n_work; item += gridDim.x) {
     const HistWork w = item == int32_t(blockIdx.x) ? w_first : work[item];
     if (w.begin >= w.end) continue;  // padding item (uniform per workgroup)
-    if constexpr (TPW == 1 && MODE == 0) {
-      if (pair_second(pairs, w.tile + 1)) {  // w.tile is the first of pair k
-        const int32_t k = __builtin_popcountll(pairs & ((1ull << w.tile) - 1ull));
+    if constexpr (MODE == 0) {
+      if (w.tile < 63 && ((pairs >> w.tile) & 1ull)) {  // the item's tiles are pair k
+        const int32_t k = __builtin_popcountll(joint_pairs & ((1ull << w.tile) - 1ull));
         const int32_t jt = joint_first < 0 ? w.tile : joint_first + k;  // its joint tile
         hist_item<GATHER, MODE, TPW, U, SPLIT, DEEP, true>(a, w, jt, lds, slotw, rot);
         continue;
@@ -1040,8 +1043,9 @@ void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t
   const uint8_t* src = rows ? row_major : bins;
   const int64_t tile_step = rows ? kTile : layout.n_rows * kTile;
   const int64_t row_step = rows ? int64_t(layout.n_tiles) * kTile : kTile;
-  // A pair's joint tile: tile n_tiles + k of the tile-major bins, or in place
-  // of the pair's first tile in the row-major copy (joint_first -1).
+  // A pair's joint tile: tile n_tiles + k of the tile-major bins for the
+  // layout's k-th pair, or in place of the pair's first tile in the row-major
+  // copy (joint_first -1).
   const int32_t joint_first = rows ? -1 : layout.n_tiles;
   const bool missing = layout.missing_bin >= 0;
   need(!(missing && skip), "skip bins apply to matrices without missing values");
@@ -1059,7 +1063,7 @@ void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(kHistThreads), lds, s, src, skip, layout.n_rows,
                      layout.n_features, layout.n_tiles, gp, ridx, work, n_work, n_work_dev,
                      bin_stride, out, part, tile_step, row_step, fmaj ? 1 : 0, pairs,
-                     joint_first);
+                     layout.paired_tiles, joint_first);
   DP_HIP(hipGetLastError());
 }
 

@@ -16,8 +16,8 @@
 //   work items per pass   512, 1024 or 2048 (fewer, longer row chunks write
 //                         fewer partial tiles; more balance the CUs better).
 // A layout with paired tiles (tiles whose features all have at most 16 bins)
-// is tuned as such: one-tile candidates pair them, two-tile candidates do not,
-// and the timings decide between them.
+// is tuned as such: one-tile candidates use every pair, two-tile candidates
+// the pairs that are one item's two tiles.
 // The contiguous (root) pass is timed over the whole matrix; the gathered pass
 // through the row-major copy, as the levels below the root read it, over 12
 // nodes whose rows are strided over the matrix (node k: rows k, k + 32, ...),
@@ -202,16 +202,21 @@ const HistTuning& tune_dense_hist(const dp_bin_layout& L, const uint8_t* bins, b
         ids[size_t(k) * size_t(per) + size_t(i)] = uint32_t(i * kStride + k);
     DeviceBuffer<uint32_t> ridx(ids.size());
     DP_HIP(hipMemcpyAsync(ridx.p, ids.data(), ridx.bytes(), hipMemcpyHostToDevice, s));
-    // The row-major copies: plain, and with the pairs' joint tiles in place
-    // of their first tiles (what one-tile items read with the pairs in use).
-    dp_bin_layout plain = L;
-    plain.paired_tiles = 0;
-    DeviceBuffer<uint8_t> rows_plain(size_t(L.n_rows) * size_t(L.n_tiles) * 16), rows_paired;
-    launch_tiles_to_rows(bins, plain, rows_plain.p, s);
-    if (L.paired_tiles) {
-      rows_paired.resize(rows_plain.n);
-      launch_tiles_to_rows(bins, L, rows_paired.p, s);
-    }
+    // The row-major copy a candidate reads: the pairs it uses (hist_pairs)
+    // hold their joint tiles in place of their first tiles; one copy per set.
+    std::map<uint64_t, DeviceBuffer<uint8_t>> copies;
+    auto rows_for = [&](const HistConfig& c) -> const uint8_t* {
+      const uint64_t used = hist_pairs(L.paired_tiles, c.tiles);
+      auto it = copies.find(used);
+      if (it == copies.end()) {
+        dp_bin_layout rl = L;
+        rl.paired_tiles = used;
+        it = copies.emplace(used, DeviceBuffer<uint8_t>(size_t(L.n_rows) * size_t(L.n_tiles) * 16))
+                 .first;
+        launch_tiles_to_rows(bins, rl, it->second.p, s);
+      }
+      return it->second.p;
+    };
     // The levels' flush layout: feature-major where the booster fuses the
     // reduce and the evaluation (it costs more per item than the LDS image).
     const bool fmaj = L.n_features >= kDenseFuseFeatures && bin_stride <= 256;
@@ -219,8 +224,8 @@ const HistTuning& tune_dense_hist(const dp_bin_layout& L, const uint8_t* bins, b
     t.level = pick(
         dense_candidates(L.n_tiles, false),
         [&](const HistConfig& c) {
-          const uint8_t* rm = hist_pairs(L.paired_tiles, c.tiles) ? rows_paired.p : rows_plain.p;
-          Pass level{&L, bins, rm, skip, ridx.p, per, kNodes, bin_stride, gpair, out.p, fmaj};
+          Pass level{&L,  bins,   rows_for(c), skip, ridx.p, per, kNodes, bin_stride,
+                     gpair, out.p, fmaj};
           return time_dense(level, c, s);
         },
         report, "gathered");

@@ -28,13 +28,14 @@ def _train(dp, values, labels, params, rounds, n, k):
     return bst.save_raw(), bst.last_positions(n), bst.margins(n, k), bst
 
 
-@pytest.mark.parametrize("case", ["c2_two_tiles", "c3_paired_tiles", "c4_odd_tiles", "missing",
-                                  "present_value"])
+@pytest.mark.parametrize("case", ["c2_two_tiles", "c3_paired_tiles", "odd_pair", "c4_odd_tiles",
+                                  "missing", "present_value"])
 def test_every_launch_shape_trains_the_same_model(dp, device, case):
     """Trees, partitions and margins are identical under all 36 forced launch shapes
     (two tiles per item over an odd tile count leaves a one-tile last group, with and without
     the lanes' swapped tile order; one or three blocks of rows in flight; C3's tiles 6 and 7
-    paired by the one-tile shapes; the MISSING kernels; present-value histograms take the
+    paired, a pair item for one-tile and for two-tile shapes; tiles 1 and 2 paired, which
+    only one-tile shapes use; the MISSING kernels; present-value histograms take the
     work-item count only)."""
     import torch
     from dpgbdt import ops
@@ -44,6 +45,15 @@ def test_every_launch_shape_trains_the_same_model(dp, device, case):
         params, k = {"objective": "binary:logistic", "max_depth": 7, "eta": 0.3}, 1
     elif case == "c3_paired_tiles":
         values, labels, _, _ = ops.synth(3, 40000, 6, n_features=128)
+        params, k = {"objective": "binary:logistic", "max_depth": 6, "eta": 0.3}, 1
+    elif case == "odd_pair":  # tile 0: 256 bins; tiles 1 and 2: 16 values each
+        g = torch.Generator(device="cpu").manual_seed(7)
+        n = 30000
+        wide = torch.randn((n, 16), generator=g)
+        narrow = torch.randint(0, 16, (n, 32), generator=g).to(torch.float32)
+        values = torch.cat([wide, narrow], dim=1).contiguous().to(device)
+        score = values[:, 0] + 0.25 * values[:, 20] - 0.2 * values[:, 33]
+        labels = (torch.sigmoid(score) > torch.rand(n, generator=g).to(device)).to(torch.float32)
         params, k = {"objective": "binary:logistic", "max_depth": 6, "eta": 0.3}, 1
     elif case == "c4_odd_tiles":
         values, labels, _, _ = ops.synth(4, 3000, 4, n_features=784)
@@ -62,6 +72,10 @@ def test_every_launch_shape_trains_the_same_model(dp, device, case):
     n = values.shape[0]
     base = _train(dp, values, labels, dict(params, dp_autotune=0), 3, n, k)
     assert base[3].tuning()["defaults"] is True
+    want = {"c3_paired_tiles": 1 << 6, "odd_pair": 1 << 1}.get(case, 0)
+    assert base[3].tuning()["paired_tiles"] == want
+    unpaired = _train(dp, values, labels, dict(params, dp_autotune=0, dp_hist_pair=0), 3, n, k)
+    assert unpaired[0] == base[0]
     for shape in SHAPES:
         if case == "present_value" and (shape["dp_hist_tiles"] == 2 or shape["dp_hist_deep"]):
             continue  # one present-value tile per item: only the item count applies
