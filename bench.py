@@ -117,19 +117,22 @@ def hist_leg(args, torch, dp, ops):
     launch_ms = [ev[k].elapsed_time(ev[k + 1]) for k in range(args.steps)]
     avg_ms = sum(launch_ms) / len(launch_ms)
     # the same pass without paired tiles (tuned on first use), for comparison
-    unpaired = torch.zeros_like(hist)
-    ops.hist_accumulate(ws, bins, plain, gp, [(0, n)], unpaired)
-    torch.cuda.synchronize()
-    ev_u = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
-    ev_u[0].record(stream)
-    for k in range(args.steps):
+    ku = args.steps if args.unpaired_steps is None else args.unpaired_steps
+    unpaired_ms = None
+    if ku > 0:
+        unpaired = torch.zeros_like(hist)
         ops.hist_accumulate(ws, bins, plain, gp, [(0, n)], unpaired)
-        ev_u[k + 1].record(stream)
-    torch.cuda.synchronize()
-    unpaired_ms = sum(ev_u[k].elapsed_time(ev_u[k + 1]) for k in range(args.steps)) / args.steps
-    assert bool((unpaired[0] * (args.warmup + args.steps) == hist[0] * (args.steps + 1)).all()), \
-        "paired and unpaired histograms differ"
-    del unpaired
+        torch.cuda.synchronize()
+        ev_u = [torch.cuda.Event(enable_timing=True) for _ in range(ku + 1)]
+        ev_u[0].record(stream)
+        for k in range(ku):
+            ops.hist_accumulate(ws, bins, plain, gp, [(0, n)], unpaired)
+            ev_u[k + 1].record(stream)
+        torch.cuda.synchronize()
+        unpaired_ms = sum(ev_u[k].elapsed_time(ev_u[k + 1]) for k in range(ku)) / ku
+        assert bool((unpaired[0] * (args.warmup + args.steps) == hist[0] * (ku + 1)).all()), \
+            "paired and unpaired histograms differ"
+        del unpaired
     # size-independent check: every feature's bins sum to the root totals
     h0 = hist[0].sum(dim=1)  # [F, 2]
     reps = args.warmup + args.steps
@@ -147,7 +150,8 @@ def hist_leg(args, torch, dp, ops):
         "paired_tiles": int(lay.paired_tiles),
         "issued_elements": n * (f - 16 * bin(int(lay.paired_tiles)).count("1")),
         "unpaired_avg_ms": unpaired_ms,
-        "unpaired_launch_shape": ops.hist_tuning(plain, stride).get("chosen", {}).get("root"),
+        "unpaired_launch_shape": (ops.hist_tuning(plain, stride).get("chosen", {}).get("root")
+                                  if unpaired_ms is not None else None),
     }
     sample = None
     if not args.skip_cpu:
@@ -482,6 +486,9 @@ def main():
     ap.add_argument("--configs", default="C1,C2,C3,C4,C5",
                     help="tree configurations timed in full/trees mode")
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--unpaired-steps", type=int, default=None,
+                    help="timed launches of the unpaired comparison pass (default: --steps; "
+                         "0 skips it, e.g. so that a profile's last launches are the paired ones)")
     ap.add_argument("--cpu-rows", type=int, default=1_000_000)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     args = ap.parse_args()
