@@ -565,9 +565,20 @@ size_t dp_layout_bytes(const dp_bin_layout* layout) {
   return tiles * size_t(layout->n_rows) * size_t(layout->tile_width);
 }
 
+// A paired layout's buffer holds joint tiles after the matrix's tiles; a
+// buffer sized before the layout was paired would be read past its end.
+static void require_paired_bins(const uint8_t* bins, const dp_bin_layout& layout) {
+  if (!layout.paired_tiles) return;
+  dp::check_pairs(layout);
+  require_device_array(reinterpret_cast<uintptr_t>(bins), dp_layout_bytes(&layout),
+                       "bins of a paired layout (dp_layout_bytes counts its joint tiles; "
+                       "pair the layout before sizing the buffer)");
+}
+
 int dp_join_tiles(uint8_t* bins, const dp_bin_layout* layout, void* stream) {
   return guarded([&] {
     dp::need(bins && layout, "null argument");
+    require_paired_bins(bins, *layout);
     dp::launch_join_tiles(bins, *layout, as_stream(stream));
   });
 }
@@ -586,6 +597,7 @@ int dp_bin_values(const float* values, const dp_bin_layout* layout, const int32_
                   const float* cut_values, uint8_t* bins, void* stream) {
   return guarded([&] {
     dp::need(values && layout && cut_ptr && cut_values && bins, "null argument");
+    require_paired_bins(bins, *layout);
     dp::launch_bin_values(values, *layout, cut_ptr, cut_values, bins, as_stream(stream));
     dp::launch_join_tiles(bins, *layout, as_stream(stream));
   });
@@ -627,6 +639,7 @@ void hist_call(dp_workspace ws, const uint8_t* bins, const dp_bin_layout* layout
                const int64_t* end, int32_t n_nodes, int32_t bin_stride, int64_t* hist,
                void* stream, bool accumulate) {
   dp::need(ws && bins && layout && gpair && begin && end && hist, "null argument");
+  require_paired_bins(bins, *layout);
   dp::need(n_nodes >= 0, "negative node count");
   dp::need(bin_stride >= 1 && bin_stride <= dp::kMaxBins, "bin_stride must be in [1, 256]");
   int64_t total = 0;

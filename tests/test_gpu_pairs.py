@@ -114,6 +114,40 @@ def test_paired_tiles_refused_with_missing_values(dp, ws, device):
         ops.hist_build(ws, bins, lay, gp, [(0, n)], 16)
 
 
+def test_paired_layout_refuses_a_buffer_sized_before_pairing(dp, ws, device):
+    """dp_layout_bytes counts a paired layout's joint tiles; a bins buffer sized for the
+    unpaired layout (a dedicated 32 MiB allocation, 16 MiB short of the paired size) is
+    refused before any launch by the histogram, binning and joining calls."""
+    import ctypes
+
+    import torch
+    from dpgbdt import ops
+
+    n, f = 1 << 20, 32
+    plain = ops.layout(n, f, 0, -1)
+    paired = ops.layout_pair_tiles(ops.layout(n, f, 0, -1), np.arange(0, 16 * f + 1, 16))
+    assert paired.paired_tiles == 1
+    assert ops.layout_bytes(paired) == ops.layout_bytes(plain) + n * 16
+    rt = ctypes.CDLL("libamdhip64.so.7")
+    rt.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+    rt.hipFree.argtypes = [ctypes.c_void_p]
+    buf = ctypes.c_void_p()
+    assert rt.hipMalloc(ctypes.byref(buf), ops.layout_bytes(plain)) == 0
+    try:
+        lib = dp.load()
+        gp = torch.zeros((n, 2), dtype=torch.int32, device=device)
+        hist = torch.zeros((1, f, 16, 2), dtype=torch.int64, device=device)
+        begin, end = np.array([0], dtype=np.int64), np.array([n], dtype=np.int64)
+        rc = lib.dp_hist_build(ws.handle, buf, ctypes.byref(paired), gp.data_ptr(), None,
+                               begin.ctypes.data, end.ctypes.data, 1, 16, hist.data_ptr(), None)
+        assert rc == -1 and "pair the layout before sizing" in lib.XGBGetLastError().decode()
+        rc = lib.dp_join_tiles(buf, ctypes.byref(paired), None)
+        assert rc == -1 and "pair the layout before sizing" in lib.XGBGetLastError().decode()
+        torch.cuda.synchronize()
+    finally:
+        rt.hipFree(buf)
+
+
 def _train(dp, values, labels, pair, rounds, extra=None):
     dtrain = dp.DMatrix(values, labels)
     params = {"objective": "binary:logistic", "max_depth": 8, "eta": 0.1, "max_bin": 256,
