@@ -177,3 +177,28 @@ def test_trees_identical_with_and_without_pairs(dp, device, extra):
     a = json.loads(with_pairs.save_raw())
     b = json.loads(without.save_raw())
     assert a["learner"]["gradient_booster"] == b["learner"]["gradient_booster"]
+
+
+def test_multiclass_sampled_trees_identical_with_and_without_pairs(dp, device):
+    """Softprob over 3 classes (three trees per round on concurrent streams, each with its
+    own grower and the shared row-major copy) with row and column sampling, on 50,000 rows:
+    tiles 0 and 1 take 16 values and pair, tile 2 has 256 bins.  The saved models with and
+    without pairs are identical."""
+    import torch
+
+    g = torch.Generator(device="cpu").manual_seed(11)
+    n = 50000
+    narrow = torch.randint(0, 16, (n, 32), generator=g).to(torch.float32)
+    wide = torch.randn((n, 16), generator=g)
+    values = torch.cat([narrow, wide], dim=1).contiguous().to(device)
+    score = torch.stack([values[:, 3] - 7.5, values[:, 20] - 7.5, 4 * values[:, 40]], dim=1)
+    labels = (score + torch.randn((n, 3), generator=g).to(device)).argmax(dim=1)
+    labels = labels.to(torch.float32).contiguous()
+    extra = {"objective": "multi:softprob", "num_class": 3, "max_depth": 6, "subsample": 0.8,
+             "colsample_bynode": 0.5, "seed": 5}
+    with_pairs = _train(dp, values, labels, 1, 3, extra)
+    assert with_pairs.tuning()["paired_tiles"] == 1
+    without = _train(dp, values, labels, 0, 3, extra)
+    a = json.loads(with_pairs.save_raw())
+    b = json.loads(without.save_raw())
+    assert a["learner"]["gradient_booster"] == b["learner"]["gradient_booster"]

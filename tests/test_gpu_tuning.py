@@ -90,8 +90,9 @@ def test_every_launch_shape_trains_the_same_model(dp, device, case):
 
 def test_autotuner_report_and_choice(dp, device):
     """The autotuned booster reports every timed candidate of the root and gathered passes
-    and chooses, of the candidates within 3 % of the fastest, the one with the fewest work
-    items (then one row per step, then the fastest); its model equals the default shape's."""
+    and chooses, of the candidates within 3 % of the fastest (5 % for the gathered passes),
+    the one with the fewest work items (then one row per step, then the fastest); its model
+    equals the default shape's."""
     from dpgbdt import ops
 
     values, labels, _, _ = ops.synth(2, 200000, 8, n_features=28)
@@ -105,7 +106,8 @@ def test_autotuner_report_and_choice(dp, device):
         assert len(cands) == (36 if name == "root" else 24)
         assert all(c["ms"] > 0 for c in cands)
         fastest = min(c["ms"] for c in cands)
-        near = [c for c in cands if c["ms"] <= fastest * 1.03]
+        band = 1.03 if name == "root" else 1.05  # the gathered passes' wider near-tie band
+        near = [c for c in cands if c["ms"] <= fastest * band]
         best = min(near, key=lambda c: (c["items"], c["unroll"], c["ms"]))
         assert report["chosen"][name] == {key: best[key]
                                           for key in ("tiles", "unroll", "items", "split", "deep")}
