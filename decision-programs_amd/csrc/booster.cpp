@@ -305,12 +305,11 @@ void Grower::prepare(const Quantized& q, const TrainParam& p, int32_t n_slots, b
                      const HistConfig& root_cfg, const HistConfig& level_cfg, bool skip,
                      uint64_t pairs, hipStream_t s) {
   const dp_bin_layout& L = q.layout;
-  need(sparse ? q.sparse.n_tiles > 0 : q.rows.n > 0, "histogram layout not built");
+  rows_major_ = sparse ? nullptr : q.row_major(hist_pairs(pairs, level_cfg.tiles));
+  need(sparse ? q.sparse.n_tiles > 0 : rows_major_ != nullptr, "histogram layout not built");
   need(!skip || (!sparse && q.skip_tiles.n > 0 && q.skip_features.n > 0),
        "skip bins not built");
   need(!pairs || (!sparse && !skip && (pairs & ~q.pairs) == 0), "tile pairs out of place");
-  need(sparse || q.rows_pairs == hist_pairs(pairs, level_cfg.tiles),
-       "row-major copy out of step with the tile pairs");
   lay_ = L;
   lay_.paired_tiles = pairs;
   check_pairs(lay_);
@@ -529,7 +528,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
         dense_fused = F >= kDenseFuseFeatures && B <= 256 && exps;
         launch_hist(q.bins.p, lay_, gpair, ridx_[cur].p, hist_work_[cur].p,
                     int32_t(plan_hist_items(nb, N, G, level_cfg_.items)),
-                    field(c, &PlanCounts::n_hist), B, h, partial_.p, s, q.rows.p, level_cfg_,
+                    field(c, &PlanCounts::n_hist), B, h, partial_.p, s, rows_major_, level_cfg_,
                     skip_tiles_, dense_fused);
         if (dense_fused)
           launch_reduce_evaluate_dense(partial_.p, reduce_jobs_[cur].p, int32_t(nb / 2 + 1),
@@ -708,6 +707,7 @@ uint64_t Grower::signature() const {
   buf(splits_); buf(eval_scratch_); buf(fmask_); buf(info_); buf(counts_); buf(slots_);
   mix(uint64_t(eager_)); mix(uint64_t(sparse_)); mix(uint64_t(colsample_)); mix(uint64_t(tiles_));
   mix(reinterpret_cast<uint64_t>(skip_tiles_)); mix(reinterpret_cast<uint64_t>(skip_features_));
+  mix(reinterpret_cast<uint64_t>(rows_major_));
   mix(uint64_t(node_cap_)); mix(uint64_t(chunk_));
   mix(uint64_t(slot_bytes_)); mix(uint64_t(root_rows_)); mix(uint64_t(root_tiles_));
   mix(uint64_t(root_items_));
@@ -1179,17 +1179,14 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
     tuning_report_ = "{\"defaults\":true}";
   }
   // The gathered passes' row-major copy: with the pairs' joint tiles in place
-  // of their first tiles when the level shape uses the pairs (one tile per
-  // item), else plain; rebuilt only when that changes.
-  if (!sparse) {
-    const uint64_t rp = hist_pairs(hl.paired_tiles, level_cfg.tiles);
-    if (q.rows.n == 0 || q.rows_pairs != rp) {
-      dp_bin_layout rl = q.layout;
-      rl.paired_tiles = rp;
-      q.rows.resize(dp_layout_bytes(&q.layout));
-      launch_tiles_to_rows(q.bins.p, rl, q.rows.p, stream_);
-      q.rows_pairs = rp;
-    }
+  // of their first tiles when the level shape uses the pairs, else plain.
+  const uint64_t rows_pairs = sparse ? 0 : hist_pairs(hl.paired_tiles, level_cfg.tiles);
+  if (!sparse && !q.row_major(rows_pairs)) {
+    dp_bin_layout rl = q.layout;
+    rl.paired_tiles = rows_pairs;
+    auto& copy = q.rows.emplace(rows_pairs, DeviceBuffer<uint8_t>(dp_layout_bytes(&q.layout)))
+                     .first->second;
+    launch_tiles_to_rows(q.bins.p, rl, copy.p, stream_);
   }
   {  // the histogram mode beside the launch shapes
     std::string mode = "{\"layout\":\"";
@@ -1241,7 +1238,7 @@ void Booster::run_round(DMatrix* d, bool with_gradients) {
       uint64_t(with_gradients), reinterpret_cast<uint64_t>(d), reinterpret_cast<uint64_t>(&q),
       reinterpret_cast<uint64_t>(q.bins.p), reinterpret_cast<uint64_t>(q.cols.p),
       reinterpret_cast<uint64_t>(q.cols16.p),
-      reinterpret_cast<uint64_t>(q.rows.p), reinterpret_cast<uint64_t>(q.d_nbins.p),
+      reinterpret_cast<uint64_t>(q.row_major(rows_pairs)), reinterpret_cast<uint64_t>(q.d_nbins.p),
       uint64_t(q.bin_stride), uint64_t(N), reinterpret_cast<uint64_t>(d->labels.p),
       uint64_t(objective_id_), uint64_t(n_groups_), reinterpret_cast<uint64_t>(margin_.p),
       reinterpret_cast<uint64_t>(leaf_values_.p), reinterpret_cast<uint64_t>(grad_.p), reinterpret_cast<uint64_t>(hess_.p),

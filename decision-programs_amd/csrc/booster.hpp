@@ -27,10 +27,14 @@ struct Quantized {
   // (missing: kWideMissing) for the partition, and every histogram from the
   // present-value layout built from them.
   DeviceBuffer<uint16_t> cols16;
-  // row-major copy: rows[(r * n_tiles + t) * 16 + j] (on demand); the first
-  // tile of each pair of rows_pairs holds the pair's joint tile instead
-  DeviceBuffer<uint8_t> rows;
-  uint64_t rows_pairs = 0;
+  // Row-major copies, rows[(r * n_tiles + t) * 16 + j], by the pairs whose
+  // joint tiles replace their first tiles (0: the plain copy); each made on
+  // first use and kept, so boosters sharing the matrix never rewrite one.
+  std::map<uint64_t, DeviceBuffer<uint8_t>> rows;
+  const uint8_t* row_major(uint64_t pairs) const {
+    const auto it = rows.find(pairs);
+    return it == rows.end() ? nullptr : it->second.p;
+  }
   SparseBins sparse;           // present-value layout (on demand, mostly-missing matrices)
   // Skip bins (matrices without missing values, on demand): each feature's most
   // frequent bin, per feature and per 16-feature tile, and the share of the
@@ -184,6 +188,7 @@ class Grower {
   HistConfig root_cfg_, level_cfg_, root_made_;
   uint64_t root_pairs_ = 0;                 // the paired tiles root_work_ was made for
   dp_bin_layout lay_{};                     // the matrix's layout with the pairs in use
+  const uint8_t* rows_major_ = nullptr;     // the row-major copy the gathered passes read
   const uint8_t* skip_tiles_ = nullptr;     // the matrix's skip bins when in use
   const uint8_t* skip_features_ = nullptr;
 };

@@ -202,3 +202,26 @@ def test_multiclass_sampled_trees_identical_with_and_without_pairs(dp, device):
     a = json.loads(with_pairs.save_raw())
     b = json.loads(without.save_raw())
     assert a["learner"]["gradient_booster"] == b["learner"]["gradient_booster"]
+
+
+def test_boosters_sharing_a_matrix_keep_their_row_copies(dp, device):
+    """Three boosters on one matrix, their rounds interleaved (each returns with its round in
+    flight): one-tile items (the row-major copy with the pair's joint tile in place), two-tile
+    items (the pair is an item's two tiles: the same copy) and no pairs (the plain copy).  Each
+    copy is made once and kept, and the three models are identical."""
+    import torch
+    from dpgbdt import ops
+
+    n = 60000
+    values, labels, _, _ = ops.synth(3, n, 20261203, device=device)
+    d = dp.DMatrix(values, labels)
+    base = {"objective": "binary:logistic", "max_depth": 6, "eta": 0.3, "max_bin": 256}
+    shapes = [{"dp_hist_tiles": 1}, {"dp_hist_tiles": 2}, {"dp_hist_pair": 0}]
+    boosters = [dp.Booster(dict(base, **s), [d]) for s in shapes]
+    for r in range(3):
+        for b in boosters:
+            b.update(d, r)
+    torch.cuda.synchronize()
+    assert [b.tuning()["paired_tiles"] for b in boosters] == [1 << 6, 1 << 6, 0]
+    models = [json.loads(b.save_raw())["learner"]["gradient_booster"] for b in boosters]
+    assert models[0] == models[1] == models[2]
