@@ -613,7 +613,7 @@ void Grower::grow(const Quantized& q, const int32_t* gpair, const int32_t* exps,
     // tiles; for dense tiles, what the level kernel's LDS and registers allow.
     a.hist_slots = sparse_ ? cus_ * 2
                            : hist_resident(true, L.missing_bin >= 0, skip_tiles_ != nullptr,
-                                           level_cfg_);
+                                           level_cfg_, a.hist_pairs != 0);
     a.hist_elems = S;
     a.part_chunk = chunk_;
     a.leaf_chunk = chunk_;

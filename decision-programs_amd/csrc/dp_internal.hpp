@@ -332,8 +332,10 @@ void check_pairs(const dp_bin_layout& layout);
 // restricted to the tile), for launch_reduce_evaluate_dense; otherwise as the
 // LDS image [bin][g of 16 features, h of 16 features] (launch_hist_reduce).
 // Histogram workgroups the device holds at once for launch_hist's kernel of
-// this configuration (gathered or contiguous rows; missing values; skip bins).
-int hist_resident(bool gather, bool missing, bool skip, const HistConfig& cfg);
+// this configuration (gathered or contiguous rows; missing values; skip bins;
+// paired tiles in use).
+int hist_resident(bool gather, bool missing, bool skip, const HistConfig& cfg,
+                  bool paired = false);
 void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t* gpair,
                  const uint32_t* ridx, const HistWork* work, int32_t n_work,
                  const int32_t* n_work_dev, int32_t bin_stride, int64_t* hist,

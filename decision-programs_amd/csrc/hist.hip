@@ -347,8 +347,11 @@ __device__ __forceinline__ void hist_item(const HistPass& a, const HistWork& w, 
   __syncthreads();  // the next item clears the LDS this item just read
 }
 
-template <bool GATHER, int MODE, int TPW, int U, int SPLIT = 0, bool DEEP = false>
-__global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(DEEP && (U == 2 || MODE != 0) ? 4 : 8 / TPW, 8 / TPW))) void hist_kernel(
+// PAIRS: the launch has paired tiles (an instantiation of its own, so that the
+// kernels of unpaired launches carry no pair items' code or registers).
+template <bool GATHER, int MODE, int TPW, int U, int SPLIT = 0, bool DEEP = false,
+          bool PAIRS = false>
+__global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(DEEP && !(PAIRS && U == 1) ? 4 : 8 / TPW, 8 / TPW))) void hist_kernel(
     const uint8_t* __restrict__ bins, const uint8_t* __restrict__ skip, int64_t n_rows,
     int32_t n_features, int32_t n_tiles,
     const int2* __restrict__ gpair, const uint32_t* __restrict__ ridx,
@@ -378,7 +381,8 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(DE
   for (int32_t item = blockIdx.x; item < n_work; item += gridDim.x) {
     const HistWork w = item == int32_t(blockIdx.x) ? w_first : work[item];
     if (w.begin >= w.end) continue;  // padding item (uniform per workgroup)
-    if constexpr (MODE == 0) {
+    if constexpr (PAIRS) {
+      static_assert(MODE == 0, "pairs take items without skips");
       if (w.tile < 63 && ((pairs >> w.tile) & 1ull)) {  // the item's tiles are pair k
         const int32_t k = __builtin_popcountll(joint_pairs & ((1ull << w.tile) - 1ull));
         const int32_t jt = joint_first < 0 ? w.tile : joint_first + k;  // its joint tile
@@ -952,29 +956,32 @@ void check_pairs(const dp_bin_layout& layout) {
 }
 
 namespace {
-template <bool GATHER, int MODE>
+template <bool GATHER, int MODE, bool PAIRS = false>
 auto hist_instance(const HistConfig& cfg) {
   if (cfg.deep)
     return cfg.tiles == 2
-               ? (cfg.unroll == 1 ? hist_kernel<GATHER, MODE, 2, 1, 0, true>
-                                  : hist_kernel<GATHER, MODE, 2, 2, 0, true>)
-               : (cfg.unroll == 1 ? hist_kernel<GATHER, MODE, 1, 1, 0, true>
-                                  : hist_kernel<GATHER, MODE, 1, 2, 0, true>);
+               ? (cfg.unroll == 1 ? hist_kernel<GATHER, MODE, 2, 1, 0, true, PAIRS>
+                                  : hist_kernel<GATHER, MODE, 2, 2, 0, true, PAIRS>)
+               : (cfg.unroll == 1 ? hist_kernel<GATHER, MODE, 1, 1, 0, true, PAIRS>
+                                  : hist_kernel<GATHER, MODE, 1, 2, 0, true, PAIRS>);
   if (cfg.tiles == 2) {
     if (cfg.split == 4)
-      return cfg.unroll == 1 ? hist_kernel<GATHER, MODE, 2, 1, 4>
-                             : hist_kernel<GATHER, MODE, 2, 2, 4>;
+      return cfg.unroll == 1 ? hist_kernel<GATHER, MODE, 2, 1, 4, false, PAIRS>
+                             : hist_kernel<GATHER, MODE, 2, 2, 4, false, PAIRS>;
     if (cfg.split == 5)
-      return cfg.unroll == 1 ? hist_kernel<GATHER, MODE, 2, 1, 5>
-                             : hist_kernel<GATHER, MODE, 2, 2, 5>;
-    return cfg.unroll == 1 ? hist_kernel<GATHER, MODE, 2, 1, 0>
-                           : hist_kernel<GATHER, MODE, 2, 2, 0>;
+      return cfg.unroll == 1 ? hist_kernel<GATHER, MODE, 2, 1, 5, false, PAIRS>
+                             : hist_kernel<GATHER, MODE, 2, 2, 5, false, PAIRS>;
+    return cfg.unroll == 1 ? hist_kernel<GATHER, MODE, 2, 1, 0, false, PAIRS>
+                           : hist_kernel<GATHER, MODE, 2, 2, 0, false, PAIRS>;
   }
-  return cfg.unroll == 1 ? hist_kernel<GATHER, MODE, 1, 1> : hist_kernel<GATHER, MODE, 1, 2>;
+  return cfg.unroll == 1 ? hist_kernel<GATHER, MODE, 1, 1, 0, false, PAIRS>
+                         : hist_kernel<GATHER, MODE, 1, 2, 0, false, PAIRS>;
 }
 
+// paired: the launch uses paired tiles (mode 0 only).
 template <bool GATHER>
-auto hist_mode(int mode, const HistConfig& cfg) {
+auto hist_mode(int mode, const HistConfig& cfg, bool paired) {
+  if (paired) return hist_instance<GATHER, 0, true>(cfg);
   return mode == 1 ? hist_instance<GATHER, 1>(cfg)
                    : (mode == 2 ? hist_instance<GATHER, 2>(cfg) : hist_instance<GATHER, 0>(cfg));
 }
@@ -1012,9 +1019,10 @@ int device_cus() {
 int mode_of(bool missing, bool skip) { return missing ? 1 : (skip ? 2 : 0); }
 }  // namespace
 
-int hist_resident(bool gather, bool missing, bool skip, const HistConfig& cfg) {
+int hist_resident(bool gather, bool missing, bool skip, const HistConfig& cfg, bool paired) {
   const int mode = mode_of(missing, skip);
-  auto kernel = gather ? hist_mode<true>(mode, cfg) : hist_mode<false>(mode, cfg);
+  need(!paired || mode == 0, "paired tiles take matrices without missing values or skip bins");
+  auto kernel = gather ? hist_mode<true>(mode, cfg, paired) : hist_mode<false>(mode, cfg, paired);
   const size_t lds = size_t(cfg.tiles) * kLdsWords * sizeof(unsigned long long);
   return prepare_hist_kernel(reinterpret_cast<const void*>(kernel), lds) * device_cus();
 }
@@ -1053,7 +1061,8 @@ void launch_hist(const uint8_t* bins, const dp_bin_layout& layout, const int32_t
   check_pairs(layout);
   need(!(pairs && skip), "paired tiles and skip bins do not combine");
   const int mode = mode_of(missing, skip != nullptr);
-  auto kernel = ridx ? hist_mode<true>(mode, cfg) : hist_mode<false>(mode, cfg);
+  auto kernel = ridx ? hist_mode<true>(mode, cfg, pairs != 0)
+                     : hist_mode<false>(mode, cfg, pairs != 0);
   const size_t lds = size_t(cfg.tiles) * kLdsWords * sizeof(unsigned long long);
   // At most two rounds of resident workgroups; a multiple of 8.
   const int resident =
