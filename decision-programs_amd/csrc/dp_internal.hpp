@@ -723,8 +723,13 @@ struct SparseBins {
   int32_t tile_features = 0, n_tiles = 0;  // n_tiles 0: not built
   int32_t bin_stride = 0;                  // the stride the entries' indexes use
   int64_t nnz = 0;
-  DeviceBuffer<uint32_t> ptr;      // [n_tiles * n_rows + 1]
-  DeviceBuffer<uint16_t> entries;  // [nnz]
+  DeviceBuffer<uint32_t> ptr;      // [n_tiles * n_rows + 1]: (tile t, row r) at t * n_rows + r
+  DeviceBuffer<uint16_t> entries;  // [nnz], tile-major (the root pass's contiguous runs)
+  // The same entries row-major, for gathered rows: (row r, tile t) at
+  // rptr[r * n_tiles + t], so the tile items of one row chunk, which run on one
+  // XCD, read each row's offsets and entries from the same L2 lines.
+  DeviceBuffer<uint32_t> rptr;      // [n_rows * n_tiles + 1]
+  DeviceBuffer<uint16_t> rentries;  // [nnz]
 };
 constexpr int64_t kSparseLdsBytes = 64 * 1024;
 // LDS of one present-value tile in the histogram kernel: g and h in planes of

@@ -475,6 +475,10 @@ __device__ __forceinline__ void evaluate_tile(const SparseEvalArgs& ev, const Hi
 
 // Histograms from the present-value layout (SparseBins): one work item = rows
 // [begin, end) of node `slot` for one sparse tile of tile_features features.
+// Contiguous rows (the root) read the tile-major entries; gathered rows read
+// the row-major copy, whose (row, tile) ranges of one row are adjacent, so the
+// tile items of a row chunk, dispatched on one XCD, share each row's offsets
+// and entries in L2.
 // The tile's histogram lives in LDS as two planes, g then h, each
 // [feature][bin_stride + 1] int64 (dynamic LDS; the h plane at the fixed word
 // kSparsePlaneWords): a plane's words of one feature are adjacent, so the
@@ -544,7 +548,7 @@ __global__ __launch_bounds__(THREADS) void hist_sparse_kernel(
     const uint32_t* __restrict__ ridx, const HistWork* __restrict__ work, int32_t n_work_host,
     const int32_t* __restrict__ n_work_dev, int32_t bin_stride,
     unsigned long long* __restrict__ hist, unsigned long long* __restrict__ partial,
-    SparseEvalArgs ev) {
+    SparseEvalArgs ev, int32_t ptr_rows) {
   extern __shared__ unsigned long long lds_tile[];  // g plane, then h plane
   constexpr int P = kPosPerLane<GATHER>;
   constexpr int kMapSlots = 64 * P;  // positions per round
@@ -592,7 +596,11 @@ __global__ __launch_bounds__(THREADS) void hist_sparse_kernel(
       lds_tile[hoff + e] = 0ull;
     }
     __syncthreads();
-    const uint32_t* tp = ptr + int64_t(w.tile) * n_rows;
+    // (tile t, row r)'s entry range starts at ptr[t * n_rows + r] in the
+    // tile-major layout (ptr_rows 1), at ptr[r * ptr_rows + t] in the row-major
+    // copy (ptr_rows = n_tiles; gathered rows only).
+    const int64_t rstep = GATHER ? ptr_rows : 1;
+    const uint32_t* tp = ptr + int64_t(w.tile) * (rstep == 1 ? n_rows : 1);
     // The rows of block i0 (rows i0 + lane): entry range start, length and
     // (g, h), loaded one block ahead (gathered row ids two blocks ahead).
     // Loads are branch-free (indexes past the item clamped, their values
@@ -608,7 +616,7 @@ __global__ __launch_bounds__(THREADS) void hist_sparse_kernel(
     };
     auto load_rows = [&](int64_t i0, uint32_t r) -> Rows {
       const bool valid = i0 + lane < w.end;
-      const uint32_t b = tp[r], e = tp[r + 1];
+      const uint32_t b = tp[int64_t(r) * rstep], e = tp[int64_t(r) * rstep + 1];
       const int2 q = gpair[r];
       return Rows{b, valid ? e - b : 0u, valid ? q : make_int2(0, 0)};
     };
@@ -1154,12 +1162,16 @@ void launch_hist_sparse(const SparseBins& sp, int64_t n_rows, int32_t n_features
   // Two workgroups per CU (at most 68 KiB of LDS each), a multiple of 8 for the XCD order.
   int grid = n_work < 1024 ? n_work : 1024;
   grid = (grid + 7) / 8 * 8;
+  // Gathered rows read the row-major copy (when built), contiguous rows the
+  // tile-major entries.
+  const bool rows = ridx && sp.rptr.n > 0;
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(eval ? kSparseEvalThreads : kHistThreads), lds, s,
-                     sp.ptr.p, sp.entries.p,
+                     rows ? sp.rptr.p : sp.ptr.p, rows ? sp.rentries.p : sp.entries.p,
                      n_rows, n_features, sp.tile_features, reinterpret_cast<const int2*>(gpair),
                      ridx, work, n_work, n_work_dev, bin_stride,
                      reinterpret_cast<unsigned long long*>(hist),
-                     reinterpret_cast<unsigned long long*>(partial), ev);
+                     reinterpret_cast<unsigned long long*>(partial), ev,
+                     rows ? sp.n_tiles : 1);
   DP_HIP(hipGetLastError());
 }
 

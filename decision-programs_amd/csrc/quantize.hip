@@ -512,6 +512,32 @@ void launch_tiles_to_columns(const uint8_t* bins, const dp_bin_layout& layout, u
 }
 
 
+// Row-major present values: counts of (row r, tile t) at r * T + t, from the
+// tile-major offsets.
+__global__ void sparse_row_counts_kernel(const uint32_t* __restrict__ ptr, int64_t n_rows,
+                                         int32_t n_tiles, uint32_t* __restrict__ counts) {
+  const int64_t n = n_rows * n_tiles;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += int64_t(blockDim.x) * gridDim.x) {
+    const int64_t r = i / n_tiles, t = i - r * n_tiles;
+    counts[i] = ptr[t * n_rows + r + 1] - ptr[t * n_rows + r];
+  }
+}
+
+// Copies each (row, tile)'s entries to their row-major place (one thread each).
+__global__ void sparse_row_fill_kernel(const uint32_t* __restrict__ ptr,
+                                       const uint16_t* __restrict__ entries, int64_t n_rows,
+                                       int32_t n_tiles, const uint32_t* __restrict__ rptr,
+                                       uint16_t* __restrict__ rentries) {
+  const int64_t n = n_rows * n_tiles;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += int64_t(blockDim.x) * gridDim.x) {
+    const int64_t r = i / n_tiles, t = i - r * n_tiles;
+    const uint32_t b = ptr[t * n_rows + r], e = ptr[t * n_rows + r + 1], d = rptr[i];
+    for (uint32_t k = 0; k < e - b; ++k) rentries[d + k] = entries[b + k];
+  }
+}
+
 int32_t sparse_tile_features(int32_t bin_stride) {
   int32_t t = int32_t(kSparseLdsBytes / (int64_t(bin_stride) * 16)) / 16 * 16;
   if (t > 256) t = 256;
@@ -559,6 +585,18 @@ double build_sparse(int64_t N, int32_t n_features, int32_t bin_stride, double ma
   DeviceBuffer<uint16_t> entries(size_t(nnz + kSparseEntryPad));
   fill(ptr.p, entries.p, tf, n);
   DP_HIP(hipGetLastError());
+  // The row-major copy: counts in (row, tile) order, their exclusive scan,
+  // then each (row, tile)'s entries copied to its place.
+  DeviceBuffer<uint32_t> rptr(size_t(n + 1));
+  const dim3 grid(grid_for(n, 256, 16384));
+  hipLaunchKernelGGL(sparse_row_counts_kernel, grid, dim3(256), 0, s, ptr.p, N, T, counts.p);
+  DP_HIP(hipGetLastError());
+  DP_HIP(rocprim::exclusive_scan(temp.p, temp_bytes, counts.p, rptr.p, 0u, size_t(n + 1),
+                                 rocprim::plus<uint32_t>(), s));
+  DeviceBuffer<uint16_t> rentries(size_t(nnz + kSparseEntryPad));
+  hipLaunchKernelGGL(sparse_row_fill_kernel, grid, dim3(256), 0, s, ptr.p, entries.p, N, T,
+                     rptr.p, rentries.p);
+  DP_HIP(hipGetLastError());
   DP_HIP(hipStreamSynchronize(s));
   out.tile_features = tf;
   out.n_tiles = T;
@@ -566,6 +604,8 @@ double build_sparse(int64_t N, int32_t n_features, int32_t bin_stride, double ma
   out.nnz = int64_t(nnz);
   out.ptr = std::move(ptr);
   out.entries = std::move(entries);
+  out.rptr = std::move(rptr);
+  out.rentries = std::move(rentries);
   return density;
 }
 
