@@ -62,6 +62,10 @@ __device__ __forceinline__ long long row_shuffle64(long long v, int src) {
   return (long long)((uint64_t(uint32_t(hi)) << 32) | uint32_t(lo));
 }
 
+// Scratch of the compacted evaluation in seg_evaluate, per wavefront: 64 slots
+// of (left g, left h) and the four rows' missing sums (g, h).  16-byte aligned.
+constexpr int kSegScratchWords = 2 * 64 + 2 * 4;
+
 // The evaluation of four features per wavefront, one per 16-lane row, four bins
 // per lane (bins 4 * (lane % 16) + j in dg, dh): the row's prefix scan and
 // argmax take the row_shr steps of the full-wave ones; the row total and the
@@ -69,6 +73,19 @@ __device__ __forceinline__ long long row_shuffle64(long long v, int src) {
 // as feature_best, with a quarter of the wavefronts and of their fixed costs.
 // The row's first lane writes feature f's best candidate of `node` (live: the
 // row's feature exists; every lane takes part in the row steps).
+//
+// Empty bins.  A bin b > 0 whose (g, h) words are both zero, and which is not
+// the skipped bin, has the left sums of bin b - 1, so its candidate's loss is
+// bit for bit that of bin b - 1: with the larger loss winning and ties going
+// to the lower bin, it can never be the feature's pick, nor change which lane
+// holds the pick.  Only the other bins are needed.  When a wavefront's needed
+// bins number at most 64 (a node of few rows: most bins are empty), they are
+// packed into consecutive lanes through the per-wavefront LDS scratch `scr`
+// (kSegScratchWords words; nullptr: never), their losses are computed there,
+// one candidate per lane instead of four bins per lane, and each returns to
+// its bin; the empty bins are not candidates.  The gains, and so every pick,
+// are those of the in-place evaluation of all bins.  (Packing into two rounds
+// of 64 was measured slower than the in-place evaluation.)
 __device__ __forceinline__ void seg_evaluate(const long long (&dg)[4], const long long (&dh)[4],
                                              int32_t node, int32_t f, bool live,
                                              int32_t n_features, const int32_t* __restrict__ n_bins,
@@ -76,7 +93,8 @@ __device__ __forceinline__ void seg_evaluate(const long long (&dg)[4], const lon
                                              double uh, const Param& p,
                                              const uint32_t* __restrict__ fmask,
                                              const uint8_t* __restrict__ skip_bins,
-                                             FeatCand* __restrict__ cand) {
+                                             FeatCand* __restrict__ cand,
+                                             long long* __restrict__ scr = nullptr) {
   constexpr int BPL = 4;
   const int lane = threadIdx.x & 63;
   const int seg = lane >> 4, sub = lane & 15;
@@ -113,32 +131,105 @@ __device__ __forceinline__ void seg_evaluate(const long long (&dg)[4], const lon
     kh = mh;
     mg = mh = 0;
   }
-
+  // Left sums of the lane's bins, and which bins exist (in) and are needed
+  // (above), one bit per bin.
+  long long lg[BPL], lh[BPL];
+  int in = 0, need = 0;
+#pragma unroll
+  for (int j = 0; j < BPL; ++j) {
+    const int b = sub * BPL + j;
+    lg[j] = og + sg[j] + (b >= skip && skip >= 0 ? kg : 0);
+    lh[j] = oh + sh[j] + (b >= skip && skip >= 0 ? kh : 0);
+    if (b < nb) {
+      in |= 1 << j;
+      if (b == 0 || b == skip || dg[j] != 0 || dh[j] != 0) need |= 1 << j;
+    }
+  }
+  // A bin's loss (the better of missing right and missing left) and its
+  // missing-value direction.
+  auto evaluate = [&](long long xg, long long xh, long long yg, long long yh, double& l,
+                      int& d) {
+    const double right_missing = split_loss(p, xg, xh, gp - xg, hp - xh, ug, uh, parent_gain);
+    const double left_missing =
+        (yg == 0 && yh == 0)
+            ? right_missing
+            : split_loss(p, xg + yg, xh + yh, gp - xg - yg, hp - xh - yh, ug, uh, parent_gain);
+    d = left_missing > right_missing;
+    l = d ? left_missing : right_missing;
+  };
+  // The lane's best bin, taken in increasing bin order (ties keep the lower).
   Cand c;
   c.loss = -INFINITY;
   c.gl = c.hl = 0;
   c.feature = f;
   c.bin = -1;
   c.dl = 0;
+  auto fold = [&](int j, double l, int d) {
+    if (l > c.loss) {
+      c.loss = l;
+      c.bin = sub * BPL + j;
+      c.dl = d;
+      c.gl = d ? lg[j] + mg : lg[j];
+      c.hl = d ? lh[j] + mh : lh[j];
+    }
+  };
+  // Lane-order slots of the needed bins: a lane has fewer than 8, so three
+  // bit ballots of its count give the exclusive prefix over the lanes.
+  unsigned long long c0 = 0, c1 = 0, c2 = 0;
+  int n_need = 65;
+  if (scr) {
+    const int cnt = __popc(need);
+    c0 = __ballot(cnt & 1);
+    c1 = __ballot(cnt & 2);
+    c2 = __ballot(cnt & 4);
+    n_need = __popcll(c0) + 2 * __popcll(c1) + 4 * __popcll(c2);
+  }
+  if (n_need <= 64) {  // uniform per wavefront: one candidate per lane
+    const unsigned long long below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    const int base = __popcll(c0 & below) + 2 * __popcll(c1 & below) + 4 * __popcll(c2 & below);
+    // Slots of row r start at lane 16 r's base; each row's missing sums sit
+    // after the 64 slots.
+    const int r1 = __builtin_amdgcn_readlane(base, 16), r2 = __builtin_amdgcn_readlane(base, 32),
+              r3 = __builtin_amdgcn_readlane(base, 48);
+    if (sub == 0) {
+      scr[128 + 2 * seg] = mg;
+      scr[128 + 2 * seg + 1] = mh;
+    }
 #pragma unroll
-  for (int j = 0; j < BPL; ++j) {
-    const int b = sub * BPL + j;
-    if (b < nb) {
-      const long long lg = og + sg[j] + (b >= skip && skip >= 0 ? kg : 0);
-      const long long lh = oh + sh[j] + (b >= skip && skip >= 0 ? kh : 0);
-      const double right_missing = split_loss(p, lg, lh, gp - lg, hp - lh, ug, uh, parent_gain);
-      const double left_missing =
-          (mg == 0 && mh == 0)
-              ? right_missing
-              : split_loss(p, lg + mg, lh + mh, gp - lg - mg, hp - lh - mh, ug, uh, parent_gain);
-      const int dl = left_missing > right_missing;
-      const double loss = dl ? left_missing : right_missing;
-      if (loss > c.loss) {
-        c.loss = loss;
-        c.bin = b;
-        c.dl = dl;
-        c.gl = dl ? lg + mg : lg;
-        c.hl = dl ? lh + mh : lh;
+    for (int j = 0; j < BPL; ++j) {
+      const int slot = base + __popc(need & ((1 << j) - 1));
+      if ((need >> j) & 1) {
+        scr[2 * slot] = lg[j];
+        scr[2 * slot + 1] = lh[j];
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    double l = -INFINITY;
+    int d = 0;
+    if (lane < n_need) {
+      const int r = (lane >= r1 ? 1 : 0) + (lane >= r2 ? 1 : 0) + (lane >= r3 ? 1 : 0);
+      evaluate(scr[2 * lane], scr[2 * lane + 1], scr[128 + 2 * r], scr[128 + 2 * r + 1], l, d);
+    }
+    const unsigned long long dmask = __ballot(d);
+    __builtin_amdgcn_wave_barrier();
+    // the slots' (g, h) have been read: their first 64 words take the losses
+    if (lane < n_need) scr[lane] = __double_as_longlong(l);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int j = 0; j < BPL; ++j) {
+      const int slot = base + __popc(need & ((1 << j) - 1));
+      if ((need >> j) & 1)
+        fold(j, __longlong_as_double(scr[slot]), int((dmask >> slot) & 1ull));
+    }
+    __builtin_amdgcn_wave_barrier();  // the next call rewrites the scratch
+  } else {
+#pragma unroll
+    for (int j = 0; j < BPL; ++j) {
+      if ((in >> j) & 1) {
+        double l;
+        int d;
+        evaluate(lg[j], lh[j], mg, mh, l, d);
+        fold(j, l, d);
       }
     }
   }

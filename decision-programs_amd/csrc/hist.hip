@@ -415,7 +415,8 @@ __device__ __forceinline__ void evaluate_tile(const SparseEvalArgs& ev, const Hi
                                               int32_t f0, int32_t nf, int32_t n_features,
                                               int32_t bin_stride, const unsigned long long* lds,
                                               uint32_t ps, uint32_t hoff,
-                                              unsigned long long* __restrict__ hist) {
+                                              unsigned long long* __restrict__ hist,
+                                              long long* __restrict__ scr) {
   constexpr int BPL = 4;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int seg = lane >> 4, sub = lane & 15;
@@ -452,7 +453,7 @@ __device__ __forceinline__ void evaluate_tile(const SparseEvalArgs& ev, const Hi
     long long g[BPL], h[BPL];
     load(fl, live, g, h);
     seg_evaluate(g, h, w.slot, f0 + fl, live, n_features, ev.n_bins, ev.node_sums, ug, uh, ev.p,
-                 ev.fmask, ev.skip_bins, ev.cand);
+                 ev.fmask, ev.skip_bins, ev.cand, scr);
     if (!sib) continue;
     // The sibling: the parent's words minus the node's (read again from LDS,
     // so that they are not held across the evaluation above).
@@ -469,7 +470,7 @@ __device__ __forceinline__ void evaluate_tile(const SparseEvalArgs& ev, const Hi
       }
     }
     seg_evaluate(g, h, w.slot ^ 1, f0 + fl, live, n_features, ev.n_bins, ev.node_sums, ug, uh,
-                 ev.p, ev.fmask, ev.skip_bins, ev.cand);
+                 ev.p, ev.fmask, ev.skip_bins, ev.cand, scr);
   }
 }
 
@@ -542,7 +543,7 @@ __device__ __forceinline__ uint32_t wave_inclusive_umax(uint32_t x) {
 }
 
 template <bool GATHER, bool EVAL, int THREADS>
-__global__ __launch_bounds__(THREADS) void hist_sparse_kernel(
+__global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(4))) void hist_sparse_kernel(
     const uint32_t* __restrict__ ptr, const uint16_t* __restrict__ entries, int64_t n_rows,
     int32_t n_features, int32_t tile_features, const int2* __restrict__ gpair,
     const uint32_t* __restrict__ ridx, const HistWork* __restrict__ work, int32_t n_work_host,
@@ -553,8 +554,11 @@ __global__ __launch_bounds__(THREADS) void hist_sparse_kernel(
   constexpr int P = kPosPerLane<GATHER>;
   constexpr int kMapSlots = 64 * P;  // positions per round
   // Each wavefront's map of one round's kMapSlots positions (16-bit words,
-  // 8-byte aligned for the lanes' wide reads).
-  __shared__ uint2 lds_map[THREADS / 64][kMapSlotsMax / 4];
+  // 8-byte aligned for the lanes' wide reads).  With EVAL the same words are
+  // also the wavefront's scratch of seg_evaluate (cleared after it).
+  constexpr int kMapWords = EVAL ? kSegScratchWords : kMapSlotsMax / 4;
+  static_assert(kMapWords >= kMapSlotsMax / 4, "the map fits its wavefront's words");
+  __shared__ __attribute__((aligned(16))) uint2 lds_map[THREADS / 64][kMapWords];
   const int32_t n_work = n_work_dev ? *n_work_dev : n_work_host;
   const int64_t slot_words = int64_t(tile_features) * bin_stride * 2;
   const uint32_t ps = uint32_t(bin_stride) + 1u;         // plane words per feature
@@ -707,8 +711,13 @@ __global__ __launch_bounds__(THREADS) void hist_sparse_kernel(
         reinterpret_cast<ulonglong2*>(out)[k] = make_ulonglong2(lds_tile[a], lds_h[a]);
       }
     if constexpr (EVAL) {
-      if (direct)
-        evaluate_tile<THREADS>(ev, w, f0, nf, n_features, bin_stride, lds_tile, ps, hoff, hist);
+      if (direct) {
+        evaluate_tile<THREADS>(ev, w, f0, nf, n_features, bin_stride, lds_tile, ps, hoff, hist,
+                               reinterpret_cast<long long*>(lds_map[wave]));
+        // The scratch overwrote the map words: none may carry a live tag.
+        __builtin_amdgcn_wave_barrier();
+        clear_words();
+      }
     }
     __syncthreads();  // the next item clears the LDS this item just read
   }

@@ -263,6 +263,24 @@ const HistTuning& tune_sparse_hist(const SparseBins& sp, int64_t n_rows, int32_t
   std::vector<HistConfig> cands;
   for (int32_t items : {512, 1024, 2048}) cands.push_back(HistConfig{1, 2, items});
   DeviceBuffer<int64_t> out(size_t(n_features) * size_t(bin_stride) * 2);
+  // The booster sums the root's partial slots in the launch that also
+  // evaluates them (reduce_evaluate_flat_kernel) whenever the bins allow it;
+  // its reduce runs one workgroup per 16 features, so its time grows with the
+  // slots far more than the reduce-only launch's.  The timed pass runs that
+  // launch, with node sums of zero (every candidate is refused at once, the
+  // same small evaluation for each candidate count).
+  const bool fused = bin_stride <= 64 && sp.tile_features % 16 == 0;  // as the booster decides
+  DeviceBuffer<int32_t> nbins(fused ? size_t(n_features) : 0);
+  DeviceBuffer<int64_t> sums(fused ? 2 : 0);
+  DeviceBuffer<int32_t> exps(fused ? 2 : 0);
+  DeviceBuffer<FeatCand> feat(fused ? size_t(n_features) : 0);
+  if (fused) {
+    const std::vector<int32_t> nb(size_t(n_features), bin_stride);
+    DP_HIP(hipMemcpyAsync(nbins.p, nb.data(), nbins.bytes(), hipMemcpyHostToDevice, s));
+    DP_HIP(hipMemsetAsync(sums.p, 0, sums.bytes(), s));
+    DP_HIP(hipMemsetAsync(exps.p, 0, exps.bytes(), s));
+  }
+  const dp_train_param zero{};
   dp_bin_layout L{};
   L.n_rows = n_rows;
   L.n_features = n_features;
@@ -286,8 +304,15 @@ const HistTuning& tune_sparse_hist(const SparseBins& sp, int64_t n_rows, int32_t
             [&] {
               launch_hist_sparse(sp, n_rows, n_features, gpair, nullptr, dw.p, int32_t(w.size()),
                                  nullptr, bin_stride, out.p, partial.p, s);
-              launch_hist_reduce_flat(partial.p, dj.p, 1, nullptr, sp.n_tiles, sp.tile_features,
-                                      n_features, bin_stride, nullptr, out.p, s);
+              if (fused)
+                launch_reduce_evaluate_flat(partial.p, dj.p, 1, nullptr, sp.n_tiles,
+                                            sp.tile_features, n_features, bin_stride, nullptr,
+                                            out.p, nbins.p, sums.p, exps.p, zero, nullptr,
+                                            nullptr, feat.p, true, s);
+              else
+                launch_hist_reduce_flat(partial.p, dj.p, 1, nullptr, sp.n_tiles,
+                                        sp.tile_features, n_features, bin_stride, nullptr, out.p,
+                                        s);
             },
             s);
         DP_HIP(hipStreamSynchronize(s));
