@@ -20,26 +20,80 @@ struct Param {
   double lambda, alpha, mcw, gamma;
 };
 
+// The three functions below are branch-free: every value is computed and the
+// refused cases are selected afterwards, so a wavefront's bins form one block of
+// straight-line code whose divisions the compiler can interleave.  A selected
+// value is the one the branching form returns, bit for bit.
 __device__ __forceinline__ double threshold_l1(double g, double alpha) {
-  if (g > alpha) return g - alpha;
-  if (g < -alpha) return g + alpha;
-  return 0.0;
+  const double up = g - alpha, down = g + alpha;
+  return g > alpha ? up : (g < -alpha ? down : 0.0);
 }
 
 __device__ __forceinline__ double calc_gain(const Param& p, double g, double h) {
-  if (h < p.mcw || h <= 0.0) return 0.0;
   const double t = threshold_l1(g, p.alpha);
-  return (t * t) / (h + p.lambda);
+  const double q = (t * t) / (h + p.lambda);
+  return (h < p.mcw || h <= 0.0) ? 0.0 : q;
 }
 
 __device__ __forceinline__ double split_loss(const Param& p, long long qgl, long long qhl,
                                              long long qgr, long long qhr, double ug, double uh,
                                              double parent_gain) {
-  if (qhl <= 0 || qhr <= 0) return -INFINITY;
   const double gl = double(qgl) * ug, hl = double(qhl) * uh;
   const double gr = double(qgr) * ug, hr = double(qhr) * uh;
-  if (hl < p.mcw || hr < p.mcw) return -INFINITY;
-  return (calc_gain(p, gl, hl) + calc_gain(p, gr, hr)) - parent_gain;
+  const double loss = (calc_gain(p, gl, hl) + calc_gain(p, gr, hr)) - parent_gain;
+  return (qhl <= 0 || qhr <= 0 || hl < p.mcw || hr < p.mcw) ? -INFINITY : loss;
+}
+
+// The best of a lane's BPL bins, in increasing bin order (ties keep the
+// lower): bin b0 + j has left sums (lg[j], lh[j]) and exists where bit j of
+// `in` is set; the node's rows the bins do not hold are (mg, mh).  Each bin's
+// loss is the better of missing right and missing left (the two are one
+// candidate, and compute to the same bits, without missing rows; when no lane
+// has any, the second is skipped).  Straight-line code, so that the bins'
+// divisions interleave -- or, with SERIAL, one bin after the other behind a
+// branch each, which holds fewer registers at once.
+template <int BPL, bool SERIAL = false>
+__device__ __forceinline__ void best_of_bins(const long long (&lg)[BPL], const long long (&lh)[BPL],
+                                             int in, int b0, long long mg, long long mh,
+                                             long long gp, long long hp, double ug, double uh,
+                                             double parent_gain, const Param& p, Cand& c) {
+  auto fold = [&](int j, double l, int d) {
+    const bool take = ((in >> j) & 1) && l > c.loss;
+    c.loss = take ? l : c.loss;
+    c.bin = take ? b0 + j : c.bin;
+    c.dl = take ? d : c.dl;
+    c.gl = take ? (d ? lg[j] + mg : lg[j]) : c.gl;
+    c.hl = take ? (d ? lh[j] + mh : lh[j]) : c.hl;
+  };
+  if constexpr (SERIAL) {
+#pragma unroll
+    for (int j = 0; j < BPL; ++j) {
+      if ((in >> j) & 1) {
+        const double right_missing =
+            split_loss(p, lg[j], lh[j], gp - lg[j], hp - lh[j], ug, uh, parent_gain);
+        const double left_missing =
+            (mg == 0 && mh == 0) ? right_missing
+                                 : split_loss(p, lg[j] + mg, lh[j] + mh, gp - lg[j] - mg,
+                                              hp - lh[j] - mh, ug, uh, parent_gain);
+        const int d = left_missing > right_missing;
+        fold(j, d ? left_missing : right_missing, d);
+      }
+    }
+  } else if (__ballot(mg != 0 || mh != 0)) {  // uniform
+#pragma unroll
+    for (int j = 0; j < BPL; ++j) {
+      const double right_missing =
+          split_loss(p, lg[j], lh[j], gp - lg[j], hp - lh[j], ug, uh, parent_gain);
+      const double left_missing = split_loss(p, lg[j] + mg, lh[j] + mh, gp - lg[j] - mg,
+                                             hp - lh[j] - mh, ug, uh, parent_gain);
+      const int d = left_missing > right_missing;
+      fold(j, d ? left_missing : right_missing, d);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < BPL; ++j)
+      fold(j, split_loss(p, lg[j], lh[j], gp - lg[j], hp - lh[j], ug, uh, parent_gain), 0);
+  }
 }
 
 // Column sampling: fmask holds one bit per feature for every node of the
@@ -86,6 +140,7 @@ constexpr int kSegScratchWords = 2 * 64 + 2 * 4;
 // its bin; the empty bins are not candidates.  The gains, and so every pick,
 // are those of the in-place evaluation of all bins.  (Packing into two rounds
 // of 64 was measured slower than the in-place evaluation.)
+template <bool SERIAL = false>
 __device__ __forceinline__ void seg_evaluate(const long long (&dg)[4], const long long (&dh)[4],
                                              int32_t node, int32_t f, bool live,
                                              int32_t n_features, const int32_t* __restrict__ n_bins,
@@ -145,18 +200,6 @@ __device__ __forceinline__ void seg_evaluate(const long long (&dg)[4], const lon
       if (b == 0 || b == skip || dg[j] != 0 || dh[j] != 0) need |= 1 << j;
     }
   }
-  // A bin's loss (the better of missing right and missing left) and its
-  // missing-value direction.
-  auto evaluate = [&](long long xg, long long xh, long long yg, long long yh, double& l,
-                      int& d) {
-    const double right_missing = split_loss(p, xg, xh, gp - xg, hp - xh, ug, uh, parent_gain);
-    const double left_missing =
-        (yg == 0 && yh == 0)
-            ? right_missing
-            : split_loss(p, xg + yg, xh + yh, gp - xg - yg, hp - xh - yh, ug, uh, parent_gain);
-    d = left_missing > right_missing;
-    l = d ? left_missing : right_missing;
-  };
   // The lane's best bin, taken in increasing bin order (ties keep the lower).
   Cand c;
   c.loss = -INFINITY;
@@ -164,15 +207,6 @@ __device__ __forceinline__ void seg_evaluate(const long long (&dg)[4], const lon
   c.feature = f;
   c.bin = -1;
   c.dl = 0;
-  auto fold = [&](int j, double l, int d) {
-    if (l > c.loss) {
-      c.loss = l;
-      c.bin = sub * BPL + j;
-      c.dl = d;
-      c.gl = d ? lg[j] + mg : lg[j];
-      c.hl = d ? lh[j] + mh : lh[j];
-    }
-  };
   // Lane-order slots of the needed bins: a lane has fewer than 8, so three
   // bit ballots of its count give the exclusive prefix over the lanes.
   unsigned long long c0 = 0, c1 = 0, c2 = 0;
@@ -208,7 +242,13 @@ __device__ __forceinline__ void seg_evaluate(const long long (&dg)[4], const lon
     int d = 0;
     if (lane < n_need) {
       const int r = (lane >= r1 ? 1 : 0) + (lane >= r2 ? 1 : 0) + (lane >= r3 ? 1 : 0);
-      evaluate(scr[2 * lane], scr[2 * lane + 1], scr[128 + 2 * r], scr[128 + 2 * r + 1], l, d);
+      const long long xg = scr[2 * lane], xh = scr[2 * lane + 1];
+      const long long yg = scr[128 + 2 * r], yh = scr[128 + 2 * r + 1];
+      const double right_missing = split_loss(p, xg, xh, gp - xg, hp - xh, ug, uh, parent_gain);
+      const double left_missing =
+          split_loss(p, xg + yg, xh + yh, gp - xg - yg, hp - xh - yh, ug, uh, parent_gain);
+      d = left_missing > right_missing;
+      l = d ? left_missing : right_missing;
     }
     const unsigned long long dmask = __ballot(d);
     __builtin_amdgcn_wave_barrier();
@@ -218,20 +258,21 @@ __device__ __forceinline__ void seg_evaluate(const long long (&dg)[4], const lon
 #pragma unroll
     for (int j = 0; j < BPL; ++j) {
       const int slot = base + __popc(need & ((1 << j) - 1));
-      if ((need >> j) & 1)
-        fold(j, __longlong_as_double(scr[slot]), int((dmask >> slot) & 1ull));
-    }
-    __builtin_amdgcn_wave_barrier();  // the next call rewrites the scratch
-  } else {
-#pragma unroll
-    for (int j = 0; j < BPL; ++j) {
-      if ((in >> j) & 1) {
-        double l;
-        int d;
-        evaluate(lg[j], lh[j], mg, mh, l, d);
-        fold(j, l, d);
+      if ((need >> j) & 1) {
+        const double l = __longlong_as_double(scr[slot]);
+        const int d = int((dmask >> slot) & 1ull);
+        if (l > c.loss) {
+          c.loss = l;
+          c.bin = sub * BPL + j;
+          c.dl = d;
+          c.gl = d ? lg[j] + mg : lg[j];
+          c.hl = d ? lh[j] + mh : lh[j];
+        }
       }
     }
+    __builtin_amdgcn_wave_barrier();  // the next call rewrites the scratch
+  } else if (__ballot(in != 0)) {  // uniform: some row's feature has bins
+    best_of_bins<BPL, SERIAL>(lg, lh, in, sub * BPL, mg, mh, gp, hp, ug, uh, parent_gain, p, c);
   }
   // Row argmax: the largest loss, then the lowest lane holding it (lanes hold
   // increasing bins and each kept its lowest bin on ties).

@@ -394,6 +394,7 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(DE
   }
 }
 
+
 // The evaluation a present-value pass does for its single-chunk nodes (EVAL).
 struct SparseEvalArgs {
   const long long* parent_base;  // previous level's node histograms
@@ -410,6 +411,9 @@ struct SparseEvalArgs {
 // EVAL's epilogue (see hist_sparse_kernel): node w.slot's features f0 .. f0 +
 // nf from the LDS planes (g, h: [feature][bin_stride + 1] words), and its sibling's from
 // the parent's words minus them; every thread of the workgroup takes part.
+// The lane's bins are evaluated one after the other (seg_evaluate<true>):
+// interleaving their divisions needs more than the 128 registers of two such
+// workgroups per CU.
 template <int THREADS>
 __device__ __forceinline__ void evaluate_tile(const SparseEvalArgs& ev, const HistWork& w,
                                               int32_t f0, int32_t nf, int32_t n_features,
@@ -452,8 +456,8 @@ __device__ __forceinline__ void evaluate_tile(const SparseEvalArgs& ev, const Hi
     }
     long long g[BPL], h[BPL];
     load(fl, live, g, h);
-    seg_evaluate(g, h, w.slot, f0 + fl, live, n_features, ev.n_bins, ev.node_sums, ug, uh, ev.p,
-                 ev.fmask, ev.skip_bins, ev.cand, scr);
+    seg_evaluate<true>(g, h, w.slot, f0 + fl, live, n_features, ev.n_bins, ev.node_sums, ug, uh,
+                       ev.p, ev.fmask, ev.skip_bins, ev.cand, scr);
     if (!sib) continue;
     // The sibling: the parent's words minus the node's (read again from LDS,
     // so that they are not held across the evaluation above).
@@ -469,8 +473,8 @@ __device__ __forceinline__ void evaluate_tile(const SparseEvalArgs& ev, const Hi
         so[2 * k + 1] = h[k];
       }
     }
-    seg_evaluate(g, h, w.slot ^ 1, f0 + fl, live, n_features, ev.n_bins, ev.node_sums, ug, uh,
-                 ev.p, ev.fmask, ev.skip_bins, ev.cand, scr);
+    seg_evaluate<true>(g, h, w.slot ^ 1, f0 + fl, live, n_features, ev.n_bins, ev.node_sums, ug,
+                       uh, ev.p, ev.fmask, ev.skip_bins, ev.cand, scr);
   }
 }
 
@@ -543,7 +547,8 @@ __device__ __forceinline__ uint32_t wave_inclusive_umax(uint32_t x) {
 }
 
 template <bool GATHER, bool EVAL, int THREADS>
-__global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(4))) void hist_sparse_kernel(
+__global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(4))) void
+hist_sparse_kernel(
     const uint32_t* __restrict__ ptr, const uint16_t* __restrict__ entries, int64_t n_rows,
     int32_t n_features, int32_t tile_features, const int2* __restrict__ gpair,
     const uint32_t* __restrict__ ridx, const HistWork* __restrict__ work, int32_t n_work_host,

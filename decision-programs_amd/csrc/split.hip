@@ -108,28 +108,17 @@ __device__ __forceinline__ Cand feature_best(const FeatBins<BPL>& d, int32_t f, 
   c.feature = f;
   c.bin = -1;
   c.dl = 0;
+  if (nb > 0) {  // uniform per wavefront (a feature left out by sampling has none)
+    long long lg[BPL], lh[BPL];
+    int in = 0;
 #pragma unroll
-  for (int j = 0; j < BPL; ++j) {
-    const int b = lane * BPL + j;
-    if (b < nb) {
-      const long long lg = og + sg[j] + (b >= skip && skip >= 0 ? kg : 0);
-      const long long lh = oh + sh[j] + (b >= skip && skip >= 0 ? kh : 0);
-      const double right_missing = split_loss(p, lg, lh, gp - lg, hp - lh, ug, uh, parent_gain);
-      // Without missing rows both directions are the same candidate.
-      const double left_missing =
-          (mg == 0 && mh == 0)
-              ? right_missing
-              : split_loss(p, lg + mg, lh + mh, gp - lg - mg, hp - lh - mh, ug, uh, parent_gain);
-      const int dl = left_missing > right_missing;
-      const double loss = dl ? left_missing : right_missing;
-      if (loss > c.loss) {
-        c.loss = loss;
-        c.bin = b;
-        c.dl = dl;
-        c.gl = dl ? lg + mg : lg;
-        c.hl = dl ? lh + mh : lh;
-      }
+    for (int j = 0; j < BPL; ++j) {
+      const int b = lane * BPL + j;
+      lg[j] = og + sg[j] + (b >= skip && skip >= 0 ? kg : 0);
+      lh[j] = oh + sh[j] + (b >= skip && skip >= 0 ? kh : 0);
+      in |= (b < nb ? 1 : 0) << j;
     }
+    best_of_bins<BPL>(lg, lh, in, lane * BPL, mg, mh, gp, hp, ug, uh, parent_gain, p, c);
   }
   // Wave argmax: the largest loss, then the lowest lane holding it (lanes hold
   // increasing bins, and each lane kept its lowest bin on ties), so the
