@@ -251,6 +251,36 @@ def test_split_search_matches_brute_force(oracle, seed):
         assert got["loss_chg"] == key[0]
 
 
+def test_split_never_picks_an_empty_bin(oracle):
+    """The evaluation's pick is never an empty bin past the first.  An empty bin b > 0 has the
+    left sums of bin b - 1, so its candidate has bin b - 1's loss and the tie goes to the lower
+    bin; the GPU evaluation of small nodes relies on this and evaluates only the non-empty bins
+    (and bin 0).  Random sparse 64-bin features with missing mass, under three parameter sets;
+    the cases where an empty bin directly follows the pick (a tie the rule resolves) are
+    counted, so the check is exercised."""
+    rng = np.random.default_rng(17)
+    ties = 0
+    for p in (oracle.params(), oracle.params(lam=0.0, alpha=0.3, min_child_weight=2.0),
+              oracle.params(lam=5.0, min_child_weight=0.0)):
+        for _ in range(400):
+            nb = int(rng.integers(2, 65))
+            hist = np.zeros((1, 64, 2), dtype=np.int64)
+            live = rng.choice(nb, size=int(rng.integers(1, min(nb, 20) + 1)), replace=False)
+            hist[0, live, 0] = rng.integers(-(1 << 20), 1 << 20, size=live.size)
+            hist[0, live, 1] = rng.integers(1, 1 << 20, size=live.size)
+            mg = int(rng.integers(-(1 << 22), 1 << 22)) if rng.random() < 0.7 else 0
+            mh = int(rng.integers(1, 1 << 22)) if mg else 0
+            gp, hp = int(hist[0, :, 0].sum()) + mg, int(hist[0, :, 1].sum()) + mh
+            got = oracle.evaluate_split(hist, np.array([nb], dtype=np.int32), gp, hp, 16, 16, p)
+            if not got["valid"]:
+                continue
+            b = got["bin"]
+            assert b == 0 or hist[0, b].any(), (nb, b)
+            if b + 1 < nb and not hist[0, b + 1].any():
+                ties += 1
+    assert ties > 50
+
+
 def test_partition_is_stable(oracle):
     x, bins, cut_ptr, cuts, mb, qg, qh, eg, eh = _quantised_case(oracle, seed=11)
     rng = np.random.default_rng(3)
