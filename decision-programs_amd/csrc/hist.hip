@@ -394,7 +394,6 @@ __global__ __launch_bounds__(kHistThreads) __attribute__((amdgpu_waves_per_eu(DE
   }
 }
 
-
 // The evaluation a present-value pass does for its single-chunk nodes (EVAL).
 struct SparseEvalArgs {
   const long long* parent_base;  // previous level's node histograms

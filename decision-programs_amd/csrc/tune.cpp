@@ -274,8 +274,9 @@ const HistTuning& tune_sparse_hist(const SparseBins& sp, int64_t n_rows, int32_t
   DeviceBuffer<int64_t> sums(fused ? 2 : 0);
   DeviceBuffer<int32_t> exps(fused ? 2 : 0);
   DeviceBuffer<FeatCand> feat(fused ? size_t(n_features) : 0);
+  std::vector<int32_t> nb;  // alive until the stream has read it (synchronised below)
   if (fused) {
-    const std::vector<int32_t> nb(size_t(n_features), bin_stride);
+    nb.assign(size_t(n_features), bin_stride);
     DP_HIP(hipMemcpyAsync(nbins.p, nb.data(), nbins.bytes(), hipMemcpyHostToDevice, s));
     DP_HIP(hipMemsetAsync(sums.p, 0, sums.bytes(), s));
     DP_HIP(hipMemsetAsync(exps.p, 0, exps.bytes(), s));
