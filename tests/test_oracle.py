@@ -278,7 +278,7 @@ def test_split_never_picks_an_empty_bin(oracle):
             assert b == 0 or hist[0, b].any(), (nb, b)
             if b + 1 < nb and not hist[0, b + 1].any():
                 ties += 1
-    assert ties > 50
+    assert ties > 300  # 730 of 1,172 valid cases with this seed
 
 
 def test_partition_is_stable(oracle):
